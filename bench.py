@@ -1,0 +1,254 @@
+"""Benchmark of the kNN / k-means hot path on one MI355X.
+
+Default (no flags): exact squared-L2 kNN over a 1,000,000 x 128 fp32 base of integer values in
+[0, 255], 10,000 queries drawn the same way, k = 100 -- one "step" is one full batch search of
+the 10,000 queries with queries and base resident in HBM (search_batch on device pointers).
+The same JSON line carries the 2,000,000 x 96, 4,096-centroid k-means workload (10 Lloyd
+iterations from the first 4,096 points) under "kmeans".
+
+Printed JSON (one line): metric/value/unit, ms_per_step, "roofline" of the dominant kernel
+(FP32-MFMA distance + filter kernel, its algorithmic flops per launch divided by its average
+launch time, measured with HIP events on the engine's stream over the timed region) and
+"cpu_baseline": the oracle's restatement of the reference CPU path (CudaKnnEngine::search_batch_cpu,
+knn.rs:312-377, AVX-512 dispatch as vector-simd) timed on this host on a bounded query sample.
+
+Other workloads: --workload cos768 | kmeans | hamming | l1 | linf | gauss (see WORKLOADS).
+"""
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "vector-rs_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+import numpy as np  # noqa: E402
+
+METRIC = "kNN queries/sec (1M×128 fp32, k=100) + k-means iter/sec; % FP32-MFMA/HBM roofline"
+PEAK_MFMA_F32 = 157.3e12   # FLOP/s, MI355X dense FP32 matrix
+PEAK_HBM = 8.0e12          # B/s
+PEAK_VALU32 = 39.3e12      # non-packed 32-bit VALU op/s (256 CU x 64 lanes x 2.4 GHz)
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def cpu_threads() -> int:
+    env = os.environ.get("OMP_NUM_THREADS")
+    if env and env.isdigit():
+        return int(env)
+    return min(16, os.cpu_count() or 1)
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor()
+
+
+def roofline(prof, bound, peak, unit):
+    if not prof["launches"] or prof["kernel_ms"] <= 0:
+        return None
+    avg_s = prof["kernel_ms"] / prof["launches"] / 1e3
+    per_launch = prof["work"] / prof["launches"]
+    achieved = per_launch / avg_s
+    scale = 1e12 if unit == "TFLOP/s" else 1e9
+    return {"bound": bound, "achieved": round(achieved / scale, 3), "peak": round(peak / scale, 3), "unit": unit,
+            "frac": round(achieved / peak, 4), "traffic": None,
+            "work_per_launch": per_launch, "avg_launch_ms": round(avg_s * 1e3, 4), "launches": prof["launches"],
+            "algorithmic_bytes_per_launch": prof["bytes"] / prof["launches"]}
+
+
+# ---------------------------------------------------------------------------------------------
+def run_knn(vh, base, queries, k, metric, steps, warmup, hamming=False):
+    """Times `steps` device-resident batch searches; returns (ms_per_step, profile, ids, dist)."""
+    nq = queries.shape[0]
+    eng = vh.HammingKnnEngine(base) if hamming else vh.CudaKnnEngine(base, base.shape[1], metric)
+    dq = vh.DeviceBuffer.from_host(queries)
+    di = vh.DeviceBuffer(nq * k * 4)
+    dd = vh.DeviceBuffer(nq * k * 4)
+
+    def step():
+        eng.search_batch_device(dq.ptr, nq, k, di.ptr, dd.ptr)
+
+    for _ in range(warmup):
+        step()
+    eng.profile(True)
+    vh.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        step()
+        log(f"  step {i + 1}/{steps} done")
+    vh.synchronize()
+    t1 = time.perf_counter()
+    prof = eng.profile_read()
+    ids = di.to_host(np.empty((nq, k), np.uint32))
+    dist = dd.to_host(np.empty((nq, k), np.uint32 if hamming else np.float32))
+    return (t1 - t0) * 1e3 / steps, prof, ids, dist
+
+
+def cpu_knn_baseline(base, queries, k, metric, sample):
+    import oracle
+
+    qs = queries[:sample]
+    th = cpu_threads()
+    t0 = time.perf_counter()
+    oracle.knn_search_batch(base, qs, k, metric, threads=th)
+    dt = time.perf_counter() - t0
+    be = {0: "scalar", 1: "AVX2+FMA", 2: "AVX-512F"}[oracle.detect_backend()]
+    return {"value": round(sample / dt, 3), "unit": "queries/s", "cores": th, "kind": "port",
+            "sample": f"{sample} of the {queries.shape[0]} queries against the full base, k={k}, "
+                      f"{be} backend, {dt:.2f} s wall on {th} threads ({cpu_model()})"}
+
+
+def bench_kmeans(vh, steps_iters, with_cpu):
+    from vector_hip import datasets as ds
+
+    n, d, kc = 2_000_000, 96, 4096
+    log(f"kmeans: generating {n} x {d} mixture of {kc}")
+    data, _, _ = ds.gaussian_mixture(n, d, kc, ds.SEED_MIXTURE)
+    init = data[:kc].copy()
+    st = vh.KMeansState(data)
+    st.set_centroids(init)
+    st.run(1)  # warm-up iteration
+    st.set_centroids(init)
+    st.profile(True)
+    vh.synchronize()
+    t0 = time.perf_counter()
+    st.run(steps_iters)
+    vh.synchronize()
+    t1 = time.perf_counter()
+    prof = st.profile_read()
+    out = st.read()
+    ms_iter = (t1 - t0) * 1e3 / steps_iters
+    res = {"workload": f"kmeans_l2_{n}x{d}_k{kc}_{steps_iters}iters_init_first_points",
+           "value": round(1e3 / ms_iter, 3), "unit": "iterations/s", "ms_per_iteration": round(ms_iter, 3),
+           "inertia": out["inertia"],
+           "roofline": roofline(prof, "mfma", PEAK_MFMA_F32, "TFLOP/s")}
+    if with_cpu:
+        import oracle
+
+        sp = 65_536
+        th = cpu_threads()
+        t0 = time.perf_counter()
+        oracle.kmeans_step(data[:sp], init, "l2", threads=th)
+        dt = (time.perf_counter() - t0) * (n / sp)
+        res["cpu_baseline"] = {"value": round(1.0 / dt, 5), "unit": "iterations/s", "cores": th, "kind": "port",
+                               "sample": f"one Lloyd iteration (KMeans::fit body) on {sp} of the {n} points "
+                                         f"against all {kc} centroids, scaled x{n / sp:g}; {th} threads "
+                                         f"({cpu_model()})"}
+        res["speedup_vs_cpu"] = round(res["value"] / res["cpu_baseline"]["value"], 1)
+    return res
+
+
+WORKLOADS = {
+    "l2int": dict(n=1_000_000, d=128, nq=10_000, k=100, metric="l2", gen="uniform_int",
+                  name="knn_l2_int0-255_1000000x128_q10000_k100"),
+    "cos768": dict(n=1_000_000, d=768, nq=10_000, k=10, metric="cosine", gen="normalized",
+                   name="knn_cosine_normalized_1000000x768_q10000_k10"),
+    "gauss": dict(n=10_000, d=128, nq=100, k=10, metric="l2", gen="gaussian", name="knn_l2_gauss_10000x128_q100_k10"),
+    "l1": dict(n=500_000, d=128, nq=4096, k=10, metric="l1", gen="uniform", name="knn_l1_uniform_500000x128_q4096_k10"),
+    "linf": dict(n=500_000, d=128, nq=4096, k=10, metric="linf", gen="uniform",
+                 name="knn_linf_uniform_500000x128_q4096_k10"),
+    "hamming": dict(n=10_000_000, d=8, nq=10_000, k=10, metric="hamming", gen="packed_bits",
+                    name="knn_hamming_packed256_10000000_q10000_k10"),
+}
+
+
+def bench_knn_workload(vh, key, steps, warmup, with_cpu):
+    from vector_hip import datasets as ds
+
+    w = WORKLOADS[key]
+    log(f"{key}: generating base {w['n']} x {w['d']} ({w['gen']})")
+    gen = getattr(ds, w["gen"])
+    if w["gen"] == "packed_bits":
+        base = gen(w["n"], 32 * w["d"], ds.SEED_BASE)
+        q = gen(w["nq"], 32 * w["d"], ds.SEED_QUERIES)
+    else:
+        base = gen(w["n"], w["d"], ds.SEED_BASE)
+        q = gen(w["nq"], w["d"], ds.SEED_QUERIES)
+    names = {"l2": "L2Squared", "dot": "DotProduct", "cosine": "CosineSimilarity", "l1": "Manhattan",
+             "linf": "Chebyshev"}
+    metric = vh.DistanceMetric[names[w["metric"]]] if w["metric"] != "hamming" else None
+    ham = w["metric"] == "hamming"
+    ms, prof, ids, dist = run_knn(vh, base, q, w["k"], metric, steps, warmup, hamming=ham)
+    gemm = w["metric"] in ("l2", "dot", "cosine")
+    if gemm:
+        rl = roofline(prof, "mfma", PEAK_MFMA_F32, "TFLOP/s")
+    else:
+        # VALU-bound: work counts element (or word) operations, each costing two VALU ops
+        p2 = dict(prof)
+        p2["work"] = prof["work"] * 2.0
+        rl = roofline(p2, "valu", PEAK_VALU32, "TFLOP/s")
+        if rl:
+            rl["unit"] = "Top/s (32-bit VALU)"
+    out = {"metric": METRIC, "value": round(w["nq"] * 1e3 / ms, 2), "unit": "queries/s", "n_gpus": 1,
+           "steps": steps, "warmup": warmup, "ms_per_step": round(ms, 3), "higher_is_better": True,
+           "scaling": "strong", "vs_baseline": None, "dtype": "u32" if ham else "f32", "data": "synthetic",
+           "config": {"workload": w["name"], "base_rows": w["n"], "dim": w["d"] * (32 if ham else 1),
+                      "queries": w["nq"], "k": w["k"], "metric": w["metric"], "parallelism": "single GPU"},
+           "roofline": rl}
+    if with_cpu:
+        if ham:
+            import oracle
+
+            sub = 500_000
+            un_b = oracle.unpack_bits(base[:sub])
+            un_q = oracle.unpack_bits(q[:64])
+            cb = cpu_knn_baseline(un_b, un_q, w["k"], "hamming", 64)
+            cb["value"] = round(cb["value"] * sub / w["n"], 4)
+            cb["sample"] = (f"reference semantics (thresholded float Hamming over codes unpacked to 0/1 floats): 64 "
+                            f"queries against {sub} of the {w['n']} codes, scaled by {sub}/{w['n']}; " + cb["sample"])
+            out["cpu_baseline"] = cb
+        else:
+            sample = 256 if w["n"] * w["d"] <= 200_000_000 else 64
+            out["cpu_baseline"] = cpu_knn_baseline(base, q, w["k"], w["metric"], min(sample, w["nq"]))
+    return out
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--workload", default="default",
+                    choices=["default", "kmeans"] + sorted(WORKLOADS))
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build has no multi-GPU path",
+              file=sys.stderr)
+        sys.exit(2)
+    import vector_hip as vh
+
+    if vh.CudaDeviceContext.device_count() < 1:
+        print("no gfx950 GPU visible", file=sys.stderr)
+        sys.exit(1)
+    ctx = vh.CudaDeviceContext(0)
+    if args.workload == "kmeans":
+        r = bench_kmeans(vh, 10, not args.no_cpu)
+        out = {"metric": METRIC, "value": r["value"], "unit": r["unit"], "n_gpus": 1, "steps": 10, "warmup": 1,
+               "ms_per_step": r["ms_per_iteration"], "higher_is_better": True, "scaling": "strong",
+               "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+               "config": {"workload": r["workload"], "parallelism": "single GPU"}, "roofline": r["roofline"],
+               "cpu_baseline": r.get("cpu_baseline")}
+    else:
+        key = "l2int" if args.workload == "default" else args.workload
+        out = bench_knn_workload(vh, key, args.steps, args.warmup, not args.no_cpu)
+        if args.workload == "default":
+            out["kmeans"] = bench_kmeans(vh, 10, not args.no_cpu)
+    out["config"]["device"] = ctx.device_name()
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

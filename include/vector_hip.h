@@ -1,0 +1,204 @@
+/*
+ * vector_hip.h -- C ABI of the MI355X (gfx950) kNN / k-means library.
+ *
+ * This is the drop-in boundary for the reference's GPU hot path (Malset2603/vector-rs,
+ * crate vector-cuda).  Each entry point names the reference interface it replaces.
+ * Plain pointers and sizes only; every host pointer is owned by the caller and the
+ * library copies what it keeps.  All functions are thread-safe per engine (an engine
+ * serialises its own calls on one HIP stream).
+ *
+ * Status codes mirror CudaError (vector-cuda/src/error.rs:7-29):
+ *   VHIP_OK, InsufficientDevices, DeviceNotFound, DriverError, HardwareNotAvailable,
+ *   InvalidConfig.  vhip_last_error() returns the calling thread's last message.
+ *
+ * Semantics kept from the reference (knn.rs:151-169, distributed_knn.rs:155-231):
+ *   effective_k = min(k, N); empty queries, k == 0 or N == 0 give empty lists;
+ *   results are best first; DotProduct / CosineSimilarity report the similarity and
+ *   sort descending; cosine with a zero-norm operand is 0; squared L2 is clamped >= 0.
+ * Semantics deliberately changed:
+ *   k is not clamped to 128 (knn.cu:218) -- any k <= VHIP_MAX_K is exact;
+ *   the Q x N distance matrix is never materialised (knn.rs:195);
+ *   k-means at one GPU runs on the GPU (distributed_kmeans.rs:80 never did);
+ *   empty clusters keep their centroid (as kmeans.cu:350-356, not a random reseed);
+ *   k-means init is explicit or seeded (the reference used an unseeded thread_rng);
+ *   there is no silent CPU fallback: a missing GPU is an error, not a slow answer.
+ */
+#ifndef VECTOR_HIP_H
+#define VECTOR_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#if defined(__GNUC__)
+#pragma GCC visibility push(default) /* the library hides everything but this API */
+#endif
+
+/* ---- status codes: CudaError (error.rs:7-29) -------------------------------- */
+#define VHIP_OK                          0
+#define VHIP_ERR_INSUFFICIENT_DEVICES  (-1) /* InsufficientDevices{requested, available} */
+#define VHIP_ERR_DEVICE_NOT_FOUND      (-2) /* DeviceNotFound{ordinal} */
+#define VHIP_ERR_DRIVER                (-3) /* DriverError(String) */
+#define VHIP_ERR_HARDWARE_NOT_AVAILABLE (-4) /* HardwareNotAvailable */
+#define VHIP_ERR_INVALID_CONFIG        (-5) /* InvalidConfig(String) */
+
+/* ---- metric codes: knn.rs:235-246 / kmeans.rs:152-163 ------------------------ */
+#define VHIP_METRIC_L2SQUARED    0
+#define VHIP_METRIC_DOTPRODUCT   1
+#define VHIP_METRIC_COSINE       2
+#define VHIP_METRIC_MANHATTAN    3
+#define VHIP_METRIC_MINKOWSKI    4 /* p = 3 */
+#define VHIP_METRIC_CHEBYSHEV    5
+#define VHIP_METRIC_HAMMING      6 /* thresholded float mismatch count, |a-b| > 1e-6 */
+#define VHIP_METRIC_MAHALANOBIS  7 /* standardised: sqrt(L2^2) */
+#define VHIP_METRIC_JACCARD      8
+#define VHIP_METRIC_HELLINGER    9
+
+/* ---- GpuShardMode (distributed_knn.rs:14-19) --------------------------------- */
+#define VHIP_SHARD_SHARDED    0
+#define VHIP_SHARD_REPLICATED 1
+
+#define VHIP_MAX_K 2048 /* largest k served exactly by one search call */
+
+/* ---- errors ------------------------------------------------------------------- */
+/* Message of the calling thread's last failed call ("" if none). */
+const char *vhip_last_error(void);
+/* requested / available of the last InsufficientDevices error of this thread. */
+void vhip_last_error_devices(size_t *requested, size_t *available);
+
+/* ---- device context: CudaDeviceContext (device.rs:110-256) ------------------- */
+/* CudaDeviceContext::device_count (device.rs:112-117): number of usable gfx950 GPUs. */
+int vhip_device_count(void);
+/* CudaDeviceContext::with_ordinal_strict (device.rs:127-171): name / total memory of a
+ * device, DeviceNotFound when ordinal >= device_count. */
+int vhip_device_info(int ordinal, char *name, size_t name_len, size_t *total_memory_bytes);
+
+/* ---- CudaKnnEngine (knn.rs:45-401) ------------------------------------------- */
+typedef struct vhip_knn vhip_knn;
+/* CudaKnnEngine::with_ordinal (knn.rs:90-140): uploads the row-major n x dim base once
+ * and keeps it resident in HBM until vhip_knn_destroy. */
+int vhip_knn_create(const float *base, size_t n, size_t dim, int metric, int ordinal, vhip_knn **out);
+/* CudaKnnEngine::search_batch (knn.rs:151-169): nq row-major queries, k neighbours.
+ * out_ids / out_dist are nq x k (row stride k); out_len[q] = min(k, n) valid entries
+ * best first.  Host buffers; the call returns when results are in them. */
+int vhip_knn_search_batch(vhip_knn *eng, const float *queries, size_t nq, size_t k, uint32_t *out_ids,
+                          float *out_dist, size_t *out_len);
+/* Same search with queries and outputs already in device memory of the engine's GPU
+ * (no reference counterpart; it serves callers whose queries are produced on the GPU).
+ * Returns after the results are written. */
+int vhip_knn_search_batch_device(vhip_knn *eng, const float *d_queries, size_t nq, size_t k, uint32_t *d_ids,
+                                 float *d_dist);
+size_t vhip_knn_dimension(const vhip_knn *eng);    /* knn.rs:387 */
+size_t vhip_knn_num_vectors(const vhip_knn *eng);  /* knn.rs:393 */
+int vhip_knn_metric(const vhip_knn *eng);          /* knn.rs:399 */
+int vhip_knn_device_id(const vhip_knn *eng);       /* knn.rs:381 context().device_id() */
+void vhip_knn_destroy(vhip_knn *eng);              /* Drop of the CudaSlice (knn.rs:50-51) */
+
+/* Kernel timing of the engine's distance kernel (HIP events on its stream).  Enable,
+ * run searches, then read the summed kernel time, launch count and the algorithmic
+ * flops (2*nq*rows*dim, or pair operations for VALU metrics) and HBM bytes (base
+ * rows + queries read once per launch) of those launches. */
+int vhip_knn_profile(vhip_knn *eng, int enable);
+int vhip_knn_profile_read(vhip_knn *eng, double *kernel_ms, uint64_t *launches, double *work, double *bytes);
+
+/* ---- DistributedKnnEngine (ddp/distributed_knn.rs:24-262) --------------------- */
+typedef struct vhip_dknn vhip_dknn;
+/* DistributedKnnEngine::try_new (:40-61): InsufficientDevices when num_gpus > device_count. */
+int vhip_dknn_try_new(const float *base, size_t n, size_t dim, size_t num_gpus, int mode, int metric,
+                      vhip_dknn **out);
+/* DistributedKnnEngine::emulator (:64-74): num_gpus ranks without the device-count check.
+ * Every rank runs on the one GPU (ordinal 0); sharded ranks hold N/G rows each and are
+ * merged with top_k_reduce, so results equal the single-rank ones. */
+int vhip_dknn_emulator(const float *base, size_t n, size_t dim, size_t num_gpus, int mode, int metric,
+                       vhip_dknn **out);
+/* DistributedKnnEngine::search_batch (:155-231); same output contract as vhip_knn_search_batch. */
+int vhip_dknn_search_batch(vhip_dknn *eng, const float *queries, size_t nq, size_t k, uint32_t *out_ids,
+                           float *out_dist, size_t *out_len);
+size_t vhip_dknn_num_gpus(const vhip_dknn *eng);     /* :235 */
+int vhip_dknn_mode(const vhip_dknn *eng);            /* :241 */
+size_t vhip_dknn_dimension(const vhip_dknn *eng);    /* :247 */
+size_t vhip_dknn_num_vectors(const vhip_dknn *eng);  /* :253 */
+int vhip_dknn_metric(const vhip_dknn *eng);          /* :259 */
+void vhip_dknn_destroy(vhip_dknn *eng);
+
+/* CollectiveOps::top_k_reduce (ddp/collective.rs:115-159), host arrays: merges the
+ * concatenated per-rank lists (total entries) into the best k, best first.  Returns
+ * the number of results. */
+size_t vhip_top_k_reduce(const uint32_t *ids, const float *dist, size_t total, size_t k, int metric,
+                         uint32_t *out_ids, float *out_dist);
+
+/* ---- packed-bit Hamming kNN (extension: the reference has only the thresholded float
+ * Hamming of scalar.rs:143-153, which equals popcount(a ^ b) on 0/1 codes) ------- */
+typedef struct vhip_hamming vhip_hamming;
+int vhip_hamming_create(const uint32_t *codes, size_t n, size_t words, int ordinal, vhip_hamming **out);
+int vhip_hamming_search_batch(vhip_hamming *eng, const uint32_t *queries, size_t nq, size_t k,
+                              uint32_t *out_ids, uint32_t *out_dist, size_t *out_len);
+int vhip_hamming_search_batch_device(vhip_hamming *eng, const uint32_t *d_queries, size_t nq, size_t k,
+                                     uint32_t *d_ids, uint32_t *d_dist);
+int vhip_hamming_profile(vhip_hamming *eng, int enable);
+int vhip_hamming_profile_read(vhip_hamming *eng, double *kernel_ms, uint64_t *launches, double *work,
+                              double *bytes);
+void vhip_hamming_destroy(vhip_hamming *eng);
+
+/* ---- k-means: CudaKMeansEngine (kmeans.rs:37-467) / DistributedKMeansEngine ---- */
+/* CudaKMeansResult (kmeans.rs:15-26) without the centroid buffer (written to out_centroids). */
+typedef struct {
+    size_t dimension;
+    size_t k;
+    size_t iterations;
+    float inertia;
+} vhip_kmeans_result;
+
+#define VHIP_INIT_KMEANSPP 0 /* CudaKMeansEngine::init_random (kmeans.rs:409-460), seeded */
+#define VHIP_INIT_SHUFFLE  1 /* DistributedKMeansEngine::init_random (distributed_kmeans.rs:524-535), seeded */
+
+/* CudaKMeansEngine::fit (kmeans.rs:58-97) on GPU `ordinal`: Lloyd iterations until
+ * max_iters or max centroid shift <= tol (tol < 0 never stops early).  k is clamped to n
+ * (effective_k); n == 0 or k == 0 gives k = 0 and writes nothing.  init_centroids
+ * (effective_k x dim) gives the starting centroids; NULL seeds them with `init_mode`
+ * from `seed`.  out_centroids receives effective_k x dim floats; out_assign (n, may be
+ * NULL) the final assignment; inertia is the sum of per-point metric values of the last
+ * assignment (kmeans.cu:110-170 conventions: L2^2, -dot, 1-cos). */
+int vhip_kmeans_fit(int ordinal, const float *data, size_t n, size_t dim, size_t k, size_t max_iters, float tol,
+                    int metric, const float *init_centroids, int init_mode, uint64_t seed, float *out_centroids,
+                    int32_t *out_assign, vhip_kmeans_result *result);
+/* DistributedKMeansEngine::try_new (distributed_kmeans.rs:28-38): validates num_gpus
+ * against the device count (InsufficientDevices). */
+int vhip_dkmeans_check(size_t num_gpus);
+
+/* Resident k-means state for per-iteration use (no reference counterpart: it exposes
+ * one Lloyd step for parity checks and the per-iteration benchmark). */
+typedef struct vhip_kmeans vhip_kmeans;
+int vhip_kmeans_create(int ordinal, const float *data, size_t n, size_t dim, int metric, vhip_kmeans **out);
+/* Sets the current centroids (k x dim host floats). */
+int vhip_kmeans_set_centroids(vhip_kmeans *km, const float *centroids, size_t k);
+/* Runs `iters` assign+update iterations on the device without host synchronisation. */
+int vhip_kmeans_run(vhip_kmeans *km, size_t iters);
+/* Copies out the state after the last iteration: centroids (k x dim), assignment (n),
+ * counts (k), per-cluster shift (k), max shift and inertia.  Any pointer may be NULL. */
+int vhip_kmeans_read(vhip_kmeans *km, float *centroids, int32_t *assign, int64_t *counts, float *shifts,
+                     float *max_shift, float *inertia);
+int vhip_kmeans_profile(vhip_kmeans *km, int enable);
+int vhip_kmeans_profile_read(vhip_kmeans *km, double *kernel_ms, uint64_t *launches, double *work,
+                             double *bytes);
+void vhip_kmeans_destroy(vhip_kmeans *km);
+
+/* ---- device memory helpers (for callers without a framework) ------------------- */
+int vhip_malloc(int ordinal, size_t bytes, void **ptr);
+int vhip_free(int ordinal, void *ptr);
+int vhip_memcpy_htod(int ordinal, void *dst, const void *src, size_t bytes);
+int vhip_memcpy_dtoh(int ordinal, void *dst, const void *src, size_t bytes);
+int vhip_synchronize(int ordinal);
+
+#if defined(__GNUC__)
+#pragma GCC visibility pop
+#endif
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VECTOR_HIP_H */

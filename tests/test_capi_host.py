@@ -1,0 +1,110 @@
+"""CPU-side tests of the C ABI: the library loads, exports every declared entry
+point, and the host logic (errors, argument checks, top_k_reduce) behaves like the
+reference.  No kernel runs here."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "vector_hip.h")
+
+
+def _declared():
+    txt = open(HEADER).read()
+    txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+    return sorted(set(re.findall(r"\b(vhip_[a-z0-9_]+)\s*\(", txt)))
+
+
+def test_library_exports_every_declared_symbol():
+    import vector_hip as vh
+
+    lib = ctypes.CDLL(vh.library_path())
+    names = _declared()
+    assert len(names) >= 40
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, f"not exported: {missing}"
+
+
+def test_no_torch_or_oracle_in_product_binding():
+    import vector_hip as vh
+
+    src = open(os.path.join(os.path.dirname(vh.__file__), "__init__.py")).read()
+    assert "import oracle" not in src and "vh_oracle" not in src
+
+
+def test_device_count_is_nonnegative():
+    import vector_hip as vh
+
+    assert vh.CudaDeviceContext.device_count() >= 0
+
+
+def test_insufficient_devices_error():
+    """distributed_knn.rs:470-494, ddp/mod.rs:106-122, integration_tests.rs:163-177."""
+    import vector_hip as vh
+
+    avail = vh.CudaDeviceContext.device_count()
+    data = np.array([1, 2, 3, 4], np.float32)
+    with pytest.raises(vh.InsufficientDevices) as ei:
+        vh.DistributedKnnEngine.try_new(data, 2, avail + 100, vh.GpuShardMode.Sharded, vh.DistanceMetric.L2Squared)
+    assert ei.value.requested == avail + 100 and ei.value.available == avail
+    with pytest.raises(vh.InsufficientDevices) as ei:
+        vh.DistributedKMeansEngine.try_new(avail + 10)
+    assert ei.value == vh.InsufficientDevices(avail + 10, avail)
+
+
+def test_invalid_config_errors():
+    import vector_hip as vh
+
+    with pytest.raises(vh.InvalidConfig):
+        vh.DistributedKnnEngine.emulator(np.zeros(4, np.float32), 2, 0)
+    with pytest.raises(vh.InvalidConfig):
+        vh.CudaKnnEngine(np.zeros(5, np.float32), 2)  # length not a multiple of dimension
+    h = ctypes.c_void_p()
+    lib = ctypes.CDLL(vh.library_path())
+    lib.vhip_knn_create.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_int, ctypes.c_int,
+                                    ctypes.c_void_p]
+    assert lib.vhip_knn_create(None, 0, 4, 42, 0, ctypes.byref(h)) == -5  # unknown metric
+    assert lib.vhip_knn_create(None, 0, 0, 0, 0, ctypes.byref(h)) == -5   # dimension 0
+
+
+@pytest.mark.skipif(os.path.exists("/dev/kfd"), reason="checks the no-GPU error path")
+def test_no_gpu_is_an_error_not_a_fallback():
+    import vector_hip as vh
+
+    with pytest.raises((vh.HardwareNotAvailable, vh.DeviceNotFound)):
+        vh.CudaKnnEngine(np.zeros((4, 2), np.float32), 2)
+
+
+def test_top_k_reduce_matches_reference_kats_and_oracle(oracle):
+    """collective.rs:239-282 known answers, and agreement with the oracle's restatement
+    (same BinaryHeap rules) on random lists with ties."""
+    import vector_hip as vh
+
+    R = vh.SearchResult
+    m = vh.CollectiveOps.top_k_reduce([[R(0, 1.0), R(1, 5.0)], [R(10, 0.5), R(11, 4.0)]], 2)
+    assert [r.id for r in m] == [10, 0]
+    assert vh.CollectiveOps.top_k_reduce([], 5) == []
+    assert vh.CollectiveOps.top_k_reduce([[R(0, 1.0)]], 0) == []
+    m = vh.CollectiveOps.top_k_reduce([[R(0, .85), R(1, .40)], [R(2, .95), R(3, .70)]], 3,
+                                      vh.DistanceMetric.CosineSimilarity)
+    assert [r.id for r in m] == [2, 0, 3]
+    m = vh.CollectiveOps.top_k_reduce([[R(0, 2.0)], [R(1, 1.0)]], 10)
+    assert [r.id for r in m] == [1, 0]
+    rng = np.random.default_rng(1)
+    for trial in range(20):
+        lists = []
+        for r in range(3):
+            n = rng.integers(0, 12)
+            ids = rng.integers(0, 1000, n)
+            d = rng.integers(0, 6, n).astype(np.float32)  # many ties
+            lists.append((ids, d))
+        k = int(rng.integers(1, 10))
+        metric = "cosine" if trial % 2 else "l2"
+        oi, od = oracle.top_k_reduce(lists, k, metric)
+        got = vh.CollectiveOps.top_k_reduce([[R(int(a), float(b)) for a, b in zip(*l)] for l in lists], k,
+                                            vh.DistanceMetric.CosineSimilarity if trial % 2 else
+                                            vh.DistanceMetric.L2Squared)
+        assert [r.id for r in got] == list(oi) and np.allclose([r.distance for r in got], od)

@@ -1,0 +1,196 @@
+"""GPU parity of k-means (Lloyd) through the C ABI.
+
+Reference tests restated (kmeans.rs:473-577, distributed_kmeans.rs:548-641,
+ivf/kmeans.rs:378-417, integration_tests.rs:7-56), plus per-iteration parity with the
+oracle on Gaussian-mixture data shaped like the 2M x 96 / 4096-centroid workload:
+assignments may differ on <= 0.01% of points and only at near-ties; centroids must be within
+1e-4 (per-centroid norm-relative) of the mean of their assigned points, and of the oracle's
+update wherever the membership agrees.  Each iteration is checked from the same centroids.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def vh():
+    import vector_hip
+
+    assert vector_hip.CudaDeviceContext.device_count() >= 1
+    return vector_hip
+
+
+def _three_clusters(n_per=50):
+    return np.concatenate([np.tile([0.1, -0.1, 0.05, -0.05], (n_per, 1)),
+                           np.tile([10.1, 9.9, 10.05, 9.95], (n_per, 1)),
+                           np.tile([20.1, 19.9, 20.05, 19.95], (n_per, 1))]).astype(np.float32)
+
+
+# ---- reference known-answer tests -----------------------------------------------------
+def test_kmeans_rs_kats(vh):
+    eng = vh.CudaKMeansEngine()
+    r = eng.fit(_three_clusters(), 4, 3, 20, 1e-4, vh.DistanceMetric.L2Squared)       # kmeans.rs:474-504
+    assert r.k == 3 and r.dimension == 4 and r.iterations > 0 and r.inertia < 1.0
+    assert all(len(r.centroid(c)) == 4 for c in range(3))
+    r = eng.fit(np.array([1, 1, 1.1, .9, .9, 1.1], np.float32), 2, 1, 10, 1e-4)        # :507-517
+    assert r.k == 1 and abs(r.centroid(0)[0] - 1) < 0.1 and abs(r.centroid(0)[1] - 1) < 0.1
+    assert eng.fit(np.zeros(0, np.float32), 4, 3, 10, 1e-4).k == 0                     # :520-527
+    assert eng.fit(np.array([1, 2], np.float32), 2, 0, 10, 1e-4).k == 0
+    assert eng.fit(np.array([1, 2, 3, 4], np.float32), 2, 5, 10, 1e-4).k == 2          # :530-537
+    data = np.array([1, 0, 0, 0, 1, 0, 0, 0, 1, .9, .1, 0], np.float32)                # :540-557
+    assert eng.fit(data, 3, 3, 10, 1e-4, vh.DistanceMetric.CosineSimilarity).k == 3
+    assert eng.fit(data, 3, 3, 10, 1e-4, vh.DistanceMetric.DotProduct).k == 3
+    hd = (np.arange(20 * 128) * 0.01).astype(np.float32)                               # :560-570
+    r = eng.fit(hd, 128, 4, 5, 1e-3)
+    assert r.k == 4 and r.dimension == 128
+    assert eng.context().device_id() == 0 and eng.context().total_memory_bytes() > 0  # :573-577
+
+
+def test_ivf_kmeans_single_cluster_mean(vh):
+    """ivf/kmeans.rs:386-395: the single centroid is the exact mean."""
+    data = np.array([1, 2, 3, 4, 1.1, 2.1, 3.1, 4.1], np.float32)
+    r = vh.CudaKMeansEngine().fit(data, 4, 1, 10, 1e-4)
+    assert abs(r.centroid(0)[0] - 1.05) < 1e-3 and abs(r.centroid(0)[1] - 2.05) < 1e-3
+
+
+def test_distributed_kmeans_kats(vh):
+    e = vh.DistributedKMeansEngine.emulator(4)                                          # :548-569
+    r = e.fit(np.array([0, 0, .1, .1, -.1, -.1, 10, 10, 10.1, 10.1, 9.9, 9.9], np.float32), 2, 2, 25, 1e-5)
+    assert r.k == 2 and r.dimension == 2 and r.iterations > 0 and r.inertia >= 0
+    c0, c1 = r.centroid(0), r.centroid(1)
+    near0, near10 = (c0, c1) if c0[0] < 5 else (c1, c0)
+    assert np.all(np.abs(near0) < 0.5) and np.all(np.abs(near10 - 10) < 0.5)
+    res = e.fit(np.zeros(0, np.float32), 2, 2, 10, 1e-4)                                # :572-584
+    assert res.k == 0 and res.centroids.size == 0 and res.iterations == 0
+    assert e.fit(np.array([1, 2, 3, 4], np.float32), 2, 0, 10, 1e-4).k == 0
+    r = vh.DistributedKMeansEngine.emulator(8).fit(np.array([1, 1, 2, 2, 3, 3], np.float32), 2, 2, 15, 1e-4)
+    assert r.k == 2 and r.centroids.size == 4                                            # :587-594
+    r = vh.DistributedKMeansEngine.emulator(2).fit(np.array([1, 1, 3, 3, 5, 5, 7, 7], np.float32), 2, 1, 10, 1e-5)
+    assert np.all(np.abs(r.centroid(0) - 4.0) < 1e-3)                                    # :597-606
+    r = vh.DistributedKMeansEngine.emulator(2).fit(np.array([1, 0, .98, .2, 0, 1, .2, .98], np.float32), 2, 2, 20,
+                                                   1e-4, vh.DistanceMetric.CosineSimilarity)
+    assert r.k == 2 and r.dimension == 2                                                 # :609-616
+    assert vh.DistributedKMeansEngine.emulator(6).num_gpus() == 6                         # :619-622
+    assert vh.DistributedKMeansEngine.try_new(1).num_gpus() == 1
+
+
+def test_integration_clustering_then_sharded_search(vh):
+    """integration_tests.rs:7-56."""
+    data = np.concatenate([np.tile([0.1, 0.0, -0.1, 0.05], (30, 1)), np.tile([9.9, 10.1, 10.0, 9.95], (30, 1)),
+                           np.tile([20.0, 19.9, 20.1, 20.05], (30, 1))]).astype(np.float32)
+    r = vh.DistributedKMeansEngine.emulator(4).fit(data, 4, 3, 30, 1e-5)
+    assert r.k == 3 and r.dimension == 4
+    knn = vh.DistributedKnnEngine.emulator(data, 4, 3, vh.GpuShardMode.Sharded)
+    assert knn.num_vectors() == 90
+    res = knn.search(np.full(4, 10.0, np.float32), 5)
+    assert len(res) == 5 and all(30 <= x.id < 60 and x.distance < 1.0 for x in res)
+
+
+# ---- per-iteration parity against the oracle -------------------------------------------
+def _check_step(oracle, data, cent, got, metric, max_flip_frac=1e-4):
+    """got: GPU state after one iteration from `cent`."""
+    ref = oracle.kmeans_step(data, cent, metric, threads=0)
+    ga, ra = got["assign"], ref["assign"]
+    flips = np.nonzero(ga != ra)[0]
+    assert len(flips) <= max(1, int(max_flip_frac * len(data))), f"{len(flips)} assignment flips"
+    for p in flips:  # only near-ties may flip
+        dg = oracle.distance(metric, data[p], cent[ga[p]])
+        dr = oracle.distance(metric, data[p], cent[ra[p]])
+        assert abs(dg - dr) <= 1e-4 * max(1.0, abs(dr)), f"point {p}: {dg} vs {dr} is not a near-tie"
+    k, d = cent.shape
+    # update = mean of the assigned points (float64), empty clusters keep their centroid
+    counts = np.bincount(ga, minlength=k)
+    assert np.array_equal(counts, got["counts"])
+    sums = np.zeros((k, d))
+    np.add.at(sums, ga, data.astype(np.float64))
+    for c in range(k):
+        if counts[c] == 0:
+            assert np.array_equal(got["centroids"][c], cent[c]) and got["shifts"][c] == 0
+            continue
+        want = sums[c] / counts[c]
+        err = np.linalg.norm(got["centroids"][c] - want)
+        assert err <= 1e-4 * max(np.linalg.norm(want), 1e-6), f"centroid {c} off by {err}"
+    # and the oracle's own f32 update wherever membership agrees
+    same = np.ones(k, bool)
+    same[np.unique(np.concatenate([ga[flips], ra[flips]]))] = False
+    for c in np.nonzero(same)[0]:
+        want = ref["centroids"][c]
+        assert np.linalg.norm(got["centroids"][c] - want) <= 1e-4 * max(np.linalg.norm(want), 1e-6)
+    assert abs(got["inertia"] - ref["inertia"]) <= 1e-4 * abs(ref["inertia"]) + 1e-3
+    return len(flips)
+
+
+def test_mixture_10_iterations_parity(vh, oracle):
+    from vector_hip import datasets as ds
+
+    data, _, _ = ds.gaussian_mixture(60_000, 96, 256, ds.SEED_MIXTURE)
+    st = vh.KMeansState(data)
+    cent = data[:256].copy()
+    st.set_centroids(cent)
+    total_flips = 0
+    for it in range(10):
+        st.run(1)
+        got = st.read()
+        total_flips += _check_step(oracle, data, cent, got, "l2")
+        cent = got["centroids"]
+        st.set_centroids(cent)
+    assert total_flips <= 10 * 6
+
+
+@pytest.mark.parametrize("metric", ["dot", "cosine", "l1", "linf", "minkowski", "hellinger", "jaccard", "mahalanobis"])
+def test_other_metrics_one_step(vh, oracle, metric):
+    from vector_hip import datasets as ds
+
+    data, _, _ = ds.gaussian_mixture(8_000, 40, 32, 11)
+    if metric in ("cosine", "dot"):
+        data = data + 3.0  # keep clusters in one orthant so similarity argmax is well posed
+    st = vh.KMeansState(data, vh.DistanceMetric(oracle.METRICS[metric]))
+    cent = data[:32].copy()
+    st.set_centroids(cent)
+    st.run(1)
+    got = st.read()
+    ref = oracle.kmeans_step(data, cent, metric, threads=0)
+    flips = np.nonzero(got["assign"] != ref["assign"])[0]
+    assert len(flips) <= 2
+    if not flips.size:
+        assert np.allclose(got["centroids"], ref["centroids"], rtol=1e-4, atol=1e-5)
+    if metric in ("l1", "linf", "minkowski", "hellinger", "jaccard", "mahalanobis"):
+        assert abs(got["inertia"] - ref["inertia"]) <= 1e-4 * abs(ref["inertia"])
+
+
+def test_fit_deterministic_and_explicit_init(vh, oracle):
+    from vector_hip import datasets as ds
+
+    data, _, _ = ds.gaussian_mixture(30_000, 96, 128, 5)
+    init = data[:128]
+    a, aa = vh.CudaKMeansEngine().fit(data, 96, 128, 6, -1.0, init=init, return_assign=True)
+    b, ba = vh.CudaKMeansEngine().fit(data, 96, 128, 6, -1.0, init=init, return_assign=True)
+    assert a.iterations == 6 and np.array_equal(a.centroids, b.centroids) and np.array_equal(aa, ba)
+    assert a.inertia == b.inertia
+    ref = oracle.kmeans_fit(data, init, 6, -1.0)
+    assert np.mean(ref["assign"] != aa) <= 1e-3
+    # seeded default inits are reproducible too
+    c = vh.CudaKMeansEngine().fit(data, 96, 16, 3, -1.0, seed=9)
+    d = vh.CudaKMeansEngine().fit(data, 96, 16, 3, -1.0, seed=9)
+    assert np.array_equal(c.centroids, d.centroids)
+    e = vh.DistributedKMeansEngine.emulator(1).fit(data, 96, 16, 3, -1.0, seed=9)
+    f = vh.DistributedKMeansEngine.emulator(1).fit(data, 96, 16, 3, -1.0, seed=9)
+    assert np.array_equal(e.centroids, f.centroids)
+
+
+def test_empty_cluster_keeps_centroid(vh):
+    rng = np.random.default_rng(0)
+    data = rng.standard_normal((5000, 16)).astype(np.float32)
+    cent = data[:8].copy()
+    cent[7] = 1000.0
+    st = vh.KMeansState(data)
+    st.set_centroids(cent)
+    st.run(1)
+    got = st.read()
+    assert got["counts"][7] == 0 and np.array_equal(got["centroids"][7], cent[7]) and got["shifts"][7] == 0
+
+
+def test_tolerance_stops_early(vh):
+    r = vh.CudaKMeansEngine().fit(_three_clusters(), 4, 3, 50, 1e-4, init=_three_clusters()[[0, 50, 100]])
+    assert r.iterations == 1  # centroids already at the cluster means

@@ -1,0 +1,99 @@
+// hamming.hip -- packed-bit Hamming distance (popcount of XOR) fused with the threshold
+// filter of the round/merge top-k.
+//
+// The reference only has the thresholded float Hamming (vector-simd/src/scalar.rs:143-153,
+// knn.cu:107-115) over f32 vectors; on 0/1 codes it equals popcount(a ^ b), which is what
+// this kernel computes on 32-bit words (v_xor_b32 + v_bcnt_u32_b32 per word, two VALU
+// operations per word per query).  Each lane owns one query's W words in registers; tiles of
+// base codes are staged in LDS and read as broadcasts.  Distances are exact integers.
+#include "vh_common.h"
+
+namespace vh {
+
+constexpr int kHamRows = 64;
+constexpr long kHamItemRows = 8192;
+
+template <int W>
+__global__ __launch_bounds__(256) void k_hamming_filter(const uint32_t *__restrict__ codes,
+                                                        const uint32_t *__restrict__ perm,
+                                                        const uint32_t *__restrict__ qry,
+                                                        const float *__restrict__ tau, int nq, int wpad,
+                                                        long row_begin, long row_end, int n_qtiles, int n_items,
+                                                        uint2 *__restrict__ cand, uint32_t *__restrict__ cnt,
+                                                        int cap) {
+    __shared__ uint32_t tile[kHamRows * W];
+    const int tid = threadIdx.x;
+    const int G = gridDim.x, g8 = G >> 3;
+    const int slot = (blockIdx.x & 7) * g8 + (blockIdx.x >> 3);
+
+    for (int item = slot; item < n_items; item += G) {
+        const int qtile = item % n_qtiles;
+        const long chunk = item / n_qtiles;
+        const int q = qtile * 256 + tid;
+        const bool qv = q < nq;
+        // tau is a float score; distances are integers, so compare against floor(tau).
+        const float tf = qv ? tau[q] : -1.0f;
+        const uint32_t tq = tf < 0.0f ? 0u : (tf >= 4294967040.0f ? 0xffffffffu : (uint32_t)tf);
+        const bool any = qv && tf >= 0.0f;
+        const long r_lo = row_begin + chunk * kHamItemRows;
+        const long r_hi = min(r_lo + kHamItemRows, row_end);
+
+        uint32_t qw[W];
+#pragma unroll
+        for (int w = 0; w < W; ++w) qw[w] = (qv && w < wpad) ? qry[(long)q * wpad + w] : 0u;
+
+        for (long rs = r_lo; rs < r_hi; rs += kHamRows) {
+            __syncthreads();
+            for (int i = tid; i < kHamRows * W; i += 256) {
+                const int row = i / W, w = i % W;
+                const long r = rs + row;
+                tile[i] = (r < r_hi && w < wpad) ? codes[r * wpad + w] : 0u;
+            }
+            __syncthreads();
+            const int nvalid = (int)min((long)kHamRows, r_hi - rs);
+#pragma unroll 4
+            for (int r = 0; r < kHamRows; ++r) {
+                uint32_t d = 0;
+#pragma unroll
+                for (int w = 0; w < W; ++w) d += (uint32_t)__popc(qw[w] ^ tile[r * W + w]);
+                if (d <= tq && any && r < nvalid) {
+                    const uint32_t at = atomicAdd(&cnt[q], 1u);
+                    if (at < (uint32_t)cap) cand[(size_t)q * cap + at] = make_uint2(score_key((float)d), perm[rs + r]);
+                }
+            }
+        }
+    }
+}
+
+int hamming_word_pad(int words) {
+    int w = 1;
+    while (w < words) w <<= 1;
+    return w;
+}
+
+void launch_hamming_filter(const uint32_t *codes, const uint32_t *perm, const uint32_t *qry, const float *tau,
+                           int nq, int wpad, long row_begin, long row_end, uint2 *cand, uint32_t *cnt, int cap,
+                           int grid_cap, hipStream_t s) {
+    if (nq <= 0 || row_end <= row_begin) return;
+    const int nqt = ceil_div(nq, 256);
+    const long n_chunks = (row_end - row_begin + kHamItemRows - 1) / kHamItemRows;
+    const long items = (long)nqt * n_chunks;
+    long grid = items < grid_cap ? items : grid_cap;
+    grid = (grid + 7) / 8 * 8;
+    const dim3 g((unsigned)grid), b(256);
+    const int it = (int)items;
+#define VH_HAM(W)                                                                                              \
+    hipLaunchKernelGGL(k_hamming_filter<W>, g, b, 0, s, codes, perm, qry, tau, nq, wpad, row_begin, row_end, nqt, \
+                       it, cand, cnt, cap)
+    switch (wpad) {
+        case 1: VH_HAM(1); break;
+        case 2: VH_HAM(2); break;
+        case 4: VH_HAM(4); break;
+        case 8: VH_HAM(8); break;
+        case 16: VH_HAM(16); break;
+        default: VH_HAM(32); break;
+    }
+#undef VH_HAM
+}
+
+}  // namespace vh

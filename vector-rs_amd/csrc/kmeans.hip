@@ -1,0 +1,550 @@
+// kmeans.hip -- Lloyd k-means on one GPU behind the C ABI.
+//
+// Replaces CudaKMeansEngine::fit_gpu (vector-cuda/src/kmeans.rs:99-237) and the kernels of
+// kmeans.cu.  One iteration is:
+//   1. assign   -- fused distance + argmin (MFMA tiles for L2 / dot / cosine in knn_gemm.hip,
+//                  VALU tiles for the other metrics in knn_valu.hip); each point also takes an
+//                  atomic ticket pos[p] in its cluster's count (integer atomics: exact);
+//   2. scan     -- exclusive scan of the k counts into segment offsets;
+//   3. scatter  -- point indices into their cluster segment at offsets[c] + pos[p];
+//   4. update   -- one workgroup per cluster sums its segment in 64-bit fixed point.  Integer
+//                  addition is associative, so the sums -- and every centroid -- are bit-identical
+//                  whatever order the atomics handed out the slots (the reference's float atomics,
+//                  kmeans.cu:298-320, and rayon fold, ivf/kmeans.rs:75-118, are order-dependent).
+//                  The fixed-point scale 2^E is chosen from max|x| and n so no sum can overflow
+//                  and the resolution (2^-E) is far below f32 rounding of the mean.
+//                  new = sum / count; shift = sum_d (new - old)^2; an empty cluster keeps its
+//                  centroid with shift 0 (kmeans.cu:350-356).
+// With tol < 0 no per-iteration host synchronisation happens.
+#include <algorithm>
+#include <cmath>
+#include <memory>
+
+#include "vh_runtime.h"
+
+namespace vh {
+
+bool is_gemm_metric(int m);
+
+// ---- kernels ---------------------------------------------------------------------------
+__global__ void k_absmax_partial(const float *__restrict__ x, size_t count, float *__restrict__ partial) {
+    __shared__ float red[256];
+    float m = 0.0f;
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < count; i += (size_t)gridDim.x * blockDim.x)
+        m = fmaxf(m, fabsf(x[i]));
+    red[threadIdx.x] = m;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+        if ((int)threadIdx.x < o) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + o]);
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) partial[blockIdx.x] = red[0];
+}
+
+// Exclusive scan of counts[k] into offsets[k+1]; one workgroup of 1024 threads.
+__global__ __launch_bounds__(1024) void k_scan_counts(const int32_t *__restrict__ counts, int k,
+                                                      int32_t *__restrict__ offsets) {
+    __shared__ int32_t part[1024];
+    const int t = threadIdx.x;
+    const int per = (k + 1023) / 1024;
+    const int b = t * per, e = min(k, b + per);
+    int32_t s = 0;
+    for (int i = b; i < e; ++i) s += counts[i];
+    part[t] = s;
+    __syncthreads();
+    for (int o = 1; o < 1024; o <<= 1) {
+        const int32_t v = t >= o ? part[t - o] : 0;
+        __syncthreads();
+        part[t] += v;
+        __syncthreads();
+    }
+    int32_t run = t > 0 ? part[t - 1] : 0;
+    for (int i = b; i < e; ++i) {
+        offsets[i] = run;
+        run += counts[i];
+    }
+    if (t == 1023) offsets[k] = part[1023];
+}
+
+__global__ void k_scatter(const int32_t *__restrict__ assign, const int32_t *__restrict__ pos,
+                          const int32_t *__restrict__ offsets, int n, int32_t *__restrict__ sorted) {
+    const int p = blockIdx.x * blockDim.x + threadIdx.x;
+    if (p < n) sorted[offsets[assign[p]] + pos[p]] = p;
+}
+
+// S = number of 64-dimension slots per lane (dpad <= 64 * S).
+template <int S>
+__global__ __launch_bounds__(256) void k_update(const float *__restrict__ pts, int dpad, int dim,
+                                                const int32_t *__restrict__ sorted,
+                                                const int32_t *__restrict__ offsets,
+                                                const int32_t *__restrict__ counts, float *__restrict__ cent,
+                                                float *__restrict__ cnorm, int norm_kind, float *__restrict__ shifts,
+                                                double scale, double inv_scale) {
+    __shared__ long long red[4][64 * S];
+    __shared__ float rs[256], rn[256];
+    const int c = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int cnt = counts[c];
+    if (cnt == 0) {
+        if (tid == 0) shifts[c] = 0.0f;
+        return;
+    }
+    const int off = offsets[c];
+    long long acc[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) acc[s] = 0;
+    for (int i = wave; i < cnt; i += 4) {
+        const float *row = pts + (size_t)sorted[off + i] * dpad;
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            const int d = lane + 64 * s;
+            if (d < dpad) acc[s] += llrint((double)row[d] * scale);
+        }
+    }
+#pragma unroll
+    for (int s = 0; s < S; ++s) red[wave][lane + 64 * s] = acc[s];
+    __syncthreads();
+    float sh = 0.0f, nn = 0.0f;
+    const double inv_cnt = 1.0 / (double)cnt;
+    for (int d = tid; d < dim; d += 256) {
+        const long long sum = red[0][d] + red[1][d] + red[2][d] + red[3][d];
+        const float nv = (float)((double)sum * inv_scale * inv_cnt);
+        float *cp = cent + (size_t)c * dpad + d;
+        const float diff = nv - *cp;
+        sh = fmaf(diff, diff, sh);
+        nn = fmaf(nv, nv, nn);
+        *cp = nv;
+    }
+    rs[tid] = sh;
+    rn[tid] = nn;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+        if (tid < o) {
+            rs[tid] += rs[tid + o];
+            rn[tid] += rn[tid + o];
+        }
+        __syncthreads();
+    }
+    if (tid == 0) {
+        shifts[c] = rs[0];
+        if (norm_kind == 1) cnorm[c] = rn[0];
+        else if (norm_kind == 2) cnorm[c] = sqrtf(rn[0]);
+    }
+}
+
+// Deterministic sum: block b sums its contiguous range in double with a fixed tree.
+__global__ void k_sum_partial(const float *__restrict__ v, size_t count, size_t chunk, double *__restrict__ partial) {
+    __shared__ double red[256];
+    const size_t b0 = blockIdx.x * chunk, e0 = min(count, b0 + chunk);
+    double s = 0.0;
+    for (size_t i = b0 + threadIdx.x; i < e0; i += blockDim.x) s += (double)v[i];
+    red[threadIdx.x] = s;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+        if ((int)threadIdx.x < o) red[threadIdx.x] += red[threadIdx.x + o];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) partial[blockIdx.x] = red[0];
+}
+
+// k-means++ step (CudaKMeansEngine::init_random, kmeans.rs:424-436): mind[i] =
+// min(mind[i], ||x_i - c||^2) in direct form, plus per-block sums of mind in double.
+constexpr int kKppBlock = 4096;
+__global__ __launch_bounds__(256) void k_kpp_update(const float *__restrict__ pts, int dpad, int n,
+                                                    const float *__restrict__ c, float *__restrict__ mind,
+                                                    double *__restrict__ partial) {
+    __shared__ double red[256];
+    const int b0 = blockIdx.x * kKppBlock;
+    double s = 0.0;
+    for (int i = b0 + threadIdx.x; i < min(n, b0 + kKppBlock); i += 256) {
+        const float *x = pts + (size_t)i * dpad;
+        float d2 = 0.0f;
+        for (int d = 0; d < dpad; d += 4) {
+            const float4 xv = *(const float4 *)(x + d);
+            const float4 cv = *(const float4 *)(c + d);
+            const float a0 = xv.x - cv.x, a1 = xv.y - cv.y, a2 = xv.z - cv.z, a3 = xv.w - cv.w;
+            d2 = fmaf(a0, a0, d2);
+            d2 = fmaf(a1, a1, d2);
+            d2 = fmaf(a2, a2, d2);
+            d2 = fmaf(a3, a3, d2);
+        }
+        const float m = fminf(mind[i], d2);
+        mind[i] = m;
+        s += (double)m;
+    }
+    red[threadIdx.x] = s;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+        if ((int)threadIdx.x < o) red[threadIdx.x] += red[threadIdx.x + o];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) partial[blockIdx.x] = red[0];
+}
+
+__global__ void k_fill(float *p, size_t count, float v) {
+    const size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+    if (i < count) p[i] = v;
+}
+
+}  // namespace vh
+
+struct vhip_kmeans {
+    int dev = 0;
+    size_t n = 0, dim = 0, dpad = 0, k = 0;
+    int metric = 0;
+    int grid_cap = 512;
+    double scale = 1.0, inv_scale = 1.0;
+    bool assigned = false;
+    hipStream_t stream = nullptr;
+    vh::DevBuf pts, pnorm, cent, cnorm, assign, pos, inertia, counts, offsets, sorted, shifts, partial;
+    vh::PinnedStager stager;
+    vh::KernelTimer timer;
+    std::mutex mu;
+    ~vhip_kmeans() {
+        if (stream) {
+            (void)hipSetDevice(dev);
+            (void)hipStreamSynchronize(stream);
+            (void)hipStreamDestroy(stream);
+        }
+    }
+};
+
+namespace vh {
+
+static int km_norm_kind(int metric) { return metric == COS ? 2 : (metric == L2 ? 1 : 0); }
+
+static int km_create(int ordinal, const float *data, size_t n, size_t dim, int metric, vhip_kmeans **out) {
+    *out = nullptr;
+    if (dim == 0) return set_error(VHIP_ERR_INVALID_CONFIG, "dimension must be > 0");
+    if (dim > 1024) return set_error(VHIP_ERR_INVALID_CONFIG, "k-means supports dimension <= 1024");
+    if (metric < 0 || metric > 9) return set_error(VHIP_ERR_INVALID_CONFIG, "unknown metric code");
+    if (n == 0 || !data) return set_error(VHIP_ERR_INVALID_CONFIG, "k-means needs at least one point");
+    if (n > 0x7fffffffull) return set_error(VHIP_ERR_INVALID_CONFIG, "k-means supports n < 2^31 points");
+    VH_CHECK(open_device(ordinal));
+    std::unique_ptr<vhip_kmeans> K(new vhip_kmeans());
+    K->dev = ordinal;
+    K->n = n;
+    K->dim = dim;
+    K->dpad = round_up(dim, kKChunk);
+    K->metric = metric;
+    K->grid_cap = device_grid_cap(ordinal);
+    hipStream_t s;
+    VH_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    K->stream = s;
+    VH_CHECK(K->stager.init(ordinal));
+    DevBuf raw;
+    VH_CHECK(raw.ensure(ordinal, n * dim * sizeof(float)));
+    VH_CHECK(K->stager.h2d(raw.p, data, n * dim * sizeof(float), s));
+    VH_CHECK(K->pts.ensure(ordinal, n * K->dpad * sizeof(float)));
+    VH_CHECK(K->pnorm.ensure(ordinal, n * sizeof(float)));
+    launch_rows_prep(raw.as<float>(), n, (int)dim, (int)K->dpad, nullptr, K->pts.as<float>(), K->pnorm.as<float>(),
+                     km_norm_kind(metric), 0, s);
+    // fixed-point scale from max |x|
+    const int nb = 1024;
+    VH_CHECK(K->partial.ensure(ordinal, 8192 * sizeof(double)));
+    hipLaunchKernelGGL(k_absmax_partial, dim3(nb), dim3(256), 0, s, raw.as<float>(), n * dim, K->partial.as<float>());
+    VH_HIP(hipGetLastError());
+    std::vector<float> pm(nb);
+    VH_HIP(hipMemcpyAsync(pm.data(), K->partial.p, nb * sizeof(float), hipMemcpyDeviceToHost, s));
+    VH_HIP(hipStreamSynchronize(s));
+    float mx = 0.0f;
+    for (float v : pm) mx = std::max(mx, v);
+    if (!std::isfinite(mx)) return set_error(VHIP_ERR_INVALID_CONFIG, "data contains non-finite values");
+    // sum over <= n points of |x| * 2^E must stay below 2^62
+    int E = 60;
+    if (mx > 0.0f) {
+        const int ex = (int)std::ceil(std::log2((double)mx)) + (int)std::ceil(std::log2((double)n + 1.0));
+        E = std::min(60, 61 - ex);
+    }
+    K->scale = std::ldexp(1.0, E);
+    K->inv_scale = std::ldexp(1.0, -E);
+    VH_CHECK(K->assign.ensure(ordinal, n * sizeof(int32_t)));
+    VH_CHECK(K->pos.ensure(ordinal, n * sizeof(int32_t)));
+    VH_CHECK(K->inertia.ensure(ordinal, n * sizeof(float)));
+    VH_CHECK(K->sorted.ensure(ordinal, n * sizeof(int32_t)));
+    *out = K.release();
+    return VHIP_OK;
+}
+
+static int km_set_centroids_dev(vhip_kmeans *K, const float *d_c, size_t k, size_t row_stride) {
+    VH_CHECK(K->cent.ensure(K->dev, k * K->dpad * sizeof(float)));
+    VH_CHECK(K->cnorm.ensure(K->dev, k * sizeof(float)));
+    VH_CHECK(K->counts.ensure(K->dev, k * sizeof(int32_t)));
+    VH_CHECK(K->offsets.ensure(K->dev, (k + 1) * sizeof(int32_t)));
+    VH_CHECK(K->shifts.ensure(K->dev, k * sizeof(float)));
+    if (row_stride == K->dim) {
+        launch_rows_prep(d_c, k, (int)K->dim, (int)K->dpad, nullptr, K->cent.as<float>(), K->cnorm.as<float>(),
+                         km_norm_kind(K->metric), 0, K->stream);
+    } else {
+        // d_c already holds padded rows (the k-means++ path builds them in place): copy out
+        // and re-prepare so the norms are computed the same way.
+        DevBuf tmp;
+        VH_CHECK(tmp.ensure(K->dev, k * K->dpad * sizeof(float)));
+        VH_HIP(hipMemcpyAsync(tmp.p, d_c, k * K->dpad * sizeof(float), hipMemcpyDeviceToDevice, K->stream));
+        launch_rows_prep(tmp.as<float>(), k, (int)K->dpad, (int)K->dpad, nullptr, K->cent.as<float>(),
+                         K->cnorm.as<float>(), km_norm_kind(K->metric), 0, K->stream);
+        VH_HIP(hipStreamSynchronize(K->stream));
+    }
+    VH_HIP(hipGetLastError());
+    K->k = k;
+    K->assigned = false;
+    return VHIP_OK;
+}
+
+static int km_iterate(vhip_kmeans *K) {
+    hipStream_t s = K->stream;
+    const int n = (int)K->n, k = (int)K->k;
+    VH_HIP(hipMemsetAsync(K->counts.p, 0, k * sizeof(int32_t), s));
+    const int t = K->timer.begin(s);
+    if (is_gemm_metric(K->metric))
+        launch_kmeans_assign(K->metric, K->cent.as<float>(), K->cnorm.as<float>(), k, K->pts.as<float>(),
+                             K->pnorm.as<float>(), n, (int)K->dpad, K->assign.as<int32_t>(), K->inertia.as<float>(),
+                             K->pos.as<int32_t>(), K->counts.as<int32_t>(), K->grid_cap, s);
+    else
+        launch_kmeans_assign_valu(K->metric, K->cent.as<float>(), k, K->pts.as<float>(), n, (int)K->dpad,
+                                  K->assign.as<int32_t>(), K->inertia.as<float>(), K->pos.as<int32_t>(),
+                                  K->counts.as<int32_t>(), K->grid_cap, s);
+    // algorithmic work: 2*n*k*dim flops (MFMA) or n*k*dim element operations; bytes: points + centroids
+    const double work = (is_gemm_metric(K->metric) ? 2.0 : 1.0) * (double)n * k * (double)K->dim;
+    K->timer.end(t, s, work, ((double)n + k) * K->dim * 4.0);
+    VH_HIP(hipGetLastError());
+    hipLaunchKernelGGL(k_scan_counts, dim3(1), dim3(1024), 0, s, K->counts.as<int32_t>(), k, K->offsets.as<int32_t>());
+    hipLaunchKernelGGL(k_scatter, dim3(ceil_div(n, 256)), dim3(256), 0, s, K->assign.as<int32_t>(),
+                       K->pos.as<int32_t>(), K->offsets.as<int32_t>(), n, K->sorted.as<int32_t>());
+    const int slots = ceil_div((long)K->dpad, 64);
+    const int nk = km_norm_kind(K->metric);
+#define VH_UPD(S)                                                                                                 \
+    hipLaunchKernelGGL(k_update<S>, dim3(k), dim3(256), 0, s, K->pts.as<float>(), (int)K->dpad, (int)K->dim,      \
+                       K->sorted.as<int32_t>(), K->offsets.as<int32_t>(), K->counts.as<int32_t>(), K->cent.as<float>(), \
+                       K->cnorm.as<float>(), nk, K->shifts.as<float>(), K->scale, K->inv_scale)
+    if (slots <= 1) VH_UPD(1);
+    else if (slots <= 2) VH_UPD(2);
+    else if (slots <= 4) VH_UPD(4);
+    else if (slots <= 8) VH_UPD(8);
+    else VH_UPD(16);
+#undef VH_UPD
+    VH_HIP(hipGetLastError());
+    K->assigned = true;
+    return VHIP_OK;
+}
+
+static int km_total_inertia(vhip_kmeans *K, float *out) {
+    const int nb = 256;
+    const size_t chunk = (K->n + nb - 1) / nb;
+    hipLaunchKernelGGL(k_sum_partial, dim3(nb), dim3(256), 0, K->stream, K->inertia.as<float>(), K->n, chunk,
+                       K->partial.as<double>());
+    VH_HIP(hipGetLastError());
+    std::vector<double> part(nb);
+    VH_HIP(hipMemcpyAsync(part.data(), K->partial.p, nb * sizeof(double), hipMemcpyDeviceToHost, K->stream));
+    VH_HIP(hipStreamSynchronize(K->stream));
+    double s = 0.0;
+    for (double v : part) s += v;
+    *out = (float)s;
+    return VHIP_OK;
+}
+
+// Seeded k-means++ (kmeans.rs:409-460): first centre uniform, then each next centre drawn
+// with probability proportional to the squared L2 distance to the nearest chosen centre.
+static int km_init_kmeanspp(vhip_kmeans *K, size_t k, uint64_t seed) {
+    hipStream_t s = K->stream;
+    const int n = (int)K->n;
+    VH_CHECK(K->cent.ensure(K->dev, k * K->dpad * sizeof(float)));
+    DevBuf mind, part;
+    const int nb = ceil_div(n, kKppBlock);
+    VH_CHECK(mind.ensure(K->dev, (size_t)n * sizeof(float)));
+    VH_CHECK(part.ensure(K->dev, (size_t)nb * sizeof(double)));
+    hipLaunchKernelGGL(k_fill, dim3(ceil_div(n, 256)), dim3(256), 0, s, mind.as<float>(), (size_t)n, 3.4028235e38f);
+    uint64_t st = seed;
+    size_t idx = splitmix64(st) % (size_t)n;
+    VH_HIP(hipMemcpyAsync(K->cent.as<float>(), K->pts.as<float>() + idx * K->dpad, K->dpad * sizeof(float),
+                          hipMemcpyDeviceToDevice, s));
+    std::vector<double> ph(nb);
+    std::vector<float> blk(kKppBlock);
+    for (size_t j = 1; j < k; ++j) {
+        hipLaunchKernelGGL(k_kpp_update, dim3(nb), dim3(256), 0, s, K->pts.as<float>(), (int)K->dpad, n,
+                           K->cent.as<float>() + (j - 1) * K->dpad, mind.as<float>(), part.as<double>());
+        VH_HIP(hipGetLastError());
+        VH_HIP(hipMemcpyAsync(ph.data(), part.p, nb * sizeof(double), hipMemcpyDeviceToHost, s));
+        VH_HIP(hipStreamSynchronize(s));
+        double total = 0.0;
+        for (double v : ph) total += v;
+        if (total <= 1e-6) {
+            idx = splitmix64(st) % (size_t)n;
+        } else {
+            const double u = (double)(splitmix64(st) >> 11) * (1.0 / 9007199254740992.0);
+            const double thr = u * total;
+            double cum = 0.0;
+            int b = 0;
+            while (b < nb - 1 && cum + ph[b] < thr) cum += ph[b++];
+            const int b0 = b * kKppBlock, cntb = std::min(kKppBlock, n - b0);
+            VH_HIP(hipMemcpyAsync(blk.data(), mind.as<float>() + b0, cntb * sizeof(float), hipMemcpyDeviceToHost, s));
+            VH_HIP(hipStreamSynchronize(s));
+            idx = 0;
+            for (int i = 0; i < cntb; ++i) {
+                cum += blk[i];
+                if (cum >= thr) {
+                    idx = (size_t)(b0 + i);
+                    break;
+                }
+            }
+        }
+        VH_HIP(hipMemcpyAsync(K->cent.as<float>() + j * K->dpad, K->pts.as<float>() + idx * K->dpad,
+                              K->dpad * sizeof(float), hipMemcpyDeviceToDevice, s));
+    }
+    VH_HIP(hipStreamSynchronize(s));
+    return km_set_centroids_dev(K, K->cent.as<float>(), k, K->dpad);
+}
+
+}  // namespace vh
+
+using namespace vh;
+
+extern "C" {
+
+int vhip_kmeans_create(int ordinal, const float *data, size_t n, size_t dim, int metric, vhip_kmeans **out) {
+    clear_error();
+    if (!out) return set_error(VHIP_ERR_INVALID_CONFIG, "out is null");
+    return km_create(ordinal, data, n, dim, metric, out);
+}
+
+int vhip_kmeans_set_centroids(vhip_kmeans *K, const float *centroids, size_t k) {
+    clear_error();
+    if (!K || !centroids || k == 0) return set_error(VHIP_ERR_INVALID_CONFIG, "null state / centroids or k == 0");
+    if (k > K->n) return set_error(VHIP_ERR_INVALID_CONFIG, "k exceeds the number of points");
+    std::lock_guard<std::mutex> lock(K->mu);
+    VH_CHECK(open_device(K->dev));
+    DevBuf raw;
+    VH_CHECK(raw.ensure(K->dev, k * K->dim * sizeof(float)));
+    VH_CHECK(K->stager.h2d(raw.p, centroids, k * K->dim * sizeof(float), K->stream));
+    VH_CHECK(km_set_centroids_dev(K, raw.as<float>(), k, K->dim));
+    VH_HIP(hipStreamSynchronize(K->stream));
+    return VHIP_OK;
+}
+
+int vhip_kmeans_run(vhip_kmeans *K, size_t iters) {
+    clear_error();
+    if (!K || K->k == 0) return set_error(VHIP_ERR_INVALID_CONFIG, "centroids not set");
+    std::lock_guard<std::mutex> lock(K->mu);
+    VH_CHECK(open_device(K->dev));
+    for (size_t i = 0; i < iters; ++i) VH_CHECK(km_iterate(K));
+    VH_HIP(hipStreamSynchronize(K->stream));
+    K->timer.collect();
+    return VHIP_OK;
+}
+
+int vhip_kmeans_read(vhip_kmeans *K, float *centroids, int32_t *assign, int64_t *counts, float *shifts,
+                     float *max_shift, float *inertia) {
+    clear_error();
+    if (!K) return set_error(VHIP_ERR_INVALID_CONFIG, "null state");
+    std::lock_guard<std::mutex> lock(K->mu);
+    VH_CHECK(open_device(K->dev));
+    hipStream_t s = K->stream;
+    if (centroids && K->k)
+        VH_HIP(hipMemcpy2DAsync(centroids, K->dim * sizeof(float), K->cent.p, K->dpad * sizeof(float),
+                                K->dim * sizeof(float), K->k, hipMemcpyDeviceToHost, s));
+    if (assign && K->assigned)
+        VH_HIP(hipMemcpyAsync(assign, K->assign.p, K->n * sizeof(int32_t), hipMemcpyDeviceToHost, s));
+    std::vector<int32_t> c32(K->k);
+    std::vector<float> sh(K->k);
+    if (K->assigned && K->k) {
+        VH_HIP(hipMemcpyAsync(c32.data(), K->counts.p, K->k * sizeof(int32_t), hipMemcpyDeviceToHost, s));
+        VH_HIP(hipMemcpyAsync(sh.data(), K->shifts.p, K->k * sizeof(float), hipMemcpyDeviceToHost, s));
+    }
+    VH_HIP(hipStreamSynchronize(s));
+    if (counts)
+        for (size_t i = 0; i < K->k; ++i) counts[i] = K->assigned ? c32[i] : 0;
+    if (shifts)
+        for (size_t i = 0; i < K->k; ++i) shifts[i] = K->assigned ? sh[i] : 0.0f;
+    if (max_shift) {
+        float m = 0.0f;
+        if (K->assigned)
+            for (float v : sh) m = std::max(m, v);
+        *max_shift = m;
+    }
+    if (inertia) {
+        *inertia = 0.0f;
+        if (K->assigned) VH_CHECK(km_total_inertia(K, inertia));
+    }
+    return VHIP_OK;
+}
+
+int vhip_kmeans_profile(vhip_kmeans *K, int enable) {
+    if (!K) return set_error(VHIP_ERR_INVALID_CONFIG, "null state");
+    std::lock_guard<std::mutex> lock(K->mu);
+    K->timer.enabled = enable != 0;
+    K->timer.reset();
+    return VHIP_OK;
+}
+
+int vhip_kmeans_profile_read(vhip_kmeans *K, double *kernel_ms, uint64_t *launches, double *work, double *bytes) {
+    if (!K) return set_error(VHIP_ERR_INVALID_CONFIG, "null state");
+    std::lock_guard<std::mutex> lock(K->mu);
+    if (kernel_ms) *kernel_ms = K->timer.ms;
+    if (launches) *launches = K->timer.launches;
+    if (work) *work = K->timer.work;
+    if (bytes) *bytes = K->timer.bytes;
+    return VHIP_OK;
+}
+
+void vhip_kmeans_destroy(vhip_kmeans *K) { delete K; }
+
+int vhip_dkmeans_check(size_t num_gpus) {
+    clear_error();
+    if (num_gpus < 1) return set_error(VHIP_ERR_INVALID_CONFIG, "num_gpus must be at least 1");
+    const size_t avail = (size_t)device_count();
+    if (num_gpus > avail) {
+        set_insufficient(num_gpus, avail);
+        return VHIP_ERR_INSUFFICIENT_DEVICES;
+    }
+    return VHIP_OK;
+}
+
+int vhip_kmeans_fit(int ordinal, const float *data, size_t n, size_t dim, size_t k, size_t max_iters, float tol,
+                    int metric, const float *init_centroids, int init_mode, uint64_t seed, float *out_centroids,
+                    int32_t *out_assign, vhip_kmeans_result *result) {
+    clear_error();
+    if (!result) return set_error(VHIP_ERR_INVALID_CONFIG, "result is null");
+    *result = vhip_kmeans_result{dim, 0, 0, 0.0f};
+    if (n == 0 || k == 0) return VHIP_OK;  // kmeans.rs:67-76
+    const size_t ek = std::min(k, n);
+    if (!out_centroids) return set_error(VHIP_ERR_INVALID_CONFIG, "out_centroids is null");
+    if (init_mode != VHIP_INIT_KMEANSPP && init_mode != VHIP_INIT_SHUFFLE)
+        return set_error(VHIP_ERR_INVALID_CONFIG, "unknown init mode");
+    vhip_kmeans *raw = nullptr;
+    VH_CHECK(km_create(ordinal, data, n, dim, metric, &raw));
+    std::unique_ptr<vhip_kmeans> K(raw);
+    if (init_centroids) {
+        VH_CHECK(vhip_kmeans_set_centroids(K.get(), init_centroids, ek));
+    } else if (init_mode == VHIP_INIT_SHUFFLE) {
+        // DistributedKMeansEngine::init_random (distributed_kmeans.rs:524-535), seeded
+        std::vector<uint32_t> idx = row_permutation(n, seed);
+        std::vector<float> c(ek * dim);
+        for (size_t j = 0; j < ek; ++j) std::memcpy(&c[j * dim], data + (size_t)idx[j] * dim, dim * sizeof(float));
+        VH_CHECK(vhip_kmeans_set_centroids(K.get(), c.data(), ek));
+    } else {
+        VH_CHECK(km_init_kmeanspp(K.get(), ek, seed));
+    }
+    size_t iters = 0;
+    {
+        std::lock_guard<std::mutex> lock(K->mu);
+        VH_CHECK(open_device(K->dev));
+        std::vector<float> sh(ek);
+        for (size_t it = 0; it < max_iters; ++it) {
+            iters = it + 1;
+            VH_CHECK(km_iterate(K.get()));
+            if (tol >= 0.0f) {  // kmeans.rs:218-223: only K floats cross PCIe per iteration
+                VH_HIP(hipMemcpyAsync(sh.data(), K->shifts.p, ek * sizeof(float), hipMemcpyDeviceToHost, K->stream));
+                VH_HIP(hipStreamSynchronize(K->stream));
+                float m = 0.0f;
+                for (float v : sh) m = std::max(m, v);
+                if (m <= tol) break;
+            }
+        }
+        VH_HIP(hipStreamSynchronize(K->stream));
+    }
+    float inertia = 0.0f;
+    VH_CHECK(vhip_kmeans_read(K.get(), out_centroids, out_assign, nullptr, nullptr, nullptr, &inertia));
+    *result = vhip_kmeans_result{dim, ek, iters, inertia};
+    return VHIP_OK;
+}
+
+}  // extern "C"

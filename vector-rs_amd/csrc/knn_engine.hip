@@ -1,0 +1,512 @@
+// knn_engine.hip -- CudaKnnEngine / DistributedKnnEngine replacements behind the C ABI.
+//
+// CudaKnnEngine::with_ordinal (vector-cuda/src/knn.rs:90-140) computed norms and an SoA
+// transpose on one host thread and kept a host copy.  Here the base is uploaded once
+// through pinned staging and laid out on the GPU: rows in a fixed pseudo-random order
+// (so every prefix of the resident base is an unbiased sample of it), padded to a
+// multiple of 32 floats, with per-row norms computed on the device.
+//
+// search_batch (knn.rs:151-310) materialised the Q x N distance matrix.  Here a search
+// is a sequence of rounds over geometrically growing row ranges of the permuted base:
+// the first round keeps every row, later rounds keep only rows whose score is <= the
+// k-th best score found so far (see topk.hip).  A query whose candidate list overflows
+// is re-run with a capacity equal to the largest round, which cannot overflow.
+#include <algorithm>
+#include <cmath>
+#include <memory>
+
+#include "vh_runtime.h"
+
+namespace vh {
+
+constexpr uint64_t kPermSeed = 0x5EEDB45E00000001ull;
+constexpr size_t kQueryBatch = 16384;
+
+bool is_gemm_metric(int m) { return m == L2 || m == DOT || m == COS; }
+
+struct Workspace {
+    DevBuf qraw, qpad, qnorm, tau, have, cnt, flags, nflag, topk, cand, oids, odist;
+};
+
+}  // namespace vh
+
+struct vhip_knn {
+    int dev = 0;
+    size_t n = 0, dim = 0, dpad = 0;
+    int metric = 0;
+    int grid_cap = 512;
+    hipStream_t stream = nullptr;
+    vh::DevBuf base, norm, perm, inv_perm;
+    std::mutex mu;
+    vh::Workspace ws;
+    vh::PinnedStager stager;
+    vh::KernelTimer timer;
+    ~vhip_knn() {
+        if (stream) {
+            (void)hipSetDevice(dev);
+            (void)hipStreamSynchronize(stream);
+            (void)hipStreamDestroy(stream);
+        }
+    }
+};
+
+namespace vh {
+
+static std::vector<std::pair<long, long>> plan_rounds(size_t n, size_t k, int cap) {
+    std::vector<std::pair<long, long>> r;
+    if (n == 0) return r;
+    size_t b = std::min(n, std::max<size_t>(256, 2 * k));
+    size_t g = 1 + (size_t)cap / (8 * std::max<size_t>(k, 1));
+    g = std::min<size_t>(32, std::max<size_t>(4, g));
+    r.emplace_back(0, (long)b);
+    while (b < n) {
+        const size_t e = std::min(n, b * g);
+        r.emplace_back((long)b, (long)e);
+        b = e;
+    }
+    return r;
+}
+
+// Runs all rounds for nq prepared queries; results stay in ws.topk / ws.have.
+static int run_rounds(vhip_knn *E, const float *qpad, const float *qnorm, int nq, int k, int cap, DevBuf &cand,
+                      DevBuf &topk, DevBuf &tau, DevBuf &have, DevBuf &cnt, DevBuf &flags, DevBuf &nflag) {
+    hipStream_t s = E->stream;
+    VH_CHECK(cand.ensure(E->dev, (size_t)nq * cap * sizeof(uint2)));
+    VH_CHECK(topk.ensure(E->dev, (size_t)nq * k * sizeof(unsigned long long)));
+    VH_CHECK(tau.ensure(E->dev, (size_t)nq * sizeof(float)));
+    VH_CHECK(have.ensure(E->dev, (size_t)nq * sizeof(uint32_t)));
+    VH_CHECK(cnt.ensure(E->dev, (size_t)nq * sizeof(uint32_t)));
+    VH_CHECK(flags.ensure(E->dev, (size_t)nq * sizeof(uint32_t)));
+    VH_CHECK(nflag.ensure(E->dev, sizeof(uint32_t)));
+    launch_topk_init(nq, tau.as<float>(), have.as<uint32_t>(), cnt.as<uint32_t>(), flags.as<uint32_t>(), s);
+    VH_HIP(hipMemsetAsync(nflag.p, 0, sizeof(uint32_t), s));
+    const bool gemm = is_gemm_metric(E->metric);
+    // The round plan depends on (n, k) only; `cap` is the storage per query and round.
+    for (auto [rb, re] : plan_rounds(E->n, (size_t)k, kCap)) {
+        // Algorithmic work per launch: 2*Q*rows*D flops (GEMM metrics), Q*rows*D element
+        // operations (VALU metrics) or Q*rows*words word operations (packed Hamming); bytes
+        // are the base rows and queries each launch must read once.
+        const double rows = (double)(re - rb);
+        const double work = gemm ? 2.0 * nq * rows * (double)E->dim : (double)nq * rows * (double)E->dim;
+        const double bytes = rows * E->dim * 4.0 + (double)nq * E->dim * 4.0;
+        const int t = E->timer.begin(s);
+        if (gemm)
+            launch_gemm_filter(E->metric, E->base.as<float>(), E->norm.as<float>(), E->perm.as<uint32_t>(), qpad,
+                               qnorm, tau.as<float>(), nq, (int)E->dpad, rb, re, cand.as<uint2>(),
+                               cnt.as<uint32_t>(), cap, E->grid_cap, s);
+        else if (E->metric == HAMMING_PACKED)
+            launch_hamming_filter(E->base.as<uint32_t>(), E->perm.as<uint32_t>(), (const uint32_t *)qpad,
+                                  tau.as<float>(), nq, (int)E->dpad, rb, re, cand.as<uint2>(), cnt.as<uint32_t>(),
+                                  cap, E->grid_cap, s);
+        else
+            launch_valu_filter(E->metric, E->base.as<float>(), E->perm.as<uint32_t>(), qpad, tau.as<float>(), nq,
+                               (int)E->dim, (int)E->dpad, rb, re, cand.as<uint2>(), cnt.as<uint32_t>(), cap,
+                               E->grid_cap, s);
+        E->timer.end(t, s, work, bytes);
+        VH_HIP(hipGetLastError());
+        launch_topk_merge(nq, k, cand.as<uint2>(), cnt.as<uint32_t>(), cap, topk.as<unsigned long long>(),
+                          have.as<uint32_t>(), tau.as<float>(), flags.as<uint32_t>(), nflag.as<uint32_t>(), s);
+        VH_HIP(hipGetLastError());
+    }
+    return VHIP_OK;
+}
+
+// Searches nq prepared queries (qpad / qnorm on device) for k = effective_k neighbours;
+// writes kout >= k entries per query (the rest marked empty) into device arrays d_ids and
+// d_dist or d_dist_u32 (row stride ostride).
+static int search_prepared(vhip_knn *E, const float *qpad, const float *qnorm, int nq, int k, int kout,
+                           uint32_t *d_ids, float *d_dist, uint32_t *d_dist_u32, int ostride) {
+    Workspace &W = E->ws;
+    hipStream_t s = E->stream;
+    VH_CHECK(run_rounds(E, qpad, qnorm, nq, k, kCap, W.cand, W.topk, W.tau, W.have, W.cnt, W.flags, W.nflag));
+    uint32_t nflag = 0;
+    VH_HIP(hipMemcpyAsync(&nflag, W.nflag.p, sizeof(uint32_t), hipMemcpyDeviceToHost, s));
+    VH_HIP(hipStreamSynchronize(s));
+    if (nflag) {
+        // Overflowed queries: re-run with a capacity of the largest round (cannot overflow).
+        std::vector<uint32_t> flags(nq);
+        VH_HIP(hipMemcpy(flags.data(), W.flags.p, nq * sizeof(uint32_t), hipMemcpyDeviceToHost));
+        std::vector<int> idx;
+        for (int q = 0; q < nq; ++q)
+            if (flags[q]) idx.push_back(q);
+        long big = 0;
+        for (auto [rb, re] : plan_rounds(E->n, (size_t)k, kCap)) big = std::max(big, re - rb);
+        const int cap_big = (int)std::max<long>(big, k);
+        const size_t per_batch = std::max<size_t>(1, ((size_t)1 << 30) / ((size_t)cap_big * sizeof(uint2)));
+        DevBuf fq, fn, fcand, ftopk, ftau, fhave, fcnt, fflags, fnflag;
+        for (size_t b0 = 0; b0 < idx.size(); b0 += per_batch) {
+            const int m = (int)std::min(per_batch, idx.size() - b0);
+            VH_CHECK(fq.ensure(E->dev, (size_t)m * E->dpad * sizeof(float)));
+            VH_CHECK(fn.ensure(E->dev, (size_t)m * sizeof(float)));
+            for (int j = 0; j < m; ++j) {
+                const int q = idx[b0 + j];
+                VH_HIP(hipMemcpyAsync(fq.as<float>() + (size_t)j * E->dpad, qpad + (size_t)q * E->dpad,
+                                      E->dpad * sizeof(float), hipMemcpyDeviceToDevice, s));
+                VH_HIP(hipMemcpyAsync(fn.as<float>() + j, qnorm + q, sizeof(float), hipMemcpyDeviceToDevice, s));
+            }
+            VH_CHECK(run_rounds(E, fq.as<float>(), fn.as<float>(), m, k, cap_big, fcand, ftopk, ftau, fhave, fcnt,
+                                fflags, fnflag));
+            for (int j = 0; j < m; ++j) {
+                const int q = idx[b0 + j];
+                VH_HIP(hipMemcpyAsync(W.topk.as<unsigned long long>() + (size_t)q * k,
+                                      ftopk.as<unsigned long long>() + (size_t)j * k, k * sizeof(unsigned long long),
+                                      hipMemcpyDeviceToDevice, s));
+                VH_HIP(hipMemcpyAsync(W.have.as<uint32_t>() + q, fhave.as<uint32_t>() + j, sizeof(uint32_t),
+                                      hipMemcpyDeviceToDevice, s));
+            }
+        }
+    }
+    if (is_gemm_metric(E->metric) && d_dist)
+        launch_topk_refine(nq, k, kout, E->metric, qpad, E->base.as<float>(), E->inv_perm.as<uint32_t>(),
+                           (int)E->dpad, W.topk.as<unsigned long long>(), W.have.as<uint32_t>(), d_ids, d_dist,
+                           ostride, s);
+    else
+        launch_topk_finalize(nq, k, kout, E->metric, W.topk.as<unsigned long long>(), W.have.as<uint32_t>(), d_ids,
+                             d_dist, d_dist_u32, ostride, s);
+    VH_HIP(hipGetLastError());
+    return VHIP_OK;
+}
+
+static int check_search_args(vhip_knn *E, size_t k) {
+    if (!E) return set_error(VHIP_ERR_INVALID_CONFIG, "null engine");
+    if (k > (size_t)kMaxK)
+        return set_error(VHIP_ERR_INVALID_CONFIG, "k = " + std::to_string(k) + " exceeds VHIP_MAX_K (2048)");
+    return VHIP_OK;
+}
+
+static int norm_kind_of(int metric) { return metric == COS ? 2 : (metric == L2 ? 1 : 0); }
+static int transform_of(int metric) { return metric == HELL ? 1 : 0; }
+
+// Creates an engine over n rows of `dim` 32-bit elements (floats, or packed code words
+// for HAMMING_PACKED, whose rows are padded to a power-of-two word count).
+static int engine_create(const void *base, size_t n, size_t dim, int metric, int ordinal, vhip_knn **out) {
+    clear_error();
+    if (!out) return set_error(VHIP_ERR_INVALID_CONFIG, "out is null");
+    *out = nullptr;
+    if (dim == 0) return set_error(VHIP_ERR_INVALID_CONFIG, "dimension must be > 0");
+    if (metric < 0 || metric > HAMMING_PACKED) return set_error(VHIP_ERR_INVALID_CONFIG, "unknown metric code");
+    if (n > 0xffffffffull) return set_error(VHIP_ERR_INVALID_CONFIG, "more than 2^32 vectors (VectorId is u32)");
+    if (n > 0 && !base) return set_error(VHIP_ERR_INVALID_CONFIG, "base is null");
+    VH_CHECK(open_device(ordinal));
+    std::unique_ptr<vhip_knn> E(new vhip_knn());
+    E->dev = ordinal;
+    E->n = n;
+    E->dim = dim;
+    E->dpad = metric == HAMMING_PACKED ? (size_t)hamming_word_pad((int)dim) : round_up(dim, kKChunk);
+    E->metric = metric;
+    E->grid_cap = device_grid_cap(ordinal);
+    VH_HIP(hipStreamCreateWithFlags(&E->stream, hipStreamNonBlocking));
+    VH_CHECK(E->stager.init(ordinal));
+    if (n > 0) {
+        std::vector<uint32_t> perm = row_permutation(n, kPermSeed);
+        VH_CHECK(E->perm.ensure(ordinal, n * sizeof(uint32_t)));
+        VH_CHECK(E->stager.h2d(E->perm.p, perm.data(), n * sizeof(uint32_t), E->stream));
+        if (is_gemm_metric(metric)) {
+            std::vector<uint32_t> inv(n);
+            for (size_t p = 0; p < n; ++p) inv[perm[p]] = (uint32_t)p;
+            VH_CHECK(E->inv_perm.ensure(ordinal, n * sizeof(uint32_t)));
+            VH_CHECK(E->stager.h2d(E->inv_perm.p, inv.data(), n * sizeof(uint32_t), E->stream));
+        }
+        DevBuf raw;
+        VH_CHECK(raw.ensure(ordinal, n * dim * sizeof(float)));
+        VH_CHECK(E->stager.h2d(raw.p, base, n * dim * sizeof(float), E->stream));
+        VH_CHECK(E->base.ensure(ordinal, n * E->dpad * sizeof(float)));
+        VH_CHECK(E->norm.ensure(ordinal, n * sizeof(float)));
+        launch_rows_prep(raw.as<float>(), n, (int)dim, (int)E->dpad, E->perm.as<uint32_t>(), E->base.as<float>(),
+                         E->norm.as<float>(), norm_kind_of(metric), transform_of(metric), E->stream);
+        VH_HIP(hipGetLastError());
+        VH_HIP(hipStreamSynchronize(E->stream));
+    }
+    *out = E.release();
+    return VHIP_OK;
+}
+
+// Device-side search: d_queries (nq x dim elements), outputs nq x k with row stride k.
+static int engine_search_device(vhip_knn *E, const void *d_queries, size_t nq, size_t k, uint32_t *d_ids,
+                                float *d_dist, uint32_t *d_dist_u32) {
+    clear_error();
+    VH_CHECK(check_search_args(E, k));
+    std::lock_guard<std::mutex> lock(E->mu);
+    VH_CHECK(open_device(E->dev));
+    const size_t ek = std::min(k, E->n);
+    if (nq == 0 || k == 0) return VHIP_OK;
+    if (ek == 0) {
+        VH_HIP(hipMemsetAsync(d_ids, 0xff, nq * k * sizeof(uint32_t), E->stream));
+        VH_HIP(hipStreamSynchronize(E->stream));
+        return VHIP_OK;
+    }
+    Workspace &W = E->ws;
+    for (size_t q0 = 0; q0 < nq; q0 += kQueryBatch) {
+        const int m = (int)std::min(kQueryBatch, nq - q0);
+        VH_CHECK(W.qpad.ensure(E->dev, (size_t)m * E->dpad * sizeof(float)));
+        VH_CHECK(W.qnorm.ensure(E->dev, (size_t)m * sizeof(float)));
+        launch_rows_prep((const float *)d_queries + q0 * E->dim, m, (int)E->dim, (int)E->dpad, nullptr,
+                         W.qpad.as<float>(), W.qnorm.as<float>(), norm_kind_of(E->metric), transform_of(E->metric),
+                         E->stream);
+        VH_HIP(hipGetLastError());
+        VH_CHECK(search_prepared(E, W.qpad.as<float>(), W.qnorm.as<float>(), m, (int)ek, (int)k, d_ids + q0 * k,
+                                 d_dist ? d_dist + q0 * k : nullptr, d_dist_u32 ? d_dist_u32 + q0 * k : nullptr,
+                                 (int)k));
+    }
+    VH_HIP(hipStreamSynchronize(E->stream));
+    E->timer.collect();
+    return VHIP_OK;
+}
+
+// Host-side search through pinned staging.
+static int engine_search_host(vhip_knn *E, const void *queries, size_t nq, size_t k, uint32_t *out_ids,
+                              void *out_dist, bool dist_u32, size_t *out_len) {
+    clear_error();
+    VH_CHECK(check_search_args(E, k));
+    if (nq == 0) return VHIP_OK;
+    if (!queries || !out_len) return set_error(VHIP_ERR_INVALID_CONFIG, "null query/output pointer");
+    const size_t ek = std::min(k, E->n);
+    if (k == 0 || ek == 0) {
+        for (size_t q = 0; q < nq; ++q) out_len[q] = 0;
+        return VHIP_OK;
+    }
+    if (!out_ids || !out_dist) return set_error(VHIP_ERR_INVALID_CONFIG, "null output pointer");
+    DevBuf dq, di, dd;
+    {
+        std::lock_guard<std::mutex> lock(E->mu);
+        VH_CHECK(open_device(E->dev));
+        VH_CHECK(dq.ensure(E->dev, nq * E->dim * sizeof(float)));
+        VH_CHECK(di.ensure(E->dev, nq * k * sizeof(uint32_t)));
+        VH_CHECK(dd.ensure(E->dev, nq * k * sizeof(float)));
+        VH_CHECK(E->stager.h2d(dq.p, queries, nq * E->dim * sizeof(float), E->stream));
+    }
+    VH_CHECK(engine_search_device(E, dq.p, nq, k, di.as<uint32_t>(), dist_u32 ? nullptr : dd.as<float>(),
+                                  dist_u32 ? dd.as<uint32_t>() : nullptr));
+    {
+        std::lock_guard<std::mutex> lock(E->mu);
+        VH_CHECK(open_device(E->dev));
+        VH_CHECK(E->stager.d2h(out_ids, di.p, nq * k * sizeof(uint32_t), E->stream));
+        VH_CHECK(E->stager.d2h(out_dist, dd.p, nq * k * sizeof(float), E->stream));
+    }
+    for (size_t q = 0; q < nq; ++q) out_len[q] = ek;
+    return VHIP_OK;
+}
+
+}  // namespace vh
+
+using namespace vh;
+
+extern "C" {
+
+int vhip_knn_create(const float *base, size_t n, size_t dim, int metric, int ordinal, vhip_knn **out) {
+    if (metric < 0 || metric > 9) {
+        if (out) *out = nullptr;
+        return set_error(VHIP_ERR_INVALID_CONFIG, "unknown metric code");
+    }
+    return engine_create(base, n, dim, metric, ordinal, out);
+}
+
+int vhip_knn_search_batch_device(vhip_knn *E, const float *d_queries, size_t nq, size_t k, uint32_t *d_ids,
+                                 float *d_dist) {
+    return engine_search_device(E, d_queries, nq, k, d_ids, d_dist, nullptr);
+}
+
+int vhip_knn_search_batch(vhip_knn *E, const float *queries, size_t nq, size_t k, uint32_t *out_ids, float *out_dist,
+                          size_t *out_len) {
+    return engine_search_host(E, queries, nq, k, out_ids, out_dist, false, out_len);
+}
+
+size_t vhip_knn_dimension(const vhip_knn *E) { return E ? E->dim : 0; }
+size_t vhip_knn_num_vectors(const vhip_knn *E) { return E ? E->n : 0; }
+int vhip_knn_metric(const vhip_knn *E) { return E ? E->metric : -1; }
+int vhip_knn_device_id(const vhip_knn *E) { return E ? E->dev : -1; }
+
+void vhip_knn_destroy(vhip_knn *E) { delete E; }
+
+int vhip_knn_profile(vhip_knn *E, int enable) {
+    if (!E) return set_error(VHIP_ERR_INVALID_CONFIG, "null engine");
+    std::lock_guard<std::mutex> lock(E->mu);
+    E->timer.enabled = enable != 0;
+    E->timer.reset();
+    return VHIP_OK;
+}
+
+int vhip_knn_profile_read(vhip_knn *E, double *kernel_ms, uint64_t *launches, double *work, double *bytes) {
+    if (!E) return set_error(VHIP_ERR_INVALID_CONFIG, "null engine");
+    std::lock_guard<std::mutex> lock(E->mu);
+    if (kernel_ms) *kernel_ms = E->timer.ms;
+    if (launches) *launches = E->timer.launches;
+    if (work) *work = E->timer.work;
+    if (bytes) *bytes = E->timer.bytes;
+    return VHIP_OK;
+}
+
+// ---- packed-bit Hamming engine: the same resident layout and round pipeline over
+// uint32 code words (HAMMING_PACKED) ----------------------------------------------------
+struct vhip_hamming {
+    vhip_knn *e = nullptr;
+    ~vhip_hamming() { vhip_knn_destroy(e); }
+};
+
+int vhip_hamming_create(const uint32_t *codes, size_t n, size_t words, int ordinal, vhip_hamming **out) {
+    if (!out) return set_error(VHIP_ERR_INVALID_CONFIG, "out is null");
+    *out = nullptr;
+    if (words == 0 || words > 32) return set_error(VHIP_ERR_INVALID_CONFIG, "words must be in 1..32 (<= 1024 bits)");
+    std::unique_ptr<vhip_hamming> H(new vhip_hamming());
+    VH_CHECK(engine_create(codes, n, words, HAMMING_PACKED, ordinal, &H->e));
+    *out = H.release();
+    return VHIP_OK;
+}
+
+int vhip_hamming_search_batch(vhip_hamming *H, const uint32_t *queries, size_t nq, size_t k, uint32_t *out_ids,
+                              uint32_t *out_dist, size_t *out_len) {
+    if (!H) return set_error(VHIP_ERR_INVALID_CONFIG, "null engine");
+    return engine_search_host(H->e, queries, nq, k, out_ids, out_dist, true, out_len);
+}
+
+int vhip_hamming_search_batch_device(vhip_hamming *H, const uint32_t *d_queries, size_t nq, size_t k,
+                                     uint32_t *d_ids, uint32_t *d_dist) {
+    if (!H) return set_error(VHIP_ERR_INVALID_CONFIG, "null engine");
+    return engine_search_device(H->e, d_queries, nq, k, d_ids, nullptr, d_dist);
+}
+
+int vhip_hamming_profile(vhip_hamming *H, int enable) {
+    if (!H) return set_error(VHIP_ERR_INVALID_CONFIG, "null engine");
+    return vhip_knn_profile(H->e, enable);
+}
+
+int vhip_hamming_profile_read(vhip_hamming *H, double *kernel_ms, uint64_t *launches, double *work, double *bytes) {
+    if (!H) return set_error(VHIP_ERR_INVALID_CONFIG, "null engine");
+    return vhip_knn_profile_read(H->e, kernel_ms, launches, work, bytes);
+}
+
+void vhip_hamming_destroy(vhip_hamming *H) { delete H; }
+
+}  // extern "C"
+
+// ============================ DistributedKnnEngine ==========================================
+struct vhip_dknn {
+    size_t num_gpus = 1, dim = 0, n = 0;
+    int mode = VHIP_SHARD_SHARDED, metric = 0;
+    std::vector<vhip_knn *> ranks;
+    std::vector<size_t> offsets;
+    ~vhip_dknn() {
+        for (auto *r : ranks) vhip_knn_destroy(r);
+    }
+};
+
+static int dknn_init(const float *base, size_t n, size_t dim, size_t num_gpus, int mode, int metric, bool emulate,
+                     vhip_dknn **out) {
+    // DistributedKnnEngine::init_engine (distributed_knn.rs:91-146)
+    std::unique_ptr<vhip_dknn> D(new vhip_dknn());
+    const size_t g = std::min(num_gpus, std::max<size_t>(n, 1));
+    D->num_gpus = g;
+    D->dim = dim;
+    D->n = n;
+    D->mode = mode;
+    D->metric = metric;
+    if (mode == VHIP_SHARD_SHARDED) {
+        const size_t chunk = (n + g - 1) / g;
+        for (size_t r = 0; r < g; ++r) {
+            const size_t s0 = r * chunk;
+            const size_t e0 = std::min(s0 + chunk, n);
+            const size_t cnt = s0 < n ? e0 - s0 : 0;
+            vhip_knn *e = nullptr;
+            VH_CHECK(vhip_knn_create(cnt ? base + s0 * dim : nullptr, cnt, dim, metric, emulate ? 0 : (int)r, &e));
+            D->ranks.push_back(e);
+            D->offsets.push_back(s0);
+        }
+    } else {
+        for (size_t r = 0; r < g; ++r) {
+            vhip_knn *e = nullptr;
+            VH_CHECK(vhip_knn_create(base, n, dim, metric, emulate ? 0 : (int)r, &e));
+            D->ranks.push_back(e);
+            D->offsets.push_back(0);
+        }
+    }
+    *out = D.release();
+    return VHIP_OK;
+}
+
+extern "C" {
+
+int vhip_dknn_try_new(const float *base, size_t n, size_t dim, size_t num_gpus, int mode, int metric,
+                      vhip_dknn **out) {
+    clear_error();
+    if (!out) return set_error(VHIP_ERR_INVALID_CONFIG, "out is null");
+    *out = nullptr;
+    if (num_gpus < 1) return set_error(VHIP_ERR_INVALID_CONFIG, "num_gpus must be at least 1");
+    if (dim == 0) return set_error(VHIP_ERR_INVALID_CONFIG, "dimension must be > 0");
+    if (mode != VHIP_SHARD_SHARDED && mode != VHIP_SHARD_REPLICATED)
+        return set_error(VHIP_ERR_INVALID_CONFIG, "unknown GpuShardMode");
+    const size_t avail = (size_t)device_count();
+    if (num_gpus > avail) {
+        set_insufficient(num_gpus, avail);
+        return VHIP_ERR_INSUFFICIENT_DEVICES;
+    }
+    return dknn_init(base, n, dim, num_gpus, mode, metric, false, out);
+}
+
+int vhip_dknn_emulator(const float *base, size_t n, size_t dim, size_t num_gpus, int mode, int metric,
+                       vhip_dknn **out) {
+    clear_error();
+    if (!out) return set_error(VHIP_ERR_INVALID_CONFIG, "out is null");
+    *out = nullptr;
+    if (num_gpus < 1) return set_error(VHIP_ERR_INVALID_CONFIG, "num_gpus must be at least 1");
+    if (dim == 0) return set_error(VHIP_ERR_INVALID_CONFIG, "dimension must be > 0");
+    if (mode != VHIP_SHARD_SHARDED && mode != VHIP_SHARD_REPLICATED)
+        return set_error(VHIP_ERR_INVALID_CONFIG, "unknown GpuShardMode");
+    return dknn_init(base, n, dim, num_gpus, mode, metric, true, out);
+}
+
+int vhip_dknn_search_batch(vhip_dknn *D, const float *queries, size_t nq, size_t k, uint32_t *out_ids,
+                           float *out_dist, size_t *out_len) {
+    clear_error();
+    if (!D) return set_error(VHIP_ERR_INVALID_CONFIG, "null engine");
+    if (nq == 0) return VHIP_OK;
+    if (k == 0 || D->n == 0) {
+        for (size_t q = 0; q < nq; ++q) out_len[q] = 0;
+        return VHIP_OK;
+    }
+    const size_t g = D->ranks.size();
+    const bool hib = D->metric == DOT || D->metric == COS;
+    if (D->mode == VHIP_SHARD_SHARDED) {
+        // distributed_knn.rs:163-199: every rank searches all queries on its shard, ids are
+        // shifted by the shard offset, then each query's lists are merged by top_k_reduce.
+        std::vector<std::vector<uint32_t>> rid(g, std::vector<uint32_t>(nq * k));
+        std::vector<std::vector<float>> rdist(g, std::vector<float>(nq * k));
+        std::vector<std::vector<size_t>> rlen(g, std::vector<size_t>(nq));
+        for (size_t r = 0; r < g; ++r) {
+            VH_CHECK(vhip_knn_search_batch(D->ranks[r], queries, nq, k, rid[r].data(), rdist[r].data(),
+                                           rlen[r].data()));
+        }
+        std::vector<uint32_t> ids;
+        std::vector<float> dist;
+        for (size_t q = 0; q < nq; ++q) {
+            ids.clear();
+            dist.clear();
+            for (size_t r = 0; r < g; ++r)
+                for (size_t j = 0; j < rlen[r][q]; ++j) {
+                    ids.push_back((uint32_t)(rid[r][q * k + j] + D->offsets[r]));
+                    dist.push_back(rdist[r][q * k + j]);
+                }
+            out_len[q] = top_k_reduce_host(ids.data(), dist.data(), ids.size(), k, hib, out_ids + q * k,
+                                           out_dist + q * k);
+        }
+    } else {
+        // distributed_knn.rs:201-229: split queries into ceil(Q/G) chunks, concatenate.
+        const size_t qc = (nq + g - 1) / g;
+        for (size_t r = 0; r < g; ++r) {
+            const size_t q0 = r * qc;
+            if (q0 >= nq) break;
+            const size_t m = std::min(qc, nq - q0);
+            VH_CHECK(vhip_knn_search_batch(D->ranks[r], queries + q0 * D->dim, m, k, out_ids + q0 * k,
+                                           out_dist + q0 * k, out_len + q0));
+        }
+    }
+    return VHIP_OK;
+}
+
+size_t vhip_dknn_num_gpus(const vhip_dknn *D) { return D ? D->num_gpus : 0; }
+int vhip_dknn_mode(const vhip_dknn *D) { return D ? D->mode : -1; }
+size_t vhip_dknn_dimension(const vhip_dknn *D) { return D ? D->dim : 0; }
+size_t vhip_dknn_num_vectors(const vhip_dknn *D) { return D ? D->n : 0; }
+int vhip_dknn_metric(const vhip_dknn *D) { return D ? D->metric : -1; }
+void vhip_dknn_destroy(vhip_dknn *D) { delete D; }
+
+}  // extern "C"

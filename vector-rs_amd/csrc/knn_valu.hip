@@ -1,0 +1,271 @@
+// knn_valu.hip -- non-contraction metrics on the vector ALUs, fused with the threshold
+// filter of the round/merge top-k (topk.hip).
+//
+// Replaces the metric switch of knn_compute_distance_matrix (vector-cuda/src/kernels/knn.cu:84-141,
+// 175-195) for L1, Minkowski p=3, L-inf, thresholded Hamming, Mahalanobis (sqrt of direct
+// L2), weighted Jaccard and Hellinger (direct L2 of sqrt|x|, then sqrt(0.5 * sum)).  Each lane owns
+// one query held in registers; a workgroup of 256 lanes streams tiles of base rows through LDS and
+// every wave reads each base element as a broadcast ds_read_b128 (all lanes the same address), so a
+// base element costs two VALU operations per query (sub + add/max with the |x| modifier).  Values
+// are computed in the direct form of the reference CPU engine (scalar.rs:81-263), so reported
+// distances follow it closely.
+#include "vh_common.h"
+
+namespace vh {
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+constexpr int kValuRows = 16;          // base rows per LDS tile
+constexpr long kValuItemRows = 2048;   // base rows per work item
+
+// k-means Hellinger: centroids are means of the raw data, so sqrt(|x|) of the centroid
+// side is taken in the loop (the point side holds sqrt(|p|)).
+constexpr int HELL_RAW = 11;
+
+template <int M>
+__device__ __forceinline__ void accum(float &a, float &b, float q, float x) {
+    if constexpr (M == HELL_RAW) {
+        const float d = q - sqrtf(fabsf(x));
+        a = fmaf(d, d, a);
+    } else if constexpr (M == L1) {
+        a += fabsf(q - x);
+    } else if constexpr (M == L2 || M == MAHA || M == HELL) {
+        const float d = q - x;
+        a = fmaf(d, d, a);
+    } else if constexpr (M == LINF) {
+        a = fmaxf(a, fabsf(q - x));
+    } else if constexpr (M == MINK) {
+        const float d = fabsf(q - x);
+        a = fmaf(d * d, d, a);
+    } else if constexpr (M == HAMF) {
+        a += fabsf(q - x) > 1e-6f ? 1.0f : 0.0f;
+    } else {  // JACC: q holds |q|
+        const float ax = fabsf(x);
+        a += fminf(q, ax);
+        b += fmaxf(q, ax);
+    }
+}
+
+template <int M>
+__device__ __forceinline__ float finish(float a, float b) {
+    if constexpr (M == MINK) return cbrtf(a);
+    else if constexpr (M == MAHA) return sqrtf(a);
+    else if constexpr (M == HELL || M == HELL_RAW) return sqrtf(0.5f * a);
+    else if constexpr (M == JACC) return b <= 1e-9f ? 0.0f : 1.0f - a / b;
+    else return a;
+}
+
+// DC: dimensions per chunk held in registers (64 or 128).
+template <int M, int DC>
+__global__ __launch_bounds__(256) void k_valu_filter(const float *__restrict__ base, const uint32_t *__restrict__ perm,
+                                                     const float *__restrict__ qry, const float *__restrict__ tau,
+                                                     int nq, int dpad, long row_begin, long row_end, int n_qtiles,
+                                                     int n_items, uint2 *__restrict__ cand,
+                                                     uint32_t *__restrict__ cnt, int cap) {
+    constexpr int V4 = DC / 4;
+    __shared__ floatx4 tile[kValuRows * V4];
+    const int tid = threadIdx.x;
+    const int nchunks = (dpad + DC - 1) / DC;
+    const int G = gridDim.x, g8 = G >> 3;
+    const int slot = (blockIdx.x & 7) * g8 + (blockIdx.x >> 3);
+
+    for (int item = slot; item < n_items; item += G) {
+        const int qtile = item % n_qtiles;
+        const long chunk = item / n_qtiles;
+        const int q = qtile * 256 + tid;
+        const bool qv = q < nq;
+        const float tq = qv ? tau[q] : -INFINITY;
+        const long r_lo = row_begin + chunk * kValuItemRows;
+        const long r_hi = min(r_lo + kValuItemRows, row_end);
+
+        float qr[DC];
+        auto load_q = [&](int c) {
+#pragma unroll
+            for (int i = 0; i < V4; ++i) {
+                const int d = c * DC + 4 * i;
+                floatx4 v = (qv && d < dpad) ? *(const floatx4 *)(qry + (long)q * dpad + d) : floatx4{0, 0, 0, 0};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) qr[4 * i + j] = (M == JACC) ? fabsf(v[j]) : v[j];
+            }
+        };
+        if (nchunks == 1) load_q(0);
+
+        for (long rs = r_lo; rs < r_hi; rs += kValuRows) {
+            float a[kValuRows], b[kValuRows];
+#pragma unroll
+            for (int r = 0; r < kValuRows; ++r) a[r] = b[r] = 0.0f;
+            for (int c = 0; c < nchunks; ++c) {
+                if (nchunks > 1) load_q(c);
+                __syncthreads();
+                for (int i = tid; i < kValuRows * V4; i += 256) {
+                    const int row = i / V4, c4 = i % V4;
+                    const long r = rs + row;
+                    const int d = c * DC + 4 * c4;
+                    tile[i] = (r < r_hi && d < dpad) ? *(const floatx4 *)(base + r * (long)dpad + d)
+                                                     : floatx4{0, 0, 0, 0};
+                }
+                __syncthreads();
+#pragma unroll
+                for (int r = 0; r < kValuRows; ++r) {
+#pragma unroll
+                    for (int i = 0; i < V4; ++i) {
+                        const floatx4 x = tile[r * V4 + i];
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) accum<M>(a[r], b[r], qr[4 * i + j], x[j]);
+                    }
+                }
+            }
+            const int nvalid = (int)min((long)kValuRows, r_hi - rs);
+#pragma unroll
+            for (int r = 0; r < kValuRows; ++r) {
+                const float v = finish<M>(a[r], b[r]);
+                if (v <= tq && r < nvalid && qv) {
+                    const uint32_t at = atomicAdd(&cnt[q], 1u);
+                    if (at < (uint32_t)cap) cand[(size_t)q * cap + at] = make_uint2(score_key(v), perm[rs + r]);
+                }
+            }
+        }
+    }
+}
+
+template <int M>
+static void launch_m(int dpad, dim3 g, hipStream_t s, const float *base, const uint32_t *perm, const float *qry,
+                     const float *tau, int nq, long rb, long re, int nqt, int items, uint2 *cand, uint32_t *cnt,
+                     int cap) {
+    if (dpad <= 128 && dpad > 64)
+        hipLaunchKernelGGL((k_valu_filter<M, 128>), g, dim3(256), 0, s, base, perm, qry, tau, nq, dpad, rb, re, nqt,
+                           items, cand, cnt, cap);
+    else
+        hipLaunchKernelGGL((k_valu_filter<M, 64>), g, dim3(256), 0, s, base, perm, qry, tau, nq, dpad, rb, re, nqt,
+                           items, cand, cnt, cap);
+}
+
+void launch_valu_filter(int metric, const float *base, const uint32_t *perm, const float *qry, const float *tau,
+                        int nq, int dim, int dpad, long row_begin, long row_end, uint2 *cand, uint32_t *cnt, int cap,
+                        int grid_cap, hipStream_t s) {
+    (void)dim;
+    if (nq <= 0 || row_end <= row_begin) return;
+    const int nqt = ceil_div(nq, 256);
+    const long n_chunks = (row_end - row_begin + kValuItemRows - 1) / kValuItemRows;
+    const long items = (long)nqt * n_chunks;
+    long grid = items < grid_cap ? items : grid_cap;
+    grid = (grid + 7) / 8 * 8;
+    const dim3 g((unsigned)grid);
+    const int it = (int)items;
+    switch (metric) {
+        case L1: launch_m<L1>(dpad, g, s, base, perm, qry, tau, nq, row_begin, row_end, nqt, it, cand, cnt, cap); break;
+        case MINK: launch_m<MINK>(dpad, g, s, base, perm, qry, tau, nq, row_begin, row_end, nqt, it, cand, cnt, cap); break;
+        case LINF: launch_m<LINF>(dpad, g, s, base, perm, qry, tau, nq, row_begin, row_end, nqt, it, cand, cnt, cap); break;
+        case HAMF: launch_m<HAMF>(dpad, g, s, base, perm, qry, tau, nq, row_begin, row_end, nqt, it, cand, cnt, cap); break;
+        case MAHA: launch_m<MAHA>(dpad, g, s, base, perm, qry, tau, nq, row_begin, row_end, nqt, it, cand, cnt, cap); break;
+        case JACC: launch_m<JACC>(dpad, g, s, base, perm, qry, tau, nq, row_begin, row_end, nqt, it, cand, cnt, cap); break;
+        case HELL: launch_m<HELL>(dpad, g, s, base, perm, qry, tau, nq, row_begin, row_end, nqt, it, cand, cnt, cap); break;
+        default: break;
+    }
+}
+
+// ---------------------------------------------------------------------------------
+// k-means assignment for the non-contraction metrics (kmeans.cu:172-271): one lane per
+// point (held in registers), centroid tiles broadcast from LDS, running argmin with a
+// strict '<' in ascending centroid order (lowest index wins ties).  Per-point inertia is the
+// metric value (kmeans.cu convention).
+// ---------------------------------------------------------------------------------
+template <int M, int DC>
+__global__ __launch_bounds__(256) void k_kmeans_assign_valu(const float *__restrict__ cent, int k,
+                                                            const float *__restrict__ pts, int n, int dpad,
+                                                            int n_tiles, int32_t *__restrict__ assign,
+                                                            float *__restrict__ inertia, int32_t *__restrict__ pos,
+                                                            int32_t *__restrict__ counts) {
+    constexpr int V4 = DC / 4;
+    __shared__ floatx4 tile[kValuRows * V4];
+    const int tid = threadIdx.x;
+    const int nchunks = (dpad + DC - 1) / DC;
+    for (int t = blockIdx.x; t < n_tiles; t += gridDim.x) {
+        const int p = t * 256 + tid;
+        const bool pv = p < n;
+        float pr[DC];
+        auto load_p = [&](int c) {
+#pragma unroll
+            for (int i = 0; i < V4; ++i) {
+                const int d = c * DC + 4 * i;
+                floatx4 v = (pv && d < dpad) ? *(const floatx4 *)(pts + (long)p * dpad + d) : floatx4{0, 0, 0, 0};
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    pr[4 * i + j] = (M == JACC) ? fabsf(v[j]) : (M == HELL_RAW ? sqrtf(fabsf(v[j])) : v[j]);
+            }
+        };
+        if (nchunks == 1) load_p(0);
+        float best = INFINITY;
+        int bi = 0;
+        for (int cs = 0; cs < k; cs += kValuRows) {
+            float a[kValuRows], b[kValuRows];
+#pragma unroll
+            for (int r = 0; r < kValuRows; ++r) a[r] = b[r] = 0.0f;
+            for (int c = 0; c < nchunks; ++c) {
+                if (nchunks > 1) load_p(c);
+                __syncthreads();
+                for (int i = tid; i < kValuRows * V4; i += 256) {
+                    const int row = i / V4, c4 = i % V4;
+                    const int r = cs + row;
+                    const int d = c * DC + 4 * c4;
+                    tile[i] = (r < k && d < dpad) ? *(const floatx4 *)(cent + (long)r * dpad + d)
+                                                  : floatx4{0, 0, 0, 0};
+                }
+                __syncthreads();
+#pragma unroll
+                for (int r = 0; r < kValuRows; ++r) {
+#pragma unroll
+                    for (int i = 0; i < V4; ++i) {
+                        const floatx4 x = tile[r * V4 + i];
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) accum<M>(a[r], b[r], pr[4 * i + j], x[j]);
+                    }
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < kValuRows; ++r) {
+                const float v = finish<M>(a[r], b[r]);
+                if (v < best && cs + r < k) {
+                    best = v;
+                    bi = cs + r;
+                }
+            }
+        }
+        if (pv) {
+            assign[p] = bi;
+            inertia[p] = best;
+            pos[p] = atomicAdd(&counts[bi], 1);
+        }
+    }
+}
+
+template <int M>
+static void launch_km(int dpad, dim3 g, hipStream_t s, const float *cent, int k, const float *pts, int n, int tiles,
+                      int32_t *assign, float *inertia, int32_t *pos, int32_t *counts) {
+    if (dpad <= 128 && dpad > 64)
+        hipLaunchKernelGGL((k_kmeans_assign_valu<M, 128>), g, dim3(256), 0, s, cent, k, pts, n, dpad, tiles, assign,
+                           inertia, pos, counts);
+    else
+        hipLaunchKernelGGL((k_kmeans_assign_valu<M, 64>), g, dim3(256), 0, s, cent, k, pts, n, dpad, tiles, assign,
+                           inertia, pos, counts);
+}
+
+void launch_kmeans_assign_valu(int metric, const float *cent, int k, const float *pts, int n, int dpad,
+                               int32_t *assign, float *inertia, int32_t *pos, int32_t *counts, int grid_cap,
+                               hipStream_t s) {
+    if (n <= 0 || k <= 0) return;
+    const int tiles = ceil_div(n, 256);
+    const dim3 g(tiles < grid_cap ? tiles : grid_cap);
+    switch (metric) {
+        case L1: launch_km<L1>(dpad, g, s, cent, k, pts, n, tiles, assign, inertia, pos, counts); break;
+        case MINK: launch_km<MINK>(dpad, g, s, cent, k, pts, n, tiles, assign, inertia, pos, counts); break;
+        case LINF: launch_km<LINF>(dpad, g, s, cent, k, pts, n, tiles, assign, inertia, pos, counts); break;
+        case HAMF: launch_km<HAMF>(dpad, g, s, cent, k, pts, n, tiles, assign, inertia, pos, counts); break;
+        case MAHA: launch_km<MAHA>(dpad, g, s, cent, k, pts, n, tiles, assign, inertia, pos, counts); break;
+        case JACC: launch_km<JACC>(dpad, g, s, cent, k, pts, n, tiles, assign, inertia, pos, counts); break;
+        case HELL: launch_km<HELL_RAW>(dpad, g, s, cent, k, pts, n, tiles, assign, inertia, pos, counts); break;
+        default: break;
+    }
+}
+
+}  // namespace vh

@@ -1,0 +1,618 @@
+"""vector_hip -- Python view of the MI355X kNN / k-means library (libvector_hip.so).
+
+The classes mirror the reference's Rust API of the GPU hot path (crate vector-cuda), so
+code written against it reads the same:
+
+* ``CudaDeviceContext.device_count()``                 device.rs:112-117
+* ``CudaKnnEngine(dataset, dimension, metric)``          knn.rs:85-401
+* ``DistributedKnnEngine.try_new / emulator / new``    ddp/distributed_knn.rs:40-262
+* ``CollectiveOps.top_k_reduce``                       ddp/collective.rs:115-159
+* ``CudaKMeansEngine().fit(...)``                      kmeans.rs:43-467
+* ``DistributedKMeansEngine.try_new / emulator``       ddp/distributed_kmeans.rs:25-541
+* ``CudaError`` and its variants                      error.rs:7-29
+* ``HammingKnnEngine``                                 packed-bit extension (no counterpart)
+
+Everything runs in the HIP library; there is no CPU fallback.  If the library is not
+built, importing this package raises ImportError.
+"""
+from __future__ import annotations
+
+import ctypes
+import enum
+import os
+from typing import List, NamedTuple, Optional, Sequence
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libvector_hip.so")
+
+if not os.path.exists(LIB_PATH):
+    raise ImportError(f"{LIB_PATH} is not built; run __graft_entry__.build() (make -C vector-rs_amd)")
+
+_lib = ctypes.CDLL(LIB_PATH)
+
+_f32p = ctypes.POINTER(ctypes.c_float)
+_u32p = ctypes.POINTER(ctypes.c_uint32)
+_i32p = ctypes.POINTER(ctypes.c_int32)
+_i64p = ctypes.POINTER(ctypes.c_int64)
+_u64p = ctypes.POINTER(ctypes.c_uint64)
+_szp = ctypes.POINTER(ctypes.c_size_t)
+_dblp = ctypes.POINTER(ctypes.c_double)
+_vp = ctypes.c_void_p
+_sz = ctypes.c_size_t
+_int = ctypes.c_int
+
+
+class _KMeansResultC(ctypes.Structure):
+    _fields_ = [("dimension", ctypes.c_size_t), ("k", ctypes.c_size_t), ("iterations", ctypes.c_size_t),
+                ("inertia", ctypes.c_float)]
+
+
+def _sig(name, restype, *argtypes):
+    f = getattr(_lib, name)
+    f.restype = restype
+    f.argtypes = list(argtypes)
+    return f
+
+
+_sig("vhip_last_error", ctypes.c_char_p)
+_sig("vhip_last_error_devices", None, _szp, _szp)
+_sig("vhip_device_count", _int)
+_sig("vhip_device_info", _int, _int, ctypes.c_char_p, _sz, _szp)
+_sig("vhip_knn_create", _int, _f32p, _sz, _sz, _int, _int, ctypes.POINTER(_vp))
+_sig("vhip_knn_search_batch", _int, _vp, _f32p, _sz, _sz, _u32p, _f32p, _szp)
+_sig("vhip_knn_search_batch_device", _int, _vp, _vp, _sz, _sz, _vp, _vp)
+_sig("vhip_knn_dimension", _sz, _vp)
+_sig("vhip_knn_num_vectors", _sz, _vp)
+_sig("vhip_knn_metric", _int, _vp)
+_sig("vhip_knn_device_id", _int, _vp)
+_sig("vhip_knn_destroy", None, _vp)
+_sig("vhip_knn_profile", _int, _vp, _int)
+_sig("vhip_knn_profile_read", _int, _vp, _dblp, _u64p, _dblp, _dblp)
+_sig("vhip_dknn_try_new", _int, _f32p, _sz, _sz, _sz, _int, _int, ctypes.POINTER(_vp))
+_sig("vhip_dknn_emulator", _int, _f32p, _sz, _sz, _sz, _int, _int, ctypes.POINTER(_vp))
+_sig("vhip_dknn_search_batch", _int, _vp, _f32p, _sz, _sz, _u32p, _f32p, _szp)
+_sig("vhip_dknn_num_gpus", _sz, _vp)
+_sig("vhip_dknn_mode", _int, _vp)
+_sig("vhip_dknn_dimension", _sz, _vp)
+_sig("vhip_dknn_num_vectors", _sz, _vp)
+_sig("vhip_dknn_metric", _int, _vp)
+_sig("vhip_dknn_destroy", None, _vp)
+_sig("vhip_top_k_reduce", _sz, _u32p, _f32p, _sz, _sz, _int, _u32p, _f32p)
+_sig("vhip_hamming_create", _int, _u32p, _sz, _sz, _int, ctypes.POINTER(_vp))
+_sig("vhip_hamming_search_batch", _int, _vp, _u32p, _sz, _sz, _u32p, _u32p, _szp)
+_sig("vhip_hamming_search_batch_device", _int, _vp, _vp, _sz, _sz, _vp, _vp)
+_sig("vhip_hamming_profile", _int, _vp, _int)
+_sig("vhip_hamming_profile_read", _int, _vp, _dblp, _u64p, _dblp, _dblp)
+_sig("vhip_hamming_destroy", None, _vp)
+_sig("vhip_malloc", _int, _int, _sz, ctypes.POINTER(_vp))
+_sig("vhip_free", _int, _int, _vp)
+_sig("vhip_memcpy_htod", _int, _int, _vp, _vp, _sz)
+_sig("vhip_memcpy_dtoh", _int, _int, _vp, _vp, _sz)
+_sig("vhip_synchronize", _int, _int)
+_HAS_KMEANS = hasattr(_lib, "vhip_kmeans_fit")
+if _HAS_KMEANS:
+    _sig("vhip_kmeans_fit", _int, _int, _f32p, _sz, _sz, _sz, _sz, ctypes.c_float, _int, _f32p, _int,
+         ctypes.c_uint64, _f32p, _i32p, ctypes.POINTER(_KMeansResultC))
+    _sig("vhip_dkmeans_check", _int, _sz)
+    _sig("vhip_kmeans_create", _int, _int, _f32p, _sz, _sz, _int, ctypes.POINTER(_vp))
+    _sig("vhip_kmeans_set_centroids", _int, _vp, _f32p, _sz)
+    _sig("vhip_kmeans_run", _int, _vp, _sz)
+    _sig("vhip_kmeans_read", _int, _vp, _f32p, _i32p, _i64p, _f32p, _f32p, _f32p)
+    _sig("vhip_kmeans_profile", _int, _vp, _int)
+    _sig("vhip_kmeans_profile_read", _int, _vp, _dblp, _u64p, _dblp, _dblp)
+    _sig("vhip_kmeans_destroy", None, _vp)
+
+
+# ---- errors: CudaError (error.rs:7-29) ---------------------------------------------------
+class CudaError(Exception):
+    """Base of the error variants; ``code`` is the C status."""
+
+    code = 0
+
+
+class InsufficientDevices(CudaError):
+    code = -1
+
+    def __init__(self, requested: int, available: int, msg: str = ""):
+        super().__init__(msg or f"requested {requested} device(s), but only {available} found")
+        self.requested = requested
+        self.available = available
+
+    def __eq__(self, other):
+        return isinstance(other, InsufficientDevices) and (self.requested, self.available) == (
+            other.requested, other.available)
+
+
+class DeviceNotFound(CudaError):
+    code = -2
+
+
+class DriverError(CudaError):
+    code = -3
+
+
+class HardwareNotAvailable(CudaError):
+    code = -4
+
+
+class InvalidConfig(CudaError):
+    code = -5
+
+
+_ERRORS = {c.code: c for c in (DeviceNotFound, DriverError, HardwareNotAvailable, InvalidConfig)}
+
+
+def _check(status: int):
+    if status == 0:
+        return
+    msg = (_lib.vhip_last_error() or b"").decode()
+    if status == InsufficientDevices.code:
+        r = _sz()
+        a = _sz()
+        _lib.vhip_last_error_devices(ctypes.byref(r), ctypes.byref(a))
+        raise InsufficientDevices(r.value, a.value, msg)
+    raise _ERRORS.get(status, CudaError)(msg)
+
+
+# ---- types ------------------------------------------------------------------------------------
+class DistanceMetric(enum.IntEnum):
+    """vector-index/src/lib.rs:50-94 with the kernel codes of knn.rs:235-246."""
+
+    L2Squared = 0
+    DotProduct = 1
+    CosineSimilarity = 2
+    Manhattan = 3
+    Minkowski = 4
+    Chebyshev = 5
+    Hamming = 6
+    Mahalanobis = 7
+    Jaccard = 8
+    Hellinger = 9
+
+    def higher_is_better(self) -> bool:
+        return self in (DistanceMetric.DotProduct, DistanceMetric.CosineSimilarity)
+
+
+class GpuShardMode(enum.IntEnum):
+    """ddp/distributed_knn.rs:14-19."""
+
+    Sharded = 0
+    Replicated = 1
+
+
+class SearchResult(NamedTuple):
+    """vector-index/src/types.rs:12-20."""
+
+    id: int
+    distance: float
+
+
+def _rows(data, dimension: Optional[int], dtype=np.float32) -> np.ndarray:
+    a = np.ascontiguousarray(data, dtype=dtype)
+    if a.ndim == 1:
+        if dimension is None or dimension <= 0:
+            raise InvalidConfig("dimension must be > 0")
+        if a.size % dimension != 0:
+            raise InvalidConfig(f"data length {a.size} is not a multiple of dimension {dimension}")
+        a = a.reshape(-1, dimension)
+    elif dimension is not None and a.shape[1] != dimension:
+        raise InvalidConfig(f"rows have {a.shape[1]} elements, dimension is {dimension}")
+    return a
+
+
+def _p(a, t):
+    return a.ctypes.data_as(t)
+
+
+def _to_lists(ids, dist, lens) -> List[List[SearchResult]]:
+    return [[SearchResult(int(ids[q, j]), float(dist[q, j])) for j in range(int(lens[q]))]
+            for q in range(ids.shape[0])]
+
+
+class CudaDeviceContext:
+    """device.rs:81-256 (hardware only: there is no software emulator context)."""
+
+    def __init__(self, ordinal: int = 0):
+        name = ctypes.create_string_buffer(256)
+        mem = _sz()
+        _check(_lib.vhip_device_info(ordinal, name, 256, ctypes.byref(mem)))
+        self._id = ordinal
+        self._name = name.value.decode()
+        self._mem = mem.value
+
+    @staticmethod
+    def device_count() -> int:
+        return _lib.vhip_device_count()
+
+    @classmethod
+    def with_ordinal_strict(cls, ordinal: int) -> "CudaDeviceContext":
+        return cls(ordinal)
+
+    def device_id(self) -> int:
+        return self._id
+
+    def device_name(self) -> str:
+        return self._name
+
+    def total_memory_bytes(self) -> int:
+        return self._mem
+
+    def is_hardware_available(self) -> bool:
+        return True
+
+
+class _Profiled:
+    _prof_fn = None
+    _read_fn = None
+
+    def profile(self, enable: bool = True):
+        _check(type(self)._prof_fn(self._h, int(enable)))
+
+    def profile_read(self) -> dict:
+        ms = ctypes.c_double()
+        n = ctypes.c_uint64()
+        w = ctypes.c_double()
+        b = ctypes.c_double()
+        _check(type(self)._read_fn(self._h, ctypes.byref(ms), ctypes.byref(n), ctypes.byref(w), ctypes.byref(b)))
+        return {"kernel_ms": ms.value, "launches": n.value, "work": w.value, "bytes": b.value}
+
+
+class CudaKnnEngine(_Profiled):
+    """knn.rs:45-401: the base is uploaded once and stays resident on the GPU."""
+
+    _prof_fn = _lib.vhip_knn_profile
+    _read_fn = _lib.vhip_knn_profile_read
+
+    def __init__(self, dataset, dimension: Optional[int] = None, metric=DistanceMetric.L2Squared, ordinal: int = 0):
+        base = _rows(dataset, dimension)
+        self._dim = base.shape[1]
+        h = _vp()
+        _check(_lib.vhip_knn_create(_p(base, _f32p), base.shape[0], self._dim, int(metric), ordinal, ctypes.byref(h)))
+        self._h = h
+
+    @classmethod
+    def new(cls, dataset, dimension, metric):
+        return cls(dataset, dimension, metric, 0)
+
+    @classmethod
+    def with_ordinal(cls, dataset, dimension, metric, ordinal):
+        return cls(dataset, dimension, metric, ordinal)
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h:
+            _lib.vhip_knn_destroy(h)
+            self._h = None
+
+    def search_batch_arrays(self, queries, k: int):
+        """Returns (ids[nq, k] u32, dist[nq, k] f32, lens[nq]); entries past lens are empty."""
+        q = _rows(queries, self._dim) if np.asarray(queries).size else np.zeros((0, self._dim), np.float32)
+        nq = q.shape[0]
+        ids = np.empty((nq, max(k, 1)), np.uint32)
+        dist = np.empty((nq, max(k, 1)), np.float32)
+        lens = np.zeros(nq, np.uintp)
+        _check(_lib.vhip_knn_search_batch(self._h, _p(q, _f32p), nq, k, _p(ids, _u32p), _p(dist, _f32p),
+                                          _p(lens, _szp)))
+        return ids[:, :k], dist[:, :k], lens
+
+    def search_batch(self, queries, k: int) -> List[List[SearchResult]]:
+        return _to_lists(*self.search_batch_arrays(queries, k))
+
+    def search(self, query, k: int) -> List[SearchResult]:
+        r = self.search_batch(query, k)
+        return r[0] if r else []
+
+    def search_batch_device(self, d_queries: int, nq: int, k: int, d_ids: int, d_dist: int):
+        """Queries / outputs are device pointers (ints) on the engine's GPU."""
+        _check(_lib.vhip_knn_search_batch_device(self._h, d_queries, nq, k, d_ids, d_dist))
+
+    def dimension(self) -> int:
+        return _lib.vhip_knn_dimension(self._h)
+
+    def num_vectors(self) -> int:
+        return _lib.vhip_knn_num_vectors(self._h)
+
+    def metric(self) -> DistanceMetric:
+        return DistanceMetric(_lib.vhip_knn_metric(self._h))
+
+    def device_id(self) -> int:
+        return _lib.vhip_knn_device_id(self._h)
+
+
+class DistributedKnnEngine:
+    """ddp/distributed_knn.rs:24-262 (all ranks on one GPU)."""
+
+    def __init__(self, handle):
+        self._h = handle
+
+    @classmethod
+    def _make(cls, fn, dataset, dimension, num_gpus, mode, metric):
+        if num_gpus < 1:
+            raise InvalidConfig("num_gpus must be at least 1")
+        base = _rows(dataset, dimension) if np.asarray(dataset).size else np.zeros((0, dimension), np.float32)
+        h = _vp()
+        _check(fn(_p(base, _f32p), base.shape[0], base.shape[1], num_gpus, int(mode), int(metric), ctypes.byref(h)))
+        e = cls(h)
+        e._dim = base.shape[1]
+        return e
+
+    @classmethod
+    def try_new(cls, dataset, dimension, num_gpus, mode=GpuShardMode.Sharded, metric=DistanceMetric.L2Squared):
+        return cls._make(_lib.vhip_dknn_try_new, dataset, dimension, num_gpus, mode, metric)
+
+    @classmethod
+    def emulator(cls, dataset, dimension, num_gpus, mode=GpuShardMode.Sharded, metric=DistanceMetric.L2Squared):
+        return cls._make(_lib.vhip_dknn_emulator, dataset, dimension, num_gpus, mode, metric)
+
+    @classmethod
+    def new(cls, dataset, dimension, num_gpus, mode=GpuShardMode.Sharded, metric=DistanceMetric.L2Squared):
+        return cls.try_new(dataset, dimension, num_gpus, mode, metric)
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h:
+            _lib.vhip_dknn_destroy(h)
+            self._h = None
+
+    def search_batch_arrays(self, queries, k: int):
+        q = _rows(queries, self._dim) if np.asarray(queries).size else np.zeros((0, self._dim), np.float32)
+        nq = q.shape[0]
+        ids = np.empty((nq, max(k, 1)), np.uint32)
+        dist = np.empty((nq, max(k, 1)), np.float32)
+        lens = np.zeros(nq, np.uintp)
+        _check(_lib.vhip_dknn_search_batch(self._h, _p(q, _f32p), nq, k, _p(ids, _u32p), _p(dist, _f32p),
+                                           _p(lens, _szp)))
+        return ids[:, :k], dist[:, :k], lens
+
+    def search_batch(self, queries, k: int) -> List[List[SearchResult]]:
+        return _to_lists(*self.search_batch_arrays(queries, k))
+
+    def search(self, query, k: int) -> List[SearchResult]:
+        r = self.search_batch(query, k)
+        return r[0] if r else []
+
+    def num_gpus(self) -> int:
+        return _lib.vhip_dknn_num_gpus(self._h)
+
+    def mode(self) -> GpuShardMode:
+        return GpuShardMode(_lib.vhip_dknn_mode(self._h))
+
+    def dimension(self) -> int:
+        return _lib.vhip_dknn_dimension(self._h)
+
+    def num_vectors(self) -> int:
+        return _lib.vhip_dknn_num_vectors(self._h)
+
+    def metric(self) -> DistanceMetric:
+        return DistanceMetric(_lib.vhip_dknn_metric(self._h))
+
+
+class CollectiveOps:
+    """ddp/collective.rs: only top_k_reduce is on the single-GPU path."""
+
+    @staticmethod
+    def top_k_reduce(partial_results_per_rank: Sequence[Sequence[SearchResult]], k: int,
+                     metric=DistanceMetric.L2Squared) -> List[SearchResult]:
+        flat = [r for rank in partial_results_per_rank for r in rank]
+        if not flat or k == 0:
+            return []
+        ids = np.array([r[0] for r in flat], np.uint32)
+        dist = np.array([r[1] for r in flat], np.float32)
+        oi = np.empty(k, np.uint32)
+        od = np.empty(k, np.float32)
+        m = _lib.vhip_top_k_reduce(_p(ids, _u32p), _p(dist, _f32p), ids.size, k, int(metric), _p(oi, _u32p),
+                                   _p(od, _f32p))
+        return [SearchResult(int(oi[i]), float(od[i])) for i in range(m)]
+
+
+class HammingKnnEngine(_Profiled):
+    """Packed-bit Hamming kNN over uint32 code words (extension; exact integer distances)."""
+
+    _prof_fn = _lib.vhip_hamming_profile
+    _read_fn = _lib.vhip_hamming_profile_read
+
+    def __init__(self, codes, ordinal: int = 0):
+        c = np.ascontiguousarray(codes, dtype=np.uint32)
+        if c.ndim != 2:
+            raise InvalidConfig("codes must be [n, words]")
+        self._words = c.shape[1]
+        h = _vp()
+        _check(_lib.vhip_hamming_create(_p(c, _u32p), c.shape[0], c.shape[1], ordinal, ctypes.byref(h)))
+        self._h = h
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h:
+            _lib.vhip_hamming_destroy(h)
+            self._h = None
+
+    def search_batch_arrays(self, queries, k: int):
+        q = np.ascontiguousarray(queries, dtype=np.uint32).reshape(-1, self._words)
+        nq = q.shape[0]
+        ids = np.empty((nq, max(k, 1)), np.uint32)
+        dist = np.empty((nq, max(k, 1)), np.uint32)
+        lens = np.zeros(nq, np.uintp)
+        _check(_lib.vhip_hamming_search_batch(self._h, _p(q, _u32p), nq, k, _p(ids, _u32p), _p(dist, _u32p),
+                                              _p(lens, _szp)))
+        return ids[:, :k], dist[:, :k], lens
+
+    def search_batch_device(self, d_queries: int, nq: int, k: int, d_ids: int, d_dist: int):
+        _check(_lib.vhip_hamming_search_batch_device(self._h, d_queries, nq, k, d_ids, d_dist))
+
+
+# ---- k-means -------------------------------------------------------------------------------
+class CudaKMeansResult(NamedTuple):
+    """kmeans.rs:15-35."""
+
+    centroids: np.ndarray
+    dimension: int
+    k: int
+    iterations: int
+    inertia: float
+
+    def centroid(self, i: int) -> np.ndarray:
+        return self.centroids[i]
+
+
+INIT_KMEANSPP = 0
+INIT_SHUFFLE = 1
+
+
+def _kmeans_fit(data, dimension, k, max_iters, tolerance, metric, init, init_mode, seed, ordinal, want_assign):
+    x = _rows(data, dimension) if np.asarray(data).size else np.zeros((0, dimension), np.float32)
+    n, d = x.shape
+    ek = min(k, n)
+    cent = np.zeros((max(ek, 1), d), np.float32)
+    assign = np.zeros(max(n, 1), np.int32) if want_assign else None
+    init_arr = None
+    if init is not None:
+        init_arr = np.ascontiguousarray(init, dtype=np.float32).reshape(-1, d)
+        if init_arr.shape[0] < ek:
+            raise InvalidConfig("init_centroids has fewer than min(k, n) rows")
+    res = _KMeansResultC()
+    _check(_lib.vhip_kmeans_fit(ordinal, _p(x, _f32p), n, d, k, max_iters, float(tolerance), int(metric),
+                                _p(init_arr, _f32p) if init_arr is not None else None, init_mode, seed,
+                                _p(cent, _f32p), _p(assign, _i32p) if assign is not None else None,
+                                ctypes.byref(res)))
+    r = CudaKMeansResult(cent[:res.k].copy(), int(res.dimension), int(res.k), int(res.iterations), float(res.inertia))
+    return (r, assign[:n]) if want_assign else r
+
+
+class CudaKMeansEngine:
+    """kmeans.rs:37-467 -- fit() runs on the GPU; init is k-means++ seeded by `seed`
+    unless explicit init centroids are given."""
+
+    def __init__(self, ordinal: int = 0):
+        self._ord = ordinal
+        self._ctx = CudaDeviceContext(ordinal)
+
+    @classmethod
+    def new(cls):
+        return cls(0)
+
+    def context(self) -> CudaDeviceContext:
+        return self._ctx
+
+    def fit(self, data, dimension, k, max_iters, tolerance, metric=DistanceMetric.L2Squared, init=None,
+            seed: int = 42, return_assign: bool = False):
+        return _kmeans_fit(data, dimension, k, max_iters, tolerance, metric, init, INIT_KMEANSPP, seed, self._ord,
+                           return_assign)
+
+
+class DistributedKMeansEngine:
+    """ddp/distributed_kmeans.rs:19-541 at one GPU: try_new validates the device count and
+    fit() runs on GPU 0 with a seeded shuffle init (the reference's init_random)."""
+
+    def __init__(self, num_gpus: int):
+        if num_gpus < 1:
+            raise InvalidConfig("num_gpus must be at least 1")
+        self._g = num_gpus
+
+    @classmethod
+    def try_new(cls, num_gpus: int):
+        if num_gpus < 1:
+            raise InvalidConfig("num_gpus must be at least 1")
+        _check(_lib.vhip_dkmeans_check(num_gpus))
+        return cls(num_gpus)
+
+    @classmethod
+    def emulator(cls, num_gpus: int):
+        return cls(num_gpus)
+
+    @classmethod
+    def new(cls, num_gpus: int):
+        return cls.try_new(num_gpus)
+
+    def num_gpus(self) -> int:
+        return self._g
+
+    def fit(self, data, dimension, k, max_iters, tolerance, metric=DistanceMetric.L2Squared, init=None,
+            seed: int = 42, return_assign: bool = False):
+        return _kmeans_fit(data, dimension, k, max_iters, tolerance, metric, init, INIT_SHUFFLE, seed, 0,
+                           return_assign)
+
+
+class KMeansState(_Profiled):
+    """Resident k-means state: set centroids, run iterations, read back (per-iteration
+    parity checks and benchmarks)."""
+
+    def __init__(self, data, metric=DistanceMetric.L2Squared, ordinal: int = 0):
+        type(self)._prof_fn = _lib.vhip_kmeans_profile
+        type(self)._read_fn = _lib.vhip_kmeans_profile_read
+        x = _rows(data, None)
+        self._n, self._d = x.shape
+        self._k = 0
+        h = _vp()
+        _check(_lib.vhip_kmeans_create(ordinal, _p(x, _f32p), self._n, self._d, int(metric), ctypes.byref(h)))
+        self._h = h
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h:
+            _lib.vhip_kmeans_destroy(h)
+            self._h = None
+
+    def set_centroids(self, centroids):
+        c = np.ascontiguousarray(centroids, dtype=np.float32).reshape(-1, self._d)
+        self._k = c.shape[0]
+        _check(_lib.vhip_kmeans_set_centroids(self._h, _p(c, _f32p), self._k))
+
+    def run(self, iters: int = 1):
+        _check(_lib.vhip_kmeans_run(self._h, iters))
+
+    def read(self) -> dict:
+        c = np.empty((self._k, self._d), np.float32)
+        a = np.empty(self._n, np.int32)
+        cnt = np.empty(self._k, np.int64)
+        sh = np.empty(self._k, np.float32)
+        ms = np.zeros(1, np.float32)
+        ine = np.zeros(1, np.float32)
+        _check(_lib.vhip_kmeans_read(self._h, _p(c, _f32p), _p(a, _i32p), _p(cnt, _i64p), _p(sh, _f32p),
+                                     _p(ms, _f32p), _p(ine, _f32p)))
+        return {"centroids": c, "assign": a, "counts": cnt, "shifts": sh, "max_shift": float(ms[0]),
+                "inertia": float(ine[0])}
+
+
+# ---- device memory for callers that stage their own inputs ----------------------------
+class DeviceBuffer:
+    """A raw device allocation on one GPU (for the *_device search entry points)."""
+
+    def __init__(self, nbytes: int, ordinal: int = 0):
+        self.ordinal = ordinal
+        self.nbytes = nbytes
+        p = _vp()
+        _check(_lib.vhip_malloc(ordinal, nbytes, ctypes.byref(p)))
+        self.ptr = p.value
+
+    @classmethod
+    def from_host(cls, arr: np.ndarray, ordinal: int = 0) -> "DeviceBuffer":
+        a = np.ascontiguousarray(arr)
+        b = cls(a.nbytes, ordinal)
+        _check(_lib.vhip_memcpy_htod(ordinal, b.ptr, a.ctypes.data, a.nbytes))
+        return b
+
+    def to_host(self, out: np.ndarray) -> np.ndarray:
+        assert out.flags.c_contiguous and out.nbytes <= self.nbytes
+        _check(_lib.vhip_memcpy_dtoh(self.ordinal, out.ctypes.data, self.ptr, out.nbytes))
+        return out
+
+    def free(self):
+        if self.ptr:
+            _check(_lib.vhip_free(self.ordinal, self.ptr))
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def synchronize(ordinal: int = 0):
+    _check(_lib.vhip_synchronize(ordinal))
+
+
+def library_path() -> str:
+    return LIB_PATH
