@@ -274,7 +274,10 @@ int vhip_device_info(int ordinal, char *name, size_t name_len, size_t *total_mem
     hipDeviceProp_t p;
     VH_HIP(hipGetDeviceProperties(&p, ordinal));
     if (name && name_len) {
-        std::string s = std::string("AMD ") + p.name + " (" + p.gcnArchName + ", GPU " + std::to_string(ordinal) + ")";
+        std::string arch(p.gcnArchName);
+        arch = arch.substr(0, arch.find(':'));
+        std::string s = std::string("AMD ") + (p.name[0] ? p.name : "Instinct") + " " + arch + " (GPU " +
+                        std::to_string(ordinal) + ", " + std::to_string(p.multiProcessorCount) + " CUs)";
         std::strncpy(name, s.c_str(), name_len - 1);
         name[name_len - 1] = 0;
     }
