@@ -150,6 +150,24 @@ def bench_kmeans(vh, steps_iters, with_cpu):
     return res
 
 
+def bench_copy(vh, nbytes=1 << 30, reps=5):
+    """Plain device-to-device copy of `nbytes` (the runtime's blit kernel).  Its FETCH_SIZE and
+    WRITE_SIZE counters calibrate the HBM traffic figures of the other kernels."""
+    a = vh.DeviceBuffer(nbytes)
+    b = vh.DeviceBuffer(nbytes)
+    b.copy_from(a)
+    vh.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        b.copy_from(a)
+    vh.synchronize()
+    dt = (time.perf_counter() - t0) / reps
+    return {"metric": "device copy GB/s (read + write)", "value": round(2 * nbytes / dt / 1e9, 1), "unit": "GB/s",
+            "n_gpus": 1, "steps": reps, "warmup": 1, "ms_per_step": round(dt * 1e3, 3), "higher_is_better": True,
+            "scaling": "strong", "vs_baseline": None, "dtype": "u8", "data": "synthetic",
+            "config": {"workload": f"copy_{nbytes >> 20}MiB", "bytes_per_copy": nbytes}}
+
+
 WORKLOADS = {
     "l2int": dict(n=1_000_000, d=128, nq=10_000, k=100, metric="l2", gen="uniform_int",
                   name="knn_l2_int0-255_1000000x128_q10000_k100"),
@@ -221,7 +239,7 @@ def main():
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--workload", default="default",
-                    choices=["default", "kmeans"] + sorted(WORKLOADS))
+                    choices=["default", "kmeans", "copy"] + sorted(WORKLOADS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -234,7 +252,9 @@ def main():
         print("no gfx950 GPU visible", file=sys.stderr)
         sys.exit(1)
     ctx = vh.CudaDeviceContext(0)
-    if args.workload == "kmeans":
+    if args.workload == "copy":
+        out = bench_copy(vh)
+    elif args.workload == "kmeans":
         r = bench_kmeans(vh, 10, not args.no_cpu)
         out = {"metric": METRIC, "value": r["value"], "unit": r["unit"], "n_gpus": 1, "steps": 10, "warmup": 1,
                "ms_per_step": r["ms_per_iteration"], "higher_is_better": True, "scaling": "strong",

@@ -191,6 +191,7 @@ int vhip_malloc(int ordinal, size_t bytes, void **ptr);
 int vhip_free(int ordinal, void *ptr);
 int vhip_memcpy_htod(int ordinal, void *dst, const void *src, size_t bytes);
 int vhip_memcpy_dtoh(int ordinal, void *dst, const void *src, size_t bytes);
+int vhip_memcpy_dtod(int ordinal, void *dst, const void *src, size_t bytes);
 int vhip_synchronize(int ordinal);
 
 #if defined(__GNUC__)

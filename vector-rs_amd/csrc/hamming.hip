@@ -15,7 +15,6 @@ constexpr long kHamItemRows = 8192;
 
 template <int W>
 __global__ __launch_bounds__(256) void k_hamming_filter(const uint32_t *__restrict__ codes,
-                                                        const uint32_t *__restrict__ perm,
                                                         const uint32_t *__restrict__ qry,
                                                         const float *__restrict__ tau, int nq, int wpad,
                                                         long row_begin, long row_end, int n_qtiles, int n_items,
@@ -58,7 +57,7 @@ __global__ __launch_bounds__(256) void k_hamming_filter(const uint32_t *__restri
                 for (int w = 0; w < W; ++w) d += (uint32_t)__popc(qw[w] ^ tile[r * W + w]);
                 if (d <= tq && any && r < nvalid) {
                     const uint32_t at = atomicAdd(&cnt[q], 1u);
-                    if (at < (uint32_t)cap) cand[(size_t)q * cap + at] = make_uint2(score_key((float)d), perm[rs + r]);
+                    if (at < (uint32_t)cap) cand[(size_t)q * cap + at] = make_uint2(score_key((float)d), (uint32_t)(rs + r));
                 }
             }
         }
@@ -71,7 +70,7 @@ int hamming_word_pad(int words) {
     return w;
 }
 
-void launch_hamming_filter(const uint32_t *codes, const uint32_t *perm, const uint32_t *qry, const float *tau,
+void launch_hamming_filter(const uint32_t *codes, const uint32_t *qry, const float *tau,
                            int nq, int wpad, long row_begin, long row_end, uint2 *cand, uint32_t *cnt, int cap,
                            int grid_cap, hipStream_t s) {
     if (nq <= 0 || row_end <= row_begin) return;
@@ -83,7 +82,7 @@ void launch_hamming_filter(const uint32_t *codes, const uint32_t *perm, const ui
     const dim3 g((unsigned)grid), b(256);
     const int it = (int)items;
 #define VH_HAM(W)                                                                                              \
-    hipLaunchKernelGGL(k_hamming_filter<W>, g, b, 0, s, codes, perm, qry, tau, nq, wpad, row_begin, row_end, nqt, \
+    hipLaunchKernelGGL(k_hamming_filter<W>, g, b, 0, s, codes, qry, tau, nq, wpad, row_begin, row_end, nqt, \
                        it, cand, cnt, cap)
     switch (wpad) {
         case 1: VH_HAM(1); break;

@@ -189,7 +189,7 @@ __global__ void k_fill(float *p, size_t count, float v) {
 
 struct vhip_kmeans {
     int dev = 0;
-    size_t n = 0, dim = 0, dpad = 0, k = 0;
+    size_t n = 0, n_pad = 0, dim = 0, dpad = 0, k = 0, kpad = 0;
     int metric = 0;
     int grid_cap = 512;
     double scale = 1.0, inv_scale = 1.0;
@@ -223,6 +223,7 @@ static int km_create(int ordinal, const float *data, size_t n, size_t dim, int m
     std::unique_ptr<vhip_kmeans> K(new vhip_kmeans());
     K->dev = ordinal;
     K->n = n;
+    K->n_pad = round_up(n, kTileCols);
     K->dim = dim;
     K->dpad = round_up(dim, kKChunk);
     K->metric = metric;
@@ -234,10 +235,11 @@ static int km_create(int ordinal, const float *data, size_t n, size_t dim, int m
     DevBuf raw;
     VH_CHECK(raw.ensure(ordinal, n * dim * sizeof(float)));
     VH_CHECK(K->stager.h2d(raw.p, data, n * dim * sizeof(float), s));
-    VH_CHECK(K->pts.ensure(ordinal, n * K->dpad * sizeof(float)));
-    VH_CHECK(K->pnorm.ensure(ordinal, n * sizeof(float)));
-    launch_rows_prep(raw.as<float>(), n, (int)dim, (int)K->dpad, nullptr, K->pts.as<float>(), K->pnorm.as<float>(),
-                     km_norm_kind(metric), 0, s);
+    // points padded to a multiple of 128 rows with zero rows (their results are never written)
+    VH_CHECK(K->pts.ensure(ordinal, K->n_pad * K->dpad * sizeof(float)));
+    VH_CHECK(K->pnorm.ensure(ordinal, K->n_pad * sizeof(float)));
+    launch_rows_prep(raw.as<float>(), n, K->n_pad, (int)dim, (int)K->dpad, nullptr, K->pts.as<float>(),
+                     K->pnorm.as<float>(), km_norm_kind(metric), 0, 0, 0.0f, s);
     // fixed-point scale from max |x|
     const int nb = 1024;
     VH_CHECK(K->partial.ensure(ordinal, 8192 * sizeof(double)));
@@ -265,27 +267,31 @@ static int km_create(int ordinal, const float *data, size_t n, size_t dim, int m
     return VHIP_OK;
 }
 
+// Centroid rows are padded to a multiple of 128 with NaN rows: their scores are NaN and
+// never win the argmin.
 static int km_set_centroids_dev(vhip_kmeans *K, const float *d_c, size_t k, size_t row_stride) {
-    VH_CHECK(K->cent.ensure(K->dev, k * K->dpad * sizeof(float)));
-    VH_CHECK(K->cnorm.ensure(K->dev, k * sizeof(float)));
+    const size_t kpad = round_up(k, kRowAlign);
+    VH_CHECK(K->cent.ensure(K->dev, kpad * K->dpad * sizeof(float)));
+    VH_CHECK(K->cnorm.ensure(K->dev, kpad * sizeof(float)));
     VH_CHECK(K->counts.ensure(K->dev, k * sizeof(int32_t)));
     VH_CHECK(K->offsets.ensure(K->dev, (k + 1) * sizeof(int32_t)));
     VH_CHECK(K->shifts.ensure(K->dev, k * sizeof(float)));
     if (row_stride == K->dim) {
-        launch_rows_prep(d_c, k, (int)K->dim, (int)K->dpad, nullptr, K->cent.as<float>(), K->cnorm.as<float>(),
-                         km_norm_kind(K->metric), 0, K->stream);
+        launch_rows_prep(d_c, k, kpad, (int)K->dim, (int)K->dpad, nullptr, K->cent.as<float>(),
+                         K->cnorm.as<float>(), km_norm_kind(K->metric), 0, 0, __builtin_nanf(""), K->stream);
     } else {
         // d_c already holds padded rows (the k-means++ path builds them in place): copy out
         // and re-prepare so the norms are computed the same way.
         DevBuf tmp;
         VH_CHECK(tmp.ensure(K->dev, k * K->dpad * sizeof(float)));
         VH_HIP(hipMemcpyAsync(tmp.p, d_c, k * K->dpad * sizeof(float), hipMemcpyDeviceToDevice, K->stream));
-        launch_rows_prep(tmp.as<float>(), k, (int)K->dpad, (int)K->dpad, nullptr, K->cent.as<float>(),
-                         K->cnorm.as<float>(), km_norm_kind(K->metric), 0, K->stream);
+        launch_rows_prep(tmp.as<float>(), k, kpad, (int)K->dpad, (int)K->dpad, nullptr, K->cent.as<float>(),
+                         K->cnorm.as<float>(), km_norm_kind(K->metric), 0, 0, __builtin_nanf(""), K->stream);
         VH_HIP(hipStreamSynchronize(K->stream));
     }
     VH_HIP(hipGetLastError());
     K->k = k;
+    K->kpad = kpad;
     K->assigned = false;
     return VHIP_OK;
 }
@@ -296,7 +302,7 @@ static int km_iterate(vhip_kmeans *K) {
     VH_HIP(hipMemsetAsync(K->counts.p, 0, k * sizeof(int32_t), s));
     const int t = K->timer.begin(s);
     if (is_gemm_metric(K->metric))
-        launch_kmeans_assign(K->metric, K->cent.as<float>(), K->cnorm.as<float>(), k, K->pts.as<float>(),
+        launch_kmeans_assign(K->metric, K->cent.as<float>(), K->cnorm.as<float>(), (int)K->kpad, K->pts.as<float>(),
                              K->pnorm.as<float>(), n, (int)K->dpad, K->assign.as<int32_t>(), K->inertia.as<float>(),
                              K->pos.as<int32_t>(), K->counts.as<int32_t>(), K->grid_cap, s);
     else
@@ -347,7 +353,7 @@ static int km_total_inertia(vhip_kmeans *K, float *out) {
 static int km_init_kmeanspp(vhip_kmeans *K, size_t k, uint64_t seed) {
     hipStream_t s = K->stream;
     const int n = (int)K->n;
-    VH_CHECK(K->cent.ensure(K->dev, k * K->dpad * sizeof(float)));
+    VH_CHECK(K->cent.ensure(K->dev, round_up(k, kRowAlign) * K->dpad * sizeof(float)));
     DevBuf mind, part;
     const int nb = ceil_div(n, kKppBlock);
     VH_CHECK(mind.ensure(K->dev, (size_t)n * sizeof(float)));

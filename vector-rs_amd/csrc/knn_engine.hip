@@ -4,7 +4,8 @@
 // transpose on one host thread and kept a host copy.  Here the base is uploaded once
 // through pinned staging and laid out on the GPU: rows in a fixed pseudo-random order
 // (so every prefix of the resident base is an unbiased sample of it), padded to a
-// multiple of 32 floats, with per-row norms computed on the device.
+// multiple of 32 floats, the row count padded to a multiple of 128 with NaN rows, with
+// per-row norms computed on the device (cosine rows are stored L2-normalised).
 //
 // search_batch (knn.rs:151-310) materialised the Q x N distance matrix.  Here a search
 // is a sequence of rounds over geometrically growing row ranges of the permuted base:
@@ -32,8 +33,9 @@ struct Workspace {
 
 struct vhip_knn {
     int dev = 0;
-    size_t n = 0, dim = 0, dpad = 0;
+    size_t n = 0, n_pad = 0, dim = 0, dpad = 0;
     int metric = 0;
+    float norm_max = 0.0f, norm_min = 0.0f;  // extremes of the per-row norm values
     int grid_cap = 512;
     hipStream_t stream = nullptr;
     vh::DevBuf base, norm, perm, inv_perm;
@@ -52,15 +54,18 @@ struct vhip_knn {
 
 namespace vh {
 
+// Row ranges of the search rounds: every boundary but the last is a multiple of the
+// 256-row MFMA stage, and each round is about g times the rows already seen, so a round's
+// expected candidate count per query is about k * g.
 static std::vector<std::pair<long, long>> plan_rounds(size_t n, size_t k, int cap) {
     std::vector<std::pair<long, long>> r;
     if (n == 0) return r;
-    size_t b = std::min(n, std::max<size_t>(256, 2 * k));
+    size_t b = std::min(n, round_up(std::max<size_t>(256, 2 * k), kRowAlign));
     size_t g = 1 + (size_t)cap / (8 * std::max<size_t>(k, 1));
     g = std::min<size_t>(32, std::max<size_t>(4, g));
     r.emplace_back(0, (long)b);
     while (b < n) {
-        const size_t e = std::min(n, b * g);
+        const size_t e = std::min(n, round_up(b * g, kRowAlign));
         r.emplace_back((long)b, (long)e);
         b = e;
     }
@@ -91,21 +96,20 @@ static int run_rounds(vhip_knn *E, const float *qpad, const float *qnorm, int nq
         const double bytes = rows * E->dim * 4.0 + (double)nq * E->dim * 4.0;
         const int t = E->timer.begin(s);
         if (gemm)
-            launch_gemm_filter(E->metric, E->base.as<float>(), E->norm.as<float>(), E->perm.as<uint32_t>(), qpad,
-                               qnorm, tau.as<float>(), nq, (int)E->dpad, rb, re, cand.as<uint2>(),
-                               cnt.as<uint32_t>(), cap, E->grid_cap, s);
+            launch_gemm_filter(E->metric, E->base.as<float>(), E->norm.as<float>(), qpad, qnorm, tau.as<float>(), nq,
+                               (int)E->dpad, rb, re, cand.as<uint2>(), cnt.as<uint32_t>(), cap, E->norm_max,
+                               E->norm_min, E->grid_cap, s);
         else if (E->metric == HAMMING_PACKED)
-            launch_hamming_filter(E->base.as<uint32_t>(), E->perm.as<uint32_t>(), (const uint32_t *)qpad,
-                                  tau.as<float>(), nq, (int)E->dpad, rb, re, cand.as<uint2>(), cnt.as<uint32_t>(),
-                                  cap, E->grid_cap, s);
+            launch_hamming_filter(E->base.as<uint32_t>(), (const uint32_t *)qpad, tau.as<float>(), nq, (int)E->dpad,
+                                  rb, re, cand.as<uint2>(), cnt.as<uint32_t>(), cap, E->grid_cap, s);
         else
-            launch_valu_filter(E->metric, E->base.as<float>(), E->perm.as<uint32_t>(), qpad, tau.as<float>(), nq,
-                               (int)E->dim, (int)E->dpad, rb, re, cand.as<uint2>(), cnt.as<uint32_t>(), cap,
-                               E->grid_cap, s);
+            launch_valu_filter(E->metric, E->base.as<float>(), qpad, tau.as<float>(), nq, (int)E->dim,
+                               (int)E->dpad, rb, re, cand.as<uint2>(), cnt.as<uint32_t>(), cap, E->grid_cap, s);
         E->timer.end(t, s, work, bytes);
         VH_HIP(hipGetLastError());
-        launch_topk_merge(nq, k, cand.as<uint2>(), cnt.as<uint32_t>(), cap, topk.as<unsigned long long>(),
-                          have.as<uint32_t>(), tau.as<float>(), flags.as<uint32_t>(), nflag.as<uint32_t>(), s);
+        launch_topk_merge(nq, k, cand.as<uint2>(), cnt.as<uint32_t>(), cap, E->perm.as<uint32_t>(),
+                          topk.as<unsigned long long>(), have.as<uint32_t>(), tau.as<float>(), flags.as<uint32_t>(),
+                          nflag.as<uint32_t>(), s);
         VH_HIP(hipGetLastError());
     }
     return VHIP_OK;
@@ -136,8 +140,11 @@ static int search_prepared(vhip_knn *E, const float *qpad, const float *qnorm, i
         DevBuf fq, fn, fcand, ftopk, ftau, fhave, fcnt, fflags, fnflag;
         for (size_t b0 = 0; b0 < idx.size(); b0 += per_batch) {
             const int m = (int)std::min(per_batch, idx.size() - b0);
-            VH_CHECK(fq.ensure(E->dev, (size_t)m * E->dpad * sizeof(float)));
-            VH_CHECK(fn.ensure(E->dev, (size_t)m * sizeof(float)));
+            const size_t m_pad = round_up((size_t)m, kTileCols);
+            VH_CHECK(fq.ensure(E->dev, m_pad * E->dpad * sizeof(float)));
+            VH_CHECK(fn.ensure(E->dev, m_pad * sizeof(float)));
+            launch_fill(fq.as<float>() + (size_t)m * E->dpad, (m_pad - m) * E->dpad, 0.0f, s);
+            launch_fill(fn.as<float>() + m, m_pad - m, 0.0f, s);
             for (int j = 0; j < m; ++j) {
                 const int q = idx[b0 + j];
                 VH_HIP(hipMemcpyAsync(fq.as<float>() + (size_t)j * E->dpad, qpad + (size_t)q * E->dpad,
@@ -158,8 +165,8 @@ static int search_prepared(vhip_knn *E, const float *qpad, const float *qnorm, i
     }
     if (is_gemm_metric(E->metric) && d_dist)
         launch_topk_refine(nq, k, kout, E->metric, qpad, E->base.as<float>(), E->inv_perm.as<uint32_t>(),
-                           (int)E->dpad, W.topk.as<unsigned long long>(), W.have.as<uint32_t>(), d_ids, d_dist,
-                           ostride, s);
+                           (int)E->dpad, qnorm, E->norm.as<float>(), W.topk.as<unsigned long long>(),
+                           W.have.as<uint32_t>(), d_ids, d_dist, ostride, s);
     else
         launch_topk_finalize(nq, k, kout, E->metric, W.topk.as<unsigned long long>(), W.have.as<uint32_t>(), d_ids,
                              d_dist, d_dist_u32, ostride, s);
@@ -176,6 +183,7 @@ static int check_search_args(vhip_knn *E, size_t k) {
 
 static int norm_kind_of(int metric) { return metric == COS ? 2 : (metric == L2 ? 1 : 0); }
 static int transform_of(int metric) { return metric == HELL ? 1 : 0; }
+static int normalize_of(int metric) { return metric == COS ? 1 : 0; }
 
 // Creates an engine over n rows of `dim` 32-bit elements (floats, or packed code words
 // for HAMMING_PACKED, whose rows are padded to a power-of-two word count).
@@ -191,6 +199,7 @@ static int engine_create(const void *base, size_t n, size_t dim, int metric, int
     std::unique_ptr<vhip_knn> E(new vhip_knn());
     E->dev = ordinal;
     E->n = n;
+    E->n_pad = round_up(n, kRowAlign);
     E->dim = dim;
     E->dpad = metric == HAMMING_PACKED ? (size_t)hamming_word_pad((int)dim) : round_up(dim, kKChunk);
     E->metric = metric;
@@ -210,11 +219,25 @@ static int engine_create(const void *base, size_t n, size_t dim, int metric, int
         DevBuf raw;
         VH_CHECK(raw.ensure(ordinal, n * dim * sizeof(float)));
         VH_CHECK(E->stager.h2d(raw.p, base, n * dim * sizeof(float), E->stream));
-        VH_CHECK(E->base.ensure(ordinal, n * E->dpad * sizeof(float)));
-        VH_CHECK(E->norm.ensure(ordinal, n * sizeof(float)));
-        launch_rows_prep(raw.as<float>(), n, (int)dim, (int)E->dpad, E->perm.as<uint32_t>(), E->base.as<float>(),
-                         E->norm.as<float>(), norm_kind_of(metric), transform_of(metric), E->stream);
+        VH_CHECK(E->base.ensure(ordinal, E->n_pad * E->dpad * sizeof(float)));
+        VH_CHECK(E->norm.ensure(ordinal, E->n_pad * sizeof(float)));
+        launch_rows_prep(raw.as<float>(), n, E->n_pad, (int)dim, (int)E->dpad, E->perm.as<uint32_t>(),
+                         E->base.as<float>(), E->norm.as<float>(), norm_kind_of(metric), transform_of(metric),
+                         normalize_of(metric), __builtin_nanf(""), E->stream);
         VH_HIP(hipGetLastError());
+        if (norm_kind_of(metric)) {
+            // extremes of the row norms: the L2 filter's rounding slack and the cosine zero-norm guard
+            std::vector<float> nh(n);
+            VH_HIP(hipMemcpyAsync(nh.data(), E->norm.p, n * sizeof(float), hipMemcpyDeviceToHost, E->stream));
+            VH_HIP(hipStreamSynchronize(E->stream));
+            float mx = 0.0f, mn = INFINITY;
+            for (float v : nh) {
+                mx = std::max(mx, v);
+                mn = std::min(mn, v);
+            }
+            E->norm_max = mx;
+            E->norm_min = mn;
+        }
         VH_HIP(hipStreamSynchronize(E->stream));
     }
     *out = E.release();
@@ -238,11 +261,12 @@ static int engine_search_device(vhip_knn *E, const void *d_queries, size_t nq, s
     Workspace &W = E->ws;
     for (size_t q0 = 0; q0 < nq; q0 += kQueryBatch) {
         const int m = (int)std::min(kQueryBatch, nq - q0);
-        VH_CHECK(W.qpad.ensure(E->dev, (size_t)m * E->dpad * sizeof(float)));
-        VH_CHECK(W.qnorm.ensure(E->dev, (size_t)m * sizeof(float)));
-        launch_rows_prep((const float *)d_queries + q0 * E->dim, m, (int)E->dim, (int)E->dpad, nullptr,
+        const size_t m_pad = round_up((size_t)m, kTileCols);
+        VH_CHECK(W.qpad.ensure(E->dev, m_pad * E->dpad * sizeof(float)));
+        VH_CHECK(W.qnorm.ensure(E->dev, m_pad * sizeof(float)));
+        launch_rows_prep((const float *)d_queries + q0 * E->dim, m, m_pad, (int)E->dim, (int)E->dpad, nullptr,
                          W.qpad.as<float>(), W.qnorm.as<float>(), norm_kind_of(E->metric), transform_of(E->metric),
-                         E->stream);
+                         normalize_of(E->metric), 0.0f, E->stream);
         VH_HIP(hipGetLastError());
         VH_CHECK(search_prepared(E, W.qpad.as<float>(), W.qnorm.as<float>(), m, (int)ek, (int)k, d_ids + q0 * k,
                                  d_dist ? d_dist + q0 * k : nullptr, d_dist_u32 ? d_dist_u32 + q0 * k : nullptr,

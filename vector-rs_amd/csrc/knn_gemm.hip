@@ -1,19 +1,38 @@
-// knn_gemm.hip -- fused FP32-MFMA distance tiles + per-query threshold filter.
+// knn_gemm.hip -- FP32-MFMA distance tiles fused with the kNN threshold filter or the
+// k-means argmin.
 //
 // Replaces knn_compute_distance_matrix + knn_topk_select (vector-cuda/src/kernels/knn.cu:21-305)
-// for the GEMM-form metrics (squared L2, dot product, cosine).  Instead of writing the
-// Q x N distance matrix, every workgroup keeps its 128 queries' current threshold tau in
-// registers and emits only the (score, id) pairs with score <= tau into a per-query
-// candidate list; topk.hip merges those lists into the running top-k between rounds.
+// for the GEMM-form metrics (squared L2, dot product, cosine) and the per-thread centroid loop
+// of kmeans_assign_and_accumulate (kmeans.cu:38-285).  The Q x N distance matrix is never
+// written: in FILTER mode every workgroup keeps its 128 queries' current threshold tau in
+// registers and stages only the (score, row) pairs with score <= tau; in ASSIGN mode every
+// lane keeps a running (score, centroid) minimum.
 //
-// Tiling (gfx950, wave64): a workgroup of 4 waves owns a 128-row x 128-query tile; each
-// wave owns a 64 x 64 sub-tile made of 2 x 2 v_mfma_f32_32x32x2f32 blocks (rows = base
-// vectors on the A side, columns = queries on the B side).  Base rows and queries stream
-// through double-buffered LDS in K-chunks of 32 floats; one ds_read_b128 per operand feeds
-// four MFMA k-steps (both operands use the same k permutation, so the contraction is
-// unchanged).  The grid is persistent and XCD-aware: work items (query tile, row chunk) are
-// handed out so that the workgroups resident on one XCD walk the same base rows together
-// and share them through that XCD's L2.
+// Operands: A = rows (resident base vectors, or centroids), B = columns (queries, or points),
+// both row-major with `dpad` floats per row (a multiple of 32, zero filled).  A's row count is
+// padded to a multiple of 256 with NaN rows, so every score they produce is NaN and fails every
+// comparison; B's row count is padded to a multiple of 128.  The inner loop has no bounds checks.
+//
+// Two kernels share the epilogues:
+//  * k_mfma_res (dpad <= 128): a workgroup of 8 waves owns a work item of 128 columns; the
+//    whole 128 x dpad column tile stays resident in LDS for the item, and 256-row stages of A
+//    stream through double-buffered LDS in K-chunks of 32 floats.  Only A crosses the L2 -> CU
+//    path per stage (64 flop per byte).
+//  * k_mfma_stream (dpad > 128): a workgroup of 4 waves streams 128-row x 128-column stages of
+//    both operands in K-chunks (32 flop per byte), two workgroups per CU.
+// Each wave owns a 64 x 64 sub-tile of 2 x 2 v_mfma_f32_32x32x2f32 blocks.  LDS tiles are
+// swizzled for gfx950's LDS (64 banks; a ds_read_b128 serves 16 lanes per pass): within 16
+// consecutive rows, row parity selects the 128-byte half of the banks and (row >> 1) & 7 XORs
+// the 16-byte slot, so the b128 operand reads and the b128 tile stores are conflict-free.
+// The pipeline is continuous: while chunk t is multiplied, chunk t+1 -- which may belong to the
+// next stage or the next work item -- is already in flight from HBM/L2.  The grid is persistent
+// and XCD-aware: work items are handed out so that the workgroups resident on one XCD walk the
+// same base rows together and share them through that XCD's L2.
+//
+// FILTER epilogue: per score two VALU operations decide "may pass" against a slightly loose
+// threshold; only groups of 8 scores in which some lane may pass take the exact path.  Passing
+// (score, row) pairs are appended to per-query LDS slots (LDS atomics) and flushed to the
+// global per-query candidate lists once per work item, with one global atomic per query.
 #include "vh_common.h"
 
 namespace vh {
@@ -21,398 +40,712 @@ namespace vh {
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
-constexpr int kLdsStride = kKChunk + 4;  // 36 floats: 144 B rows keep b128 reads conflict-free
-constexpr int kItemStages = 16;          // 128-row stages per work item (2048 base rows)
+constexpr int kFilter = 0, kAssign = 1;
+constexpr int kItemRows = 2048;  // base rows per kNN work item
+constexpr int kResSlots = 16;    // LDS candidate slots per query per work item (resident kernel)
+constexpr int kStrSlots = 14;    // same for the streaming kernel (two workgroups share a CU's LDS)
+
+// float4 index of (row, c4) in a 32-float-wide swizzled tile
+__device__ __forceinline__ int swz(int row, int c4) { return row * 8 + (c4 ^ ((row >> 1) & 7)); }
 
 // ---------------------------------------------------------------------------------
-// Row preparation: pad to dpad, optional permutation gather, per-row norm.
-// norm_kind: 0 none, 1 squared L2 norm, 2 L2 norm (cosine).
-// One wave per row; the norm is a lane-strided sum followed by a fixed xor butterfly,
-// so it is deterministic.
+// Row preparation: rows [0, n) are copied (optionally gathered through `perm`, optionally
+// sqrt(|x|)-transformed, optionally L2-normalised) into rows of `dpad` floats with zero fill;
+// rows [n, n_out) are filled with `pad_fill`.  norm_kind 1 writes the squared L2 norm,
+// 2 the L2 norm (of the row before normalisation); padding rows get `pad_fill`.
+// One wave per row; the norm is a lane-strided sum followed by a fixed xor butterfly, so
+// it is deterministic.  With norm_kind 0, transform 0 and normalize 0 the copy is bit-exact,
+// so it also moves packed uint32 codes.
 // ---------------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_rows_prep(const float *__restrict__ in, size_t n, int dim, int dpad,
-                                                   const uint32_t *__restrict__ perm, float *__restrict__ out,
-                                                   float *__restrict__ norm, int norm_kind, int transform) {
+__global__ __launch_bounds__(256) void k_rows_prep(const float *__restrict__ in, size_t n, size_t n_out, int dim,
+                                                   int dpad, const uint32_t *__restrict__ perm,
+                                                   float *__restrict__ out, float *__restrict__ norm, int norm_kind,
+                                                   int transform, int normalize, float pad_fill) {
     const int lane = threadIdx.x & 63;
     const size_t wave = (blockIdx.x * (size_t)blockDim.x + threadIdx.x) >> 6;
     const size_t nwaves = (gridDim.x * (size_t)blockDim.x) >> 6;
-    for (size_t p = wave; p < n; p += nwaves) {
+    for (size_t p = wave; p < n_out; p += nwaves) {
+        float *orow = out + p * (size_t)dpad;
+        if (p >= n) {
+            for (int d = lane; d < dpad; d += 64) orow[d] = pad_fill;
+            if (norm && lane == 0) norm[p] = pad_fill;
+            continue;
+        }
         const size_t src = perm ? perm[p] : p;
         const float *row = in + src * (size_t)dim;
-        float *orow = out + p * (size_t)dpad;
         float ss = 0.0f;
         for (int d = lane; d < dpad; d += 64) {
             float v = d < dim ? row[d] : 0.0f;
             if (transform) v = sqrtf(fabsf(v));
-            orow[d] = v;
+            if (!normalize) orow[d] = v;
             ss = fmaf(v, v, ss);
         }
-        if (norm_kind) {
 #pragma unroll
-            for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
-            if (lane == 0) norm[p] = norm_kind == 2 ? sqrtf(ss) : ss;
+        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+        if (normalize) {
+            const float nr = sqrtf(ss);
+            const float inv = nr > 0.0f ? 1.0f / nr : 0.0f;
+            for (int d = lane; d < dpad; d += 64) {
+                float v = d < dim ? row[d] : 0.0f;
+                if (transform) v = sqrtf(fabsf(v));
+                orow[d] = v * inv;
+            }
         }
+        if (norm_kind && lane == 0) norm[p] = norm_kind == 2 ? sqrtf(ss) : ss;
     }
 }
 
-void launch_rows_prep(const float *in, size_t n, int dim, int dpad, const uint32_t *perm, float *out, float *norm,
-                      int norm_kind, int transform, hipStream_t s) {
-    if (n == 0) return;
-    size_t blocks = (n + 3) / 4;
+void launch_rows_prep(const float *in, size_t n, size_t n_out, int dim, int dpad, const uint32_t *perm, float *out,
+                      float *norm, int norm_kind, int transform, int normalize, float pad_fill, hipStream_t s) {
+    if (n_out == 0) return;
+    size_t blocks = (n_out + 3) / 4;
     if (blocks > 65536) blocks = 65536;
-    hipLaunchKernelGGL(k_rows_prep, dim3((unsigned)blocks), dim3(256), 0, s, in, n, dim, dpad, perm, out, norm,
-                       norm_kind, transform);
+    hipLaunchKernelGGL(k_rows_prep, dim3((unsigned)blocks), dim3(256), 0, s, in, n, n_out, dim, dpad, perm, out, norm,
+                       norm_kind, transform, normalize, pad_fill);
 }
 
 // ---------------------------------------------------------------------------------
-// Score of one (query, base row) pair; smaller is better.
-//   L2 : ||q||^2 + ||x||^2 - 2 q.x clamped at 0        (knn.cu:158-163 form)
-//   DOT: -q.x                                           (argmax similarity)
-//   COS: -q.x / (||q|| ||x||), 0 when the product <= 1e-9 (knn.cu:168-173)
+// Kernel arguments.  Work item i covers column tile (i % n_ctiles) and the row range
+// [row_begin + (i / n_ctiles) * item_rows, min(.. + item_rows, row_end)); row_begin and
+// item_rows are multiples of 256 and row_end is a multiple of 256 or the padded end.
 // ---------------------------------------------------------------------------------
-template <int M>
-__device__ __forceinline__ float pair_score(float dot, float qn, float xn) {
-    if constexpr (M == L2) {
-        return fmaxf(fmaf(-2.0f, dot, qn + xn), 0.0f);
-    } else if constexpr (M == DOT) {
-        return -dot;
-    } else {
-        float den = qn * xn;
-        return den > 1e-9f ? -(dot / den) : -0.0f;
-    }
-}
-
-struct Stage {
-    floatx4 a[4];  // 4 x float4 of the base tile chunk per thread
-    floatx4 b[4];  // 4 x float4 of the query tile chunk per thread
+struct ScanArgs {
+    const float *A;      // rows: base vectors / centroids
+    const float *anorm;  // per-row epilogue value: L2 squared norm, cosine norm (NaN on padding rows)
+    const float *B;      // columns: queries / points
+    const float *bnorm;  // per-column norm: L2 squared norm, cosine norm
+    int dpad;
+    int ncols;  // real number of columns
+    int n_ctiles;
+    int n_items;
+    long row_begin, row_end;
+    long item_rows;
+    // FILTER
+    const float *tau;
+    uint2 *cand;
+    uint32_t *cnt;
+    int cap;
+    float anorm_max;  // largest row value of anorm (L2 slack bound)
+    float anorm_min;  // smallest row norm (cosine zero-norm guard)
+    // ASSIGN
+    int32_t *assign;
+    float *inertia;
+    int32_t *pos;
+    int32_t *counts;
 };
 
-__device__ __forceinline__ void load_chunk(Stage &st, const float *__restrict__ base, const float *__restrict__ qry,
-                                           long rs, long r_hi, int q0, int nq, int dpad, int k0) {
-    const int tid = threadIdx.x;
+// -0.0 and +0.0 are the same distance; give them one key.
+__device__ __forceinline__ float canon(float s) { return s + 0.0f; }
+
+// 4 x 16 = 64 MFMAs per wave on one K-chunk.  A / B point at the chunk's float4 rows; `bidx`
+// maps (column row, c4) to the B tile's float4 index.
+template <class BIdx>
+__device__ __forceinline__ void mfma_chunk(floatx16 (&acc)[2][2], const floatx4 *__restrict__ A,
+                                           const floatx4 *__restrict__ B, BIdx bidx, int wr, int wc, int l32,
+                                           int h) {
+    const int ra0 = 64 * wr + l32, ra1 = ra0 + 32;
+    const int rb0 = 64 * wc + l32, rb1 = rb0 + 32;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int f = tid + 256 * i;
-        const int row = f >> 3, c4 = f & 7;
-        const long r = rs + row;
-        st.a[i] = r < r_hi ? *(const floatx4 *)(base + r * (long)dpad + k0 + 4 * c4) : floatx4{0, 0, 0, 0};
-        const int q = q0 + row;
-        st.b[i] = q < nq ? *(const floatx4 *)(qry + (long)q * dpad + k0 + 4 * c4) : floatx4{0, 0, 0, 0};
+    for (int g = 0; g < kKChunk / 8; ++g) {
+        const int c4 = 2 * g + h;
+        const floatx4 a0 = A[swz(ra0, c4)];
+        const floatx4 a1 = A[swz(ra1, c4)];
+        const floatx4 b0 = B[bidx(rb0, c4)];
+        const floatx4 b1 = B[bidx(rb1, c4)];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[t], b0[t], acc[0][0], 0, 0, 0);
+            acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[t], b1[t], acc[0][1], 0, 0, 0);
+            acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[t], b0[t], acc[1][0], 0, 0, 0);
+            acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[t], b1[t], acc[1][1], 0, 0, 0);
+        }
     }
 }
 
-__device__ __forceinline__ void store_chunk(const Stage &st, float *sA, float *sB) {
-    const int tid = threadIdx.x;
+// ---- per-item epilogue state -----------------------------------------------------------
+struct EpiState {
+    float tau_e[2], T[2], cn[2];  // FILTER: exact threshold, loose "may pass" threshold, column norm
+    bool guard;                   // FILTER cosine: some column may meet a near-zero-norm row
+    float bs[2];                  // ASSIGN: running best (score, row)
+    int bi[2];
+};
+
+template <int MODE, int M>
+__device__ __forceinline__ void item_begin(EpiState &st, const ScanArgs &a, int col0, int wc, int l32) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int f = tid + 256 * i;
-        const int row = f >> 3, c4 = f & 7;
-        *(floatx4 *)(sA + row * kLdsStride + 4 * c4) = st.a[i];
-        *(floatx4 *)(sB + row * kLdsStride + 4 * c4) = st.b[i];
+    for (int cb = 0; cb < 2; ++cb) {
+        const int q = col0 + 64 * wc + 32 * cb + l32;
+        const bool v = q < a.ncols;
+        st.cn[cb] = v ? a.bnorm[q] : 0.0f;
+        if constexpr (MODE == kFilter) {
+            const float t = v ? a.tau[q] : -INFINITY;
+            st.tau_e[cb] = t;
+            if constexpr (M == L2) {
+                // |(qn + xn - 2 q.x) - (qn + fl(xn - 2 q.x))| <= 2^-21 (qn + xn); the slack doubles that.
+                st.T[cb] = (t < INFINITY && t > -INFINITY)
+                               ? (t - st.cn[cb]) + 0x1p-19f * (st.cn[cb] + a.anorm_max + fabsf(t))
+                               : t;
+            } else {
+                st.T[cb] = -t;  // score = -dot <= tau  <=>  dot >= -tau (exact)
+            }
+        } else {
+            st.bs[cb] = INFINITY;
+            st.bi[cb] = 0;
+        }
+    }
+    st.guard = false;
+    if constexpr (MODE == kFilter && M == COS) {
+        const bool g0 = (col0 + 64 * wc + l32 < a.ncols) && st.cn[0] * a.anorm_min <= 1e-9f;
+        const bool g1 = (col0 + 64 * wc + 32 + l32 < a.ncols) && st.cn[1] * a.anorm_min <= 1e-9f;
+        st.guard = __builtin_amdgcn_ballot_w64(g0 || g1) != 0;
     }
 }
 
+// FILTER: stage every (score, row) of this stage with score <= tau.  Accumulator register
+// 4g+j of block (rb, cb) holds row 64wr + 32rb + 8g + 4h + j of the stage and column
+// 64wc + 32cb + l32 of the tile.
+template <int M, int SLOTS>
+__device__ __forceinline__ void filter_stage(const floatx16 (&acc)[2][2], const float *nrow, const EpiState &st,
+                                             const ScanArgs &a, int wr, int wc, int l32, int h, long rs, long r_lo,
+                                             int col0, uint32_t *s_qcnt, uint2 *s_slot) {
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int rl0 = 64 * wr + 32 * rb + 8 * g + 4 * h;
+            const floatx4 n4 = *(const floatx4 *)(nrow + rl0);
+            bool p[4][2];
+            bool any = false;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int cb = 0; cb < 2; ++cb) {
+                    const float dot = acc[rb][cb][4 * g + j];
+                    if constexpr (M == L2) p[j][cb] = fmaf(-2.0f, dot, n4[j]) <= st.T[cb];
+                    else p[j][cb] = dot >= st.T[cb];
+                    any = any || p[j][cb];
+                }
+            if (M == COS && st.guard) {
+                // a (query, row) pair with ||q|| ||x|| <= 1e-9 has similarity 0 (knn.cu:168-173)
+                any = false;
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+#pragma unroll
+                    for (int cb = 0; cb < 2; ++cb) {
+                        const float dot = acc[rb][cb][4 * g + j];
+                        const float s = st.cn[cb] * n4[j] > 1e-9f ? -dot : 0.0f * dot;
+                        p[j][cb] = s <= st.tau_e[cb];
+                        any = any || p[j][cb];
+                    }
+            }
+            if (__builtin_amdgcn_ballot_w64(any)) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+#pragma unroll
+                    for (int cb = 0; cb < 2; ++cb) {
+                        if (!p[j][cb]) continue;
+                        const float dot = acc[rb][cb][4 * g + j];
+                        float s;
+                        if constexpr (M == L2) {
+                            s = fmaxf(fmaf(-2.0f, dot, st.cn[cb] + n4[j]), 0.0f);
+                            if (!(s <= st.tau_e[cb])) continue;
+                        } else if constexpr (M == DOT) {
+                            s = canon(-dot);
+                        } else {
+                            s = st.guard ? (st.cn[cb] * n4[j] > 1e-9f ? canon(-dot) : 0.0f) : canon(-dot);
+                        }
+                        const int ql = 64 * wc + 32 * cb + l32;
+                        const uint32_t key = score_key(s);
+                        const uint32_t r = atomicAdd(&s_qcnt[ql], 1u);
+                        if (r < (uint32_t)SLOTS) {
+                            s_slot[ql * SLOTS + r] = make_uint2(key, (uint32_t)(rs - r_lo) + rl0 + j);
+                        } else {
+                            const int q = col0 + ql;
+                            const uint32_t at = atomicAdd(&a.cnt[q], 1u);
+                            if (at < (uint32_t)a.cap)
+                                a.cand[(size_t)q * a.cap + at] = make_uint2(key, (uint32_t)(rs + rl0 + j));
+                        }
+                    }
+            }
+        }
+    }
+}
+
+// FILTER item end: one global atomic per query with staged candidates.  Must be called by
+// all threads; contains a barrier.
+template <int SLOTS>
+__device__ __forceinline__ void filter_flush(const ScanArgs &a, int col0, long r_lo, uint32_t *s_qcnt,
+                                             uint2 *s_slot) {
+    __syncthreads();
+    const int tid = threadIdx.x;
+    if (tid < kTileCols) {
+        uint32_t c = s_qcnt[tid];
+        if (c) {
+            s_qcnt[tid] = 0;
+            c = min(c, (uint32_t)SLOTS);
+            const int q = col0 + tid;
+            const uint32_t base = atomicAdd(&a.cnt[q], c);
+            for (uint32_t j = 0; j < c; ++j) {
+                if (base + j < (uint32_t)a.cap) {
+                    const uint2 e = s_slot[tid * SLOTS + j];
+                    a.cand[(size_t)q * a.cap + base + j] = make_uint2(e.x, (uint32_t)(r_lo + e.y));
+                }
+            }
+        }
+    }
+}
+
+// ASSIGN: per column, the minimum score over this stage's 32 rows held by the lane, then the
+// first (lowest) row reaching it.  Rows are visited in ascending order with a strict '<' across
+// stages, so the lowest index wins ties (kmeans.cu:110-114).
 template <int M>
-__global__ __launch_bounds__(256) void k_gemm_filter(
-    const float *__restrict__ base, const float *__restrict__ bnorm, const uint32_t *__restrict__ perm,
-    const float *__restrict__ qry, const float *__restrict__ qnorm, const float *__restrict__ tau, int nq, int dpad,
-    long row_begin, long row_end, int n_qtiles, int n_items, uint2 *__restrict__ cand, uint32_t *__restrict__ cnt,
-    int cap) {
-    __shared__ __attribute__((aligned(16))) float sA[2][kTileRows * kLdsStride];
-    __shared__ __attribute__((aligned(16))) float sB[2][kTileCols * kLdsStride];
-    __shared__ __attribute__((aligned(16))) float sN[kTileRows];
+__device__ __forceinline__ void assign_stage(floatx16 (&acc)[2][2], const float *nrow, EpiState &st, int wr, int h,
+                                             long rs) {
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) {
+        float m = INFINITY;
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int rl0 = 64 * wr + 32 * rb + 8 * g + 4 * h;
+                const floatx4 n4 = *(const floatx4 *)(nrow + rl0);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float dot = acc[rb][cb][4 * g + j];
+                    float u;
+                    if constexpr (M == L2) {
+                        u = fmaf(-2.0f, dot, n4[j]);
+                    } else if constexpr (M == DOT) {
+                        u = -dot;
+                    } else {
+                        const float den = st.cn[cb] * n4[j];
+                        u = den > 1e-9f ? -(dot / den) : canon(0.0f * dot);
+                    }
+                    acc[rb][cb][4 * g + j] = u;
+                    m = fminf(m, u);
+                }
+            }
+        if (m < st.bs[cb]) {
+            int idx = 31;
+#pragma unroll
+            for (int r = 31; r >= 0; --r) idx = acc[r >> 4][cb][r & 15] == m ? r : idx;
+            st.bs[cb] = m;
+            st.bi[cb] = (int)rs + 64 * wr + 4 * h + 32 * (idx >> 4) + 8 * ((idx >> 2) & 3) + (idx & 3);
+        }
+    }
+}
+
+// ASSIGN item end: combine lanes l and l^32 (row halves) and the RW row waves, write the
+// outputs.  Must be called by all threads; contains a barrier.
+template <int M, int RW>
+__device__ __forceinline__ void assign_finish(EpiState &st, const ScanArgs &a, int col0, int wr, int wc, int l32,
+                                              int h, float *s_xs, int *s_xi) {
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) {
+        const float os = __shfl_xor(st.bs[cb], 32, 64);
+        const int oi = __shfl_xor(st.bi[cb], 32, 64);
+        if (os < st.bs[cb] || (os == st.bs[cb] && oi < st.bi[cb])) {
+            st.bs[cb] = os;
+            st.bi[cb] = oi;
+        }
+    }
+    if (wr > 0 && h == 0) {
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) {
+            s_xs[(wr - 1) * kTileCols + 64 * wc + 32 * cb + l32] = st.bs[cb];
+            s_xi[(wr - 1) * kTileCols + 64 * wc + 32 * cb + l32] = st.bi[cb];
+        }
+    }
+    __syncthreads();
+    if (wr == 0 && h == 0) {
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) {
+#pragma unroll
+            for (int w = 0; w < RW - 1; ++w) {
+                const float os = s_xs[w * kTileCols + 64 * wc + 32 * cb + l32];
+                const int oi = s_xi[w * kTileCols + 64 * wc + 32 * cb + l32];
+                if (os < st.bs[cb] || (os == st.bs[cb] && oi < st.bi[cb])) {
+                    st.bs[cb] = os;
+                    st.bi[cb] = oi;
+                }
+            }
+            const int p = col0 + 64 * wc + 32 * cb + l32;
+            if (p < a.ncols) {
+                const int c = st.bi[cb];
+                a.assign[p] = c;
+                float in;
+                if constexpr (M == L2) in = fmaxf(st.cn[cb] + st.bs[cb], 0.0f);  // + ||x||^2
+                else if constexpr (M == DOT) in = st.bs[cb];                     // -dot
+                else in = 1.0f + st.bs[cb];                                      // 1 - cos
+                a.inertia[p] = in;
+                a.pos[p] = atomicAdd(&a.counts[c], 1);
+            }
+        }
+    }
+}
+
+__device__ __forceinline__ void decode_item(const ScanArgs &a, int it, int &c0, long &lo, long &hi) {
+    const int ct = it % a.n_ctiles;
+    const long chunk = it / a.n_ctiles;
+    c0 = ct * kTileCols;
+    lo = a.row_begin + chunk * a.item_rows;
+    hi = min(lo + a.item_rows, a.row_end);
+}
+
+// XCD-aware order: workgroup b runs on XCD b % 8; at step t the XCD x takes the contiguous
+// item block [t*G + x*G/8, t*G + (x+1)*G/8) (G, the grid size, is a multiple of 8).
+__device__ __forceinline__ int first_item() {
+    return (blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3);
+}
+
+// =========================================================================================
+// Resident-column kernel: 8 waves, 256-row stages, NK K-chunks (dpad = 32 NK <= 128).
+// =========================================================================================
+template <int MODE, int M, int NK>
+__global__ __launch_bounds__(512, 1) void k_mfma_res(ScanArgs a) {
+    constexpr int RW = 4, TR = 256;
+    __shared__ floatx4 sA[2][TR * 8];
+    __shared__ floatx4 sB[kTileCols * 8 * NK];
+    __shared__ __attribute__((aligned(16))) float sN[2][TR];
+    __shared__ uint32_t s_qcnt[MODE == kFilter ? kTileCols : 1];
+    __shared__ uint2 s_slot[MODE == kFilter ? kTileCols * kResSlots : 1];
+    __shared__ float s_xs[MODE == kAssign ? (RW - 1) * kTileCols : 1];
+    __shared__ int s_xi[MODE == kAssign ? (RW - 1) * kTileCols : 1];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wr = wave & 3, wc = wave >> 2;
+    const int l32 = lane & 31, h = lane >> 5;
+    const int G = gridDim.x;
+    int item = first_item();
+    if (item >= a.n_items) return;
+
+    // B tile: row r, chunk kc, slot c4.  Row parity (with the chunk) picks the bank half.
+    auto bidx_kc = [](int r, int kc, int c4) {
+        const int pch = (NK % 2 == 0) ? (kc ^ (r & 1)) : kc;
+        return r * (8 * NK) + pch * 8 + (c4 ^ ((r >> 1) & 7));
+    };
+    auto load_a = [&](floatx4 (&ra)[4], long rs, int k0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int f = tid + 512 * i;
+            ra[i] = *(const floatx4 *)(a.A + (rs + (f >> 3)) * (long)(32 * NK) + k0 + 4 * (f & 7));
+        }
+    };
+    auto store_a = [&](const floatx4 (&ra)[4], floatx4 *dst) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int f = tid + 512 * i;
+            dst[swz(f >> 3, f & 7)] = ra[i];
+        }
+    };
+    auto load_b = [&](floatx4 (&rq)[2 * NK], int c0) {
+#pragma unroll
+        for (int i = 0; i < 2 * NK; ++i) {
+            const int f = tid + 512 * i;
+            const int r = f / (8 * NK), rem = f % (8 * NK);
+            rq[i] = *(const floatx4 *)(a.B + (long)(c0 + r) * (32 * NK) + 4 * rem);
+        }
+    };
+    auto store_b = [&](const floatx4 (&rq)[2 * NK]) {
+#pragma unroll
+        for (int i = 0; i < 2 * NK; ++i) {
+            const int f = tid + 512 * i;
+            const int r = f / (8 * NK), rem = f % (8 * NK);
+            sB[bidx_kc(r, rem >> 3, rem & 7)] = rq[i];
+        }
+    };
+
+    int col0;
+    long r_lo, r_hi;
+    decode_item(a, item, col0, r_lo, r_hi);
+    long rs = r_lo;
+    EpiState st;
+    item_begin<MODE, M>(st, a, col0, wc, l32);
+
+    // ---- pipeline prologue ----
+    floatx4 ra[4], rq[2 * NK];
+    float rn = 0.0f;
+    load_b(rq, col0);
+    load_a(ra, rs, 0);
+    if (tid < TR) rn = a.anorm[rs + tid];
+    store_b(rq);
+    store_a(ra, sA[0]);
+    if (tid < TR) sN[0][tid] = rn;
+    if constexpr (MODE == kFilter) {
+        if (tid < kTileCols) s_qcnt[tid] = 0;
+    }
+    __syncthreads();
+    int buf = 0, sb = 0;
+
+    for (;;) {
+        long nrs = rs + TR;
+        int nitem = item, ncol0 = col0;
+        long nlo = r_lo, nhi = r_hi;
+        const bool item_end = nrs >= r_hi;
+        bool more = true;
+        if (item_end) {
+            nitem = item + G;
+            more = nitem < a.n_items;
+            if (more) {
+                decode_item(a, nitem, ncol0, nlo, nhi);
+                nrs = nlo;
+            }
+        }
+
+        floatx16 acc[2][2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) acc[i][j] = floatx16{0};
+
+#pragma unroll
+        for (int kc = 0; kc < NK; ++kc) {
+            const bool last = kc + 1 == NK;
+            if (!last) {
+                load_a(ra, rs, (kc + 1) * kKChunk);
+            } else if (more) {
+                load_a(ra, nrs, 0);
+                if (tid < TR) rn = a.anorm[nrs + tid];
+            }
+            mfma_chunk(acc, sA[buf], sB, [&](int r, int c4) { return bidx_kc(r, kc, c4); }, wr, wc, l32, h);
+            if (!last || more) {
+                store_a(ra, sA[buf ^ 1]);
+                if (last && tid < TR) sN[sb ^ 1][tid] = rn;
+            }
+            __syncthreads();
+            buf ^= 1;
+        }
+        // The next item's column tile is fetched while this stage's epilogue runs.
+        const bool new_cols = item_end && more;
+        if (new_cols) load_b(rq, ncol0);
+
+        const float *nrow = sN[sb];
+        if constexpr (MODE == kFilter) {
+            filter_stage<M, kResSlots>(acc, nrow, st, a, wr, wc, l32, h, rs, r_lo, col0, s_qcnt, s_slot);
+            if (item_end) filter_flush<kResSlots>(a, col0, r_lo, s_qcnt, s_slot);
+        } else {
+            assign_stage<M>(acc, nrow, st, wr, h, rs);
+            if (item_end) assign_finish<M, RW>(st, a, col0, wr, wc, l32, h, s_xs, s_xi);
+        }
+
+        if (!more) break;
+        if (new_cols) {
+            // every wave finished this item's MFMAs (barrier after the last chunk)
+            store_b(rq);
+            __syncthreads();
+            item = nitem;
+            col0 = ncol0;
+            r_lo = nlo;
+            r_hi = nhi;
+            item_begin<MODE, M>(st, a, col0, wc, l32);
+        }
+        rs = nrs;
+        sb ^= 1;
+    }
+}
+
+// =========================================================================================
+// Streaming kernel: 4 waves, 128-row stages, both operands streamed per K-chunk (any dpad).
+// =========================================================================================
+template <int MODE, int M>
+__global__ __launch_bounds__(256, 2) void k_mfma_stream(ScanArgs a) {
+    constexpr int RW = 2, TR = 128;
+    __shared__ floatx4 sA[2][TR * 8];
+    __shared__ floatx4 sB[2][kTileCols * 8];
+    __shared__ __attribute__((aligned(16))) float sN[2][TR];
+    __shared__ uint32_t s_qcnt[MODE == kFilter ? kTileCols : 1];
+    __shared__ uint2 s_slot[MODE == kFilter ? kTileCols * kStrSlots : 1];
+    __shared__ float s_xs[MODE == kAssign ? (RW - 1) * kTileCols : 1];
+    __shared__ int s_xi[MODE == kAssign ? (RW - 1) * kTileCols : 1];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wr = wave & 1, wc = wave >> 1;
     const int l32 = lane & 31, h = lane >> 5;
-    const int nk = dpad / kKChunk;
-    const long item_rows = (long)kItemStages * kTileRows;
+    const int nk = a.dpad / kKChunk;
+    const int G = gridDim.x;
+    int item = first_item();
+    if (item >= a.n_items) return;
 
-    // XCD-aware persistent schedule: gridDim.x is a multiple of 8 and workgroup b runs on
-    // XCD b % 8.  At step t the XCD x takes the contiguous item block
-    // [t*G + x*G/8, t*G + (x+1)*G/8), so its workgroups share row chunks.
-    const int G = gridDim.x, g8 = G >> 3;
-    const int slot = (blockIdx.x & 7) * g8 + (blockIdx.x >> 3);
-
-    for (int item = slot; item < n_items; item += G) {
-        const int qtile = item % n_qtiles;
-        const long chunk = item / n_qtiles;
-        const int q0 = qtile * kTileCols;
-        const long r_lo = row_begin + chunk * item_rows;
-        const long r_hi = min(r_lo + item_rows, row_end);
-
-        float qn[2], tq[2];
-        int qi[2];
+    auto load = [&](floatx4 (&ra)[4], floatx4 (&rb)[4], long rs, int c0, int k0) {
 #pragma unroll
-        for (int cb = 0; cb < 2; ++cb) {
-            const int q = q0 + 64 * wc + 32 * cb + l32;
-            qi[cb] = q;
-            qn[cb] = q < nq ? qnorm[q] : 0.0f;
-            tq[cb] = q < nq ? tau[q] : -INFINITY;
+        for (int i = 0; i < 4; ++i) {
+            const int f = tid + 256 * i;
+            const int row = f >> 3, c4 = f & 7;
+            ra[i] = *(const floatx4 *)(a.A + (rs + row) * (long)a.dpad + k0 + 4 * c4);
+            rb[i] = *(const floatx4 *)(a.B + (long)(c0 + row) * a.dpad + k0 + 4 * c4);
+        }
+    };
+    auto store = [&](const floatx4 (&ra)[4], const floatx4 (&rb)[4], floatx4 *dA, floatx4 *dB) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int f = tid + 256 * i;
+            dA[swz(f >> 3, f & 7)] = ra[i];
+            dB[swz(f >> 3, f & 7)] = rb[i];
+        }
+    };
+
+    int col0;
+    long r_lo, r_hi;
+    decode_item(a, item, col0, r_lo, r_hi);
+    long rs = r_lo;
+    EpiState st;
+    item_begin<MODE, M>(st, a, col0, wc, l32);
+
+    floatx4 ra[4], rbv[4];
+    float rn = 0.0f;
+    load(ra, rbv, rs, col0, 0);
+    if (tid < TR) rn = a.anorm[rs + tid];
+    store(ra, rbv, sA[0], sB[0]);
+    if (tid < TR) sN[0][tid] = rn;
+    if constexpr (MODE == kFilter) {
+        if (tid < kTileCols) s_qcnt[tid] = 0;
+    }
+    __syncthreads();
+    int buf = 0, sb = 0;
+
+    for (;;) {
+        long nrs = rs + TR;
+        int nitem = item, ncol0 = col0;
+        long nlo = r_lo, nhi = r_hi;
+        const bool item_end = nrs >= r_hi;
+        bool more = true;
+        if (item_end) {
+            nitem = item + G;
+            more = nitem < a.n_items;
+            if (more) {
+                decode_item(a, nitem, ncol0, nlo, nhi);
+                nrs = nlo;
+            }
         }
 
-        for (long rs = r_lo; rs < r_hi; rs += kTileRows) {
-            floatx16 acc[2][2];
+        floatx16 acc[2][2];
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < 2; ++i)
 #pragma unroll
-                for (int j = 0; j < 2; ++j) acc[i][j] = floatx16{0};
+            for (int j = 0; j < 2; ++j) acc[i][j] = floatx16{0};
 
-            Stage st;
-            load_chunk(st, base, qry, rs, r_hi, q0, nq, dpad, 0);
-            if (tid < kTileRows) sN[tid] = (rs + tid < r_hi) ? bnorm[rs + tid] : 0.0f;
-            store_chunk(st, sA[0], sB[0]);
+        for (int kc = 0; kc < nk; ++kc) {
+            const bool last = kc + 1 == nk;
+            if (!last) {
+                load(ra, rbv, rs, col0, (kc + 1) * kKChunk);
+            } else if (more) {
+                load(ra, rbv, nrs, ncol0, 0);
+                if (tid < TR) rn = a.anorm[nrs + tid];
+            }
+            mfma_chunk(acc, sA[buf], sB[buf], [](int r, int c4) { return swz(r, c4); }, wr, wc, l32, h);
+            if (!last || more) {
+                store(ra, rbv, sA[buf ^ 1], sB[buf ^ 1]);
+                if (last && tid < TR) sN[sb ^ 1][tid] = rn;
+            }
             __syncthreads();
+            buf ^= 1;
+        }
 
-            for (int kc = 0; kc < nk; ++kc) {
-                const int buf = kc & 1;
-                if (kc + 1 < nk) load_chunk(st, base, qry, rs, r_hi, q0, nq, dpad, (kc + 1) * kKChunk);
-                const float *A = sA[buf];
-                const float *B = sB[buf];
-#pragma unroll
-                for (int g = 0; g < kKChunk / 8; ++g) {
-                    const int ko = 8 * g + 4 * h;
-                    const floatx4 a0 = *(const floatx4 *)(A + (64 * wr + l32) * kLdsStride + ko);
-                    const floatx4 a1 = *(const floatx4 *)(A + (64 * wr + 32 + l32) * kLdsStride + ko);
-                    const floatx4 b0 = *(const floatx4 *)(B + (64 * wc + l32) * kLdsStride + ko);
-                    const floatx4 b1 = *(const floatx4 *)(B + (64 * wc + 32 + l32) * kLdsStride + ko);
-#pragma unroll
-                    for (int t = 0; t < 4; ++t) {
-                        acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[t], b0[t], acc[0][0], 0, 0, 0);
-                        acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[t], b1[t], acc[0][1], 0, 0, 0);
-                        acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[t], b0[t], acc[1][0], 0, 0, 0);
-                        acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[t], b1[t], acc[1][1], 0, 0, 0);
-                    }
-                }
-                if (kc + 1 < nk) store_chunk(st, sA[buf ^ 1], sB[buf ^ 1]);
-                __syncthreads();
-            }
+        const float *nrow = sN[sb];
+        if constexpr (MODE == kFilter) {
+            filter_stage<M, kStrSlots>(acc, nrow, st, a, wr, wc, l32, h, rs, r_lo, col0, s_qcnt, s_slot);
+            if (item_end) filter_flush<kStrSlots>(a, col0, r_lo, s_qcnt, s_slot);
+        } else {
+            assign_stage<M>(acc, nrow, st, wr, h, rs);
+            if (item_end) assign_finish<M, RW>(st, a, col0, wr, wc, l32, h, s_xs, s_xi);
+        }
 
-            // Epilogue: accumulator register r of block (rb, cb) holds row
-            // 64*wr + 32*rb + 8*(r/4) + 4*h + r%4 of the stage and query column l32.
-            const int nvalid = (int)min((long)kTileRows, r_hi - rs);
-#pragma unroll
-            for (int rb = 0; rb < 2; ++rb) {
-#pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    const int rl0 = 64 * wr + 32 * rb + 8 * g + 4 * h;
-                    const floatx4 n4 = *(const floatx4 *)(sN + rl0);
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-#pragma unroll
-                        for (int cb = 0; cb < 2; ++cb) {
-                            const float s = pair_score<M>(acc[rb][cb][4 * g + j], qn[cb], n4[j]);
-                            if (s <= tq[cb] && rl0 + j < nvalid && qi[cb] < nq) {
-                                const uint32_t at = atomicAdd(&cnt[qi[cb]], 1u);
-                                if (at < (uint32_t)cap)
-                                    cand[(size_t)qi[cb] * cap + at] = make_uint2(score_key(s), perm[rs + rl0 + j]);
-                            }
-                        }
-                    }
-                }
-            }
-            __syncthreads();  // sN / LDS buffers are rewritten by the next stage
+        if (!more) break;
+        rs = nrs;
+        sb ^= 1;
+        if (item_end) {
+            item = nitem;
+            col0 = ncol0;
+            r_lo = nlo;
+            r_hi = nhi;
+            item_begin<MODE, M>(st, a, col0, wc, l32);
         }
     }
 }
 
-// ---------------------------------------------------------------------------------
-// k-means assignment (replaces the per-thread loop of kmeans_assign_and_accumulate,
-// vector-cuda/src/kernels/kmeans.cu:38-285): the same MFMA tiles with centroids as the
-// A operand (streamed, L2-resident) and each workgroup's 128 points as the B operand.
-// Every lane keeps a running (score, centroid) minimum over its rows, visiting rows in
-// ascending order with a strict '<', so the lowest index wins ties as in kmeans.cu:110-114;
-// partial minima are combined lexicographically.  Scores: L2 ||c||^2 - 2 x.c (the point's
-// own norm is constant), DOT -x.c, COS -x.c/(||x|| ||c||) with the 1e-9 guard.
-// Writes assign[p], the per-point inertia in the kmeans.cu convention (L2^2, -dot, 1-cos)
-// and pos[p] = the point's slot inside its cluster (an atomic ticket on counts[c]).
-// ---------------------------------------------------------------------------------
-template <int M>
-__global__ __launch_bounds__(256) void k_kmeans_assign(const float *__restrict__ cent, const float *__restrict__ cnorm,
-                                                       int k, const float *__restrict__ pts,
-                                                       const float *__restrict__ pnorm, int n, int dpad,
-                                                       int n_tiles, int32_t *__restrict__ assign,
-                                                       float *__restrict__ inertia, int32_t *__restrict__ pos,
-                                                       int32_t *__restrict__ counts) {
-    __shared__ __attribute__((aligned(16))) float sA[2][kTileRows * kLdsStride];
-    __shared__ __attribute__((aligned(16))) float sB[2][kTileCols * kLdsStride];
-    __shared__ __attribute__((aligned(16))) float sN[kTileRows];
-    __shared__ float xs[2][64];
-    __shared__ int xi[2][64];
+// ---- launch ----------------------------------------------------------------------------
+static int grid_for(long n_items, int cap) {
+    long g = n_items < cap ? n_items : cap;
+    return (int)((g + 7) / 8 * 8);
+}
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wr = wave & 1, wc = wave >> 1;
-    const int l32 = lane & 31, h = lane >> 5;
-    const int nk = dpad / kKChunk;
-
-    for (int tile = blockIdx.x; tile < n_tiles; tile += gridDim.x) {
-        const int p0 = tile * kTileCols;
-        float pn[2], bs[2];
-        int bi[2];
-#pragma unroll
-        for (int cb = 0; cb < 2; ++cb) {
-            const int p = p0 + 64 * wc + 32 * cb + l32;
-            pn[cb] = p < n ? pnorm[p] : 0.0f;
-            bs[cb] = INFINITY;
-            bi[cb] = 0;
+// grid_cap: 2 workgroups per CU (the streaming kernel's residency); the resident-column
+// kernel runs one 8-wave workgroup per CU.
+template <int MODE, int M>
+static void launch_scan(const ScanArgs &a, int grid_cap, hipStream_t s) {
+    const int cus = grid_cap / 2;
+    const int nk = a.dpad / kKChunk;
+    if (nk <= 4) {
+        const dim3 g(grid_for(a.n_items, cus)), b(512);
+        switch (nk) {
+            case 1: hipLaunchKernelGGL((k_mfma_res<MODE, M, 1>), g, b, 0, s, a); break;
+            case 2: hipLaunchKernelGGL((k_mfma_res<MODE, M, 2>), g, b, 0, s, a); break;
+            case 3: hipLaunchKernelGGL((k_mfma_res<MODE, M, 3>), g, b, 0, s, a); break;
+            default: hipLaunchKernelGGL((k_mfma_res<MODE, M, 4>), g, b, 0, s, a); break;
         }
-        for (long rs = 0; rs < k; rs += kTileRows) {
-            floatx16 acc[2][2];
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j) acc[i][j] = floatx16{0};
-            Stage st;
-            load_chunk(st, cent, pts, rs, k, p0, n, dpad, 0);
-            if (tid < kTileRows) sN[tid] = (rs + tid < k) ? cnorm[rs + tid] : 0.0f;
-            store_chunk(st, sA[0], sB[0]);
-            __syncthreads();
-            for (int kc = 0; kc < nk; ++kc) {
-                const int buf = kc & 1;
-                if (kc + 1 < nk) load_chunk(st, cent, pts, rs, k, p0, n, dpad, (kc + 1) * kKChunk);
-                const float *A = sA[buf];
-                const float *B = sB[buf];
-#pragma unroll
-                for (int g = 0; g < kKChunk / 8; ++g) {
-                    const int ko = 8 * g + 4 * h;
-                    const floatx4 a0 = *(const floatx4 *)(A + (64 * wr + l32) * kLdsStride + ko);
-                    const floatx4 a1 = *(const floatx4 *)(A + (64 * wr + 32 + l32) * kLdsStride + ko);
-                    const floatx4 b0 = *(const floatx4 *)(B + (64 * wc + l32) * kLdsStride + ko);
-                    const floatx4 b1 = *(const floatx4 *)(B + (64 * wc + 32 + l32) * kLdsStride + ko);
-#pragma unroll
-                    for (int t = 0; t < 4; ++t) {
-                        acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[t], b0[t], acc[0][0], 0, 0, 0);
-                        acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[t], b1[t], acc[0][1], 0, 0, 0);
-                        acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[t], b0[t], acc[1][0], 0, 0, 0);
-                        acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[t], b1[t], acc[1][1], 0, 0, 0);
-                    }
-                }
-                if (kc + 1 < nk) store_chunk(st, sA[buf ^ 1], sB[buf ^ 1]);
-                __syncthreads();
-            }
-            const int nvalid = (int)min((long)kTileRows, (long)k - rs);
-#pragma unroll
-            for (int rb = 0; rb < 2; ++rb) {
-#pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    const int rl0 = 64 * wr + 32 * rb + 8 * g + 4 * h;
-                    const floatx4 n4 = *(const floatx4 *)(sN + rl0);
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-#pragma unroll
-                        for (int cb = 0; cb < 2; ++cb) {
-                            const float dot = acc[rb][cb][4 * g + j];
-                            float sc;
-                            if constexpr (M == L2) {
-                                sc = fmaf(-2.0f, dot, n4[j]);
-                            } else if constexpr (M == DOT) {
-                                sc = -dot;
-                            } else {
-                                const float den = pn[cb] * n4[j];
-                                sc = den > 1e-9f ? -(dot / den) : -0.0f;
-                            }
-                            if (sc < bs[cb] && rl0 + j < nvalid) {
-                                bs[cb] = sc;
-                                bi[cb] = (int)rs + rl0 + j;
-                            }
-                        }
-                    }
-                }
-            }
-            __syncthreads();
-        }
-        // combine the two row halves held by lanes l and l^32, then the two row waves
-#pragma unroll
-        for (int cb = 0; cb < 2; ++cb) {
-            const float os = __shfl_xor(bs[cb], 32, 64);
-            const int oi = __shfl_xor(bi[cb], 32, 64);
-            if (os < bs[cb] || (os == bs[cb] && oi < bi[cb])) {
-                bs[cb] = os;
-                bi[cb] = oi;
-            }
-        }
-        if (wr == 1 && h == 0) {
-#pragma unroll
-            for (int cb = 0; cb < 2; ++cb) {
-                xs[wc][32 * cb + l32] = bs[cb];
-                xi[wc][32 * cb + l32] = bi[cb];
-            }
-        }
-        __syncthreads();
-        if (wr == 0 && h == 0) {
-#pragma unroll
-            for (int cb = 0; cb < 2; ++cb) {
-                const float os = xs[wc][32 * cb + l32];
-                const int oi = xi[wc][32 * cb + l32];
-                if (os < bs[cb] || (os == bs[cb] && oi < bi[cb])) {
-                    bs[cb] = os;
-                    bi[cb] = oi;
-                }
-                const int p = p0 + 64 * wc + 32 * cb + l32;
-                if (p < n) {
-                    const int c = bi[cb];
-                    assign[p] = c;
-                    float in;
-                    if constexpr (M == L2) in = fmaxf(pn[cb] + bs[cb], 0.0f);
-                    else if constexpr (M == DOT) in = bs[cb];
-                    else in = 1.0f + bs[cb];
-                    inertia[p] = in;
-                    pos[p] = atomicAdd(&counts[c], 1);
-                }
-            }
-        }
-        __syncthreads();
+    } else {
+        const dim3 g(grid_for(a.n_items, 2 * cus)), b(256);
+        hipLaunchKernelGGL((k_mfma_stream<MODE, M>), g, b, 0, s, a);
     }
 }
 
-void launch_kmeans_assign(int metric, const float *cent, const float *cnorm, int k, const float *pts,
+template <int MODE>
+static void launch_metric(int metric, const ScanArgs &a, int grid_cap, hipStream_t s) {
+    switch (metric) {
+        case L2: launch_scan<MODE, L2>(a, grid_cap, s); break;
+        case DOT: launch_scan<MODE, DOT>(a, grid_cap, s); break;
+        default: launch_scan<MODE, COS>(a, grid_cap, s); break;
+    }
+}
+
+void launch_gemm_filter(int metric, const float *base, const float *bnorm, const float *qry, const float *qnorm,
+                        const float *tau, int nq, int dpad, long row_begin, long row_end, uint2 *cand, uint32_t *cnt,
+                        int cap, float anorm_max, float anorm_min, int grid_cap, hipStream_t s) {
+    if (nq <= 0 || row_end <= row_begin) return;
+    ScanArgs a{};
+    a.A = base;
+    a.anorm = bnorm;
+    a.B = qry;
+    a.bnorm = qnorm;
+    a.dpad = dpad;
+    a.ncols = nq;
+    a.n_ctiles = ceil_div(nq, kTileCols);
+    a.item_rows = kItemRows;
+    a.row_begin = row_begin;
+    a.row_end = row_end;
+    const long n_chunks = (row_end - row_begin + a.item_rows - 1) / a.item_rows;
+    a.n_items = (int)((long)a.n_ctiles * n_chunks);
+    a.tau = tau;
+    a.cand = cand;
+    a.cnt = cnt;
+    a.cap = cap;
+    a.anorm_max = anorm_max;
+    a.anorm_min = anorm_min;
+    launch_metric<kFilter>(metric, a, grid_cap, s);
+}
+
+void launch_kmeans_assign(int metric, const float *cent, const float *cnorm, int kpad, const float *pts,
                           const float *pnorm, int n, int dpad, int32_t *assign, float *inertia, int32_t *pos,
                           int32_t *counts, int grid_cap, hipStream_t s) {
-    if (n <= 0 || k <= 0) return;
-    const int tiles = ceil_div(n, kTileCols);
-    const int grid = tiles < grid_cap ? tiles : grid_cap;
-    const dim3 g(grid), b(256);
-    switch (metric) {
-        case L2:
-            hipLaunchKernelGGL(k_kmeans_assign<L2>, g, b, 0, s, cent, cnorm, k, pts, pnorm, n, dpad, tiles, assign,
-                               inertia, pos, counts);
-            break;
-        case DOT:
-            hipLaunchKernelGGL(k_kmeans_assign<DOT>, g, b, 0, s, cent, cnorm, k, pts, pnorm, n, dpad, tiles, assign,
-                               inertia, pos, counts);
-            break;
-        default:
-            hipLaunchKernelGGL(k_kmeans_assign<COS>, g, b, 0, s, cent, cnorm, k, pts, pnorm, n, dpad, tiles, assign,
-                               inertia, pos, counts);
-            break;
-    }
-}
-
-void launch_gemm_filter(int metric, const float *base, const float *bnorm, const uint32_t *perm, const float *qry,
-                        const float *qnorm, const float *tau, int nq, int dpad, long row_begin, long row_end,
-                        uint2 *cand, uint32_t *cnt, int cap, int grid_cap, hipStream_t s) {
-    if (nq <= 0 || row_end <= row_begin) return;
-    const int n_qtiles = ceil_div(nq, kTileCols);
-    const long item_rows = (long)kItemStages * kTileRows;
-    const long n_chunks = (row_end - row_begin + item_rows - 1) / item_rows;
-    const long n_items = (long)n_qtiles * n_chunks;
-    long grid = n_items < grid_cap ? n_items : grid_cap;
-    grid = (grid + 7) / 8 * 8;
-    const dim3 g((unsigned)grid), b(256);
-    switch (metric) {
-        case L2:
-            hipLaunchKernelGGL(k_gemm_filter<L2>, g, b, 0, s, base, bnorm, perm, qry, qnorm, tau, nq, dpad, row_begin,
-                               row_end, n_qtiles, (int)n_items, cand, cnt, cap);
-            break;
-        case DOT:
-            hipLaunchKernelGGL(k_gemm_filter<DOT>, g, b, 0, s, base, bnorm, perm, qry, qnorm, tau, nq, dpad,
-                               row_begin, row_end, n_qtiles, (int)n_items, cand, cnt, cap);
-            break;
-        default:
-            hipLaunchKernelGGL(k_gemm_filter<COS>, g, b, 0, s, base, bnorm, perm, qry, qnorm, tau, nq, dpad,
-                               row_begin, row_end, n_qtiles, (int)n_items, cand, cnt, cap);
-            break;
-    }
+    if (n <= 0 || kpad <= 0) return;
+    ScanArgs a{};
+    a.A = cent;
+    a.anorm = cnorm;
+    a.B = pts;
+    a.bnorm = pnorm;
+    a.dpad = dpad;
+    a.ncols = n;
+    a.n_ctiles = ceil_div(n, kTileCols);
+    a.n_items = a.n_ctiles;
+    a.row_begin = 0;
+    a.row_end = kpad;
+    a.item_rows = kpad;
+    a.assign = assign;
+    a.inertia = inertia;
+    a.pos = pos;
+    a.counts = counts;
+    launch_metric<kAssign>(metric, a, grid_cap, s);
 }
 
 }  // namespace vh

@@ -57,7 +57,7 @@ __device__ __forceinline__ float finish(float a, float b) {
 
 // DC: dimensions per chunk held in registers (64 or 128).
 template <int M, int DC>
-__global__ __launch_bounds__(256) void k_valu_filter(const float *__restrict__ base, const uint32_t *__restrict__ perm,
+__global__ __launch_bounds__(256) void k_valu_filter(const float *__restrict__ base,
                                                      const float *__restrict__ qry, const float *__restrict__ tau,
                                                      int nq, int dpad, long row_begin, long row_end, int n_qtiles,
                                                      int n_items, uint2 *__restrict__ cand,
@@ -121,7 +121,7 @@ __global__ __launch_bounds__(256) void k_valu_filter(const float *__restrict__ b
                 const float v = finish<M>(a[r], b[r]);
                 if (v <= tq && r < nvalid && qv) {
                     const uint32_t at = atomicAdd(&cnt[q], 1u);
-                    if (at < (uint32_t)cap) cand[(size_t)q * cap + at] = make_uint2(score_key(v), perm[rs + r]);
+                    if (at < (uint32_t)cap) cand[(size_t)q * cap + at] = make_uint2(score_key(v), (uint32_t)(rs + r));
                 }
             }
         }
@@ -129,18 +129,18 @@ __global__ __launch_bounds__(256) void k_valu_filter(const float *__restrict__ b
 }
 
 template <int M>
-static void launch_m(int dpad, dim3 g, hipStream_t s, const float *base, const uint32_t *perm, const float *qry,
+static void launch_m(int dpad, dim3 g, hipStream_t s, const float *base, const float *qry,
                      const float *tau, int nq, long rb, long re, int nqt, int items, uint2 *cand, uint32_t *cnt,
                      int cap) {
     if (dpad <= 128 && dpad > 64)
-        hipLaunchKernelGGL((k_valu_filter<M, 128>), g, dim3(256), 0, s, base, perm, qry, tau, nq, dpad, rb, re, nqt,
+        hipLaunchKernelGGL((k_valu_filter<M, 128>), g, dim3(256), 0, s, base, qry, tau, nq, dpad, rb, re, nqt,
                            items, cand, cnt, cap);
     else
-        hipLaunchKernelGGL((k_valu_filter<M, 64>), g, dim3(256), 0, s, base, perm, qry, tau, nq, dpad, rb, re, nqt,
+        hipLaunchKernelGGL((k_valu_filter<M, 64>), g, dim3(256), 0, s, base, qry, tau, nq, dpad, rb, re, nqt,
                            items, cand, cnt, cap);
 }
 
-void launch_valu_filter(int metric, const float *base, const uint32_t *perm, const float *qry, const float *tau,
+void launch_valu_filter(int metric, const float *base, const float *qry, const float *tau,
                         int nq, int dim, int dpad, long row_begin, long row_end, uint2 *cand, uint32_t *cnt, int cap,
                         int grid_cap, hipStream_t s) {
     (void)dim;
@@ -153,13 +153,13 @@ void launch_valu_filter(int metric, const float *base, const uint32_t *perm, con
     const dim3 g((unsigned)grid);
     const int it = (int)items;
     switch (metric) {
-        case L1: launch_m<L1>(dpad, g, s, base, perm, qry, tau, nq, row_begin, row_end, nqt, it, cand, cnt, cap); break;
-        case MINK: launch_m<MINK>(dpad, g, s, base, perm, qry, tau, nq, row_begin, row_end, nqt, it, cand, cnt, cap); break;
-        case LINF: launch_m<LINF>(dpad, g, s, base, perm, qry, tau, nq, row_begin, row_end, nqt, it, cand, cnt, cap); break;
-        case HAMF: launch_m<HAMF>(dpad, g, s, base, perm, qry, tau, nq, row_begin, row_end, nqt, it, cand, cnt, cap); break;
-        case MAHA: launch_m<MAHA>(dpad, g, s, base, perm, qry, tau, nq, row_begin, row_end, nqt, it, cand, cnt, cap); break;
-        case JACC: launch_m<JACC>(dpad, g, s, base, perm, qry, tau, nq, row_begin, row_end, nqt, it, cand, cnt, cap); break;
-        case HELL: launch_m<HELL>(dpad, g, s, base, perm, qry, tau, nq, row_begin, row_end, nqt, it, cand, cnt, cap); break;
+        case L1: launch_m<L1>(dpad, g, s, base, qry, tau, nq, row_begin, row_end, nqt, it, cand, cnt, cap); break;
+        case MINK: launch_m<MINK>(dpad, g, s, base, qry, tau, nq, row_begin, row_end, nqt, it, cand, cnt, cap); break;
+        case LINF: launch_m<LINF>(dpad, g, s, base, qry, tau, nq, row_begin, row_end, nqt, it, cand, cnt, cap); break;
+        case HAMF: launch_m<HAMF>(dpad, g, s, base, qry, tau, nq, row_begin, row_end, nqt, it, cand, cnt, cap); break;
+        case MAHA: launch_m<MAHA>(dpad, g, s, base, qry, tau, nq, row_begin, row_end, nqt, it, cand, cnt, cap); break;
+        case JACC: launch_m<JACC>(dpad, g, s, base, qry, tau, nq, row_begin, row_end, nqt, it, cand, cnt, cap); break;
+        case HELL: launch_m<HELL>(dpad, g, s, base, qry, tau, nq, row_begin, row_end, nqt, it, cand, cnt, cap); break;
         default: break;
     }
 }

@@ -305,6 +305,11 @@ int vhip_memcpy_dtoh(int ordinal, void *dst, const void *src, size_t bytes) {
     VH_HIP(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
     return VHIP_OK;
 }
+int vhip_memcpy_dtod(int ordinal, void *dst, const void *src, size_t bytes) {
+    VH_CHECK(open_device(ordinal));
+    VH_HIP(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToDevice));
+    return VHIP_OK;
+}
 int vhip_synchronize(int ordinal) {
     VH_CHECK(open_device(ordinal));
     VH_HIP(hipDeviceSynchronize());

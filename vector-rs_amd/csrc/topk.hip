@@ -23,6 +23,16 @@ __global__ void k_topk_init(int nq, float *tau, uint32_t *have, uint32_t *cnt, u
     }
 }
 
+__global__ void k_fill_f32(float *p, size_t count, float v) {
+    const size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+    if (i < count) p[i] = v;
+}
+
+void launch_fill(float *p, size_t count, float v, hipStream_t s) {
+    if (count == 0) return;
+    hipLaunchKernelGGL(k_fill_f32, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, s, p, count, v);
+}
+
 void launch_topk_init(int nq, float *tau, uint32_t *have, uint32_t *cnt, uint32_t *flags, hipStream_t s) {
     if (nq <= 0) return;
     hipLaunchKernelGGL(k_topk_init, dim3(ceil_div(nq, 256)), dim3(256), 0, s, nq, tau, have, cnt, flags);
@@ -49,7 +59,8 @@ __device__ __forceinline__ void bitonic_sort_lds(u64 *buf, int P) {
 }
 
 __global__ __launch_bounds__(256) void k_topk_merge(int k, const uint2 *__restrict__ cand, uint32_t *__restrict__ cnt,
-                                                    int cap, u64 *__restrict__ topk, uint32_t *__restrict__ have,
+                                                    int cap, const uint32_t *__restrict__ perm,
+                                                    u64 *__restrict__ topk, uint32_t *__restrict__ have,
                                                     float *__restrict__ tau, uint32_t *__restrict__ flags,
                                                     uint32_t *__restrict__ nflagged) {
     __shared__ u64 buf[kSortSlots];
@@ -72,7 +83,7 @@ __global__ __launch_bounds__(256) void k_topk_merge(int k, const uint2 *__restri
         const uint32_t take = min(c - done, (uint32_t)kSortSlots - h);
         for (uint32_t i = tid; i < take; i += 256) {
             const uint2 e = cq[done + i];
-            buf[h + i] = ((u64)e.x << 32) | (u64)e.y;
+            buf[h + i] = ((u64)e.x << 32) | (u64)perm[e.y];  // base position -> vector id
         }
         const uint32_t total = h + take;
         int P = 2;
@@ -99,10 +110,12 @@ __global__ __launch_bounds__(256) void k_topk_merge(int k, const uint2 *__restri
     }
 }
 
-void launch_topk_merge(int nq, int k, const uint2 *cand, uint32_t *cnt, int cap, unsigned long long *topk,
-                       uint32_t *have, float *tau, uint32_t *flags, uint32_t *nflagged, hipStream_t s) {
+void launch_topk_merge(int nq, int k, const uint2 *cand, uint32_t *cnt, int cap, const uint32_t *perm,
+                       unsigned long long *topk, uint32_t *have, float *tau, uint32_t *flags, uint32_t *nflagged,
+                       hipStream_t s) {
     if (nq <= 0) return;
-    hipLaunchKernelGGL(k_topk_merge, dim3(nq), dim3(256), 0, s, k, cand, cnt, cap, topk, have, tau, flags, nflagged);
+    hipLaunchKernelGGL(k_topk_merge, dim3(nq), dim3(256), 0, s, k, cand, cnt, cap, perm, topk, have, tau, flags,
+                       nflagged);
 }
 
 __global__ void k_topk_finalize(int nq, int k, int kout, int metric, const u64 *__restrict__ topk,
@@ -115,7 +128,7 @@ __global__ void k_topk_finalize(int nq, int k, int kout, int metric, const u64 *
     if ((uint32_t)j < have[q]) {
         const u64 e = topk[(size_t)q * k + j];
         const float sc = key_score((uint32_t)(e >> 32));
-        const float d = (metric == DOT || metric == COS) ? -sc : sc;
+        const float d = (metric == DOT || metric == COS) ? -sc + 0.0f : sc;
         out_ids[o] = (uint32_t)e;
         if (out_dist) out_dist[o] = d;
         if (out_dist_u32) out_dist_u32[o] = (uint32_t)d;
@@ -144,6 +157,7 @@ void launch_topk_finalize(int nq, int k, int kout, int metric, const unsigned lo
 __global__ __launch_bounds__(256) void k_topk_refine(int k, int kout, int metric, const float *__restrict__ qpad,
                                                      const float *__restrict__ base,
                                                      const uint32_t *__restrict__ inv_perm, int dpad,
+                                                     const float *__restrict__ qnorm, const float *__restrict__ bnorm,
                                                      const u64 *__restrict__ topk, const uint32_t *__restrict__ have,
                                                      uint32_t *__restrict__ out_ids, float *__restrict__ out_dist,
                                                      int ostride) {
@@ -154,7 +168,8 @@ __global__ __launch_bounds__(256) void k_topk_refine(int k, int kout, int metric
     for (int j = wave; j < h; j += 4) {
         const u64 e = topk[(size_t)q * k + j];
         const uint32_t id = (uint32_t)e;
-        const float *xv = base + (size_t)inv_perm[id] * dpad;
+        const uint32_t row = inv_perm[id];
+        const float *xv = base + (size_t)row * dpad;
         float a = 0.0f, nq = 0.0f, nx = 0.0f;
         for (int d = lane; d < dpad; d += 64) {
             const float x = xv[d], y = qv[d];
@@ -177,10 +192,11 @@ __global__ __launch_bounds__(256) void k_topk_refine(int k, int kout, int metric
         if (metric == L2) {
             sc = a;
         } else if (metric == DOT) {
-            sc = -a;
+            sc = -a + 0.0f;
         } else {
+            // rows and queries are stored L2-normalised; the zero-norm rule uses the original norms
             const float den = sqrtf(nq) * sqrtf(nx);
-            sc = den <= 1e-9f ? -0.0f : -(a / den);
+            sc = (den <= 1e-9f || qnorm[q] * bnorm[row] <= 1e-9f) ? 0.0f : -(a / den) + 0.0f;
         }
         if (lane == 0) buf[j] = ((u64)score_key(sc) << 32) | id;
     }
@@ -194,7 +210,7 @@ __global__ __launch_bounds__(256) void k_topk_refine(int k, int kout, int metric
         if (j < h) {
             const float sc = key_score((uint32_t)(buf[j] >> 32));
             out_ids[o] = (uint32_t)buf[j];
-            out_dist[o] = metric == L2 ? sc : -sc;
+            out_dist[o] = metric == L2 ? sc : -sc + 0.0f;
         } else {
             out_ids[o] = 0xffffffffu;
             out_dist[o] = __builtin_nanf("");
@@ -203,11 +219,12 @@ __global__ __launch_bounds__(256) void k_topk_refine(int k, int kout, int metric
 }
 
 void launch_topk_refine(int nq, int k, int kout, int metric, const float *qpad, const float *base,
-                        const uint32_t *inv_perm, int dpad, const unsigned long long *topk, const uint32_t *have,
-                        uint32_t *out_ids, float *out_dist, int ostride, hipStream_t s) {
+                        const uint32_t *inv_perm, int dpad, const float *qnorm, const float *bnorm,
+                        const unsigned long long *topk, const uint32_t *have, uint32_t *out_ids, float *out_dist,
+                        int ostride, hipStream_t s) {
     if (nq <= 0) return;
-    hipLaunchKernelGGL(k_topk_refine, dim3(nq), dim3(256), 0, s, k, kout, metric, qpad, base, inv_perm, dpad, topk,
-                       have, out_ids, out_dist, ostride);
+    hipLaunchKernelGGL(k_topk_refine, dim3(nq), dim3(256), 0, s, k, kout, metric, qpad, base, inv_perm, dpad, qnorm,
+                       bnorm, topk, have, out_ids, out_dist, ostride);
 }
 
 }  // namespace vh

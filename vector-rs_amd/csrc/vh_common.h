@@ -16,8 +16,9 @@ constexpr int kCap = 16384;          // candidate slots per query per round (def
 constexpr int kMaxK = 2048;          // VHIP_MAX_K
 constexpr int kSortSlots = 4096;     // LDS sort buffer of the merge kernel (u64 keys)
 constexpr int kKChunk = 32;          // K (dimension) chunk of the MFMA tiles
-constexpr int kTileRows = 128;       // base rows per MFMA stage
-constexpr int kTileCols = 128;       // queries per MFMA workgroup
+constexpr int kTileCols = 128;       // queries (or k-means points) per MFMA work item
+constexpr int kRowAlign = 256;       // row counts of MFMA row operands and round boundaries
+                                     // are multiples of this (the largest MFMA stage)
 
 // Maps a float score (smaller is better) to an unsigned key with the same order.
 __host__ __device__ inline uint32_t score_key(float s) {
@@ -33,30 +34,39 @@ inline int ceil_div(long a, long b) { return (int)((a + b - 1) / b); }
 inline size_t round_up(size_t a, size_t b) { return (a + b - 1) / b * b; }
 
 // ---- launchers (defined in the .hip files) ----------------------------------
-// knn_gemm.hip
-// Copies n rows of `dim` floats into padded rows of `dpad` floats (zero fill), in the
-// order given by `perm` (out row p = in row perm[p]) or identity if perm == nullptr,
-// and writes per-row squared norms (norm_kind 1) or L2 norms (norm_kind 2) to `norm`.
-// transform 1 stores sqrt(|x|) instead of x (Hellinger).  With norm_kind 0 and transform 0
-// the copy is bit-exact, so it also moves packed uint32 codes.
-void launch_rows_prep(const float *in, size_t n, int dim, int dpad, const uint32_t *perm, float *out,
-                      float *norm, int norm_kind, int transform, hipStream_t s);
-// One round of the fused MFMA distance + threshold filter.
-// grid_cap: number of workgroups of the persistent grid (resident capacity of the GPU).
-void launch_gemm_filter(int metric, const float *base, const float *bnorm, const uint32_t *perm,
-                        const float *qry, const float *qnorm, const float *tau, int nq, int dpad, long row_begin,
-                        long row_end, uint2 *cand, uint32_t *cnt, int cap, int grid_cap, hipStream_t s);
+// Candidate lists: every filter kernel appends (score key, row) pairs where `row` is the
+// position in the resident (permuted) base; k_topk_merge maps positions to vector ids.
 
-// MFMA k-means assignment (knn_gemm.hip); metric L2 / DOT / COS.  cnorm holds squared
-// norms for L2 and L2 norms for COS; pnorm likewise for the points.
-void launch_kmeans_assign(int metric, const float *cent, const float *cnorm, int k, const float *pts,
+// knn_gemm.hip
+// Copies rows [0, n) of `dim` floats into rows of `dpad` floats (zero fill), in the order
+// given by `perm` (out row p = in row perm[p]) or identity if perm == nullptr, optionally
+// sqrt(|x|)-transformed (transform 1, Hellinger) and L2-normalised (normalize 1), and fills
+// rows [n, n_out) with `pad_fill`.  norm_kind 1 writes per-row squared L2 norms, 2 L2 norms
+// (before normalisation).  With norm_kind 0, transform 0 and normalize 0 the copy is
+// bit-exact, so it also moves packed uint32 codes.
+void launch_rows_prep(const float *in, size_t n, size_t n_out, int dim, int dpad, const uint32_t *perm, float *out,
+                      float *norm, int norm_kind, int transform, int normalize, float pad_fill, hipStream_t s);
+// One round of the fused MFMA distance + threshold filter over base rows [row_begin, row_end)
+// (row_begin a multiple of 128, row_end a multiple of 128 or the padded end of the base).
+// `base` has its rows padded to a multiple of 128 with NaN rows; `qry` has nq rows padded to a
+// multiple of 128.  anorm_max / anorm_min: extremes of bnorm over the real rows.
+// grid_cap: number of workgroups of the persistent grid (resident capacity of the GPU).
+void launch_gemm_filter(int metric, const float *base, const float *bnorm, const float *qry, const float *qnorm,
+                        const float *tau, int nq, int dpad, long row_begin, long row_end, uint2 *cand, uint32_t *cnt,
+                        int cap, float anorm_max, float anorm_min, int grid_cap, hipStream_t s);
+
+// MFMA k-means assignment (knn_gemm.hip); metric L2 / DOT / COS.  `cent` has kpad rows
+// (a multiple of 128, NaN padding rows), `pts` n rows padded to a multiple of 128 (zeros).
+// cnorm / pnorm hold squared norms for L2 and L2 norms for COS.
+void launch_kmeans_assign(int metric, const float *cent, const float *cnorm, int kpad, const float *pts,
                           const float *pnorm, int n, int dpad, int32_t *assign, float *inertia, int32_t *pos,
                           int32_t *counts, int grid_cap, hipStream_t s);
 
 // topk.hip
 void launch_topk_init(int nq, float *tau, uint32_t *have, uint32_t *cnt, uint32_t *flags, hipStream_t s);
-void launch_topk_merge(int nq, int k, const uint2 *cand, uint32_t *cnt, int cap, unsigned long long *topk,
-                       uint32_t *have, float *tau, uint32_t *flags, uint32_t *nflagged, hipStream_t s);
+void launch_topk_merge(int nq, int k, const uint2 *cand, uint32_t *cnt, int cap, const uint32_t *perm,
+                       unsigned long long *topk, uint32_t *have, float *tau, uint32_t *flags, uint32_t *nflagged,
+                       hipStream_t s);
 // Writes results: out_ids[q*ostride + j], out_dist[...] for j < have[q]; distance is the
 // metric value recovered from the score (negated for similarities, transformed for
 // Minkowski / Mahalanobis / Hellinger).  Entries past have[q] are set to UINT32_MAX / NaN.
@@ -66,21 +76,25 @@ void launch_topk_finalize(int nq, int k, int kout, int metric, const unsigned lo
                           const uint32_t *have, uint32_t *out_ids, float *out_dist, uint32_t *out_dist_u32,
                           int ostride, hipStream_t s);
 // GEMM metrics: recompute the kept distances in direct form, re-sort by (distance, id) and
-// write them (same output contract as launch_topk_finalize; out_dist required).
+// write them (same output contract as launch_topk_finalize; out_dist required).  qnorm / bnorm
+// are the original L2 norms (cosine zero-norm guard; unused for the other metrics).
 void launch_topk_refine(int nq, int k, int kout, int metric, const float *qpad, const float *base,
-                        const uint32_t *inv_perm, int dpad, const unsigned long long *topk, const uint32_t *have,
-                        uint32_t *out_ids, float *out_dist, int ostride, hipStream_t s);
+                        const uint32_t *inv_perm, int dpad, const float *qnorm, const float *bnorm,
+                        const unsigned long long *topk, const uint32_t *have, uint32_t *out_ids, float *out_dist,
+                        int ostride, hipStream_t s);
 // hamming.hip
 int hamming_word_pad(int words);
-void launch_hamming_filter(const uint32_t *codes, const uint32_t *perm, const uint32_t *qry, const float *tau,
-                           int nq, int wpad, long row_begin, long row_end, uint2 *cand, uint32_t *cnt, int cap,
-                           int grid_cap, hipStream_t s);
+void launch_hamming_filter(const uint32_t *codes, const uint32_t *qry, const float *tau, int nq, int wpad,
+                           long row_begin, long row_end, uint2 *cand, uint32_t *cnt, int cap, int grid_cap,
+                           hipStream_t s);
 // knn_valu.hip
 void launch_kmeans_assign_valu(int metric, const float *cent, int k, const float *pts, int n, int dpad,
                                int32_t *assign, float *inertia, int32_t *pos, int32_t *counts, int grid_cap,
                                hipStream_t s);
-void launch_valu_filter(int metric, const float *base, const uint32_t *perm, const float *qry, const float *tau,
-                        int nq, int dim, int dpad, long row_begin, long row_end, uint2 *cand, uint32_t *cnt, int cap,
-                        int grid_cap, hipStream_t s);
+void launch_valu_filter(int metric, const float *base, const float *qry, const float *tau, int nq, int dim, int dpad,
+                        long row_begin, long row_end, uint2 *cand, uint32_t *cnt, int cap, int grid_cap,
+                        hipStream_t s);
+// Fills count floats with v (a kernel, so it is safe inside captured graphs).
+void launch_fill(float *p, size_t count, float v, hipStream_t s);
 
 }  // namespace vh

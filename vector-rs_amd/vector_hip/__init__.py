@@ -90,6 +90,7 @@ _sig("vhip_malloc", _int, _int, _sz, ctypes.POINTER(_vp))
 _sig("vhip_free", _int, _int, _vp)
 _sig("vhip_memcpy_htod", _int, _int, _vp, _vp, _sz)
 _sig("vhip_memcpy_dtoh", _int, _int, _vp, _vp, _sz)
+_sig("vhip_memcpy_dtod", _int, _int, _vp, _vp, _sz)
 _sig("vhip_synchronize", _int, _int)
 _HAS_KMEANS = hasattr(_lib, "vhip_kmeans_fit")
 if _HAS_KMEANS:
@@ -597,6 +598,12 @@ class DeviceBuffer:
         assert out.flags.c_contiguous and out.nbytes <= self.nbytes
         _check(_lib.vhip_memcpy_dtoh(self.ordinal, out.ctypes.data, self.ptr, out.nbytes))
         return out
+
+    def copy_from(self, other: "DeviceBuffer", nbytes: Optional[int] = None):
+        """Device-to-device copy of nbytes (default: all of `other`)."""
+        nb = other.nbytes if nbytes is None else nbytes
+        assert nb <= self.nbytes and nb <= other.nbytes
+        _check(_lib.vhip_memcpy_dtod(self.ordinal, self.ptr, other.ptr, nb))
 
     def free(self):
         if self.ptr:
