@@ -5,12 +5,14 @@
 // knn.cu:107-115) over f32 vectors; on 0/1 codes it equals popcount(a ^ b), which is what
 // this kernel computes on 32-bit words (v_xor_b32 + v_bcnt_u32_b32 per word, two VALU
 // operations per word per query).  Each lane owns one query's W words in registers; tiles of
-// base codes are staged in LDS and read as broadcasts.  Distances are exact integers.
+// base codes are staged in LDS and read as broadcasts.  Distances are exact integers.  The
+// threshold test is batched over 4 rows (one wave-uniform branch per 4 rows) and the grid runs
+// 8 workgroups per CU, so tile loads of one workgroup hide behind the others' popcounts.
 #include "vh_common.h"
 
 namespace vh {
 
-constexpr int kHamRows = 64;
+constexpr int kHamRows = 128;
 constexpr long kHamItemRows = 8192;
 
 template <int W>
@@ -43,21 +45,40 @@ __global__ __launch_bounds__(256) void k_hamming_filter(const uint32_t *__restri
 
         for (long rs = r_lo; rs < r_hi; rs += kHamRows) {
             __syncthreads();
-            for (int i = tid; i < kHamRows * W; i += 256) {
-                const int row = i / W, w = i % W;
-                const long r = rs + row;
-                tile[i] = (r < r_hi && w < wpad) ? codes[r * wpad + w] : 0u;
+            if constexpr (W >= 4) {
+                // rows are W words (W = wpad here), so the tile is a contiguous run of uint4
+                for (int i = tid; i < kHamRows * W / 4; i += 256) {
+                    const long r = rs + (i * 4) / W;
+                    ((uint4 *)tile)[i] = r < r_hi ? ((const uint4 *)(codes + rs * W))[i] : make_uint4(0, 0, 0, 0);
+                }
+            } else {
+                for (int i = tid; i < kHamRows * W; i += 256) {
+                    const int row = i / W, w = i % W;
+                    const long r = rs + row;
+                    tile[i] = (r < r_hi && w < wpad) ? codes[r * wpad + w] : 0u;
+                }
             }
             __syncthreads();
             const int nvalid = (int)min((long)kHamRows, r_hi - rs);
-#pragma unroll 4
-            for (int r = 0; r < kHamRows; ++r) {
-                uint32_t d = 0;
+#pragma unroll 2
+            for (int r = 0; r < kHamRows; r += 4) {
+                uint32_t d[4];
 #pragma unroll
-                for (int w = 0; w < W; ++w) d += (uint32_t)__popc(qw[w] ^ tile[r * W + w]);
-                if (d <= tq && any && r < nvalid) {
-                    const uint32_t at = atomicAdd(&cnt[q], 1u);
-                    if (at < (uint32_t)cap) cand[(size_t)q * cap + at] = make_uint2(score_key((float)d), (uint32_t)(rs + r));
+                for (int i = 0; i < 4; ++i) {
+                    d[i] = 0;
+#pragma unroll
+                    for (int w = 0; w < W; ++w) d[i] += (uint32_t)__popc(qw[w] ^ tile[(r + i) * W + w]);
+                }
+                const bool p = any && (d[0] <= tq || d[1] <= tq || d[2] <= tq || d[3] <= tq);
+                if (__builtin_amdgcn_ballot_w64(p)) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        if (any && d[i] <= tq && r + i < nvalid) {
+                            const uint32_t at = atomicAdd(&cnt[q], 1u);
+                            if (at < (uint32_t)cap)
+                                cand[(size_t)q * cap + at] = make_uint2(score_key((float)d[i]), (uint32_t)(rs + r + i));
+                        }
+                    }
                 }
             }
         }
@@ -77,7 +98,8 @@ void launch_hamming_filter(const uint32_t *codes, const uint32_t *qry, const flo
     const int nqt = ceil_div(nq, 256);
     const long n_chunks = (row_end - row_begin + kHamItemRows - 1) / kHamItemRows;
     const long items = (long)nqt * n_chunks;
-    long grid = items < grid_cap ? items : grid_cap;
+    const long resident = 4L * grid_cap;  // 8 workgroups per CU
+    long grid = items < resident ? items : resident;
     grid = (grid + 7) / 8 * 8;
     const dim3 g((unsigned)grid), b(256);
     const int it = (int)items;
