@@ -1,0 +1,376 @@
+/*
+ * vector_hip.hpp -- C++ host API over the C ABI of vector_hip.h, mirroring the Rust API of the
+ * reference's GPU hot path (crate vector-cuda) so that code written against it reads the same:
+ *
+ *   CudaDeviceContext     vector-cuda/src/device.rs:81-256      (hardware only, no emulator)
+ *   CudaKnnEngine         vector-cuda/src/knn.rs:45-401
+ *   DistributedKnnEngine  vector-cuda/src/ddp/distributed_knn.rs:24-262, GpuShardMode :14-19
+ *   CollectiveOps         vector-cuda/src/ddp/collective.rs:115-159 (top_k_reduce only)
+ *   CudaKMeansEngine      vector-cuda/src/kmeans.rs:37-467, CudaKMeansResult :15-35
+ *   DistributedKMeansEngine vector-cuda/src/ddp/distributed_kmeans.rs:19-541
+ *   CudaError             vector-cuda/src/error.rs:7-29 (thrown; Result<T, CudaError> -> T or throw)
+ *   DistanceMetric, SearchResult, VectorId   vector-index/src/lib.rs:50-94, types.rs:5-20
+ *
+ * Rust slices (&[f32]) become (pointer, length) pairs or std::vector; Vec<Vec<SearchResult>>
+ * becomes std::vector<std::vector<SearchResult>>.  Where the Rust API panics on a violated
+ * precondition (assert!), this API throws CudaError(InvalidConfig).  Where the reference
+ * silently fell back to the CPU, this API throws: every call runs on the GPU or fails.
+ * Extensions (no reference counterpart): explicit initial centroids and seeds for k-means,
+ * and HammingKnnEngine for packed-bit codes.
+ */
+#ifndef VECTOR_HIP_HPP
+#define VECTOR_HIP_HPP
+
+#include <cstdint>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <utility>
+#include <vector>
+
+#include "vector_hip.h"
+
+namespace vector_hip {
+
+using VectorId = uint32_t;
+
+enum class DistanceMetric : int {
+    L2Squared = VHIP_METRIC_L2SQUARED,
+    DotProduct = VHIP_METRIC_DOTPRODUCT,
+    CosineSimilarity = VHIP_METRIC_COSINE,
+    Manhattan = VHIP_METRIC_MANHATTAN,
+    Minkowski = VHIP_METRIC_MINKOWSKI,
+    Chebyshev = VHIP_METRIC_CHEBYSHEV,
+    Hamming = VHIP_METRIC_HAMMING,
+    Mahalanobis = VHIP_METRIC_MAHALANOBIS,
+    Jaccard = VHIP_METRIC_JACCARD,
+    Hellinger = VHIP_METRIC_HELLINGER,
+};
+
+/* DistanceMetric::higher_is_better (lib.rs:89-94) */
+inline bool higher_is_better(DistanceMetric m) {
+    return m == DistanceMetric::DotProduct || m == DistanceMetric::CosineSimilarity;
+}
+
+enum class GpuShardMode : int { Sharded = VHIP_SHARD_SHARDED, Replicated = VHIP_SHARD_REPLICATED };
+
+struct SearchResult {
+    VectorId id;
+    float distance;
+};
+
+class CudaError : public std::runtime_error {
+public:
+    enum class Kind { InsufficientDevices, DeviceNotFound, DriverError, HardwareNotAvailable, InvalidConfig };
+    CudaError(Kind kind, const std::string &msg, size_t requested = 0, size_t available = 0)
+        : std::runtime_error(msg), kind_(kind), requested_(requested), available_(available) {}
+    Kind kind() const { return kind_; }
+    size_t requested() const { return requested_; } /* InsufficientDevices */
+    size_t available() const { return available_; } /* InsufficientDevices */
+
+private:
+    Kind kind_;
+    size_t requested_, available_;
+};
+
+namespace detail {
+inline void check(int status) {
+    if (status == VHIP_OK) return;
+    const std::string msg = vhip_last_error();
+    switch (status) {
+        case VHIP_ERR_INSUFFICIENT_DEVICES: {
+            size_t r = 0, a = 0;
+            vhip_last_error_devices(&r, &a);
+            throw CudaError(CudaError::Kind::InsufficientDevices, msg, r, a);
+        }
+        case VHIP_ERR_DEVICE_NOT_FOUND: throw CudaError(CudaError::Kind::DeviceNotFound, msg);
+        case VHIP_ERR_HARDWARE_NOT_AVAILABLE: throw CudaError(CudaError::Kind::HardwareNotAvailable, msg);
+        case VHIP_ERR_INVALID_CONFIG: throw CudaError(CudaError::Kind::InvalidConfig, msg);
+        default: throw CudaError(CudaError::Kind::DriverError, msg);
+    }
+}
+inline void require(bool ok, const char *what) {
+    if (!ok) throw CudaError(CudaError::Kind::InvalidConfig, what);
+}
+inline std::vector<std::vector<SearchResult>> to_lists(size_t nq, size_t k, const std::vector<uint32_t> &ids,
+                                                       const std::vector<float> &dist,
+                                                       const std::vector<size_t> &len) {
+    std::vector<std::vector<SearchResult>> out(nq);
+    for (size_t q = 0; q < nq; ++q) {
+        out[q].reserve(len[q]);
+        for (size_t j = 0; j < len[q]; ++j) out[q].push_back(SearchResult{ids[q * k + j], dist[q * k + j]});
+    }
+    return out;
+}
+}  // namespace detail
+
+/* ---- CudaDeviceContext (device.rs:81-256) -------------------------------------------------- */
+class CudaDeviceContext {
+public:
+    static size_t device_count() { return (size_t)vhip_device_count(); }
+    /* CudaDeviceContext::new(): ordinal 0 */
+    CudaDeviceContext() : CudaDeviceContext(0) {}
+    static CudaDeviceContext with_ordinal_strict(size_t ordinal) { return CudaDeviceContext(ordinal); }
+    size_t device_id() const { return id_; }
+    const std::string &device_name() const { return name_; }
+    size_t total_memory_bytes() const { return mem_; }
+    bool is_hardware_available() const { return true; }
+
+private:
+    explicit CudaDeviceContext(size_t ordinal) : id_(ordinal) {
+        char buf[256];
+        detail::check(vhip_device_info((int)ordinal, buf, sizeof buf, &mem_));
+        name_ = buf;
+    }
+    size_t id_ = 0, mem_ = 0;
+    std::string name_;
+};
+
+/* ---- CudaKnnEngine (knn.rs:45-401) ------------------------------------------------------- */
+class CudaKnnEngine {
+public:
+    /* CudaKnnEngine::new (knn.rs:85-88) */
+    CudaKnnEngine(const float *dataset, size_t len, size_t dimension, DistanceMetric metric)
+        : CudaKnnEngine(dataset, len, dimension, metric, 0) {}
+    CudaKnnEngine(const std::vector<float> &dataset, size_t dimension, DistanceMetric metric)
+        : CudaKnnEngine(dataset.data(), dataset.size(), dimension, metric, 0) {}
+    /* CudaKnnEngine::with_ordinal (knn.rs:90-140) */
+    static CudaKnnEngine with_ordinal(const std::vector<float> &dataset, size_t dimension, DistanceMetric metric,
+                                      size_t ordinal) {
+        return CudaKnnEngine(dataset.data(), dataset.size(), dimension, metric, ordinal);
+    }
+
+    /* knn.rs:143-149: the first query's results (empty for an empty query) */
+    std::vector<SearchResult> search(const float *query, size_t len, size_t k) const {
+        auto r = search_batch(query, len, k);
+        return r.empty() ? std::vector<SearchResult>{} : std::move(r[0]);
+    }
+    std::vector<SearchResult> search(const std::vector<float> &query, size_t k) const {
+        return search(query.data(), query.size(), k);
+    }
+    /* knn.rs:151-169: len / dimension queries, min(k, N) results each, best first */
+    std::vector<std::vector<SearchResult>> search_batch(const float *queries, size_t len, size_t k) const {
+        detail::require(len % dim_ == 0, "query length is not a multiple of the dimension");
+        const size_t nq = len / dim_;
+        if (nq == 0) return {};
+        std::vector<uint32_t> ids(nq * (k ? k : 1));
+        std::vector<float> dist(nq * (k ? k : 1));
+        std::vector<size_t> lens(nq);
+        detail::check(vhip_knn_search_batch(h_.get(), queries, nq, k, ids.data(), dist.data(), lens.data()));
+        return detail::to_lists(nq, k ? k : 1, ids, dist, lens);
+    }
+    std::vector<std::vector<SearchResult>> search_batch(const std::vector<float> &queries, size_t k) const {
+        return search_batch(queries.data(), queries.size(), k);
+    }
+
+    CudaDeviceContext context() const { return CudaDeviceContext::with_ordinal_strict(device_id()); }
+    size_t device_id() const { return (size_t)vhip_knn_device_id(h_.get()); }
+    size_t dimension() const { return vhip_knn_dimension(h_.get()); }
+    size_t num_vectors() const { return vhip_knn_num_vectors(h_.get()); }
+    DistanceMetric metric() const { return (DistanceMetric)vhip_knn_metric(h_.get()); }
+    vhip_knn *raw() const { return h_.get(); }
+
+private:
+    CudaKnnEngine(const float *dataset, size_t len, size_t dimension, DistanceMetric metric, size_t ordinal)
+        : dim_(dimension) {
+        detail::require(dimension > 0, "dimension must be > 0");
+        detail::require(len % dimension == 0, "dataset length is not a multiple of the dimension");
+        vhip_knn *h = nullptr;
+        detail::check(vhip_knn_create(dataset, len / dimension, dimension, (int)metric, (int)ordinal, &h));
+        h_.reset(h);
+    }
+    struct Del {
+        void operator()(vhip_knn *p) const { vhip_knn_destroy(p); }
+    };
+    size_t dim_;
+    std::unique_ptr<vhip_knn, Del> h_;
+};
+
+/* ---- DistributedKnnEngine (ddp/distributed_knn.rs:24-262) ------------------------------- */
+class DistributedKnnEngine {
+public:
+    /* :40-61 -- InsufficientDevices when num_gpus exceeds the device count */
+    static DistributedKnnEngine try_new(const std::vector<float> &dataset, size_t dimension, size_t num_gpus,
+                                        GpuShardMode mode, DistanceMetric metric) {
+        return DistributedKnnEngine(dataset, dimension, num_gpus, mode, metric, false);
+    }
+    /* :64-74 -- no device-count check; every rank runs on GPU 0 */
+    static DistributedKnnEngine emulator(const std::vector<float> &dataset, size_t dimension, size_t num_gpus,
+                                         GpuShardMode mode, DistanceMetric metric) {
+        return DistributedKnnEngine(dataset, dimension, num_gpus, mode, metric, true);
+    }
+    /* :77-89 (the Rust new() panics where try_new errs; this one throws) */
+    static DistributedKnnEngine new_(const std::vector<float> &dataset, size_t dimension, size_t num_gpus,
+                                     GpuShardMode mode, DistanceMetric metric) {
+        return try_new(dataset, dimension, num_gpus, mode, metric);
+    }
+
+    std::vector<SearchResult> search(const std::vector<float> &query, size_t k) const {
+        auto r = search_batch(query, k);
+        return r.empty() ? std::vector<SearchResult>{} : std::move(r[0]);
+    }
+    std::vector<std::vector<SearchResult>> search_batch(const std::vector<float> &queries, size_t k) const {
+        detail::require(queries.size() % dim_ == 0, "query length is not a multiple of the dimension");
+        const size_t nq = queries.size() / dim_;
+        if (nq == 0) return {};
+        std::vector<uint32_t> ids(nq * (k ? k : 1));
+        std::vector<float> dist(nq * (k ? k : 1));
+        std::vector<size_t> lens(nq);
+        detail::check(vhip_dknn_search_batch(h_.get(), queries.data(), nq, k, ids.data(), dist.data(), lens.data()));
+        return detail::to_lists(nq, k ? k : 1, ids, dist, lens);
+    }
+    size_t num_gpus() const { return vhip_dknn_num_gpus(h_.get()); }
+    GpuShardMode mode() const { return (GpuShardMode)vhip_dknn_mode(h_.get()); }
+    size_t dimension() const { return vhip_dknn_dimension(h_.get()); }
+    size_t num_vectors() const { return vhip_dknn_num_vectors(h_.get()); }
+    DistanceMetric metric() const { return (DistanceMetric)vhip_dknn_metric(h_.get()); }
+
+private:
+    DistributedKnnEngine(const std::vector<float> &dataset, size_t dimension, size_t num_gpus, GpuShardMode mode,
+                         DistanceMetric metric, bool emulate)
+        : dim_(dimension) {
+        detail::require(num_gpus >= 1, "num_gpus must be at least 1");
+        detail::require(dimension > 0 && dataset.size() % dimension == 0,
+                        "dataset length is not a multiple of the dimension");
+        vhip_dknn *h = nullptr;
+        auto fn = emulate ? vhip_dknn_emulator : vhip_dknn_try_new;
+        detail::check(fn(dataset.data(), dataset.size() / dimension, dimension, num_gpus, (int)mode, (int)metric, &h));
+        h_.reset(h);
+    }
+    struct Del {
+        void operator()(vhip_dknn *p) const { vhip_dknn_destroy(p); }
+    };
+    size_t dim_;
+    std::unique_ptr<vhip_dknn, Del> h_;
+};
+
+/* ---- CollectiveOps::top_k_reduce (ddp/collective.rs:115-159) ------------------------------ */
+struct CollectiveOps {
+    static std::vector<SearchResult> top_k_reduce(const std::vector<std::vector<SearchResult>> &per_rank, size_t k,
+                                                  DistanceMetric metric) {
+        std::vector<uint32_t> ids;
+        std::vector<float> dist;
+        for (const auto &r : per_rank)
+            for (const auto &e : r) {
+                ids.push_back(e.id);
+                dist.push_back(e.distance);
+            }
+        if (ids.empty() || k == 0) return {};
+        std::vector<uint32_t> oi(k);
+        std::vector<float> od(k);
+        const size_t m = vhip_top_k_reduce(ids.data(), dist.data(), ids.size(), k, (int)metric, oi.data(), od.data());
+        std::vector<SearchResult> out(m);
+        for (size_t i = 0; i < m; ++i) out[i] = SearchResult{oi[i], od[i]};
+        return out;
+    }
+};
+
+/* ---- k-means (kmeans.rs:15-467, ddp/distributed_kmeans.rs) -------------------------------- */
+struct CudaKMeansResult {
+    std::vector<float> centroids; /* k x dimension */
+    size_t dimension = 0;
+    size_t k = 0;
+    size_t iterations = 0;
+    float inertia = 0.0f;
+    const float *centroid(size_t i) const { return centroids.data() + i * dimension; }
+};
+
+/* Extension: where the initial centroids come from (the reference drew them from an unseeded
+ * thread_rng). */
+struct KMeansInit {
+    const float *centroids = nullptr; /* effective_k x dimension, or null for a seeded init */
+    uint64_t seed = 42;
+};
+
+namespace detail {
+inline CudaKMeansResult kmeans_fit(size_t ordinal, const float *data, size_t len, size_t dimension, size_t k,
+                                   size_t max_iters, float tolerance, DistanceMetric metric, int init_mode,
+                                   const KMeansInit &init, std::vector<int32_t> *assign) {
+    require(dimension > 0, "dimension must be > 0");
+    const size_t n = len / dimension;
+    CudaKMeansResult r;
+    r.dimension = dimension;
+    if (n == 0 || k == 0) return r; /* kmeans.rs:67-76 */
+    const size_t ek = k < n ? k : n;
+    r.centroids.resize(ek * dimension);
+    if (assign) assign->resize(n);
+    vhip_kmeans_result c{};
+    check(vhip_kmeans_fit((int)ordinal, data, n, dimension, k, max_iters, tolerance, (int)metric, init.centroids,
+                          init_mode, init.seed, r.centroids.data(), assign ? assign->data() : nullptr, &c));
+    r.k = c.k;
+    r.iterations = c.iterations;
+    r.inertia = c.inertia;
+    return r;
+}
+}  // namespace detail
+
+class CudaKMeansEngine {
+public:
+    CudaKMeansEngine() : ctx_(CudaDeviceContext()) {}
+    const CudaDeviceContext &context() const { return ctx_; }
+    /* kmeans.rs:58-97 -- seeded k-means++ init (kmeans.rs:409-460) unless init.centroids is set */
+    CudaKMeansResult fit(const std::vector<float> &data, size_t dimension, size_t k, size_t max_iters,
+                         float tolerance, DistanceMetric metric, const KMeansInit &init = {},
+                         std::vector<int32_t> *assign = nullptr) const {
+        return detail::kmeans_fit(ctx_.device_id(), data.data(), data.size(), dimension, k, max_iters, tolerance,
+                                  metric, VHIP_INIT_KMEANSPP, init, assign);
+    }
+
+private:
+    CudaDeviceContext ctx_;
+};
+
+class DistributedKMeansEngine {
+public:
+    /* distributed_kmeans.rs:28-38 */
+    static DistributedKMeansEngine try_new(size_t num_gpus) {
+        detail::require(num_gpus >= 1, "num_gpus must be at least 1");
+        detail::check(vhip_dkmeans_check(num_gpus));
+        return DistributedKMeansEngine(num_gpus);
+    }
+    /* :41-44 */
+    static DistributedKMeansEngine emulator(size_t num_gpus) {
+        detail::require(num_gpus >= 1, "num_gpus must be at least 1");
+        return DistributedKMeansEngine(num_gpus);
+    }
+    static DistributedKMeansEngine new_(size_t num_gpus) { return try_new(num_gpus); }
+    size_t num_gpus() const { return g_; }
+    /* :55-106 at one GPU: runs on GPU 0 (the reference ran fit_cpu), seeded shuffle init
+     * (distributed_kmeans.rs:524-535) unless init.centroids is set */
+    CudaKMeansResult fit(const std::vector<float> &data, size_t dimension, size_t k, size_t max_iters,
+                         float tolerance, DistanceMetric metric, const KMeansInit &init = {},
+                         std::vector<int32_t> *assign = nullptr) const {
+        return detail::kmeans_fit(0, data.data(), data.size(), dimension, k, max_iters, tolerance, metric,
+                                  VHIP_INIT_SHUFFLE, init, assign);
+    }
+
+private:
+    explicit DistributedKMeansEngine(size_t g) : g_(g) {}
+    size_t g_;
+};
+
+/* ---- packed-bit Hamming kNN (extension) -------------------------------------------------- */
+class HammingKnnEngine {
+public:
+    HammingKnnEngine(const uint32_t *codes, size_t n, size_t words, size_t ordinal = 0) : words_(words) {
+        vhip_hamming *h = nullptr;
+        detail::check(vhip_hamming_create(codes, n, words, (int)ordinal, &h));
+        h_.reset(h);
+    }
+    /* nq x k ids and exact integer distances, best first; lens[q] = min(k, n) */
+    void search_batch(const uint32_t *queries, size_t nq, size_t k, uint32_t *ids, uint32_t *dist,
+                      size_t *lens) const {
+        detail::check(vhip_hamming_search_batch(h_.get(), queries, nq, k, ids, dist, lens));
+    }
+
+private:
+    struct Del {
+        void operator()(vhip_hamming *p) const { vhip_hamming_destroy(p); }
+    };
+    size_t words_;
+    std::unique_ptr<vhip_hamming, Del> h_;
+};
+
+}  // namespace vector_hip
+
+#endif /* VECTOR_HIP_HPP */

@@ -1,0 +1,365 @@
+// C++ restatement of the reference's own tests of the GPU hot path, run against the C++ host
+// API (include/vector_hip.hpp) over the C ABI.  Each test names the Rust test it restates.
+//
+//   test_facade --host   tests that need no GPU (error semantics, collective merge)
+//   test_facade          all tests (a gfx950 GPU must be visible)
+//
+// Exit status 0 when every test passed; one line per test on stdout.
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <functional>
+#include <string>
+#include <vector>
+
+#include "vector_hip.hpp"
+
+using namespace vector_hip;
+
+static int g_failed = 0;
+#define CHECK(cond)                                                                        \
+    do {                                                                                   \
+        if (!(cond)) throw std::runtime_error(std::string("check failed: ") + #cond);     \
+    } while (0)
+
+static void run(const char *name, const std::function<void()> &f) {
+    try {
+        f();
+        std::printf("PASS %s\n", name);
+    } catch (const std::exception &e) {
+        ++g_failed;
+        std::printf("FAIL %s: %s\n", name, e.what());
+    }
+    std::fflush(stdout);
+}
+
+// exact squared-L2 top-k in double with lowest-id ties (the FlatIndex answer for these data)
+static std::vector<std::pair<uint32_t, double>> brute_l2(const std::vector<float> &data, size_t dim,
+                                                         const float *q, size_t k) {
+    const size_t n = data.size() / dim;
+    std::vector<std::pair<uint32_t, double>> all;
+    for (size_t i = 0; i < n; ++i) {
+        double s = 0;
+        for (size_t d = 0; d < dim; ++d) {
+            const double t = (double)data[i * dim + d] - q[d];
+            s += t * t;
+        }
+        all.push_back({(uint32_t)i, s});
+    }
+    std::stable_sort(all.begin(), all.end(), [](auto &a, auto &b) { return a.second < b.second; });
+    all.resize(std::min(k, n));
+    return all;
+}
+
+static std::vector<float> knn_rs_data(int n) {  // knn.rs:416-425
+    std::vector<float> v;
+    for (int i = 0; i < n; ++i) {
+        v.push_back((float)(i * i) * 0.1f);
+        v.push_back((float)i * 2.0f);
+        v.push_back((float)(i + 5));
+        v.push_back((float)(i * 3));
+    }
+    return v;
+}
+
+template <class F>
+static CudaError expect_error(F f) {
+    try {
+        f();
+    } catch (const CudaError &e) {
+        return e;
+    }
+    throw std::runtime_error("expected a CudaError");
+}
+
+static void host_tests() {
+    run("ddp_knn_insufficient_hardware_error (distributed_knn.rs:470)", [] {
+        const size_t avail = CudaDeviceContext::device_count(), req = avail + 100;
+        auto e = expect_error([&] {
+            DistributedKnnEngine::try_new({1, 2, 3, 4}, 2, req, GpuShardMode::Sharded, DistanceMetric::L2Squared);
+        });
+        CHECK(e.kind() == CudaError::Kind::InsufficientDevices);
+        CHECK(e.requested() == req && e.available() == avail);
+    });
+    run("ddp_kmeans_insufficient_hardware_error (distributed_kmeans.rs:625)", [] {
+        const size_t avail = CudaDeviceContext::device_count(), req = avail + 100;
+        auto e = expect_error([&] { DistributedKMeansEngine::try_new(req); });
+        CHECK(e.kind() == CudaError::Kind::InsufficientDevices && e.requested() == req && e.available() == avail);
+    });
+    run("strict_hardware_validation_error (integration_tests.rs:164)", [] {
+        const size_t avail = CudaDeviceContext::device_count(), req = avail + 10;
+        auto e = expect_error([&] { DistributedKMeansEngine::try_new(req); });
+        CHECK(e.kind() == CudaError::Kind::InsufficientDevices && e.requested() == req && e.available() == avail);
+    });
+    run("ddp_kmeans_getters (distributed_kmeans.rs:619)", [] {
+        CHECK(DistributedKMeansEngine::emulator(6).num_gpus() == 6);
+    });
+    run("num_gpus >= 1 and dimension divisibility are enforced", [] {
+        CHECK(expect_error([] { DistributedKMeansEngine::emulator(0); }).kind() == CudaError::Kind::InvalidConfig);
+        CHECK(expect_error([] {
+                  DistributedKnnEngine::emulator({1, 2, 3}, 2, 1, GpuShardMode::Sharded, DistanceMetric::L2Squared);
+              }).kind() == CudaError::Kind::InvalidConfig);
+    });
+    run("top_k_reduce (collective.rs:239)", [] {
+        auto m = CollectiveOps::top_k_reduce({{{0, 1.0f}, {1, 5.0f}}, {{10, 0.5f}, {11, 4.0f}}}, 2,
+                                             DistanceMetric::L2Squared);
+        CHECK(m.size() == 2 && m[0].id == 10 && m[1].id == 0);
+    });
+    run("top_k_reduce_empty_and_zero_k (collective.rs:250)", [] {
+        CHECK(CollectiveOps::top_k_reduce({}, 5, DistanceMetric::L2Squared).empty());
+        CHECK(CollectiveOps::top_k_reduce({{{0, 1.0f}}}, 0, DistanceMetric::L2Squared).empty());
+    });
+    run("top_k_reduce_cosine_metric (collective.rs:260)", [] {
+        auto m = CollectiveOps::top_k_reduce({{{0, 0.85f}, {1, 0.40f}}, {{2, 0.95f}, {3, 0.70f}}}, 3,
+                                             DistanceMetric::CosineSimilarity);
+        CHECK(m.size() == 3 && m[0].id == 2 && m[1].id == 0 && m[2].id == 3);
+    });
+    run("top_k_reduce_k_greater_than_total_candidates (collective.rs:274)", [] {
+        auto m = CollectiveOps::top_k_reduce({{{0, 2.0f}}, {{1, 1.0f}}}, 10, DistanceMetric::L2Squared);
+        CHECK(m.size() == 2 && m[0].id == 1 && m[1].id == 0);
+    });
+}
+
+static void gpu_tests() {
+    // ---- knn.rs:410-542 ----
+    run("cuda_knn_exact_match_vs_cpu_flat (knn.rs:411)", [] {
+        auto data = knn_rs_data(50);
+        CudaKnnEngine e(data, 4, DistanceMetric::L2Squared);
+        auto gpu = e.search(std::vector<float>(data.begin() + 40, data.begin() + 44), 5);
+        auto cpu = brute_l2(data, 4, data.data() + 40, 5);
+        CHECK(gpu.size() == 5);
+        for (int i = 0; i < 5; ++i) CHECK(gpu[i].id == cpu[i].first && std::fabs(gpu[i].distance - cpu[i].second) < 1e-4);
+    });
+    run("cuda_knn_batch_queries (knn.rs:444)", [] {
+        CudaKnnEngine e({0, 0, 1, 1, 2, 2}, 2, DistanceMetric::L2Squared);
+        auto r = e.search_batch({0.1f, 0.1f, 1.9f, 1.9f}, 1);
+        CHECK(r.size() == 2 && r[0][0].id == 0 && r[1][0].id == 2);
+    });
+    run("cuda_knn_empty_and_zero_k (knn.rs:458)", [] {
+        CudaKnnEngine e({1, 2, 3, 4}, 2, DistanceMetric::L2Squared);
+        CHECK(e.search(std::vector<float>{}, 5).empty() && e.search_batch(std::vector<float>{}, 5).empty());
+        CHECK(e.search({1, 2}, 0).empty());
+        auto b = e.search_batch({1, 2}, 0);
+        CHECK(b.size() == 1 && b[0].empty());
+    });
+    run("cuda_knn_k_greater_than_num_vectors (knn.rs:475)", [] {
+        CudaKnnEngine e({0, 0, 1, 1, 2, 2}, 2, DistanceMetric::L2Squared);
+        CHECK(e.search({0.5f, 0.5f}, 100).size() == 3);
+    });
+    run("cuda_knn_cosine_similarity (knn.rs:485)", [] {
+        CudaKnnEngine e({1, 0, 0, 1, -1, 0}, 2, DistanceMetric::CosineSimilarity);
+        auto r = e.search({0.95f, 0.05f}, 3);
+        CHECK(r.size() == 3 && r[0].id == 0 && r[2].id == 2);
+    });
+    run("cuda_knn_dot_product (knn.rs:502)", [] {
+        CudaKnnEngine e({1, 1, 2, 2, 3, 3}, 2, DistanceMetric::DotProduct);
+        auto r = e.search({2, 3}, 2);
+        CHECK(r.size() == 2 && r[0].id == 2 && r[1].id == 1 && std::fabs(r[0].distance - 15.0f) < 1e-5);
+    });
+    run("cuda_knn_engine_getters (knn.rs:519)", [] {
+        CudaKnnEngine e({1, 2, 3, 4, 5, 6}, 3, DistanceMetric::L2Squared);
+        CHECK(e.dimension() == 3 && e.num_vectors() == 2 && e.metric() == DistanceMetric::L2Squared);
+        CHECK(e.context().device_id() == 0);
+    });
+    run("cuda_knn_exact_self_query (knn.rs:531)", [] {
+        std::vector<float> data{10, 20, 30, 40, 50, 60};
+        CudaKnnEngine e(data, 2, DistanceMetric::L2Squared);
+        for (uint32_t i = 0; i < 3; ++i) {
+            auto r = e.search(std::vector<float>(data.begin() + 2 * i, data.begin() + 2 * i + 2), 1);
+            CHECK(r.size() == 1 && r[0].id == i && std::fabs(r[0].distance) < 1e-4);
+        }
+    });
+    // ---- ddp/distributed_knn.rs:270-467 ----
+    run("ddp_knn_sharded_mode_exact_match (distributed_knn.rs:271)", [] {
+        auto data = knn_rs_data(60);
+        auto e = DistributedKnnEngine::emulator(data, 4, 3, GpuShardMode::Sharded, DistanceMetric::L2Squared);
+        CHECK(e.num_gpus() == 3 && e.num_vectors() == 60);
+        auto r = e.search(std::vector<float>(data.begin() + 100, data.begin() + 104), 5);
+        auto cpu = brute_l2(data, 4, data.data() + 100, 5);
+        CHECK(r.size() == 5);
+        for (int i = 0; i < 5; ++i) CHECK(r[i].id == cpu[i].first && std::fabs(r[i].distance - cpu[i].second) < 1e-4);
+    });
+    run("ddp_knn_replicated_mode (distributed_knn.rs:313)", [] {
+        auto e = DistributedKnnEngine::emulator({0, 0, 1, 1, 2, 2, 3, 3}, 2, 2, GpuShardMode::Replicated,
+                                                DistanceMetric::L2Squared);
+        auto r = e.search_batch({0.1f, 0.1f, 2.9f, 2.9f}, 1);
+        CHECK(r.size() == 2 && r[0][0].id == 0 && r[1][0].id == 3);
+    });
+    run("ddp_knn_empty_and_zero_k (distributed_knn.rs:334)", [] {
+        for (auto mode : {GpuShardMode::Sharded, GpuShardMode::Replicated}) {
+            auto e = DistributedKnnEngine::emulator({1, 2, 3, 4}, 2, 2, mode, DistanceMetric::L2Squared);
+            CHECK(e.search(std::vector<float>{}, 5).empty() && e.search_batch(std::vector<float>{}, 5).empty());
+            CHECK(e.search({1, 2}, 0).empty());
+        }
+    });
+    run("ddp_knn_sharded_global_id_mapping (distributed_knn.rs:364)", [] {
+        auto e = DistributedKnnEngine::emulator({10, 10, 20, 20, 30, 30, 40, 40}, 2, 2, GpuShardMode::Sharded,
+                                                DistanceMetric::L2Squared);
+        CHECK(e.search({39.9f, 40.1f}, 1)[0].id == 3 && e.search({20.1f, 19.9f}, 1)[0].id == 1);
+    });
+    run("ddp_knn_cosine_metric_sharded_and_replicated (distributed_knn.rs:394)", [] {
+        for (auto mode : {GpuShardMode::Sharded, GpuShardMode::Replicated}) {
+            auto e = DistributedKnnEngine::emulator({1, 0, 0, 1, -1, 0, 0, -1}, 2, 2, mode,
+                                                    DistanceMetric::CosineSimilarity);
+            auto r = e.search({0.99f, 0.01f}, 2);
+            CHECK(r.size() == 2 && r[0].id == 0);
+        }
+    });
+    run("ddp_knn_more_gpus_than_vectors (distributed_knn.rs:430)", [] {
+        auto e = DistributedKnnEngine::emulator({1, 1, 2, 2}, 2, 8, GpuShardMode::Sharded, DistanceMetric::L2Squared);
+        CHECK(e.num_gpus() == 2 && e.num_vectors() == 2);
+        auto r = e.search({1, 1}, 2);
+        CHECK(r.size() == 2 && r[0].id == 0);
+    });
+    run("ddp_knn_getters (distributed_knn.rs:451)", [] {
+        auto e = DistributedKnnEngine::emulator({1, 2, 3, 4, 5, 6}, 3, 2, GpuShardMode::Sharded,
+                                                DistanceMetric::L2Squared);
+        CHECK(e.num_gpus() == 2 && e.num_vectors() == 2 && e.dimension() == 3);
+        CHECK(e.mode() == GpuShardMode::Sharded && e.metric() == DistanceMetric::L2Squared);
+    });
+    run("ddp_try_new_single_gpu routes to the GPU", [] {
+        auto data = knn_rs_data(40);
+        auto e = DistributedKnnEngine::try_new(data, 4, 1, GpuShardMode::Sharded, DistanceMetric::L2Squared);
+        CHECK(e.num_gpus() == 1 && e.search(std::vector<float>(data.begin() + 28, data.begin() + 32), 1)[0].id == 7);
+    });
+    // ---- kmeans.rs:473-577 ----
+    run("cuda_kmeans_clustering (kmeans.rs:474)", [] {
+        std::vector<float> data;
+        for (int c = 0; c < 3; ++c)
+            for (int i = 0; i < 50; ++i) {
+                const float b = 10.0f * c;
+                for (float v : {b + 0.1f, b - 0.1f, b + 0.05f, b - 0.05f}) data.push_back(v);
+            }
+        CudaKMeansEngine eng;
+        auto r = eng.fit(data, 4, 3, 20, 1e-4f, DistanceMetric::L2Squared);
+        CHECK(r.k == 3 && r.dimension == 4 && r.iterations > 0 && r.inertia < 1.0f);
+    });
+    run("cuda_kmeans_single_cluster (kmeans.rs:507)", [] {
+        auto r = CudaKMeansEngine().fit({1.0f, 1.0f, 1.1f, 0.9f, 0.9f, 1.1f}, 2, 1, 10, 1e-4f,
+                                        DistanceMetric::L2Squared);
+        CHECK(r.k == 1 && std::fabs(r.centroid(0)[0] - 1.0f) < 0.1f && std::fabs(r.centroid(0)[1] - 1.0f) < 0.1f);
+    });
+    run("cuda_kmeans_empty_and_zero_k (kmeans.rs:520)", [] {
+        CudaKMeansEngine eng;
+        CHECK(eng.fit({}, 4, 3, 10, 1e-4f, DistanceMetric::L2Squared).k == 0);
+        CHECK(eng.fit({1, 2}, 2, 0, 10, 1e-4f, DistanceMetric::L2Squared).k == 0);
+    });
+    run("cuda_kmeans_k_greater_than_n (kmeans.rs:530)", [] {
+        CHECK(CudaKMeansEngine().fit({1, 2, 3, 4}, 2, 5, 10, 1e-4f, DistanceMetric::L2Squared).k == 2);
+    });
+    run("cuda_kmeans_cosine_and_dot_product_metrics (kmeans.rs:540)", [] {
+        std::vector<float> data{1, 0, 0, 0, 1, 0, 0, 0, 1, 0.9f, 0.1f, 0};
+        CudaKMeansEngine eng;
+        CHECK(eng.fit(data, 3, 3, 10, 1e-4f, DistanceMetric::CosineSimilarity).k == 3);
+        CHECK(eng.fit(data, 3, 3, 10, 1e-4f, DistanceMetric::DotProduct).k == 3);
+    });
+    run("cuda_kmeans_high_dimension (kmeans.rs:560)", [] {
+        std::vector<float> data(20 * 128);
+        for (size_t i = 0; i < data.size(); ++i) data[i] = (float)i * 0.01f;
+        auto r = CudaKMeansEngine().fit(data, 128, 4, 5, 1e-3f, DistanceMetric::L2Squared);
+        CHECK(r.k == 4 && r.dimension == 128);
+    });
+    run("cuda_kmeans_engine_context (kmeans.rs:573)", [] {
+        CudaKMeansEngine eng;
+        CHECK(eng.context().device_id() == 0 && eng.context().total_memory_bytes() > 0);
+    });
+    // ---- ddp/distributed_kmeans.rs:548-618 ----
+    run("ddp_kmeans_multi_gpu (distributed_kmeans.rs:549)", [] {
+        auto r = DistributedKMeansEngine::emulator(4).fit({0, 0, 0.1f, 0.1f, -0.1f, -0.1f, 10, 10, 10.1f, 10.1f,
+                                                           9.9f, 9.9f},
+                                                          2, 2, 25, 1e-5f, DistanceMetric::L2Squared);
+        CHECK(r.k == 2 && r.dimension == 2 && r.iterations > 0 && r.inertia >= 0.0f);
+        const float *c0 = r.centroid(0), *c1 = r.centroid(1);
+        const float *n0 = c0[0] < 5.0f ? c0 : c1, *n10 = c0[0] < 5.0f ? c1 : c0;
+        CHECK(std::fabs(n0[0]) < 0.5f && std::fabs(n0[1]) < 0.5f);
+        CHECK(std::fabs(n10[0] - 10.0f) < 0.5f && std::fabs(n10[1] - 10.0f) < 0.5f);
+    });
+    run("ddp_kmeans_empty_and_zero_k (distributed_kmeans.rs:572)", [] {
+        auto e = DistributedKMeansEngine::emulator(4);
+        auto a = e.fit({}, 2, 2, 10, 1e-4f, DistanceMetric::L2Squared);
+        CHECK(a.k == 0 && a.centroids.empty() && a.iterations == 0);
+        auto b = e.fit({1, 2, 3, 4}, 2, 0, 10, 1e-4f, DistanceMetric::L2Squared);
+        CHECK(b.k == 0 && b.centroids.empty());
+    });
+    run("ddp_kmeans_more_gpus_than_vectors (distributed_kmeans.rs:587)", [] {
+        auto r = DistributedKMeansEngine::emulator(8).fit({1, 1, 2, 2, 3, 3}, 2, 2, 15, 1e-4f,
+                                                          DistanceMetric::L2Squared);
+        CHECK(r.k == 2 && r.centroids.size() == 4);
+    });
+    run("ddp_kmeans_single_cluster (distributed_kmeans.rs:597)", [] {
+        auto r = DistributedKMeansEngine::emulator(2).fit({1, 1, 3, 3, 5, 5, 7, 7}, 2, 1, 10, 1e-5f,
+                                                          DistanceMetric::L2Squared);
+        CHECK(r.k == 1 && std::fabs(r.centroid(0)[0] - 4.0f) < 1e-3f && std::fabs(r.centroid(0)[1] - 4.0f) < 1e-3f);
+    });
+    run("ddp_kmeans_cosine_metric (distributed_kmeans.rs:609)", [] {
+        auto r = DistributedKMeansEngine::emulator(2).fit({1, 0, 0.98f, 0.2f, 0, 1, 0.2f, 0.98f}, 2, 2, 20, 1e-4f,
+                                                          DistanceMetric::CosineSimilarity);
+        CHECK(r.k == 2 && r.dimension == 2);
+    });
+    // ---- tests/integration_tests.rs ----
+    run("end_to_end_clustering_and_sharded_search (integration_tests.rs:8)", [] {
+        std::vector<float> data;
+        const float cl[3][4] = {{0.1f, 0.0f, -0.1f, 0.05f}, {9.9f, 10.1f, 10.0f, 9.95f}, {20.0f, 19.9f, 20.1f, 20.05f}};
+        for (int c = 0; c < 3; ++c)
+            for (int i = 0; i < 30; ++i) data.insert(data.end(), cl[c], cl[c] + 4);
+        auto km = DistributedKMeansEngine::emulator(4).fit(data, 4, 3, 30, 1e-5f, DistanceMetric::L2Squared);
+        CHECK(km.k == 3 && km.dimension == 4);
+        auto knn = DistributedKnnEngine::emulator(data, 4, 3, GpuShardMode::Sharded, DistanceMetric::L2Squared);
+        CHECK(knn.num_vectors() == 90);
+        auto r = knn.search({10, 10, 10, 10}, 5);
+        CHECK(r.size() == 5);
+        for (auto &x : r) CHECK(x.id >= 30 && x.id < 60 && x.distance < 1.0f);
+    });
+    run("single_gpu_vs_multi_gpu_consistency (integration_tests.rs:59)", [] {
+        std::vector<float> data;
+        for (int i = 0; i < 60; ++i) {
+            data.push_back((float)i * 0.5f);
+            data.push_back((float)(i * i) * 0.05f);
+            data.push_back(std::sin((float)i + 3.0f));
+        }
+        std::vector<float> q{1.0f, 2.0f, 0.5f, 15.0f, 45.0f, -0.5f, 25.0f, 120.0f, 0.8f};
+        auto single = CudaKnnEngine(data, 3, DistanceMetric::L2Squared).search_batch(q, 5);
+        for (auto mode : {GpuShardMode::Sharded, GpuShardMode::Replicated}) {
+            auto other = DistributedKnnEngine::emulator(data, 3, 4, mode, DistanceMetric::L2Squared).search_batch(q, 5);
+            CHECK(single.size() == 3 && other.size() == 3);
+            for (int a = 0; a < 3; ++a)
+                for (int b = 0; b < 5; ++b)
+                    CHECK(other[a][b].id == single[a][b].id &&
+                          std::fabs(other[a][b].distance - single[a][b].distance) < 1e-4f);
+        }
+    });
+    run("all_metrics_consistency (integration_tests.rs:122)", [] {
+        std::vector<float> data{0.8f, 0.6f, 0.8f, 0.0f, 0.0f, 0.6f, 0.1f, 0.1f, -1.0f, -1.0f};
+        for (int m = 0; m < 10; ++m) {
+            const auto metric = (DistanceMetric)m;
+            auto s = CudaKnnEngine(data, 2, metric).search({0.8f, 0.6f}, 3);
+            auto d = DistributedKnnEngine::emulator(data, 2, 2, GpuShardMode::Sharded, metric).search({0.8f, 0.6f}, 3);
+            CHECK(s.size() == 3 && d.size() == 3);
+            for (int i = 0; i < 3; ++i) CHECK(std::fabs(s[i].distance - d[i].distance) < 1e-4f);
+        }
+    });
+    run("explicit-init k-means is deterministic (extension)", [] {
+        std::vector<float> data;
+        for (int i = 0; i < 4000; ++i) data.push_back(std::sin(0.37f * i) * 3.0f + (i % 7));
+        std::vector<float> init(data.begin(), data.begin() + 8 * 4);
+        KMeansInit ini;
+        ini.centroids = init.data();
+        auto a = CudaKMeansEngine().fit(data, 4, 8, 6, -1.0f, DistanceMetric::L2Squared, ini);
+        auto b = CudaKMeansEngine().fit(data, 4, 8, 6, -1.0f, DistanceMetric::L2Squared, ini);
+        CHECK(a.iterations == 6 && a.centroids == b.centroids);
+    });
+}
+
+int main(int argc, char **argv) {
+    const bool host_only = argc > 1 && std::strcmp(argv[1], "--host") == 0;
+    host_tests();
+    if (!host_only) {
+        if (CudaDeviceContext::device_count() < 1) {
+            std::printf("FAIL no gfx950 GPU visible\n");
+            return 1;
+        }
+        gpu_tests();
+    }
+    std::printf("%s: %d failed\n", host_only ? "host tests" : "all tests", g_failed);
+    return g_failed ? 1 : 0;
+}
