@@ -55,7 +55,35 @@ def cpu_model() -> str:
     return platform.processor()
 
 
-def roofline(prof, bound, peak, unit):
+# rocprofv3 counter summaries (FETCH_SIZE + WRITE_SIZE of the dominant kernel, scaled by a 1 GiB
+# copy) per workload; each holds a "traffic_bytes_per_launch:" line.
+PROFILES = {
+    "l2int": "k_mfma_res_filter__knn_l2_int_1000000x128_q10000_k100.txt",
+    "kmeans": "k_mfma_res_assign__kmeans_l2_2000000x96_k4096.txt",
+    "cos768": "k_mfma_stream_filter__knn_cosine_1000000x768_q10000_k10.txt",
+    "hamming": "k_hamming_filter__knn_hamming_packed256_10000000_q10000_k10.txt",
+    "l1": "k_valu_filter__knn_l1_uniform_500000x128_q4096_k10.txt",
+    "linf": "k_valu_filter__knn_linf_uniform_500000x128_q4096_k10.txt",
+}
+
+
+def profiled_traffic(key):
+    """HBM bytes per launch of the workload's dominant kernel from its committed counter summary
+    (None when there is no summary)."""
+    name = PROFILES.get(key)
+    if not name:
+        return None
+    try:
+        with open(os.path.join(ROOT, "profiles", name)) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(float(line.split(":", 1)[1]))
+    except OSError:
+        pass
+    return None
+
+
+def roofline(prof, bound, peak, unit, key=None):
     if not prof["launches"] or prof["kernel_ms"] <= 0:
         return None
     avg_s = prof["kernel_ms"] / prof["launches"] / 1e3
@@ -63,7 +91,8 @@ def roofline(prof, bound, peak, unit):
     achieved = per_launch / avg_s
     scale = 1e12 if unit == "TFLOP/s" else 1e9
     return {"bound": bound, "achieved": round(achieved / scale, 3), "peak": round(peak / scale, 3), "unit": unit,
-            "frac": round(achieved / peak, 4), "traffic": None,
+            "frac": round(achieved / peak, 4), "traffic": profiled_traffic(key),
+            "traffic_source": f"profiles/{PROFILES[key]}" if key in PROFILES else None,
             "work_per_launch": per_launch, "avg_launch_ms": round(avg_s * 1e3, 4), "launches": prof["launches"],
             "algorithmic_bytes_per_launch": prof["bytes"] / prof["launches"]}
 
@@ -100,13 +129,22 @@ def run_knn(vh, base, queries, k, metric, steps, warmup, hamming=False):
     return (t1 - t0) * 1e3 / steps, prof, ids, dist, host_ms
 
 
-def cpu_knn_baseline(base, queries, k, metric, sample):
+CPU_TARGET_S = 10.0  # wall time the CPU baseline leg aims for (bounded sample of the workload)
+
+
+def cpu_knn_baseline(base, queries, k, metric, max_sample=None):
+    """Times the oracle's restatement of search_batch_cpu on a query sample sized (from a 16-query
+    probe) to take about CPU_TARGET_S seconds on this host's threads."""
     import oracle
 
-    qs = queries[:sample]
     th = cpu_threads()
+    cap = min(queries.shape[0], max_sample or queries.shape[0])
     t0 = time.perf_counter()
-    oracle.knn_search_batch(base, qs, k, metric, threads=th)
+    oracle.knn_search_batch(base, queries[:16], k, metric, threads=th)
+    probe = time.perf_counter() - t0
+    sample = int(max(16, min(cap, 16 * CPU_TARGET_S / max(probe, 1e-6))))
+    t0 = time.perf_counter()
+    oracle.knn_search_batch(base, queries[:sample], k, metric, threads=th)
     dt = time.perf_counter() - t0
     be = {0: "scalar", 1: "AVX2+FMA", 2: "AVX-512F"}[oracle.detect_backend()]
     return {"value": round(sample / dt, 3), "unit": "queries/s", "cores": th, "kind": "port",
@@ -137,19 +175,24 @@ def bench_kmeans(vh, steps_iters, with_cpu):
     res = {"workload": f"kmeans_l2_{n}x{d}_k{kc}_{steps_iters}iters_init_first_points",
            "value": round(1e3 / ms_iter, 3), "unit": "iterations/s", "ms_per_iteration": round(ms_iter, 3),
            "inertia": out["inertia"],
-           "roofline": roofline(prof, "mfma", PEAK_MFMA_F32, "TFLOP/s")}
+           "roofline": roofline(prof, "mfma", PEAK_MFMA_F32, "TFLOP/s", "kmeans")}
     if with_cpu:
         import oracle
 
-        sp = 65_536
+        # whole Lloyd iterations (KMeans::fit body) over all points from the same initial
+        # centroids, repeated until about CPU_TARGET_S seconds have passed
         th = cpu_threads()
+        its = 0
         t0 = time.perf_counter()
-        oracle.kmeans_step(data[:sp], init, "l2", threads=th)
-        dt = (time.perf_counter() - t0) * (n / sp)
+        while True:
+            oracle.kmeans_step(data, init, "l2", threads=th)
+            its += 1
+            if time.perf_counter() - t0 >= CPU_TARGET_S or its >= 10:
+                break
+        dt = (time.perf_counter() - t0) / its
         res["cpu_baseline"] = {"value": round(1.0 / dt, 5), "unit": "iterations/s", "cores": th, "kind": "port",
-                               "sample": f"one Lloyd iteration (KMeans::fit body) on {sp} of the {n} points "
-                                         f"against all {kc} centroids, scaled x{n / sp:g}; {th} threads "
-                                         f"({cpu_model()})"}
+                               "sample": f"{its} full Lloyd iteration(s) (KMeans::fit body) over all {n} points "
+                                         f"and {kc} centroids, {dt:.2f} s each on {th} threads ({cpu_model()})"}
         res["speedup_vs_cpu"] = round(res["value"] / res["cpu_baseline"]["value"], 1)
     return res
 
@@ -205,12 +248,12 @@ def bench_knn_workload(vh, key, steps, warmup, with_cpu):
     ms, prof, ids, dist, host_ms = run_knn(vh, base, q, w["k"], metric, steps, warmup, hamming=ham)
     gemm = w["metric"] in ("l2", "dot", "cosine")
     if gemm:
-        rl = roofline(prof, "mfma", PEAK_MFMA_F32, "TFLOP/s")
+        rl = roofline(prof, "mfma", PEAK_MFMA_F32, "TFLOP/s", key)
     else:
         # VALU-bound: work counts element (or word) operations, each costing two VALU ops
         p2 = dict(prof)
         p2["work"] = prof["work"] * 2.0
-        rl = roofline(p2, "valu", PEAK_VALU32, "TFLOP/s")
+        rl = roofline(p2, "valu", PEAK_VALU32, "TFLOP/s", key)
         if rl:
             rl["unit"] = "Top/s (32-bit VALU)"
     out = {"metric": METRIC, "value": round(w["nq"] * 1e3 / ms, 2), "unit": "queries/s", "n_gpus": 1,
@@ -228,15 +271,14 @@ def bench_knn_workload(vh, key, steps, warmup, with_cpu):
 
             sub = 500_000
             un_b = oracle.unpack_bits(base[:sub])
-            un_q = oracle.unpack_bits(q[:64])
-            cb = cpu_knn_baseline(un_b, un_q, w["k"], "hamming", 64)
+            un_q = oracle.unpack_bits(q)
+            cb = cpu_knn_baseline(un_b, un_q, w["k"], "hamming")
             cb["value"] = round(cb["value"] * sub / w["n"], 4)
-            cb["sample"] = (f"reference semantics (thresholded float Hamming over codes unpacked to 0/1 floats): 64 "
-                            f"queries against {sub} of the {w['n']} codes, scaled by {sub}/{w['n']}; " + cb["sample"])
+            cb["sample"] = (f"reference semantics (thresholded float Hamming over codes unpacked to 0/1 floats) "
+                            f"against {sub} of the {w['n']} codes, rate scaled by {sub}/{w['n']}; " + cb["sample"])
             out["cpu_baseline"] = cb
         else:
-            sample = 256 if w["n"] * w["d"] <= 200_000_000 else 64
-            out["cpu_baseline"] = cpu_knn_baseline(base, q, w["k"], w["metric"], min(sample, w["nq"]))
+            out["cpu_baseline"] = cpu_knn_baseline(base, q, w["k"], w["metric"])
     return out
 
 
