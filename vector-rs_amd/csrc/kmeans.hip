@@ -7,14 +7,19 @@
 //                  atomic ticket pos[p] in its cluster's count (integer atomics: exact);
 //   2. scan     -- exclusive scan of the k counts into segment offsets;
 //   3. scatter  -- point indices into their cluster segment at offsets[c] + pos[p];
-//   4. update   -- one workgroup per cluster sums its segment in 64-bit fixed point.  Integer
-//                  addition is associative, so the sums -- and every centroid -- are bit-identical
-//                  whatever order the atomics handed out the slots (the reference's float atomics,
-//                  kmeans.cu:298-320, and rayon fold, ivf/kmeans.rs:75-118, are order-dependent).
-//                  The fixed-point scale 2^E is chosen from max|x| and n so no sum can overflow
-//                  and the resolution (2^-E) is far below f32 rounding of the mean.
-//                  new = sum / count; shift = sum_d (new - old)^2; an empty cluster keeps its
-//                  centroid with shift 0 (kmeans.cu:350-356).
+//   4. sums     -- every wave walks a fixed 256-slot window of the cluster-sorted order, adds its
+//                  rows in 64-bit fixed point and, at each cluster boundary, adds the partial sum
+//                  into the cluster's 64-bit accumulators with integer atomics.  Integer addition
+//                  is associative, so the sums -- and every centroid -- are bit-identical whatever
+//                  order the atomics handed out the slots or the windows were scheduled (the
+//                  reference's float atomics, kmeans.cu:298-320, and rayon fold,
+//                  ivf/kmeans.rs:75-118, are order-dependent).  Windows of equal size keep large
+//                  and small clusters balanced across the GPU.  The fixed-point scale 2^E is chosen
+//                  from max|x| and n so no sum can overflow and the resolution (2^-E) is far below
+//                  f32 rounding of the mean;
+//   5. finalize -- one wave per cluster: new = sum / count; shift = sum_d (new - old)^2; an empty
+//                  cluster keeps its centroid with shift 0 (kmeans.cu:350-356); the accumulators
+//                  are cleared for the next iteration.
 // With tol < 0 no per-iteration host synchronisation happens.
 #include <algorithm>
 #include <cmath>
@@ -72,62 +77,124 @@ __global__ void k_scatter(const int32_t *__restrict__ assign, const int32_t *__r
     if (p < n) sorted[offsets[assign[p]] + pos[p]] = p;
 }
 
-// S = number of 64-dimension slots per lane (dpad <= 64 * S).
-template <int S>
-__global__ __launch_bounds__(256) void k_update(const float *__restrict__ pts, int dpad, int dim,
-                                                const int32_t *__restrict__ sorted,
-                                                const int32_t *__restrict__ offsets,
-                                                const int32_t *__restrict__ counts, float *__restrict__ cent,
-                                                float *__restrict__ cnorm, int norm_kind, float *__restrict__ shifts,
-                                                double scale, double inv_scale) {
-    __shared__ long long red[4][64 * S];
-    __shared__ float rs[256], rn[256];
-    const int c = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int cnt = counts[c];
-    if (cnt == 0) {
-        if (tid == 0) shifts[c] = 0.0f;
-        return;
+// ---- update ----------------------------------------------------------------------------
+constexpr int kUpdSlotsPerWave = 256;  // sorted slots per wave window
+
+// Largest c in [0, k) with offsets[c] <= i: the (non-empty) cluster whose segment holds slot i.
+__device__ __forceinline__ int segment_of(const int32_t *__restrict__ offsets, int k, int i) {
+    int lo = 0, hi = k - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (offsets[mid] <= i) lo = mid;
+        else hi = mid - 1;
     }
-    const int off = offsets[c];
+    return lo;
+}
+
+// S = number of 64-dimension slots per lane (dpad <= 64 * S).  Lane l of a wave owns dimensions
+// l, l + 64, ...; the wave adds the rows of its window slot by slot in fixed point and flushes the
+// running sum into sums[c] whenever the window crosses into the next cluster's segment.
+template <int S>
+constexpr int upd_unroll() { return S >= 8 ? 4 : (S >= 4 ? 8 : 16); }  // rows in flight per wave
+
+template <int S>
+__global__ __launch_bounds__(256) void k_update_sums(const float *__restrict__ pts, int dpad, int dim, int n, int k,
+                                                     const int32_t *__restrict__ sorted,
+                                                     const int32_t *__restrict__ offsets,
+                                                     unsigned long long *__restrict__ sums, double scale) {
+    constexpr int kUpdUnroll = upd_unroll<S>();
+    const int lane = threadIdx.x & 63;
+    const int wave = (int)((blockIdx.x * (size_t)blockDim.x + threadIdx.x) >> 6);
+    const int s0 = wave * kUpdSlotsPerWave;
+    if (s0 >= n) return;
+    const int s1 = min(n, s0 + kUpdSlotsPerWave);
+    int c = segment_of(offsets, k, s0);
+    int next = offsets[c + 1];
     long long acc[S];
 #pragma unroll
     for (int s = 0; s < S; ++s) acc[s] = 0;
-    for (int i = wave; i < cnt; i += 4) {
-        const float *row = pts + (size_t)sorted[off + i] * dpad;
+    auto flush = [&](int cc) {
 #pragma unroll
         for (int s = 0; s < S; ++s) {
             const int d = lane + 64 * s;
-            if (d < dpad) acc[s] += llrint((double)row[d] * scale);
+            if (d < dim && acc[s] != 0)
+                atomicAdd(sums + (size_t)cc * dpad + d, (unsigned long long)acc[s]);
+            acc[s] = 0;
+        }
+    };
+    for (int b = s0; b < s1; b += 64) {
+        const int nb = min(64, s1 - b);
+        const int mine = lane < nb ? sorted[b + lane] : 0;
+        for (int j = 0; j < nb; j += kUpdUnroll) {
+            float v[kUpdUnroll][S];
+#pragma unroll
+            for (int u = 0; u < kUpdUnroll; ++u) {
+                const int p = __builtin_amdgcn_readlane(mine, j + u);
+                const bool live = j + u < nb;
+#pragma unroll
+                for (int s = 0; s < S; ++s) {
+                    const int d = lane + 64 * s;
+                    v[u][s] = (live && d < dpad) ? pts[(size_t)p * dpad + d] : 0.0f;
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < kUpdUnroll; ++u) {
+                const int i = b + j + u;
+                if (i >= s1) break;
+                while (i >= next) {  // offsets[k] = n > i, so c stays below k
+                    flush(c);
+                    ++c;
+                    next = offsets[c + 1];
+                }
+#pragma unroll
+                for (int s = 0; s < S; ++s) acc[s] += llrint((double)v[u][s] * scale);
+            }
+        }
+    }
+    flush(c);
+}
+
+// One wave per cluster: new = sum / count, shift, norm (lane-strided sum + fixed xor butterfly,
+// the order of k_rows_prep), and the accumulators are cleared for the next iteration.
+template <int S>
+__global__ __launch_bounds__(256) void k_update_finalize(int k, int dpad, int dim, unsigned long long *__restrict__ sums,
+                                                         const int32_t *__restrict__ counts, float *__restrict__ cent,
+                                                         float *__restrict__ cnorm, int norm_kind,
+                                                         float *__restrict__ shifts, double inv_scale) {
+    const int lane = threadIdx.x & 63;
+    const int c = (int)((blockIdx.x * (size_t)blockDim.x + threadIdx.x) >> 6);
+    if (c >= k) return;
+    const int cnt = counts[c];
+    const double inv_cnt = cnt > 0 ? 1.0 / (double)cnt : 0.0;
+    float sh = 0.0f, nn = 0.0f;
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+        const int d = lane + 64 * s;
+        if (d < dim) {
+            unsigned long long *sp = sums + (size_t)c * dpad + d;
+            const long long sum = (long long)*sp;
+            *sp = 0ull;
+            if (cnt > 0) {
+                float *cp = cent + (size_t)c * dpad + d;
+                const float nv = (float)((double)sum * inv_scale * inv_cnt);
+                const float diff = nv - *cp;
+                sh = fmaf(diff, diff, sh);
+                nn = fmaf(nv, nv, nn);
+                *cp = nv;
+            }
         }
     }
 #pragma unroll
-    for (int s = 0; s < S; ++s) red[wave][lane + 64 * s] = acc[s];
-    __syncthreads();
-    float sh = 0.0f, nn = 0.0f;
-    const double inv_cnt = 1.0 / (double)cnt;
-    for (int d = tid; d < dim; d += 256) {
-        const long long sum = red[0][d] + red[1][d] + red[2][d] + red[3][d];
-        const float nv = (float)((double)sum * inv_scale * inv_cnt);
-        float *cp = cent + (size_t)c * dpad + d;
-        const float diff = nv - *cp;
-        sh = fmaf(diff, diff, sh);
-        nn = fmaf(nv, nv, nn);
-        *cp = nv;
+    for (int o = 32; o > 0; o >>= 1) {
+        sh += __shfl_xor(sh, o, 64);
+        nn += __shfl_xor(nn, o, 64);
     }
-    rs[tid] = sh;
-    rn[tid] = nn;
-    __syncthreads();
-    for (int o = 128; o > 0; o >>= 1) {
-        if (tid < o) {
-            rs[tid] += rs[tid + o];
-            rn[tid] += rn[tid + o];
+    if (lane == 0) {
+        shifts[c] = cnt > 0 ? sh : 0.0f;
+        if (cnt > 0) {
+            if (norm_kind == 1) cnorm[c] = nn;
+            else if (norm_kind == 2) cnorm[c] = sqrtf(nn);
         }
-        __syncthreads();
-    }
-    if (tid == 0) {
-        shifts[c] = rs[0];
-        if (norm_kind == 1) cnorm[c] = rn[0];
-        else if (norm_kind == 2) cnorm[c] = sqrtf(rn[0]);
     }
 }
 
@@ -195,7 +262,7 @@ struct vhip_kmeans {
     double scale = 1.0, inv_scale = 1.0;
     bool assigned = false;
     hipStream_t stream = nullptr;
-    vh::DevBuf pts, pnorm, cent, cnorm, assign, pos, inertia, counts, offsets, sorted, shifts, partial;
+    vh::DevBuf pts, pnorm, cent, cnorm, assign, pos, inertia, counts, offsets, sorted, shifts, partial, sums;
     vh::PinnedStager stager;
     vh::KernelTimer timer;
     std::mutex mu;
@@ -276,6 +343,8 @@ static int km_set_centroids_dev(vhip_kmeans *K, const float *d_c, size_t k, size
     VH_CHECK(K->counts.ensure(K->dev, k * sizeof(int32_t)));
     VH_CHECK(K->offsets.ensure(K->dev, (k + 1) * sizeof(int32_t)));
     VH_CHECK(K->shifts.ensure(K->dev, k * sizeof(float)));
+    VH_CHECK(K->sums.ensure(K->dev, k * K->dpad * sizeof(unsigned long long)));
+    launch_fill_u32(K->sums.as<uint32_t>(), 2 * k * K->dpad, 0u, K->stream);
     if (row_stride == K->dim) {
         launch_rows_prep(d_c, k, kpad, (int)K->dim, (int)K->dpad, nullptr, K->cent.as<float>(),
                          K->cnorm.as<float>(), km_norm_kind(K->metric), 0, 0, __builtin_nanf(""), K->stream);
@@ -299,7 +368,7 @@ static int km_set_centroids_dev(vhip_kmeans *K, const float *d_c, size_t k, size
 static int km_iterate(vhip_kmeans *K) {
     hipStream_t s = K->stream;
     const int n = (int)K->n, k = (int)K->k;
-    VH_HIP(hipMemsetAsync(K->counts.p, 0, k * sizeof(int32_t), s));
+    launch_fill_u32(K->counts.as<uint32_t>(), k, 0u, s);
     const int t = K->timer.begin(s);
     if (is_gemm_metric(K->metric))
         launch_kmeans_assign(K->metric, K->cent.as<float>(), K->cnorm.as<float>(), (int)K->kpad, K->pts.as<float>(),
@@ -318,10 +387,17 @@ static int km_iterate(vhip_kmeans *K) {
                        K->pos.as<int32_t>(), K->offsets.as<int32_t>(), n, K->sorted.as<int32_t>());
     const int slots = ceil_div((long)K->dpad, 64);
     const int nk = km_norm_kind(K->metric);
-#define VH_UPD(S)                                                                                                 \
-    hipLaunchKernelGGL(k_update<S>, dim3(k), dim3(256), 0, s, K->pts.as<float>(), (int)K->dpad, (int)K->dim,      \
-                       K->sorted.as<int32_t>(), K->offsets.as<int32_t>(), K->counts.as<int32_t>(), K->cent.as<float>(), \
-                       K->cnorm.as<float>(), nk, K->shifts.as<float>(), K->scale, K->inv_scale)
+    const int waves = ceil_div(n, kUpdSlotsPerWave);
+    unsigned long long *sums = K->sums.as<unsigned long long>();
+#define VH_UPD(S)                                                                                                  \
+    do {                                                                                                           \
+        hipLaunchKernelGGL(k_update_sums<S>, dim3(ceil_div(waves, 4)), dim3(256), 0, s, K->pts.as<float>(),       \
+                           (int)K->dpad, (int)K->dim, n, k, K->sorted.as<int32_t>(), K->offsets.as<int32_t>(),      \
+                           sums, K->scale);                                                                         \
+        hipLaunchKernelGGL(k_update_finalize<S>, dim3(ceil_div(k, 4)), dim3(256), 0, s, k, (int)K->dpad,          \
+                           (int)K->dim, sums, K->counts.as<int32_t>(), K->cent.as<float>(), K->cnorm.as<float>(), nk, \
+                           K->shifts.as<float>(), K->inv_scale);                                                    \
+    } while (0)
     if (slots <= 1) VH_UPD(1);
     else if (slots <= 2) VH_UPD(2);
     else if (slots <= 4) VH_UPD(4);

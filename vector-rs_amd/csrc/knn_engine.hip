@@ -84,7 +84,7 @@ static int run_rounds(vhip_knn *E, const float *qpad, const float *qnorm, int nq
     VH_CHECK(flags.ensure(E->dev, (size_t)nq * sizeof(uint32_t)));
     VH_CHECK(nflag.ensure(E->dev, sizeof(uint32_t)));
     launch_topk_init(nq, tau.as<float>(), have.as<uint32_t>(), cnt.as<uint32_t>(), flags.as<uint32_t>(), s);
-    VH_HIP(hipMemsetAsync(nflag.p, 0, sizeof(uint32_t), s));
+    launch_fill_u32(nflag.as<uint32_t>(), 1, 0u, s);
     const bool gemm = is_gemm_metric(E->metric);
     // The round plan depends on (n, k) only; `cap` is the storage per query and round.
     for (auto [rb, re] : plan_rounds(E->n, (size_t)k, kCap)) {
@@ -254,7 +254,8 @@ static int engine_search_device(vhip_knn *E, const void *d_queries, size_t nq, s
     const size_t ek = std::min(k, E->n);
     if (nq == 0 || k == 0) return VHIP_OK;
     if (ek == 0) {
-        VH_HIP(hipMemsetAsync(d_ids, 0xff, nq * k * sizeof(uint32_t), E->stream));
+        launch_fill_u32(d_ids, nq * k, 0xffffffffu, E->stream);
+        VH_HIP(hipGetLastError());
         VH_HIP(hipStreamSynchronize(E->stream));
         return VHIP_OK;
     }

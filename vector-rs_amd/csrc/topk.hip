@@ -33,6 +33,18 @@ void launch_fill(float *p, size_t count, float v, hipStream_t s) {
     hipLaunchKernelGGL(k_fill_f32, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, s, p, count, v);
 }
 
+__global__ void k_fill_u32(uint32_t *p, size_t count, uint32_t v) {
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < count; i += (size_t)gridDim.x * blockDim.x)
+        p[i] = v;
+}
+
+void launch_fill_u32(uint32_t *p, size_t count, uint32_t v, hipStream_t s) {
+    if (count == 0) return;
+    size_t blocks = (count + 255) / 256;
+    if (blocks > 16384) blocks = 16384;
+    hipLaunchKernelGGL(k_fill_u32, dim3((unsigned)blocks), dim3(256), 0, s, p, count, v);
+}
+
 void launch_topk_init(int nq, float *tau, uint32_t *have, uint32_t *cnt, uint32_t *flags, hipStream_t s) {
     if (nq <= 0) return;
     hipLaunchKernelGGL(k_topk_init, dim3(ceil_div(nq, 256)), dim3(256), 0, s, nq, tau, have, cnt, flags);

@@ -94,7 +94,9 @@ void launch_kmeans_assign_valu(int metric, const float *cent, int k, const float
 void launch_valu_filter(int metric, const float *base, const float *qry, const float *tau, int nq, int dim, int dpad,
                         long row_begin, long row_end, uint2 *cand, uint32_t *cnt, int cap, int grid_cap,
                         hipStream_t s);
-// Fills count floats with v (a kernel, so it is safe inside captured graphs).
+// Fills count floats (32-bit words) with v.  Kernels rather than hipMemsetAsync, so a caller may
+// capture the engines' work in a HIP graph.
 void launch_fill(float *p, size_t count, float v, hipStream_t s);
+void launch_fill_u32(uint32_t *p, size_t count, uint32_t v, hipStream_t s);
 
 }  // namespace vh
