@@ -54,25 +54,48 @@ struct vhip_knn {
 
 namespace vh {
 
-// Row ranges of the search rounds: every boundary but the last is a multiple of the
-// 256-row MFMA stage, and each round is about g times the rows already seen, so a round's
-// expected candidate count per query is about k * g.
-static std::vector<std::pair<long, long>> plan_rounds(size_t n, size_t k, int cap) {
-    std::vector<std::pair<long, long>> r;
+// Search rounds.  Round 0 scores rows [0, b0) with b0 about 20 k, the first 256-row multiple
+// at or above it: for the GEMM metrics densely (every score written, no atomics), for the others
+// through the filter with tau = +inf.  Every later round covers about 8 times the rows seen so
+// far and keeps only rows scoring <= tau, the k-th best so far.  Because the base rows are in a
+// pseudo-random order, round i passes about k * (rows_i / seen_i) ~ 7 k candidates per query at a
+// rate p_i = k / seen_i per scored pair.  item_rows of the MFMA filter is sized so that a work
+// item's expected passes per query, item_rows * p_i, stay at most a third of the LDS slots.
+struct Round {
+    long rb, re;
+    bool dense;
+    long item_rows;
+};
+
+static std::vector<Round> plan_rounds(size_t n, size_t k, bool gemm, int dpad) {
+    std::vector<Round> r;
     if (n == 0) return r;
-    size_t b = std::min(n, round_up(std::max<size_t>(256, 2 * k), kRowAlign));
-    size_t g = 1 + (size_t)cap / (8 * std::max<size_t>(k, 1));
-    g = std::min<size_t>(32, std::max<size_t>(4, g));
-    r.emplace_back(0, (long)b);
-    while (b < n) {
-        const size_t e = std::min(n, round_up(b * g, kRowAlign));
-        r.emplace_back((long)b, (long)e);
-        b = e;
+    const size_t kk = std::max<size_t>(k, 1);
+    const size_t b0 = std::min(n, round_up(std::max<size_t>(256, 20 * kk), kRowAlign));
+    r.push_back({0, (long)b0, gemm, (long)kRowAlign});
+    const int slots = dpad <= 128 ? kGemmSlotsReg : kGemmSlotsStream;
+    size_t seen = b0;
+    while (seen < n) {
+        const size_t e = std::min(n, round_up(seen * 8, kRowAlign));
+        size_t item = (size_t)slots * seen / (3 * kk);
+        item = std::max<size_t>(kRowAlign, std::min<size_t>(4096, item / kRowAlign * kRowAlign));
+        r.push_back({(long)seen, (long)e, false, (long)item});
+        seen = e;
     }
     return r;
 }
 
-// Runs all rounds for nq prepared queries; results stay in ws.topk / ws.have.
+// Candidate capacity per query and round: the dense round's rows, and room for several times
+// the ~7 k expected passes of a filter round.  A query that still overflows is re-run with a
+// capacity equal to the largest round.
+static int round_cap(size_t n, size_t k, bool gemm, int dpad) {
+    size_t cap = std::max<size_t>(2048, 32 * std::max<size_t>(k, 1));
+    for (const Round &r : plan_rounds(n, k, gemm, dpad))
+        if (r.rb == 0) cap = std::max(cap, (size_t)(r.re - r.rb));
+    return (int)round_up(cap, kRowAlign);
+}
+
+// Runs all rounds for nq prepared queries; results stay in topk / have.
 static int run_rounds(vhip_knn *E, const float *qpad, const float *qnorm, int nq, int k, int cap, DevBuf &cand,
                       DevBuf &topk, DevBuf &tau, DevBuf &have, DevBuf &cnt, DevBuf &flags, DevBuf &nflag) {
     hipStream_t s = E->stream;
@@ -86,19 +109,20 @@ static int run_rounds(vhip_knn *E, const float *qpad, const float *qnorm, int nq
     launch_topk_init(nq, tau.as<float>(), have.as<uint32_t>(), cnt.as<uint32_t>(), flags.as<uint32_t>(), s);
     launch_fill_u32(nflag.as<uint32_t>(), 1, 0u, s);
     const bool gemm = is_gemm_metric(E->metric);
-    // The round plan depends on (n, k) only; `cap` is the storage per query and round.
-    for (auto [rb, re] : plan_rounds(E->n, (size_t)k, kCap)) {
+    for (const Round &rd : plan_rounds(E->n, (size_t)k, gemm, (int)E->dpad)) {
+        const long rb = rd.rb, re = rd.re;
         // Algorithmic work per launch: 2*Q*rows*D flops (GEMM metrics), Q*rows*D element
         // operations (VALU metrics) or Q*rows*words word operations (packed Hamming); bytes
         // are the base rows and queries each launch must read once.
         const double rows = (double)(re - rb);
         const double work = gemm ? 2.0 * nq * rows * (double)E->dim : (double)nq * rows * (double)E->dim;
         const double bytes = rows * E->dim * 4.0 + (double)nq * E->dim * 4.0;
+        if (rd.dense) launch_fill_u32(cnt.as<uint32_t>(), (size_t)nq, (uint32_t)(re - rb), s);
         const int t = E->timer.begin(s);
         if (gemm)
-            launch_gemm_filter(E->metric, E->base.as<float>(), E->norm.as<float>(), qpad, qnorm, tau.as<float>(), nq,
-                               (int)E->dpad, rb, re, cand.as<uint2>(), cnt.as<uint32_t>(), cap, E->norm_max,
-                               E->norm_min, E->grid_cap, s);
+            launch_gemm_filter(E->metric, rd.dense, rd.item_rows, E->base.as<float>(), E->norm.as<float>(), qpad,
+                               qnorm, tau.as<float>(), nq, (int)E->dpad, rb, re, cand.as<uint2>(),
+                               cnt.as<uint32_t>(), cap, E->norm_max, E->norm_min, E->grid_cap, s);
         else if (E->metric == HAMMING_PACKED)
             launch_hamming_filter(E->base.as<uint32_t>(), (const uint32_t *)qpad, tau.as<float>(), nq, (int)E->dpad,
                                   rb, re, cand.as<uint2>(), cnt.as<uint32_t>(), cap, E->grid_cap, s);
@@ -122,7 +146,9 @@ static int search_prepared(vhip_knn *E, const float *qpad, const float *qnorm, i
                            uint32_t *d_ids, float *d_dist, uint32_t *d_dist_u32, int ostride) {
     Workspace &W = E->ws;
     hipStream_t s = E->stream;
-    VH_CHECK(run_rounds(E, qpad, qnorm, nq, k, kCap, W.cand, W.topk, W.tau, W.have, W.cnt, W.flags, W.nflag));
+    const bool gemm = is_gemm_metric(E->metric);
+    const int cap = round_cap(E->n, (size_t)k, gemm, (int)E->dpad);
+    VH_CHECK(run_rounds(E, qpad, qnorm, nq, k, cap, W.cand, W.topk, W.tau, W.have, W.cnt, W.flags, W.nflag));
     uint32_t nflag = 0;
     VH_HIP(hipMemcpyAsync(&nflag, W.nflag.p, sizeof(uint32_t), hipMemcpyDeviceToHost, s));
     VH_HIP(hipStreamSynchronize(s));
@@ -133,9 +159,9 @@ static int search_prepared(vhip_knn *E, const float *qpad, const float *qnorm, i
         std::vector<int> idx;
         for (int q = 0; q < nq; ++q)
             if (flags[q]) idx.push_back(q);
-        long big = 0;
-        for (auto [rb, re] : plan_rounds(E->n, (size_t)k, kCap)) big = std::max(big, re - rb);
-        const int cap_big = (int)std::max<long>(big, k);
+        long big = cap;
+        for (const Round &rd : plan_rounds(E->n, (size_t)k, gemm, (int)E->dpad)) big = std::max(big, rd.re - rd.rb);
+        const int cap_big = (int)round_up((size_t)std::max<long>(big, k), kRowAlign);
         const size_t per_batch = std::max<size_t>(1, ((size_t)1 << 30) / ((size_t)cap_big * sizeof(uint2)));
         DevBuf fq, fn, fcand, ftopk, ftau, fhave, fcnt, fflags, fnflag;
         for (size_t b0 = 0; b0 < idx.size(); b0 += per_batch) {

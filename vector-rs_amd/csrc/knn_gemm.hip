@@ -6,7 +6,8 @@
 // of kmeans_assign_and_accumulate (kmeans.cu:38-285).  The Q x N distance matrix is never
 // written: in FILTER mode every workgroup keeps its 128 queries' current threshold tau in
 // registers and stages only the (score, row) pairs with score <= tau; in ASSIGN mode every
-// lane keeps a running (score, centroid) minimum.
+// lane keeps a running (score, centroid) minimum; DENSE mode (the first, small round of a
+// search) writes every score of its rows.
 //
 // Operands: A = rows (resident base vectors, or centroids), B = columns (queries, or points),
 // both row-major with `dpad` floats per row (a multiple of 32, zero filled).  A's row count is
@@ -14,25 +15,25 @@
 // comparison; B's row count is padded to a multiple of 128.  The inner loop has no bounds checks.
 //
 // Two kernels share the epilogues:
-//  * k_mfma_res (dpad <= 128): a workgroup of 8 waves owns a work item of 128 columns; the
-//    whole 128 x dpad column tile stays resident in LDS for the item, and 256-row stages of A
-//    stream through double-buffered LDS in K-chunks of 32 floats.  Only A crosses the L2 -> CU
-//    path per stage (64 flop per byte).
+//  * k_mfma_reg (dpad <= 128): a workgroup of 8 waves owns a work item of 128 columns whose
+//    128 x dpad tile stays resident in LDS; each wave streams its own 64 rows of A straight from
+//    L2 into registers one K-chunk (32 floats) ahead, so waves need no barrier inside an item.
 //  * k_mfma_stream (dpad > 128): a workgroup of 4 waves streams 128-row x 128-column stages of
-//    both operands in K-chunks (32 flop per byte), two workgroups per CU.
+//    both operands through double-buffered LDS in K-chunks (32 flop per byte), two workgroups
+//    per CU.
 // Each wave owns a 64 x 64 sub-tile of 2 x 2 v_mfma_f32_32x32x2f32 blocks.  LDS tiles are
 // swizzled for gfx950's LDS (64 banks; a ds_read_b128 serves 16 lanes per pass): within 16
 // consecutive rows, row parity selects the 128-byte half of the banks and (row >> 1) & 7 XORs
 // the 16-byte slot, so the b128 operand reads and the b128 tile stores are conflict-free.
-// The pipeline is continuous: while chunk t is multiplied, chunk t+1 -- which may belong to the
-// next stage or the next work item -- is already in flight from HBM/L2.  The grid is persistent
-// and XCD-aware: work items are handed out so that the workgroups resident on one XCD walk the
-// same base rows together and share them through that XCD's L2.
+// The grid is persistent and XCD-aware: work items are handed out so that the workgroups
+// resident on one XCD walk the same base rows together and share them through that XCD's L2.
 //
 // FILTER epilogue: per score two VALU operations decide "may pass" against a slightly loose
 // threshold; only groups of 8 scores in which some lane may pass take the exact path.  Passing
 // (score, row) pairs are appended to per-query LDS slots (LDS atomics) and flushed to the
-// global per-query candidate lists once per work item, with one global atomic per query.
+// global per-query candidate lists once per work item, with one global atomic per query.  The
+// host sizes each round's work items so that the expected passes per query and item stay well
+// below the slot count.
 #include "vh_common.h"
 
 namespace vh {
@@ -40,10 +41,9 @@ namespace vh {
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
-constexpr int kFilter = 0, kAssign = 1;
-constexpr int kItemRows = 2048;  // base rows per kNN work item
-constexpr int kResSlots = 16;    // LDS candidate slots per query per work item (resident kernel)
-constexpr int kStrSlots = 14;    // same for the streaming kernel (two workgroups share a CU's LDS)
+constexpr int kFilter = 0, kAssign = 1, kDense = 2;
+constexpr int kRegSlots = kGemmSlotsReg;     // LDS candidate slots per query per work item (register-fed kernel)
+constexpr int kStrSlots = kGemmSlotsStream;  // same for the streaming kernel (two workgroups share a CU's LDS)
 
 // float4 index of (row, c4) in a 32-float-wide swizzled tile
 __device__ __forceinline__ int swz(int row, int c4) { return row * 8 + (c4 ^ ((row >> 1) & 7)); }
@@ -188,7 +188,7 @@ __device__ __forceinline__ void item_begin(EpiState &st, const ScanArgs &a, int 
             } else {
                 st.T[cb] = -t;  // score = -dot <= tau  <=>  dot >= -tau (exact)
             }
-        } else {
+        } else if constexpr (MODE == kAssign) {
             st.bs[cb] = INFINITY;
             st.bi[cb] = 0;
         }
@@ -201,19 +201,37 @@ __device__ __forceinline__ void item_begin(EpiState &st, const ScanArgs &a, int 
     }
 }
 
+// Appends (key, row) to query column ql's LDS slots; a full slot list spills to the global
+// candidate list with one atomic per entry.
+template <int SLOTS>
+__device__ __forceinline__ void append_candidate(const ScanArgs &a, int ql, uint32_t key, uint32_t row_in_item,
+                                                 long r_lo, int col0, uint32_t *s_qcnt, uint2 *s_slot) {
+    const uint32_t r = atomicAdd(&s_qcnt[ql], 1u);
+    if (r < (uint32_t)SLOTS) {
+        s_slot[ql * SLOTS + r] = make_uint2(key, row_in_item);
+    } else {
+        const int q = col0 + ql;
+        const uint32_t at = atomicAdd(&a.cnt[q], 1u);
+        if (at < (uint32_t)a.cap) a.cand[(size_t)q * a.cap + at] = make_uint2(key, (uint32_t)(r_lo + row_in_item));
+    }
+}
+
 // FILTER: stage every (score, row) of this stage with score <= tau.  Accumulator register
 // 4g+j of block (rb, cb) holds row 64wr + 32rb + 8g + 4h + j of the stage and column
-// 64wc + 32cb + l32 of the tile.
-template <int M, int SLOTS>
-__device__ __forceinline__ void filter_stage(const floatx16 (&acc)[2][2], const float *nrow, const EpiState &st,
+// 64wc + 32cb + l32 of the tile.  `nf(rb, g)` returns the epilogue values (row norms) of rows
+// rl0 .. rl0 + 3 below.  Each score costs two VALU operations against a slightly loose
+// threshold; only a group of 8 scores in which some lane of the wave may pass takes the exact
+// path (one wave-uniform branch per group).
+template <int M, int SLOTS, class NF>
+__device__ __forceinline__ void filter_stage(const floatx16 (&acc)[2][2], NF nf, const EpiState &st,
                                              const ScanArgs &a, int wr, int wc, int l32, int h, long rs, long r_lo,
                                              int col0, uint32_t *s_qcnt, uint2 *s_slot) {
+    const uint32_t row0 = (uint32_t)(rs - r_lo) + 64 * wr + 4 * h;
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-            const int rl0 = 64 * wr + 32 * rb + 8 * g + 4 * h;
-            const floatx4 n4 = *(const floatx4 *)(nrow + rl0);
+            const floatx4 n4 = nf(rb, g);
             bool p[4][2];
             bool any = false;
 #pragma unroll
@@ -233,8 +251,8 @@ __device__ __forceinline__ void filter_stage(const floatx16 (&acc)[2][2], const 
 #pragma unroll
                     for (int cb = 0; cb < 2; ++cb) {
                         const float dot = acc[rb][cb][4 * g + j];
-                        const float s = st.cn[cb] * n4[j] > 1e-9f ? -dot : 0.0f * dot;
-                        p[j][cb] = s <= st.tau_e[cb];
+                        const float sc = st.cn[cb] * n4[j] > 1e-9f ? -dot : 0.0f * dot;
+                        p[j][cb] = sc <= st.tau_e[cb];
                         any = any || p[j][cb];
                     }
             }
@@ -245,26 +263,17 @@ __device__ __forceinline__ void filter_stage(const floatx16 (&acc)[2][2], const 
                     for (int cb = 0; cb < 2; ++cb) {
                         if (!p[j][cb]) continue;
                         const float dot = acc[rb][cb][4 * g + j];
-                        float s;
+                        float sc;
                         if constexpr (M == L2) {
-                            s = fmaxf(fmaf(-2.0f, dot, st.cn[cb] + n4[j]), 0.0f);
-                            if (!(s <= st.tau_e[cb])) continue;
+                            sc = fmaxf(fmaf(-2.0f, dot, st.cn[cb] + n4[j]), 0.0f);
+                            if (!(sc <= st.tau_e[cb])) continue;
                         } else if constexpr (M == DOT) {
-                            s = canon(-dot);
+                            sc = canon(-dot);
                         } else {
-                            s = st.guard ? (st.cn[cb] * n4[j] > 1e-9f ? canon(-dot) : 0.0f) : canon(-dot);
+                            sc = st.guard ? (st.cn[cb] * n4[j] > 1e-9f ? canon(-dot) : 0.0f) : canon(-dot);
                         }
-                        const int ql = 64 * wc + 32 * cb + l32;
-                        const uint32_t key = score_key(s);
-                        const uint32_t r = atomicAdd(&s_qcnt[ql], 1u);
-                        if (r < (uint32_t)SLOTS) {
-                            s_slot[ql * SLOTS + r] = make_uint2(key, (uint32_t)(rs - r_lo) + rl0 + j);
-                        } else {
-                            const int q = col0 + ql;
-                            const uint32_t at = atomicAdd(&a.cnt[q], 1u);
-                            if (at < (uint32_t)a.cap)
-                                a.cand[(size_t)q * a.cap + at] = make_uint2(key, (uint32_t)(rs + rl0 + j));
-                        }
+                        append_candidate<SLOTS>(a, 64 * wc + 32 * cb + l32, score_key(sc),
+                                                row0 + 32 * rb + 8 * g + j, r_lo, col0, s_qcnt, s_slot);
                     }
             }
         }
@@ -295,12 +304,52 @@ __device__ __forceinline__ void filter_flush(const ScanArgs &a, int col0, long r
     }
 }
 
+// DENSE: every (score, row) of the stage with row < row_end is written to
+// cand[q * cap + (row - row_begin)] (the round's rows fit the per-query capacity), four
+// consecutive rows of one column per pair of 16-byte stores.  Scores are the exact-path values
+// of FILTER mode.
+template <int M, class NF>
+__device__ __forceinline__ void dense_stage(const floatx16 (&acc)[2][2], NF nf, const EpiState &st,
+                                            const ScanArgs &a, int wr, int wc, int l32, int h, long rs, int col0) {
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) {
+        const int q = col0 + 64 * wc + 32 * cb + l32;
+        if (q >= a.ncols) continue;
+        uint2 *dst = a.cand + (size_t)q * a.cap;
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const floatx4 n4 = nf(rb, g);
+                const long row = rs + 64 * wr + 32 * rb + 8 * g + 4 * h;
+                uint32_t key[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float dot = acc[rb][cb][4 * g + j];
+                    float sc;
+                    if constexpr (M == L2) sc = fmaxf(fmaf(-2.0f, dot, st.cn[cb] + n4[j]), 0.0f);
+                    else if constexpr (M == DOT) sc = canon(-dot);
+                    else sc = st.cn[cb] * n4[j] > 1e-9f ? canon(-dot) : 0.0f;
+                    key[j] = score_key(sc);
+                }
+                const uint32_t p0 = (uint32_t)(row - a.row_begin);
+                if (row + 3 < a.row_end) {
+                    *(uint4 *)(dst + p0) = make_uint4(key[0], (uint32_t)row, key[1], (uint32_t)row + 1);
+                    *(uint4 *)(dst + p0 + 2) = make_uint4(key[2], (uint32_t)row + 2, key[3], (uint32_t)row + 3);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        if (row + j < a.row_end) dst[p0 + j] = make_uint2(key[j], (uint32_t)(row + j));
+                }
+            }
+    }
+}
+
 // ASSIGN: per column, the minimum score over this stage's 32 rows held by the lane, then the
 // first (lowest) row reaching it.  Rows are visited in ascending order with a strict '<' across
 // stages, so the lowest index wins ties (kmeans.cu:110-114).
-template <int M>
-__device__ __forceinline__ void assign_stage(floatx16 (&acc)[2][2], const float *nrow, EpiState &st, int wr, int h,
-                                             long rs) {
+template <int M, class NF>
+__device__ __forceinline__ void assign_stage(floatx16 (&acc)[2][2], NF nf, EpiState &st, int wr, int h, long rs) {
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb) {
         float m = INFINITY;
@@ -308,8 +357,7 @@ __device__ __forceinline__ void assign_stage(floatx16 (&acc)[2][2], const float 
         for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-                const int rl0 = 64 * wr + 32 * rb + 8 * g + 4 * h;
-                const floatx4 n4 = *(const floatx4 *)(nrow + rl0);
+                const floatx4 n4 = nf(rb, g);
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const float dot = acc[rb][cb][4 * g + j];
@@ -397,152 +445,6 @@ __device__ __forceinline__ void decode_item(const ScanArgs &a, int it, int &c0, 
 // item block [t*G + x*G/8, t*G + (x+1)*G/8) (G, the grid size, is a multiple of 8).
 __device__ __forceinline__ int first_item() {
     return (blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3);
-}
-
-// =========================================================================================
-// Resident-column kernel: 8 waves, 256-row stages, NK K-chunks (dpad = 32 NK <= 128).
-// =========================================================================================
-template <int MODE, int M, int NK>
-__global__ __launch_bounds__(512, 1) void k_mfma_res(ScanArgs a) {
-    constexpr int RW = 4, TR = 256;
-    __shared__ floatx4 sA[2][TR * 8];
-    __shared__ floatx4 sB[kTileCols * 8 * NK];
-    __shared__ __attribute__((aligned(16))) float sN[2][TR];
-    __shared__ uint32_t s_qcnt[MODE == kFilter ? kTileCols : 1];
-    __shared__ uint2 s_slot[MODE == kFilter ? kTileCols * kResSlots : 1];
-    __shared__ float s_xs[MODE == kAssign ? (RW - 1) * kTileCols : 1];
-    __shared__ int s_xi[MODE == kAssign ? (RW - 1) * kTileCols : 1];
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wr = wave & 3, wc = wave >> 2;
-    const int l32 = lane & 31, h = lane >> 5;
-    const int G = gridDim.x;
-    int item = first_item();
-    if (item >= a.n_items) return;
-
-    // B tile: row r, chunk kc, slot c4.  Row parity (with the chunk) picks the bank half.
-    auto bidx_kc = [](int r, int kc, int c4) {
-        const int pch = (NK % 2 == 0) ? (kc ^ (r & 1)) : kc;
-        return r * (8 * NK) + pch * 8 + (c4 ^ ((r >> 1) & 7));
-    };
-    auto load_a = [&](floatx4 (&ra)[4], long rs, int k0) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int f = tid + 512 * i;
-            ra[i] = *(const floatx4 *)(a.A + (rs + (f >> 3)) * (long)(32 * NK) + k0 + 4 * (f & 7));
-        }
-    };
-    auto store_a = [&](const floatx4 (&ra)[4], floatx4 *dst) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int f = tid + 512 * i;
-            dst[swz(f >> 3, f & 7)] = ra[i];
-        }
-    };
-    auto load_b = [&](floatx4 (&rq)[2 * NK], int c0) {
-#pragma unroll
-        for (int i = 0; i < 2 * NK; ++i) {
-            const int f = tid + 512 * i;
-            const int r = f / (8 * NK), rem = f % (8 * NK);
-            rq[i] = *(const floatx4 *)(a.B + (long)(c0 + r) * (32 * NK) + 4 * rem);
-        }
-    };
-    auto store_b = [&](const floatx4 (&rq)[2 * NK]) {
-#pragma unroll
-        for (int i = 0; i < 2 * NK; ++i) {
-            const int f = tid + 512 * i;
-            const int r = f / (8 * NK), rem = f % (8 * NK);
-            sB[bidx_kc(r, rem >> 3, rem & 7)] = rq[i];
-        }
-    };
-
-    int col0;
-    long r_lo, r_hi;
-    decode_item(a, item, col0, r_lo, r_hi);
-    long rs = r_lo;
-    EpiState st;
-    item_begin<MODE, M>(st, a, col0, wc, l32);
-
-    // ---- pipeline prologue ----
-    floatx4 ra[4], rq[2 * NK];
-    float rn = 0.0f;
-    load_b(rq, col0);
-    load_a(ra, rs, 0);
-    if (tid < TR) rn = a.anorm[rs + tid];
-    store_b(rq);
-    store_a(ra, sA[0]);
-    if (tid < TR) sN[0][tid] = rn;
-    if constexpr (MODE == kFilter) {
-        if (tid < kTileCols) s_qcnt[tid] = 0;
-    }
-    __syncthreads();
-    int buf = 0, sb = 0;
-
-    for (;;) {
-        long nrs = rs + TR;
-        int nitem = item, ncol0 = col0;
-        long nlo = r_lo, nhi = r_hi;
-        const bool item_end = nrs >= r_hi;
-        bool more = true;
-        if (item_end) {
-            nitem = item + G;
-            more = nitem < a.n_items;
-            if (more) {
-                decode_item(a, nitem, ncol0, nlo, nhi);
-                nrs = nlo;
-            }
-        }
-
-        floatx16 acc[2][2];
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int j = 0; j < 2; ++j) acc[i][j] = floatx16{0};
-
-#pragma unroll
-        for (int kc = 0; kc < NK; ++kc) {
-            const bool last = kc + 1 == NK;
-            if (!last) {
-                load_a(ra, rs, (kc + 1) * kKChunk);
-            } else if (more) {
-                load_a(ra, nrs, 0);
-                if (tid < TR) rn = a.anorm[nrs + tid];
-            }
-            mfma_chunk(acc, sA[buf], sB, [&](int r, int c4) { return bidx_kc(r, kc, c4); }, wr, wc, l32, h);
-            if (!last || more) {
-                store_a(ra, sA[buf ^ 1]);
-                if (last && tid < TR) sN[sb ^ 1][tid] = rn;
-            }
-            __syncthreads();
-            buf ^= 1;
-        }
-        // The next item's column tile is fetched while this stage's epilogue runs.
-        const bool new_cols = item_end && more;
-        if (new_cols) load_b(rq, ncol0);
-
-        const float *nrow = sN[sb];
-        if constexpr (MODE == kFilter) {
-            filter_stage<M, kResSlots>(acc, nrow, st, a, wr, wc, l32, h, rs, r_lo, col0, s_qcnt, s_slot);
-            if (item_end) filter_flush<kResSlots>(a, col0, r_lo, s_qcnt, s_slot);
-        } else {
-            assign_stage<M>(acc, nrow, st, wr, h, rs);
-            if (item_end) assign_finish<M, RW>(st, a, col0, wr, wc, l32, h, s_xs, s_xi);
-        }
-
-        if (!more) break;
-        if (new_cols) {
-            // every wave finished this item's MFMAs (barrier after the last chunk)
-            store_b(rq);
-            __syncthreads();
-            item = nitem;
-            col0 = ncol0;
-            r_lo = nlo;
-            r_hi = nhi;
-            item_begin<MODE, M>(st, a, col0, wc, l32);
-        }
-        rs = nrs;
-        sb ^= 1;
-    }
 }
 
 // =========================================================================================
@@ -643,11 +545,14 @@ __global__ __launch_bounds__(256, 2) void k_mfma_stream(ScanArgs a) {
         }
 
         const float *nrow = sN[sb];
+        auto nf = [&](int rb, int g) { return *(const floatx4 *)(nrow + 64 * wr + 32 * rb + 8 * g + 4 * h); };
         if constexpr (MODE == kFilter) {
-            filter_stage<M, kStrSlots>(acc, nrow, st, a, wr, wc, l32, h, rs, r_lo, col0, s_qcnt, s_slot);
+            filter_stage<M, kStrSlots>(acc, nf, st, a, wr, wc, l32, h, rs, r_lo, col0, s_qcnt, s_slot);
             if (item_end) filter_flush<kStrSlots>(a, col0, r_lo, s_qcnt, s_slot);
+        } else if constexpr (MODE == kDense) {
+            dense_stage<M>(acc, nf, st, a, wr, wc, l32, h, rs, col0);
         } else {
-            assign_stage<M>(acc, nrow, st, wr, h, rs);
+            assign_stage<M>(acc, nf, st, wr, h, rs);
             if (item_end) assign_finish<M, RW>(st, a, col0, wr, wc, l32, h, s_xs, s_xi);
         }
 
@@ -661,6 +566,159 @@ __global__ __launch_bounds__(256, 2) void k_mfma_stream(ScanArgs a) {
             r_hi = nhi;
             item_begin<MODE, M>(st, a, col0, wc, l32);
         }
+    }
+}
+
+// =========================================================================================
+// Register-fed kernel: 8 waves, 256-row stages, NK K-chunks (dpad = 32 NK <= 128).  The
+// 128-column tile stays resident in LDS for a work item, as in k_mfma_res, but every wave loads
+// its own 64 rows of A straight from L2 into registers, one K-chunk ahead, so there is no barrier
+// inside an item: the waves of a SIMD drift apart and one wave's epilogue runs under the other
+// wave's MFMAs.  Barriers remain only at item boundaries (candidate flush / argmin combine and
+// the column-tile reload).
+// =========================================================================================
+template <int MODE, int M, int NK>
+__global__ __launch_bounds__(512, 1) void k_mfma_reg(ScanArgs a) {
+    constexpr int RW = 4, TR = 256, D = 32 * NK;
+    __shared__ floatx4 sB[kTileCols * 8 * NK];
+    __shared__ uint32_t s_qcnt[MODE == kFilter ? kTileCols : 1];
+    __shared__ uint2 s_slot[MODE == kFilter ? kTileCols * kRegSlots : 1];
+    __shared__ float s_xs[MODE == kAssign ? (RW - 1) * kTileCols : 1];
+    __shared__ int s_xi[MODE == kAssign ? (RW - 1) * kTileCols : 1];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wr = wave & 3, wc = wave >> 2;
+    const int l32 = lane & 31, h = lane >> 5;
+    const int G = gridDim.x;
+    int item = first_item();
+    if (item >= a.n_items) return;
+
+    auto bidx_kc = [](int r, int kc, int c4) {
+        const int pch = (NK % 2 == 0) ? (kc ^ (r & 1)) : kc;
+        return r * (8 * NK) + pch * 8 + (c4 ^ ((r >> 1) & 7));
+    };
+    // Column tile: 128 rows of D floats, 2 NK float4 per thread.
+    auto fill_b = [&](int c0) {
+        floatx4 rq[2 * NK];
+#pragma unroll
+        for (int i = 0; i < 2 * NK; ++i) {
+            const int f = tid + 512 * i;
+            const int r = f / (8 * NK), rem = f % (8 * NK);
+            rq[i] = *(const floatx4 *)(a.B + (long)(c0 + r) * D + 4 * rem);
+        }
+#pragma unroll
+        for (int i = 0; i < 2 * NK; ++i) {
+            const int f = tid + 512 * i;
+            const int r = f / (8 * NK), rem = f % (8 * NK);
+            sB[bidx_kc(r, rem >> 3, rem & 7)] = rq[i];
+        }
+    };
+    // A chunk kc of the stage at row rs: lane (l32, h) holds rows 64 wr + l32 (+32) at floats
+    // 32 kc + 8 g + 4 h .. + 3 (g = 0..3), the operand layout mfma_chunk expects.
+    auto load_a = [&](floatx4 (&r)[8], long rs, int kc) {
+        const float *p0 = a.A + (rs + 64 * wr + l32) * (long)D + 32 * kc + 4 * h;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            r[g] = *(const floatx4 *)(p0 + 8 * g);
+            r[4 + g] = *(const floatx4 *)(p0 + 32 * D + 8 * g);
+        }
+    };
+
+    int col0;
+    long r_lo, r_hi;
+    decode_item(a, item, col0, r_lo, r_hi);
+    fill_b(col0);
+    if constexpr (MODE == kFilter) {
+        if (tid < kTileCols) s_qcnt[tid] = 0;
+    }
+    long rs = r_lo;
+    EpiState st;
+    item_begin<MODE, M>(st, a, col0, wc, l32);
+    floatx4 cur[8];
+    load_a(cur, rs, 0);
+    __syncthreads();
+
+    for (;;) {
+        long nrs = rs + TR;
+        int nitem = item, ncol0 = col0;
+        long nlo = r_lo, nhi = r_hi;
+        const bool item_end = nrs >= r_hi;
+        bool more = true;
+        if (item_end) {
+            nitem = item + G;
+            more = nitem < a.n_items;
+            if (more) {
+                decode_item(a, nitem, ncol0, nlo, nhi);
+                nrs = nlo;
+            }
+        }
+        floatx4 nv[8];  // row epilogue values of this stage (rows 64 wr + 32 rb + 8 g + 4 h .. + 3)
+        floatx16 acc[2][2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) acc[i][j] = floatx16{0};
+
+#pragma unroll
+        for (int kc = 0; kc < NK; ++kc) {
+            floatx4 nxt[8];
+            const bool last = kc + 1 == NK;
+            if (!last) load_a(nxt, rs, kc + 1);
+            else if (more) load_a(nxt, nrs, 0);
+            if (last) {
+#pragma unroll
+                for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+                    for (int g = 0; g < 4; ++g)
+                        nv[4 * rb + g] = *(const floatx4 *)(a.anorm + rs + 64 * wr + 32 * rb + 8 * g + 4 * h);
+            }
+            // keep the loads above the MFMAs: the scheduler would otherwise sink them next to
+            // their first use and expose the L2 latency
+            __builtin_amdgcn_sched_barrier(0);
+            const int rb0 = 64 * wc + l32, rb1 = rb0 + 32;
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int c4 = 2 * g + h;
+                const floatx4 a0 = cur[g], a1 = cur[4 + g];
+                const floatx4 b0 = sB[bidx_kc(rb0, kc, c4)];
+                const floatx4 b1 = sB[bidx_kc(rb1, kc, c4)];
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[t], b0[t], acc[0][0], 0, 0, 0);
+                    acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[t], b1[t], acc[0][1], 0, 0, 0);
+                    acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[t], b0[t], acc[1][0], 0, 0, 0);
+                    acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[t], b1[t], acc[1][1], 0, 0, 0);
+                }
+            }
+            if (!last || more) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) cur[i] = nxt[i];
+            }
+        }
+
+        auto nf = [&](int rb, int g) { return nv[4 * rb + g]; };
+        if constexpr (MODE == kFilter) {
+            filter_stage<M, kRegSlots>(acc, nf, st, a, wr, wc, l32, h, rs, r_lo, col0, s_qcnt, s_slot);
+            if (item_end) filter_flush<kRegSlots>(a, col0, r_lo, s_qcnt, s_slot);
+        } else if constexpr (MODE == kDense) {
+            dense_stage<M>(acc, nf, st, a, wr, wc, l32, h, rs, col0);
+        } else {
+            assign_stage<M>(acc, nf, st, wr, h, rs);
+            if (item_end) assign_finish<M, RW>(st, a, col0, wr, wc, l32, h, s_xs, s_xi);
+        }
+
+        if (!more) break;
+        if (item_end) {
+            // every wave is past this item's MFMAs (barrier in the flush / combine above)
+            fill_b(ncol0);
+            __syncthreads();
+            item = nitem;
+            col0 = ncol0;
+            r_lo = nlo;
+            r_hi = nhi;
+            item_begin<MODE, M>(st, a, col0, wc, l32);
+        }
+        rs = nrs;
     }
 }
 
@@ -679,10 +737,10 @@ static void launch_scan(const ScanArgs &a, int grid_cap, hipStream_t s) {
     if (nk <= 4) {
         const dim3 g(grid_for(a.n_items, cus)), b(512);
         switch (nk) {
-            case 1: hipLaunchKernelGGL((k_mfma_res<MODE, M, 1>), g, b, 0, s, a); break;
-            case 2: hipLaunchKernelGGL((k_mfma_res<MODE, M, 2>), g, b, 0, s, a); break;
-            case 3: hipLaunchKernelGGL((k_mfma_res<MODE, M, 3>), g, b, 0, s, a); break;
-            default: hipLaunchKernelGGL((k_mfma_res<MODE, M, 4>), g, b, 0, s, a); break;
+            case 1: hipLaunchKernelGGL((k_mfma_reg<MODE, M, 1>), g, b, 0, s, a); break;
+            case 2: hipLaunchKernelGGL((k_mfma_reg<MODE, M, 2>), g, b, 0, s, a); break;
+            case 3: hipLaunchKernelGGL((k_mfma_reg<MODE, M, 3>), g, b, 0, s, a); break;
+            default: hipLaunchKernelGGL((k_mfma_reg<MODE, M, 4>), g, b, 0, s, a); break;
         }
     } else {
         const dim3 g(grid_for(a.n_items, 2 * cus)), b(256);
@@ -699,9 +757,10 @@ static void launch_metric(int metric, const ScanArgs &a, int grid_cap, hipStream
     }
 }
 
-void launch_gemm_filter(int metric, const float *base, const float *bnorm, const float *qry, const float *qnorm,
-                        const float *tau, int nq, int dpad, long row_begin, long row_end, uint2 *cand, uint32_t *cnt,
-                        int cap, float anorm_max, float anorm_min, int grid_cap, hipStream_t s) {
+void launch_gemm_filter(int metric, bool dense, long item_rows, const float *base, const float *bnorm,
+                        const float *qry, const float *qnorm, const float *tau, int nq, int dpad, long row_begin,
+                        long row_end, uint2 *cand, uint32_t *cnt, int cap, float anorm_max, float anorm_min,
+                        int grid_cap, hipStream_t s) {
     if (nq <= 0 || row_end <= row_begin) return;
     ScanArgs a{};
     a.A = base;
@@ -711,7 +770,7 @@ void launch_gemm_filter(int metric, const float *base, const float *bnorm, const
     a.dpad = dpad;
     a.ncols = nq;
     a.n_ctiles = ceil_div(nq, kTileCols);
-    a.item_rows = kItemRows;
+    a.item_rows = item_rows;
     a.row_begin = row_begin;
     a.row_end = row_end;
     const long n_chunks = (row_end - row_begin + a.item_rows - 1) / a.item_rows;
@@ -722,7 +781,8 @@ void launch_gemm_filter(int metric, const float *base, const float *bnorm, const
     a.cap = cap;
     a.anorm_max = anorm_max;
     a.anorm_min = anorm_min;
-    launch_metric<kFilter>(metric, a, grid_cap, s);
+    if (dense) launch_metric<kDense>(metric, a, grid_cap, s);
+    else launch_metric<kFilter>(metric, a, grid_cap, s);
 }
 
 void launch_kmeans_assign(int metric, const float *cent, const float *cnorm, int kpad, const float *pts,

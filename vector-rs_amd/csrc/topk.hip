@@ -2,11 +2,13 @@
 //
 // A search runs the base in rounds of geometrically growing row ranges.  The filter
 // kernels (knn_gemm.hip, knn_valu.hip, hamming.hip) append every (score, id) with
-// score <= tau[q] to the query's candidate list; k_topk_merge then sorts the running
-// top-k together with those candidates (64-bit keys: ordered score << 32 | id, so ties
-// break towards the lower id) and keeps the best k.  The new tau is the k-th score, an
+// score <= tau[q] to the query's candidate list; k_topk_merge then selects the best k of the
+// running top-k and those candidates (64-bit keys: ordered score << 32 | id, so ties break
+// towards the lower id).  The new tau is the k-th score, an
 // upper bound of the final k-th score, so no true neighbour can be filtered out later.
 // This replaces knn_topk_select (knn.cu:206-305) and its K <= 128 clamp.
+#include <algorithm>
+
 #include "vh_common.h"
 
 namespace vh {
@@ -70,12 +72,46 @@ __device__ __forceinline__ void bitonic_sort_lds(u64 *buf, int P) {
     }
 }
 
-__global__ __launch_bounds__(256) void k_topk_merge(int k, const uint2 *__restrict__ cand, uint32_t *__restrict__ cnt,
-                                                    int cap, const uint32_t *__restrict__ perm,
-                                                    u64 *__restrict__ topk, uint32_t *__restrict__ have,
-                                                    float *__restrict__ tau, uint32_t *__restrict__ flags,
-                                                    uint32_t *__restrict__ nflagged) {
-    __shared__ u64 buf[kSortSlots];
+// ---- merge: running top-k + this round's candidates -> new top-k -------------------------
+// Element i of query q is the running entry topk[q][i] for i < have[q], else candidate
+// cand[q][i - have[q]]; its 64-bit key is (score key << 32) | vector id.  Keys are unique (every
+// base row is scanned by exactly one round), so "the k smallest keys" is well defined.
+//
+// Small merges (T = have + c <= kMergeDirect) sort everything in LDS.  Larger ones select
+// first: a histogram of the 32-bit score keys over kMergeBins equal-width buckets of
+// [min, max] finds the bucket holding the k-th smallest; the elements below it (fewer than k)
+// and those in it are gathered into LDS and only they are sorted.  When the boundary bucket is
+// too large for the buffer (massive score ties) the merge falls back to sorting chunks of the
+// elements against the running best k.
+constexpr int kMergeBins = 1024;
+constexpr int kMergeDirect = 512;
+
+__device__ __forceinline__ uint32_t block_reduce_u32(uint32_t v, bool is_max, uint32_t *red) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const uint32_t w = __shfl_xor(v, o, 64);
+        v = is_max ? max(v, w) : min(v, w);
+    }
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    v = red[0];
+    for (int w = 1; w < (int)(blockDim.x >> 6); ++w) v = is_max ? max(v, red[w]) : min(v, red[w]);
+    return v;
+}
+
+// buf holds `bufn` u64 entries (dynamic LDS, bufn >= 2 * pow2(k), >= kMergeDirect).
+__global__ __launch_bounds__(256) void k_topk_merge(int k, int bufn, const uint2 *__restrict__ cand,
+                                                    uint32_t *__restrict__ cnt, int cap,
+                                                    const uint32_t *__restrict__ perm, u64 *__restrict__ topk,
+                                                    uint32_t *__restrict__ have, float *__restrict__ tau,
+                                                    uint32_t *__restrict__ flags, uint32_t *__restrict__ nflagged) {
+    extern __shared__ u64 buf[];
+    __shared__ uint32_t hist[kMergeBins];
+    __shared__ uint32_t red[8];
+    __shared__ uint32_t s_part[256];
+    __shared__ uint32_t s_sel[4];  // boundary bucket, count below it, gather counters
     const int q = blockIdx.x, tid = threadIdx.x;
     const uint32_t c_all = cnt[q];
     if (flags[q] || c_all == 0) {
@@ -87,28 +123,104 @@ __global__ __launch_bounds__(256) void k_topk_merge(int k, const uint2 *__restri
     const uint32_t c = overflow ? (uint32_t)cap : c_all;
     u64 *tk = topk + (size_t)q * k;
     const uint2 *cq = cand + (size_t)q * cap;
+    const uint32_t h = have[q];
+    const uint32_t T = h + c;
+    auto key32 = [&](uint32_t i) -> uint32_t { return i < h ? (uint32_t)(tk[i] >> 32) : cq[i - h].x; };
+    auto key64 = [&](uint32_t i) -> u64 {
+        if (i < h) return tk[i];
+        const uint2 e = cq[i - h];
+        return ((u64)e.x << 32) | (u64)perm[e.y];  // base position -> vector id
+    };
 
-    uint32_t h = have[q];
-    for (uint32_t i = tid; i < h; i += 256) buf[i] = tk[i];
-    uint32_t done = 0;
-    while (done < c) {
-        const uint32_t take = min(c - done, (uint32_t)kSortSlots - h);
-        for (uint32_t i = tid; i < take; i += 256) {
-            const uint2 e = cq[done + i];
-            buf[h + i] = ((u64)e.x << 32) | (u64)perm[e.y];  // base position -> vector id
+    uint32_t hn = 0;  // entries of the new top-k, sorted in buf[0 .. hn)
+    bool done = false;
+    if (T > (uint32_t)kMergeDirect && T > (uint32_t)k) {
+        // ---- bucket select ----
+        uint32_t lo = 0xffffffffu, hi = 0u;
+        for (uint32_t i = tid; i < T; i += 256) {
+            const uint32_t v = key32(i);
+            lo = min(lo, v);
+            hi = max(hi, v);
         }
-        const uint32_t total = h + take;
-        int P = 2;
-        while ((uint32_t)P < total) P <<= 1;
-        for (uint32_t i = total + tid; i < (uint32_t)P; i += 256) buf[i] = ~0ull;
-        __syncthreads();
-        bitonic_sort_lds(buf, P);
-        h = min(total, (uint32_t)k);
-        done += take;
+        lo = block_reduce_u32(lo, false, red);
+        hi = block_reduce_u32(hi, true, red + 4);
+        if (lo < hi) {
+            const float scale = (float)kMergeBins / ((float)(hi - lo) + 1.0f);
+            auto bucket = [&](uint32_t v) { return min(kMergeBins - 1, (int)((float)(v - lo) * scale)); };
+            for (int i = tid; i < kMergeBins; i += 256) hist[i] = 0;
+            __syncthreads();
+            for (uint32_t i = tid; i < T; i += 256) atomicAdd(&hist[bucket(key32(i))], 1u);
+            __syncthreads();
+            // bucket b* holding the k-th smallest: cum(b*) < k <= cum(b*) + hist[b*]
+            constexpr int per = kMergeBins / 256;
+            uint32_t loc = 0;
+#pragma unroll
+            for (int j = 0; j < per; ++j) loc += hist[tid * per + j];
+            s_part[tid] = loc;
+            __syncthreads();
+            for (int o = 1; o < 256; o <<= 1) {
+                const uint32_t v = tid >= o ? s_part[tid - o] : 0u;
+                __syncthreads();
+                s_part[tid] += v;
+                __syncthreads();
+            }
+            uint32_t cum = s_part[tid] - loc;  // elements in buckets before this thread's bins
+#pragma unroll
+            for (int j = 0; j < per; ++j) {
+                const uint32_t hb = hist[tid * per + j];
+                if (cum < (uint32_t)k && (uint32_t)k <= cum + hb) {
+                    s_sel[0] = (uint32_t)(tid * per + j);
+                    s_sel[1] = cum;
+                }
+                cum += hb;
+            }
+            if (tid == 0) {
+                s_sel[2] = 0;
+                s_sel[3] = 0;
+            }
+            __syncthreads();
+            const int bstar = (int)s_sel[0];
+            const uint32_t below = s_sel[1];
+            const uint32_t inb = hist[bstar];
+            if (below + inb <= (uint32_t)bufn) {
+                for (uint32_t i = tid; i < T; i += 256) {
+                    const int b = bucket(key32(i));
+                    if (b < bstar) buf[atomicAdd(&s_sel[2], 1u)] = key64(i);
+                    else if (b == bstar) buf[below + atomicAdd(&s_sel[3], 1u)] = key64(i);
+                }
+                const uint32_t total = below + inb;
+                int P = 2;
+                while ((uint32_t)P < total) P <<= 1;
+                for (uint32_t i = total + tid; i < (uint32_t)P; i += 256) buf[i] = ~0ull;
+                __syncthreads();
+                bitonic_sort_lds(buf, P);
+                hn = (uint32_t)k;
+                done = true;
+            }
+        }
     }
-    for (uint32_t i = tid; i < h; i += 256) tk[i] = buf[i];
+    if (!done) {
+        // ---- sort everything, in chunks against the running best k ----
+        uint32_t hh = 0, next = 0;
+        while (next < T || hh == 0) {
+            const uint32_t take = min(T - next, (uint32_t)bufn - hh);
+            for (uint32_t i = tid; i < take; i += 256) buf[hh + i] = key64(next + i);
+            const uint32_t total = hh + take;
+            int P = 2;
+            while ((uint32_t)P < total) P <<= 1;
+            for (uint32_t i = total + tid; i < (uint32_t)P; i += 256) buf[i] = ~0ull;
+            __syncthreads();
+            bitonic_sort_lds(buf, P);
+            hh = min(total, (uint32_t)k);
+            next += take;
+            if (next >= T) break;
+        }
+        hn = hh;
+    }
+    __syncthreads();
+    for (uint32_t i = tid; i < hn; i += 256) tk[i] = buf[i];
     if (tid == 0) {
-        have[q] = h;
+        have[q] = hn;
         cnt[q] = 0;
         if (overflow) {
             // The list is incomplete: stop filtering for this query; the host re-runs it
@@ -117,17 +229,24 @@ __global__ __launch_bounds__(256) void k_topk_merge(int k, const uint2 *__restri
             tau[q] = -INFINITY;
             atomicAdd(nflagged, 1u);
         } else {
-            tau[q] = h >= (uint32_t)k ? key_score((uint32_t)(buf[k - 1] >> 32)) : INFINITY;
+            tau[q] = hn >= (uint32_t)k ? key_score((uint32_t)(buf[k - 1] >> 32)) : INFINITY;
         }
     }
+}
+
+int merge_buffer_entries(int k) {
+    int p = 1;
+    while (p < k) p <<= 1;
+    return std::max(2 * p, 1024);
 }
 
 void launch_topk_merge(int nq, int k, const uint2 *cand, uint32_t *cnt, int cap, const uint32_t *perm,
                        unsigned long long *topk, uint32_t *have, float *tau, uint32_t *flags, uint32_t *nflagged,
                        hipStream_t s) {
     if (nq <= 0) return;
-    hipLaunchKernelGGL(k_topk_merge, dim3(nq), dim3(256), 0, s, k, cand, cnt, cap, perm, topk, have, tau, flags,
-                       nflagged);
+    const int bufn = merge_buffer_entries(k);
+    hipLaunchKernelGGL(k_topk_merge, dim3(nq), dim3(256), (size_t)bufn * sizeof(u64), s, k, bufn, cand, cnt, cap,
+                       perm, topk, have, tau, flags, nflagged);
 }
 
 __global__ void k_topk_finalize(int nq, int k, int kout, int metric, const u64 *__restrict__ topk,

@@ -12,9 +12,9 @@ enum Metric : int {
     HAMMING_PACKED = 10  // internal: packed-bit codes (uint32 words), popcount distance
 };
 
-constexpr int kCap = 16384;          // candidate slots per query per round (default)
 constexpr int kMaxK = 2048;          // VHIP_MAX_K
-constexpr int kSortSlots = 4096;     // LDS sort buffer of the merge kernel (u64 keys)
+constexpr int kGemmSlotsReg = 48;    // LDS candidate slots per query and work item, register-fed MFMA kernel
+constexpr int kGemmSlotsStream = 14; // same, streaming MFMA kernel (D > 128)
 constexpr int kKChunk = 32;          // K (dimension) chunk of the MFMA tiles
 constexpr int kTileCols = 128;       // queries (or k-means points) per MFMA work item
 constexpr int kRowAlign = 256;       // row counts of MFMA row operands and round boundaries
@@ -47,13 +47,16 @@ inline size_t round_up(size_t a, size_t b) { return (a + b - 1) / b * b; }
 void launch_rows_prep(const float *in, size_t n, size_t n_out, int dim, int dpad, const uint32_t *perm, float *out,
                       float *norm, int norm_kind, int transform, int normalize, float pad_fill, hipStream_t s);
 // One round of the fused MFMA distance + threshold filter over base rows [row_begin, row_end)
-// (row_begin a multiple of 128, row_end a multiple of 128 or the padded end of the base).
-// `base` has its rows padded to a multiple of 128 with NaN rows; `qry` has nq rows padded to a
-// multiple of 128.  anorm_max / anorm_min: extremes of bnorm over the real rows.
-// grid_cap: number of workgroups of the persistent grid (resident capacity of the GPU).
-void launch_gemm_filter(int metric, const float *base, const float *bnorm, const float *qry, const float *qnorm,
-                        const float *tau, int nq, int dpad, long row_begin, long row_end, uint2 *cand, uint32_t *cnt,
-                        int cap, float anorm_max, float anorm_min, int grid_cap, hipStream_t s);
+// (row_begin a multiple of 256; rows past the real base are NaN padding up to a multiple of 256).
+// `base` has its rows padded to a multiple of 256 with NaN rows; `qry` has nq rows padded to a
+// multiple of 128.  anorm_max / anorm_min: extremes of bnorm over the real rows.  item_rows (a
+// multiple of 256): base rows per work item.  dense: write every score of rows < row_end to
+// cand[q * cap + (row - row_begin)] instead of filtering (needs row_end - row_begin <= cap; the
+// caller sets cnt).  grid_cap: number of workgroups of the persistent grid.
+void launch_gemm_filter(int metric, bool dense, long item_rows, const float *base, const float *bnorm,
+                        const float *qry, const float *qnorm, const float *tau, int nq, int dpad, long row_begin,
+                        long row_end, uint2 *cand, uint32_t *cnt, int cap, float anorm_max, float anorm_min,
+                        int grid_cap, hipStream_t s);
 
 // MFMA k-means assignment (knn_gemm.hip); metric L2 / DOT / COS.  `cent` has kpad rows
 // (a multiple of 128, NaN padding rows), `pts` n rows padded to a multiple of 128 (zeros).
