@@ -58,8 +58,8 @@ def cpu_model() -> str:
 # rocprofv3 counter summaries (FETCH_SIZE + WRITE_SIZE of the dominant kernel, scaled by a 1 GiB
 # copy) per workload; each holds a "traffic_bytes_per_launch:" line.
 PROFILES = {
-    "l2int": "k_mfma_res_filter__knn_l2_int_1000000x128_q10000_k100.txt",
-    "kmeans": "k_mfma_res_assign__kmeans_l2_2000000x96_k4096.txt",
+    "l2int": "k_mfma_reg_filter__knn_l2_int_1000000x128_q10000_k100.txt",
+    "kmeans": "k_mfma_reg_assign__kmeans_l2_2000000x96_k4096.txt",
     "cos768": "k_mfma_stream_filter__knn_cosine_1000000x768_q10000_k10.txt",
     "hamming": "k_hamming_filter__knn_hamming_packed256_10000000_q10000_k10.txt",
     "l1": "k_valu_filter__knn_l1_uniform_500000x128_q4096_k10.txt",
