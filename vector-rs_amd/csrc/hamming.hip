@@ -8,20 +8,22 @@
 // base codes are staged in LDS and read as broadcasts.  Distances are exact integers.  The
 // threshold test is batched over 4 rows (one wave-uniform branch per 4 rows) and the grid runs
 // 8 workgroups per CU, so tile loads of one workgroup hide behind the others' popcounts.
+#include <algorithm>
+
 #include "vh_common.h"
 
 namespace vh {
 
 constexpr int kHamRows = 128;
-constexpr long kHamItemRows = 8192;
+constexpr long kHamItemRowsMax = 8192;
 
 template <int W>
 __global__ __launch_bounds__(256) void k_hamming_filter(const uint32_t *__restrict__ codes,
                                                         const uint32_t *__restrict__ qry,
                                                         const float *__restrict__ tau, int nq, int wpad,
                                                         long row_begin, long row_end, int n_qtiles, int n_items,
-                                                        uint2 *__restrict__ cand, uint32_t *__restrict__ cnt,
-                                                        int cap) {
+                                                        long item_rows, uint2 *__restrict__ cand,
+                                                        uint32_t *__restrict__ cnt, int cap) {
     __shared__ uint32_t tile[kHamRows * W];
     const int tid = threadIdx.x;
     const int G = gridDim.x, g8 = G >> 3;
@@ -36,8 +38,8 @@ __global__ __launch_bounds__(256) void k_hamming_filter(const uint32_t *__restri
         const float tf = qv ? tau[q] : -1.0f;
         const uint32_t tq = tf < 0.0f ? 0u : (tf >= 4294967040.0f ? 0xffffffffu : (uint32_t)tf);
         const bool any = qv && tf >= 0.0f;
-        const long r_lo = row_begin + chunk * kHamItemRows;
-        const long r_hi = min(r_lo + kHamItemRows, row_end);
+        const long r_lo = row_begin + chunk * item_rows;
+        const long r_hi = min(r_lo + item_rows, row_end);
 
         uint32_t qw[W];
 #pragma unroll
@@ -96,16 +98,20 @@ void launch_hamming_filter(const uint32_t *codes, const uint32_t *qry, const flo
                            int grid_cap, hipStream_t s) {
     if (nq <= 0 || row_end <= row_begin) return;
     const int nqt = ceil_div(nq, 256);
-    const long n_chunks = (row_end - row_begin + kHamItemRows - 1) / kHamItemRows;
-    const long items = (long)nqt * n_chunks;
     const long resident = 4L * grid_cap;  // 8 workgroups per CU
+    // rows per work item: small rounds are cut finer so every resident workgroup gets work
+    const long rows = row_end - row_begin;
+    long item_rows = (rows * nqt + 2 * resident - 1) / (2 * resident);
+    item_rows = std::min(kHamItemRowsMax, std::max((long)kHamRows, (item_rows + kHamRows - 1) / kHamRows * kHamRows));
+    const long n_chunks = (rows + item_rows - 1) / item_rows;
+    const long items = (long)nqt * n_chunks;
     long grid = items < resident ? items : resident;
     grid = (grid + 7) / 8 * 8;
     const dim3 g((unsigned)grid), b(256);
     const int it = (int)items;
 #define VH_HAM(W)                                                                                              \
     hipLaunchKernelGGL(k_hamming_filter<W>, g, b, 0, s, codes, qry, tau, nq, wpad, row_begin, row_end, nqt, \
-                       it, cand, cnt, cap)
+                       it, item_rows, cand, cnt, cap)
     switch (wpad) {
         case 1: VH_HAM(1); break;
         case 2: VH_HAM(2); break;

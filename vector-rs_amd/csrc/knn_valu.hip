@@ -9,14 +9,16 @@
 // base element costs two VALU operations per query (sub + add/max with the |x| modifier).  Values
 // are computed in the direct form of the reference CPU engine (scalar.rs:81-263), so reported
 // distances follow it closely.
+#include <algorithm>
+
 #include "vh_common.h"
 
 namespace vh {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-constexpr int kValuRows = 16;          // base rows per LDS tile
-constexpr long kValuItemRows = 2048;   // base rows per work item
+constexpr int kValuRows = 16;             // base rows per LDS tile
+constexpr long kValuItemRowsMax = 2048;   // base rows per work item (large rounds)
 
 // k-means Hellinger: centroids are means of the raw data, so sqrt(|x|) of the centroid
 // side is taken in the loop (the point side holds sqrt(|p|)).
@@ -60,7 +62,7 @@ template <int M, int DC>
 __global__ __launch_bounds__(256) void k_valu_filter(const float *__restrict__ base,
                                                      const float *__restrict__ qry, const float *__restrict__ tau,
                                                      int nq, int dpad, long row_begin, long row_end, int n_qtiles,
-                                                     int n_items, uint2 *__restrict__ cand,
+                                                     int n_items, long item_rows, uint2 *__restrict__ cand,
                                                      uint32_t *__restrict__ cnt, int cap) {
     constexpr int V4 = DC / 4;
     __shared__ floatx4 tile[kValuRows * V4];
@@ -75,8 +77,8 @@ __global__ __launch_bounds__(256) void k_valu_filter(const float *__restrict__ b
         const int q = qtile * 256 + tid;
         const bool qv = q < nq;
         const float tq = qv ? tau[q] : -INFINITY;
-        const long r_lo = row_begin + chunk * kValuItemRows;
-        const long r_hi = min(r_lo + kValuItemRows, row_end);
+        const long r_lo = row_begin + chunk * item_rows;
+        const long r_hi = min(r_lo + item_rows, row_end);
 
         float qr[DC];
         auto load_q = [&](int c) {
@@ -130,14 +132,14 @@ __global__ __launch_bounds__(256) void k_valu_filter(const float *__restrict__ b
 
 template <int M>
 static void launch_m(int dpad, dim3 g, hipStream_t s, const float *base, const float *qry,
-                     const float *tau, int nq, long rb, long re, int nqt, int items, uint2 *cand, uint32_t *cnt,
-                     int cap) {
+                     const float *tau, int nq, long rb, long re, int nqt, int items, long item_rows, uint2 *cand,
+                     uint32_t *cnt, int cap) {
     if (dpad <= 128 && dpad > 64)
         hipLaunchKernelGGL((k_valu_filter<M, 128>), g, dim3(256), 0, s, base, qry, tau, nq, dpad, rb, re, nqt,
-                           items, cand, cnt, cap);
+                           items, item_rows, cand, cnt, cap);
     else
         hipLaunchKernelGGL((k_valu_filter<M, 64>), g, dim3(256), 0, s, base, qry, tau, nq, dpad, rb, re, nqt,
-                           items, cand, cnt, cap);
+                           items, item_rows, cand, cnt, cap);
 }
 
 void launch_valu_filter(int metric, const float *base, const float *qry, const float *tau,
@@ -146,20 +148,31 @@ void launch_valu_filter(int metric, const float *base, const float *qry, const f
     (void)dim;
     if (nq <= 0 || row_end <= row_begin) return;
     const int nqt = ceil_div(nq, 256);
-    const long n_chunks = (row_end - row_begin + kValuItemRows - 1) / kValuItemRows;
+    // rows per work item: small rounds are cut finer so that they still give every resident
+    // workgroup about four items
+    const long rows = row_end - row_begin;
+    long item_rows = (rows * nqt + 4L * grid_cap - 1) / (4L * grid_cap);
+    item_rows = std::min(kValuItemRowsMax, std::max(4L * kValuRows, (item_rows + kValuRows - 1) / kValuRows * kValuRows));
+    const long n_chunks = (rows + item_rows - 1) / item_rows;
     const long items = (long)nqt * n_chunks;
     long grid = items < grid_cap ? items : grid_cap;
     grid = (grid + 7) / 8 * 8;
     const dim3 g((unsigned)grid);
     const int it = (int)items;
     switch (metric) {
-        case L1: launch_m<L1>(dpad, g, s, base, qry, tau, nq, row_begin, row_end, nqt, it, cand, cnt, cap); break;
-        case MINK: launch_m<MINK>(dpad, g, s, base, qry, tau, nq, row_begin, row_end, nqt, it, cand, cnt, cap); break;
-        case LINF: launch_m<LINF>(dpad, g, s, base, qry, tau, nq, row_begin, row_end, nqt, it, cand, cnt, cap); break;
-        case HAMF: launch_m<HAMF>(dpad, g, s, base, qry, tau, nq, row_begin, row_end, nqt, it, cand, cnt, cap); break;
-        case MAHA: launch_m<MAHA>(dpad, g, s, base, qry, tau, nq, row_begin, row_end, nqt, it, cand, cnt, cap); break;
-        case JACC: launch_m<JACC>(dpad, g, s, base, qry, tau, nq, row_begin, row_end, nqt, it, cand, cnt, cap); break;
-        case HELL: launch_m<HELL>(dpad, g, s, base, qry, tau, nq, row_begin, row_end, nqt, it, cand, cnt, cap); break;
+        case L1: launch_m<L1>(dpad, g, s, base, qry, tau, nq, row_begin, row_end, nqt, it, item_rows, cand, cnt, cap); break;
+        case MINK: launch_m<MINK>(dpad, g, s, base, qry, tau, nq, row_begin, row_end, nqt, it, item_rows, cand,
+                                          cnt, cap); break;
+        case LINF: launch_m<LINF>(dpad, g, s, base, qry, tau, nq, row_begin, row_end, nqt, it, item_rows, cand,
+                                          cnt, cap); break;
+        case HAMF: launch_m<HAMF>(dpad, g, s, base, qry, tau, nq, row_begin, row_end, nqt, it, item_rows, cand,
+                                          cnt, cap); break;
+        case MAHA: launch_m<MAHA>(dpad, g, s, base, qry, tau, nq, row_begin, row_end, nqt, it, item_rows, cand,
+                                          cnt, cap); break;
+        case JACC: launch_m<JACC>(dpad, g, s, base, qry, tau, nq, row_begin, row_end, nqt, it, item_rows, cand,
+                                          cnt, cap); break;
+        case HELL: launch_m<HELL>(dpad, g, s, base, qry, tau, nq, row_begin, row_end, nqt, it, item_rows, cand,
+                                          cnt, cap); break;
         default: break;
     }
 }
