@@ -194,3 +194,16 @@ def test_empty_cluster_keeps_centroid(vh):
 def test_tolerance_stops_early(vh):
     r = vh.CudaKMeansEngine().fit(_three_clusters(), 4, 3, 50, 1e-4, init=_three_clusters()[[0, 50, 100]])
     assert r.iterations == 1  # centroids already at the cluster means
+
+
+@pytest.mark.parametrize("dim", [256, 200])
+def test_high_dimension_one_step(vh, oracle, dim):
+    """k-means assign above 128 dimensions: the panel kernel (256) and the streaming kernel (200)."""
+    from vector_hip import datasets as ds
+
+    data, _, _ = ds.gaussian_mixture(12_000, dim, 64, 13)
+    st = vh.KMeansState(data)
+    cent = data[:64].copy()
+    st.set_centroids(cent)
+    st.run(1)
+    _check_step(oracle, data, cent, st.read(), "l2")

@@ -259,3 +259,20 @@ def test_repeat_runs_bit_identical(vh):
     a = eng.search_batch_arrays(q, 32)
     b = eng.search_batch_arrays(q, 32)
     assert np.array_equal(a[0], b[0]) and np.array_equal(a[1], b[1])
+
+
+@pytest.mark.parametrize("dim", [256, 768, 200, 300])
+@pytest.mark.parametrize("metric", ["l2", "dot", "cosine"])
+def test_high_dimension_parity(vh, oracle, metric, dim):
+    """Dimensions above 128: multiples of 128 run the panel kernel (the 1M x 768 cosine
+    workload's shape), others the streaming kernel.  300 queries span three column tiles
+    and k = 100 makes the dense first round cover 2048 rows."""
+    from vector_hip import datasets as ds
+
+    base = ds.normalized(12_000, dim, 31) if metric == "cosine" else ds.gaussian(12_000, dim, 31)
+    q = ds.normalized(300, dim, 32) if metric == "cosine" else ds.gaussian(300, dim, 32)
+    for k in (10, 100):
+        ids, dist, lens = vh.CudaKnnEngine(base, dim, vh.DistanceMetric(oracle.METRICS[metric])
+                                           ).search_batch_arrays(q, k)
+        assert np.all(lens == k)
+        check_knn(oracle, base, q, ids, dist, k, metric, rtol=1e-4, atol=1e-5)

@@ -73,7 +73,7 @@ static std::vector<Round> plan_rounds(size_t n, size_t k, bool gemm, int dpad) {
     const size_t kk = std::max<size_t>(k, 1);
     const size_t b0 = std::min(n, round_up(std::max<size_t>(256, 20 * kk), kRowAlign));
     r.push_back({0, (long)b0, gemm, (long)kRowAlign});
-    const int slots = dpad <= 128 ? kGemmSlotsReg : kGemmSlotsStream;
+    const int slots = gemm_slots(dpad);
     size_t seen = b0;
     while (seen < n) {
         const size_t e = std::min(n, round_up(seen * 8, kRowAlign));

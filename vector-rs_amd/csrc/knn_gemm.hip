@@ -18,9 +18,12 @@
 //  * k_mfma_reg (dpad <= 128): a workgroup of 8 waves owns a work item of 128 columns whose
 //    128 x dpad tile stays resident in LDS; each wave streams its own 64 rows of A straight from
 //    L2 into registers one K-chunk (32 floats) ahead, so waves need no barrier inside an item.
-//  * k_mfma_stream (dpad > 128): a workgroup of 4 waves streams 128-row x 128-column stages of
-//    both operands through double-buffered LDS in K-chunks (32 flop per byte), two workgroups
-//    per CU.
+//  * k_mfma_pnl (dpad a multiple of 128 above 128): the same per-wave register feed of A; the
+//    column tile passes through double-buffered LDS in K-panels of 128 floats, copied by
+//    global_load_lds one panel ahead, with one barrier per panel.
+//  * k_mfma_stream (other dpad > 128): a workgroup of 4 waves streams 128-row x 128-column
+//    stages of both operands through double-buffered LDS in K-chunks (32 flop per byte), two
+//    workgroups per CU.
 // Each wave owns a 64 x 64 sub-tile of 2 x 2 v_mfma_f32_32x32x2f32 blocks.  LDS tiles are
 // swizzled for gfx950's LDS (64 banks; a ds_read_b128 serves 16 lanes per pass): within 16
 // consecutive rows, row parity selects the 128-byte half of the banks and (row >> 1) & 7 XORs
@@ -43,6 +46,7 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr int kFilter = 0, kAssign = 1, kDense = 2;
 constexpr int kRegSlots = kGemmSlotsReg;     // LDS candidate slots per query per work item (register-fed kernel)
+constexpr int kPnlSlots = kGemmSlotsPanel;   // same for the panel kernel
 constexpr int kStrSlots = kGemmSlotsStream;  // same for the streaming kernel (two workgroups share a CU's LDS)
 
 // float4 index of (row, c4) in a 32-float-wide swizzled tile
@@ -722,6 +726,171 @@ __global__ __launch_bounds__(512, 1) void k_mfma_reg(ScanArgs a) {
     }
 }
 
+// =========================================================================================
+// Panel kernel (dpad a multiple of 128, e.g. 768): 8 waves, 256-row stages.  As in k_mfma_reg
+// every wave streams its own 64 rows of A from L2 into registers one K-chunk ahead.  The
+// 128-column tile is too large to stay resident, so it passes through LDS in K-panels of 128
+// floats (64 KB): while panel p is multiplied, panel p+1 -- of this stage, the next stage or
+// the next work item -- is copied from global memory straight into the other LDS buffer by
+// global_load_lds (no VGPRs), and one barrier per panel hands the buffers over.
+// =========================================================================================
+template <int MODE, int M>
+__global__ __launch_bounds__(512, 1) void k_mfma_pnl(ScanArgs a) {
+    constexpr int RW = 4, TR = 256;
+    __shared__ floatx4 sB[2][kTileCols * 32];
+    __shared__ floatx4 sN[2][TR / 4];  // row epilogue values (norms) of the current / next stage
+    __shared__ uint32_t s_qcnt[MODE == kFilter ? kTileCols : 1];
+    __shared__ uint2 s_slot[MODE == kFilter ? kTileCols * kPnlSlots : 1];
+    __shared__ float s_xs[MODE == kAssign ? (RW - 1) * kTileCols : 1];
+    __shared__ int s_xi[MODE == kAssign ? (RW - 1) * kTileCols : 1];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wr = wave & 3, wc = wave >> 2;
+    const int l32 = lane & 31, h = lane >> 5;
+    const int G = gridDim.x;
+    const int D = a.dpad, NK = D / kKChunk, NP = NK / 4;
+    int item = first_item();
+    if (item >= a.n_items) return;
+
+    // swizzled panel layout (row r, chunk kc of the panel, 16-byte slot c4), as k_mfma_reg with NK = 4
+    auto bidx = [](int r, int kc, int c4) { return r * 32 + (kc ^ (r & 1)) * 8 + (c4 ^ ((r >> 1) & 7)); };
+    // Panel p of the column tile at c0 into buffer b.  Instruction i of wave w fills LDS slots
+    // [512 i + 64 w, + 64); each lane fetches the 16 bytes the swizzle puts in its slot.
+    // Slot f = 512 i + tid holds row r = 16 i + (tid >> 5); its chunk and slot depend on tid only
+    // (r & 1 = (tid >> 5) & 1, (r >> 1) & 7 = (tid >> 6) & 7), so one lane address plus a stride
+    // of 16 rows serves all eight instructions.
+    const int dr = tid >> 5, drem = tid & 31;
+    const int dkc = (drem >> 3) ^ (dr & 1), dc4 = (drem & 7) ^ ((tid >> 6) & 7);
+    const long dstride = 16L * D;
+    auto dma_panel = [&](int b, int c0, int p) {
+        const float *src = a.B + (long)(c0 + dr) * D + 128 * p + 32 * dkc + 4 * dc4;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            __builtin_amdgcn_global_load_lds((const void *)(src + i * dstride),
+                                             (__attribute__((address_space(3))) void *)&sB[b][512 * i + 64 * wave],
+                                             16, 0, 0);
+    };
+    // row epilogue values of the stage at row rs into norm buffer b (wave 0: 64 lanes x 16 bytes)
+    auto dma_norms = [&](int b, long rs) {
+        if (wave == 0)
+            __builtin_amdgcn_global_load_lds((const void *)(a.anorm + rs + 4 * lane),
+                                             (__attribute__((address_space(3))) void *)&sN[b][0], 16, 0, 0);
+    };
+    auto load_a = [&](floatx4 (&r)[8], long rs, int kc) {
+        const float *p0 = a.A + (rs + 64 * wr + l32) * (long)D + 32 * kc + 4 * h;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            r[g] = *(const floatx4 *)(p0 + 8 * g);
+            r[4 + g] = *(const floatx4 *)(p0 + 32 * (long)D + 8 * g);
+        }
+    };
+
+    int col0;
+    long r_lo, r_hi;
+    decode_item(a, item, col0, r_lo, r_hi);
+    int pb = 0, sb = 0;
+    dma_panel(0, col0, 0);
+    dma_norms(0, r_lo);
+    if constexpr (MODE == kFilter) {
+        if (tid < kTileCols) s_qcnt[tid] = 0;
+    }
+    long rs = r_lo;
+    EpiState st;
+    item_begin<MODE, M>(st, a, col0, wc, l32);
+    floatx4 cur[8];
+    load_a(cur, rs, 0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+
+    for (;;) {
+        long nrs = rs + TR;
+        int nitem = item, ncol0 = col0;
+        long nlo = r_lo, nhi = r_hi;
+        const bool item_end = nrs >= r_hi;
+        bool more = true;
+        if (item_end) {
+            nitem = item + G;
+            more = nitem < a.n_items;
+            if (more) {
+                decode_item(a, nitem, ncol0, nlo, nhi);
+                nrs = nlo;
+            }
+        }
+        floatx16 acc[2][2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) acc[i][j] = floatx16{0};
+
+        for (int p = 0; p < NP; ++p) {
+            // the panel after this one goes into the other buffer (free: every wave passed the
+            // barrier that ended its last use)
+            if (p + 1 < NP) {
+                dma_panel(pb ^ 1, col0, p + 1);
+            } else if (more) {
+                dma_panel(pb ^ 1, ncol0, 0);
+                dma_norms(sb ^ 1, nrs);
+            }
+            const bool last_p = p + 1 == NP;
+#pragma unroll
+            for (int kc = 0; kc < 4; ++kc) {
+                floatx4 nxt[8];
+                const bool last = last_p && kc == 3;
+                if (!last) load_a(nxt, rs, 4 * p + kc + 1);
+                else if (more) load_a(nxt, nrs, 0);
+                __builtin_amdgcn_sched_barrier(0);
+                const int rb0 = 64 * wc + l32, rb1 = rb0 + 32;
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int c4 = 2 * g + h;
+                    const floatx4 a0 = cur[g], a1 = cur[4 + g];
+                    const floatx4 b0 = sB[pb][bidx(rb0, kc, c4)];
+                    const floatx4 b1 = sB[pb][bidx(rb1, kc, c4)];
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[t], b0[t], acc[0][0], 0, 0, 0);
+                        acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[t], b1[t], acc[0][1], 0, 0, 0);
+                        acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[t], b0[t], acc[1][0], 0, 0, 0);
+                        acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[t], b1[t], acc[1][1], 0, 0, 0);
+                    }
+                }
+                if (!last || more) {
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) cur[i] = nxt[i];
+                }
+            }
+            // this wave's share of the next panel has landed; after the barrier every wave's has,
+            // and nobody reads buffer pb any more
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+            pb ^= 1;
+        }
+
+        const float *nrow = (const float *)&sN[sb][0];
+        auto nf = [&](int rb, int g) { return *(const floatx4 *)(nrow + 64 * wr + 32 * rb + 8 * g + 4 * h); };
+        if constexpr (MODE == kFilter) {
+            filter_stage<M, kPnlSlots>(acc, nf, st, a, wr, wc, l32, h, rs, r_lo, col0, s_qcnt, s_slot);
+            if (item_end) filter_flush<kPnlSlots>(a, col0, r_lo, s_qcnt, s_slot);
+        } else if constexpr (MODE == kDense) {
+            dense_stage<M>(acc, nf, st, a, wr, wc, l32, h, rs, col0);
+        } else {
+            assign_stage<M>(acc, nf, st, wr, h, rs);
+            if (item_end) assign_finish<M, RW>(st, a, col0, wr, wc, l32, h, s_xs, s_xi);
+        }
+
+        if (!more) break;
+        if (item_end) {
+            item = nitem;
+            col0 = ncol0;
+            r_lo = nlo;
+            r_hi = nhi;
+            item_begin<MODE, M>(st, a, col0, wc, l32);
+        }
+        rs = nrs;
+        sb ^= 1;
+    }
+}
+
 // ---- launch ----------------------------------------------------------------------------
 static int grid_for(long n_items, int cap) {
     long g = n_items < cap ? n_items : cap;
@@ -742,6 +911,9 @@ static void launch_scan(const ScanArgs &a, int grid_cap, hipStream_t s) {
             case 3: hipLaunchKernelGGL((k_mfma_reg<MODE, M, 3>), g, b, 0, s, a); break;
             default: hipLaunchKernelGGL((k_mfma_reg<MODE, M, 4>), g, b, 0, s, a); break;
         }
+    } else if (nk % 4 == 0) {
+        const dim3 g(grid_for(a.n_items, cus)), b(512);
+        hipLaunchKernelGGL((k_mfma_pnl<MODE, M>), g, b, 0, s, a);
     } else {
         const dim3 g(grid_for(a.n_items, 2 * cus)), b(256);
         hipLaunchKernelGGL((k_mfma_stream<MODE, M>), g, b, 0, s, a);

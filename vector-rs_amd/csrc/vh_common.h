@@ -14,7 +14,12 @@ enum Metric : int {
 
 constexpr int kMaxK = 2048;          // VHIP_MAX_K
 constexpr int kGemmSlotsReg = 48;    // LDS candidate slots per query and work item, register-fed MFMA kernel
-constexpr int kGemmSlotsStream = 14; // same, streaming MFMA kernel (D > 128)
+constexpr int kGemmSlotsPanel = 24;  // same, panel MFMA kernel (dpad a multiple of 128 above 128)
+constexpr int kGemmSlotsStream = 14; // same, streaming MFMA kernel (other dpad > 128)
+// LDS candidate slots of the MFMA filter kernel that serves rows of dpad floats
+inline int gemm_slots(int dpad) {
+    return dpad <= 128 ? kGemmSlotsReg : (dpad % 128 == 0 ? kGemmSlotsPanel : kGemmSlotsStream);
+}
 constexpr int kKChunk = 32;          // K (dimension) chunk of the MFMA tiles
 constexpr int kTileCols = 128;       // queries (or k-means points) per MFMA work item
 constexpr int kRowAlign = 256;       // row counts of MFMA row operands and round boundaries
