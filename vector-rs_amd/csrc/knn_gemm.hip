@@ -15,9 +15,11 @@
 // comparison; B's row count is padded to a multiple of 128.  The inner loop has no bounds checks.
 //
 // Two kernels share the epilogues:
-//  * k_mfma_reg (dpad <= 128): a workgroup of 8 waves owns a work item of 128 columns whose
-//    128 x dpad tile stays resident in LDS; each wave streams its own 64 rows of A straight from
-//    L2 into registers one K-chunk (32 floats) ahead, so waves need no barrier inside an item.
+//  * k_mfma_hs (dpad <= 128): a workgroup of 8 waves owns a work item of 128 columns whose
+//    128 x dpad tile stays resident in LDS; each wave streams its own rows of A straight from
+//    L2 into registers one step ahead, so waves need no barrier inside an item, and computes its
+//    64 x 64 tile in two 32-row halves so that the epilogue of one half runs under the MFMAs of
+//    the other.
 //  * k_mfma_pnl (dpad a multiple of 128 above 128): the same per-wave register feed of A; the
 //    column tile passes through double-buffered LDS in K-panels of 128 floats, copied by
 //    global_load_lds one panel ahead, with one barrier per panel.
@@ -574,160 +576,7 @@ __global__ __launch_bounds__(256, 2) void k_mfma_stream(ScanArgs a) {
 }
 
 // =========================================================================================
-// Register-fed kernel: 8 waves, 256-row stages, NK K-chunks (dpad = 32 NK <= 128).  The
-// 128-column tile stays resident in LDS for a work item, as in k_mfma_res, but every wave loads
-// its own 64 rows of A straight from L2 into registers, one K-chunk ahead, so there is no barrier
-// inside an item: the waves of a SIMD drift apart and one wave's epilogue runs under the other
-// wave's MFMAs.  Barriers remain only at item boundaries (candidate flush / argmin combine and
-// the column-tile reload).
-// =========================================================================================
-template <int MODE, int M, int NK>
-__global__ __launch_bounds__(512, 1) void k_mfma_reg(ScanArgs a) {
-    constexpr int RW = 4, TR = 256, D = 32 * NK;
-    __shared__ floatx4 sB[kTileCols * 8 * NK];
-    __shared__ uint32_t s_qcnt[MODE == kFilter ? kTileCols : 1];
-    __shared__ uint2 s_slot[MODE == kFilter ? kTileCols * kRegSlots : 1];
-    __shared__ float s_xs[MODE == kAssign ? (RW - 1) * kTileCols : 1];
-    __shared__ int s_xi[MODE == kAssign ? (RW - 1) * kTileCols : 1];
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wr = wave & 3, wc = wave >> 2;
-    const int l32 = lane & 31, h = lane >> 5;
-    const int G = gridDim.x;
-    int item = first_item();
-    if (item >= a.n_items) return;
-
-    auto bidx_kc = [](int r, int kc, int c4) {
-        const int pch = (NK % 2 == 0) ? (kc ^ (r & 1)) : kc;
-        return r * (8 * NK) + pch * 8 + (c4 ^ ((r >> 1) & 7));
-    };
-    // Column tile: 128 rows of D floats, 2 NK float4 per thread.
-    auto fill_b = [&](int c0) {
-        floatx4 rq[2 * NK];
-#pragma unroll
-        for (int i = 0; i < 2 * NK; ++i) {
-            const int f = tid + 512 * i;
-            const int r = f / (8 * NK), rem = f % (8 * NK);
-            rq[i] = *(const floatx4 *)(a.B + (long)(c0 + r) * D + 4 * rem);
-        }
-#pragma unroll
-        for (int i = 0; i < 2 * NK; ++i) {
-            const int f = tid + 512 * i;
-            const int r = f / (8 * NK), rem = f % (8 * NK);
-            sB[bidx_kc(r, rem >> 3, rem & 7)] = rq[i];
-        }
-    };
-    // A chunk kc of the stage at row rs: lane (l32, h) holds rows 64 wr + l32 (+32) at floats
-    // 32 kc + 8 g + 4 h .. + 3 (g = 0..3), the operand layout mfma_chunk expects.
-    auto load_a = [&](floatx4 (&r)[8], long rs, int kc) {
-        const float *p0 = a.A + (rs + 64 * wr + l32) * (long)D + 32 * kc + 4 * h;
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            r[g] = *(const floatx4 *)(p0 + 8 * g);
-            r[4 + g] = *(const floatx4 *)(p0 + 32 * D + 8 * g);
-        }
-    };
-
-    int col0;
-    long r_lo, r_hi;
-    decode_item(a, item, col0, r_lo, r_hi);
-    fill_b(col0);
-    if constexpr (MODE == kFilter) {
-        if (tid < kTileCols) s_qcnt[tid] = 0;
-    }
-    long rs = r_lo;
-    EpiState st;
-    item_begin<MODE, M>(st, a, col0, wc, l32);
-    floatx4 cur[8];
-    load_a(cur, rs, 0);
-    __syncthreads();
-
-    for (;;) {
-        long nrs = rs + TR;
-        int nitem = item, ncol0 = col0;
-        long nlo = r_lo, nhi = r_hi;
-        const bool item_end = nrs >= r_hi;
-        bool more = true;
-        if (item_end) {
-            nitem = item + G;
-            more = nitem < a.n_items;
-            if (more) {
-                decode_item(a, nitem, ncol0, nlo, nhi);
-                nrs = nlo;
-            }
-        }
-        floatx4 nv[8];  // row epilogue values of this stage (rows 64 wr + 32 rb + 8 g + 4 h .. + 3)
-        floatx16 acc[2][2];
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int j = 0; j < 2; ++j) acc[i][j] = floatx16{0};
-
-#pragma unroll
-        for (int kc = 0; kc < NK; ++kc) {
-            floatx4 nxt[8];
-            const bool last = kc + 1 == NK;
-            if (!last) load_a(nxt, rs, kc + 1);
-            else if (more) load_a(nxt, nrs, 0);
-            if (last) {
-#pragma unroll
-                for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-                    for (int g = 0; g < 4; ++g)
-                        nv[4 * rb + g] = *(const floatx4 *)(a.anorm + rs + 64 * wr + 32 * rb + 8 * g + 4 * h);
-            }
-            // keep the loads above the MFMAs: the scheduler would otherwise sink them next to
-            // their first use and expose the L2 latency
-            __builtin_amdgcn_sched_barrier(0);
-            const int rb0 = 64 * wc + l32, rb1 = rb0 + 32;
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int c4 = 2 * g + h;
-                const floatx4 a0 = cur[g], a1 = cur[4 + g];
-                const floatx4 b0 = sB[bidx_kc(rb0, kc, c4)];
-                const floatx4 b1 = sB[bidx_kc(rb1, kc, c4)];
-#pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[t], b0[t], acc[0][0], 0, 0, 0);
-                    acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[t], b1[t], acc[0][1], 0, 0, 0);
-                    acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[t], b0[t], acc[1][0], 0, 0, 0);
-                    acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[t], b1[t], acc[1][1], 0, 0, 0);
-                }
-            }
-            if (!last || more) {
-#pragma unroll
-                for (int i = 0; i < 8; ++i) cur[i] = nxt[i];
-            }
-        }
-
-        auto nf = [&](int rb, int g) { return nv[4 * rb + g]; };
-        if constexpr (MODE == kFilter) {
-            filter_stage<M, kRegSlots>(acc, nf, st, a, wr, wc, l32, h, rs, r_lo, col0, s_qcnt, s_slot);
-            if (item_end) filter_flush<kRegSlots>(a, col0, r_lo, s_qcnt, s_slot);
-        } else if constexpr (MODE == kDense) {
-            dense_stage<M>(acc, nf, st, a, wr, wc, l32, h, rs, col0);
-        } else {
-            assign_stage<M>(acc, nf, st, wr, h, rs);
-            if (item_end) assign_finish<M, RW>(st, a, col0, wr, wc, l32, h, s_xs, s_xi);
-        }
-
-        if (!more) break;
-        if (item_end) {
-            // every wave is past this item's MFMAs (barrier in the flush / combine above)
-            fill_b(ncol0);
-            __syncthreads();
-            item = nitem;
-            col0 = ncol0;
-            r_lo = nlo;
-            r_hi = nhi;
-            item_begin<MODE, M>(st, a, col0, wc, l32);
-        }
-        rs = nrs;
-    }
-}
-
-// =========================================================================================
-// Panel kernel (dpad a multiple of 128, e.g. 768): 8 waves, 256-row stages.  As in k_mfma_reg
+// Panel kernel (dpad a multiple of 128, e.g. 768): 8 waves, 256-row stages.  As in k_mfma_hs
 // every wave streams its own 64 rows of A from L2 into registers one K-chunk ahead.  The
 // 128-column tile is too large to stay resident, so it passes through LDS in K-panels of 128
 // floats (64 KB): while panel p is multiplied, panel p+1 -- of this stage, the next stage or
@@ -752,7 +601,7 @@ __global__ __launch_bounds__(512, 1) void k_mfma_pnl(ScanArgs a) {
     int item = first_item();
     if (item >= a.n_items) return;
 
-    // swizzled panel layout (row r, chunk kc of the panel, 16-byte slot c4), as k_mfma_reg with NK = 4
+    // swizzled panel layout (row r, chunk kc of the panel, 16-byte slot c4), as k_mfma_hs with NK = 4
     auto bidx = [](int r, int kc, int c4) { return r * 32 + (kc ^ (r & 1)) * 8 + (c4 ^ ((r >> 1) & 7)); };
     // Panel p of the column tile at c0 into buffer b.  Instruction i of wave w fills LDS slots
     // [512 i + 64 w, + 64); each lane fetches the 16 bytes the swizzle puts in its slot.
@@ -891,6 +740,314 @@ __global__ __launch_bounds__(512, 1) void k_mfma_pnl(ScanArgs a) {
     }
 }
 
+// =========================================================================================
+// Half-staged register-fed kernel (dpad <= 128).  The 128-column tile of a work item stays in
+// LDS; every wave loads its own rows of A from L2 into registers one step (half x K-chunk)
+// ahead, and computes its 64 x 64 tile in two halves of 32 rows: while the MFMAs of one half
+// run, the wave evaluates the epilogue of the other half (the previous stage's second half, or
+// this stage's first half).  Both halves live in the same accumulator registers as before, so
+// the epilogue's VALU work hides in the MFMA shadow without extra registers, and the two waves
+// of a SIMD never sit in their epilogues while the matrix pipe idles.  There is no barrier inside
+// a work item; barriers remain at item boundaries (candidate flush / argmin combine and the
+// column-tile reload).
+// =========================================================================================
+
+// Epilogue pieces of one half.  acc2[cb] register 4g+j holds row rb0 + 8g + j (rb0 = the half's
+// first row in this lane's layout, i.e. rs + 64 wr + 32 hf + 4 h) and column 64wc + 32cb + l32.
+template <int M, int SLOTS>
+__device__ __forceinline__ void filter_group(const floatx16 (&acc2)[2], floatx4 n4, const EpiState &st,
+                                             const ScanArgs &a, int wc, int l32, uint32_t row_g, long r_lo,
+                                             int col0, uint32_t *s_qcnt, uint2 *s_slot, int g, bool enable) {
+    bool p[4][2];
+    bool any = false;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) {
+            const float dot = acc2[cb][4 * g + j];
+            if constexpr (M == L2) p[j][cb] = fmaf(-2.0f, dot, n4[j]) <= st.T[cb];
+            else p[j][cb] = dot >= st.T[cb];
+            any = any || p[j][cb];
+        }
+    if (M == COS && st.guard) {
+        // a (query, row) pair with ||q|| ||x|| <= 1e-9 has similarity 0 (knn.cu:168-173)
+        any = false;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb) {
+                const float dot = acc2[cb][4 * g + j];
+                const float sc = st.cn[cb] * n4[j] > 1e-9f ? -dot : 0.0f * dot;
+                p[j][cb] = sc <= st.tau_e[cb];
+                any = any || p[j][cb];
+            }
+    }
+    if (__builtin_amdgcn_ballot_w64(any && enable)) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb) {
+                if (!p[j][cb]) continue;
+                const float dot = acc2[cb][4 * g + j];
+                float sc;
+                if constexpr (M == L2) {
+                    sc = fmaxf(fmaf(-2.0f, dot, st.cn[cb] + n4[j]), 0.0f);
+                    if (!(sc <= st.tau_e[cb])) continue;
+                } else if constexpr (M == DOT) {
+                    sc = canon(-dot);
+                } else {
+                    sc = st.guard ? (st.cn[cb] * n4[j] > 1e-9f ? canon(-dot) : 0.0f) : canon(-dot);
+                }
+                append_candidate<SLOTS>(a, 64 * wc + 32 * cb + l32, score_key(sc), row_g + j, r_lo, col0, s_qcnt,
+                                        s_slot);
+            }
+    }
+}
+
+template <int M>
+__device__ __forceinline__ void dense_group(const floatx16 (&acc2)[2], floatx4 n4, const EpiState &st,
+                                            const ScanArgs &a, int wc, int l32, long row, int col0, int g) {
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) {
+        const int q = col0 + 64 * wc + 32 * cb + l32;
+        if (q >= a.ncols) continue;
+        uint2 *dst = a.cand + (size_t)q * a.cap;
+        uint32_t key[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float dot = acc2[cb][4 * g + j];
+            float sc;
+            if constexpr (M == L2) sc = fmaxf(fmaf(-2.0f, dot, st.cn[cb] + n4[j]), 0.0f);
+            else if constexpr (M == DOT) sc = canon(-dot);
+            else sc = st.cn[cb] * n4[j] > 1e-9f ? canon(-dot) : 0.0f;
+            key[j] = score_key(sc);
+        }
+        const uint32_t p0 = (uint32_t)(row - a.row_begin);
+        if (row + 3 < a.row_end) {
+            *(uint4 *)(dst + p0) = make_uint4(key[0], (uint32_t)row, key[1], (uint32_t)row + 1);
+            *(uint4 *)(dst + p0 + 2) = make_uint4(key[2], (uint32_t)row + 2, key[3], (uint32_t)row + 3);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (row + j < a.row_end) dst[p0 + j] = make_uint2(key[j], (uint32_t)(row + j));
+        }
+    }
+}
+
+// ASSIGN for one half: per column, the minimum over the half's 16 rows held by the lane, then
+// the first (lowest) row reaching it; halves and stages are visited in ascending row order with
+// a strict '<', so the lowest index wins ties (kmeans.cu:110-114).
+template <int M>
+__device__ __forceinline__ void assign_half(floatx16 (&acc2)[2], const floatx4 (&n)[4], EpiState &st, long rb0) {
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) {
+        float m = INFINITY;
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float dot = acc2[cb][4 * g + j];
+                float u;
+                if constexpr (M == L2) {
+                    u = fmaf(-2.0f, dot, n[g][j]);
+                } else if constexpr (M == DOT) {
+                    u = -dot;
+                } else {
+                    const float den = st.cn[cb] * n[g][j];
+                    u = den > 1e-9f ? -(dot / den) : canon(0.0f * dot);
+                }
+                acc2[cb][4 * g + j] = u;
+                m = fminf(m, u);
+            }
+        if (m < st.bs[cb]) {
+            int idx = 15;
+#pragma unroll
+            for (int r = 15; r >= 0; --r) idx = acc2[cb][r] == m ? r : idx;
+            st.bs[cb] = m;
+            st.bi[cb] = (int)rb0 + 8 * (idx >> 2) + (idx & 3);
+        }
+    }
+}
+
+template <int MODE, int M, int NK>
+__global__ __launch_bounds__(512, 1) void k_mfma_hs(ScanArgs a) {
+    constexpr int RW = 4, TR = 256, D = 32 * NK;
+    __shared__ floatx4 sB[kTileCols * 8 * NK];
+    __shared__ uint32_t s_qcnt[MODE == kFilter ? kTileCols : 1];
+    __shared__ uint2 s_slot[MODE == kFilter ? kTileCols * kRegSlots : 1];
+    __shared__ float s_xs[MODE == kAssign ? (RW - 1) * kTileCols : 1];
+    __shared__ int s_xi[MODE == kAssign ? (RW - 1) * kTileCols : 1];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wr = wave & 3, wc = wave >> 2;
+    const int l32 = lane & 31, h = lane >> 5;
+    const int G = gridDim.x;
+    int item = first_item();
+    if (item >= a.n_items) return;
+
+    auto bidx_kc = [](int r, int kc, int c4) {
+        const int pch = (NK % 2 == 0) ? (kc ^ (r & 1)) : kc;
+        return r * (8 * NK) + pch * 8 + (c4 ^ ((r >> 1) & 7));
+    };
+    auto fill_b = [&](int c0) {
+        floatx4 rq[2 * NK];
+#pragma unroll
+        for (int i = 0; i < 2 * NK; ++i) {
+            const int f = tid + 512 * i;
+            const int r = f / (8 * NK), rem = f % (8 * NK);
+            rq[i] = *(const floatx4 *)(a.B + (long)(c0 + r) * D + 4 * rem);
+        }
+#pragma unroll
+        for (int i = 0; i < 2 * NK; ++i) {
+            const int f = tid + 512 * i;
+            const int r = f / (8 * NK), rem = f % (8 * NK);
+            sB[bidx_kc(r, rem >> 3, rem & 7)] = rq[i];
+        }
+    };
+    // A of half hf, chunk kc of the stage at rs: row rs + 64 wr + 32 hf + l32, floats 32 kc + 8 g + 4 h.
+    auto load_a = [&](floatx4 (&r)[4], long rs, int hf, int kc) {
+        const float *p0 = a.A + (rs + 64 * wr + 32 * hf + l32) * (long)D + 32 * kc + 4 * h;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) r[g] = *(const floatx4 *)(p0 + 8 * g);
+    };
+    auto load_n = [&](floatx4 (&n)[4], long rs, int hf) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) n[g] = *(const floatx4 *)(a.anorm + rs + 64 * wr + 32 * hf + 8 * g + 4 * h);
+    };
+    auto mfma_step = [&](floatx16 (&ac)[2], const floatx4 (&ra)[4], int kc) {
+        const int rb0 = 64 * wc + l32, rb1 = rb0 + 32;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int c4 = 2 * g + h;
+            const floatx4 b0 = sB[bidx_kc(rb0, kc, c4)];
+            const floatx4 b1 = sB[bidx_kc(rb1, kc, c4)];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                ac[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(ra[g][t], b0[t], ac[0], 0, 0, 0);
+                ac[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(ra[g][t], b1[t], ac[1], 0, 0, 0);
+            }
+        }
+    };
+
+    int col0;
+    long r_lo, r_hi;
+    decode_item(a, item, col0, r_lo, r_hi);
+    fill_b(col0);
+    if constexpr (MODE == kFilter) {
+        if (tid < kTileCols) s_qcnt[tid] = 0;
+    }
+    long rs = r_lo;
+    EpiState st;
+    item_begin<MODE, M>(st, a, col0, wc, l32);
+    floatx4 cur[4];
+    load_a(cur, rs, 0, 0);
+    __syncthreads();
+
+    floatx16 acc[2][2];  // acc[half][cb]
+    floatx4 nrm[2][4];   // epilogue values of each half's rows
+    bool prev = false;   // the previous stage's second half is still to be evaluated
+
+    // Epilogue of half hf of the stage at srs, groups [g0, g1); `enable` false makes it a no-op
+    // (FILTER folds it into the wave-uniform branch, so the MFMAs and the threshold tests stay in
+    // one basic block and the scheduler can interleave them).
+    auto epi = [&](floatx16 (&ac)[2], const floatx4 (&n)[4], long srs, int hf, int g0, int g1, bool enable) {
+        if constexpr (MODE == kAssign) {
+            if (g0 == 0 && enable) assign_half<M>(ac, n, st, srs + 64 * wr + 32 * hf + 4 * h);
+        } else {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                if (g < g0 || g >= g1) continue;
+                if constexpr (MODE == kFilter) {
+                    filter_group<M, kRegSlots>(ac, n[g], st, a, wc, l32,
+                                               (uint32_t)(srs - r_lo) + 64 * wr + 32 * hf + 8 * g + 4 * h, r_lo,
+                                               col0, s_qcnt, s_slot, g, enable);
+                } else if (enable) {
+                    dense_group<M>(ac, n[g], st, a, wc, l32, srs + 64 * wr + 32 * hf + 8 * g + 4 * h, col0, g);
+                }
+            }
+        }
+    };
+    // Interleave the step's MFMAs with the epilogue's VALU work: 1 MFMA, then up to 2 VALU.
+    auto interleave = [&]() {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+        }
+    };
+
+    for (;;) {
+        long nrs = rs + TR;
+        int nitem = item, ncol0 = col0;
+        long nlo = r_lo, nhi = r_hi;
+        const bool item_end = nrs >= r_hi;
+        bool more = true;
+        if (item_end) {
+            nitem = item + G;
+            more = nitem < a.n_items;
+            if (more) {
+                decode_item(a, nitem, ncol0, nlo, nhi);
+                nrs = nlo;
+            }
+        }
+        // ---- half 0: MFMAs into acc[0]; epilogue of the previous stage's half 1 ----
+        load_n(nrm[0], rs, 0);
+        acc[0][0] = floatx16{0};
+        acc[0][1] = floatx16{0};
+#pragma unroll
+        for (int kc = 0; kc < NK; ++kc) {
+            floatx4 nxt[4];
+            if (kc + 1 < NK) load_a(nxt, rs, 0, kc + 1);
+            else load_a(nxt, rs, 1, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            mfma_step(acc[0], cur, kc);
+            epi(acc[1], nrm[1], rs - TR, 1, (4 * kc) / NK, (4 * (kc + 1)) / NK, prev);
+            interleave();
+#pragma unroll
+            for (int i = 0; i < 4; ++i) cur[i] = nxt[i];
+        }
+        // ---- half 1: MFMAs into acc[1]; epilogue of this stage's half 0 ----
+        load_n(nrm[1], rs, 1);
+        acc[1][0] = floatx16{0};
+        acc[1][1] = floatx16{0};
+#pragma unroll
+        for (int kc = 0; kc < NK; ++kc) {
+            floatx4 nxt[4];
+            const bool last = kc + 1 == NK;
+            if (!last) load_a(nxt, rs, 1, kc + 1);
+            else if (more) load_a(nxt, nrs, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            mfma_step(acc[1], cur, kc);
+            epi(acc[0], nrm[0], rs, 0, (4 * kc) / NK, (4 * (kc + 1)) / NK, true);
+            interleave();
+            if (!last || more) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) cur[i] = nxt[i];
+            }
+        }
+        prev = true;
+        if (item_end) {
+            // drain: this stage's half 1, then the item's cross-wave work
+            epi(acc[1], nrm[1], rs, 1, 0, 4, true);
+            if constexpr (MODE == kFilter) filter_flush<kRegSlots>(a, col0, r_lo, s_qcnt, s_slot);
+            else if constexpr (MODE == kAssign) assign_finish<M, RW>(st, a, col0, wr, wc, l32, h, s_xs, s_xi);
+            if (!more) break;
+            // every wave is past this item's MFMAs (barrier in the flush / combine above; DENSE
+            // has none, so take one here)
+            if constexpr (MODE == kDense) __syncthreads();
+            fill_b(ncol0);
+            __syncthreads();
+            item = nitem;
+            col0 = ncol0;
+            r_lo = nlo;
+            r_hi = nhi;
+            item_begin<MODE, M>(st, a, col0, wc, l32);
+            prev = false;
+        }
+        rs = nrs;
+    }
+}
+
 // ---- launch ----------------------------------------------------------------------------
 static int grid_for(long n_items, int cap) {
     long g = n_items < cap ? n_items : cap;
@@ -906,10 +1063,10 @@ static void launch_scan(const ScanArgs &a, int grid_cap, hipStream_t s) {
     if (nk <= 4) {
         const dim3 g(grid_for(a.n_items, cus)), b(512);
         switch (nk) {
-            case 1: hipLaunchKernelGGL((k_mfma_reg<MODE, M, 1>), g, b, 0, s, a); break;
-            case 2: hipLaunchKernelGGL((k_mfma_reg<MODE, M, 2>), g, b, 0, s, a); break;
-            case 3: hipLaunchKernelGGL((k_mfma_reg<MODE, M, 3>), g, b, 0, s, a); break;
-            default: hipLaunchKernelGGL((k_mfma_reg<MODE, M, 4>), g, b, 0, s, a); break;
+            case 1: hipLaunchKernelGGL((k_mfma_hs<MODE, M, 1>), g, b, 0, s, a); break;
+            case 2: hipLaunchKernelGGL((k_mfma_hs<MODE, M, 2>), g, b, 0, s, a); break;
+            case 3: hipLaunchKernelGGL((k_mfma_hs<MODE, M, 3>), g, b, 0, s, a); break;
+            default: hipLaunchKernelGGL((k_mfma_hs<MODE, M, 4>), g, b, 0, s, a); break;
         }
     } else if (nk % 4 == 0) {
         const dim3 g(grid_for(a.n_items, cus)), b(512);
