@@ -186,6 +186,60 @@ int vhip_kmeans_profile_read(vhip_kmeans *km, double *kernel_ms, uint64_t *launc
                              double *bytes);
 void vhip_kmeans_destroy(vhip_kmeans *km);
 
+/* One assignment step without the centroid update: every point's nearest centroid (as
+ * KMeans::find_nearest_centroid, ivf/kmeans.rs:262-309, lowest index on ties), the metric value
+ * of that pair in the reference's direct form (squared L2, dot, cosine similarity, ...; NULL to
+ * skip) and the residual point - centroid (n x dim, NULL to skip) as IvfPqIndex::build forms it
+ * (ivf/mod.rs:119-132).  No reference counterpart as one call: it replaces that serial loop. */
+int vhip_kmeans_assign_only(vhip_kmeans *km, int32_t *out_assign, float *out_score, float *out_residual);
+
+/* ---- IVF coarse quantizer: IvfPqIndex build + search front end (ivf/mod.rs:106-133, 270-283) ---- */
+typedef struct vhip_coarse vhip_coarse;
+/* Holds nlist x dim coarse centroids (KMeans::fit output) on GPU `ordinal`. */
+int vhip_coarse_create(const float *centroids, size_t nlist, size_t dim, int metric, int ordinal,
+                       vhip_coarse **out);
+/* KMeans::find_nearest_centroid (ivf/kmeans.rs:262-309) for n row-major points: cluster index,
+ * its metric value (similarity for dot / cosine) and, if out_residual is not NULL, the residual
+ * point - centroid (n x dim) of the IVF-PQ build loop (ivf/mod.rs:119-132).  Host buffers. */
+int vhip_coarse_assign(vhip_coarse *q, const float *points, size_t n, uint32_t *out_cluster, float *out_score,
+                       float *out_residual);
+/* KMeans::find_top_centroids (ivf/kmeans.rs:311-356) for nq queries: min(nprobe, nlist)
+ * (index, score) pairs per query, best first, ties in ascending index order; same output
+ * contract as vhip_knn_search_batch (row stride nprobe). */
+int vhip_coarse_probe(vhip_coarse *q, const float *queries, size_t nq, size_t nprobe, uint32_t *out_ids,
+                      float *out_scores, size_t *out_len);
+size_t vhip_coarse_nlist(const vhip_coarse *q);
+size_t vhip_coarse_dimension(const vhip_coarse *q);
+void vhip_coarse_destroy(vhip_coarse *q);
+
+/* ---- files of the offline trainer ------------------------------------------------ */
+/* MmapStorage::create_from_flat (storage/mmap.rs:128-160): VECRSTOR file (u64 magic
+ * 0x5645435253544F52, u64 n, u64 dim, n x dim f32, little-endian). */
+int vhip_vecrstor_write(const char *path, const float *data, size_t n, size_t dim);
+/* MmapStorage::open (storage/mmap.rs:171-224): validates magic and size, returns n and dim. */
+int vhip_vecrstor_open(const char *path, size_t *n, size_t *dim);
+/* Copies the n x dim vectors of a VECRSTOR file (n, dim as vhip_vecrstor_open reported). */
+int vhip_vecrstor_read(const char *path, float *out, size_t n, size_t dim);
+/* IvfPqSerializer::save_centroid_file (ivf/serializer.rs:264-306): VRSKMEAN file (u64 magic
+ * 0x5652534B4D45414E, u32 version 1, u8 metric, u32 dim, u32 k, u32 iterations, f32 inertia,
+ * k x dim f32, little-endian). */
+int vhip_centroid_file_save(const char *path, const float *centroids, size_t dim, size_t k, int metric,
+                            size_t iterations, float inertia);
+/* IvfPqSerializer::load_centroid_file (ivf/serializer.rs:309-360), header part: validates magic,
+ * version and metric code.  Any output pointer may be NULL. */
+int vhip_centroid_file_info(const char *path, size_t *dim, size_t *k, int *metric, size_t *iterations,
+                            float *inertia);
+/* ... and the k x dim centroid data (k, dim as vhip_centroid_file_info reported). */
+int vhip_centroid_file_load(const char *path, float *centroids, size_t k, size_t dim);
+/* vector-mpi fit_cuda_aware (src/distributed_kmeans.rs:375-415) as mpi_kmeans --use-cuda runs it
+ * (src/bin/mpi_kmeans.rs:284-364): loads data_dir/shard_0.bin, shard_1.bin, ... (VECRSTOR,
+ * until the first missing index), fits k-means on GPU 0 (seeded k-means++ init) and writes the
+ * VRSKMEAN file data_dir/output.  num_gpus is accepted as fit_cuda_aware does (max(1); more GPUs
+ * than present fall back to the emulator there, to the one GPU here).  num_shards (may be NULL)
+ * receives the number of shard files read. */
+int vhip_train_from_shards(const char *data_dir, size_t k, size_t max_iters, float tol, int metric, size_t num_gpus,
+                           const char *output, uint64_t seed, vhip_kmeans_result *result, size_t *num_shards);
+
 /* ---- device memory helpers (for callers without a framework) ------------------- */
 int vhip_malloc(int ordinal, size_t bytes, void **ptr);
 int vhip_free(int ordinal, void *ptr);

@@ -140,14 +140,15 @@ __global__ __launch_bounds__(256) void k_update_sums(const float *__restrict__ p
 #pragma unroll
             for (int u = 0; u < kUpdUnroll; ++u) {
                 const int i = b + j + u;
-                if (i >= s1) break;
-                while (i >= next) {  // offsets[k] = n > i, so c stays below k
-                    flush(c);
-                    ++c;
-                    next = offsets[c + 1];
-                }
+                if (i < s1) {
+                    while (i >= next) {  // offsets[k] = n > i, so c stays below k
+                        flush(c);
+                        ++c;
+                        next = offsets[c + 1];
+                    }
 #pragma unroll
-                for (int s = 0; s < S; ++s) acc[s] += llrint((double)v[u][s] * scale);
+                    for (int s = 0; s < S; ++s) acc[s] += llrint((double)v[u][s] * scale);
+                }
             }
         }
     }
@@ -211,6 +212,83 @@ __global__ void k_sum_partial(const float *__restrict__ v, size_t count, size_t 
         __syncthreads();
     }
     if (threadIdx.x == 0) partial[blockIdx.x] = red[0];
+}
+
+// Direct-form metric of each point and its assigned centroid, and optionally the residual
+// x - c: the value KMeans::find_nearest_centroid returns (ivf/kmeans.rs:262-309: the engine's
+// squared L2, dot product, cosine similarity, ... with the formulas of scalar.rs:14-263) and the
+// residual IvfPqIndex::build computes for PQ training (ivf/mod.rs:119-132).  One wave per point:
+// a lane-strided sum over the dimensions and a fixed xor butterfly (max for Chebyshev).
+__global__ __launch_bounds__(256) void k_coarse_score(const float *__restrict__ pts, int dpad, int dim, int n,
+                                                      const float *__restrict__ cent,
+                                                      const int32_t *__restrict__ assign, int metric,
+                                                      float *__restrict__ score, float *__restrict__ resid) {
+    const int lane = threadIdx.x & 63;
+    const size_t wave = (blockIdx.x * (size_t)blockDim.x + threadIdx.x) >> 6;
+    const size_t nwaves = (gridDim.x * (size_t)blockDim.x) >> 6;
+    for (size_t p = wave; p < (size_t)n; p += nwaves) {
+        const float *x = pts + p * (size_t)dpad;
+        const float *c = cent + (size_t)assign[p] * dpad;
+        float a = 0.0f, b = 0.0f, e = 0.0f;
+        for (int d = lane; d < dim; d += 64) {
+            const float xv = x[d], cv = c[d];
+            if (resid) resid[p * (size_t)dim + d] = xv - cv;
+            switch (metric) {
+                case DOT: a = fmaf(xv, cv, a); break;
+                case COS:
+                    a = fmaf(xv, cv, a);
+                    b = fmaf(xv, xv, b);
+                    e = fmaf(cv, cv, e);
+                    break;
+                case L1: a += fabsf(xv - cv); break;
+                case MINK: {
+                    const float t = fabsf(xv - cv);
+                    a = fmaf(t * t, t, a);
+                    break;
+                }
+                case LINF: a = fmaxf(a, fabsf(xv - cv)); break;
+                case HAMF: a += fabsf(xv - cv) > 1e-6f ? 1.0f : 0.0f; break;
+                case JACC: {
+                    const float ax = fabsf(xv), ac = fabsf(cv);
+                    a += fminf(ax, ac);
+                    b += fmaxf(ax, ac);
+                    break;
+                }
+                case HELL: {
+                    const float t = sqrtf(fabsf(xv)) - sqrtf(fabsf(cv));
+                    a = fmaf(t, t, a);
+                    break;
+                }
+                default: {  // L2, MAHA
+                    const float t = xv - cv;
+                    a = fmaf(t, t, a);
+                }
+            }
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const float oa = __shfl_xor(a, o, 64);
+            a = metric == LINF ? fmaxf(a, oa) : a + oa;
+            b += __shfl_xor(b, o, 64);
+            e += __shfl_xor(e, o, 64);
+        }
+        if (lane == 0) {
+            float v;
+            switch (metric) {
+                case COS: {
+                    const float den = sqrtf(b) * sqrtf(e);
+                    v = den <= 1e-9f ? 0.0f : a / den;
+                    break;
+                }
+                case MINK: v = cbrtf(a); break;
+                case MAHA: v = sqrtf(a); break;
+                case JACC: v = b <= 1e-9f ? 0.0f : 1.0f - a / b; break;
+                case HELL: v = sqrtf(0.5f * a); break;
+                default: v = a;
+            }
+            score[p] = v;
+        }
+    }
 }
 
 // k-means++ step (CudaKMeansEngine::init_random, kmeans.rs:424-436): mind[i] =
@@ -491,7 +569,6 @@ int vhip_kmeans_create(int ordinal, const float *data, size_t n, size_t dim, int
 int vhip_kmeans_set_centroids(vhip_kmeans *K, const float *centroids, size_t k) {
     clear_error();
     if (!K || !centroids || k == 0) return set_error(VHIP_ERR_INVALID_CONFIG, "null state / centroids or k == 0");
-    if (k > K->n) return set_error(VHIP_ERR_INVALID_CONFIG, "k exceeds the number of points");
     std::lock_guard<std::mutex> lock(K->mu);
     VH_CHECK(open_device(K->dev));
     DevBuf raw;
@@ -510,6 +587,41 @@ int vhip_kmeans_run(vhip_kmeans *K, size_t iters) {
     for (size_t i = 0; i < iters; ++i) VH_CHECK(km_iterate(K));
     VH_HIP(hipStreamSynchronize(K->stream));
     K->timer.collect();
+    return VHIP_OK;
+}
+
+int vhip_kmeans_assign_only(vhip_kmeans *K, int32_t *out_assign, float *out_score, float *out_residual) {
+    clear_error();
+    if (!K || K->k == 0) return set_error(VHIP_ERR_INVALID_CONFIG, "centroids not set");
+    std::lock_guard<std::mutex> lock(K->mu);
+    VH_CHECK(open_device(K->dev));
+    hipStream_t s = K->stream;
+    const int n = (int)K->n, k = (int)K->k;
+    launch_fill_u32(K->counts.as<uint32_t>(), k, 0u, s);
+    if (is_gemm_metric(K->metric))
+        launch_kmeans_assign(K->metric, K->cent.as<float>(), K->cnorm.as<float>(), (int)K->kpad, K->pts.as<float>(),
+                             K->pnorm.as<float>(), n, (int)K->dpad, K->assign.as<int32_t>(), K->inertia.as<float>(),
+                             K->pos.as<int32_t>(), K->counts.as<int32_t>(), K->grid_cap, s);
+    else
+        launch_kmeans_assign_valu(K->metric, K->cent.as<float>(), k, K->pts.as<float>(), n, (int)K->dpad,
+                                  K->assign.as<int32_t>(), K->inertia.as<float>(), K->pos.as<int32_t>(),
+                                  K->counts.as<int32_t>(), K->grid_cap, s);
+    VH_HIP(hipGetLastError());
+    DevBuf score, resid;
+    if (out_score || out_residual) {
+        VH_CHECK(score.ensure(K->dev, K->n * sizeof(float)));
+        if (out_residual) VH_CHECK(resid.ensure(K->dev, K->n * K->dim * sizeof(float)));
+        const size_t blocks = std::min<size_t>(65536, (K->n + 3) / 4);
+        hipLaunchKernelGGL(k_coarse_score, dim3((unsigned)blocks), dim3(256), 0, s, K->pts.as<float>(), (int)K->dpad,
+                           (int)K->dim, n, K->cent.as<float>(), K->assign.as<int32_t>(), K->metric,
+                           score.as<float>(), out_residual ? resid.as<float>() : nullptr);
+        VH_HIP(hipGetLastError());
+    }
+    if (out_assign) VH_CHECK(K->stager.d2h(out_assign, K->assign.p, K->n * sizeof(int32_t), s));
+    if (out_score) VH_CHECK(K->stager.d2h(out_score, score.p, K->n * sizeof(float), s));
+    if (out_residual) VH_CHECK(K->stager.d2h(out_residual, resid.p, K->n * K->dim * sizeof(float), s));
+    VH_HIP(hipStreamSynchronize(s));
+    K->assigned = false;  // counts / centroids describe no update
     return VHIP_OK;
 }
 

@@ -1,0 +1,303 @@
+// storage.cpp -- the file formats around the k-means trainer, and the trainer itself.
+//
+//  * VECRSTOR vector files: MmapStorage (vector-index/src/storage/mmap.rs:9-16, 90-224):
+//      u64 magic 0x56454352_53544F52 ("VECRSTOR"), u64 n, u64 dim, then n x dim f32, all
+//      little-endian.  open() validates the magic and that the file holds the declared data.
+//  * VRSKMEAN centroid files: IvfPqSerializer::save/load_centroid_file
+//      (vector-index/src/ivf/serializer.rs:264-360, 374-377): u64 magic 0x5652534B_4D45414E,
+//      u32 version 1, u8 metric code, u32 dim, u32 k, u32 iterations, f32 inertia, then k x dim
+//      f32, little-endian, no padding (29-byte header).
+//  * Offline trainer: vector-mpi fit_cuda_aware (src/distributed_kmeans.rs:375-415) reached from
+//      mpi_kmeans --use-cuda (src/bin/mpi_kmeans.rs:284-364): load data_dir/shard_0.bin,
+//      shard_1.bin, ... (until the first missing index), fit k-means on the GPU, write the
+//      centroid file data_dir/output.
+// Host code only: it reads and writes files and calls the GPU k-means through the C ABI.
+#include <algorithm>
+#include <cerrno>
+#include <cstdio>
+#include <cstring>
+#include <memory>
+#include <string>
+#include <sys/stat.h>
+#include <vector>
+
+#include "vector_hip.h"
+#include "vh_error.h"
+
+namespace {
+
+constexpr uint64_t kVecMagic = 0x5645435253544F52ull;
+constexpr uint64_t kCentroidMagic = 0x5652534B4D45414Eull;
+constexpr uint32_t kCentroidVersion = 1;
+constexpr size_t kVecHeader = 24;
+constexpr size_t kCentroidHeader = 29;
+
+struct File {
+    FILE *f = nullptr;
+    explicit File(FILE *p) : f(p) {}
+    ~File() {
+        if (f) fclose(f);
+    }
+};
+
+// Little-endian encode / decode (the formats are LE regardless of the host).
+void put_u64(unsigned char *p, uint64_t v) {
+    for (int i = 0; i < 8; ++i) p[i] = (unsigned char)(v >> (8 * i));
+}
+void put_u32(unsigned char *p, uint32_t v) {
+    for (int i = 0; i < 4; ++i) p[i] = (unsigned char)(v >> (8 * i));
+}
+uint64_t get_u64(const unsigned char *p) {
+    uint64_t v = 0;
+    for (int i = 7; i >= 0; --i) v = (v << 8) | p[i];
+    return v;
+}
+uint32_t get_u32(const unsigned char *p) {
+    uint32_t v = 0;
+    for (int i = 3; i >= 0; --i) v = (v << 8) | p[i];
+    return v;
+}
+bool host_is_le() {
+    const uint32_t one = 1;
+    unsigned char b;
+    std::memcpy(&b, &one, 1);
+    return b == 1;
+}
+
+// Writes / reads count floats in little-endian order.
+bool write_f32(FILE *f, const float *v, size_t count) {
+    if (host_is_le()) return fwrite(v, sizeof(float), count, f) == count;
+    unsigned char b[4];
+    for (size_t i = 0; i < count; ++i) {
+        uint32_t u;
+        std::memcpy(&u, &v[i], 4);
+        put_u32(b, u);
+        if (fwrite(b, 1, 4, f) != 4) return false;
+    }
+    return true;
+}
+bool read_f32(FILE *f, float *v, size_t count) {
+    if (fread(v, sizeof(float), count, f) != count) return false;
+    if (!host_is_le()) {
+        for (size_t i = 0; i < count; ++i) {
+            unsigned char b[4];
+            std::memcpy(b, &v[i], 4);
+            const uint32_t u = get_u32(b);
+            std::memcpy(&v[i], &u, 4);
+        }
+    }
+    return true;
+}
+
+int io_error(const std::string &what, const char *path) {
+    return vh::set_error(VHIP_ERR_INVALID_CONFIG, what + " '" + path + "': " + std::strerror(errno));
+}
+
+long long file_size(const char *path) {
+    struct stat st;
+    if (stat(path, &st) != 0) return -1;
+    return (long long)st.st_size;
+}
+
+// MmapStorage::open validation (mmap.rs:171-224).
+int vec_header(const char *path, size_t *n, size_t *dim) {
+    const long long size = file_size(path);
+    if (size < 0) return io_error("cannot open vector file", path);
+    if (size < (long long)kVecHeader)
+        return vh::set_error(VHIP_ERR_INVALID_CONFIG, std::string("invalid header in '") + path +
+                                                          "': file too small: " + std::to_string(size) +
+                                                          " bytes (minimum 24)");
+    File f(fopen(path, "rb"));
+    if (!f.f) return io_error("cannot open vector file", path);
+    unsigned char h[kVecHeader];
+    if (fread(h, 1, kVecHeader, f.f) != kVecHeader) return io_error("cannot read vector file header", path);
+    const uint64_t magic = get_u64(h);
+    if (magic != kVecMagic) {
+        char msg[160];
+        snprintf(msg, sizeof msg, "invalid magic number: 0x%016llX (expected 0x%016llX)", (unsigned long long)magic,
+                 (unsigned long long)kVecMagic);
+        return vh::set_error(VHIP_ERR_INVALID_CONFIG, std::string("invalid header in '") + path + "': " + msg);
+    }
+    const uint64_t nv = get_u64(h + 8), d = get_u64(h + 16);
+    if (d != 0 && nv > (uint64_t)(size) / 4 / d + 1)
+        return vh::set_error(VHIP_ERR_INVALID_CONFIG, std::string("file size mismatch in '") + path + "'");
+    const unsigned long long need = kVecHeader + (unsigned long long)nv * d * 4ull;
+    if ((unsigned long long)size < need)
+        return vh::set_error(VHIP_ERR_INVALID_CONFIG, std::string("file size mismatch in '") + path +
+                                                          "': expected " + std::to_string(need) + " bytes, got " +
+                                                          std::to_string(size));
+    *n = (size_t)nv;
+    *dim = (size_t)d;
+    return VHIP_OK;
+}
+
+int centroid_header(FILE *f, const char *path, size_t *dim, size_t *k, int *metric, size_t *iters, float *inertia) {
+    unsigned char h[kCentroidHeader];
+    if (fread(h, 1, kCentroidHeader, f) != kCentroidHeader)
+        return vh::set_error(VHIP_ERR_INVALID_CONFIG, std::string("truncated centroid file '") + path + "'");
+    const uint64_t magic = get_u64(h);
+    if (magic != kCentroidMagic) {
+        char msg[160];
+        snprintf(msg, sizeof msg, "expected centroid magic 0x%llX, got 0x%llX", (unsigned long long)kCentroidMagic,
+                 (unsigned long long)magic);
+        return vh::set_error(VHIP_ERR_INVALID_CONFIG, std::string("invalid header in '") + path + "': " + msg);
+    }
+    const uint32_t version = get_u32(h + 8);
+    if (version != kCentroidVersion)
+        return vh::set_error(VHIP_ERR_INVALID_CONFIG, std::string("invalid header in '") + path +
+                                                          "': unsupported centroid file version: " +
+                                                          std::to_string(version));
+    const unsigned code = h[12];
+    if (code > 9)
+        return vh::set_error(VHIP_ERR_INVALID_CONFIG, std::string("invalid header in '") + path +
+                                                          "': unknown metric code " + std::to_string(code));
+    uint32_t ib = get_u32(h + 25);
+    float in;
+    std::memcpy(&in, &ib, 4);
+    if (dim) *dim = get_u32(h + 13);
+    if (k) *k = get_u32(h + 17);
+    if (metric) *metric = (int)code;
+    if (iters) *iters = get_u32(h + 21);
+    if (inertia) *inertia = in;
+    return VHIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int vhip_vecrstor_write(const char *path, const float *data, size_t n, size_t dim) {
+    vh::clear_error();
+    if (!path || (n * dim > 0 && !data)) return vh::set_error(VHIP_ERR_INVALID_CONFIG, "null path or data");
+    File f(fopen(path, "wb"));
+    if (!f.f) return io_error("cannot create vector file", path);
+    unsigned char h[kVecHeader];
+    put_u64(h, kVecMagic);
+    put_u64(h + 8, (uint64_t)n);
+    put_u64(h + 16, (uint64_t)dim);
+    if (fwrite(h, 1, kVecHeader, f.f) != kVecHeader || !write_f32(f.f, data, n * dim))
+        return io_error("cannot write vector file", path);
+    if (fflush(f.f) != 0) return io_error("cannot write vector file", path);
+    return VHIP_OK;
+}
+
+int vhip_vecrstor_open(const char *path, size_t *n, size_t *dim) {
+    vh::clear_error();
+    if (!path || !n || !dim) return vh::set_error(VHIP_ERR_INVALID_CONFIG, "null argument");
+    return vec_header(path, n, dim);
+}
+
+int vhip_vecrstor_read(const char *path, float *out, size_t n, size_t dim) {
+    vh::clear_error();
+    if (!path || (n * dim > 0 && !out)) return vh::set_error(VHIP_ERR_INVALID_CONFIG, "null argument");
+    size_t fn = 0, fd = 0;
+    const int rc = vec_header(path, &fn, &fd);
+    if (rc != VHIP_OK) return rc;
+    if (fn != n || fd != dim)
+        return vh::set_error(VHIP_ERR_INVALID_CONFIG, std::string("'") + path + "' holds " + std::to_string(fn) +
+                                                          " x " + std::to_string(fd) + " vectors, not " +
+                                                          std::to_string(n) + " x " + std::to_string(dim));
+    File f(fopen(path, "rb"));
+    if (!f.f) return io_error("cannot open vector file", path);
+    if (fseek(f.f, (long)kVecHeader, SEEK_SET) != 0 || !read_f32(f.f, out, n * dim))
+        return io_error("cannot read vector file", path);
+    return VHIP_OK;
+}
+
+int vhip_centroid_file_save(const char *path, const float *centroids, size_t dim, size_t k, int metric,
+                            size_t iterations, float inertia) {
+    vh::clear_error();
+    if (!path || (k * dim > 0 && !centroids)) return vh::set_error(VHIP_ERR_INVALID_CONFIG, "null argument");
+    if (metric < 0 || metric > 9) return vh::set_error(VHIP_ERR_INVALID_CONFIG, "unknown metric code");
+    if (dim > 0xffffffffull || k > 0xffffffffull || iterations > 0xffffffffull)
+        return vh::set_error(VHIP_ERR_INVALID_CONFIG, "dimension, k and iterations are stored as u32");
+    File f(fopen(path, "wb"));
+    if (!f.f) return io_error("cannot create centroid file", path);
+    unsigned char h[kCentroidHeader];
+    put_u64(h, kCentroidMagic);
+    put_u32(h + 8, kCentroidVersion);
+    h[12] = (unsigned char)metric;
+    put_u32(h + 13, (uint32_t)dim);
+    put_u32(h + 17, (uint32_t)k);
+    put_u32(h + 21, (uint32_t)iterations);
+    uint32_t ib;
+    std::memcpy(&ib, &inertia, 4);
+    put_u32(h + 25, ib);
+    if (fwrite(h, 1, kCentroidHeader, f.f) != kCentroidHeader || !write_f32(f.f, centroids, k * dim))
+        return io_error("cannot write centroid file", path);
+    if (fflush(f.f) != 0) return io_error("cannot write centroid file", path);
+    return VHIP_OK;
+}
+
+int vhip_centroid_file_info(const char *path, size_t *dim, size_t *k, int *metric, size_t *iterations,
+                            float *inertia) {
+    vh::clear_error();
+    if (!path) return vh::set_error(VHIP_ERR_INVALID_CONFIG, "null path");
+    File f(fopen(path, "rb"));
+    if (!f.f) return io_error("cannot open centroid file", path);
+    return centroid_header(f.f, path, dim, k, metric, iterations, inertia);
+}
+
+int vhip_centroid_file_load(const char *path, float *centroids, size_t k, size_t dim) {
+    vh::clear_error();
+    if (!path || (k * dim > 0 && !centroids)) return vh::set_error(VHIP_ERR_INVALID_CONFIG, "null argument");
+    File f(fopen(path, "rb"));
+    if (!f.f) return io_error("cannot open centroid file", path);
+    size_t fd = 0, fk = 0;
+    const int rc = centroid_header(f.f, path, &fd, &fk, nullptr, nullptr, nullptr);
+    if (rc != VHIP_OK) return rc;
+    if (fd != dim || fk != k)
+        return vh::set_error(VHIP_ERR_INVALID_CONFIG, std::string("'") + path + "' holds " + std::to_string(fk) +
+                                                          " x " + std::to_string(fd) + " centroids, not " +
+                                                          std::to_string(k) + " x " + std::to_string(dim));
+    if (!read_f32(f.f, centroids, k * dim))
+        return vh::set_error(VHIP_ERR_INVALID_CONFIG, std::string("truncated centroid file '") + path + "'");
+    return VHIP_OK;
+}
+
+int vhip_train_from_shards(const char *data_dir, size_t k, size_t max_iters, float tol, int metric, size_t num_gpus,
+                           const char *output, uint64_t seed, vhip_kmeans_result *result, size_t *num_shards) {
+    vh::clear_error();
+    if (!data_dir || !output || !result) return vh::set_error(VHIP_ERR_INVALID_CONFIG, "null argument");
+    *result = vhip_kmeans_result{0, 0, 0, 0.0f};
+    if (num_shards) *num_shards = 0;
+    // fit_cuda_aware takes num_gpus.max(1) and, when more GPUs are requested than exist, runs
+    // the DDP engine's emulator (distributed_kmeans.rs:385-392); here one GPU runs every request.
+    (void)num_gpus;
+    std::vector<std::string> shards;
+    for (size_t i = 0;; ++i) {
+        std::string p = std::string(data_dir) + "/shard_" + std::to_string(i) + ".bin";
+        if (file_size(p.c_str()) < 0) break;
+        shards.push_back(p);
+    }
+    if (shards.empty())
+        return vh::set_error(VHIP_ERR_INVALID_CONFIG, std::string("no shard files (shard_0.bin, shard_1.bin, ...) "
+                                                                  "found in ") + data_dir);
+    std::vector<float> all;
+    size_t dim = 0;
+    for (const std::string &p : shards) {
+        size_t n = 0, d = 0;
+        int rc = vhip_vecrstor_open(p.c_str(), &n, &d);
+        if (rc != VHIP_OK) return rc;
+        if (dim == 0) dim = d;
+        else if (d != dim) return vh::set_error(VHIP_ERR_INVALID_CONFIG, "dimension mismatch across shard files");
+        const size_t off = all.size();
+        all.resize(off + n * d);
+        rc = vhip_vecrstor_read(p.c_str(), all.data() + off, n, d);
+        if (rc != VHIP_OK) return rc;
+    }
+    if (dim == 0) return vh::set_error(VHIP_ERR_INVALID_CONFIG, "shard files hold zero-dimensional vectors");
+    const size_t n = all.size() / dim;
+    std::vector<float> cent(std::min(k, n) * dim);
+    int rc = vhip_kmeans_fit(0, all.data(), n, dim, k, max_iters, tol, metric, nullptr, VHIP_INIT_KMEANSPP, seed,
+                             cent.data(), nullptr, result);
+    if (rc != VHIP_OK) return rc;
+    const std::string out = std::string(data_dir) + "/" + output;
+    rc = vhip_centroid_file_save(out.c_str(), cent.data(), result->dimension, result->k, metric, result->iterations,
+                                 result->inertia);
+    if (rc != VHIP_OK) return rc;
+    if (num_shards) *num_shards = shards.size();
+    return VHIP_OK;
+}
+
+}  // extern "C"

@@ -13,13 +13,10 @@
 
 #include "vector_hip.h"
 #include "vh_common.h"
+#include "vh_error.h"
 
 namespace vh {
 
-// ---- error state (thread local, like the Result<_, CudaError> of each call) ----
-int set_error(int code, const std::string &msg);
-void set_insufficient(size_t requested, size_t available);
-void clear_error();
 
 #define VH_HIP(expr)                                                                              \
     do {                                                                                          \

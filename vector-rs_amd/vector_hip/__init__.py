@@ -104,6 +104,21 @@ if _HAS_KMEANS:
     _sig("vhip_kmeans_profile", _int, _vp, _int)
     _sig("vhip_kmeans_profile_read", _int, _vp, _dblp, _u64p, _dblp, _dblp)
     _sig("vhip_kmeans_destroy", None, _vp)
+    _sig("vhip_kmeans_assign_only", _int, _vp, _i32p, _f32p, _f32p)
+    _sig("vhip_coarse_create", _int, _f32p, _sz, _sz, _int, _int, ctypes.POINTER(_vp))
+    _sig("vhip_coarse_assign", _int, _vp, _f32p, _sz, _u32p, _f32p, _f32p)
+    _sig("vhip_coarse_probe", _int, _vp, _f32p, _sz, _sz, _u32p, _f32p, _szp)
+    _sig("vhip_coarse_nlist", _sz, _vp)
+    _sig("vhip_coarse_dimension", _sz, _vp)
+    _sig("vhip_coarse_destroy", None, _vp)
+    _sig("vhip_train_from_shards", _int, ctypes.c_char_p, _sz, _sz, ctypes.c_float, _int, _sz, ctypes.c_char_p,
+         ctypes.c_uint64, ctypes.POINTER(_KMeansResultC), _szp)
+_sig("vhip_vecrstor_write", _int, ctypes.c_char_p, _f32p, _sz, _sz)
+_sig("vhip_vecrstor_open", _int, ctypes.c_char_p, _szp, _szp)
+_sig("vhip_vecrstor_read", _int, ctypes.c_char_p, _f32p, _sz, _sz)
+_sig("vhip_centroid_file_save", _int, ctypes.c_char_p, _f32p, _sz, _sz, _int, _sz, ctypes.c_float)
+_sig("vhip_centroid_file_info", _int, ctypes.c_char_p, _szp, _szp, ctypes.POINTER(_int), _szp, _f32p)
+_sig("vhip_centroid_file_load", _int, ctypes.c_char_p, _f32p, _sz, _sz)
 
 
 # ---- errors: CudaError (error.rs:7-29) ---------------------------------------------------
@@ -563,6 +578,17 @@ class KMeansState(_Profiled):
     def run(self, iters: int = 1):
         _check(_lib.vhip_kmeans_run(self._h, iters))
 
+    def assign_only(self, residuals: bool = False):
+        """Nearest centroid of every point without an update: (assign int32[n], score f32[n],
+        residual f32[n, d] or None).  Scores are the metric values KMeans::find_nearest_centroid
+        returns (ivf/kmeans.rs:262-309)."""
+        a = np.empty(self._n, np.int32)
+        sc = np.empty(self._n, np.float32)
+        r = np.empty((self._n, self._d), np.float32) if residuals else None
+        _check(_lib.vhip_kmeans_assign_only(self._h, _p(a, _i32p), _p(sc, _f32p),
+                                            _p(r, _f32p) if r is not None else None))
+        return a, sc, r
+
     def read(self) -> dict:
         c = np.empty((self._k, self._d), np.float32)
         a = np.empty(self._n, np.int32)
@@ -574,6 +600,174 @@ class KMeansState(_Profiled):
                                      _p(ms, _f32p), _p(ine, _f32p)))
         return {"centroids": c, "assign": a, "counts": cnt, "shifts": sh, "max_shift": float(ms[0]),
                 "inertia": float(ine[0])}
+
+
+# ---- IVF coarse quantizer (ivf/mod.rs:106-133, ivf/kmeans.rs:262-356) -------------------
+class IvfCoarseQuantizer:
+    """The coarse stage of IvfPqIndex on the GPU: find_nearest_centroid for every vector of a
+    build (plus the residuals x - c of the PQ stage) and find_top_centroids for query batches."""
+
+    def __init__(self, centroids, dimension: int, metric=DistanceMetric.L2Squared, ordinal: int = 0):
+        c = _rows(centroids, dimension)
+        self._nlist, self._d = c.shape
+        self.metric = DistanceMetric(int(metric))
+        h = _vp()
+        _check(_lib.vhip_coarse_create(_p(c, _f32p), self._nlist, self._d, int(metric), ordinal, ctypes.byref(h)))
+        self._h = h
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h:
+            _lib.vhip_coarse_destroy(h)
+            self._h = None
+
+    def nlist(self) -> int:
+        return int(_lib.vhip_coarse_nlist(self._h))
+
+    def dimension(self) -> int:
+        return int(_lib.vhip_coarse_dimension(self._h))
+
+    def assign(self, points, residuals: bool = False):
+        """(cluster uint32[n], score float32[n], residual float32[n, d] or None)."""
+        x = _rows(points, self._d) if np.asarray(points).size else np.zeros((0, self._d), np.float32)
+        n = x.shape[0]
+        cl = np.empty(n, np.uint32)
+        sc = np.empty(n, np.float32)
+        r = np.empty((n, self._d), np.float32) if residuals else None
+        _check(_lib.vhip_coarse_assign(self._h, _p(x, _f32p), n, _p(cl, _u32p), _p(sc, _f32p),
+                                       _p(r, _f32p) if r is not None else None))
+        return cl, sc, r
+
+    def find_nearest_centroid(self, vector):
+        """ivf/kmeans.rs:262-309 for one vector: (index, score)."""
+        cl, sc, _ = self.assign(np.asarray(vector, np.float32).reshape(1, self._d))
+        return int(cl[0]), float(sc[0])
+
+    def probe_batch(self, queries, nprobe: int):
+        """find_top_centroids for each query: (ids [nq, p], scores [nq, p], lens [nq])."""
+        q = _rows(queries, self._d) if np.asarray(queries).size else np.zeros((0, self._d), np.float32)
+        nq = q.shape[0]
+        w = max(nprobe, 1)
+        ids = np.empty((max(nq, 1), w), np.uint32)
+        sc = np.empty((max(nq, 1), w), np.float32)
+        lens = np.zeros(max(nq, 1), np.uintp)
+        _check(_lib.vhip_coarse_probe(self._h, _p(q, _f32p), nq, nprobe, _p(ids, _u32p), _p(sc, _f32p),
+                                      lens.ctypes.data_as(_szp)))
+        return ids[:nq, :nprobe], sc[:nq, :nprobe], lens[:nq]
+
+    def find_top_centroids(self, query, nprobe: int):
+        """ivf/kmeans.rs:311-356: [(index, score)] best first, min(nprobe, nlist) entries."""
+        ids, sc, lens = self.probe_batch(np.asarray(query, np.float32).reshape(1, self._d), nprobe)
+        return [(int(ids[0, j]), float(sc[0, j])) for j in range(int(lens[0]))] if nprobe else []
+
+
+# ---- files of the offline trainer (storage/mmap.rs, ivf/serializer.rs) -------------------
+def _path(p) -> bytes:
+    return os.fsencode(os.fspath(p))
+
+
+class MmapStorage:
+    """VECRSTOR vector files (storage/mmap.rs:9-16): create / create_from_flat write one,
+    open validates and loads it (the reference memory-maps; this reads the data once)."""
+
+    def __init__(self, data: np.ndarray, dimension: int):
+        self._data = data
+        self._dim = dimension
+
+    @staticmethod
+    def create(path, dimension: int, vectors) -> None:
+        for v in vectors:
+            if len(v) != dimension:
+                raise InvalidConfig(f"dimension mismatch: expected {dimension}, got {len(v)}")
+        flat = np.concatenate([np.asarray(v, np.float32) for v in vectors]) if len(vectors) else np.zeros(0, np.float32)
+        MmapStorage.create_from_flat(path, dimension, flat)
+
+    @staticmethod
+    def create_from_flat(path, dimension: int, flat_data) -> None:
+        f = np.ascontiguousarray(flat_data, dtype=np.float32).reshape(-1)
+        if dimension == 0 or f.size % dimension:
+            raise InvalidConfig(f"dimension mismatch: expected {dimension}, got {f.size % max(dimension, 1)}")
+        _check(_lib.vhip_vecrstor_write(_path(path), _p(f, _f32p), f.size // dimension, dimension))
+
+    @classmethod
+    def open(cls, path) -> "MmapStorage":
+        n = ctypes.c_size_t()
+        d = ctypes.c_size_t()
+        _check(_lib.vhip_vecrstor_open(_path(path), ctypes.byref(n), ctypes.byref(d)))
+        data = np.empty((n.value, d.value), np.float32)
+        _check(_lib.vhip_vecrstor_read(_path(path), _p(data, _f32p), n.value, d.value))
+        return cls(data, d.value)
+
+    def dimension(self) -> int:
+        return self._dim
+
+    def __len__(self) -> int:
+        return self._data.shape[0]
+
+    def is_empty(self) -> bool:
+        return len(self) == 0
+
+    def get(self, i: int) -> np.ndarray:
+        if not 0 <= i < len(self):
+            raise IndexError(f"vector id {i} out of bounds (len={len(self)})")
+        return self._data[i]
+
+    def as_raw_slice(self) -> np.ndarray:
+        return self._data.reshape(-1)
+
+
+class CentroidFileData(NamedTuple):
+    """ivf/serializer.rs:380-393."""
+
+    centroids: np.ndarray
+    dimension: int
+    k: int
+    metric: DistanceMetric
+    iterations: int
+    inertia: float
+
+
+def save_centroid_file(path, centroids, dimension: int, k: int, metric, iterations: int, inertia: float) -> None:
+    """IvfPqSerializer::save_centroid_file (ivf/serializer.rs:264-306)."""
+    c = np.ascontiguousarray(centroids, dtype=np.float32).reshape(-1)
+    if c.size != k * dimension:
+        raise InvalidConfig("centroids must hold k x dimension floats")
+    _check(_lib.vhip_centroid_file_save(_path(path), _p(c, _f32p), dimension, k, int(metric), iterations,
+                                        float(inertia)))
+
+
+def load_centroid_file(path) -> CentroidFileData:
+    """IvfPqSerializer::load_centroid_file (ivf/serializer.rs:309-360)."""
+    d, k, it = ctypes.c_size_t(), ctypes.c_size_t(), ctypes.c_size_t()
+    m = _int()
+    ine = np.zeros(1, np.float32)
+    _check(_lib.vhip_centroid_file_info(_path(path), ctypes.byref(d), ctypes.byref(k), ctypes.byref(m),
+                                        ctypes.byref(it), _p(ine, _f32p)))
+    c = np.empty(k.value * d.value, np.float32)
+    _check(_lib.vhip_centroid_file_load(_path(path), _p(c, _f32p), k.value, d.value))
+    return CentroidFileData(c, d.value, k.value, DistanceMetric(m.value), it.value, float(ine[0]))
+
+
+def fit_cuda_aware(all_data, dimension: int, k: int, max_iters: int, tolerance: float, metric=DistanceMetric.L2Squared,
+                   num_gpus: int = 1, seed: int = 42) -> CudaKMeansResult:
+    """vector-mpi fit_cuda_aware (src/distributed_kmeans.rs:375-415): one GPU runs the fit for any
+    num_gpus (more than present is the emulator there, the same one GPU here)."""
+    if max(num_gpus, 1) > 1:
+        return DistributedKMeansEngine.emulator(num_gpus).fit(all_data, dimension, k, max_iters, tolerance, metric,
+                                                              seed=seed)
+    return CudaKMeansEngine(0).fit(all_data, dimension, k, max_iters, tolerance, metric, seed=seed)
+
+
+def train_from_shards(data_dir, k: int = 64, max_iters: int = 30, tolerance: float = 1e-4,
+                      metric=DistanceMetric.L2Squared, num_gpus: int = 1, output: str = "centroids_global.bin",
+                      seed: int = 42):
+    """mpi_kmeans --use-cuda (src/bin/mpi_kmeans.rs:284-364): shard_*.bin in data_dir ->
+    data_dir/output.  Returns (result, number of shards read)."""
+    res = _KMeansResultC()
+    ns = ctypes.c_size_t()
+    _check(_lib.vhip_train_from_shards(_path(data_dir), k, max_iters, float(tolerance), int(metric), num_gpus,
+                                       output.encode(), seed, ctypes.byref(res), ctypes.byref(ns)))
+    return (int(res.dimension), int(res.k), int(res.iterations), float(res.inertia)), int(ns.value)
 
 
 # ---- device memory for callers that stage their own inputs ----------------------------
