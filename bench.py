@@ -12,7 +12,8 @@ launch time, measured with HIP events on the engine's stream over the timed regi
 "cpu_baseline": the oracle's restatement of the reference CPU path (CudaKnnEngine::search_batch_cpu,
 knn.rs:312-377, AVX-512 dispatch as vector-simd) timed on this host on a bounded query sample.
 
-Other workloads: --workload cos768 | kmeans | hamming | l1 | linf | gauss (see WORKLOADS).
+Other workloads: --workload cos768 | kmeans | hamming | l1 | linf | gauss (see WORKLOADS), ivf_coarse
+(the IVF coarse quantizer), copy (counter calibration).
 """
 import argparse
 import json
@@ -58,12 +59,13 @@ def cpu_model() -> str:
 # rocprofv3 counter summaries (FETCH_SIZE + WRITE_SIZE of the dominant kernel, scaled by a 1 GiB
 # copy) per workload; each holds a "traffic_bytes_per_launch:" line.
 PROFILES = {
-    "l2int": "k_mfma_reg_filter__knn_l2_int_1000000x128_q10000_k100.txt",
-    "kmeans": "k_mfma_reg_assign__kmeans_l2_2000000x96_k4096.txt",
-    "cos768": "k_mfma_stream_filter__knn_cosine_1000000x768_q10000_k10.txt",
+    "l2int": "k_mfma_hs_filter__knn_l2_int_1000000x128_q10000_k100.txt",
+    "kmeans": "k_mfma_hs_assign__kmeans_l2_2000000x96_k4096.txt",
+    "cos768": "k_mfma_pnl_filter__knn_cosine_1000000x768_q10000_k10.txt",
     "hamming": "k_hamming_filter__knn_hamming_packed256_10000000_q10000_k10.txt",
     "l1": "k_valu_filter__knn_l1_uniform_500000x128_q4096_k10.txt",
     "linf": "k_valu_filter__knn_linf_uniform_500000x128_q4096_k10.txt",
+    "ivf_coarse": "k_mfma_hs_assign__ivf_coarse_l2_2000000x96_nlist4096.txt",
 }
 
 
@@ -197,6 +199,68 @@ def bench_kmeans(vh, steps_iters, with_cpu):
     return res
 
 
+def bench_ivf_coarse(vh, steps, warmup, with_cpu):
+    """IVF coarse quantizer (ivf/mod.rs:106-133): the build's find_nearest_centroid over all
+    2,000,000 x 96 points of the k-means workload against 4,096 centroids (points resident, one
+    step = one assignment of every point; assignments and scores come back to the host), and
+    find_top_centroids for 10,000 queries at nprobe = 32."""
+    from vector_hip import datasets as ds
+
+    n, d, nlist, nq, nprobe = 2_000_000, 96, 4096, 10_000, 32
+    log(f"ivf_coarse: generating {n} x {d} mixture of {nlist}")
+    data, _, _ = ds.gaussian_mixture(n, d, nlist, ds.SEED_MIXTURE)
+    cent = data[:nlist].copy()
+    q = ds.gaussian_mixture(nq, d, nlist, ds.SEED_QUERIES)[0]
+    st = vh.KMeansState(data)
+    st.set_centroids(cent)
+    for _ in range(warmup):
+        st.assign_only()
+    st.profile(True)
+    vh.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        st.assign_only()
+        log(f"  step {i + 1}/{steps} done")
+    vh.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    prof = st.profile_read()
+    cq = vh.IvfCoarseQuantizer(cent, d)
+    cq.probe_batch(q, nprobe)
+    t0 = time.perf_counter()
+    cq.probe_batch(q, nprobe)
+    probe_ms = (time.perf_counter() - t0) * 1e3
+    t0 = time.perf_counter()
+    cq.assign(data, residuals=True)
+    host_ms = (time.perf_counter() - t0) * 1e3
+    out = {"metric": "IVF coarse assignment points/sec (2M x 96 -> 4096 centroids)", "value": round(n * 1e3 / ms, 1),
+           "unit": "points/s", "n_gpus": 1, "steps": steps, "warmup": warmup, "ms_per_step": round(ms, 3),
+           "higher_is_better": True, "scaling": "strong", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+           "config": {"workload": f"ivf_coarse_assign_l2_{n}x{d}_nlist{nlist}", "parallelism": "single GPU"},
+           "roofline": roofline(prof, "mfma", PEAK_MFMA_F32, "TFLOP/s", "ivf_coarse"),
+           "probe": {"queries": nq, "nprobe": nprobe, "ms": round(probe_ms, 3),
+                     "value": round(nq * 1e3 / probe_ms, 1), "unit": "queries/s (host buffers)"},
+           "host_buffers": {"value": round(n * 1e3 / host_ms, 1), "unit": "points/s", "ms": round(host_ms, 3),
+                            "note": "IvfCoarseQuantizer.assign with residuals, points and results over PCIe"}}
+    if with_cpu:
+        import oracle
+
+        # the reference's build loop is serial (ivf/mod.rs:119-132): one thread
+        sp = 4096
+        t0 = time.perf_counter()
+        oracle.kmeans_step(data[:sp], cent, "l2", threads=1)
+        dt = time.perf_counter() - t0
+        sp = int(min(n, max(sp, sp * CPU_TARGET_S / max(dt, 1e-6))))
+        t0 = time.perf_counter()
+        oracle.kmeans_step(data[:sp], cent, "l2", threads=1)
+        dt = time.perf_counter() - t0
+        be = {0: "scalar", 1: "AVX2+FMA", 2: "AVX-512F"}[oracle.detect_backend()]
+        out["cpu_baseline"] = {"value": round(sp / dt, 1), "unit": "points/s", "cores": 1, "kind": "port",
+                               "sample": f"find_nearest_centroid of {sp} of the {n} points against all {nlist} "
+                                         f"centroids (the serial build loop), {be} backend, {dt:.2f} s on 1 thread "
+                                         f"({cpu_model()})"}
+    return out
+
+
 def bench_copy(vh, nbytes=1 << 30, reps=5):
     """Plain device-to-device copy of `nbytes` (the runtime's blit kernel).  Its FETCH_SIZE and
     WRITE_SIZE counters calibrate the HBM traffic figures of the other kernels."""
@@ -288,7 +352,7 @@ def main():
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--workload", default="default",
-                    choices=["default", "kmeans", "copy"] + sorted(WORKLOADS))
+                    choices=["default", "kmeans", "copy", "ivf_coarse"] + sorted(WORKLOADS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -303,6 +367,8 @@ def main():
     ctx = vh.CudaDeviceContext(0)
     if args.workload == "copy":
         out = bench_copy(vh)
+    elif args.workload == "ivf_coarse":
+        out = bench_ivf_coarse(vh, args.steps, args.warmup, not args.no_cpu)
     elif args.workload == "kmeans":
         r = bench_kmeans(vh, 10, not args.no_cpu)
         out = {"metric": METRIC, "value": r["value"], "unit": r["unit"], "n_gpus": 1, "steps": 10, "warmup": 1,

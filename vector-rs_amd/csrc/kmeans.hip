@@ -598,6 +598,7 @@ int vhip_kmeans_assign_only(vhip_kmeans *K, int32_t *out_assign, float *out_scor
     hipStream_t s = K->stream;
     const int n = (int)K->n, k = (int)K->k;
     launch_fill_u32(K->counts.as<uint32_t>(), k, 0u, s);
+    const int t = K->timer.begin(s);
     if (is_gemm_metric(K->metric))
         launch_kmeans_assign(K->metric, K->cent.as<float>(), K->cnorm.as<float>(), (int)K->kpad, K->pts.as<float>(),
                              K->pnorm.as<float>(), n, (int)K->dpad, K->assign.as<int32_t>(), K->inertia.as<float>(),
@@ -606,6 +607,8 @@ int vhip_kmeans_assign_only(vhip_kmeans *K, int32_t *out_assign, float *out_scor
         launch_kmeans_assign_valu(K->metric, K->cent.as<float>(), k, K->pts.as<float>(), n, (int)K->dpad,
                                   K->assign.as<int32_t>(), K->inertia.as<float>(), K->pos.as<int32_t>(),
                                   K->counts.as<int32_t>(), K->grid_cap, s);
+    K->timer.end(t, s, (is_gemm_metric(K->metric) ? 2.0 : 1.0) * (double)n * k * (double)K->dim,
+                 ((double)n + k) * K->dim * 4.0);
     VH_HIP(hipGetLastError());
     DevBuf score, resid;
     if (out_score || out_residual) {
@@ -621,6 +624,7 @@ int vhip_kmeans_assign_only(vhip_kmeans *K, int32_t *out_assign, float *out_scor
     if (out_score) VH_CHECK(K->stager.d2h(out_score, score.p, K->n * sizeof(float), s));
     if (out_residual) VH_CHECK(K->stager.d2h(out_residual, resid.p, K->n * K->dim * sizeof(float), s));
     VH_HIP(hipStreamSynchronize(s));
+    K->timer.collect();
     K->assigned = false;  // counts / centroids describe no update
     return VHIP_OK;
 }
