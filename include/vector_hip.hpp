@@ -371,6 +371,132 @@ private:
     std::unique_ptr<vhip_hamming, Del> h_;
 };
 
+/* ---- IVF coarse quantizer (ivf/mod.rs:106-133, ivf/kmeans.rs:262-356) --------------------- */
+class IvfCoarseQuantizer {
+public:
+    IvfCoarseQuantizer(const std::vector<float> &centroids, size_t dimension,
+                       DistanceMetric metric = DistanceMetric::L2Squared, size_t ordinal = 0)
+        : dim_(dimension) {
+        detail::require(dimension > 0 && centroids.size() % dimension == 0, "centroids must be k x dimension");
+        vhip_coarse *h = nullptr;
+        detail::check(vhip_coarse_create(centroids.data(), centroids.size() / dimension, dimension, (int)metric,
+                                         (int)ordinal, &h));
+        h_.reset(h);
+    }
+    size_t nlist() const { return vhip_coarse_nlist(h_.get()); }
+    size_t dimension() const { return dim_; }
+    /* KMeans::find_nearest_centroid (ivf/kmeans.rs:262-309): (index, metric value) */
+    std::pair<size_t, float> find_nearest_centroid(const std::vector<float> &vector) const {
+        detail::require(vector.size() == dim_, "dimension mismatch");
+        uint32_t c = 0;
+        float sc = 0.0f;
+        detail::check(vhip_coarse_assign(h_.get(), vector.data(), 1, &c, &sc, nullptr));
+        return {c, sc};
+    }
+    /* the IVF-PQ build loop (ivf/mod.rs:119-132): cluster per point and, if asked, residuals */
+    void assign(const std::vector<float> &points, std::vector<uint32_t> &cluster, std::vector<float> &score,
+                std::vector<float> *residuals = nullptr) const {
+        const size_t n = points.size() / dim_;
+        cluster.resize(n);
+        score.resize(n);
+        if (residuals) residuals->resize(n * dim_);
+        detail::check(vhip_coarse_assign(h_.get(), points.data(), n, cluster.data(), score.data(),
+                                         residuals ? residuals->data() : nullptr));
+    }
+    /* KMeans::find_top_centroids (ivf/kmeans.rs:311-356): best first, min(nprobe, nlist) entries */
+    std::vector<std::pair<size_t, float>> find_top_centroids(const std::vector<float> &query, size_t nprobe) const {
+        detail::require(query.size() == dim_, "dimension mismatch");
+        std::vector<std::pair<size_t, float>> out;
+        if (nprobe == 0) return out;
+        std::vector<uint32_t> ids(nprobe);
+        std::vector<float> sc(nprobe);
+        size_t len = 0;
+        detail::check(vhip_coarse_probe(h_.get(), query.data(), 1, nprobe, ids.data(), sc.data(), &len));
+        for (size_t j = 0; j < len; ++j) out.emplace_back(ids[j], sc[j]);
+        return out;
+    }
+
+private:
+    struct Del {
+        void operator()(vhip_coarse *p) const { vhip_coarse_destroy(p); }
+    };
+    size_t dim_;
+    std::unique_ptr<vhip_coarse, Del> h_;
+};
+
+/* ---- files of the offline trainer (storage/mmap.rs, ivf/serializer.rs) ------------------- */
+/* MmapStorage (storage/mmap.rs:56-260); open() reads the data once instead of mapping it */
+class MmapStorage {
+public:
+    static void create_from_flat(const std::string &path, size_t dimension, const std::vector<float> &flat) {
+        detail::require(dimension > 0 && flat.size() % dimension == 0, "dimension mismatch");
+        detail::check(vhip_vecrstor_write(path.c_str(), flat.data(), flat.size() / dimension, dimension));
+    }
+    static MmapStorage open(const std::string &path) {
+        size_t n = 0, d = 0;
+        detail::check(vhip_vecrstor_open(path.c_str(), &n, &d));
+        MmapStorage s;
+        s.dim_ = d;
+        s.data_.resize(n * d);
+        detail::check(vhip_vecrstor_read(path.c_str(), s.data_.data(), n, d));
+        return s;
+    }
+    size_t dimension() const { return dim_; }
+    size_t len() const { return dim_ ? data_.size() / dim_ : 0; }
+    bool is_empty() const { return len() == 0; }
+    const float *get(size_t id) const {
+        detail::require(id < len(), "vector id out of bounds");
+        return data_.data() + id * dim_;
+    }
+    const std::vector<float> &as_raw_slice() const { return data_; }
+
+private:
+    size_t dim_ = 0;
+    std::vector<float> data_;
+};
+
+/* CentroidFileData (ivf/serializer.rs:380-393) */
+struct CentroidFileData {
+    std::vector<float> centroids;
+    size_t dimension = 0;
+    size_t k = 0;
+    DistanceMetric metric = DistanceMetric::L2Squared;
+    size_t iterations = 0;
+    float inertia = 0.0f;
+};
+
+struct IvfPqSerializer {
+    /* ivf/serializer.rs:264-306 */
+    static void save_centroid_file(const std::string &path, const std::vector<float> &centroids, size_t dimension,
+                                   size_t k, DistanceMetric metric, size_t iterations, float inertia) {
+        detail::require(centroids.size() == k * dimension, "centroids must be k x dimension");
+        detail::check(vhip_centroid_file_save(path.c_str(), centroids.data(), dimension, k, (int)metric, iterations,
+                                              inertia));
+    }
+    /* ivf/serializer.rs:309-360 */
+    static CentroidFileData load_centroid_file(const std::string &path) {
+        CentroidFileData f;
+        int m = 0;
+        detail::check(vhip_centroid_file_info(path.c_str(), &f.dimension, &f.k, &m, &f.iterations, &f.inertia));
+        f.metric = (DistanceMetric)m;
+        f.centroids.resize(f.k * f.dimension);
+        detail::check(vhip_centroid_file_load(path.c_str(), f.centroids.data(), f.k, f.dimension));
+        return f;
+    }
+};
+
+/* vector-mpi fit_cuda_aware (src/distributed_kmeans.rs:375-415) */
+inline CudaKMeansResult fit_cuda_aware(const std::vector<float> &all_data, size_t dimension, size_t k,
+                                       size_t max_iters, float tolerance, DistanceMetric metric, size_t num_gpus,
+                                       uint64_t seed = 42) {
+    KMeansInit ini;
+    ini.seed = seed;
+    if ((num_gpus ? num_gpus : 1) > 1)
+        return DistributedKMeansEngine::emulator(num_gpus).fit(all_data, dimension, k, max_iters, tolerance, metric,
+                                                              ini);
+    return CudaKMeansEngine().fit(all_data, dimension, k, max_iters, tolerance, metric, ini);
+}
+
 }  // namespace vector_hip
 
 #endif /* VECTOR_HIP_HPP */

@@ -73,6 +73,21 @@ static CudaError expect_error(F f) {
 }
 
 static void host_tests() {
+    run("centroid_file_roundtrip (ivf/serializer.rs:552-575)", [] {
+        const std::string p = "/tmp/vhip_facade_centroids.bin";
+        IvfPqSerializer::save_centroid_file(p, {1, 2, 3, 4, 5, 6, 7, 8}, 4, 2, DistanceMetric::L2Squared, 15, 42.5f);
+        auto f = IvfPqSerializer::load_centroid_file(p);
+        CHECK((f.centroids == std::vector<float>{1, 2, 3, 4, 5, 6, 7, 8}) && f.dimension == 4 && f.k == 2);
+        CHECK(f.metric == DistanceMetric::L2Squared && f.iterations == 15 && std::fabs(f.inertia - 42.5f) < 1e-6f);
+        std::remove(p.c_str());
+    });
+    run("mmap storage round trip (storage/mmap.rs:297-310)", [] {
+        const std::string p = "/tmp/vhip_facade_vectors.bin";
+        MmapStorage::create_from_flat(p, 3, {1, 2, 3, 4, 5, 6});
+        auto st = MmapStorage::open(p);
+        CHECK(st.len() == 2 && st.dimension() == 3 && st.get(1)[0] == 4.0f && st.get(1)[2] == 6.0f);
+        std::remove(p.c_str());
+    });
     run("ddp_knn_insufficient_hardware_error (distributed_knn.rs:470)", [] {
         const size_t avail = CudaDeviceContext::device_count(), req = avail + 100;
         auto e = expect_error([&] {
@@ -336,6 +351,22 @@ static void gpu_tests() {
             auto d = DistributedKnnEngine::emulator(data, 2, 2, GpuShardMode::Sharded, metric).search({0.8f, 0.6f}, 3);
             CHECK(s.size() == 3 && d.size() == 3);
             for (int i = 0; i < 3; ++i) CHECK(std::fabs(s[i].distance - d[i].distance) < 1e-4f);
+        }
+    });
+    run("find_nearest_centroid_l2 / dot (vector-mpi distributed_kmeans.rs:497-520)", [] {
+        IvfCoarseQuantizer q({0, 0, 10, 10}, 2);
+        auto r = q.find_nearest_centroid({1, 1});
+        CHECK(r.first == 0 && std::fabs(r.second - 2.0f) < 1e-5f);
+        IvfCoarseQuantizer d({1, 0, 0, 1}, 2, DistanceMetric::DotProduct);
+        CHECK(d.find_nearest_centroid({1, 0}).first == 0);
+        auto top = q.find_top_centroids({9, 9}, 5);
+        CHECK(top.size() == 2 && top[0].first == 1 && top[1].first == 0);
+    });
+    run("fit_cuda_aware single and multi GPU (vector-mpi distributed_kmeans.rs:522-548)", [] {
+        std::vector<float> data{0.0f, 0.1f, 0.1f, 0.0f, -0.1f, 0.0f, 10.0f, 10.1f, 10.1f, 10.0f, 9.9f, 10.0f};
+        for (size_t g : {1, 2}) {
+            auto r = fit_cuda_aware(data, 2, 2, 30, 1e-5f, DistanceMetric::L2Squared, g);
+            CHECK(r.k == 2 && r.dimension == 2 && r.iterations > 0);
         }
     });
     run("explicit-init k-means is deterministic (extension)", [] {
