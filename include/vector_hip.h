@@ -44,6 +44,7 @@ extern "C" {
 #define VHIP_ERR_DRIVER                (-3) /* DriverError(String) */
 #define VHIP_ERR_HARDWARE_NOT_AVAILABLE (-4) /* HardwareNotAvailable */
 #define VHIP_ERR_INVALID_CONFIG        (-5) /* InvalidConfig(String) */
+#define VHIP_ERR_EMPTY_INDEX           (-6) /* vector-index VectorIndexError::EmptyIndex (types.rs) */
 
 /* ---- metric codes: knn.rs:235-246 / kmeans.rs:152-163 ------------------------ */
 #define VHIP_METRIC_L2SQUARED    0
@@ -247,6 +248,94 @@ int vhip_memcpy_htod(int ordinal, void *dst, const void *src, size_t bytes);
 int vhip_memcpy_dtoh(int ordinal, void *dst, const void *src, size_t bytes);
 int vhip_memcpy_dtod(int ordinal, void *dst, const void *src, size_t bytes);
 int vhip_synchronize(int ordinal);
+
+/* ---- product quantization and the IVF-PQ index (vector-index/src/ivf) ------------- */
+/* IvfPqConfig (ivf/config.rs:25-44); max_train_points 0 means None (the build does not read it,
+ * like ivf/mod.rs). */
+typedef struct {
+    size_t nlist;
+    size_t nprobe;
+    size_t num_subvectors;
+    size_t sub_clusters;
+    size_t max_kmeans_iters;
+    float kmeans_tolerance;
+    size_t max_train_points;
+} vhip_ivfpq_config;
+/* IvfPqConfig::default (config.rs:46-58) */
+void vhip_ivfpq_config_default(vhip_ivfpq_config *cfg);
+/* IvfPqConfig::validate (config.rs:96-147): InvalidConfig with the reference's reasons. */
+int vhip_ivfpq_config_validate(const vhip_ivfpq_config *cfg, size_t dim);
+
+/* ProductQuantizer::train (pq.rs:53-107): one k-means per sub-space on the GPU, codebooks
+ * M x Ks x (dim / M) floats, zero rows past min(Ks, n) (pq.rs:84-88).  Initial sub-centroids
+ * are a seeded sample without replacement (KMeans::init_centroids_random, ivf/kmeans.rs:359-371,
+ * draws from an unseeded thread_rng) or, with init_codebooks != NULL, the given
+ * min(Ks, n) x ds rows of each sub-space (at stride Ks rows). */
+int vhip_pq_train(int ordinal, const float *data, size_t n, size_t dim, size_t num_subvectors, size_t sub_clusters,
+                  size_t max_iters, float tol, int metric, const float *init_codebooks, uint64_t seed,
+                  float *out_codebooks);
+/* ProductQuantizer::encode_batch (pq.rs:178-214): out_codes n x M bytes. */
+int vhip_pq_encode(int ordinal, const float *codebooks, size_t dim, size_t num_subvectors, size_t sub_clusters,
+                   int metric, const float *data, size_t n, uint8_t *out_codes);
+/* ProductQuantizer::compute_adc_lut (pq.rs:233-266) for nq queries: out_lut nq x M x Ks. */
+int vhip_pq_adc_lut(int ordinal, const float *codebooks, size_t dim, size_t num_subvectors, size_t sub_clusters,
+                    int metric, const float *queries, size_t nq, float *out_lut);
+
+/* IvfPqIndex (ivf/mod.rs:63-71): coarse centroids, product quantizer and inverted lists resident
+ * on one GPU.  Lists are held in CSR order: list c is entries [sum of sizes < c, + size c) of
+ * ids / codes (M bytes each). */
+typedef struct vhip_ivfpq vhip_ivfpq;
+#define VHIP_IVFPQ_MAX_K 1024
+typedef struct {
+    size_t dimension;
+    int metric;
+    size_t nlist; /* lists held (coarse centroids actually trained) */
+    size_t num_subvectors;
+    size_t sub_clusters;
+    size_t num_vectors; /* InvertedIndex::total_vectors */
+    vhip_ivfpq_config config;
+} vhip_ivfpq_desc;
+/* IvfPqIndex::build_parallel_with_config (ivf/mod.rs:90-165): validate, coarse k-means (seeded
+ * sample init), assignment + residuals, PQ training on the residuals, codes, inverted lists in
+ * ascending id order.  EmptyIndex for n == 0. */
+int vhip_ivfpq_build(int ordinal, const float *data, size_t n, size_t dim, const vhip_ivfpq_config *cfg, int metric,
+                     uint64_t seed, vhip_ivfpq **out);
+/* An index from its parts (IvfPqIndex::load_from_file, ivf/mod.rs:388-408, after
+ * IvfPqSerializer::load_from_file): list_sizes has nlist entries, ids / codes their sum. */
+int vhip_ivfpq_create(int ordinal, size_t dim, int metric, const vhip_ivfpq_config *cfg, const float *coarse,
+                      size_t nlist, const float *codebooks, const uint32_t *list_sizes, const uint32_t *ids,
+                      const uint8_t *codes, vhip_ivfpq **out);
+/* IvfPqIndex::search_with_nprobe (ivf/mod.rs:256-345) for a batch: rows of k results (ids, ADC
+ * distance, similarity for dot / cosine), best first, out_len[q] = min(k, entries in the probed
+ * lists); unused slots hold UINT32_MAX / NaN.  nprobe is clamped to [1, nlist]; k <= VHIP_IVFPQ_MAX_K. */
+int vhip_ivfpq_search_batch(vhip_ivfpq *ix, const float *queries, size_t nq, size_t k, size_t nprobe,
+                            uint32_t *out_ids, float *out_dist, size_t *out_len);
+/* Same search with queries and outputs in device memory of the index's GPU (no reference
+ * counterpart; for callers whose queries live on the GPU).  Returns after the results are written. */
+int vhip_ivfpq_search_batch_device(vhip_ivfpq *ix, const float *d_queries, size_t nq, size_t k, size_t nprobe,
+                                   uint32_t *d_ids, float *d_dist, uint32_t *d_len);
+/* The coarse probe lists the search uses (KMeans::find_top_centroids, ivf/kmeans.rs:311-356),
+ * nq x min(max(nprobe, 1), nlist) list indices, best first. */
+int vhip_ivfpq_probe(vhip_ivfpq *ix, const float *queries, size_t nq, size_t nprobe, uint32_t *out_lists);
+/* Getters (ivf/mod.rs:411-449) and the parts for IvfPqSerializer::save_to_file. */
+int vhip_ivfpq_info(const vhip_ivfpq *ix, vhip_ivfpq_desc *info);
+int vhip_ivfpq_export(const vhip_ivfpq *ix, float *coarse, float *codebooks, uint32_t *list_sizes, uint32_t *ids,
+                      uint8_t *codes);
+/* Kernel time of the ADC scan (HIP events on the index's stream). */
+int vhip_ivfpq_profile(vhip_ivfpq *ix, int enable);
+int vhip_ivfpq_profile_read(vhip_ivfpq *ix, double *kernel_ms, uint64_t *launches);
+void vhip_ivfpq_destroy(vhip_ivfpq *ix);
+/* IvfPqSerializer::save_to_file (ivf/serializer.rs:26-99): the IVFPQVEC file of an index's
+ * parts; list_sizes has nlists entries, ids / codes (num_subvectors bytes each) their sum. */
+int vhip_ivfpq_file_save(const char *path, const vhip_ivfpq_config *cfg, size_t dim, int metric, const float *coarse,
+                         size_t num_centroids, const float *codebooks, size_t codebooks_len,
+                         const uint32_t *list_sizes, size_t nlists, const uint32_t *ids, const uint8_t *codes);
+/* IvfPqSerializer::load_from_file (:102-254) in two calls: the header and sizes (InvalidConfig
+ * for a bad magic, version, metric code, codebook shape or a truncated file), then the arrays. */
+int vhip_ivfpq_file_info(const char *path, vhip_ivfpq_config *cfg, size_t *dim, int *metric, size_t *num_centroids,
+                         size_t *codebooks_len, size_t *nlists, size_t *total_vectors);
+int vhip_ivfpq_file_load(const char *path, float *coarse, float *codebooks, uint32_t *list_sizes, uint32_t *ids,
+                         uint8_t *codes);
 
 #if defined(__GNUC__)
 #pragma GCC visibility pop

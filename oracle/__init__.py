@@ -12,6 +12,9 @@ ctypes bindings over ``oracle/libvh_oracle.so`` (built from ``vh_oracle.c`` by
                          explicit init, empty clusters keep the old centroid.
 * ``hamming_packed_knn`` packed-bit Hamming (an extension; equals scalar.rs:143-153 on
                          unpacked 0/1 codes).
+* ``pq_encode`` / ``pq_adc_lut`` / ``pq_distance_with_lut``  ``ProductQuantizer`` (vector-index/src/ivf/pq.rs:178-293).
+* ``find_top_centroids`` ``KMeans::find_top_centroids`` (ivf/kmeans.rs:311-356).
+* ``ivfpq_search``       ``IvfPqIndex::search_with_nprobe`` (ivf/mod.rs:256-345) with given probes.
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg
 may import this package, and only as the checker / CPU baseline.
@@ -39,6 +42,8 @@ _u32p = ctypes.POINTER(ctypes.c_uint32)
 _i32p = ctypes.POINTER(ctypes.c_int32)
 _i64p = ctypes.POINTER(ctypes.c_int64)
 _szp = ctypes.POINTER(ctypes.c_size_t)
+_u8p = ctypes.POINTER(ctypes.c_uint8)
+_u64p = ctypes.POINTER(ctypes.c_uint64)
 _sz = ctypes.c_size_t
 
 
@@ -78,6 +83,17 @@ def lib():
         L.vho_hamming_packed_knn.argtypes = [_u32p, _sz, _sz, _u32p, _sz, _sz, ctypes.c_int, _u32p, _u32p, _szp]
         L.vho_unpack_bits.restype = None
         L.vho_unpack_bits.argtypes = [_u32p, _sz, _sz, _f32p]
+        L.vho_pq_encode.restype = ctypes.c_int
+        L.vho_pq_encode.argtypes = [_f32p, _sz, _sz, _sz, _sz, _f32p, ctypes.c_int, ctypes.c_int, _u8p]
+        L.vho_pq_adc_lut.restype = ctypes.c_int
+        L.vho_pq_adc_lut.argtypes = [_f32p, _sz, _sz, _sz, _f32p, ctypes.c_int, ctypes.c_int, _f32p]
+        L.vho_pq_distance_with_lut.restype = ctypes.c_float
+        L.vho_pq_distance_with_lut.argtypes = [_u8p, _sz, _sz, _f32p]
+        L.vho_find_top_centroids.restype = ctypes.c_size_t
+        L.vho_find_top_centroids.argtypes = [_f32p, _f32p, _sz, _sz, _sz, ctypes.c_int, ctypes.c_int, _u32p, _f32p]
+        L.vho_ivfpq_search.restype = ctypes.c_size_t
+        L.vho_ivfpq_search.argtypes = [_f32p, _sz, ctypes.c_int, ctypes.c_int, _f32p, _sz, _sz, _sz, _f32p,
+                                       _u64p, _u32p, _u8p, _u32p, _sz, _sz, _u32p, _f32p]
         _lib = L
     return _lib
 
@@ -208,3 +224,64 @@ def unpack_bits(codes) -> np.ndarray:
     out = np.empty((n, words * 32), np.float32)
     lib().vho_unpack_bits(_p(codes, _u32p), n, words, _p(out, _f32p))
     return out
+
+
+# ---- product quantization and IVF-PQ (vector-index/src/ivf) -------------------------------
+def pq_encode(data, codebooks, num_subvectors, sub_clusters, metric="l2", backend: int = -1):
+    """ProductQuantizer::encode_batch: codes[n, M] uint8."""
+    data = np.ascontiguousarray(data, dtype=np.float32)
+    codebooks = np.ascontiguousarray(codebooks, dtype=np.float32).ravel()
+    n, dim = data.shape
+    out = np.zeros((n, num_subvectors), np.uint8)
+    rc = lib().vho_pq_encode(_p(data, _f32p), n, dim, num_subvectors, sub_clusters, _p(codebooks, _f32p),
+                             _metric(metric), backend, _p(out, _u8p))
+    assert rc == 0
+    return out
+
+
+def pq_adc_lut(query, codebooks, num_subvectors, sub_clusters, metric="l2", backend: int = -1):
+    """ProductQuantizer::compute_adc_lut: lut[M * Ks] float32."""
+    query = np.ascontiguousarray(query, dtype=np.float32).ravel()
+    codebooks = np.ascontiguousarray(codebooks, dtype=np.float32).ravel()
+    lut = np.zeros(num_subvectors * sub_clusters, np.float32)
+    rc = lib().vho_pq_adc_lut(_p(query, _f32p), query.size, num_subvectors, sub_clusters, _p(codebooks, _f32p),
+                              _metric(metric), backend, _p(lut, _f32p))
+    assert rc == 0
+    return lut
+
+
+def pq_distance_with_lut(code, lut, sub_clusters) -> float:
+    code = np.ascontiguousarray(code, dtype=np.uint8).ravel()
+    lut = np.ascontiguousarray(lut, dtype=np.float32).ravel()
+    return float(lib().vho_pq_distance_with_lut(_p(code, _u8p), code.size, sub_clusters, _p(lut, _f32p)))
+
+
+def find_top_centroids(query, centroids, nprobe, metric="l2", backend: int = -1):
+    """KMeans::find_top_centroids: (indices uint32, scores float32), best first."""
+    query = np.ascontiguousarray(query, dtype=np.float32).ravel()
+    centroids = np.ascontiguousarray(centroids, dtype=np.float32)
+    k, dim = centroids.shape
+    idx = np.zeros(max(1, min(nprobe, k)), np.uint32)
+    sc = np.zeros(idx.size, np.float32)
+    r = lib().vho_find_top_centroids(_p(query, _f32p), _p(centroids, _f32p), k, dim, nprobe, _metric(metric),
+                                     backend, _p(idx, _u32p), _p(sc, _f32p))
+    return idx[:r], sc[:r]
+
+
+def ivfpq_search(query, coarse, codebooks, num_subvectors, sub_clusters, list_off, ids, codes, probes, k,
+                 metric="l2", backend: int = -1):
+    """IvfPqIndex::search_with_nprobe for one query with the probe list given (CSR lists)."""
+    query = np.ascontiguousarray(query, dtype=np.float32).ravel()
+    coarse = np.ascontiguousarray(coarse, dtype=np.float32)
+    codebooks = np.ascontiguousarray(codebooks, dtype=np.float32).ravel()
+    list_off = np.ascontiguousarray(list_off, dtype=np.uint64)
+    ids = np.ascontiguousarray(ids, dtype=np.uint32)
+    codes = np.ascontiguousarray(codes, dtype=np.uint8).ravel()
+    probes = np.ascontiguousarray(probes, dtype=np.uint32).ravel()
+    out_i = np.zeros(max(k, 1), np.uint32)
+    out_d = np.zeros(max(k, 1), np.float32)
+    r = lib().vho_ivfpq_search(_p(query, _f32p), query.size, _metric(metric), backend, _p(coarse, _f32p),
+                               coarse.shape[0], num_subvectors, sub_clusters, _p(codebooks, _f32p),
+                               _p(list_off, _u64p), _p(ids, _u32p), _p(codes, _u8p), _p(probes, _u32p),
+                               probes.size, k, _p(out_i, _u32p), _p(out_d, _f32p))
+    return out_i[:r], out_d[:r]

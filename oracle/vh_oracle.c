@@ -1,5 +1,5 @@
 /*
- * vh_oracle.c -- CPU oracle for the vector-hip kNN / k-means hot path.
+ * vh_oracle.c -- CPU oracle for the vector-hip kNN / k-means / IVF-PQ hot path.
  *
  * TEST INFRASTRUCTURE ONLY.  This file restates, in C, the reference's CPU
  * path (the Rust crates vector-simd, vector-index::flat, vector-index::ivf::kmeans
@@ -13,6 +13,10 @@
  *   vho_top_k_reduce                                    pinned: reference KATs (collective.rs tests)
  *   vho_kmeans_step / vho_kmeans_fit                    pinned: reference KATs + closed-form means
  *   vho_hamming_packed_knn                              pinned: identity with float-Hamming on unpacked codes
+ *   vho_pq_encode / vho_pq_adc_lut                      pinned: reference KATs (pq.rs tests) + brute force in double
+ *   vho_pq_distance_with_lut                            pinned: reference KATs + the closed-form sum on integer tables
+ *   vho_find_top_centroids                              pinned: full sort in double on tiny inputs
+ *   vho_ivfpq_search                                    pinned: brute-force ADC top-k on tiny indexes + reference KATs
  *   Empty-cluster reseeding and random init: parity unpinned (the reference uses an unseeded
  *   thread_rng); this oracle keeps the old centroid, like kmeans.cu:350-356.
  */
@@ -757,4 +761,136 @@ VHO_EXPORT void vho_unpack_bits(const uint32_t *codes, size_t n, size_t words, f
         for (size_t w = 0; w < words; ++w)
             for (int j = 0; j < 32; ++j)
                 out[i * words * 32 + w * 32 + j] = (float)((codes[i * words + w] >> j) & 1u);
+}
+
+/* ------------------------------------------------------------------------- */
+/* Product quantization (vector-index/src/ivf/pq.rs) and the IVF-PQ search     */
+/* (vector-index/src/ivf/mod.rs).  Codebooks are M x Ks x ds floats, flat       */
+/* (pq.rs:21-25); codes one byte per sub-space.                                 */
+/* ------------------------------------------------------------------------- */
+static int pq_shape_ok(size_t dim, size_t m_sub, size_t ks, int metric) {
+    return metric >= 0 && metric <= 9 && m_sub > 0 && dim % m_sub == 0 && ks > 0 && ks <= 256;
+}
+
+/* ProductQuantizer::encode / encode_batch (pq.rs:178-214): per sub-space the
+ * nearest sub-centroid of KMeans::find_nearest_centroid (ivf/kmeans.rs:262-309,
+ * strict compare in ascending index, so the lowest index wins ties). */
+VHO_EXPORT int vho_pq_encode(const float *data, size_t n, size_t dim, size_t m_sub, size_t ks,
+                             const float *codebooks, int metric, int backend, uint8_t *out_codes) {
+    if (!pq_shape_ok(dim, m_sub, ks, metric)) return -1;
+    const size_t ds = dim / m_sub;
+    dist_fn f = pick(metric, backend);
+    int hib = higher_is_better(metric);
+    for (size_t i = 0; i < n; ++i)
+        for (size_t m = 0; m < m_sub; ++m) {
+            int32_t b;
+            float s;
+            nearest(data + i * dim + m * ds, codebooks + m * ks * ds, ks, ds, f, hib, &b, &s);
+            out_codes[i * m_sub + m] = (uint8_t)b;
+        }
+    return 0;
+}
+
+/* ProductQuantizer::compute_adc_lut (pq.rs:233-266): lut[m * ks + j] = metric of
+ * query sub-vector m and sub-centroid (m, j), Minkowski with p = 3. */
+VHO_EXPORT int vho_pq_adc_lut(const float *query, size_t dim, size_t m_sub, size_t ks, const float *codebooks,
+                              int metric, int backend, float *lut) {
+    if (!pq_shape_ok(dim, m_sub, ks, metric)) return -1;
+    const size_t ds = dim / m_sub;
+    dist_fn f = pick(metric, backend);
+    for (size_t m = 0; m < m_sub; ++m)
+        for (size_t j = 0; j < ks; ++j) lut[m * ks + j] = f(query + m * ds, codebooks + (m * ks + j) * ds, ds);
+    return 0;
+}
+
+/* ProductQuantizer::compute_distance_with_lut (pq.rs:270-293): quads of codes
+ * summed as (d0 + d1) + (d2 + d3) into the running total, then the remainder
+ * one by one. */
+VHO_EXPORT float vho_pq_distance_with_lut(const uint8_t *code, size_t m_sub, size_t ks, const float *lut) {
+    float total = 0.0f;
+    size_t m = 0;
+    for (; m + 4 <= m_sub; m += 4) {
+        const float d0 = lut[m * ks + code[m]];
+        const float d1 = lut[(m + 1) * ks + code[m + 1]];
+        const float d2 = lut[(m + 2) * ks + code[m + 2]];
+        const float d3 = lut[(m + 3) * ks + code[m + 3]];
+        total += (d0 + d1) + (d2 + d3);
+    }
+    for (; m < m_sub; ++m) total += lut[m * ks + code[m]];
+    return total;
+}
+
+/* KMeans::find_top_centroids (ivf/kmeans.rs:311-356): every centroid scored, a
+ * stable sort (descending for similarities) truncated to min(nprobe, k).  For
+ * finite scores a stable sort equals the order by (score, index). */
+typedef struct { float s; uint32_t i; int hib; } tc_t;
+static int tc_cmp(const void *pa, const void *pb) {
+    const tc_t *a = (const tc_t *)pa, *b = (const tc_t *)pb;
+    if (a->s != b->s) {
+        int a_first = a->hib ? (a->s > b->s) : (a->s < b->s);
+        int b_first = a->hib ? (b->s > a->s) : (b->s < a->s);
+        if (a_first) return -1;
+        if (b_first) return 1;
+    }
+    return a->i < b->i ? -1 : (a->i > b->i);
+}
+VHO_EXPORT size_t vho_find_top_centroids(const float *query, const float *cent, size_t k, size_t dim, size_t nprobe,
+                                         int metric, int backend, uint32_t *out_idx, float *out_score) {
+    size_t p = nprobe < k ? nprobe : k;
+    if (p == 0 || metric < 0 || metric > 9) return 0;
+    dist_fn f = pick(metric, backend);
+    tc_t *t = (tc_t *)malloc(k * sizeof(tc_t));
+    for (size_t c = 0; c < k; ++c) {
+        t[c].s = f(query, cent + c * dim, dim);
+        t[c].i = (uint32_t)c;
+        t[c].hib = higher_is_better(metric);
+    }
+    qsort(t, k, sizeof(tc_t), tc_cmp);
+    for (size_t j = 0; j < p; ++j) {
+        out_idx[j] = t[j].i;
+        if (out_score) out_score[j] = t[j].s;
+    }
+    free(t);
+    return p;
+}
+
+/* IvfPqIndex::search_with_nprobe (ivf/mod.rs:256-345) for one query, with the
+ * coarse probe list given (best first, as find_top_centroids returns it).  Per
+ * probed non-empty list: residual q - c, ADC table, every code scored with
+ * compute_distance_with_lut and offered to the bounded BinaryHeap (strict
+ * eviction); the heap is popped and reversed.  Lists in CSR form: list c holds
+ * entries [list_off[c], list_off[c+1]) of ids / codes (M bytes each), in the
+ * order IvfPqIndex::build appended them.  Returns the number of results. */
+VHO_EXPORT size_t vho_ivfpq_search(const float *query, size_t dim, int metric, int backend, const float *coarse,
+                                   size_t nlist, size_t m_sub, size_t ks, const float *codebooks,
+                                   const uint64_t *list_off, const uint32_t *ids, const uint8_t *codes,
+                                   const uint32_t *probes, size_t nprobe, size_t k, uint32_t *out_ids,
+                                   float *out_dist) {
+    if (k == 0 || !pq_shape_ok(dim, m_sub, ks, metric)) return 0;
+    const int hib = higher_is_better(metric);
+    float *res = (float *)malloc(dim * sizeof(float));
+    float *lut = (float *)malloc(m_sub * ks * sizeof(float));
+    cand_t *h = (cand_t *)malloc((k + 1) * sizeof(cand_t));
+    size_t len = 0;
+    for (size_t p = 0; p < nprobe; ++p) {
+        const uint32_t c = probes[p];
+        if (c >= nlist) continue;
+        const uint64_t b = list_off[c], e = list_off[c + 1];
+        if (b == e) continue;
+        for (size_t d = 0; d < dim; ++d) res[d] = query[d] - coarse[(size_t)c * dim + d];
+        vho_pq_adc_lut(res, dim, m_sub, ks, codebooks, metric, backend, lut);
+        for (uint64_t i = b; i < e; ++i) {
+            const float dist = vho_pq_distance_with_lut(codes + i * m_sub, m_sub, ks, lut);
+            cand_t cd = {hib ? -dist : dist, dist, ids[i]};
+            heap_offer(h, &len, k, cd);
+        }
+    }
+    const size_t cnt = len;
+    for (size_t j = cnt; j-- > 0;) {
+        cand_t c = heap_pop(h, &len);
+        out_ids[j] = c.id;
+        out_dist[j] = c.dist;
+    }
+    free(res); free(lut); free(h);
+    return cnt;
 }

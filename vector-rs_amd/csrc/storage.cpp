@@ -7,6 +7,11 @@
 //      (vector-index/src/ivf/serializer.rs:264-360, 374-377): u64 magic 0x5652534B_4D45414E,
 //      u32 version 1, u8 metric code, u32 dim, u32 k, u32 iterations, f32 inertia, then k x dim
 //      f32, little-endian, no padding (29-byte header).
+//  * IVFPQVEC index files: IvfPqSerializer::save_to_file / load_from_file
+//      (vector-index/src/ivf/serializer.rs:16-254): u64 magic 0x49564650_51564543, u32 version 1,
+//      u8 metric, u32 dim, u32 nlist, nprobe, num_subvectors, sub_clusters, max_kmeans_iters,
+//      f32 tolerance, u32 centroid count + f32 coarse centroids, u32 codebook length + f32
+//      codebooks, u32 list count, then per list u32 count, count x u32 ids, count x M code bytes.
 //  * Offline trainer: vector-mpi fit_cuda_aware (src/distributed_kmeans.rs:375-415) reached from
 //      mpi_kmeans --use-cuda (src/bin/mpi_kmeans.rs:284-364): load data_dir/shard_0.bin,
 //      shard_1.bin, ... (until the first missing index), fit k-means on the GPU, write the
@@ -31,6 +36,8 @@ constexpr uint64_t kCentroidMagic = 0x5652534B4D45414Eull;
 constexpr uint32_t kCentroidVersion = 1;
 constexpr size_t kVecHeader = 24;
 constexpr size_t kCentroidHeader = 29;
+constexpr uint64_t kIvfPqMagic = 0x4956465051564543ull;
+constexpr uint32_t kIvfPqVersion = 1;
 
 struct File {
     FILE *f = nullptr;
@@ -253,6 +260,183 @@ int vhip_centroid_file_load(const char *path, float *centroids, size_t k, size_t
     if (!read_f32(f.f, centroids, k * dim))
         return vh::set_error(VHIP_ERR_INVALID_CONFIG, std::string("truncated centroid file '") + path + "'");
     return VHIP_OK;
+}
+
+namespace {
+
+bool write_u32(FILE *f, uint32_t v) {
+    unsigned char b[4];
+    put_u32(b, v);
+    return fwrite(b, 1, 4, f) == 4;
+}
+bool read_u32(FILE *f, uint32_t *v) {
+    unsigned char b[4];
+    if (fread(b, 1, 4, f) != 4) return false;
+    *v = get_u32(b);
+    return true;
+}
+
+struct IvfPqHead {
+    vhip_ivfpq_config cfg{};
+    size_t dim = 0, num_centroids = 0, codebooks_len = 0, nlists = 0, total = 0;
+    int metric = 0;
+};
+
+// Parses an IVFPQVEC file (serializer.rs:102-254).  Arrays that are null are skipped; with all
+// of them null the call only fills `h` (sizes included, so callers can allocate).
+int ivfpq_read(const char *path, IvfPqHead *h, float *coarse, float *codebooks, uint32_t *sizes, uint32_t *ids,
+               uint8_t *codes) {
+    File f(fopen(path, "rb"));
+    if (!f.f) return io_error("cannot open IVF-PQ index file", path);
+    auto truncated = [&] {
+        return vh::set_error(VHIP_ERR_INVALID_CONFIG, std::string("truncated IVF-PQ index file '") + path + "'");
+    };
+    auto bad = [&](const std::string &why) {
+        return vh::set_error(VHIP_ERR_INVALID_CONFIG, std::string("invalid header in '") + path + "': " + why);
+    };
+    unsigned char b8[8];
+    if (fread(b8, 1, 8, f.f) != 8) return truncated();
+    const uint64_t magic = get_u64(b8);
+    if (magic != kIvfPqMagic) {
+        char msg[96];
+        snprintf(msg, sizeof msg, "expected magic %#llX, got %#llX", (unsigned long long)kIvfPqMagic,
+                 (unsigned long long)magic);
+        return bad(msg);
+    }
+    uint32_t v = 0;
+    if (!read_u32(f.f, &v)) return truncated();
+    if (v != kIvfPqVersion) return bad("unsupported version: " + std::to_string(v));
+    unsigned char mc;
+    if (fread(&mc, 1, 1, f.f) != 1) return truncated();
+    if (mc > 9) return bad("invalid metric code: " + std::to_string(mc));
+    h->metric = mc;
+    uint32_t u[6];
+    for (int j = 0; j < 6; ++j)
+        if (!read_u32(f.f, &u[j])) return truncated();
+    h->dim = u[0];
+    h->cfg.nlist = u[1];
+    h->cfg.nprobe = u[2];
+    h->cfg.num_subvectors = u[3];
+    h->cfg.sub_clusters = u[4];
+    h->cfg.max_kmeans_iters = u[5];
+    if (!read_f32(f.f, &h->cfg.kmeans_tolerance, 1)) return truncated();
+    h->cfg.max_train_points = 0;
+    const size_t m_sub = h->cfg.num_subvectors;
+    if (!read_u32(f.f, &v)) return truncated();
+    h->num_centroids = v;
+    if (coarse) {
+        if (!read_f32(f.f, coarse, h->num_centroids * h->dim)) return truncated();
+    } else if (fseek(f.f, (long)(h->num_centroids * h->dim * 4), SEEK_CUR) != 0) {
+        return truncated();
+    }
+    if (!read_u32(f.f, &v)) return truncated();
+    h->codebooks_len = v;
+    // ProductQuantizer::new (pq.rs:30-50) asserts these; here they are errors
+    if (m_sub == 0 || h->dim % m_sub != 0)
+        return bad("dimension " + std::to_string(h->dim) + " is not divisible by num_subvectors " +
+                   std::to_string(m_sub));
+    if (h->codebooks_len != m_sub * h->cfg.sub_clusters * (h->dim / m_sub))
+        return bad("codebook length " + std::to_string(h->codebooks_len) + " is not num_subvectors x sub_clusters x " +
+                   "sub_dimension");
+    if (codebooks) {
+        if (!read_f32(f.f, codebooks, h->codebooks_len)) return truncated();
+    } else if (fseek(f.f, (long)(h->codebooks_len * 4), SEEK_CUR) != 0) {
+        return truncated();
+    }
+    if (!read_u32(f.f, &v)) return truncated();
+    h->nlists = v;
+    size_t total = 0;
+    for (size_t c = 0; c < h->nlists; ++c) {
+        uint32_t cnt = 0;
+        if (!read_u32(f.f, &cnt)) return truncated();
+        if (sizes) sizes[c] = cnt;
+        if (ids) {
+            for (uint32_t j = 0; j < cnt; ++j)
+                if (!read_u32(f.f, &ids[total + j])) return truncated();
+        } else if (fseek(f.f, (long)cnt * 4, SEEK_CUR) != 0) {
+            return truncated();
+        }
+        const size_t nb = (size_t)cnt * m_sub;
+        if (codes) {
+            if (fread(codes + total * m_sub, 1, nb, f.f) != nb) return truncated();
+        } else if (fseek(f.f, (long)nb, SEEK_CUR) != 0) {
+            return truncated();
+        }
+        total += cnt;
+    }
+    // fseek past the end succeeds: confirm that the last list really is in the file
+    const long pos = ftell(f.f);
+    if (pos < 0 || file_size(path) < pos) return truncated();
+    h->total = total;
+    return VHIP_OK;
+}
+
+}  // namespace
+
+int vhip_ivfpq_file_save(const char *path, const vhip_ivfpq_config *cfg, size_t dim, int metric, const float *coarse,
+                         size_t num_centroids, const float *codebooks, size_t codebooks_len,
+                         const uint32_t *list_sizes, size_t nlists, const uint32_t *ids, const uint8_t *codes) {
+    vh::clear_error();
+    if (!path || !cfg) return vh::set_error(VHIP_ERR_INVALID_CONFIG, "null argument");
+    if (metric < 0 || metric > 9) return vh::set_error(VHIP_ERR_INVALID_CONFIG, "unknown metric code");
+    size_t total = 0;
+    for (size_t c = 0; c < nlists; ++c) total += list_sizes ? list_sizes[c] : 0;
+    if ((num_centroids * dim != 0 && !coarse) || (codebooks_len && !codebooks) || (nlists && !list_sizes) ||
+        (total && (!ids || !codes)))
+        return vh::set_error(VHIP_ERR_INVALID_CONFIG, "null argument");
+    const size_t u32s[] = {dim, cfg->nlist, cfg->nprobe, cfg->num_subvectors, cfg->sub_clusters,
+                           cfg->max_kmeans_iters, num_centroids, codebooks_len, nlists};
+    for (size_t x : u32s)
+        if (x > 0xffffffffull) return vh::set_error(VHIP_ERR_INVALID_CONFIG, "a stored size exceeds u32");
+    File f(fopen(path, "wb"));
+    if (!f.f) return io_error("cannot create IVF-PQ index file", path);
+    unsigned char b8[8];
+    put_u64(b8, kIvfPqMagic);
+    const unsigned char mc = (unsigned char)metric;
+    bool ok = fwrite(b8, 1, 8, f.f) == 8 && write_u32(f.f, kIvfPqVersion) && fwrite(&mc, 1, 1, f.f) == 1 &&
+              write_u32(f.f, (uint32_t)dim) && write_u32(f.f, (uint32_t)cfg->nlist) &&
+              write_u32(f.f, (uint32_t)cfg->nprobe) && write_u32(f.f, (uint32_t)cfg->num_subvectors) &&
+              write_u32(f.f, (uint32_t)cfg->sub_clusters) && write_u32(f.f, (uint32_t)cfg->max_kmeans_iters) &&
+              write_f32(f.f, &cfg->kmeans_tolerance, 1) && write_u32(f.f, (uint32_t)num_centroids) &&
+              write_f32(f.f, coarse, num_centroids * dim) && write_u32(f.f, (uint32_t)codebooks_len) &&
+              write_f32(f.f, codebooks, codebooks_len) && write_u32(f.f, (uint32_t)nlists);
+    size_t off = 0;
+    for (size_t c = 0; ok && c < nlists; ++c) {
+        const uint32_t cnt = list_sizes[c];
+        ok = write_u32(f.f, cnt);
+        for (uint32_t j = 0; ok && j < cnt; ++j) ok = write_u32(f.f, ids[off + j]);
+        const size_t nb = (size_t)cnt * cfg->num_subvectors;
+        ok = ok && fwrite(codes + off * cfg->num_subvectors, 1, nb, f.f) == nb;
+        off += cnt;
+    }
+    if (!ok || fflush(f.f) != 0) return io_error("cannot write IVF-PQ index file", path);
+    return VHIP_OK;
+}
+
+int vhip_ivfpq_file_info(const char *path, vhip_ivfpq_config *cfg, size_t *dim, int *metric, size_t *num_centroids,
+                         size_t *codebooks_len, size_t *nlists, size_t *total_vectors) {
+    vh::clear_error();
+    if (!path) return vh::set_error(VHIP_ERR_INVALID_CONFIG, "null path");
+    IvfPqHead h;
+    const int rc = ivfpq_read(path, &h, nullptr, nullptr, nullptr, nullptr, nullptr);
+    if (rc != VHIP_OK) return rc;
+    if (cfg) *cfg = h.cfg;
+    if (dim) *dim = h.dim;
+    if (metric) *metric = h.metric;
+    if (num_centroids) *num_centroids = h.num_centroids;
+    if (codebooks_len) *codebooks_len = h.codebooks_len;
+    if (nlists) *nlists = h.nlists;
+    if (total_vectors) *total_vectors = h.total;
+    return VHIP_OK;
+}
+
+int vhip_ivfpq_file_load(const char *path, float *coarse, float *codebooks, uint32_t *list_sizes, uint32_t *ids,
+                         uint8_t *codes) {
+    vh::clear_error();
+    if (!path || !coarse || !codebooks || !list_sizes || !ids || !codes)
+        return vh::set_error(VHIP_ERR_INVALID_CONFIG, "null argument");
+    IvfPqHead h;
+    return ivfpq_read(path, &h, coarse, codebooks, list_sizes, ids, codes);
 }
 
 int vhip_train_from_shards(const char *data_dir, size_t k, size_t max_iters, float tol, int metric, size_t num_gpus,

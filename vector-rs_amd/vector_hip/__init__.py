@@ -18,6 +18,7 @@ built, importing this package raises ImportError.
 from __future__ import annotations
 
 import ctypes
+import dataclasses
 import enum
 import os
 from typing import List, NamedTuple, Optional, Sequence
@@ -113,6 +114,41 @@ if _HAS_KMEANS:
     _sig("vhip_coarse_destroy", None, _vp)
     _sig("vhip_train_from_shards", _int, ctypes.c_char_p, _sz, _sz, ctypes.c_float, _int, _sz, ctypes.c_char_p,
          ctypes.c_uint64, ctypes.POINTER(_KMeansResultC), _szp)
+class _IvfPqConfigC(ctypes.Structure):
+    _fields_ = [("nlist", _sz), ("nprobe", _sz), ("num_subvectors", _sz), ("sub_clusters", _sz),
+                ("max_kmeans_iters", _sz), ("kmeans_tolerance", ctypes.c_float), ("max_train_points", _sz)]
+
+
+class _IvfPqDescC(ctypes.Structure):
+    _fields_ = [("dimension", _sz), ("metric", _int), ("nlist", _sz), ("num_subvectors", _sz),
+                ("sub_clusters", _sz), ("num_vectors", _sz), ("config", _IvfPqConfigC)]
+
+
+_HAS_IVFPQ = hasattr(_lib, "vhip_ivfpq_build")
+if _HAS_IVFPQ:
+    _u8p = ctypes.POINTER(ctypes.c_uint8)
+    _cfgp = ctypes.POINTER(_IvfPqConfigC)
+    _sig("vhip_ivfpq_config_default", None, _cfgp)
+    _sig("vhip_ivfpq_config_validate", _int, _cfgp, _sz)
+    _sig("vhip_pq_train", _int, _int, _f32p, _sz, _sz, _sz, _sz, _sz, ctypes.c_float, _int, _f32p, ctypes.c_uint64,
+         _f32p)
+    _sig("vhip_pq_encode", _int, _int, _f32p, _sz, _sz, _sz, _int, _f32p, _sz, _u8p)
+    _sig("vhip_pq_adc_lut", _int, _int, _f32p, _sz, _sz, _sz, _int, _f32p, _sz, _f32p)
+    _sig("vhip_ivfpq_build", _int, _int, _f32p, _sz, _sz, _cfgp, _int, ctypes.c_uint64, ctypes.POINTER(_vp))
+    _sig("vhip_ivfpq_create", _int, _int, _sz, _int, _cfgp, _f32p, _sz, _f32p, _u32p, _u32p, _u8p,
+         ctypes.POINTER(_vp))
+    _sig("vhip_ivfpq_search_batch", _int, _vp, _f32p, _sz, _sz, _sz, _u32p, _f32p, _szp)
+    _sig("vhip_ivfpq_search_batch_device", _int, _vp, _vp, _sz, _sz, _sz, _vp, _vp, _vp)
+    _sig("vhip_ivfpq_probe", _int, _vp, _f32p, _sz, _sz, _u32p)
+    _sig("vhip_ivfpq_info", _int, _vp, ctypes.POINTER(_IvfPqDescC))
+    _sig("vhip_ivfpq_export", _int, _vp, _f32p, _f32p, _u32p, _u32p, _u8p)
+    _sig("vhip_ivfpq_profile", _int, _vp, _int)
+    _sig("vhip_ivfpq_profile_read", _int, _vp, _dblp, _u64p)
+    _sig("vhip_ivfpq_destroy", None, _vp)
+    _sig("vhip_ivfpq_file_save", _int, ctypes.c_char_p, _cfgp, _sz, _int, _f32p, _sz, _f32p, _sz, _u32p, _sz, _u32p,
+         _u8p)
+    _sig("vhip_ivfpq_file_info", _int, ctypes.c_char_p, _cfgp, _szp, ctypes.POINTER(_int), _szp, _szp, _szp, _szp)
+    _sig("vhip_ivfpq_file_load", _int, ctypes.c_char_p, _f32p, _f32p, _u32p, _u32p, _u8p)
 _sig("vhip_vecrstor_write", _int, ctypes.c_char_p, _f32p, _sz, _sz)
 _sig("vhip_vecrstor_open", _int, ctypes.c_char_p, _szp, _szp)
 _sig("vhip_vecrstor_read", _int, ctypes.c_char_p, _f32p, _sz, _sz)
@@ -157,7 +193,24 @@ class InvalidConfig(CudaError):
     code = -5
 
 
-_ERRORS = {c.code: c for c in (DeviceNotFound, DriverError, HardwareNotAvailable, InvalidConfig)}
+class EmptyIndex(CudaError):
+    """vector-index VectorIndexError::EmptyIndex (types.rs)."""
+
+    code = -6
+
+
+class DimensionMismatch(CudaError):
+    """vector-index VectorIndexError::DimensionMismatch{expected, got} (types.rs)."""
+
+    code = -5
+
+    def __init__(self, expected: int, got: int):
+        super().__init__(f"dimension mismatch: expected {expected}, got {got}")
+        self.expected = expected
+        self.got = got
+
+
+_ERRORS = {c.code: c for c in (DeviceNotFound, DriverError, HardwareNotAvailable, InvalidConfig, EmptyIndex)}
 
 
 def _check(status: int):
@@ -768,6 +821,461 @@ def train_from_shards(data_dir, k: int = 64, max_iters: int = 30, tolerance: flo
     _check(_lib.vhip_train_from_shards(_path(data_dir), k, max_iters, float(tolerance), int(metric), num_gpus,
                                        output.encode(), seed, ctypes.byref(res), ctypes.byref(ns)))
     return (int(res.dimension), int(res.k), int(res.iterations), float(res.inertia)), int(ns.value)
+
+
+# ---- product quantization and the IVF-PQ index (vector-index/src/ivf) -------------------
+@dataclasses.dataclass
+class IvfPqConfig:
+    """IvfPqConfig (ivf/config.rs:25-154): defaults of config.rs:6-21, builder methods, validate."""
+
+    nlist: int = 64
+    nprobe: int = 8
+    num_subvectors: int = 8
+    sub_clusters: int = 256
+    max_kmeans_iters: int = 25
+    kmeans_tolerance: float = 1e-4
+    max_train_points: Optional[int] = None
+
+    def __post_init__(self):
+        self.kmeans_tolerance = float(np.float32(self.kmeans_tolerance))  # an f32 field in the reference
+
+    @classmethod
+    def new(cls, nlist: int, nprobe: int, num_subvectors: int) -> "IvfPqConfig":
+        return cls(nlist=nlist, nprobe=nprobe, num_subvectors=num_subvectors)
+
+    def with_sub_clusters(self, sub_clusters: int) -> "IvfPqConfig":
+        return dataclasses.replace(self, sub_clusters=sub_clusters)
+
+    def with_max_kmeans_iters(self, iters: int) -> "IvfPqConfig":
+        return dataclasses.replace(self, max_kmeans_iters=iters)
+
+    def with_kmeans_tolerance(self, tol: float) -> "IvfPqConfig":
+        return dataclasses.replace(self, kmeans_tolerance=tol)
+
+    def with_max_train_points(self, max_points: Optional[int]) -> "IvfPqConfig":
+        return dataclasses.replace(self, max_train_points=max_points)
+
+    def sub_dimension(self, dimension: int) -> int:
+        return dimension // self.num_subvectors if self.num_subvectors else 0
+
+    def _c(self) -> "_IvfPqConfigC":
+        for f in ("nlist", "nprobe", "num_subvectors", "sub_clusters", "max_kmeans_iters"):
+            if getattr(self, f) < 0:
+                raise InvalidConfig(f"{f} must be non-negative")
+        return _IvfPqConfigC(self.nlist, self.nprobe, self.num_subvectors, self.sub_clusters, self.max_kmeans_iters,
+                             float(self.kmeans_tolerance), self.max_train_points or 0)
+
+    @classmethod
+    def _from_c(cls, c) -> "IvfPqConfig":
+        return cls(int(c.nlist), int(c.nprobe), int(c.num_subvectors), int(c.sub_clusters), int(c.max_kmeans_iters),
+                   float(c.kmeans_tolerance), int(c.max_train_points) or None)
+
+    def validate(self, dimension: int) -> None:
+        """config.rs:96-147: raises InvalidConfig with the reference's reason."""
+        c = self._c()
+        _check(_lib.vhip_ivfpq_config_validate(ctypes.byref(c), dimension))
+
+
+class ProductQuantizer:
+    """ProductQuantizer (ivf/pq.rs:12-293): M codebooks of Ks sub-centroids over D / M dimensions.
+    train / encode_batch / compute_adc_lut run on the GPU; decode and compute_distance_with_lut
+    are the reference's host helpers."""
+
+    def __init__(self, dimension: int, num_subvectors: int, sub_clusters: int, codebooks, ordinal: int = 0):
+        if num_subvectors == 0 or dimension % num_subvectors:
+            raise InvalidConfig(f"vector dimension ({dimension}) must be divisible by num_subvectors "
+                                f"({num_subvectors})")
+        cb = np.ascontiguousarray(codebooks, dtype=np.float32).reshape(-1)
+        ds = dimension // num_subvectors
+        if cb.size != num_subvectors * sub_clusters * ds:  # pq.rs:38-41
+            raise InvalidConfig("codebooks must hold num_subvectors x sub_clusters x sub_dimension floats")
+        self.dimension = dimension
+        self.num_subvectors = num_subvectors
+        self.sub_dimension = ds
+        self.sub_clusters = sub_clusters
+        self.codebooks = cb
+        self.ordinal = ordinal
+
+    @classmethod
+    def new(cls, dimension: int, num_subvectors: int, sub_clusters: int, codebooks) -> "ProductQuantizer":
+        return cls(dimension, num_subvectors, sub_clusters, codebooks)
+
+    @classmethod
+    def train(cls, data, dimension: int, num_subvectors: int, sub_clusters: int, max_iters: int, tolerance: float,
+              metric=DistanceMetric.L2Squared, seed: int = 42, init_codebooks=None,
+              ordinal: int = 0) -> "ProductQuantizer":
+        """pq.rs:53-107 (sub-space k-means on the GPU; seeded init, or init_codebooks)."""
+        x = _rows(data, dimension) if np.asarray(data).size else np.zeros((0, dimension), np.float32)
+        if num_subvectors == 0 or dimension % num_subvectors:
+            raise InvalidConfig(f"vector dimension ({dimension}) must be divisible by num_subvectors "
+                                f"({num_subvectors})")
+        cb = np.zeros(num_subvectors * sub_clusters * (dimension // num_subvectors), np.float32)
+        ini = None if init_codebooks is None else np.ascontiguousarray(init_codebooks, dtype=np.float32).reshape(-1)
+        if ini is not None and ini.size != cb.size:
+            raise InvalidConfig("init_codebooks must hold num_subvectors x sub_clusters x sub_dimension floats")
+        _check(_lib.vhip_pq_train(ordinal, _p(x, _f32p), x.shape[0], dimension, num_subvectors, sub_clusters,
+                                  max_iters, float(tolerance), int(metric), _p(ini, _f32p) if ini is not None else None,
+                                  seed, _p(cb, _f32p)))
+        return cls(dimension, num_subvectors, sub_clusters, cb, ordinal)
+
+    train_sequential = train  # pq.rs:112-165: the same result, one sub-space after another
+
+    def get_sub_centroid(self, m: int, k: int) -> np.ndarray:
+        s = (m * self.sub_clusters + k) * self.sub_dimension
+        return self.codebooks[s:s + self.sub_dimension]
+
+    def encode_batch(self, data, metric=DistanceMetric.L2Squared) -> np.ndarray:
+        """pq.rs:203-214: codes [n, M] uint8."""
+        x = _rows(data, self.dimension) if np.asarray(data).size else np.zeros((0, self.dimension), np.float32)
+        out = np.zeros((x.shape[0], self.num_subvectors), np.uint8)
+        _check(_lib.vhip_pq_encode(self.ordinal, _p(self.codebooks, _f32p), self.dimension, self.num_subvectors,
+                                   self.sub_clusters, int(metric), _p(x, _f32p), x.shape[0], _p(out, _u8p)))
+        return out
+
+    def encode(self, vector, metric=DistanceMetric.L2Squared) -> np.ndarray:
+        """pq.rs:178-200."""
+        v = np.asarray(vector, np.float32).reshape(-1)
+        if v.size != self.dimension:
+            raise DimensionMismatch(self.dimension, v.size)
+        return self.encode_batch(v.reshape(1, -1), metric)[0]
+
+    def decode(self, code) -> np.ndarray:
+        """pq.rs:217-229."""
+        c = np.asarray(code, np.uint8).reshape(-1)
+        if c.size != self.num_subvectors:
+            raise InvalidConfig("code length must equal num_subvectors")
+        return np.concatenate([self.get_sub_centroid(m, int(c[m])) for m in range(self.num_subvectors)])
+
+    def compute_adc_lut_batch(self, queries, metric=DistanceMetric.L2Squared) -> np.ndarray:
+        """compute_adc_lut for a batch: [nq, M * Ks]."""
+        q = _rows(queries, self.dimension)
+        lut = np.zeros((q.shape[0], self.num_subvectors * self.sub_clusters), np.float32)
+        _check(_lib.vhip_pq_adc_lut(self.ordinal, _p(self.codebooks, _f32p), self.dimension, self.num_subvectors,
+                                    self.sub_clusters, int(metric), _p(q, _f32p), q.shape[0], _p(lut, _f32p)))
+        return lut
+
+    def compute_adc_lut(self, query, metric=DistanceMetric.L2Squared) -> np.ndarray:
+        """pq.rs:233-266: lut[m * Ks + k]."""
+        q = np.asarray(query, np.float32).reshape(-1)
+        if q.size != self.dimension:
+            raise DimensionMismatch(self.dimension, q.size)
+        return self.compute_adc_lut_batch(q.reshape(1, -1), metric)[0]
+
+    def compute_distance_with_lut(self, code, lut) -> float:
+        """pq.rs:270-293: quads summed as (d0 + d1) + (d2 + d3), then the remainder, in f32."""
+        c = np.asarray(code, np.uint8).reshape(-1)
+        t = np.asarray(lut, np.float32).reshape(-1)
+        ks = self.sub_clusters
+        total = np.float32(0.0)
+        m = 0
+        while m + 4 <= c.size:
+            d = [t[(m + j) * ks + int(c[m + j])] for j in range(4)]
+            total = np.float32(total + np.float32(np.float32(d[0] + d[1]) + np.float32(d[2] + d[3])))
+            m += 4
+        while m < c.size:
+            total = np.float32(total + t[m * ks + int(c[m])])
+            m += 1
+        return float(total)
+
+    def __eq__(self, other):
+        return (isinstance(other, ProductQuantizer) and
+                (self.dimension, self.num_subvectors, self.sub_clusters) ==
+                (other.dimension, other.num_subvectors, other.sub_clusters) and
+                np.array_equal(self.codebooks, other.codebooks))
+
+
+@dataclasses.dataclass
+class InvertedList:
+    """ivf/inverted_list.rs:8-56: ids and M-byte codes of one coarse cluster."""
+
+    ids: np.ndarray
+    codes: np.ndarray  # [len, M] uint8
+
+    def __len__(self) -> int:
+        return int(self.ids.size)
+
+    def len(self) -> int:
+        return len(self)
+
+    def is_empty(self) -> bool:
+        return self.ids.size == 0
+
+    def get_code(self, index: int, num_subvectors: int) -> np.ndarray:
+        return self.codes.reshape(-1)[index * num_subvectors:(index + 1) * num_subvectors]
+
+    def __eq__(self, other):
+        return (isinstance(other, InvertedList) and np.array_equal(self.ids, other.ids) and
+                np.array_equal(self.codes.reshape(-1), other.codes.reshape(-1)))
+
+
+class InvertedIndex:
+    """ivf/inverted_list.rs:58-120 (host view of an index's lists)."""
+
+    def __init__(self, nlist: int, num_subvectors: int):
+        self.lists = [InvertedList(np.zeros(0, np.uint32), np.zeros((0, num_subvectors), np.uint8))
+                      for _ in range(nlist)]
+        self.num_subvectors = num_subvectors
+        self._total = 0
+
+    def add(self, cluster_id: int, id: int, code) -> None:
+        c = np.asarray(code, np.uint8).reshape(1, -1)
+        if c.shape[1] != self.num_subvectors:
+            raise InvalidConfig("code length must equal num_subvectors")
+        L = self.lists[cluster_id]
+        self.lists[cluster_id] = InvertedList(np.append(L.ids, np.uint32(id)), np.vstack([L.codes, c]))
+        self._total += 1
+
+    def total_vectors(self) -> int:
+        return self._total
+
+    def nlist(self) -> int:
+        return len(self.lists)
+
+    def get_list(self, cluster_id: int) -> InvertedList:
+        return self.lists[cluster_id]
+
+    def _csr(self):
+        sizes = np.array([len(L) for L in self.lists], np.uint32)
+        ids = np.concatenate([L.ids for L in self.lists]).astype(np.uint32) if self.lists else np.zeros(0, np.uint32)
+        codes = (np.concatenate([L.codes.reshape(-1, self.num_subvectors) for L in self.lists]).astype(np.uint8)
+                 if self.lists else np.zeros((0, self.num_subvectors), np.uint8))
+        return sizes, np.ascontiguousarray(ids), np.ascontiguousarray(codes)
+
+    @classmethod
+    def from_csr(cls, sizes, ids, codes, num_subvectors) -> "InvertedIndex":
+        """Lists from CSR parts: list c holds sizes[c] consecutive entries of ids / codes."""
+        ix = cls(0, num_subvectors)
+        codes = np.asarray(codes, np.uint8).reshape(-1, num_subvectors)
+        off = 0
+        for n in sizes.tolist():
+            ix.lists.append(InvertedList(ids[off:off + n].copy(), codes[off:off + n].reshape(n, num_subvectors).copy()))
+            off += n
+        ix._total = off
+        return ix
+
+    def __eq__(self, other):
+        return (isinstance(other, InvertedIndex) and self.num_subvectors == other.num_subvectors and
+                self._total == other._total and self.lists == other.lists)
+
+
+class IvfPqSerializer:
+    """ivf/serializer.rs:23-254 (IVFPQVEC files)."""
+
+    @staticmethod
+    def save_to_file(path, config: IvfPqConfig, coarse_centroids, pq: ProductQuantizer,
+                     inverted_index: InvertedIndex, dimension: int, metric) -> None:
+        c = config._c()
+        cc = np.ascontiguousarray(coarse_centroids, dtype=np.float32).reshape(-1)
+        sizes, ids, codes = inverted_index._csr()
+        _check(_lib.vhip_ivfpq_file_save(_path(path), ctypes.byref(c), dimension, int(metric), _p(cc, _f32p),
+                                         cc.size // max(dimension, 1), _p(pq.codebooks, _f32p), pq.codebooks.size,
+                                         _p(sizes, _u32p), sizes.size, _p(ids, _u32p), _p(codes, _u8p)))
+
+    @staticmethod
+    def load_from_file(path):
+        """(config, coarse_centroids, pq, inverted_index, dimension, metric)."""
+        c = _IvfPqConfigC()
+        d, nc, cbl, nl, tot = (ctypes.c_size_t() for _ in range(5))
+        m = _int()
+        _check(_lib.vhip_ivfpq_file_info(_path(path), ctypes.byref(c), ctypes.byref(d), ctypes.byref(m),
+                                         ctypes.byref(nc), ctypes.byref(cbl), ctypes.byref(nl), ctypes.byref(tot)))
+        cfg = IvfPqConfig._from_c(c)
+        coarse = np.zeros(nc.value * d.value, np.float32)
+        cb = np.zeros(cbl.value, np.float32)
+        sizes = np.zeros(nl.value, np.uint32)
+        ids = np.zeros(max(tot.value, 1), np.uint32)
+        codes = np.zeros(max(tot.value * cfg.num_subvectors, 1), np.uint8)
+        _check(_lib.vhip_ivfpq_file_load(_path(path), _p(coarse, _f32p), _p(cb, _f32p), _p(sizes, _u32p),
+                                         _p(ids, _u32p), _p(codes, _u8p)))
+        pq = ProductQuantizer(d.value, cfg.num_subvectors, cfg.sub_clusters, cb)
+        inv = InvertedIndex.from_csr(sizes, ids[:tot.value], codes[:tot.value * cfg.num_subvectors],
+                                      cfg.num_subvectors)
+        return cfg, coarse, pq, inv, d.value, DistanceMetric(m.value)
+
+
+def _storage_rows(storage, dimension: Optional[int] = None) -> np.ndarray:
+    if isinstance(storage, MmapStorage):
+        return storage.as_raw_slice().reshape(-1, storage.dimension()) if len(storage) else np.zeros(
+            (0, storage.dimension()), np.float32)
+    a = np.asarray(storage, dtype=np.float32)
+    if a.size == 0:
+        return np.zeros((0, dimension or (a.shape[1] if a.ndim == 2 else 0)), np.float32)
+    return _rows(a, dimension)
+
+
+class IvfPqIndex:
+    """IvfPqIndex (ivf/mod.rs:63-449) on one GPU: coarse centroids, product quantizer and
+    inverted lists resident in device memory.  `storage` is an MmapStorage or an [n, d] array."""
+
+    def __init__(self, handle, storage, config: IvfPqConfig, metric):
+        self._h = handle
+        self._storage = storage
+        self._config = config
+        self._metric = DistanceMetric(int(metric))
+        info = _IvfPqDescC()
+        _check(_lib.vhip_ivfpq_info(handle, ctypes.byref(info)))
+        self._info = info
+        self._parts = None
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h:
+            _lib.vhip_ivfpq_destroy(h)
+            self._h = None
+
+    # ---- construction (ivf/mod.rs:76-165) ----
+    @classmethod
+    def build(cls, storage, metric=DistanceMetric.L2Squared, dimension: Optional[int] = None, seed: int = 42,
+              ordinal: int = 0) -> "IvfPqIndex":
+        return cls.build_with_config(storage, IvfPqConfig(), metric, dimension, seed, ordinal)
+
+    @classmethod
+    def build_with_config(cls, storage, config: IvfPqConfig, metric=DistanceMetric.L2Squared,
+                          dimension: Optional[int] = None, seed: int = 42, ordinal: int = 0) -> "IvfPqIndex":
+        x = _storage_rows(storage, dimension)
+        c = config._c()
+        h = _vp()
+        _check(_lib.vhip_ivfpq_build(ordinal, _p(x, _f32p), x.shape[0], x.shape[1], ctypes.byref(c), int(metric), seed,
+                                     ctypes.byref(h)))
+        return cls(h, storage, config, metric)
+
+    build_parallel_with_config = build_with_config
+    build_sequential_with_config = build_with_config  # ivf/mod.rs:173-248: the same index
+
+    @classmethod
+    def build_sequential(cls, storage, metric=DistanceMetric.L2Squared, **kw) -> "IvfPqIndex":
+        return cls.build(storage, metric, **kw)
+
+    @classmethod
+    def from_parts(cls, storage, config: IvfPqConfig, coarse_centroids, pq: ProductQuantizer,
+                   inverted_index: InvertedIndex, dimension: int, metric, ordinal: int = 0) -> "IvfPqIndex":
+        cc = np.ascontiguousarray(coarse_centroids, dtype=np.float32).reshape(-1)
+        sizes, ids, codes = inverted_index._csr()
+        c = config._c()
+        h = _vp()
+        _check(_lib.vhip_ivfpq_create(ordinal, dimension, int(metric), ctypes.byref(c), _p(cc, _f32p),
+                                      cc.size // max(dimension, 1), _p(pq.codebooks, _f32p), _p(sizes, _u32p),
+                                      _p(ids, _u32p), _p(codes, _u8p), ctypes.byref(h)))
+        return cls(h, storage, config, metric)
+
+    # ---- search (ivf/mod.rs:251-345) ----
+    def search(self, query, k: int) -> List[SearchResult]:
+        return self.search_with_nprobe(query, k, self._config.nprobe)
+
+    def search_with_nprobe(self, query, k: int, nprobe: int) -> List[SearchResult]:
+        q = np.asarray(query, np.float32).reshape(-1)
+        if q.size != self.dimension():
+            raise DimensionMismatch(self.dimension(), q.size)
+        return self.search_batch(q.reshape(1, -1), k, nprobe)[0]
+
+    def search_batch(self, queries, k: int, nprobe: Optional[int] = None) -> List[List[SearchResult]]:
+        ids, dist, lens = self.search_batch_arrays(queries, k, nprobe)
+        return _to_lists(ids, dist, lens)
+
+    def search_batch_arrays(self, queries, k: int, nprobe: Optional[int] = None):
+        """(ids [nq, k] uint32, dist [nq, k] float32, lens [nq])."""
+        q = _rows(queries, self.dimension())
+        nq = q.shape[0]
+        w = max(k, 1)
+        ids = np.empty((max(nq, 1), w), np.uint32)
+        dist = np.empty((max(nq, 1), w), np.float32)
+        lens = np.zeros(max(nq, 1), np.uintp)
+        np_ = self._config.nprobe if nprobe is None else nprobe
+        _check(_lib.vhip_ivfpq_search_batch(self._h, _p(q, _f32p), nq, k, np_, _p(ids, _u32p), _p(dist, _f32p),
+                                            lens.ctypes.data_as(_szp)))
+        return ids[:nq, :k], dist[:nq, :k], lens[:nq]
+
+    def search_batch_device(self, d_queries: int, nq: int, k: int, nprobe: int, d_ids: int, d_dist: int,
+                            d_len: int) -> None:
+        _check(_lib.vhip_ivfpq_search_batch_device(self._h, d_queries, nq, k, nprobe, d_ids, d_dist, d_len))
+
+    def probe(self, queries, nprobe: int) -> np.ndarray:
+        """The coarse lists the search scans: [nq, min(max(nprobe, 1), nlist)], best first."""
+        q = _rows(queries, self.dimension())
+        w = max(1, min(nprobe, self.nlist()))
+        out = np.empty((max(q.shape[0], 1), w), np.uint32)
+        _check(_lib.vhip_ivfpq_probe(self._h, _p(q, _f32p), q.shape[0], nprobe, _p(out, _u32p)))
+        return out[:q.shape[0]]
+
+    def profile(self, enable: bool = True) -> None:
+        _check(_lib.vhip_ivfpq_profile(self._h, 1 if enable else 0))
+
+    def profile_read(self):
+        ms = ctypes.c_double()
+        n = ctypes.c_uint64()
+        _check(_lib.vhip_ivfpq_profile_read(self._h, ctypes.byref(ms), ctypes.byref(n)))
+        return {"kernel_ms": ms.value, "launches": n.value}
+
+    @staticmethod
+    def evaluate_recall(ground_truth, results) -> float:
+        """ivf/mod.rs:358-372."""
+        if not ground_truth or not results:
+            return 0.0
+        k = min(len(ground_truth), len(results))
+        gt = {r.id for r in list(ground_truth)[:k]}
+        return sum(1 for r in list(results)[:k] if r.id in gt) / k
+
+    # ---- persistence (ivf/mod.rs:375-408) ----
+    def _export(self):
+        if self._parts is None:
+            i = self._info
+            cc = np.zeros(i.nlist * i.dimension, np.float32)
+            cb = np.zeros(i.num_subvectors * i.sub_clusters * (i.dimension // i.num_subvectors), np.float32)
+            sizes = np.zeros(i.nlist, np.uint32)
+            ids = np.zeros(max(i.num_vectors, 1), np.uint32)
+            codes = np.zeros((max(i.num_vectors, 1), i.num_subvectors), np.uint8)
+            _check(_lib.vhip_ivfpq_export(self._h, _p(cc, _f32p), _p(cb, _f32p), _p(sizes, _u32p), _p(ids, _u32p),
+                                          _p(codes, _u8p)))
+            self._parts = (cc, cb, sizes, ids[:i.num_vectors], codes[:i.num_vectors])
+        return self._parts
+
+    def save_to_file(self, path) -> None:
+        IvfPqSerializer.save_to_file(path, self._config, self.coarse_centroids(), self.pq(), self.inverted_index(),
+                                     self.dimension(), self._metric)
+
+    @classmethod
+    def load_from_file(cls, storage, path, ordinal: int = 0) -> "IvfPqIndex":
+        cfg, coarse, pq, inv, dim, metric = IvfPqSerializer.load_from_file(path)
+        sd = storage.dimension() if isinstance(storage, MmapStorage) else _storage_rows(storage).shape[1]
+        if sd != dim:
+            raise DimensionMismatch(sd, dim)
+        return cls.from_parts(storage, cfg, coarse, pq, inv, dim, metric, ordinal)
+
+    # ---- getters (ivf/mod.rs:411-449) ----
+    def storage(self):
+        return self._storage
+
+    def config(self) -> IvfPqConfig:
+        return self._config
+
+    def metric(self) -> DistanceMetric:
+        return self._metric
+
+    def dimension(self) -> int:
+        return int(self._info.dimension)
+
+    def nlist(self) -> int:
+        return int(self._info.nlist)
+
+    def __len__(self) -> int:
+        return int(self._info.num_vectors)
+
+    def len(self) -> int:
+        return len(self)
+
+    def is_empty(self) -> bool:
+        return len(self) == 0
+
+    def coarse_centroids(self) -> np.ndarray:
+        return self._export()[0]
+
+    def pq(self) -> ProductQuantizer:
+        i = self._info
+        return ProductQuantizer(i.dimension, i.num_subvectors, i.sub_clusters, self._export()[1])
+
+    def inverted_index(self) -> InvertedIndex:
+        _, _, sizes, ids, codes = self._export()
+        return InvertedIndex.from_csr(sizes, ids, codes, int(self._info.num_subvectors))
 
 
 # ---- device memory for callers that stage their own inputs ----------------------------
