@@ -13,7 +13,7 @@ launch time, measured with HIP events on the engine's stream over the timed regi
 knn.rs:312-377, AVX-512 dispatch as vector-simd) timed on this host on a bounded query sample.
 
 Other workloads: --workload cos768 | kmeans | hamming | l1 | linf | gauss (see WORKLOADS), ivf_coarse
-(the IVF coarse quantizer), copy (counter calibration).
+(the IVF coarse quantizer), ivfpq (IVF-PQ search), copy (counter calibration).
 """
 import argparse
 import json
@@ -261,6 +261,97 @@ def bench_ivf_coarse(vh, steps, warmup, with_cpu):
     return out
 
 
+def bench_ivfpq(vh, steps, warmup, with_cpu):
+    """IVF-PQ search (ivf/mod.rs:256-345): 1,000,000 x 128 base drawn U[-1, 1] like the
+    reference's ivf_bench generator, squared L2, nlist 1024, 16 sub-spaces of 256 sub-centroids,
+    nprobe 32, 10,000 queries, k = 10.  One step = one batch search with queries resident
+    (coarse probe + ADC scan); the roofline is the ADC scan kernel's."""
+    from vector_hip import datasets as ds
+
+    n, d, nlist, m_sub, ks, nprobe, nq, k = 1_000_000, 128, 1024, 16, 256, 32, 10_000, 10
+    log(f"ivfpq: generating {n} x {d} U[-1, 1]")
+    base = ds.uniform(n, d, ds.SEED_BASE)
+    q = ds.uniform(nq, d, ds.SEED_QUERIES)
+    cfg = vh.IvfPqConfig.new(nlist, nprobe, m_sub).with_sub_clusters(ks).with_max_kmeans_iters(10)
+    t0 = time.perf_counter()
+    ix = vh.IvfPqIndex.build_with_config(base, cfg, vh.DistanceMetric.L2Squared)
+    build_s = time.perf_counter() - t0
+    log(f"  build {build_s:.2f} s")
+    dq = vh.DeviceBuffer.from_host(q)
+    di = vh.DeviceBuffer(nq * k * 4)
+    dd = vh.DeviceBuffer(nq * k * 4)
+    dl = vh.DeviceBuffer(nq * 4)
+
+    def step():
+        ix.search_batch_device(dq.ptr, nq, k, nprobe, di.ptr, dd.ptr, dl.ptr)
+
+    for _ in range(warmup):
+        step()
+    ix.profile(True)
+    vh.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        step()
+        log(f"  step {i + 1}/{steps} done")
+    vh.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    prof = ix.profile_read()
+    ids = di.to_host(np.empty((nq, k), np.uint32))
+    # algorithmic work of one scan launch: every (query, probed list) builds an M x Ks table over
+    # D dimensions (a subtract and a multiply-add per element), every scanned code does M table
+    # lookups and M adds
+    probes = ix.probe(q, nprobe)
+    sizes = np.array([len(L) for L in ix.inverted_index().lists], np.int64)
+    scanned = int(sizes[probes].sum())
+    pairs = int((sizes[probes] > 0).sum())
+    work = pairs * 2.0 * ks * d + scanned * 2.0 * m_sub
+    prof_full = {"kernel_ms": prof["kernel_ms"], "launches": prof["launches"], "work": work * prof["launches"],
+                 "bytes": scanned * (m_sub + 0.0) * prof["launches"]}
+    rl = roofline(prof_full, "valu", PEAK_VALU32, "TFLOP/s", "ivfpq")
+    if rl:
+        rl["unit"] = "Top/s"
+        rl["work_note"] = ("VALU/LDS ops per launch: 2*Ks*D per (query, probed list) table + 2*M per scanned code; "
+                           f"{pairs} tables, {scanned} codes")
+    # recall@10 against the exact kNN
+    eid = vh.CudaKnnEngine(base, d, vh.DistanceMetric.L2Squared).search_batch_arrays(q, k)[0]
+    recall = round(float(np.mean([len(set(ids[i]) & set(eid[i])) / k for i in range(nq)])), 4)
+    out = {"metric": "IVF-PQ queries/sec (1M x 128, nlist 1024, PQ16x256, nprobe 32, k=10)",
+           "value": round(nq * 1e3 / ms, 1), "unit": "queries/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+           "ms_per_step": round(ms, 3), "higher_is_better": True, "scaling": "strong", "vs_baseline": None,
+           "dtype": "f32", "data": "synthetic",
+           "config": {"workload": f"ivfpq_l2_uniform_{n}x{d}_nlist{nlist}_m{m_sub}_ks{ks}_nprobe{nprobe}_q{nq}_k{k}",
+                      "parallelism": "single GPU", "build_s": round(build_s, 2), "recall_at_10": recall,
+                      "codes_scanned_per_query": round(scanned / nq, 1)},
+           "roofline": rl}
+    if with_cpu:
+        import oracle
+
+        # IvfPqIndex::search_with_nprobe is one query on one thread (ivf/mod.rs:256-345)
+        inv = ix.inverted_index()
+        sz, lids, lcodes = inv._csr()
+        off = np.concatenate([[0], np.cumsum(sz)]).astype(np.uint64)
+        cc = ix.coarse_centroids().reshape(-1, d)
+        cb = ix.pq().codebooks
+
+        def run(nsamp):
+            t = time.perf_counter()
+            for i in range(nsamp):
+                pr, _ = oracle.find_top_centroids(q[i], cc, nprobe, "l2")
+                oracle.ivfpq_search(q[i], cc, cb, m_sub, ks, off, lids, lcodes, pr, k, "l2")
+            return time.perf_counter() - t
+
+        sp = 16
+        dt = run(sp)
+        sp = int(min(nq, max(sp, sp * CPU_TARGET_S / max(dt, 1e-6))))
+        dt = run(sp)
+        be = {0: "scalar", 1: "AVX2+FMA", 2: "AVX-512F"}[oracle.detect_backend()]
+        out["cpu_baseline"] = {"value": round(sp / dt, 2), "unit": "queries/s", "cores": 1, "kind": "port",
+                               "sample": f"{sp} of the {nq} queries through the oracle's find_top_centroids + "
+                                         f"search_with_nprobe on the built index, {be} backend, {dt:.2f} s on "
+                                         f"1 thread ({cpu_model()})"}
+    return out
+
+
 def bench_copy(vh, nbytes=1 << 30, reps=5):
     """Plain device-to-device copy of `nbytes` (the runtime's blit kernel).  Its FETCH_SIZE and
     WRITE_SIZE counters calibrate the HBM traffic figures of the other kernels."""
@@ -352,7 +443,7 @@ def main():
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--workload", default="default",
-                    choices=["default", "kmeans", "copy", "ivf_coarse"] + sorted(WORKLOADS))
+                    choices=["default", "kmeans", "copy", "ivf_coarse", "ivfpq"] + sorted(WORKLOADS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -369,6 +460,8 @@ def main():
         out = bench_copy(vh)
     elif args.workload == "ivf_coarse":
         out = bench_ivf_coarse(vh, args.steps, args.warmup, not args.no_cpu)
+    elif args.workload == "ivfpq":
+        out = bench_ivfpq(vh, args.steps, args.warmup, not args.no_cpu)
     elif args.workload == "kmeans":
         r = bench_kmeans(vh, 10, not args.no_cpu)
         out = {"metric": METRIC, "value": r["value"], "unit": r["unit"], "n_gpus": 1, "steps": 10, "warmup": 1,

@@ -198,8 +198,11 @@ def _check_search(vh, oracle, ix, parts, queries, k, nprobe, metric, m_sub, ks, 
         assert np.all(np.diff(gd) <= 0) if hib else np.all(np.diff(gd) >= 0)
 
 
-SHAPES = [  # dim, M, Ks: register path (ds 4/8/32), cached path (ds 2 / 6), code paths 16 / 4 / 1 byte
-    (16, 4, 16), (64, 8, 256), (128, 4, 64), (96, 3, 100), (32, 16, 256), (30, 5, 7), (24, 4, 256)]
+SHAPES = [  # dim, M, Ks: register-held codebooks (ds 4 / 8 / 32 with Ks 256), cached codebooks
+    # (ds 2 / 6 / 32, Ks <= 128), code rows through the DMA rings (M 16 / 32) and through
+    # registers (16-, 4- and 1-byte pieces)
+    (16, 4, 16), (64, 8, 256), (128, 4, 64), (96, 3, 100), (32, 16, 256), (30, 5, 7), (24, 4, 256),
+    (128, 32, 256), (64, 32, 256), (256, 16, 128), (64, 16, 256)]
 
 
 @pytest.mark.parametrize("dim,m_sub,ks", SHAPES)

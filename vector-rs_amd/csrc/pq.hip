@@ -6,91 +6,17 @@
 //    argmin of find_nearest_centroid (ivf/kmeans.rs:262-309) over the sub-space's codebook in LDS;
 //  * compute_adc_lut (pq.rs:233-266): k_pq_lut, one thread per table entry;
 //  * search (ivf/mod.rs:256-345): coarse probe through a kNN engine over the coarse centroids
-//    (k = nprobe, best first), then k_ivfpq_scan: one workgroup per query walks its probed lists
-//    in probe order, builds each list's ADC table in LDS from the query residual (codebooks held
-//    in registers, one sub-centroid column per thread), scores every code with the reference's
-//    summation order (pq.rs:270-293); each wave keeps its own threshold-filtered candidate buffer
-//    in LDS, sorted down to its k best whenever it fills, and the four buffers are sorted together
-//    at the end of the query.
-//
-// Candidate keys are (order-preserving score key << 32) | vector id, so the k best are unique
-// and equal scores are ordered by ascending id.  The reference keeps, among entries that tie at
-// the k-th score, whichever its BinaryHeap keeps; the sets differ only inside such a tie.
+//    (k = nprobe, best first), then the fused ADC scan k_ivfpq_scan (pq_scan.h).
 #include <algorithm>
 #include <cmath>
 #include <memory>
 #include <vector>
 
+#include "pq_scan.h"
 #include "vh_runtime.h"
 
 namespace vh {
 namespace {
-
-// ---- direct-form metric of two short vectors: the formulas of scalar.rs:14-263 -------------
-template <int MT>
-struct Acc {
-    float a = 0.0f, b = 0.0f, e = 0.0f;
-    __device__ __forceinline__ void step(float x, float c) {
-        if constexpr (MT == DOT) {
-            a = fmaf(x, c, a);
-        } else if constexpr (MT == COS) {
-            a = fmaf(x, c, a);
-            b = fmaf(x, x, b);
-            e = fmaf(c, c, e);
-        } else if constexpr (MT == L1) {
-            a += fabsf(x - c);
-        } else if constexpr (MT == MINK) {
-            const float t = fabsf(x - c);
-            a = fmaf(t * t, t, a);
-        } else if constexpr (MT == LINF) {
-            a = fmaxf(a, fabsf(x - c));
-        } else if constexpr (MT == HAMF) {
-            a += fabsf(x - c) > 1e-6f ? 1.0f : 0.0f;
-        } else if constexpr (MT == JACC) {
-            const float ax = fabsf(x), ac = fabsf(c);
-            a += fminf(ax, ac);
-            b += fmaxf(ax, ac);
-        } else if constexpr (MT == HELL) {
-            const float t = sqrtf(fabsf(x)) - sqrtf(fabsf(c));
-            a = fmaf(t, t, a);
-        } else {  // L2, MAHA
-            const float t = x - c;
-            a = fmaf(t, t, a);
-        }
-    }
-    __device__ __forceinline__ float finish() const {
-        if constexpr (MT == COS) {
-            const float den = sqrtf(b) * sqrtf(e);
-            return den <= 1e-9f ? 0.0f : a / den;
-        } else if constexpr (MT == MINK) {
-            return cbrtf(a);
-        } else if constexpr (MT == MAHA) {
-            return sqrtf(a);
-        } else if constexpr (MT == JACC) {
-            return b <= 1e-9f ? 0.0f : 1.0f - a / b;
-        } else if constexpr (MT == HELL) {
-            return sqrtf(0.5f * a);
-        } else {
-            return a;
-        }
-    }
-};
-
-constexpr bool hib_metric(int m) { return m == DOT || m == COS; }
-
-#define VH_METRIC_SWITCH(metric, CALL) \
-    switch (metric) {                  \
-        case L2: CALL(L2); break;      \
-        case DOT: CALL(DOT); break;    \
-        case COS: CALL(COS); break;    \
-        case L1: CALL(L1); break;      \
-        case MINK: CALL(MINK); break;  \
-        case LINF: CALL(LINF); break;  \
-        case HAMF: CALL(HAMF); break;  \
-        case MAHA: CALL(MAHA); break;  \
-        case JACC: CALL(JACC); break;  \
-        default: CALL(HELL); break;    \
-    }
 
 // ---- encode -------------------------------------------------------------------------------
 constexpr int kEncRegDims = 32;          // sub-vector floats held in registers
@@ -164,234 +90,12 @@ __global__ __launch_bounds__(256) void k_pq_lut(const float *__restrict__ qry, l
     lut[t] = acc.finish();
 }
 
-// ---- IVF-PQ scan ------------------------------------------------------------------------------
-constexpr int kScanThreads = 256;
-constexpr int kScanWaves = kScanThreads / 64;
-constexpr int kLutRegs = 128;       // codebook floats per thread in the register layout
-
-struct ScanArgs {
-    const float *qry;          // nq x dim
-    const float *coarse;       // nlist x dim
-    const uint32_t *probes;    // nq x nprobe, best first
-    const uint32_t *list_off;  // nlist + 1
-    const uint32_t *ids;       // n, list order
-    const uint8_t *codes;      // n x m_sub, list order
-    const float *cb;           // m_sub x ks x ds
-    const float *cbt;          // 256 x kLutRegs thread-major register layout (register path)
-    uint32_t *out_ids;         // nq x k
-    float *out_dist;           // nq x k
-    uint32_t *out_len;         // nq
-    int nq, dim, nprobe, nlist, m_sub, ks, ds, k, metric, groups, mg;
-    int capw;                  // candidate slots per wave, a power of two >= k + 64
-};
-
-// Orders LDS accesses of the lanes of one wave (no other wave touches the region).
-__device__ __forceinline__ void wave_sync() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
-// Ascending bitonic sort of s[0, P) (P a power of two) by `nthr` threads with index `tid`;
-// `sync` orders the stages.
-template <class Sync>
-__device__ __forceinline__ void bitonic_sort_u64(unsigned long long *s, int P, int tid, int nthr, Sync sync) {
-    for (int size = 2; size <= P; size <<= 1) {
-        for (int stride = size >> 1; stride > 0; stride >>= 1) {
-            for (int t = tid; t < (P >> 1); t += nthr) {
-                const int lo = 2 * t - (t & (stride - 1));
-                const int hi = lo + stride;
-                const bool asc = (lo & size) == 0;
-                const unsigned long long a = s[lo], b = s[hi];
-                if ((a > b) == asc) {
-                    s[lo] = b;
-                    s[hi] = a;
-                }
-            }
-            sync();
-        }
-    }
-}
-
-// Sorts the wave's `cnt` candidates, keeps the k best and, once k are held, tightens the
-// wave's threshold to the k-th.  cnt and tau are wave-uniform.
-__device__ void wave_compact(unsigned long long *s_w, uint32_t &cnt, unsigned long long &tau, int k) {
-    const int lane = threadIdx.x & 63;
-    int P = 2;
-    while (P < (int)cnt) P <<= 1;
-    for (int t = (int)cnt + lane; t < P; t += 64) s_w[t] = ~0ull;
-    wave_sync();
-    bitonic_sort_u64(s_w, P, lane, 64, wave_sync);
-    if ((int)cnt >= k) tau = s_w[k - 1];
-    cnt = min((int)cnt, k);
-}
-
-// ADC table of one probe: thread t = (group g, sub-centroid j) writes lut[m][j] for the group's
-// sub-spaces.  Register path: DS = sub-dimension, codebook column in cbr.
-template <int MT, int DS>
-__device__ __forceinline__ void lut_build_reg(const ScanArgs &A, const float *s_r, float *s_lut, const float *cbr) {
-    const int g = threadIdx.x / A.ks, j = threadIdx.x - g * A.ks;
-    if (g >= A.groups) return;
-    const int m0 = g * A.mg;
-#pragma unroll
-    for (int ml = 0; ml < kLutRegs / DS; ++ml) {
-        if (ml < A.mg && m0 + ml < A.m_sub) {
-            Acc<MT> acc;
-#pragma unroll
-            for (int d = 0; d < DS; ++d) acc.step(s_r[(m0 + ml) * DS + d], cbr[ml * DS + d]);
-            s_lut[(m0 + ml) * A.ks + j] = acc.finish();
-        }
-    }
-}
-
-template <int MT>
-__device__ __forceinline__ void lut_build_mem(const ScanArgs &A, const float *s_r, float *s_lut) {
-    const int g = threadIdx.x / A.ks, j = threadIdx.x - g * A.ks;
-    if (g >= A.groups) return;
-    const int m0 = g * A.mg, m1 = min(A.m_sub, m0 + A.mg);
-    for (int m = m0; m < m1; ++m) {
-        const float *c = A.cb + ((size_t)m * A.ks + j) * A.ds;
-        Acc<MT> acc;
-        for (int d = 0; d < A.ds; ++d) acc.step(s_r[m * A.ds + d], c[d]);
-        s_lut[m * A.ks + j] = acc.finish();
-    }
-}
-
-__device__ __forceinline__ float adc_quad(const float *L, int ks, uint32_t w) {
-    const float d0 = L[w & 255u];
-    const float d1 = L[ks + ((w >> 8) & 255u)];
-    const float d2 = L[2 * ks + ((w >> 16) & 255u)];
-    const float d3 = L[3 * ks + (w >> 24)];
-    return (d0 + d1) + (d2 + d3);
-}
-
-// compute_distance_with_lut (pq.rs:270-293) of code row `cp`.
-__device__ __forceinline__ float adc_score(const uint8_t *__restrict__ cp, const float *s_lut, int m_sub, int ks) {
-    float total = 0.0f;
-    if ((m_sub & 15) == 0) {
-        const uint4 *c4 = reinterpret_cast<const uint4 *>(cp);
-        const float *L = s_lut;
-        for (int v = 0; v < (m_sub >> 4); ++v) {
-            const uint4 w = c4[v];
-            total += adc_quad(L, ks, w.x);
-            total += adc_quad(L + 4 * ks, ks, w.y);
-            total += adc_quad(L + 8 * ks, ks, w.z);
-            total += adc_quad(L + 12 * ks, ks, w.w);
-            L += 16 * ks;
-        }
-    } else if ((m_sub & 3) == 0) {
-        const uint32_t *c1 = reinterpret_cast<const uint32_t *>(cp);
-        for (int v = 0; v < (m_sub >> 2); ++v) total += adc_quad(s_lut + 4 * v * ks, ks, c1[v]);
-    } else {
-        int m = 0;
-        for (; m + 4 <= m_sub; m += 4) {
-            const float *L = s_lut + m * ks;
-            const float d0 = L[cp[m]], d1 = L[ks + cp[m + 1]], d2 = L[2 * ks + cp[m + 2]], d3 = L[3 * ks + cp[m + 3]];
-            total += (d0 + d1) + (d2 + d3);
-        }
-        for (; m < m_sub; ++m) total += s_lut[m * ks + cp[m]];
-    }
-    return total;
-}
-
-// One workgroup per query (grid-stride over queries).  Each wave scans every fourth run of 64
-// list entries into its own candidate region with its own threshold, so the scan needs no
-// workgroup barrier; the four regions are sorted together at the end of the query.
-// Dynamic LDS: 4 x capw u64 candidates, then the query, the residual and the ADC table.
-template <int MT, int DS>
-__global__ __launch_bounds__(kScanThreads) void k_ivfpq_scan(ScanArgs A) {
-    extern __shared__ unsigned long long s_dyn[];
-    const int capw = A.capw;
-    unsigned long long *s_all = s_dyn;
-    float *s_q = reinterpret_cast<float *>(s_dyn + kScanWaves * capw);
-    float *s_r = s_q + A.dim;
-    float *s_lut = s_r + A.dim;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    unsigned long long *s_w = s_all + wave * capw;
-    const unsigned long long lanes_below = (1ull << lane) - 1ull;
-
-    float cbr[DS > 0 ? kLutRegs : 1];
-    if constexpr (DS > 0) {
-        const float4 *src = reinterpret_cast<const float4 *>(A.cbt + (size_t)threadIdx.x * kLutRegs);
-#pragma unroll
-        for (int v = 0; v < kLutRegs / 4; ++v) {
-            const float4 f = src[v];
-            cbr[4 * v] = f.x;
-            cbr[4 * v + 1] = f.y;
-            cbr[4 * v + 2] = f.z;
-            cbr[4 * v + 3] = f.w;
-        }
-    }
-    constexpr bool hib = hib_metric(MT);
-
-    for (int q = blockIdx.x; q < A.nq; q += gridDim.x) {
-        for (int d = threadIdx.x; d < A.dim; d += kScanThreads) s_q[d] = A.qry[(size_t)q * A.dim + d];
-        uint32_t cnt = 0;
-        unsigned long long tau = ~0ull;
-        for (int p = 0; p < A.nprobe; ++p) {
-            const uint32_t c = A.probes[(size_t)q * A.nprobe + p];
-            if (c >= (uint32_t)A.nlist) continue;  // an unfilled probe slot
-            const uint32_t beg = A.list_off[c], len = A.list_off[c + 1] - beg;
-            if (len == 0) continue;  // ivf/mod.rs:296-298
-            __syncthreads();         // the previous table is no longer read; s_q is written
-            for (int d = threadIdx.x; d < A.dim; d += kScanThreads) s_r[d] = s_q[d] - A.coarse[(size_t)c * A.dim + d];
-            __syncthreads();
-            if constexpr (DS > 0)
-                lut_build_reg<MT, DS>(A, s_r, s_lut, cbr);
-            else
-                lut_build_mem<MT>(A, s_r, s_lut);
-            __syncthreads();
-            for (uint32_t base = (uint32_t)wave * 64; base < len; base += kScanThreads) {
-                if (cnt > (uint32_t)(capw - 64)) wave_compact(s_w, cnt, tau, A.k);
-                const uint32_t i = base + lane;
-                bool pass = false;
-                unsigned long long cand = 0;
-                if (i < len) {
-                    const float total = adc_score(A.codes + (size_t)(beg + i) * A.m_sub, s_lut, A.m_sub, A.ks);
-                    const float hs = (hib ? -total : total) + 0.0f;  // -0 sorts with +0
-                    const uint32_t key = score_key(hs);
-                    if (key <= (uint32_t)(tau >> 32)) {
-                        cand = ((unsigned long long)key << 32) | A.ids[beg + i];
-                        pass = cand < tau;
-                    }
-                }
-                const unsigned long long bal = __ballot(pass);
-                if (pass) s_w[cnt + __popcll(bal & lanes_below)] = cand;
-                cnt += (uint32_t)__popcll(bal);
-            }
-        }
-        for (int t = (int)cnt + lane; t < capw; t += 64) s_w[t] = ~0ull;
-        __syncthreads();
-        bitonic_sort_u64(s_all, kScanWaves * capw, threadIdx.x, kScanThreads, [] { __syncthreads(); });
-        for (int j = threadIdx.x; j < A.k; j += kScanThreads) {
-            const size_t o = (size_t)q * A.k + j;
-            const unsigned long long cnd = s_all[j];
-            if (cnd != ~0ull) {
-                const float hs = key_score((uint32_t)(cnd >> 32));
-                A.out_ids[o] = (uint32_t)cnd;
-                A.out_dist[o] = hib ? -hs : hs;
-            } else {
-                A.out_ids[o] = 0xffffffffu;
-                A.out_dist[o] = __builtin_nanf("");
-            }
-        }
-        if (threadIdx.x == 0) {  // kept entries: the finite prefix of the first k
-            int lo = 0, hi = A.k;
-            while (lo < hi) {
-                const int mid = (lo + hi) >> 1;
-                if (s_all[mid] != ~0ull) lo = mid + 1; else hi = mid;
-            }
-            A.out_len[q] = (uint32_t)lo;
-        }
-        __syncthreads();  // the candidate regions and s_q are reused by the next query
-    }
-}
-
 }  // namespace
 
-// Register-layout eligibility: squared L2, dot or cosine, sub-dimension 4, 8, 16 or 32, and
-// the group's sub-spaces fit kLutRegs floats.  Other shapes build the table from codebooks read
-// through the caches.
+// Register-layout eligibility: squared L2, dot or cosine, sub-dimension 4, 8, 16 or 32, more
+// than 128 sub-centroids (one thread per sub-centroid) and every sub-space's column within
+// kLutRegs floats (dimension <= 128).  Other shapes build the tables from codebooks read through
+// the caches, the threads split into 256 / ks groups of sub-spaces.
 static bool lut_reg_layout(int metric, size_t m_sub, size_t ks, size_t ds, int *groups, int *mg) {
     const int G = (int)(kScanThreads / ks);
     const int Mg = (int)((m_sub + G - 1) / G);
@@ -399,18 +103,34 @@ static bool lut_reg_layout(int metric, size_t m_sub, size_t ks, size_t ds, int *
     *mg = Mg;
     const bool fast_metric = metric == L2 || metric == DOT || metric == COS;
     const bool pow2 = ds == 4 || ds == 8 || ds == 16 || ds == 32;
-    return fast_metric && pow2 && (size_t)Mg * ds <= (size_t)kLutRegs;
+    return fast_metric && pow2 && G == 1 && m_sub * ds <= (size_t)kLutRegs;
 }
 
-// Candidate slots per wave for k results: room for k kept plus one 64-entry step.
+// Candidate slots per wave for k results: room for k kept plus one step of 64 x kScanU entries.
 static int scan_capw(size_t k) {
     int c = 256;
-    while ((size_t)c < k + 64) c <<= 1;
+    while ((size_t)c < k + 64 * kScanU) c <<= 1;
     return c;
 }
 
-static size_t scan_lds_bytes(size_t dim, size_t m_sub, size_t ks, size_t k) {
-    return (size_t)kScanWaves * scan_capw(k) * sizeof(unsigned long long) + (2 * dim + m_sub * ks) * sizeof(float);
+// Sixteen-byte pieces of a code row streamed through the DMA rings (rows of 16 or 32 bytes with
+// 256 sub-centroids), 0 for the register-load path.
+static int scan_nv(size_t m_sub, size_t ks) {
+    return ks != 256 ? 0 : (m_sub == 16 ? 1 : (m_sub == 32 ? 2 : 0));
+}
+
+// LDS of one scan workgroup, dynamic part plus the static rings.
+static size_t scan_lds_total(size_t dim, size_t m_sub, size_t ks, size_t k, int pg) {
+    return scan_lds_bytes(dim, m_sub, ks, scan_capw(k), pg) + (size_t)ring_bytes(scan_nv(m_sub, ks));
+}
+
+// Probes per group: the most (4, 2, 1) whose tables leave room for two workgroups per CU
+// (160 KB of LDS), else 1.
+constexpr size_t kScanLdsPair = 80u * 1024u;
+static int scan_pg(size_t dim, size_t m_sub, size_t ks, size_t k) {
+    for (int pg = kScanWaves; pg > 1; pg >>= 1)
+        if (scan_lds_total(dim, m_sub, ks, k, pg) <= kScanLdsPair) return pg;
+    return 1;
 }
 
 }  // namespace vh
@@ -425,7 +145,8 @@ struct vhip_ivfpq {
     vhip_ivfpq_config cfg{};
     bool reg = false;
     int groups = 1, mg = 1;
-    size_t lds_limit = 65536;  // dynamic LDS bytes per workgroup the device accepts
+    size_t lds_limit = 65536;  // LDS bytes per workgroup the device accepts
+    int cus = 256;             // compute units of the device
     std::vector<float> coarse, codebooks;  // host copies (export / save)
     std::vector<uint32_t> list_off;        // nlist + 1
     std::vector<uint32_t> ids;             // list order
@@ -515,7 +236,8 @@ static int ivfpq_init(vhip_ivfpq *X, int ordinal, size_t dim, int metric, const 
     int lim = 0;
     VH_HIP(hipDeviceGetAttribute(&lim, hipDeviceAttributeMaxSharedMemoryPerBlock, ordinal));
     X->lds_limit = (size_t)lim;
-    if (scan_lds_bytes(dim, m_sub, ks, 1) > X->lds_limit)
+    VH_HIP(hipDeviceGetAttribute(&X->cus, hipDeviceAttributeMultiprocessorCount, ordinal));
+    if (scan_lds_total(dim, m_sub, ks, 1, 1) > X->lds_limit)
         return set_error(VHIP_ERR_INVALID_CONFIG, "ADC table and query exceed the " + std::to_string(lim) +
                                                       " bytes of LDS of a workgroup (" + std::to_string(m_sub) +
                                                       " x " + std::to_string(ks) + " table entries, dimension " +
@@ -600,35 +322,20 @@ static int ivfpq_search_dev(vhip_ivfpq *X, const float *d_q, size_t nq, size_t k
     A.groups = X->groups;
     A.mg = X->mg;
     A.capw = scan_capw(k);
-    const size_t lds = scan_lds_bytes(X->dim, X->m_sub, X->ks, k);
-    if (lds > X->lds_limit)
+    A.pg = scan_pg(X->dim, X->m_sub, X->ks, k);
+    const int nv = scan_nv(X->m_sub, X->ks);
+    const size_t lds = scan_lds_bytes(X->dim, X->m_sub, X->ks, A.capw, A.pg);
+    if (lds + ring_bytes(nv) > X->lds_limit)
         return set_error(VHIP_ERR_INVALID_CONFIG, "k = " + std::to_string(k) + " needs " + std::to_string(lds) +
                                                       " bytes of LDS with this index, the device allows " +
                                                       std::to_string(X->lds_limit));
-    const unsigned grid = (unsigned)std::min<size_t>(nq, 3u * 256u);
     const int t = X->timer.begin(s);
-    const dim3 g(grid), b(kScanThreads);
-#define VH_SCAN(MT, DS) hipLaunchKernelGGL((k_ivfpq_scan<MT, DS>), g, b, lds, s, A)
-#define VH_SCAN_MEM(MT) VH_SCAN(MT, 0)
-#define VH_SCAN_REG(MT)                          \
-    switch (X->ds) {                             \
-        case 4: VH_SCAN(MT, 4); break;           \
-        case 8: VH_SCAN(MT, 8); break;           \
-        case 16: VH_SCAN(MT, 16); break;         \
-        default: VH_SCAN(MT, 32); break;         \
-    }
-    if (!X->reg) {
-        VH_METRIC_SWITCH(X->metric, VH_SCAN_MEM)
-    } else if (X->metric == L2) {
-        VH_SCAN_REG(L2)
-    } else if (X->metric == DOT) {
-        VH_SCAN_REG(DOT)
-    } else {
-        VH_SCAN_REG(COS)
-    }
-#undef VH_SCAN_REG
-#undef VH_SCAN_MEM
-#undef VH_SCAN
+    if (!X->reg)
+        launch_ivfpq_scan_mem(A, nv, X->cus, lds, s);
+    else if (X->metric == L2)
+        launch_ivfpq_scan_l2(A, (int)X->ds, nv, X->cus, lds, s);
+    else
+        launch_ivfpq_scan_ip(A, (int)X->ds, nv, X->cus, lds, s);
     VH_HIP(hipGetLastError());
     // work and bytes are filled in by the caller's accounting (scanned entries are data dependent)
     X->timer.end(t, s, 0.0, 0.0);
