@@ -121,7 +121,8 @@ static int scan_nv(size_t m_sub, size_t ks) {
 
 // LDS of one scan workgroup, dynamic part plus the static rings.
 static size_t scan_lds_total(size_t dim, size_t m_sub, size_t ks, size_t k, int pg) {
-    return scan_lds_bytes(dim, m_sub, ks, scan_capw(k), pg) + (size_t)ring_bytes(scan_nv(m_sub, ks));
+    const int nv = scan_nv(m_sub, ks);
+    return scan_lds_bytes(dim, m_sub, ks, scan_capw(k), pg, nv) + (size_t)ring_bytes(nv) + 3 * kMetaWin * 4;
 }
 
 // Probes per group: the most (4, 2, 1) whose tables leave room for two workgroups per CU
@@ -324,8 +325,8 @@ static int ivfpq_search_dev(vhip_ivfpq *X, const float *d_q, size_t nq, size_t k
     A.capw = scan_capw(k);
     A.pg = scan_pg(X->dim, X->m_sub, X->ks, k);
     const int nv = scan_nv(X->m_sub, X->ks);
-    const size_t lds = scan_lds_bytes(X->dim, X->m_sub, X->ks, A.capw, A.pg);
-    if (lds + ring_bytes(nv) > X->lds_limit)
+    const size_t lds = scan_lds_bytes(X->dim, X->m_sub, X->ks, A.capw, A.pg, nv);
+    if (scan_lds_total(X->dim, X->m_sub, X->ks, k, A.pg) > X->lds_limit)
         return set_error(VHIP_ERR_INVALID_CONFIG, "k = " + std::to_string(k) + " needs " + std::to_string(lds) +
                                                       " bytes of LDS with this index, the device allows " +
                                                       std::to_string(X->lds_limit));

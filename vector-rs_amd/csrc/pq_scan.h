@@ -11,10 +11,11 @@
 // and sorted down to its k best whenever it fills; the four buffers are sorted together at the
 // end of the query.
 //
-// With 256 sub-centroids, code rows of 16 or 32 bytes (NV = 1 or 2 sixteen-byte pieces) stream
-// into a per-wave ring of NB chunks of 64 rows (NB = 8 or 4) with global->LDS DMA (no registers
-// held), NB - 1 chunks ahead of the row being scored; the first NB - 1, which cover a wave's share
-// of a typical list, are issued before the tables are built and land while they are.  A chunk is read only
+// With 256 sub-centroids, code rows of 16 or 32 bytes (NV = 1 or 2 sixteen-byte pieces) and their
+// vector ids stream into a per-wave ring of NB chunks of 64 rows (NB = 6 or 4) with global->LDS DMA
+// (no registers held); chunks are scored two at a time, with NB - 2 chunks issued ahead of the
+// pair being read.  The first NB - 2 are issued before the tables are built and land while they
+// are.  A chunk is read only
 // after an explicit vmcnt wait that leaves exactly the younger DMAs in flight (vector memory
 // loads complete in order), through an inline-asm LDS read: the compiler's own wait insertion
 // would otherwise wait for every DMA in flight before any read of the ring.  Other row sizes are
@@ -36,8 +37,11 @@ constexpr int kScanThreads = 256;
 constexpr int kScanWaves = kScanThreads / 64;
 constexpr int kLutRegs = 128;  // codebook floats per thread in the register layout
 constexpr int kScanU = 2;      // rows per lane per step on the register-load path
-// DMA ring depth in chunks of 64 code rows: 8 chunks of 16-byte rows (8 KB per wave), 4 of 32-byte
-constexpr int ring_chunks(int nv) { return nv == 2 ? 4 : 8; }
+// DMA ring depth in chunks of 64 code rows and ids: 6 chunks of 16-byte rows (7.5 KB per wave), 4
+// of 32-byte rows, so that two workgroups fit in a CU's LDS; at least 4, as chunks are scored in
+// pairs with two more in flight
+constexpr int ring_chunks(int nv) { return nv == 2 ? 4 : 6; }
+static_assert(ring_chunks(1) >= 4 && ring_chunks(2) >= 4, "pairs of chunks with two more in flight");
 
 struct ScanArgs {
     const float *qry;          // nq x dim
@@ -56,8 +60,12 @@ struct ScanArgs {
     int pg;                    // probes per group: 1, 2 or 4
 };
 
-// LDS bytes of the per-wave DMA rings for code rows of NV sixteen-byte pieces.
-constexpr int ring_bytes(int nv) { return kScanWaves * ring_chunks(nv) * nv * 64 * 16; }
+constexpr int kMetaWin = 128;  // probes whose list bounds are staged in LDS at a time
+
+// LDS bytes of the per-wave DMA rings for code rows of NV sixteen-byte pieces and their ids.
+// A ring chunk holds 64 code rows (nv pieces of 64 x 16 bytes) and their 64 vector ids.
+constexpr int ring_chunk_bytes(int nv) { return nv * 1024 + 256; }
+constexpr int ring_bytes(int nv) { return kScanWaves * ring_chunks(nv) * ring_chunk_bytes(nv); }
 
 namespace {
 
@@ -256,19 +264,20 @@ __device__ __forceinline__ float adc_score(const uint8_t *__restrict__ cp, const
 // outstanding, leaving the export and LDS counters unconstrained.
 #define VH_VMCNT(n) (((n) & 15) | (7 << 4) | (15 << 8))
 
-// Waits until at most `younger` (<= ring_chunks(NV) - 2) chunks of NV DMAs each are still in
-// flight: s_waitcnt takes its count as an immediate, hence one case per count.
+// Waits until at most `younger` (<= ring_chunks(NV) - 2) chunks of NV + 1 DMAs each are still
+// in flight: s_waitcnt takes its count as an immediate, hence one case per count.
 template <int NV>
 __device__ __forceinline__ void ring_wait(int younger) {
-    static_assert((ring_chunks(NV) - 2) * NV < 16, "vmcnt immediates stay below 16");
+    constexpr int P = NV + 1;
+    static_assert((ring_chunks(NV) - 2) * P < 16, "vmcnt immediates stay below 16");
     switch (younger) {
         case 0: __builtin_amdgcn_s_waitcnt(VH_VMCNT(0)); break;
-        case 1: __builtin_amdgcn_s_waitcnt(VH_VMCNT(NV)); break;
-        case 2: __builtin_amdgcn_s_waitcnt(VH_VMCNT(2 * NV)); break;
-        case 3: __builtin_amdgcn_s_waitcnt(VH_VMCNT(3 * NV)); break;
-        case 4: __builtin_amdgcn_s_waitcnt(VH_VMCNT(4 * NV)); break;
-        case 5: __builtin_amdgcn_s_waitcnt(VH_VMCNT(5 * NV)); break;
-        default: __builtin_amdgcn_s_waitcnt(VH_VMCNT(6 * NV)); break;
+        case 1: __builtin_amdgcn_s_waitcnt(VH_VMCNT(P)); break;
+        case 2: __builtin_amdgcn_s_waitcnt(VH_VMCNT(2 * P)); break;
+        case 3: __builtin_amdgcn_s_waitcnt(VH_VMCNT(3 * P)); break;
+        case 4: __builtin_amdgcn_s_waitcnt(VH_VMCNT(4 * P)); break;
+        case 5: __builtin_amdgcn_s_waitcnt(VH_VMCNT(5 * P)); break;
+        default: __builtin_amdgcn_s_waitcnt(VH_VMCNT(6 * P)); break;
     }
 }
 
@@ -278,25 +287,44 @@ __device__ __forceinline__ uint4 lds_read16(uint32_t addr) {
     asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(addr) : "memory");
     return v;
 }
+// Reads 4 bytes at LDS byte address `addr` (completed before it returns).
+__device__ __forceinline__ uint32_t lds_read4(uint32_t addr) {
+    uint32_t v;
+    asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(addr) : "memory");
+    return v;
+}
 
-// Offers one scored row to the wave's candidate buffer.
+// Offers one scored list entry (vector id `id`) to the wave's candidate buffer.
 template <bool HIB>
-__device__ __forceinline__ void offer(const ScanArgs &A, float total, bool valid, uint32_t row,
-                                      unsigned long long *s_w, uint32_t &cnt, unsigned long long tau,
-                                      unsigned long long lanes_below) {
+__device__ __forceinline__ void offer(float total, bool valid, uint32_t id, unsigned long long *s_w, uint32_t &cnt,
+                                      unsigned long long tau, unsigned long long lanes_below) {
     bool pass = false;
     unsigned long long cand = 0;
     if (valid) {
         const float hs = (HIB ? -total : total) + 0.0f;  // -0 sorts with +0
-        const uint32_t key = score_key(hs);
-        if (key <= (uint32_t)(tau >> 32)) {
-            cand = ((unsigned long long)key << 32) | A.ids[row];
-            pass = cand < tau;
-        }
+        cand = ((unsigned long long)score_key(hs) << 32) | id;
+        pass = cand < tau;
     }
     const unsigned long long bal = __ballot(pass);
     if (pass) s_w[cnt + __popcll(bal & lanes_below)] = cand;
-    cnt += (uint32_t)__popcll(bal);
+    cnt = __builtin_amdgcn_readfirstlane(cnt + (uint32_t)__popcll(bal));
+}
+
+// Floats of the coarse-row buffer of the DMA path: pg rows, rounded up to whole DMA instructions
+// of one wave (64 lanes x 4 floats).
+__host__ __device__ constexpr int coarse_rows_floats(int pg, int dim) { return (pg * dim + 255) / 256 * 256; }
+
+// Wave 0 copies the coarse rows of probes pc[0, pg) into s_cr (row w at s_cr + w * dim) with
+// global->LDS DMA; an invalid probe copies row 0 (its residual is never used).  dim % 4 == 0.
+__device__ __forceinline__ void coarse_dma(const ScanArgs &A, const uint32_t *pc, float *s_cr, int pg, int lane) {
+    const int pieces = pg * A.dim / 4;
+    for (int i0 = 0; i0 < pieces; i0 += 64) {
+        const int f = min(i0 + lane, pieces - 1);
+        const int w = 4 * f / A.dim, d = 4 * f - w * A.dim;
+        const uint32_t c = pc[w] != 0xffffffffu ? pc[w] : 0u;
+        __builtin_amdgcn_global_load_lds((const void *)(A.coarse + (size_t)c * A.dim + d),
+                                         (__attribute__((address_space(3))) void *)(s_cr + 4 * i0), 16, 0, 0);
+    }
 }
 
 // Scan of one list through the DMA ring (code rows of 16 * NV bytes, 256 sub-centroids): the
@@ -305,6 +333,7 @@ __device__ __forceinline__ void offer(const ScanArgs &A, float total, bool valid
 // a code byte plus an LDS read with the sub-space offset as its immediate.
 struct RingScan {
     const uint8_t *codes;
+    const uint32_t *ids;
     unsigned char *ring;   // this wave's ring (generic pointer into LDS)
     uint32_t ring_lds;     // its LDS byte address
     uint32_t beg, len;
@@ -315,62 +344,114 @@ template <int NV>
 __device__ __forceinline__ void ring_dma(const RingScan &R, int t) {
     const uint32_t i = min((uint32_t)((R.part + t * R.wpl) * 64 + R.lane), R.len - 1);
     const unsigned char *src = R.codes + (size_t)(R.beg + i) * (16 * NV);
-    unsigned char *dst = R.ring + (t % ring_chunks(NV)) * (NV * 1024);
+    unsigned char *dst = R.ring + (t % ring_chunks(NV)) * ring_chunk_bytes(NV);
 #pragma unroll
     for (int v = 0; v < NV; ++v)
         __builtin_amdgcn_global_load_lds((const void *)(src + 16 * v),
                                          (__attribute__((address_space(3))) void *)(dst + v * 1024), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds((const void *)(R.ids + R.beg + i),
+                                     (__attribute__((address_space(3))) void *)(dst + NV * 1024), 4, 0, 0);
 }
 
+// Reads the code pieces and ids of two ring chunks at LDS byte addresses a0 and a1 (lane
+// offsets included) with one wait for all of them.  The outputs are early-clobber: a later read
+// of the block still needs its address after an earlier one has written its result.
+template <int NV>
+__device__ __forceinline__ void lds_read_pair(uint32_t a0, uint32_t a1, uint32_t i0, uint32_t i1, uint4 (&w0)[NV],
+                                              uint4 (&w1)[NV], uint32_t &id0, uint32_t &id1) {
+    if constexpr (NV == 1) {
+        asm volatile(
+            "ds_read_b128 %0, %4\n\t"
+            "ds_read_b128 %1, %5\n\t"
+            "ds_read_b32 %2, %6\n\t"
+            "ds_read_b32 %3, %7\n\t"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(w0[0]), "=&v"(w1[0]), "=&v"(id0), "=&v"(id1)
+            : "v"(a0), "v"(a1), "v"(i0), "v"(i1)
+            : "memory");
+    } else {
+        asm volatile(
+            "ds_read_b128 %0, %6\n\t"
+            "ds_read_b128 %1, %6 offset:1024\n\t"
+            "ds_read_b128 %2, %7\n\t"
+            "ds_read_b128 %3, %7 offset:1024\n\t"
+            "ds_read_b32 %4, %8\n\t"
+            "ds_read_b32 %5, %9\n\t"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(w0[0]), "=&v"(w0[1]), "=&v"(w1[0]), "=&v"(w1[1]), "=&v"(id0), "=&v"(id1)
+            : "v"(a0), "v"(a1), "v"(i0), "v"(i1)
+            : "memory");
+    }
+}
+
+template <int NV>
+__device__ __forceinline__ float ring_score(const float *lut, const uint4 (&w)[NV]) {
+    constexpr int KS = 256;
+    float total = 0.0f;
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+        const uint32_t ww[4] = {w[v].x, w[v].y, w[v].z, w[v].w};
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+            const float *L = lut + (16 * v + 4 * h) * KS;
+            const float d0 = L[ww[h] & 255u], d1 = L[KS + ((ww[h] >> 8) & 255u)];
+            const float d2 = L[2 * KS + ((ww[h] >> 16) & 255u)], d3 = L[3 * KS + (ww[h] >> 24)];
+            total += (d0 + d1) + (d2 + d3);
+        }
+    }
+    return total;
+}
+
+// Chunks are taken two at a time.  Invariant: before the pair (t, t + 1) is read, the chunks
+// below issued = min(t + NB - 2, mine) have been issued; after the read, the next two are.
 template <int NV, int SLOT, bool HIB>
 __device__ __forceinline__ void ring_scan(const ScanArgs &A, const RingScan &R, const float *s_lut0,
                                           unsigned long long *s_w, uint32_t &cnt, unsigned long long &tau, int capw,
                                           unsigned long long lanes_below) {
-    constexpr int M = 16 * NV, KS = 256, NB = ring_chunks(NV);
+    constexpr int M = 16 * NV, KS = 256, NB = ring_chunks(NV), CB = ring_chunk_bytes(NV);
     const float *lut = s_lut0 + SLOT * M * KS;
-    for (int t = 0; t < R.mine; ++t) {
-        if (cnt > (uint32_t)(capw - 64)) wave_compact(s_w, cnt, tau, A.k);
-        ring_wait<NV>(min(NB - 2, R.mine - 1 - t));
-        const uint32_t at = R.ring_lds + (t % NB) * (NV * 1024) + R.lane * 16;
-        uint4 w[NV];
-#pragma unroll
-        for (int v = 0; v < NV; ++v) w[v] = lds_read16(at + v * 1024);
-        if (t + NB - 1 < R.mine) ring_dma<NV>(R, t + NB - 1);
-        float total = 0.0f;
-#pragma unroll
-        for (int v = 0; v < NV; ++v) {
-            const uint32_t ww[4] = {w[v].x, w[v].y, w[v].z, w[v].w};
-#pragma unroll
-            for (int h = 0; h < 4; ++h) {
-                const float *L = lut + (16 * v + 4 * h) * KS;
-                const float d0 = L[ww[h] & 255u], d1 = L[KS + ((ww[h] >> 8) & 255u)];
-                const float d2 = L[2 * KS + ((ww[h] >> 16) & 255u)], d3 = L[3 * KS + (ww[h] >> 24)];
-                total += (d0 + d1) + (d2 + d3);
-            }
-        }
-        const uint32_t i = (uint32_t)((R.part + t * R.wpl) * 64 + R.lane);
-        offer<HIB>(A, total, i < R.len, R.beg + i, s_w, cnt, tau, lanes_below);
+    // wave-uniform loop state in scalar registers: the waits and DMA issues branch uniformly
+    const int mine = __builtin_amdgcn_readfirstlane(R.mine);
+    for (int t = 0; t < mine; t += 2) {
+        if (cnt > (uint32_t)(capw - 128)) wave_compact(s_w, cnt, tau, A.k);
+        const int issued = __builtin_amdgcn_readfirstlane(min(t + NB - 2, mine));
+        const int last = __builtin_amdgcn_readfirstlane(min(t + 1, mine - 1));  // second chunk of the pair
+        ring_wait<NV>(issued - 1 - last);
+        const uint32_t s0 = R.ring_lds + (t % NB) * CB, s1 = R.ring_lds + (last % NB) * CB;
+        uint4 w0[NV], w1[NV];
+        uint32_t id0, id1;
+        lds_read_pair<NV>(s0 + R.lane * 16, s1 + R.lane * 16, s0 + NV * 1024 + R.lane * 4,
+                          s1 + NV * 1024 + R.lane * 4, w0, w1, id0, id1);
+        if (issued < mine) ring_dma<NV>(R, issued);
+        if (issued + 1 < mine) ring_dma<NV>(R, issued + 1);
+        const float tot0 = ring_score<NV>(lut, w0);
+        const float tot1 = ring_score<NV>(lut, w1);
+        const uint32_t i0 = (uint32_t)((R.part + t * R.wpl) * 64 + R.lane);
+        const uint32_t i1 = (uint32_t)((R.part + (t + 1) * R.wpl) * 64 + R.lane);
+        offer<HIB>(tot0, i0 < R.len, id0, s_w, cnt, tau, lanes_below);
+        offer<HIB>(tot1, t + 1 < mine && i1 < R.len, id1, s_w, cnt, tau, lanes_below);
     }
 }
 
-// Dynamic LDS: PG ADC tables, 4 x capw u64 candidates, the query and PG residuals; static LDS:
-// the DMA rings (NV > 0).
+// Dynamic LDS: PG ADC tables, 4 x capw u64 candidates, the query, PG residuals and (NV > 0) the
+// group's coarse rows; static LDS: the DMA rings (NV > 0) and the probe metadata of kMetaWin probes.
 template <int MT, int DS, int NV>
 __global__ __launch_bounds__(kScanThreads) void k_ivfpq_scan(ScanArgs A) {
     extern __shared__ unsigned long long s_dyn[];
     // the rings are their own LDS object: reads of the other LDS data then need no wait for
     // the DMAs in flight
     __shared__ __attribute__((aligned(16))) unsigned char s_ring[NV > 0 ? ring_bytes(NV) : 16];
-    __shared__ uint32_t s_mc[kScanWaves], s_mb[kScanWaves], s_ml[kScanWaves];
+    __shared__ uint32_t s_pc[kMetaWin], s_pb[kMetaWin], s_pl[kMetaWin];  // probe list, begin, length
     const int capw = A.capw, pg = A.pg, tstride = A.m_sub * A.ks;
     float *s_lut = reinterpret_cast<float *>(s_dyn);
     unsigned long long *s_all = reinterpret_cast<unsigned long long *>(s_lut + pg * tstride);
     float *s_q = reinterpret_cast<float *>(s_all + kScanWaves * capw);
     float *s_r = s_q + A.dim;
+    float *s_cr = s_r + pg * A.dim;  // DMA path: the group's coarse rows (coarse_rows_floats)
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int slot = wave % pg, part = wave / pg, wpl = kScanWaves / pg;
     unsigned long long *s_w = s_all + wave * capw;
-    unsigned char *ring = s_ring + wave * (ring_chunks(NV) * NV * 1024);
+    unsigned char *ring = s_ring + wave * (ring_chunks(NV) * ring_chunk_bytes(NV));
     const unsigned long long lanes_below = (1ull << lane) - 1ull;
 
     float cbr[DS > 0 ? kLutRegs : 1];
@@ -392,33 +473,56 @@ __global__ __launch_bounds__(kScanThreads) void k_ivfpq_scan(ScanArgs A) {
         uint32_t cnt = 0;
         unsigned long long tau = ~0ull;
         for (int g0 = 0; g0 < A.nprobe; g0 += pg) {
-            __syncthreads();  // the previous group's tables are no longer read; s_q is written
-            if (threadIdx.x < pg) {
-                const int p = g0 + threadIdx.x;
-                const uint32_t c = p < A.nprobe ? A.probes[(size_t)q * A.nprobe + p] : 0xffffffffu;
-                const bool ok = c < (uint32_t)A.nlist;  // past the last probe, or an unfilled slot
-                const uint32_t beg = ok ? A.list_off[c] : 0u;
-                s_mc[threadIdx.x] = ok ? c : 0xffffffffu;
-                s_mb[threadIdx.x] = beg;
-                s_ml[threadIdx.x] = ok ? A.list_off[c + 1] - beg : 0u;
+            const int wbase = g0 - g0 % kMetaWin;  // pg divides kMetaWin
+            const int w0 = g0 - wbase;               // this group's first probe in the window
+            __syncthreads();  // the previous group's tables, residuals and metadata are no longer read
+            if (w0 == 0) {
+                // probe lists and their bounds for the next kMetaWin probes (ivf/mod.rs:286-298:
+                // empty lists, and slots past the last probe, get length 0)
+                for (int t = threadIdx.x; t < kMetaWin; t += kScanThreads) {
+                    const int p = wbase + t;
+                    const uint32_t c = p < A.nprobe ? A.probes[(size_t)q * A.nprobe + p] : 0xffffffffu;
+                    const bool ok = c < (uint32_t)A.nlist;  // an unfilled probe slot is skipped too
+                    const uint32_t beg = ok ? A.list_off[c] : 0u;
+                    s_pc[t] = ok ? c : 0xffffffffu;
+                    s_pb[t] = beg;
+                    s_pl[t] = ok ? A.list_off[c + 1] - beg : 0u;
+                }
+                if constexpr (NV > 0) {
+                    __syncthreads();
+                    if (wave == 0) {
+                        coarse_dma(A, s_pc, s_cr, pg, lane);
+                        __builtin_amdgcn_s_waitcnt(VH_VMCNT(0));
+                    }
+                }
+                __syncthreads();
             }
-            __syncthreads();
             for (int t = threadIdx.x; t < pg * A.dim; t += kScanThreads) {
                 const int w = t / A.dim, d = t - w * A.dim;
-                const uint32_t c = s_mc[w];
-                s_r[t] = c != 0xffffffffu ? s_q[d] - A.coarse[(size_t)c * A.dim + d] : 0.0f;
-            }
-            // this wave's list (empty lists, ivf/mod.rs:296-298, have length 0)
-            const uint32_t beg = s_mb[slot], len = s_ml[slot];
-            const float *lut = s_lut + slot * tstride;
-            // DMA path: the wave's chunks are part + t * wpl (64 rows each), t < mine
-            const int nch = (int)((len + 63) / 64);
-            RingScan R{A.codes, ring, (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)ring, beg, len,
-                       part, wpl, nch > part ? (nch - part + wpl - 1) / wpl : 0, lane};
-            if constexpr (NV > 0) {
-                for (int t = 0; t < ring_chunks(NV) - 1 && t < R.mine; ++t) ring_dma<NV>(R, t);  // lands during the tables
+                const uint32_t c = s_pc[w0 + w];
+                float r = 0.0f;
+                if (c != 0xffffffffu) {
+                    if constexpr (NV > 0)
+                        r = s_q[d] - s_cr[t];
+                    else
+                        r = s_q[d] - A.coarse[(size_t)c * A.dim + d];
+                }
+                s_r[t] = r;
             }
             __syncthreads();
+            // this wave's list; the DMA path scans chunks part + t * wpl (64 rows each), t < mine
+            const uint32_t beg = s_pb[w0 + slot], len = s_pl[w0 + slot];
+            const float *lut = s_lut + slot * tstride;
+            const int nch = (int)((len + 63) / 64);
+            RingScan R{A.codes, A.ids, ring, (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)ring,
+                       beg, len, part, wpl, nch > part ? (nch - part + wpl - 1) / wpl : 0, lane};
+            if constexpr (NV > 0) {
+                // the next group's coarse rows (older than this group's ring DMAs, so landed once
+                // any chunk has), then the first chunks of this wave's list: both land while the
+                // tables are built
+                if (wave == 0 && w0 + pg < kMetaWin && g0 + pg < A.nprobe) coarse_dma(A, s_pc + w0 + pg, s_cr, pg, lane);
+                for (int t = 0; t < ring_chunks(NV) - 2 && t < R.mine; ++t) ring_dma<NV>(R, t);
+            }
             if constexpr (DS > 0)
                 lut_build_reg<MT, DS>(A, pg, s_r, s_lut, cbr);
             else
@@ -432,20 +536,23 @@ __global__ __launch_bounds__(kScanThreads) void k_ivfpq_scan(ScanArgs A) {
                     case 2: ring_scan<NV, 2, hib>(A, R, lut0, s_w, cnt, tau, capw, lanes_below); break;
                     default: ring_scan<NV, 3, hib>(A, R, lut0, s_w, cnt, tau, capw, lanes_below); break;
                 }
+                __builtin_amdgcn_s_waitcnt(VH_VMCNT(0));  // every DMA of this wave has landed
             } else {
                 for (uint32_t base = (uint32_t)part * 64 * kScanU; base < len;
                      base += (uint32_t)wpl * 64 * kScanU) {
                     if (cnt > (uint32_t)(capw - 64 * kScanU)) wave_compact(s_w, cnt, tau, A.k);
                     float total[kScanU];
+                    uint32_t id[kScanU];
 #pragma unroll
-                    for (int u = 0; u < kScanU; ++u) {
+                    for (int u = 0; u < kScanU; ++u) {  // ids load with the codes
                         const uint32_t i = min(base + u * 64 + lane, len - 1);
+                        id[u] = A.ids[beg + i];
                         total[u] = adc_score(A.codes + (size_t)(beg + i) * A.m_sub, lut, A.m_sub, A.ks);
                     }
 #pragma unroll
                     for (int u = 0; u < kScanU; ++u) {
                         const uint32_t i = base + u * 64 + lane;
-                        offer<hib>(A, total[u], i < len, beg + i, s_w, cnt, tau, lanes_below);
+                        offer<hib>(total[u], i < len, id[u], s_w, cnt, tau, lanes_below);
                     }
                 }
             }
@@ -513,10 +620,12 @@ void launch_scan_reg(const ScanArgs &A, int ds, int nv, int cus, size_t lds, hip
 
 }  // namespace
 
-// Dynamic LDS bytes of k_ivfpq_scan (candidates for capw slots per wave, query, pg residuals and
-// pg tables); the rings of NV pieces add ring_bytes(nv) of static LDS.
-inline size_t scan_lds_bytes(size_t dim, size_t m_sub, size_t ks, int capw, int pg) {
-    return (size_t)kScanWaves * capw * sizeof(unsigned long long) + ((1 + pg) * dim + pg * m_sub * ks) * sizeof(float);
+// Dynamic LDS bytes of k_ivfpq_scan (pg tables, candidates for capw slots per wave, query, pg
+// residuals, coarse rows for NV > 0); the rings of NV pieces add ring_bytes(nv) of static LDS and
+// the probe metadata 3 x kMetaWin words.
+inline size_t scan_lds_bytes(size_t dim, size_t m_sub, size_t ks, int capw, int pg, int nv) {
+    return (size_t)kScanWaves * capw * sizeof(unsigned long long) +
+           ((1 + pg) * dim + pg * m_sub * ks + (nv > 0 ? coarse_rows_floats(pg, (int)dim) : 0)) * sizeof(float);
 }
 
 // Launchers (pq_scan_l2.hip, pq_scan_ip.hip, pq_scan_mem.hip).  `ds` selects the register-path
