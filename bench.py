@@ -66,6 +66,7 @@ PROFILES = {
     "l1": "k_valu_filter__knn_l1_uniform_500000x128_q4096_k10.txt",
     "linf": "k_valu_filter__knn_linf_uniform_500000x128_q4096_k10.txt",
     "ivf_coarse": "k_mfma_hs_assign__ivf_coarse_l2_2000000x96_nlist4096.txt",
+    "ivfpq": "k_ivfpq_scan__ivfpq_l2_uniform_1000000x128_nlist1024_m16_ks256_nprobe32_q10000_k10.txt",
 }
 
 
