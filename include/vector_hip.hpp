@@ -17,11 +17,23 @@
  * silently fell back to the CPU, this API throws: every call runs on the GPU or fails.
  * Extensions (no reference counterpart): explicit initial centroids and seeds for k-means,
  * and HammingKnnEngine for packed-bit codes.
+ *
+ * The IVF stack of vector-index (src/ivf) sits on the same library:
+ *   IvfCoarseQuantizer    ivf/mod.rs:106-133, ivf/kmeans.rs:262-356
+ *   IvfPqConfig           ivf/config.rs:25-154
+ *   ProductQuantizer      ivf/pq.rs:12-293
+ *   InvertedList/Index    ivf/inverted_list.rs
+ *   IvfPqIndex            ivf/mod.rs:63-449 (storage: a flat row-major float array)
+ *   IvfPqSerializer       ivf/serializer.rs:16-377 (IVFPQVEC and VRSKMEAN files)
+ * VectorIndexError::EmptyIndex is CudaError(EmptyIndex); DimensionMismatch and the config's
+ * reasons are CudaError(InvalidConfig).
  */
 #ifndef VECTOR_HIP_HPP
 #define VECTOR_HIP_HPP
 
+#include <algorithm>
 #include <cstdint>
+#include <cstring>
 #include <memory>
 #include <stdexcept>
 #include <string>
@@ -61,7 +73,7 @@ struct SearchResult {
 
 class CudaError : public std::runtime_error {
 public:
-    enum class Kind { InsufficientDevices, DeviceNotFound, DriverError, HardwareNotAvailable, InvalidConfig };
+    enum class Kind { InsufficientDevices, DeviceNotFound, DriverError, HardwareNotAvailable, InvalidConfig, EmptyIndex };
     CudaError(Kind kind, const std::string &msg, size_t requested = 0, size_t available = 0)
         : std::runtime_error(msg), kind_(kind), requested_(requested), available_(available) {}
     Kind kind() const { return kind_; }
@@ -86,6 +98,7 @@ inline void check(int status) {
         case VHIP_ERR_DEVICE_NOT_FOUND: throw CudaError(CudaError::Kind::DeviceNotFound, msg);
         case VHIP_ERR_HARDWARE_NOT_AVAILABLE: throw CudaError(CudaError::Kind::HardwareNotAvailable, msg);
         case VHIP_ERR_INVALID_CONFIG: throw CudaError(CudaError::Kind::InvalidConfig, msg);
+        case VHIP_ERR_EMPTY_INDEX: throw CudaError(CudaError::Kind::EmptyIndex, msg);
         default: throw CudaError(CudaError::Kind::DriverError, msg);
     }
 }
@@ -496,6 +509,311 @@ inline CudaKMeansResult fit_cuda_aware(const std::vector<float> &all_data, size_
                                                               ini);
     return CudaKMeansEngine().fit(all_data, dimension, k, max_iters, tolerance, metric, ini);
 }
+
+/* ---- product quantization and the IVF-PQ index (vector-index/src/ivf) ------------------ */
+/* IvfPqConfig (ivf/config.rs:25-154); max_train_points 0 stands for None */
+struct IvfPqConfig {
+    size_t nlist = 64, nprobe = 8, num_subvectors = 8, sub_clusters = 256, max_kmeans_iters = 25;
+    float kmeans_tolerance = 1e-4f;
+    size_t max_train_points = 0;
+
+    static IvfPqConfig make(size_t nlist, size_t nprobe, size_t num_subvectors) {
+        IvfPqConfig c;
+        c.nlist = nlist;
+        c.nprobe = nprobe;
+        c.num_subvectors = num_subvectors;
+        return c;
+    }
+    IvfPqConfig with_sub_clusters(size_t v) const { IvfPqConfig c = *this; c.sub_clusters = v; return c; }
+    IvfPqConfig with_max_kmeans_iters(size_t v) const { IvfPqConfig c = *this; c.max_kmeans_iters = v; return c; }
+    IvfPqConfig with_kmeans_tolerance(float v) const { IvfPqConfig c = *this; c.kmeans_tolerance = v; return c; }
+    IvfPqConfig with_max_train_points(size_t v) const { IvfPqConfig c = *this; c.max_train_points = v; return c; }
+    size_t sub_dimension(size_t dimension) const { return num_subvectors ? dimension / num_subvectors : 0; }
+    vhip_ivfpq_config c() const {
+        return vhip_ivfpq_config{nlist, nprobe, num_subvectors, sub_clusters, max_kmeans_iters, kmeans_tolerance,
+                                 max_train_points};
+    }
+    static IvfPqConfig from_c(const vhip_ivfpq_config &v) {
+        IvfPqConfig c;
+        c.nlist = v.nlist;
+        c.nprobe = v.nprobe;
+        c.num_subvectors = v.num_subvectors;
+        c.sub_clusters = v.sub_clusters;
+        c.max_kmeans_iters = v.max_kmeans_iters;
+        c.kmeans_tolerance = v.kmeans_tolerance;
+        c.max_train_points = v.max_train_points;
+        return c;
+    }
+    void validate(size_t dimension) const {
+        const vhip_ivfpq_config v = c();
+        detail::check(vhip_ivfpq_config_validate(&v, dimension));
+    }
+    bool operator==(const IvfPqConfig &o) const {
+        return nlist == o.nlist && nprobe == o.nprobe && num_subvectors == o.num_subvectors &&
+               sub_clusters == o.sub_clusters && max_kmeans_iters == o.max_kmeans_iters &&
+               kmeans_tolerance == o.kmeans_tolerance && max_train_points == o.max_train_points;
+    }
+};
+
+/* ProductQuantizer (ivf/pq.rs:12-293): training, encoding and ADC tables run on the GPU */
+class ProductQuantizer {
+public:
+    size_t dimension = 0, num_subvectors = 0, sub_dimension = 0, sub_clusters = 0;
+    std::vector<float> codebooks;  // num_subvectors x sub_clusters x sub_dimension
+
+    ProductQuantizer() = default;
+    ProductQuantizer(size_t dim, size_t m, size_t ks, std::vector<float> cb)
+        : dimension(dim), num_subvectors(m), sub_dimension(m ? dim / m : 0), sub_clusters(ks), codebooks(std::move(cb)) {
+        detail::require(m > 0 && dim % m == 0, "dimension must be divisible by num_subvectors");
+        detail::require(codebooks.size() == m * ks * sub_dimension, "codebooks must hold M x Ks x sub_dimension floats");
+    }
+    /* pq.rs:53-107 */
+    static ProductQuantizer train(const std::vector<float> &data, size_t dim, size_t m, size_t ks, size_t max_iters,
+                                  float tolerance, DistanceMetric metric, uint64_t seed = 42, size_t ordinal = 0) {
+        detail::require(m > 0 && dim % m == 0, "dimension must be divisible by num_subvectors");
+        std::vector<float> cb(m * ks * (dim / m));
+        detail::check(vhip_pq_train((int)ordinal, data.data(), data.size() / dim, dim, m, ks, max_iters, tolerance,
+                                    (int)metric, nullptr, seed, cb.data()));
+        return ProductQuantizer(dim, m, ks, std::move(cb));
+    }
+    const float *get_sub_centroid(size_t m, size_t k) const {
+        return codebooks.data() + (m * sub_clusters + k) * sub_dimension;
+    }
+    /* pq.rs:203-214 */
+    std::vector<uint8_t> encode_batch(const std::vector<float> &data, DistanceMetric metric, size_t ordinal = 0) const {
+        const size_t n = data.size() / dimension;
+        std::vector<uint8_t> codes(n * num_subvectors);
+        detail::check(vhip_pq_encode((int)ordinal, codebooks.data(), dimension, num_subvectors, sub_clusters,
+                                     (int)metric, data.data(), n, codes.data()));
+        return codes;
+    }
+    /* pq.rs:178-200 */
+    std::vector<uint8_t> encode(const std::vector<float> &vector, DistanceMetric metric) const {
+        detail::require(vector.size() == dimension, "dimension mismatch");
+        return encode_batch(vector, metric);
+    }
+    /* pq.rs:217-229 */
+    std::vector<float> decode(const std::vector<uint8_t> &code) const {
+        detail::require(code.size() == num_subvectors, "code length must equal num_subvectors");
+        std::vector<float> v(dimension);
+        for (size_t m = 0; m < num_subvectors; ++m)
+            std::memcpy(&v[m * sub_dimension], get_sub_centroid(m, code[m]), sub_dimension * sizeof(float));
+        return v;
+    }
+    /* pq.rs:233-266 */
+    std::vector<float> compute_adc_lut(const std::vector<float> &query, DistanceMetric metric, size_t ordinal = 0) const {
+        detail::require(query.size() == dimension, "dimension mismatch");
+        std::vector<float> lut(num_subvectors * sub_clusters);
+        detail::check(vhip_pq_adc_lut((int)ordinal, codebooks.data(), dimension, num_subvectors, sub_clusters,
+                                      (int)metric, query.data(), 1, lut.data()));
+        return lut;
+    }
+    /* pq.rs:270-293: quads as (d0 + d1) + (d2 + d3), then the remainder */
+    float compute_distance_with_lut(const uint8_t *code, const std::vector<float> &lut) const {
+        float total = 0.0f;
+        size_t m = 0;
+        for (; m + 4 <= num_subvectors; m += 4) {
+            const float d0 = lut[m * sub_clusters + code[m]], d1 = lut[(m + 1) * sub_clusters + code[m + 1]];
+            const float d2 = lut[(m + 2) * sub_clusters + code[m + 2]], d3 = lut[(m + 3) * sub_clusters + code[m + 3]];
+            total += (d0 + d1) + (d2 + d3);
+        }
+        for (; m < num_subvectors; ++m) total += lut[m * sub_clusters + code[m]];
+        return total;
+    }
+    bool operator==(const ProductQuantizer &o) const {
+        return dimension == o.dimension && num_subvectors == o.num_subvectors && sub_clusters == o.sub_clusters &&
+               codebooks == o.codebooks;
+    }
+};
+
+/* InvertedList / InvertedIndex (ivf/inverted_list.rs:8-120) */
+struct InvertedList {
+    std::vector<VectorId> ids;
+    std::vector<uint8_t> codes;
+    size_t len() const { return ids.size(); }
+    bool is_empty() const { return ids.empty(); }
+    const uint8_t *get_code(size_t index, size_t num_subvectors) const { return codes.data() + index * num_subvectors; }
+    bool operator==(const InvertedList &o) const { return ids == o.ids && codes == o.codes; }
+};
+struct InvertedIndex {
+    std::vector<InvertedList> lists;
+    size_t num_subvectors = 0, total_vectors = 0;
+    InvertedIndex(size_t nlist = 0, size_t m = 0) : lists(nlist), num_subvectors(m) {}
+    void add(size_t cluster, VectorId id, const std::vector<uint8_t> &code) {
+        detail::require(code.size() == num_subvectors, "code length must equal num_subvectors");
+        lists.at(cluster).ids.push_back(id);
+        lists[cluster].codes.insert(lists[cluster].codes.end(), code.begin(), code.end());
+        ++total_vectors;
+    }
+    size_t nlist() const { return lists.size(); }
+    const InvertedList &get_list(size_t c) const { return lists.at(c); }
+    bool operator==(const InvertedIndex &o) const {
+        return num_subvectors == o.num_subvectors && total_vectors == o.total_vectors && lists == o.lists;
+    }
+    // CSR parts: sizes, ids, codes
+    void csr(std::vector<uint32_t> &sizes, std::vector<uint32_t> &ids, std::vector<uint8_t> &codes) const {
+        sizes.clear(); ids.clear(); codes.clear();
+        for (const auto &l : lists) {
+            sizes.push_back((uint32_t)l.ids.size());
+            ids.insert(ids.end(), l.ids.begin(), l.ids.end());
+            codes.insert(codes.end(), l.codes.begin(), l.codes.end());
+        }
+    }
+    static InvertedIndex from_csr(const std::vector<uint32_t> &sizes, const uint32_t *ids, const uint8_t *codes,
+                                  size_t m) {
+        InvertedIndex ix(sizes.size(), m);
+        size_t off = 0;
+        for (size_t c = 0; c < sizes.size(); ++c) {
+            ix.lists[c].ids.assign(ids + off, ids + off + sizes[c]);
+            ix.lists[c].codes.assign(codes + off * m, codes + (off + sizes[c]) * m);
+            off += sizes[c];
+        }
+        ix.total_vectors = off;
+        return ix;
+    }
+};
+
+/* IvfPqSerializer::save_to_file / load_from_file (ivf/serializer.rs:26-254) */
+struct IvfPqFile {
+    IvfPqConfig config;
+    std::vector<float> coarse_centroids;
+    ProductQuantizer pq;
+    InvertedIndex inverted_index;
+    size_t dimension = 0;
+    DistanceMetric metric = DistanceMetric::L2Squared;
+};
+struct IvfPqFiles {
+    static void save_to_file(const std::string &path, const IvfPqConfig &config, const std::vector<float> &coarse,
+                             const ProductQuantizer &pq, const InvertedIndex &inv, size_t dimension,
+                             DistanceMetric metric) {
+        std::vector<uint32_t> sizes, ids;
+        std::vector<uint8_t> codes;
+        inv.csr(sizes, ids, codes);
+        const vhip_ivfpq_config c = config.c();
+        detail::check(vhip_ivfpq_file_save(path.c_str(), &c, dimension, (int)metric, coarse.data(),
+                                           dimension ? coarse.size() / dimension : 0, pq.codebooks.data(),
+                                           pq.codebooks.size(), sizes.data(), sizes.size(), ids.data(), codes.data()));
+    }
+    static IvfPqFile load_from_file(const std::string &path) {
+        vhip_ivfpq_config c{};
+        size_t dim = 0, nc = 0, cbl = 0, nl = 0, tot = 0;
+        int m = 0;
+        detail::check(vhip_ivfpq_file_info(path.c_str(), &c, &dim, &m, &nc, &cbl, &nl, &tot));
+        IvfPqFile f;
+        f.config = IvfPqConfig::from_c(c);
+        f.dimension = dim;
+        f.metric = (DistanceMetric)m;
+        f.coarse_centroids.resize(nc * dim);
+        std::vector<float> cb(cbl);
+        std::vector<uint32_t> sizes(nl), ids(tot + 1);
+        std::vector<uint8_t> codes(tot * c.num_subvectors + 1);
+        detail::check(vhip_ivfpq_file_load(path.c_str(), f.coarse_centroids.data(), cb.data(), sizes.data(), ids.data(),
+                                           codes.data()));
+        f.pq = ProductQuantizer(dim, c.num_subvectors, c.sub_clusters, std::move(cb));
+        f.inverted_index = InvertedIndex::from_csr(sizes, ids.data(), codes.data(), c.num_subvectors);
+        return f;
+    }
+};
+
+/* IvfPqIndex (ivf/mod.rs:63-449) over a flat row-major storage of `dimension` floats per vector */
+class IvfPqIndex {
+public:
+    /* ivf/mod.rs:81-165 (parallel and sequential builds give the same index) */
+    static IvfPqIndex build_with_config(const std::vector<float> &storage, size_t dimension, const IvfPqConfig &config,
+                                        DistanceMetric metric, uint64_t seed = 42, size_t ordinal = 0) {
+        detail::require(dimension > 0 && storage.size() % dimension == 0, "storage is not a multiple of dimension");
+        const vhip_ivfpq_config c = config.c();
+        vhip_ivfpq *h = nullptr;
+        detail::check(vhip_ivfpq_build((int)ordinal, storage.data(), storage.size() / dimension, dimension, &c,
+                                       (int)metric, seed, &h));
+        return IvfPqIndex(h, config, metric);
+    }
+    static IvfPqIndex build(const std::vector<float> &storage, size_t dimension, DistanceMetric metric) {
+        return build_with_config(storage, dimension, IvfPqConfig(), metric);
+    }
+    static IvfPqIndex from_parts(const IvfPqConfig &config, const std::vector<float> &coarse, const ProductQuantizer &pq,
+                                 const InvertedIndex &inv, size_t dimension, DistanceMetric metric, size_t ordinal = 0) {
+        std::vector<uint32_t> sizes, ids;
+        std::vector<uint8_t> codes;
+        inv.csr(sizes, ids, codes);
+        const vhip_ivfpq_config c = config.c();
+        vhip_ivfpq *h = nullptr;
+        detail::check(vhip_ivfpq_create((int)ordinal, dimension, (int)metric, &c, coarse.data(), coarse.size() / dimension,
+                                        pq.codebooks.data(), sizes.data(), ids.data(), codes.data(), &h));
+        return IvfPqIndex(h, config, metric);
+    }
+    /* ivf/mod.rs:251-345 */
+    std::vector<SearchResult> search(const std::vector<float> &query, size_t k) const {
+        return search_with_nprobe(query, k, config_.nprobe);
+    }
+    std::vector<SearchResult> search_with_nprobe(const std::vector<float> &query, size_t k, size_t nprobe) const {
+        detail::require(query.size() == info_.dimension, "dimension mismatch");
+        return search_batch(query, k, nprobe)[0];
+    }
+    std::vector<std::vector<SearchResult>> search_batch(const std::vector<float> &queries, size_t k,
+                                                        size_t nprobe) const {
+        const size_t nq = queries.size() / info_.dimension, kk = std::max<size_t>(k, 1);
+        std::vector<uint32_t> ids(nq * kk);
+        std::vector<float> dist(nq * kk);
+        std::vector<size_t> len(nq);
+        detail::check(vhip_ivfpq_search_batch(h_.get(), queries.data(), nq, k, nprobe, ids.data(), dist.data(),
+                                              len.data()));
+        return detail::to_lists(nq, kk, ids, dist, len);
+    }
+    /* ivf/mod.rs:358-372 */
+    static float evaluate_recall(const std::vector<SearchResult> &gt, const std::vector<SearchResult> &res) {
+        if (gt.empty() || res.empty()) return 0.0f;
+        const size_t k = std::min(gt.size(), res.size());
+        size_t hit = 0;
+        for (size_t i = 0; i < k; ++i)
+            for (size_t j = 0; j < k; ++j)
+                if (res[i].id == gt[j].id) { ++hit; break; }
+        return (float)hit / (float)k;
+    }
+    /* ivf/mod.rs:375-408 */
+    void save_to_file(const std::string &path) const {
+        IvfPqFiles::save_to_file(path, config_, coarse_centroids(), pq(), inverted_index(), info_.dimension, metric_);
+    }
+    static IvfPqIndex load_from_file(size_t storage_dimension, const std::string &path) {
+        IvfPqFile f = IvfPqFiles::load_from_file(path);
+        detail::require(f.dimension == storage_dimension, "dimension mismatch");
+        return from_parts(f.config, f.coarse_centroids, f.pq, f.inverted_index, f.dimension, f.metric);
+    }
+    /* getters (ivf/mod.rs:411-449) */
+    const IvfPqConfig &config() const { return config_; }
+    DistanceMetric metric() const { return metric_; }
+    size_t dimension() const { return info_.dimension; }
+    size_t len() const { return info_.num_vectors; }
+    bool is_empty() const { return len() == 0; }
+    std::vector<float> coarse_centroids() const {
+        std::vector<float> c(info_.nlist * info_.dimension);
+        detail::check(vhip_ivfpq_export(h_.get(), c.data(), nullptr, nullptr, nullptr, nullptr));
+        return c;
+    }
+    ProductQuantizer pq() const {
+        std::vector<float> cb(info_.num_subvectors * info_.sub_clusters * (info_.dimension / info_.num_subvectors));
+        detail::check(vhip_ivfpq_export(h_.get(), nullptr, cb.data(), nullptr, nullptr, nullptr));
+        return ProductQuantizer(info_.dimension, info_.num_subvectors, info_.sub_clusters, std::move(cb));
+    }
+    InvertedIndex inverted_index() const {
+        std::vector<uint32_t> sizes(info_.nlist), ids(info_.num_vectors + 1);
+        std::vector<uint8_t> codes(info_.num_vectors * info_.num_subvectors + 1);
+        detail::check(vhip_ivfpq_export(h_.get(), nullptr, nullptr, sizes.data(), ids.data(), codes.data()));
+        return InvertedIndex::from_csr(sizes, ids.data(), codes.data(), info_.num_subvectors);
+    }
+
+private:
+    struct Del {
+        void operator()(vhip_ivfpq *p) const { vhip_ivfpq_destroy(p); }
+    };
+    IvfPqIndex(vhip_ivfpq *h, const IvfPqConfig &c, DistanceMetric m) : h_(h), config_(c), metric_(m) {
+        detail::check(vhip_ivfpq_info(h, &info_));
+    }
+    std::unique_ptr<vhip_ivfpq, Del> h_;
+    IvfPqConfig config_;
+    DistanceMetric metric_;
+    vhip_ivfpq_desc info_{};
+};
 
 }  // namespace vector_hip
 

@@ -73,6 +73,48 @@ static CudaError expect_error(F f) {
 }
 
 static void host_tests() {
+    run("ivf_pq_config default / builders / validation (ivf/config.rs:156-240)", [] {
+        IvfPqConfig d;
+        CHECK(d.nlist == 64 && d.nprobe == 8 && d.num_subvectors == 8 && d.sub_clusters == 256 && d.max_kmeans_iters == 25);
+        d.validate(128);
+        auto c = IvfPqConfig::make(32, 4, 4).with_sub_clusters(64).with_max_kmeans_iters(15).with_kmeans_tolerance(1e-5f);
+        CHECK(c.sub_dimension(128) == 32);
+        c.validate(128);
+        const IvfPqConfig bad[] = {IvfPqConfig::make(0, 1, 4), IvfPqConfig::make(10, 0, 4), IvfPqConfig::make(10, 11, 4),
+                                   IvfPqConfig::make(10, 5, 0), IvfPqConfig::make(10, 5, 5),
+                                   IvfPqConfig::make(10, 5, 4).with_sub_clusters(0),
+                                   IvfPqConfig::make(10, 5, 4).with_sub_clusters(300),
+                                   IvfPqConfig::make(10, 5, 4).with_max_kmeans_iters(0),
+                                   IvfPqConfig::make(10, 5, 4).with_kmeans_tolerance(-1.0f)};
+        for (const auto &b : bad) {
+            bool threw = false;
+            try { b.validate(128); } catch (const CudaError &e) { threw = e.kind() == CudaError::Kind::InvalidConfig; }
+            CHECK(threw);
+        }
+    });
+    run("pq distance_with_lut and sub-centroid accessor (ivf/pq.rs:349-426)", [] {
+        ProductQuantizer pq(4, 2, 2, {0, 0, 1, 1, 0, 0, 2, 2});
+        const std::vector<float> lut{2, 0, 8, 0};
+        const uint8_t c11[2] = {1, 1}, c00[2] = {0, 0};
+        CHECK(pq.compute_distance_with_lut(c11, lut) == 0.0f && pq.compute_distance_with_lut(c00, lut) == 10.0f);
+        ProductQuantizer acc(4, 2, 2, {1, 2, 3, 4, 5, 6, 7, 8});
+        CHECK(acc.get_sub_centroid(1, 0)[0] == 5.0f && acc.get_sub_centroid(0, 1)[1] == 4.0f);
+        CHECK((acc.decode({1, 0}) == std::vector<float>{3, 4, 5, 6}));
+    });
+    run("ivf_pq serializer roundtrip (ivf/serializer.rs:438-480)", [] {
+        const std::string p = "/tmp/vhip_facade_ivfpq.bin";
+        auto cfg = IvfPqConfig::make(2, 1, 2).with_sub_clusters(2).with_max_kmeans_iters(10);
+        std::vector<float> coarse{0, 0, 0, 0, 1, 1, 1, 1};
+        ProductQuantizer pq(4, 2, 2, {0, 0, 0.5f, 0.5f, 0, 0, 0.5f, 0.5f});
+        InvertedIndex inv(2, 2);
+        inv.add(0, 10, {0, 1});
+        inv.add(1, 20, {1, 0});
+        IvfPqFiles::save_to_file(p, cfg, coarse, pq, inv, 4, DistanceMetric::L2Squared);
+        auto f = IvfPqFiles::load_from_file(p);
+        CHECK(f.config == cfg && f.coarse_centroids == coarse && f.pq == pq && f.inverted_index == inv);
+        CHECK(f.dimension == 4 && f.metric == DistanceMetric::L2Squared);
+        std::remove(p.c_str());
+    });
     run("centroid_file_roundtrip (ivf/serializer.rs:552-575)", [] {
         const std::string p = "/tmp/vhip_facade_centroids.bin";
         IvfPqSerializer::save_centroid_file(p, {1, 2, 3, 4, 5, 6, 7, 8}, 4, 2, DistanceMetric::L2Squared, 15, 42.5f);
@@ -368,6 +410,82 @@ static void gpu_tests() {
             auto r = fit_cuda_aware(data, 2, 2, 30, 1e-5f, DistanceMetric::L2Squared, g);
             CHECK(r.k == 2 && r.dimension == 2 && r.iterations > 0);
         }
+    });
+    run("ivf_pq end-to-end search and getters (ivf/mod.rs:456-485, 633-646)", [] {
+        std::vector<float> st;
+        for (int i = 0; i < 50; ++i)
+            for (int d = 0; d < 8; ++d) st.push_back((float)(i * 10 + d) * 0.1f);
+        auto cfg = IvfPqConfig::make(4, 2, 2).with_sub_clusters(8).with_max_kmeans_iters(15);
+        auto ix = IvfPqIndex::build_with_config(st, 8, cfg, DistanceMetric::L2Squared);
+        CHECK(ix.len() == 50 && !ix.is_empty() && ix.config().nlist == 4);
+        std::vector<float> q(st.begin() + 80, st.begin() + 88);
+        auto r = ix.search(q, 5);
+        bool has10 = false;
+        for (auto &x : r) has10 |= x.id == 10;
+        CHECK(r.size() == 5 && has10);
+        CHECK(ix.coarse_centroids().size() == 4 * 8 && ix.pq().num_subvectors == 2 && ix.inverted_index().nlist() == 4);
+    });
+    run("ivf_pq recall vs flat (ivf/mod.rs:487-515)", [] {
+        std::vector<float> st;
+        for (int i = 0; i < 100; ++i)
+            for (int d = 0; d < 16; ++d) st.push_back((float)((i * 7 + d) % 30));
+        auto cfg = IvfPqConfig::make(8, 4, 4).with_sub_clusters(16).with_max_kmeans_iters(20);
+        auto ix = IvfPqIndex::build_with_config(st, 16, cfg, DistanceMetric::L2Squared);
+        std::vector<float> q(st.begin() + 42 * 16, st.begin() + 43 * 16);
+        CudaKnnEngine flat(st, 16, DistanceMetric::L2Squared);
+        CHECK(IvfPqIndex::evaluate_recall(flat.search(q, 10), ix.search(q, 10)) >= 0.5f);
+        CHECK(IvfPqIndex::evaluate_recall({}, {}) == 0.0f);
+    });
+    run("ivf_pq save/load, cosine/dot, k = 0, empty storage, nprobe, dimension mismatch (ivf/mod.rs:517-631)", [] {
+        const std::string p = "/tmp/vhip_facade_ivfpq_ix.bin";
+        std::vector<float> st{1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12};
+        auto ix = IvfPqIndex::build_with_config(st, 4, IvfPqConfig::make(2, 2, 2).with_sub_clusters(4),
+                                                DistanceMetric::L2Squared);
+        ix.save_to_file(p);
+        auto lo = IvfPqIndex::load_from_file(4, p);
+        CHECK(lo.len() == 3 && lo.inverted_index().nlist() == 2);
+        std::remove(p.c_str());
+        std::vector<float> cs, ds;
+        for (int i = 1; i <= 20; ++i) {
+            const float f = (float)i;
+            cs.insert(cs.end(), {f, f + 1, f + 2, f + 3});
+            ds.insert(ds.end(), {f, f * 2, f * 0.5f, f + 1});
+        }
+        auto cfg = IvfPqConfig::make(2, 2, 2).with_sub_clusters(4);
+        CHECK(IvfPqIndex::build_with_config(cs, 4, cfg, DistanceMetric::CosineSimilarity).search({1, 2, 3, 4}, 2).size() == 2);
+        CHECK(IvfPqIndex::build_with_config(ds, 4, cfg, DistanceMetric::DotProduct).search({1, 2, 0.5f, 2}, 2).size() == 2);
+        bool empty_threw = false;
+        try {
+            IvfPqIndex::build_with_config({}, 2, IvfPqConfig::make(1, 1, 1).with_sub_clusters(1), DistanceMetric::L2Squared);
+        } catch (const CudaError &e) { empty_threw = e.kind() == CudaError::Kind::EmptyIndex; }
+        CHECK(empty_threw);
+        auto one = IvfPqIndex::build_with_config({1, 2}, 2, IvfPqConfig::make(1, 1, 1).with_sub_clusters(1),
+                                                 DistanceMetric::L2Squared);
+        CHECK(one.search({1, 2}, 0).empty());
+        std::vector<float> s30;
+        for (int i = 0; i < 30; ++i) s30.insert(s30.end(), {(float)i, (float)i + 1, (float)i + 2, (float)i + 3});
+        auto ix30 = IvfPqIndex::build_with_config(s30, 4, IvfPqConfig::make(4, 1, 2).with_sub_clusters(4),
+                                                  DistanceMetric::L2Squared);
+        CHECK(!ix30.search_with_nprobe({0, 1, 2, 3}, 3, 1).empty() && !ix30.search_with_nprobe({0, 1, 2, 3}, 3, 4).empty());
+        bool dim_threw = false;
+        try { ix30.search({1, 2}, 1); } catch (const CudaError &e) { dim_threw = e.kind() == CudaError::Kind::InvalidConfig; }
+        CHECK(dim_threw);
+    });
+    run("pq training and encoding (ivf/pq.rs:302-346)", [] {
+        std::vector<float> data;
+        for (int i = 0; i < 20; ++i) {
+            const float v = (float)i;
+            data.insert(data.end(), {v, v + 1, v + 2, v + 3, v, v, v, v});
+        }
+        auto pq = ProductQuantizer::train(data, 8, 2, 4, 15, 1e-4f, DistanceMetric::L2Squared);
+        CHECK(pq.dimension == 8 && pq.num_subvectors == 2 && pq.sub_dimension == 4 && pq.sub_clusters == 4);
+        CHECK(pq.codebooks.size() == 32);
+        auto code = pq.encode(std::vector<float>(data.begin(), data.begin() + 8), DistanceMetric::L2Squared);
+        CHECK(code[0] < 4 && code[1] < 4 && pq.decode(code).size() == 8);
+        auto batch = pq.encode_batch(data, DistanceMetric::L2Squared);
+        CHECK(batch[0] == code[0] && batch[1] == code[1]);
+        auto lut = pq.compute_adc_lut(std::vector<float>(data.begin(), data.begin() + 8), DistanceMetric::L2Squared);
+        CHECK(lut.size() == 8);
     });
     run("explicit-init k-means is deterministic (extension)", [] {
         std::vector<float> data;
