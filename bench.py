@@ -13,7 +13,8 @@ launch time, measured with HIP events on the engine's stream over the timed regi
 knn.rs:312-377, AVX-512 dispatch as vector-simd) timed on this host on a bounded query sample.
 
 Other workloads: --workload cos768 | kmeans | hamming | l1 | linf | gauss (see WORKLOADS), ivf_coarse
-(the IVF coarse quantizer), ivfpq (IVF-PQ search), copy (counter calibration).
+(the IVF coarse quantizer), ivfpq (IVF-PQ search), upload (engine builds from VECRSTOR files),
+copy (counter calibration).
 """
 import argparse
 import json
@@ -371,6 +372,83 @@ def bench_copy(vh, nbytes=1 << 30, reps=5):
             "config": {"workload": f"copy_{nbytes >> 20}MiB", "bytes_per_copy": nbytes}}
 
 
+PEAK_PCIE5_X16 = 64.0e9   # B/s per direction, PCIe 5.0 x16 (the host link of one MI355X)
+
+
+def bench_upload(vh, steps, warmup):
+    """Engine builds from VECRSTOR files.  The reference reads each file into a Vec and uploads
+    that (mpi_kmeans.rs:307-325, knn.rs:111-122); here the file is mapped and streamed through the
+    pinned staging ring.  Legs, each the median of `steps` full engine builds (allocation, H2D,
+    on-device row preparation) with the file warm in the page cache: the mapped file; the same
+    rows already resident in a host array; and the reference's flow, read the file into an array
+    then build.  Plus k-means over the 2M x 96 point set split into 8 shard files (segments) versus
+    reading and concatenating the shards first."""
+    import shutil
+    import tempfile
+
+    from vector_hip import datasets as ds
+
+    def median_s(fn):
+        for _ in range(warmup):
+            fn()
+        ts = []
+        for _ in range(steps):
+            vh.synchronize()
+            t0 = time.perf_counter()
+            e = fn()
+            vh.synchronize()
+            ts.append(time.perf_counter() - t0)
+            del e
+        return float(np.median(ts))
+
+    n, d = 1_000_000, 128
+    base = ds.uniform_int(n, d, ds.SEED_BASE)
+    tmp = tempfile.mkdtemp(prefix="vh_upload_", dir=os.environ.get("TMPDIR", "/tmp"))
+    try:
+        p = os.path.join(tmp, "base.bin")
+        vh.MmapStorage.create_from_flat(p, d, base)
+        nbytes = n * d * 4
+        log("upload: knn engine from mapped file / array / read-then-build")
+        t_map = median_s(lambda: vh.CudaKnnEngine.from_vecrstor(p))
+        t_arr = median_s(lambda: vh.CudaKnnEngine(base, d))
+        t_read = median_s(lambda: vh.CudaKnnEngine(np.fromfile(p, dtype="<f4", offset=24).reshape(n, d), d))
+        kn, kd, ns = 2_000_000, 96, 8
+        log(f"upload: k-means state over {ns} shard files of a {kn} x {kd} mixture")
+        pts, _, _ = ds.gaussian_mixture(kn, kd, 4096, ds.SEED_MIXTURE)
+        paths = []
+        for i, part in enumerate(np.array_split(pts, ns)):
+            sp = os.path.join(tmp, f"shard_{i}.bin")
+            vh.MmapStorage.create_from_flat(sp, kd, part)
+            paths.append(sp)
+        del pts
+
+        def read_concat():
+            return vh.KMeansState(np.concatenate([np.fromfile(sp, dtype="<f4", offset=24).reshape(-1, kd)
+                                                  for sp in paths]))
+
+        t_seg = median_s(lambda: vh.KMeansState.from_vecrstor(paths))
+        t_cat = median_s(read_concat)
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+    kbytes = kn * kd * 4
+    gbs = round(nbytes / t_map / 1e9, 2)
+    return {"metric": "engine build GB/s from a VECRSTOR file (1M x 128 fp32 base)", "value": gbs, "unit": "GB/s",
+            "n_gpus": 1, "steps": steps, "warmup": warmup, "ms_per_step": round(t_map * 1e3, 2),
+            "higher_is_better": True, "scaling": "strong", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+            "config": {"workload": "upload_vecrstor_1000000x128_knn_and_2000000x96_8shards_kmeans",
+                       "page_cache": "warm", "parallelism": "single GPU"},
+            "roofline": {"bound": "pcie", "achieved": gbs, "peak": PEAK_PCIE5_X16 / 1e9, "unit": "GB/s",
+                         "frac": round(nbytes / t_map / PEAK_PCIE5_X16, 3), "traffic": None},
+            "legs_ms": {"knn_mapped_file": round(t_map * 1e3, 2), "knn_host_array": round(t_arr * 1e3, 2),
+                        "knn_read_then_build": round(t_read * 1e3, 2),
+                        "kmeans_8_mapped_shards": round(t_seg * 1e3, 2),
+                        "kmeans_read_concat_then_build": round(t_cat * 1e3, 2)},
+            "legs_gbs": {"knn_mapped_file": gbs, "knn_host_array": round(nbytes / t_arr / 1e9, 2),
+                         "knn_read_then_build": round(nbytes / t_read / 1e9, 2),
+                         "kmeans_8_mapped_shards": round(kbytes / t_seg / 1e9, 2),
+                         "kmeans_read_concat_then_build": round(kbytes / t_cat / 1e9, 2)}}
+
+
 WORKLOADS = {
     "l2int": dict(n=1_000_000, d=128, nq=10_000, k=100, metric="l2", gen="uniform_int",
                   name="knn_l2_int0-255_1000000x128_q10000_k100"),
@@ -444,7 +522,7 @@ def main():
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--workload", default="default",
-                    choices=["default", "kmeans", "copy", "ivf_coarse", "ivfpq"] + sorted(WORKLOADS))
+                    choices=["default", "kmeans", "copy", "ivf_coarse", "ivfpq", "upload"] + sorted(WORKLOADS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -463,6 +541,8 @@ def main():
         out = bench_ivf_coarse(vh, args.steps, args.warmup, not args.no_cpu)
     elif args.workload == "ivfpq":
         out = bench_ivfpq(vh, args.steps, args.warmup, not args.no_cpu)
+    elif args.workload == "upload":
+        out = bench_upload(vh, args.steps, args.warmup)
     elif args.workload == "kmeans":
         r = bench_kmeans(vh, 10, not args.no_cpu)
         out = {"metric": METRIC, "value": r["value"], "unit": r["unit"], "n_gpus": 1, "steps": 10, "warmup": 1,

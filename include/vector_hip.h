@@ -174,6 +174,16 @@ int vhip_dkmeans_check(size_t num_gpus);
  * one Lloyd step for parity checks and the per-iteration benchmark). */
 typedef struct vhip_kmeans vhip_kmeans;
 int vhip_kmeans_create(int ordinal, const float *data, size_t n, size_t dim, int metric, vhip_kmeans **out);
+/* The same state from nseg host segments (segment i: counts[i] rows of dim floats) uploaded one
+ * after another (no reference counterpart: it serves callers with several shards, such as the
+ * trainer over mapped VECRSTOR files, which would otherwise concatenate them on the host). */
+int vhip_kmeans_create_segments(int ordinal, const float *const *segments, const size_t *counts, size_t nseg,
+                                size_t dim, int metric, vhip_kmeans **out);
+/* CudaKMeansEngine::fit (kmeans.rs:58-237) on the points of an existing state; the same
+ * arguments and results as vhip_kmeans_fit. */
+int vhip_kmeans_fit_state(vhip_kmeans *km, size_t k, size_t max_iters, float tol, const float *init_centroids,
+                          int init_mode, uint64_t seed, float *out_centroids, int32_t *out_assign,
+                          vhip_kmeans_result *result);
 /* Sets the current centroids (k x dim host floats). */
 int vhip_kmeans_set_centroids(vhip_kmeans *km, const float *centroids, size_t k);
 /* Runs `iters` assign+update iterations on the device without host synchronisation. */
@@ -221,6 +231,19 @@ int vhip_vecrstor_write(const char *path, const float *data, size_t n, size_t di
 int vhip_vecrstor_open(const char *path, size_t *n, size_t *dim);
 /* Copies the n x dim vectors of a VECRSTOR file (n, dim as vhip_vecrstor_open reported). */
 int vhip_vecrstor_read(const char *path, float *out, size_t n, size_t dim);
+/* MmapStorage::open + as_raw_slice (storage/mmap.rs:171-260) without a copy: the file mapped
+ * read-only, *data pointing at its n x dim floats until vhip_vecrstor_unmap.  Every entry point
+ * that takes host vectors accepts such a view; their uploads stream it from the page cache. */
+typedef struct vhip_vecrstor_view vhip_vecrstor_view;
+int vhip_vecrstor_map(const char *path, const float **data, size_t *n, size_t *dim, vhip_vecrstor_view **view);
+void vhip_vecrstor_unmap(vhip_vecrstor_view *view);
+/* CudaKnnEngine::new over MmapStorage::open(path).as_raw_slice() (knn.rs:85-140): the base is
+ * uploaded straight from the mapped file. */
+int vhip_knn_create_from_vecrstor(const char *path, int metric, int ordinal, vhip_knn **out);
+/* A k-means state over the concatenation of npaths VECRSTOR files (mpi_kmeans.rs:307-325 loads
+ * them into one Vec), uploaded from the mapped files one after another. */
+int vhip_kmeans_create_from_vecrstor(int ordinal, const char *const *paths, size_t npaths, int metric,
+                                     vhip_kmeans **out);
 /* IvfPqSerializer::save_centroid_file (ivf/serializer.rs:264-306): VRSKMEAN file (u64 magic
  * 0x5652534B4D45414E, u32 version 1, u8 metric, u32 dim, u32 k, u32 iterations, f32 inertia,
  * k x dim f32, little-endian). */

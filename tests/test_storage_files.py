@@ -96,6 +96,43 @@ def test_vecrstor_bytes(vh, tmp_path):
     assert p.read_bytes()[:8] == b"ROTSRCEV"  # "VECRSTOR" as a little-endian u64
 
 
+def test_vecrstor_map_view(vh, tmp_path):
+    """The zero-copy view: the pointer reads the file's floats in place, 24 bytes past its start,
+    and the same header checks as open() reject bad files."""
+    import ctypes
+
+    lib = vh._lib
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((37, 11)).astype(np.float32)
+    p = tmp_path / "m.bin"
+    vh.MmapStorage.create_from_flat(p, 11, x)
+    data, n, d, view = ctypes.POINTER(ctypes.c_float)(), ctypes.c_size_t(), ctypes.c_size_t(), ctypes.c_void_p()
+    assert lib.vhip_vecrstor_map(os.fsencode(p), ctypes.byref(data), ctypes.byref(n), ctypes.byref(d),
+                                 ctypes.byref(view)) == 0
+    try:
+        assert (n.value, d.value) == (37, 11)
+        got = np.ctypeslib.as_array(data, shape=(37 * 11,)).copy()
+        assert np.array_equal(got.reshape(37, 11), x)
+        # the view maps the file itself: the pointer sits at the mapping's start plus the header
+        assert ctypes.addressof(data.contents) % 4096 == 24
+    finally:
+        lib.vhip_vecrstor_unmap(view)
+    e = tmp_path / "e.bin"
+    vh.MmapStorage.create_from_flat(e, 3, np.zeros(0, np.float32))
+    assert lib.vhip_vecrstor_map(os.fsencode(e), ctypes.byref(data), ctypes.byref(n), ctypes.byref(d),
+                                 ctypes.byref(view)) == 0
+    assert (n.value, d.value) == (0, 3)
+    lib.vhip_vecrstor_unmap(view)
+    bad = tmp_path / "bad.bin"
+    bad.write_bytes(struct.pack("<QQQ", VEC_MAGIC, 10, 4) + b"\0" * 16)  # 10 x 4 floats promised, 4 present
+    rc = lib.vhip_vecrstor_map(os.fsencode(bad), ctypes.byref(data), ctypes.byref(n), ctypes.byref(d),
+                               ctypes.byref(view))
+    assert rc != 0 and not view.value and b"size mismatch" in lib.vhip_last_error()
+    rc = lib.vhip_vecrstor_map(os.fsencode(tmp_path / "missing.bin"), ctypes.byref(data), ctypes.byref(n),
+                               ctypes.byref(d), ctypes.byref(view))
+    assert rc != 0 and not view.value
+
+
 # ---- VRSKMEAN (ivf/serializer.rs) -----------------------------------------------------------
 def test_centroid_file_roundtrip(vh, tmp_path):
     p = tmp_path / "c.bin"

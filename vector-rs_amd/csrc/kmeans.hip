@@ -330,6 +330,16 @@ __global__ void k_fill(float *p, size_t count, float v) {
     if (i < count) p[i] = v;
 }
 
+// dst row r (dpad floats) = src row idx[r], for r < k.
+__global__ __launch_bounds__(256) void k_gather_rows(const float *__restrict__ src, const uint32_t *__restrict__ idx,
+                                                     int k, int dpad, float *__restrict__ dst) {
+    const size_t total = (size_t)k * dpad;
+    for (size_t t = blockIdx.x * 256 + threadIdx.x; t < total; t += (size_t)gridDim.x * 256) {
+        const size_t r = t / dpad, c = t - r * dpad;
+        dst[t] = src[(size_t)idx[r] * dpad + c];
+    }
+}
+
 }  // namespace vh
 
 struct vhip_kmeans {
@@ -357,12 +367,20 @@ namespace vh {
 
 static int km_norm_kind(int metric) { return metric == COS ? 2 : (metric == L2 ? 1 : 0); }
 
-static int km_create(int ordinal, const float *data, size_t n, size_t dim, int metric, vhip_kmeans **out) {
+// Points given as nseg host segments (segment i: counts[i] rows of dim floats), uploaded one after
+// another into one device buffer, so callers with several shards need no concatenated copy.
+static int km_create(int ordinal, const float *const *segs, const size_t *counts, size_t nseg, size_t dim, int metric,
+                     vhip_kmeans **out) {
     *out = nullptr;
     if (dim == 0) return set_error(VHIP_ERR_INVALID_CONFIG, "dimension must be > 0");
     if (dim > 1024) return set_error(VHIP_ERR_INVALID_CONFIG, "k-means supports dimension <= 1024");
     if (metric < 0 || metric > 9) return set_error(VHIP_ERR_INVALID_CONFIG, "unknown metric code");
-    if (n == 0 || !data) return set_error(VHIP_ERR_INVALID_CONFIG, "k-means needs at least one point");
+    size_t n = 0;
+    for (size_t i = 0; i < nseg; ++i) {
+        if (counts[i] && !segs[i]) return set_error(VHIP_ERR_INVALID_CONFIG, "a point segment is null");
+        n += counts[i];
+    }
+    if (n == 0) return set_error(VHIP_ERR_INVALID_CONFIG, "k-means needs at least one point");
     if (n > 0x7fffffffull) return set_error(VHIP_ERR_INVALID_CONFIG, "k-means supports n < 2^31 points");
     VH_CHECK(open_device(ordinal));
     std::unique_ptr<vhip_kmeans> K(new vhip_kmeans());
@@ -379,7 +397,12 @@ static int km_create(int ordinal, const float *data, size_t n, size_t dim, int m
     VH_CHECK(K->stager.init(ordinal));
     DevBuf raw;
     VH_CHECK(raw.ensure(ordinal, n * dim * sizeof(float)));
-    VH_CHECK(K->stager.h2d(raw.p, data, n * dim * sizeof(float), s));
+    size_t row = 0;
+    for (size_t i = 0; i < nseg; ++i) {
+        if (counts[i])
+            VH_CHECK(K->stager.h2d(raw.as<float>() + row * dim, segs[i], counts[i] * dim * sizeof(float), s));
+        row += counts[i];
+    }
     // points padded to a multiple of 128 rows with zero rows (their results are never written)
     VH_CHECK(K->pts.ensure(ordinal, K->n_pad * K->dpad * sizeof(float)));
     VH_CHECK(K->pnorm.ensure(ordinal, K->n_pad * sizeof(float)));
@@ -563,7 +586,14 @@ extern "C" {
 int vhip_kmeans_create(int ordinal, const float *data, size_t n, size_t dim, int metric, vhip_kmeans **out) {
     clear_error();
     if (!out) return set_error(VHIP_ERR_INVALID_CONFIG, "out is null");
-    return km_create(ordinal, data, n, dim, metric, out);
+    return km_create(ordinal, &data, &n, 1, dim, metric, out);
+}
+
+int vhip_kmeans_create_segments(int ordinal, const float *const *segments, const size_t *counts, size_t nseg,
+                                size_t dim, int metric, vhip_kmeans **out) {
+    clear_error();
+    if (!out || (nseg && (!segments || !counts))) return set_error(VHIP_ERR_INVALID_CONFIG, "null argument");
+    return km_create(ordinal, segments, counts, nseg, dim, metric, out);
 }
 
 int vhip_kmeans_set_centroids(vhip_kmeans *K, const float *centroids, size_t k) {
@@ -696,30 +726,39 @@ int vhip_dkmeans_check(size_t num_gpus) {
     return VHIP_OK;
 }
 
-int vhip_kmeans_fit(int ordinal, const float *data, size_t n, size_t dim, size_t k, size_t max_iters, float tol,
-                    int metric, const float *init_centroids, int init_mode, uint64_t seed, float *out_centroids,
-                    int32_t *out_assign, vhip_kmeans_result *result) {
+int vhip_kmeans_fit_state(vhip_kmeans *K, size_t k, size_t max_iters, float tol, const float *init_centroids,
+                          int init_mode, uint64_t seed, float *out_centroids, int32_t *out_assign,
+                          vhip_kmeans_result *result) {
     clear_error();
-    if (!result) return set_error(VHIP_ERR_INVALID_CONFIG, "result is null");
-    *result = vhip_kmeans_result{dim, 0, 0, 0.0f};
-    if (n == 0 || k == 0) return VHIP_OK;  // kmeans.rs:67-76
-    const size_t ek = std::min(k, n);
+    if (!K || !result) return set_error(VHIP_ERR_INVALID_CONFIG, "null state or result");
+    *result = vhip_kmeans_result{K->dim, 0, 0, 0.0f};
+    if (k == 0) return VHIP_OK;  // kmeans.rs:67-76
+    const size_t n = K->n, dim = K->dim, ek = std::min(k, n);
     if (!out_centroids) return set_error(VHIP_ERR_INVALID_CONFIG, "out_centroids is null");
     if (init_mode != VHIP_INIT_KMEANSPP && init_mode != VHIP_INIT_SHUFFLE)
         return set_error(VHIP_ERR_INVALID_CONFIG, "unknown init mode");
-    vhip_kmeans *raw = nullptr;
-    VH_CHECK(km_create(ordinal, data, n, dim, metric, &raw));
-    std::unique_ptr<vhip_kmeans> K(raw);
     if (init_centroids) {
-        VH_CHECK(vhip_kmeans_set_centroids(K.get(), init_centroids, ek));
+        VH_CHECK(vhip_kmeans_set_centroids(K, init_centroids, ek));
     } else if (init_mode == VHIP_INIT_SHUFFLE) {
-        // DistributedKMeansEngine::init_random (distributed_kmeans.rs:524-535), seeded
+        // DistributedKMeansEngine::init_random (distributed_kmeans.rs:524-535), seeded: the first
+        // ek indices of a seeded permutation, gathered from the resident points
+        std::lock_guard<std::mutex> lock(K->mu);
+        VH_CHECK(open_device(K->dev));
         std::vector<uint32_t> idx = row_permutation(n, seed);
-        std::vector<float> c(ek * dim);
-        for (size_t j = 0; j < ek; ++j) std::memcpy(&c[j * dim], data + (size_t)idx[j] * dim, dim * sizeof(float));
-        VH_CHECK(vhip_kmeans_set_centroids(K.get(), c.data(), ek));
+        DevBuf didx, rows;
+        VH_CHECK(didx.ensure(K->dev, ek * sizeof(uint32_t)));
+        VH_CHECK(rows.ensure(K->dev, ek * K->dpad * sizeof(float)));
+        VH_HIP(hipMemcpyAsync(didx.p, idx.data(), ek * sizeof(uint32_t), hipMemcpyHostToDevice, K->stream));
+        const unsigned blocks = (unsigned)std::min<size_t>(4096, (ek * K->dpad + 255) / 256);
+        hipLaunchKernelGGL(k_gather_rows, dim3(blocks), dim3(256), 0, K->stream, K->pts.as<float>(),
+                           didx.as<uint32_t>(), (int)ek, (int)K->dpad, rows.as<float>());
+        VH_HIP(hipGetLastError());
+        VH_CHECK(km_set_centroids_dev(K, rows.as<float>(), ek, K->dpad));
+        VH_HIP(hipStreamSynchronize(K->stream));  // didx/rows/idx are released at scope end
     } else {
-        VH_CHECK(km_init_kmeanspp(K.get(), ek, seed));
+        std::lock_guard<std::mutex> lock(K->mu);
+        VH_CHECK(open_device(K->dev));
+        VH_CHECK(km_init_kmeanspp(K, ek, seed));
     }
     size_t iters = 0;
     {
@@ -728,7 +767,7 @@ int vhip_kmeans_fit(int ordinal, const float *data, size_t n, size_t dim, size_t
         std::vector<float> sh(ek);
         for (size_t it = 0; it < max_iters; ++it) {
             iters = it + 1;
-            VH_CHECK(km_iterate(K.get()));
+            VH_CHECK(km_iterate(K));
             if (tol >= 0.0f) {  // kmeans.rs:218-223: only K floats cross PCIe per iteration
                 VH_HIP(hipMemcpyAsync(sh.data(), K->shifts.p, ek * sizeof(float), hipMemcpyDeviceToHost, K->stream));
                 VH_HIP(hipStreamSynchronize(K->stream));
@@ -740,9 +779,23 @@ int vhip_kmeans_fit(int ordinal, const float *data, size_t n, size_t dim, size_t
         VH_HIP(hipStreamSynchronize(K->stream));
     }
     float inertia = 0.0f;
-    VH_CHECK(vhip_kmeans_read(K.get(), out_centroids, out_assign, nullptr, nullptr, nullptr, &inertia));
+    VH_CHECK(vhip_kmeans_read(K, out_centroids, out_assign, nullptr, nullptr, nullptr, &inertia));
     *result = vhip_kmeans_result{dim, ek, iters, inertia};
     return VHIP_OK;
+}
+
+int vhip_kmeans_fit(int ordinal, const float *data, size_t n, size_t dim, size_t k, size_t max_iters, float tol,
+                    int metric, const float *init_centroids, int init_mode, uint64_t seed, float *out_centroids,
+                    int32_t *out_assign, vhip_kmeans_result *result) {
+    clear_error();
+    if (!result) return set_error(VHIP_ERR_INVALID_CONFIG, "result is null");
+    *result = vhip_kmeans_result{dim, 0, 0, 0.0f};
+    if (n == 0 || k == 0) return VHIP_OK;  // kmeans.rs:67-76
+    vhip_kmeans *raw = nullptr;
+    VH_CHECK(km_create(ordinal, &data, &n, 1, dim, metric, &raw));
+    std::unique_ptr<vhip_kmeans> K(raw);
+    return vhip_kmeans_fit_state(K.get(), k, max_iters, tol, init_centroids, init_mode, seed, out_centroids,
+                                 out_assign, result);
 }
 
 }  // extern "C"

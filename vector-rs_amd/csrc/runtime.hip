@@ -2,6 +2,7 @@
 // host-side top_k_reduce of the C ABI.
 #include <algorithm>
 #include <cmath>
+#include <thread>
 
 #include "vh_runtime.h"
 
@@ -66,6 +67,31 @@ int device_grid_cap(int ordinal) {
 }
 
 // ---- pinned staging ---------------------------------------------------------------------
+namespace {
+// Host copy into a pinned block, split over a few threads for large blocks: a single thread
+// copying from pageable (or freshly mapped, page-cache backed) memory reaches only a fraction of
+// what the PCIe DMA drains.
+void staged_copy(void *dst, const void *src, size_t bytes) {
+    constexpr size_t kPart = 4u << 20;
+    const unsigned hw = std::max(1u, std::thread::hardware_concurrency());
+    const unsigned nt = (unsigned)std::min<size_t>(std::min(8u, hw), (bytes + kPart - 1) / kPart);
+    if (nt <= 1) {
+        std::memcpy(dst, src, bytes);
+        return;
+    }
+    const size_t per = (bytes + nt - 1) / nt;
+    std::vector<std::thread> th;
+    th.reserve(nt - 1);
+    for (unsigned t = 1; t < nt; ++t) {
+        const size_t o = t * per;
+        if (o >= bytes) break;
+        th.emplace_back([=] { std::memcpy((char *)dst + o, (const char *)src + o, std::min(per, bytes - o)); });
+    }
+    std::memcpy(dst, src, std::min(per, bytes));
+    for (auto &x : th) x.join();
+}
+}  // namespace
+
 PinnedStager::~PinnedStager() {
     if (dev >= 0) (void)hipSetDevice(dev);
     for (int i = 0; i < 2; ++i) {
@@ -92,7 +118,7 @@ int PinnedStager::h2d(void *dst, const void *src, size_t bytes, hipStream_t s) {
     while (off < bytes) {
         const size_t b = std::min(kBlock, bytes - off);
         if (pending[i]) VH_HIP(hipEventSynchronize(ev[i]));
-        std::memcpy(buf[i], (const char *)src + off, b);
+        staged_copy(buf[i], (const char *)src + off, b);
         VH_HIP(hipMemcpyAsync((char *)dst + off, buf[i], b, hipMemcpyHostToDevice, s));
         VH_HIP(hipEventRecord(ev[i], s));
         pending[i] = true;

@@ -12,6 +12,10 @@
 //      u8 metric, u32 dim, u32 nlist, nprobe, num_subvectors, sub_clusters, max_kmeans_iters,
 //      f32 tolerance, u32 centroid count + f32 coarse centroids, u32 codebook length + f32
 //      codebooks, u32 list count, then per list u32 count, count x u32 ids, count x M code bytes.
+//  * Zero-copy VECRSTOR views (vhip_vecrstor_map): the file mapped read-only, its data handed
+//      to the engines' uploads, which stream it from the page cache through their pinned staging
+//      buffers: no host copy of the vectors (the reference copies every shard into one Vec,
+//      mpi_kmeans.rs:307-325, and CudaKnnEngine copies and transposes the base, knn.rs:111-122).
 //  * Offline trainer: vector-mpi fit_cuda_aware (src/distributed_kmeans.rs:375-415) reached from
 //      mpi_kmeans --use-cuda (src/bin/mpi_kmeans.rs:284-364): load data_dir/shard_0.bin,
 //      shard_1.bin, ... (until the first missing index), fit k-means on the GPU, write the
@@ -23,7 +27,10 @@
 #include <cstring>
 #include <memory>
 #include <string>
+#include <fcntl.h>
+#include <sys/mman.h>
 #include <sys/stat.h>
+#include <unistd.h>
 #include <vector>
 
 #include "vector_hip.h"
@@ -439,6 +446,82 @@ int vhip_ivfpq_file_load(const char *path, float *coarse, float *codebooks, uint
     return ivfpq_read(path, &h, coarse, codebooks, list_sizes, ids, codes);
 }
 
+struct vhip_vecrstor_view {
+    void *base = nullptr;
+    size_t bytes = 0;
+    size_t n = 0, dim = 0;
+    ~vhip_vecrstor_view() {
+        if (base) munmap(base, bytes);
+    }
+};
+
+int vhip_vecrstor_map(const char *path, const float **data, size_t *n, size_t *dim, vhip_vecrstor_view **view) {
+    vh::clear_error();
+    if (!path || !data || !n || !dim || !view) return vh::set_error(VHIP_ERR_INVALID_CONFIG, "null argument");
+    *view = nullptr;
+    *data = nullptr;
+    size_t fn = 0, fd = 0;
+    const int rc = vec_header(path, &fn, &fd);
+    if (rc != VHIP_OK) return rc;
+    std::unique_ptr<vhip_vecrstor_view> v(new vhip_vecrstor_view());
+    v->n = fn;
+    v->dim = fd;
+    v->bytes = kVecHeader + fn * fd * sizeof(float);
+    const int fdesc = open(path, O_RDONLY);
+    if (fdesc < 0) return io_error("cannot open vector file", path);
+    void *m = mmap(nullptr, v->bytes, PROT_READ, MAP_PRIVATE, fdesc, 0);
+    close(fdesc);
+    if (m == MAP_FAILED) return io_error("cannot map vector file", path);
+    v->base = m;
+    (void)madvise(m, v->bytes, MADV_SEQUENTIAL);
+    // the format is little-endian; a big-endian host would need a converting read instead
+    if (!host_is_le()) return vh::set_error(VHIP_ERR_INVALID_CONFIG, "mapped VECRSTOR views need a little-endian host");
+    *data = reinterpret_cast<const float *>(static_cast<const unsigned char *>(m) + kVecHeader);
+    *n = fn;
+    *dim = fd;
+    *view = v.release();
+    return VHIP_OK;
+}
+
+void vhip_vecrstor_unmap(vhip_vecrstor_view *view) { delete view; }
+
+int vhip_knn_create_from_vecrstor(const char *path, int metric, int ordinal, vhip_knn **out) {
+    vh::clear_error();
+    if (!out) return vh::set_error(VHIP_ERR_INVALID_CONFIG, "out is null");
+    *out = nullptr;
+    const float *data = nullptr;
+    size_t n = 0, dim = 0;
+    vhip_vecrstor_view *v = nullptr;
+    int rc = vhip_vecrstor_map(path, &data, &n, &dim, &v);
+    if (rc != VHIP_OK) return rc;
+    std::unique_ptr<vhip_vecrstor_view> hold(v);
+    return vhip_knn_create(data, n, dim, metric, ordinal, out);
+}
+
+int vhip_kmeans_create_from_vecrstor(int ordinal, const char *const *paths, size_t npaths, int metric,
+                                     vhip_kmeans **out) {
+    vh::clear_error();
+    if (!out || (npaths && !paths)) return vh::set_error(VHIP_ERR_INVALID_CONFIG, "null argument");
+    *out = nullptr;
+    std::vector<std::unique_ptr<vhip_vecrstor_view>> views;
+    std::vector<const float *> segs;
+    std::vector<size_t> counts;
+    size_t dim = 0;
+    for (size_t i = 0; i < npaths; ++i) {
+        const float *data = nullptr;
+        size_t n = 0, d = 0;
+        vhip_vecrstor_view *v = nullptr;
+        const int rc = vhip_vecrstor_map(paths[i], &data, &n, &d, &v);
+        if (rc != VHIP_OK) return rc;
+        views.emplace_back(v);
+        if (i == 0) dim = d;
+        else if (d != dim) return vh::set_error(VHIP_ERR_INVALID_CONFIG, "dimension mismatch across shard files");
+        segs.push_back(data);
+        counts.push_back(n);
+    }
+    return vhip_kmeans_create_segments(ordinal, segs.data(), counts.data(), segs.size(), dim, metric, out);
+}
+
 int vhip_train_from_shards(const char *data_dir, size_t k, size_t max_iters, float tol, int metric, size_t num_gpus,
                            const char *output, uint64_t seed, vhip_kmeans_result *result, size_t *num_shards) {
     vh::clear_error();
@@ -457,24 +540,21 @@ int vhip_train_from_shards(const char *data_dir, size_t k, size_t max_iters, flo
     if (shards.empty())
         return vh::set_error(VHIP_ERR_INVALID_CONFIG, std::string("no shard files (shard_0.bin, shard_1.bin, ...) "
                                                                   "found in ") + data_dir);
-    std::vector<float> all;
-    size_t dim = 0;
+    // shards are mapped and uploaded one after another: no concatenated host copy
+    std::vector<const char *> paths;
+    for (const std::string &p : shards) paths.push_back(p.c_str());
+    vhip_kmeans *K = nullptr;
+    int rc = vhip_kmeans_create_from_vecrstor(0, paths.data(), paths.size(), metric, &K);
+    if (rc != VHIP_OK) return rc;
+    std::unique_ptr<vhip_kmeans, void (*)(vhip_kmeans *)> hold(K, vhip_kmeans_destroy);
+    size_t dim = 0, n = 0;
     for (const std::string &p : shards) {
-        size_t n = 0, d = 0;
-        int rc = vhip_vecrstor_open(p.c_str(), &n, &d);
-        if (rc != VHIP_OK) return rc;
-        if (dim == 0) dim = d;
-        else if (d != dim) return vh::set_error(VHIP_ERR_INVALID_CONFIG, "dimension mismatch across shard files");
-        const size_t off = all.size();
-        all.resize(off + n * d);
-        rc = vhip_vecrstor_read(p.c_str(), all.data() + off, n, d);
-        if (rc != VHIP_OK) return rc;
+        size_t sn = 0;
+        (void)vhip_vecrstor_open(p.c_str(), &sn, &dim);
+        n += sn;
     }
-    if (dim == 0) return vh::set_error(VHIP_ERR_INVALID_CONFIG, "shard files hold zero-dimensional vectors");
-    const size_t n = all.size() / dim;
     std::vector<float> cent(std::min(k, n) * dim);
-    int rc = vhip_kmeans_fit(0, all.data(), n, dim, k, max_iters, tol, metric, nullptr, VHIP_INIT_KMEANSPP, seed,
-                             cent.data(), nullptr, result);
+    rc = vhip_kmeans_fit_state(K, k, max_iters, tol, nullptr, VHIP_INIT_KMEANSPP, seed, cent.data(), nullptr, result);
     if (rc != VHIP_OK) return rc;
     const std::string out = std::string(data_dir) + "/" + output;
     rc = vhip_centroid_file_save(out.c_str(), cent.data(), result->dimension, result->k, metric, result->iterations,

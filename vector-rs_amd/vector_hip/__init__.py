@@ -152,6 +152,15 @@ if _HAS_IVFPQ:
 _sig("vhip_vecrstor_write", _int, ctypes.c_char_p, _f32p, _sz, _sz)
 _sig("vhip_vecrstor_open", _int, ctypes.c_char_p, _szp, _szp)
 _sig("vhip_vecrstor_read", _int, ctypes.c_char_p, _f32p, _sz, _sz)
+_sig("vhip_knn_create_from_vecrstor", _int, ctypes.c_char_p, _int, _int, ctypes.POINTER(_vp))
+_sig("vhip_vecrstor_map", _int, ctypes.c_char_p, ctypes.POINTER(_f32p), _szp, _szp, ctypes.POINTER(_vp))
+_sig("vhip_vecrstor_unmap", None, _vp)
+if _HAS_KMEANS:
+    _sig("vhip_kmeans_create_from_vecrstor", _int, _int, ctypes.POINTER(ctypes.c_char_p), _sz, _int,
+         ctypes.POINTER(_vp))
+    _sig("vhip_kmeans_create_segments", _int, _int, ctypes.POINTER(_f32p), _szp, _sz, _sz, _int, ctypes.POINTER(_vp))
+    _sig("vhip_kmeans_fit_state", _int, _vp, _sz, _sz, ctypes.c_float, _f32p, _int, ctypes.c_uint64, _f32p, _i32p,
+         ctypes.POINTER(_KMeansResultC))
 _sig("vhip_centroid_file_save", _int, ctypes.c_char_p, _f32p, _sz, _sz, _int, _sz, ctypes.c_float)
 _sig("vhip_centroid_file_info", _int, ctypes.c_char_p, _szp, _szp, ctypes.POINTER(_int), _szp, _f32p)
 _sig("vhip_centroid_file_load", _int, ctypes.c_char_p, _f32p, _sz, _sz)
@@ -344,6 +353,19 @@ class CudaKnnEngine(_Profiled):
     @classmethod
     def new(cls, dataset, dimension, metric):
         return cls(dataset, dimension, metric, 0)
+
+    @classmethod
+    def from_vecrstor(cls, path, metric=DistanceMetric.L2Squared, ordinal: int = 0) -> "CudaKnnEngine":
+        """CudaKnnEngine::new over MmapStorage::open(path): the base streams from the mapped file
+        to the GPU with no host copy."""
+        self = cls.__new__(cls)
+        n, d = ctypes.c_size_t(), ctypes.c_size_t()
+        _check(_lib.vhip_vecrstor_open(_path(path), ctypes.byref(n), ctypes.byref(d)))
+        h = _vp()
+        _check(_lib.vhip_knn_create_from_vecrstor(_path(path), int(metric), ordinal, ctypes.byref(h)))
+        self._h = h
+        self._dim = d.value
+        return self
 
     @classmethod
     def with_ordinal(cls, dataset, dimension, metric, ordinal):
@@ -623,6 +645,38 @@ class KMeansState(_Profiled):
             _lib.vhip_kmeans_destroy(h)
             self._h = None
 
+    @classmethod
+    def from_vecrstor(cls, paths, metric=DistanceMetric.L2Squared, ordinal: int = 0) -> "KMeansState":
+        """A state over the rows of one or more VECRSTOR files, uploaded from the mapped files one
+        after another (no concatenated host copy)."""
+        paths = [paths] if isinstance(paths, (str, bytes, os.PathLike)) else list(paths)
+        n, d = 0, 0
+        for pth in paths:
+            fn, fd = ctypes.c_size_t(), ctypes.c_size_t()
+            _check(_lib.vhip_vecrstor_open(_path(pth), ctypes.byref(fn), ctypes.byref(fd)))
+            n, d = n + fn.value, fd.value
+        arr = (ctypes.c_char_p * len(paths))(*[_path(pth) for pth in paths])
+        self = cls.__new__(cls)
+        type(self)._prof_fn = _lib.vhip_kmeans_profile
+        type(self)._read_fn = _lib.vhip_kmeans_profile_read
+        h = _vp()
+        _check(_lib.vhip_kmeans_create_from_vecrstor(ordinal, arr, len(paths), int(metric), ctypes.byref(h)))
+        self._h, self._n, self._d, self._k = h, n, d, 0
+        return self
+
+    def fit(self, k: int, max_iters: int, tolerance: float, init=None, init_mode: int = 0, seed: int = 42):
+        """CudaKMeansEngine::fit on the resident points: (centroids [k, d], assign int32[n], result)."""
+        ek = min(k, self._n)
+        c = np.zeros((max(ek, 1), self._d), np.float32)
+        a = np.zeros(max(self._n, 1), np.int32)
+        ini = None if init is None else np.ascontiguousarray(init, dtype=np.float32).reshape(-1, self._d)
+        res = _KMeansResultC()
+        _check(_lib.vhip_kmeans_fit_state(self._h, k, max_iters, float(tolerance),
+                                          _p(ini, _f32p) if ini is not None else None, init_mode, seed,
+                                          _p(c, _f32p), _p(a, _i32p), ctypes.byref(res)))
+        self._k = ek
+        return c[:ek], a[:self._n], (int(res.dimension), int(res.k), int(res.iterations), float(res.inertia))
+
     def set_centroids(self, centroids):
         c = np.ascontiguousarray(centroids, dtype=np.float32).reshape(-1, self._d)
         self._k = c.shape[0]
@@ -720,8 +774,9 @@ def _path(p) -> bytes:
 
 
 class MmapStorage:
-    """VECRSTOR vector files (storage/mmap.rs:9-16): create / create_from_flat write one,
-    open validates and loads it (the reference memory-maps; this reads the data once)."""
+    """VECRSTOR vector files (storage/mmap.rs:9-16): create / create_from_flat write one, open
+    validates the header and maps the file read-only (numpy memmap), so as_raw_slice() is a
+    view of the mapping: engines built from it upload straight from the page cache."""
 
     def __init__(self, data: np.ndarray, dimension: int):
         self._data = data
@@ -747,8 +802,9 @@ class MmapStorage:
         n = ctypes.c_size_t()
         d = ctypes.c_size_t()
         _check(_lib.vhip_vecrstor_open(_path(path), ctypes.byref(n), ctypes.byref(d)))
-        data = np.empty((n.value, d.value), np.float32)
-        _check(_lib.vhip_vecrstor_read(_path(path), _p(data, _f32p), n.value, d.value))
+        if n.value * d.value == 0:
+            return cls(np.zeros((n.value, d.value), np.float32), d.value)
+        data = np.memmap(os.fspath(path), dtype="<f4", mode="r", offset=24, shape=(n.value, d.value))
         return cls(data, d.value)
 
     def dimension(self) -> int:
