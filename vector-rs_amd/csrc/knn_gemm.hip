@@ -33,8 +33,12 @@
 // The grid is persistent and XCD-aware: work items are handed out so that the workgroups
 // resident on one XCD walk the same base rows together and share them through that XCD's L2.
 //
-// FILTER epilogue: per score two VALU operations decide "may pass" against a slightly loose
-// threshold; only groups of 8 scores in which some lane may pass take the exact path.  Passing
+// FILTER epilogue: scores are tested against a slightly loose threshold, per group of 8 (4 rows x
+// 2 columns per lane) first on each column's best value (two compares per group); only a group
+// in which some lane may pass takes the per-score and exact tests.  In k_mfma_hs the squared-L2
+// accumulators start from the row norms and the column tile holds -2 q, so the accumulator is
+// the test value ||x||^2 - 2 q.x itself (exact for integer data in [0, 255] at dpad <= 128: every
+// partial sum stays below 2^24 in magnitude).  Passing
 // (score, row) pairs are appended to per-query LDS slots (LDS atomics) and flushed to the
 // global per-query candidate lists once per work item, with one global atomic per query.  The
 // host sizes each round's work items so that the expected passes per query and item stay well
@@ -187,7 +191,9 @@ __device__ __forceinline__ void item_begin(EpiState &st, const ScanArgs &a, int 
             const float t = v ? a.tau[q] : -INFINITY;
             st.tau_e[cb] = t;
             if constexpr (M == L2) {
-                // |(qn + xn - 2 q.x) - (qn + fl(xn - 2 q.x))| <= 2^-21 (qn + xn); the slack doubles that.
+                // The loose test compares u = xn - 2 q.x (as computed) with T; the exact score is
+                // fl(qn + u) (register kernel) or fl(fl(qn + xn) - 2 q.x) (the others), which
+                // differ from qn + u by at most 2^-21 (qn + xn + |t|); the slack doubles that.
                 st.T[cb] = (t < INFINITY && t > -INFINITY)
                                ? (t - st.cn[cb]) + 0x1p-19f * (st.cn[cb] + a.anorm_max + fabsf(t))
                                : t;
@@ -208,7 +214,11 @@ __device__ __forceinline__ void item_begin(EpiState &st, const ScanArgs &a, int 
 }
 
 // Appends (key, row) to query column ql's LDS slots; a full slot list spills to the global
-// candidate list with one atomic per entry.
+// candidate list with one atomic per entry.  The spill path (rare: the host sizes work items so
+// that the expected passes stay well below SLOTS) waits for its own store, so no vector-memory
+// store is pending where it rejoins the main loop: with loads alone in flight the compiler can
+// wait for exactly the operand loads each MFMA step needs, rather than for all of them
+// (including the prefetch of the next step).
 template <int SLOTS>
 __device__ __forceinline__ void append_candidate(const ScanArgs &a, int ql, uint32_t key, uint32_t row_in_item,
                                                  long r_lo, int col0, uint32_t *s_qcnt, uint2 *s_slot) {
@@ -217,8 +227,10 @@ __device__ __forceinline__ void append_candidate(const ScanArgs &a, int ql, uint
         s_slot[ql * SLOTS + r] = make_uint2(key, row_in_item);
     } else {
         const int q = col0 + ql;
-        const uint32_t at = atomicAdd(&a.cnt[q], 1u);
-        if (at < (uint32_t)a.cap) a.cand[(size_t)q * a.cap + at] = make_uint2(key, (uint32_t)(r_lo + row_in_item));
+        const uint32_t at = __hip_atomic_fetch_add((gu32 *)a.cnt + q, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (at < (uint32_t)a.cap)
+            ((gu64 *)a.cand)[(size_t)q * a.cap + at] = pack_u2(key, (uint32_t)(r_lo + row_in_item));
+        __builtin_amdgcn_s_waitcnt(VH_VMCNT(0));
     }
 }
 
@@ -754,22 +766,41 @@ __global__ __launch_bounds__(512, 1) void k_mfma_pnl(ScanArgs a) {
 
 // Epilogue pieces of one half.  acc2[cb] register 4g+j holds row rb0 + 8g + j (rb0 = the half's
 // first row in this lane's layout, i.e. rs + 64 wr + 32 hf + 4 h) and column 64wc + 32cb + l32.
+// For squared L2 the register kernel's accumulators start from the row norms and its column
+// tile holds the queries times -2, so a register already holds u = ||x||^2 - 2 q.x and the
+// score is max(||q||^2 + u, 0); for the other metrics it holds q.x.
 template <int M, int SLOTS>
 __device__ __forceinline__ void filter_group(const floatx16 (&acc2)[2], floatx4 n4, const EpiState &st,
                                              const ScanArgs &a, int wc, int l32, uint32_t row_g, long r_lo,
                                              int col0, uint32_t *s_qcnt, uint2 *s_slot, int g, bool enable) {
     bool p[4][2];
     bool any = false;
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
+    if (!(M == COS && st.guard)) {
+        // Wave test on each column's extremum over the group's 4 rows: two compares, whose lane
+        // masks are OR-ed in scalar registers.  Only a group with some candidate lane takes the
+        // per-score tests below.
+        float e[2];
 #pragma unroll
         for (int cb = 0; cb < 2; ++cb) {
-            const float dot = acc2[cb][4 * g + j];
-            if constexpr (M == L2) p[j][cb] = fmaf(-2.0f, dot, n4[j]) <= st.T[cb];
-            else p[j][cb] = dot >= st.T[cb];
-            any = any || p[j][cb];
+            const float v0 = acc2[cb][4 * g], v1 = acc2[cb][4 * g + 1];
+            const float v2 = acc2[cb][4 * g + 2], v3 = acc2[cb][4 * g + 3];
+            // fminf / fmaxf ignore the quiet NaN of padding rows
+            e[cb] = M == L2 ? fminf(fminf(v0, v1), fminf(v2, v3)) : fmaxf(fmaxf(v0, v1), fmaxf(v2, v3));
         }
-    if (M == COS && st.guard) {
+        const uint64_t m = M == L2 ? __builtin_amdgcn_ballot_w64(e[0] <= st.T[0]) |
+                                         __builtin_amdgcn_ballot_w64(e[1] <= st.T[1])
+                                   : __builtin_amdgcn_ballot_w64(e[0] >= st.T[0]) |
+                                         __builtin_amdgcn_ballot_w64(e[1] >= st.T[1]);
+        if (!(m != 0 && enable)) return;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb) {
+                const float v = acc2[cb][4 * g + j];
+                p[j][cb] = M == L2 ? v <= st.T[cb] : v >= st.T[cb];
+            }
+        any = true;
+    } else {
         // a (query, row) pair with ||q|| ||x|| <= 1e-9 has similarity 0 (knn.cu:168-173)
         any = false;
 #pragma unroll
@@ -791,7 +822,7 @@ __device__ __forceinline__ void filter_group(const floatx16 (&acc2)[2], floatx4 
                 const float dot = acc2[cb][4 * g + j];
                 float sc;
                 if constexpr (M == L2) {
-                    sc = fmaxf(fmaf(-2.0f, dot, st.cn[cb] + n4[j]), 0.0f);
+                    sc = fmaxf(st.cn[cb] + dot, 0.0f);  // dot holds u (see above)
                     if (!(sc <= st.tau_e[cb])) continue;
                 } else if constexpr (M == DOT) {
                     sc = canon(-dot);
@@ -817,7 +848,7 @@ __device__ __forceinline__ void dense_group(const floatx16 (&acc2)[2], floatx4 n
         for (int j = 0; j < 4; ++j) {
             const float dot = acc2[cb][4 * g + j];
             float sc;
-            if constexpr (M == L2) sc = fmaxf(fmaf(-2.0f, dot, st.cn[cb] + n4[j]), 0.0f);
+            if constexpr (M == L2) sc = fmaxf(st.cn[cb] + dot, 0.0f);  // dot holds u (see filter_group)
             else if constexpr (M == DOT) sc = canon(-dot);
             else sc = st.cn[cb] * n4[j] > 1e-9f ? canon(-dot) : 0.0f;
             key[j] = score_key(sc);
@@ -872,6 +903,9 @@ __device__ __forceinline__ void assign_half(floatx16 (&acc2)[2], const floatx4 (
 template <int MODE, int M, int NK>
 __global__ __launch_bounds__(512, 1) void k_mfma_hs(ScanArgs a) {
     constexpr int RW = 4, TR = 256, D = 32 * NK;
+    // squared-L2 scan: accumulators start from the row norms and the column tile holds -2 q, so
+    // they end as ||x||^2 - 2 q.x (the filter's test value) with no epilogue arithmetic
+    constexpr bool FUSE = M == L2 && MODE != kAssign;
     __shared__ floatx4 sB[kTileCols * 8 * NK];
     __shared__ uint32_t s_qcnt[MODE == kFilter ? kTileCols : 1];
     __shared__ uint2 s_slot[MODE == kFilter ? kTileCols * kRegSlots : 1];
@@ -897,6 +931,10 @@ __global__ __launch_bounds__(512, 1) void k_mfma_hs(ScanArgs a) {
             const int r = f / (8 * NK), rem = f % (8 * NK);
             rq[i] = *(const floatx4 *)(a.B + (long)(c0 + r) * D + 4 * rem);
         }
+        if constexpr (FUSE) {
+#pragma unroll
+            for (int i = 0; i < 2 * NK; ++i) rq[i] = rq[i] * -2.0f;  // exact
+        }
 #pragma unroll
         for (int i = 0; i < 2 * NK; ++i) {
             const int f = tid + 512 * i;
@@ -914,7 +952,8 @@ __global__ __launch_bounds__(512, 1) void k_mfma_hs(ScanArgs a) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) n[g] = *(const floatx4 *)(a.anorm + rs + 64 * wr + 32 * hf + 8 * g + 4 * h);
     };
-    auto mfma_step = [&](floatx16 (&ac)[2], const floatx4 (&ra)[4], int kc) {
+    // `first`: the accumulators start from `init` instead of their contents
+    auto mfma_step = [&](floatx16 (&ac)[2], const floatx4 (&ra)[4], int kc, const floatx16 &init, bool first) {
         const int rb0 = 64 * wc + l32, rb1 = rb0 + 32;
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
@@ -923,10 +962,20 @@ __global__ __launch_bounds__(512, 1) void k_mfma_hs(ScanArgs a) {
             const floatx4 b1 = sB[bidx_kc(rb1, kc, c4)];
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
-                ac[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(ra[g][t], b0[t], ac[0], 0, 0, 0);
-                ac[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(ra[g][t], b1[t], ac[1], 0, 0, 0);
+                const bool i0 = first && g == 0 && t == 0;
+                ac[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(ra[g][t], b0[t], i0 ? init : ac[0], 0, 0, 0);
+                ac[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(ra[g][t], b1[t], i0 ? init : ac[1], 0, 0, 0);
             }
         }
+    };
+    // the 4 x 4 row values of a half in accumulator order (register 4g+j = row 8g+j of the lane)
+    auto n16 = [](const floatx4 (&n)[4]) {
+        floatx16 v;
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[4 * g + j] = n[g][j];
+        return v;
     };
 
     int col0;
@@ -992,15 +1041,18 @@ __global__ __launch_bounds__(512, 1) void k_mfma_hs(ScanArgs a) {
         }
         // ---- half 0: MFMAs into acc[0]; epilogue of the previous stage's half 1 ----
         load_n(nrm[0], rs, 0);
-        acc[0][0] = floatx16{0};
-        acc[0][1] = floatx16{0};
+        if constexpr (!FUSE) {
+            acc[0][0] = floatx16{0};
+            acc[0][1] = floatx16{0};
+        }
+        const floatx16 init0 = n16(nrm[0]);
 #pragma unroll
         for (int kc = 0; kc < NK; ++kc) {
             floatx4 nxt[4];
             if (kc + 1 < NK) load_a(nxt, rs, 0, kc + 1);
             else load_a(nxt, rs, 1, 0);
             __builtin_amdgcn_sched_barrier(0);
-            mfma_step(acc[0], cur, kc);
+            mfma_step(acc[0], cur, kc, init0, FUSE && kc == 0);
             epi(acc[1], nrm[1], rs - TR, 1, (4 * kc) / NK, (4 * (kc + 1)) / NK, prev);
             interleave();
 #pragma unroll
@@ -1008,8 +1060,11 @@ __global__ __launch_bounds__(512, 1) void k_mfma_hs(ScanArgs a) {
         }
         // ---- half 1: MFMAs into acc[1]; epilogue of this stage's half 0 ----
         load_n(nrm[1], rs, 1);
-        acc[1][0] = floatx16{0};
-        acc[1][1] = floatx16{0};
+        if constexpr (!FUSE) {
+            acc[1][0] = floatx16{0};
+            acc[1][1] = floatx16{0};
+        }
+        const floatx16 init1 = n16(nrm[1]);
 #pragma unroll
         for (int kc = 0; kc < NK; ++kc) {
             floatx4 nxt[4];
@@ -1017,7 +1072,7 @@ __global__ __launch_bounds__(512, 1) void k_mfma_hs(ScanArgs a) {
             if (!last) load_a(nxt, rs, 1, kc + 1);
             else if (more) load_a(nxt, nrs, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
-            mfma_step(acc[1], cur, kc);
+            mfma_step(acc[1], cur, kc, init1, FUSE && kc == 0);
             epi(acc[0], nrm[0], rs, 0, (4 * kc) / NK, (4 * (kc + 1)) / NK, true);
             interleave();
             if (!last || more) {

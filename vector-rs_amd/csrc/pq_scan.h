@@ -260,10 +260,6 @@ __device__ __forceinline__ float adc_score(const uint8_t *__restrict__ cp, const
     return total;
 }
 
-// s_waitcnt immediate that waits until at most n (< 16) vector memory operations are
-// outstanding, leaving the export and LDS counters unconstrained.
-#define VH_VMCNT(n) (((n) & 15) | (7 << 4) | (15 << 8))
-
 // Waits until at most `younger` (<= ring_chunks(NV) - 2) chunks of NV + 1 DMAs each are still
 // in flight: s_waitcnt takes its count as an immediate, hence one case per count.
 template <int NV>

@@ -25,6 +25,19 @@ constexpr int kTileCols = 128;       // queries (or k-means points) per MFMA wor
 constexpr int kRowAlign = 256;       // row counts of MFMA row operands and round boundaries
                                      // are multiples of this (the largest MFMA stage)
 
+// s_waitcnt immediate that waits until at most n (< 16) vector memory operations are
+// outstanding, leaving the export and LDS counters unconstrained.
+#define VH_VMCNT(n) (((n) & 15) | (7 << 4) | (15 << 8))
+
+// Global-memory views of device pointers.  Accesses through them compile to global_* rather
+// than flat_* instructions: a flat access counts against both the vector-memory and the LDS
+// wait counters, so one pending flat store makes the compiler wait for every outstanding load
+// before the next LDS or register use.
+typedef __attribute__((address_space(1))) uint32_t gu32;
+typedef __attribute__((address_space(1))) uint64_t gu64;
+// the 8 bytes of a uint2 {x, y} as one little-endian 64-bit word
+__device__ __forceinline__ uint64_t pack_u2(uint32_t x, uint32_t y) { return (uint64_t)y << 32 | x; }
+
 // Maps a float score (smaller is better) to an unsigned key with the same order.
 __host__ __device__ inline uint32_t score_key(float s) {
     uint32_t u = __builtin_bit_cast(uint32_t, s);
