@@ -183,6 +183,23 @@ def test_integer_l2_exact_k100(vh, oracle):
     check_knn(oracle, base, q, ids, dist, 100, "l2", rtol=0.0, atol=0.0)
 
 
+@pytest.mark.parametrize("dim", [32, 96, 128])
+def test_integer_l2_extremes_exact(vh, oracle, dim):
+    """Entries only 0 or 255: the largest norms (128 * 255^2) and cross terms the [0, 255]
+    range allows, where the register kernel's accumulators (row norm minus 2 q.x) reach their
+    widest partial sums.  Distances are exact integers and must match bit for bit; the heavy
+    ties (multiples of 255^2) exercise the tie-aware check."""
+    rng = np.random.default_rng(dim)
+    base = (rng.integers(0, 2, (30_000, dim)) * 255).astype(np.float32)
+    q = (rng.integers(0, 2, (40, dim)) * 255).astype(np.float32)
+    q[0] = 255.0  # all-255 query against all-0 / all-255 rows
+    base[:2] = 0.0
+    base[2:4] = 255.0
+    ids, dist, lens = vh.CudaKnnEngine(base, dim).search_batch_arrays(q, 20)
+    assert np.all(lens == 20)
+    check_knn(oracle, base, q, ids, dist, 20, "l2", rtol=0.0, atol=0.0)
+
+
 def test_large_k_beyond_reference_clamp(vh, oracle):
     """k = 1000 > the reference kernel's MAX_K = 128 (knn.cu:203,218)."""
     from vector_hip import datasets as ds
