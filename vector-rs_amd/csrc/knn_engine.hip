@@ -78,11 +78,29 @@ static std::vector<Round> plan_rounds(size_t n, size_t k, bool gemm, int dpad) {
     while (seen < n) {
         const size_t e = std::min(n, round_up(seen * 8, kRowAlign));
         size_t item = (size_t)slots * seen / (3 * kk);
-        item = std::max<size_t>(kRowAlign, std::min<size_t>(4096, item / kRowAlign * kRowAlign));
+        item = std::max<size_t>(kRowAlign, std::min<size_t>(8192, item / kRowAlign * kRowAlign));
         r.push_back({(long)seen, (long)e, false, (long)item});
         seen = e;
     }
     return r;
+}
+
+// Work-item rows for an MFMA filter round (one workgroup per CU): among multiples of 256 up to
+// the slot-derived `cap_item`, the one with the least estimated time, i.e. the fewest
+// item-rounds over the resident workgroups times the item length (plus a per-item cost of
+// about 64 rows for the tile load and flush).  Larger items win ties.
+static long balanced_item(long cap_item, long rows, int n_ctiles, int wgs) {
+    long best = cap_item;
+    double best_cost = 0.0;
+    for (long it = cap_item; it >= kRowAlign; it -= kRowAlign) {
+        const long items = (rows + it - 1) / it * n_ctiles;
+        const double cost = (double)((items + wgs - 1) / wgs) * (double)(it + 64);
+        if (it == cap_item || cost < best_cost * 0.999) {
+            best_cost = cost;
+            best = it;
+        }
+    }
+    return best;
 }
 
 // Candidate capacity per query and round: the dense round's rows, and room for several times
@@ -119,8 +137,11 @@ static int run_rounds(vhip_knn *E, const float *qpad, const float *qnorm, int nq
         const double bytes = rows * E->dim * 4.0 + (double)nq * E->dim * 4.0;
         if (rd.dense) launch_fill_u32(cnt.as<uint32_t>(), (size_t)nq, (uint32_t)(re - rb), s);
         const int t = E->timer.begin(s);
+        const long item =
+            gemm && !rd.dense ? balanced_item(rd.item_rows, re - rb, ceil_div(nq, kTileCols), E->grid_cap / 2)
+                              : rd.item_rows;
         if (gemm)
-            launch_gemm_filter(E->metric, rd.dense, rd.item_rows, E->base.as<float>(), E->norm.as<float>(), qpad,
+            launch_gemm_filter(E->metric, rd.dense, item, E->base.as<float>(), E->norm.as<float>(), qpad,
                                qnorm, tau.as<float>(), nq, (int)E->dpad, rb, re, cand.as<uint2>(),
                                cnt.as<uint32_t>(), cap, E->norm_max, E->norm_min, E->grid_cap, s);
         else if (E->metric == HAMMING_PACKED)
