@@ -147,6 +147,15 @@ public:
         : CudaKnnEngine(dataset, len, dimension, metric, 0) {}
     CudaKnnEngine(const std::vector<float> &dataset, size_t dimension, DistanceMetric metric)
         : CudaKnnEngine(dataset.data(), dataset.size(), dimension, metric, 0) {}
+    /* CudaKnnEngine::new over MmapStorage::open(path).as_raw_slice(): the base streams from the
+     * mapped file to the GPU with no host copy (vhip_knn_create_from_vecrstor) */
+    static CudaKnnEngine from_vecrstor(const std::string &path, DistanceMetric metric, size_t ordinal = 0) {
+        size_t n = 0, d = 0;
+        detail::check(vhip_vecrstor_open(path.c_str(), &n, &d));
+        vhip_knn *h = nullptr;
+        detail::check(vhip_knn_create_from_vecrstor(path.c_str(), (int)metric, (int)ordinal, &h));
+        return CudaKnnEngine(h, d);
+    }
     /* CudaKnnEngine::with_ordinal (knn.rs:90-140) */
     static CudaKnnEngine with_ordinal(const std::vector<float> &dataset, size_t dimension, DistanceMetric metric,
                                       size_t ordinal) {
@@ -192,6 +201,7 @@ private:
         detail::check(vhip_knn_create(dataset, len / dimension, dimension, (int)metric, (int)ordinal, &h));
         h_.reset(h);
     }
+    CudaKnnEngine(vhip_knn *h, size_t dimension) : dim_(dimension), h_(h) {}
     struct Del {
         void operator()(vhip_knn *p) const { vhip_knn_destroy(p); }
     };
@@ -438,34 +448,55 @@ private:
 };
 
 /* ---- files of the offline trainer (storage/mmap.rs, ivf/serializer.rs) ------------------- */
-/* MmapStorage (storage/mmap.rs:56-260); open() reads the data once instead of mapping it */
+/* A read-only view of n floats (the &[f32] that MmapStorage::as_raw_slice returns). */
+struct FloatSlice {
+    const float *ptr = nullptr;
+    size_t n = 0;
+    const float *data() const { return ptr; }
+    size_t size() const { return n; }
+    bool empty() const { return n == 0; }
+    const float *begin() const { return ptr; }
+    const float *end() const { return ptr + n; }
+    float operator[](size_t i) const { return ptr[i]; }
+};
+
+/* MmapStorage (storage/mmap.rs:56-260): open() maps the file read-only (vhip_vecrstor_map);
+ * get() and as_raw_slice() read the mapping in place, and engines built from the slice upload
+ * straight from the page cache.  Copies share the mapping, which is unmapped with the last. */
 class MmapStorage {
 public:
+    static void create(const std::string &path, size_t dimension, const std::vector<std::vector<float>> &vectors) {
+        std::vector<float> flat;
+        for (const auto &v : vectors) {
+            detail::require(v.size() == dimension, "dimension mismatch");
+            flat.insert(flat.end(), v.begin(), v.end());
+        }
+        create_from_flat(path, dimension, flat);
+    }
     static void create_from_flat(const std::string &path, size_t dimension, const std::vector<float> &flat) {
         detail::require(dimension > 0 && flat.size() % dimension == 0, "dimension mismatch");
         detail::check(vhip_vecrstor_write(path.c_str(), flat.data(), flat.size() / dimension, dimension));
     }
     static MmapStorage open(const std::string &path) {
-        size_t n = 0, d = 0;
-        detail::check(vhip_vecrstor_open(path.c_str(), &n, &d));
         MmapStorage s;
-        s.dim_ = d;
-        s.data_.resize(n * d);
-        detail::check(vhip_vecrstor_read(path.c_str(), s.data_.data(), n, d));
+        vhip_vecrstor_view *v = nullptr;
+        detail::check(vhip_vecrstor_map(path.c_str(), &s.data_, &s.n_, &s.dim_, &v));
+        s.view_.reset(v, vhip_vecrstor_unmap);
         return s;
     }
     size_t dimension() const { return dim_; }
-    size_t len() const { return dim_ ? data_.size() / dim_ : 0; }
-    bool is_empty() const { return len() == 0; }
+    size_t len() const { return n_; }
+    bool is_empty() const { return n_ == 0; }
     const float *get(size_t id) const {
-        detail::require(id < len(), "vector id out of bounds");
-        return data_.data() + id * dim_;
+        detail::require(id < n_, "vector id out of bounds");
+        return data_ + id * dim_;
     }
-    const std::vector<float> &as_raw_slice() const { return data_; }
+    FloatSlice as_raw_slice() const { return FloatSlice{data_, n_ * dim_}; }
 
 private:
-    size_t dim_ = 0;
-    std::vector<float> data_;
+    std::shared_ptr<vhip_vecrstor_view> view_;
+    const float *data_ = nullptr;
+    size_t n_ = 0, dim_ = 0;
 };
 
 /* CentroidFileData (ivf/serializer.rs:380-393) */

@@ -128,6 +128,16 @@ static void host_tests() {
         MmapStorage::create_from_flat(p, 3, {1, 2, 3, 4, 5, 6});
         auto st = MmapStorage::open(p);
         CHECK(st.len() == 2 && st.dimension() == 3 && st.get(1)[0] == 4.0f && st.get(1)[2] == 6.0f);
+        // as_raw_slice is the mapping itself, 24 bytes past a page boundary
+        auto sl = st.as_raw_slice();
+        CHECK(sl.size() == 6 && sl[5] == 6.0f && (reinterpret_cast<uintptr_t>(sl.data()) & 4095u) == 24u);
+        auto copy = st;  // copies share the mapping
+        CHECK(copy.as_raw_slice().data() == sl.data());
+        MmapStorage::create(p, 2, {{1, 2}, {3, 4}, {5, 6}});
+        auto st2 = MmapStorage::open(p);
+        CHECK(st2.len() == 3 && st2.get(2)[1] == 6.0f);
+        CHECK(expect_error([&] { MmapStorage::create(p, 3, {{1, 2}}); }).kind() == CudaError::Kind::InvalidConfig);
+        CHECK(expect_error([&] { MmapStorage::open("/tmp/vhip_facade_missing.bin"); }).kind() == CudaError::Kind::InvalidConfig);
         std::remove(p.c_str());
     });
     run("ddp_knn_insufficient_hardware_error (distributed_knn.rs:470)", [] {
@@ -225,6 +235,25 @@ static void gpu_tests() {
             auto r = e.search(std::vector<float>(data.begin() + 2 * i, data.begin() + 2 * i + 2), 1);
             CHECK(r.size() == 1 && r[0].id == i && std::fabs(r[0].distance) < 1e-4);
         }
+    });
+    run("engine built from a mapped VECRSTOR file (storage/mmap.rs + knn.rs:85)", [] {
+        const std::string p = "/tmp/vhip_facade_base.bin";
+        auto data = knn_rs_data(300);
+        MmapStorage::create_from_flat(p, 4, data);
+        auto st = MmapStorage::open(p);
+        CudaKnnEngine a(data, 4, DistanceMetric::L2Squared);
+        CudaKnnEngine b(st.as_raw_slice().data(), st.as_raw_slice().size(), 4, DistanceMetric::L2Squared);
+        auto c = CudaKnnEngine::from_vecrstor(p, DistanceMetric::L2Squared);
+        CHECK(c.num_vectors() == 300 && c.dimension() == 4);
+        std::vector<float> q(data.begin() + 40, data.begin() + 56);
+        auto ra = a.search_batch(q, 7), rb = b.search_batch(q, 7), rc = c.search_batch(q, 7);
+        CHECK(ra.size() == 4 && rb.size() == 4 && rc.size() == 4);
+        for (size_t i = 0; i < ra.size(); ++i)
+            for (size_t j = 0; j < ra[i].size(); ++j) {
+                CHECK(ra[i][j].id == rb[i][j].id && ra[i][j].distance == rb[i][j].distance);
+                CHECK(ra[i][j].id == rc[i][j].id && ra[i][j].distance == rc[i][j].distance);
+            }
+        std::remove(p.c_str());
     });
     // ---- ddp/distributed_knn.rs:270-467 ----
     run("ddp_knn_sharded_mode_exact_match (distributed_knn.rs:271)", [] {
