@@ -179,6 +179,31 @@ def test_fit_deterministic_and_explicit_init(vh, oracle):
     assert np.array_equal(e.centroids, f.centroids)
 
 
+@pytest.mark.parametrize("init_mode", [0, 1])
+def test_seeded_inits_draw_distinct_data_rows(vh, init_mode):
+    """Both seeded inits pick data points as centroids, as the reference's do: k-means++
+    (kmeans.rs:409-460) samples rows by D^2 weight, init_random (distributed_kmeans.rs:524-535)
+    takes the first k of a shuffle.  With no iteration the state holds the drawn rows: each must
+    be an exact row of the data (a wrong gather index or row stride fails this), all distinct,
+    reproducible by seed and different across seeds.  The dimension (40, padded to 64 on the
+    device) exercises the padded gather."""
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal((5_000, 40)).astype(np.float32)
+    st = vh.KMeansState(x)
+    rows = {r.tobytes(): i for i, r in enumerate(x)}
+    c, _, (d, k, iters, _) = st.fit(100, 0, -1.0, init_mode=init_mode, seed=5)
+    assert (d, k, iters) == (40, 100, 0)
+    picked = [rows.get(v.tobytes()) for v in c]
+    assert None not in picked and len(set(picked)) == 100
+    c2, _, _ = st.fit(100, 0, -1.0, init_mode=init_mode, seed=5)
+    c3, _, _ = st.fit(100, 0, -1.0, init_mode=init_mode, seed=6)
+    assert np.array_equal(c, c2) and not np.array_equal(c, c3)
+    # k = n draws every row exactly once
+    small = vh.KMeansState(x[:64])
+    cs, _, _ = small.fit(64, 0, -1.0, init_mode=init_mode, seed=1)
+    assert sorted(rows[v.tobytes()] for v in cs) == list(range(64))
+
+
 def test_empty_cluster_keeps_centroid(vh):
     rng = np.random.default_rng(0)
     data = rng.standard_normal((5000, 16)).astype(np.float32)
