@@ -34,6 +34,7 @@ METRIC = "kNN queries/sec (1M×128 fp32, k=100) + k-means iter/sec; % FP32-MFMA/
 PEAK_MFMA_F32 = 157.3e12   # FLOP/s, MI355X dense FP32 matrix
 PEAK_HBM = 8.0e12          # B/s
 PEAK_VALU32 = 39.3e12      # non-packed 32-bit VALU op/s (256 CU x 64 lanes x 2.4 GHz)
+PEAK_MFMA_I8 = 5.0e15      # OP/s, MI355X dense int8 matrix
 
 
 def log(*a):
@@ -63,7 +64,7 @@ PROFILES = {
     "l2int": "k_mfma_hs_filter__knn_l2_int_1000000x128_q10000_k100.txt",
     "kmeans": "k_mfma_hs_assign__kmeans_l2_2000000x96_k4096.txt",
     "cos768": "k_mfma_pnl_filter__knn_cosine_1000000x768_q10000_k10.txt",
-    "hamming": "k_hamming_filter__knn_hamming_packed256_10000000_q10000_k10.txt",
+    "hamming": "k_mfma_ham__knn_hamming_packed256_10000000_q10000_k10.txt",
     "l1": "k_valu_filter__knn_l1_uniform_500000x128_q4096_k10.txt",
     "linf": "k_valu_filter__knn_linf_uniform_500000x128_q4096_k10.txt",
     "ivf_coarse": "k_mfma_hs_assign__ivf_coarse_l2_2000000x96_nlist4096.txt",
@@ -483,6 +484,13 @@ def bench_knn_workload(vh, key, steps, warmup, with_cpu):
     gemm = w["metric"] in ("l2", "dot", "cosine")
     if gemm:
         rl = roofline(prof, "mfma", PEAK_MFMA_F32, "TFLOP/s", key)
+    elif ham and w["d"] <= 16:
+        # codes of up to 512 bits run on the int8 matrix cores: 2 K int8 operations per
+        # (query, row), K = 32 * padded words
+        p2 = dict(prof)
+        rl = roofline(p2, "mfma", PEAK_MFMA_I8, "TFLOP/s", key)
+        if rl:
+            rl["unit"] = "TOP/s (int8 MFMA)"
     else:
         # VALU-bound: work counts element (or word) operations, each costing two VALU ops
         p2 = dict(prof)
@@ -492,7 +500,8 @@ def bench_knn_workload(vh, key, steps, warmup, with_cpu):
             rl["unit"] = "Top/s (32-bit VALU)"
     out = {"metric": METRIC, "value": round(w["nq"] * 1e3 / ms, 2), "unit": "queries/s", "n_gpus": 1,
            "steps": steps, "warmup": warmup, "ms_per_step": round(ms, 3), "higher_is_better": True,
-           "scaling": "strong", "vs_baseline": None, "dtype": "u32" if ham else "f32", "data": "synthetic",
+           "scaling": "strong", "vs_baseline": None,
+           "dtype": ("i8" if w["d"] <= 16 else "u32") if ham else "f32", "data": "synthetic",
            "config": {"workload": w["name"], "base_rows": w["n"], "dim": w["d"] * (32 if ham else 1),
                       "queries": w["nq"], "k": w["k"], "metric": w["metric"], "parallelism": "single GPU"},
            "roofline": rl,

@@ -14,8 +14,11 @@ def vh():
     return vector_hip
 
 
+# Codes of up to 512 bits run on the int8 matrix cores (32..512 bits: every expanded width),
+# wider ones on the popcount kernel (1024 bits).
 @pytest.mark.parametrize("n,bits,nq,k", [(100_000, 256, 50, 10), (5000, 64, 17, 33), (777, 96, 3, 777),
-                                         (300_000, 256, 8, 100)])
+                                         (300_000, 256, 8, 100), (20_000, 32, 40, 10), (3000, 160, 11, 64),
+                                         (50_000, 512, 20, 50), (10_000, 1024, 9, 20), (300, 256, 130, 7)])
 def test_hamming_bit_exact(vh, oracle, n, bits, nq, k):
     from vector_hip import datasets as ds
 
@@ -40,3 +43,19 @@ def test_hamming_equals_reference_float_hamming(vh, oracle):
     for r in range(4):
         ref = oracle.distance_rows("hamming", np.repeat(un_q[r:r + 1], 10, 0), un_c[ids[r]])
         assert np.array_equal(ref, dist[r].astype(np.float32))
+
+
+@pytest.mark.parametrize("bits", [256, 1024])
+def test_hamming_massive_ties(vh, oracle, bits):
+    """Every base code identical: every row ties, the per-query candidate slots overflow into
+    the global lists and the overflow re-run, and the k lowest ids must come back."""
+    from vector_hip import datasets as ds
+
+    one = ds.packed_bits(1, bits, 3)
+    codes = np.repeat(one, 40_000, axis=0)
+    q = ds.packed_bits(5, bits, 4)
+    ids, dist, lens = vh.HammingKnnEngine(codes).search_batch_arrays(q, 12)
+    rids, rdist, _ = oracle.hamming_packed_knn(codes, q, 12)
+    assert np.all(lens == 12)
+    assert np.array_equal(dist, rdist) and np.array_equal(ids, rids)
+    assert np.array_equal(ids, np.tile(np.arange(12, dtype=ids.dtype), (5, 1)))

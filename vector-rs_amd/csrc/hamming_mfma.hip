@@ -1,0 +1,319 @@
+// hamming_mfma.hip -- packed-bit Hamming kNN on the int8 matrix cores.
+//
+// The popcount kernel (hamming.hip) runs at the VALU issue limit: two VALU operations (XOR,
+// bit count) per 32-bit word per query.  Here each bit of a code is expanded once to one int8,
+// x = 1 - 2 b (+1 for 0, -1 for 1).  For K-bit codes a and b the expanded vectors give
+// x . y = K - 2 popcount(a ^ b), so the Hamming distance is (K - x . y) / 2, exact in int32,
+// and the scan becomes an int8 GEMM on v_mfma_i32_32x32x32_i8 fused with the same threshold
+// filter as the FP32 kernels.  The reference's thresholded float Hamming (scalar.rs:143-153)
+// equals this distance on 0/1 codes.
+//
+// Tiling: a workgroup of 8 waves owns a work item of 128 query columns (their K-byte rows
+// resident in LDS, 16-byte slots XOR-swizzled by column so a 16-lane pass of ds_read_b128 is
+// conflict-free) x item_rows base rows, in stages of 512 rows; every wave streams its own 64
+// rows from L2 straight into registers, three K-chunks ahead (the base is stored in the A
+// operand's lane order, so each load is 1 KB contiguous), and computes a 64 x 128 block as 2 x 4
+// 32 x 32 tiles, so each base byte feeds 128 queries from registers.  The grid is persistent
+// and XCD-aware like the FP32 kernels.  FILTER keeps (distance, row) pairs with distance <= tau
+// in per-query LDS slots flushed once per item; DENSE (the first round) writes every pair.
+#include <algorithm>
+
+#include "vh_common.h"
+
+namespace vh {
+
+typedef int intx4 __attribute__((ext_vector_type(4)));
+typedef int intx16 __attribute__((ext_vector_type(16)));
+
+namespace {
+
+constexpr int kHmCols = 128;             // query columns per work item
+constexpr int kHmStage = 512;            // base rows per stage: 8 waves x 64
+constexpr int kHmSlots = kGemmSlotsReg;  // LDS candidate slots per query per work item
+constexpr int kHmFilter = 0, kHmDense = 1;
+
+struct HamArgs {
+    const int8_t *A;  // expanded base codes, K bytes per row, rows readable up to row_end + kHmStage
+    const int8_t *B;  // expanded query codes, K bytes per row, rows padded to a multiple of 128
+    const float *tau;
+    int nq, n_ctiles, n_items;
+    long row_begin, row_end, item_rows;
+    uint2 *cand;
+    uint32_t *cnt;
+    int cap;
+};
+
+// Expands rows of `words` packed uint32 (row stride wstride) to K = 32 * words int8 values
+// (bit i of word w -> byte 32 w + i: +1 for a clear bit, -1 for a set one).  Rows at or past
+// `rows` become all +1.  One thread writes the 4 bytes of one nibble.
+//  * tiled = false: row-major, K bytes per row (the query tiles, staged through LDS).
+//  * tiled = true: the layout of the MFMA A operand, so that one 16-byte load per lane of a wave
+//    reads 1 KB contiguous (8 whole cache lines, not 32 partial ones): byte b of row r sits at
+//    ((r / 32) * KC + b / 32) * 1024 + ((b / 16) & 1) * 512 + (r % 32) * 16 + b % 16.
+__global__ __launch_bounds__(256) void k_ham_expand(const uint32_t *__restrict__ src, size_t rows, int words,
+                                                    int wstride, size_t rows_out, bool tiled,
+                                                    uint32_t *__restrict__ dst) {
+    const size_t per_row = (size_t)words * 8, total = rows_out * per_row;
+    for (size_t t = blockIdx.x * (size_t)blockDim.x + threadIdx.x; t < total; t += (size_t)gridDim.x * blockDim.x) {
+        const size_t r = t / per_row;
+        const int rem = (int)(t - r * per_row), w = rem >> 3, nib = rem & 7;
+        const uint32_t word = r < rows ? src[r * (size_t)wstride + w] : 0u;
+        const uint32_t b = (word >> (4 * nib)) & 15u;
+        uint32_t out = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) out |= ((b >> i) & 1u ? 0xffu : 0x01u) << (8 * i);
+        size_t o = t;  // in 4-byte units
+        if (tiled) {
+            const int byte = 4 * rem;  // first of the 4 bytes within the row
+            const size_t blk = (r >> 5) * (size_t)words + (size_t)(byte >> 5);
+            o = (blk * 1024 + (size_t)((byte >> 4) & 1) * 512 + (r & 31) * 16 + (byte & 15)) >> 2;
+        }
+        dst[o] = out;
+    }
+}
+
+__device__ __forceinline__ int ham_first_item() { return (blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3); }
+
+template <int MODE, int KC>
+__global__ __launch_bounds__(512, 1) void k_mfma_ham(HamArgs a) {
+    constexpr int K = 32 * KC, NS = K / 16;  // bytes per row, 16-byte slots per row
+    constexpr int SW = NS < 16 ? NS - 1 : 15;
+    __shared__ intx4 sB[kHmCols * NS];
+    __shared__ uint32_t s_qcnt[MODE == kHmFilter ? kHmCols : 1];
+    __shared__ uint2 s_slot[MODE == kHmFilter ? kHmCols * kHmSlots : 1];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int l32 = lane & 31, h = lane >> 5;
+    int item = ham_first_item();
+    if (item >= a.n_items) return;
+
+    auto bslot = [](int c, int s) { return c * NS + (s ^ (c & SW)); };
+    auto decode = [&](int it, int &c0, long &lo, long &hi) {
+        const int ct = it % a.n_ctiles;
+        const long chunk = it / a.n_ctiles;
+        c0 = ct * kHmCols;
+        lo = a.row_begin + chunk * a.item_rows;
+        hi = min(lo + a.item_rows, a.row_end);
+    };
+    auto fill_b = [&](int c0) {
+        for (int f = tid; f < kHmCols * NS; f += 512) {
+            const int c = f / NS, sidx = f - c * NS;
+            sB[bslot(c, sidx)] = *(const intx4 *)(a.B + (size_t)(c0 + c) * K + 16 * sidx);
+        }
+    };
+    // the two 16-byte operands of K-chunk kc for this wave's rows rs + 64 wave + 32 rb + l32
+    // (tiled layout: 32-row blocks of KC chunks of 1 KB, lane-contiguous)
+    auto load_a = [&](intx4 (&r)[2], long rs, int kc) {
+        const int8_t *p = a.A + ((size_t)((rs + 64 * wave) >> 5) * KC + kc) * 1024 + 16 * lane;
+        r[0] = *(const intx4 *)p;
+        r[1] = *(const intx4 *)(p + (size_t)KC * 1024);
+    };
+
+    int col0;
+    long r_lo, r_hi;
+    decode(item, col0, r_lo, r_hi);
+    fill_b(col0);
+    if constexpr (MODE == kHmFilter) {
+        if (tid < kHmCols) s_qcnt[tid] = 0;
+    }
+    // per column: distance <= tq  <=>  dot >= T = K - 2 tq (distances are integers)
+    int T[4];
+    auto item_begin = [&]() {
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb) {
+            const int q = col0 + 32 * cb + l32;
+            const float t = q < a.nq ? a.tau[q] : -1.0f;
+            T[cb] = t < 0.0f ? K + 1 : (t >= (float)K ? -K : K - 2 * (int)t);
+        }
+    };
+    item_begin();
+    long rs = r_lo;
+    // A operands in a ring of RING K-chunks, loaded RING - 1 chunks ahead (across stages): a
+    // chunk is only 8 MFMAs, too short to cover an L2 round trip on its own.  RING divides KC,
+    // so every ring index is a compile-time constant.
+    constexpr int RING = KC >= 16 ? 4 : (KC < 8 ? KC : 8), PD = RING - 1;  // 4 at KC 16: registers
+    intx4 ring[RING][2];
+#pragma unroll
+    for (int c = 0; c < PD; ++c) load_a(ring[c], rs, c);
+    __syncthreads();
+
+    for (;;) {
+        long nrs = rs + kHmStage;
+        int nitem = item, ncol0 = col0;
+        long nlo = r_lo, nhi = r_hi;
+        const bool item_end = nrs >= r_hi;
+        bool more = true;
+        if (item_end) {
+            nitem = item + (int)gridDim.x;
+            more = nitem < a.n_items;
+            if (more) {
+                decode(nitem, ncol0, nlo, nhi);
+                nrs = nlo;
+            }
+        }
+        intx16 acc[2][4];
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+            for (int cb = 0; cb < 4; ++cb) acc[rb][cb] = intx16{0};
+#pragma unroll
+        for (int kc = 0; kc < KC; ++kc) {
+            if constexpr (PD > 0) {
+                if (kc + PD < KC) load_a(ring[(kc + PD) % RING], rs, kc + PD);
+                else if (more) load_a(ring[(kc + PD) % RING], nrs, kc + PD - KC);
+            }
+            intx4 b[4];
+#pragma unroll
+            for (int cb = 0; cb < 4; ++cb) b[cb] = sB[bslot(32 * cb + l32, 2 * kc + h)];
+            if constexpr (PD == 0) load_a(ring[0], rs, kc);  // KC == 1
+#pragma unroll
+            for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+                for (int cb = 0; cb < 4; ++cb)
+                    acc[rb][cb] =
+                        __builtin_amdgcn_mfma_i32_32x32x32_i8(ring[kc % RING][rb], b[cb], acc[rb][cb], 0, 0, 0);
+        }
+        // ---- epilogue: register 4g+j of tile (rb, cb) holds row rs + 64 wave + 32 rb + 8 g + 4 h + j
+        // and column 32 cb + l32 ----
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const long row0 = rs + 64 * wave + 32 * rb + 8 * g + 4 * h;
+                if constexpr (MODE == kHmDense) {
+#pragma unroll
+                    for (int cb = 0; cb < 4; ++cb) {
+                        const int q = col0 + 32 * cb + l32;
+                        if (q >= a.nq) continue;
+                        uint2 *dst = a.cand + (size_t)q * a.cap;
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            const long row = row0 + j;
+                            if (row < r_hi) {
+                                const int dist = (K - acc[rb][cb][4 * g + j]) >> 1;
+                                dst[row - a.row_begin] = make_uint2(score_key((float)dist), (uint32_t)row);
+                            }
+                        }
+                    }
+                } else {
+                    uint64_t m = 0;
+#pragma unroll
+                    for (int cb = 0; cb < 4; ++cb) {
+                        const intx16 &v = acc[rb][cb];
+                        const int mx = max(max(v[4 * g], v[4 * g + 1]), max(v[4 * g + 2], v[4 * g + 3]));
+                        m |= __builtin_amdgcn_ballot_w64(mx >= T[cb]);
+                    }
+                    if (m == 0) continue;
+#pragma unroll
+                    for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            const int dot = acc[rb][cb][4 * g + j];
+                            const long row = row0 + j;
+                            if (dot < T[cb] || row >= r_hi) continue;
+                            const int ql = 32 * cb + l32;
+                            const uint32_t key = score_key((float)((K - dot) >> 1));
+                            const uint32_t rii = (uint32_t)(row - r_lo);
+                            const uint32_t r = atomicAdd(&s_qcnt[ql], 1u);
+                            if (r < (uint32_t)kHmSlots) {
+                                s_slot[ql * kHmSlots + r] = make_uint2(key, rii);
+                            } else {
+                                // rare overflow: straight to the global list, drained here so no
+                                // store is pending where this path rejoins the loop
+                                const int q = col0 + ql;
+                                const uint32_t at = __hip_atomic_fetch_add((gu32 *)a.cnt + q, 1u, __ATOMIC_RELAXED,
+                                                                           __HIP_MEMORY_SCOPE_AGENT);
+                                if (at < (uint32_t)a.cap)
+                                    ((gu64 *)a.cand)[(size_t)q * a.cap + at] = pack_u2(key, (uint32_t)row);
+                                __builtin_amdgcn_s_waitcnt(VH_VMCNT(0));
+                            }
+                        }
+                }
+            }
+        }
+        if (item_end) {
+            __syncthreads();  // every wave is past this item's tile and slot appends
+            if constexpr (MODE == kHmFilter) {
+                if (tid < kHmCols) {
+                    uint32_t c = s_qcnt[tid];
+                    if (c) {
+                        s_qcnt[tid] = 0;
+                        c = min(c, (uint32_t)kHmSlots);
+                        const int q = col0 + tid;
+                        const uint32_t base = atomicAdd(&a.cnt[q], c);
+                        for (uint32_t j = 0; j < c; ++j)
+                            if (base + j < (uint32_t)a.cap) {
+                                const uint2 e = s_slot[tid * kHmSlots + j];
+                                a.cand[(size_t)q * a.cap + base + j] = make_uint2(e.x, (uint32_t)(r_lo + e.y));
+                            }
+                    }
+                }
+            }
+            if (!more) break;
+            fill_b(ncol0);
+            __syncthreads();
+            item = nitem;
+            col0 = ncol0;
+            r_lo = nlo;
+            r_hi = nhi;
+            item_begin();
+        }
+        rs = nrs;
+    }
+}
+
+}  // namespace
+
+size_t ham_mfma_rows(size_t n) { return round_up(n, kHmStage) + kHmStage; }
+
+bool ham_mfma_supported(int wpad) { return wpad >= 1 && wpad <= 16; }
+
+void launch_ham_expand(const uint32_t *src, size_t rows, int words, int wstride, size_t rows_out, bool tiled,
+                       int8_t *dst, hipStream_t s) {
+    const size_t total = rows_out * (size_t)words * 8;
+    if (total == 0) return;
+    const unsigned blocks = (unsigned)std::min<size_t>(65536, (total + 255) / 256);
+    hipLaunchKernelGGL(k_ham_expand, dim3(blocks), dim3(256), 0, s, src, rows, words, wstride, rows_out, tiled,
+                       (uint32_t *)dst);
+}
+
+void launch_ham_mfma(bool dense, long item_rows, const int8_t *base8, const int8_t *qry8, int wpad,
+                     const float *tau, int nq, long row_begin, long row_end, uint2 *cand, uint32_t *cnt, int cap,
+                     int grid_cap, hipStream_t s) {
+    if (nq <= 0 || row_end <= row_begin) return;
+    HamArgs a{};
+    a.A = base8;
+    a.B = qry8;
+    a.tau = tau;
+    a.nq = nq;
+    a.n_ctiles = ceil_div(nq, kHmCols);
+    a.item_rows = item_rows;
+    a.row_begin = row_begin;
+    a.row_end = row_end;
+    const long n_chunks = (row_end - row_begin + item_rows - 1) / item_rows;
+    a.n_items = (int)((long)a.n_ctiles * n_chunks);
+    a.cand = cand;
+    a.cnt = cnt;
+    a.cap = cap;
+    const int cus = grid_cap / 2;
+    long g = a.n_items < cus ? a.n_items : cus;
+    const dim3 grid((unsigned)((g + 7) / 8 * 8)), block(512);
+#define VH_HM(MODE, KC) hipLaunchKernelGGL((k_mfma_ham<MODE, KC>), grid, block, 0, s, a)
+#define VH_HM_K(MODE)                 \
+    switch (wpad) {                    \
+        case 1: VH_HM(MODE, 1); break; \
+        case 2: VH_HM(MODE, 2); break; \
+        case 4: VH_HM(MODE, 4); break; \
+        case 8: VH_HM(MODE, 8); break; \
+        default: VH_HM(MODE, 16); break; \
+    }
+    if (dense) {
+        VH_HM_K(kHmDense)
+    } else {
+        VH_HM_K(kHmFilter)
+    }
+#undef VH_HM_K
+#undef VH_HM
+}
+
+}  // namespace vh

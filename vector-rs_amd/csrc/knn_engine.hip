@@ -26,7 +26,7 @@ constexpr size_t kQueryBatch = 16384;
 bool is_gemm_metric(int m) { return m == L2 || m == DOT || m == COS; }
 
 struct Workspace {
-    DevBuf qraw, qpad, qnorm, tau, have, cnt, flags, nflag, topk, cand, oids, odist;
+    DevBuf qraw, qpad, qnorm, tau, have, cnt, flags, nflag, topk, cand, oids, odist, q8;
 };
 
 }  // namespace vh
@@ -39,6 +39,8 @@ struct vhip_knn {
     int grid_cap = 512;
     hipStream_t stream = nullptr;
     vh::DevBuf base, norm, perm, inv_perm;
+    vh::DevBuf base8;  // packed Hamming on the int8 matrix cores: one +1/-1 byte per code bit
+    bool ham8 = false;
     std::mutex mu;
     vh::Workspace ws;
     vh::PinnedStager stager;
@@ -85,14 +87,15 @@ static std::vector<Round> plan_rounds(size_t n, size_t k, bool gemm, int dpad) {
     return r;
 }
 
-// Work-item rows for an MFMA filter round (one workgroup per CU): among multiples of 256 up to
+// Work-item rows for an MFMA filter round (one workgroup per CU): among multiples of `step` up to
 // the slot-derived `cap_item`, the one with the least estimated time, i.e. the fewest
 // item-rounds over the resident workgroups times the item length (plus a per-item cost of
 // about 64 rows for the tile load and flush).  Larger items win ties.
-static long balanced_item(long cap_item, long rows, int n_ctiles, int wgs) {
+static long balanced_item(long cap_item, long rows, int n_ctiles, int wgs, long step = kRowAlign) {
+    cap_item = std::max(step, cap_item / step * step);
     long best = cap_item;
     double best_cost = 0.0;
-    for (long it = cap_item; it >= kRowAlign; it -= kRowAlign) {
+    for (long it = cap_item; it >= step; it -= step) {
         const long items = (rows + it - 1) / it * n_ctiles;
         const double cost = (double)((items + wgs - 1) / wgs) * (double)(it + 64);
         if (it == cap_item || cost < best_cost * 0.999) {
@@ -127,20 +130,40 @@ static int run_rounds(vhip_knn *E, const float *qpad, const float *qnorm, int nq
     launch_topk_init(nq, tau.as<float>(), have.as<uint32_t>(), cnt.as<uint32_t>(), flags.as<uint32_t>(), s);
     launch_fill_u32(nflag.as<uint32_t>(), 1, 0u, s);
     const bool gemm = is_gemm_metric(E->metric);
+    const int8_t *q8 = nullptr;
+    if (E->ham8) {
+        // the queries' +1/-1 bytes, rows padded to the 128-query tiles
+        const size_t rows = round_up((size_t)nq, kTileCols);
+        VH_CHECK(E->ws.q8.ensure(E->dev, rows * 32 * E->dpad));
+        launch_ham_expand((const uint32_t *)qpad, (size_t)nq, (int)E->dpad, (int)E->dpad, rows, false,
+                          E->ws.q8.as<int8_t>(), s);
+        q8 = E->ws.q8.as<int8_t>();
+    }
     for (const Round &rd : plan_rounds(E->n, (size_t)k, gemm, (int)E->dpad)) {
         const long rb = rd.rb, re = rd.re;
+        const bool dense = rd.dense || (E->ham8 && rb == 0);
         // Algorithmic work per launch: 2*Q*rows*D flops (GEMM metrics), Q*rows*D element
         // operations (VALU metrics) or Q*rows*words word operations (packed Hamming); bytes
         // are the base rows and queries each launch must read once.
         const double rows = (double)(re - rb);
-        const double work = gemm ? 2.0 * nq * rows * (double)E->dim : (double)nq * rows * (double)E->dim;
-        const double bytes = rows * E->dim * 4.0 + (double)nq * E->dim * 4.0;
-        if (rd.dense) launch_fill_u32(cnt.as<uint32_t>(), (size_t)nq, (uint32_t)(re - rb), s);
+        const double work = gemm ? 2.0 * nq * rows * (double)E->dim
+                                 : (E->ham8 ? 2.0 * nq * rows * 32.0 * (double)E->dpad
+                                            : (double)nq * rows * (double)E->dim);
+        const double bytes = E->ham8 ? (rows + nq) * 32.0 * (double)E->dpad  // the expanded int8 codes
+                                     : rows * E->dim * 4.0 + (double)nq * E->dim * 4.0;
+        if (dense) launch_fill_u32(cnt.as<uint32_t>(), (size_t)nq, (uint32_t)(re - rb), s);
         const int t = E->timer.begin(s);
         const long item =
             gemm && !rd.dense ? balanced_item(rd.item_rows, re - rb, ceil_div(nq, kTileCols), E->grid_cap / 2)
                               : rd.item_rows;
-        if (gemm)
+        if (E->ham8) {
+            // int8 matrix-core Hamming: 2 K operations per (query, row), K = 32 * dpad bits
+            const long hitem =
+                dense ? re - rb
+                      : balanced_item(rd.item_rows, re - rb, ceil_div(nq, kTileCols), E->grid_cap / 2, 512);
+            launch_ham_mfma(dense, hitem, E->base8.as<int8_t>(), q8, (int)E->dpad, tau.as<float>(), nq, rb, re,
+                            cand.as<uint2>(), cnt.as<uint32_t>(), cap, E->grid_cap, s);
+        } else if (gemm)
             launch_gemm_filter(E->metric, rd.dense, item, E->base.as<float>(), E->norm.as<float>(), qpad,
                                qnorm, tau.as<float>(), nq, (int)E->dpad, rb, re, cand.as<uint2>(),
                                cnt.as<uint32_t>(), cap, E->norm_max, E->norm_min, E->grid_cap, s);
@@ -272,6 +295,14 @@ static int engine_create(const void *base, size_t n, size_t dim, int metric, int
                          E->base.as<float>(), E->norm.as<float>(), norm_kind_of(metric), transform_of(metric),
                          normalize_of(metric), __builtin_nanf(""), E->stream);
         VH_HIP(hipGetLastError());
+        if (metric == HAMMING_PACKED && ham_mfma_supported((int)E->dpad)) {
+            const size_t rows8 = ham_mfma_rows(n);
+            VH_CHECK(E->base8.ensure(ordinal, rows8 * 32 * E->dpad));
+            launch_ham_expand(E->base.as<uint32_t>(), n, (int)E->dpad, (int)E->dpad, rows8, true,
+                              E->base8.as<int8_t>(), E->stream);
+            VH_HIP(hipGetLastError());
+            E->ham8 = true;
+        }
         if (norm_kind_of(metric)) {
             // extremes of the row norms: the L2 filter's rounding slack and the cosine zero-norm guard
             std::vector<float> nh(n);

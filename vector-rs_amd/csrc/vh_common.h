@@ -105,6 +105,14 @@ void launch_topk_refine(int nq, int k, int kout, int metric, const float *qpad, 
                         int ostride, hipStream_t s);
 // hamming.hip
 int hamming_word_pad(int words);
+// int8 matrix-core path of packed Hamming (hamming_mfma.hip): expanded code rows of 32 * wpad bytes
+size_t ham_mfma_rows(size_t n);
+bool ham_mfma_supported(int wpad);
+void launch_ham_expand(const uint32_t *src, size_t rows, int words, int wstride, size_t rows_out, bool tiled,
+                       int8_t *dst, hipStream_t s);
+void launch_ham_mfma(bool dense, long item_rows, const int8_t *base8, const int8_t *qry8, int wpad,
+                     const float *tau, int nq, long row_begin, long row_end, uint2 *cand, uint32_t *cnt, int cap,
+                     int grid_cap, hipStream_t s);
 void launch_hamming_filter(const uint32_t *codes, const uint32_t *qry, const float *tau, int nq, int wpad,
                            long row_begin, long row_end, uint2 *cand, uint32_t *cnt, int cap, int grid_cap,
                            hipStream_t s);
