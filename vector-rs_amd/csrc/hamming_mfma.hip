@@ -177,6 +177,20 @@ __global__ __launch_bounds__(512, 1) void k_mfma_ham(HamArgs a) {
         // and column 32 cb + l32 ----
 #pragma unroll
         for (int rb = 0; rb < 2; ++rb) {
+            if constexpr (MODE == kHmFilter) {
+                // first each column's best over all 16 rows of the tile half: one compare per
+                // column; only a half with some candidate lane takes the per-group tests
+                uint64_t m = 0;
+#pragma unroll
+                for (int cb = 0; cb < 4; ++cb) {
+                    const intx16 &v = acc[rb][cb];
+                    int mx = v[0];
+#pragma unroll
+                    for (int i = 1; i < 16; ++i) mx = max(mx, v[i]);
+                    m |= __builtin_amdgcn_ballot_w64(mx >= T[cb]);
+                }
+                if (m == 0) continue;
+            }
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 const long row0 = rs + 64 * wave + 32 * rb + 8 * g + 4 * h;
