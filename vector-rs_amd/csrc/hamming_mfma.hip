@@ -131,7 +131,7 @@ __global__ __launch_bounds__(512, 1) void k_mfma_ham(HamArgs a) {
     // A operands in a ring of RING K-chunks, loaded RING - 1 chunks ahead (across stages): a
     // chunk is only 8 MFMAs, too short to cover an L2 round trip on its own.  RING divides KC,
     // so every ring index is a compile-time constant.
-    constexpr int RING = KC >= 16 ? 4 : (KC < 8 ? KC : 8), PD = RING - 1;  // 4 at KC 16: registers
+    constexpr int RING = KC < 4 ? KC : 4, PD = RING - 1;
     intx4 ring[RING][2];
 #pragma unroll
     for (int c = 0; c < PD; ++c) load_a(ring[c], rs, c);
@@ -156,15 +156,21 @@ __global__ __launch_bounds__(512, 1) void k_mfma_ham(HamArgs a) {
         for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
             for (int cb = 0; cb < 4; ++cb) acc[rb][cb] = intx16{0};
+        // B operands one K-chunk ahead (the LDS read of chunk kc + 1 overlaps the MFMAs of kc)
+        intx4 bq[2][4];
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb) bq[0][cb] = sB[bslot(32 * cb + l32, h)];
 #pragma unroll
         for (int kc = 0; kc < KC; ++kc) {
             if constexpr (PD > 0) {
                 if (kc + PD < KC) load_a(ring[(kc + PD) % RING], rs, kc + PD);
                 else if (more) load_a(ring[(kc + PD) % RING], nrs, kc + PD - KC);
             }
-            intx4 b[4];
+            if (kc + 1 < KC) {
 #pragma unroll
-            for (int cb = 0; cb < 4; ++cb) b[cb] = sB[bslot(32 * cb + l32, 2 * kc + h)];
+                for (int cb = 0; cb < 4; ++cb) bq[(kc + 1) & 1][cb] = sB[bslot(32 * cb + l32, 2 * (kc + 1) + h)];
+            }
+            const intx4 (&b)[4] = bq[kc & 1];
             if constexpr (PD == 0) load_a(ring[0], rs, kc);  // KC == 1
 #pragma unroll
             for (int rb = 0; rb < 2; ++rb)
