@@ -34,7 +34,7 @@ METRIC = "kNN queries/sec (1M×128 fp32, k=100) + k-means iter/sec; % FP32-MFMA/
 PEAK_MFMA_F32 = 157.3e12   # FLOP/s, MI355X dense FP32 matrix
 PEAK_HBM = 8.0e12          # B/s
 PEAK_VALU32 = 39.3e12      # non-packed 32-bit VALU op/s (256 CU x 64 lanes x 2.4 GHz)
-PEAK_MFMA_I8 = 5.0e15      # OP/s, MI355X dense int8 matrix
+PEAK_MFMA_FP4 = 10.1e15    # OP/s, MI355X dense fp4 matrix
 
 
 def log(*a):
@@ -484,13 +484,12 @@ def bench_knn_workload(vh, key, steps, warmup, with_cpu):
     gemm = w["metric"] in ("l2", "dot", "cosine")
     if gemm:
         rl = roofline(prof, "mfma", PEAK_MFMA_F32, "TFLOP/s", key)
-    elif ham and w["d"] <= 16:
-        # codes of up to 512 bits run on the int8 matrix cores: 2 K int8 operations per
-        # (query, row), K = 32 * padded words
-        p2 = dict(prof)
-        rl = roofline(p2, "mfma", PEAK_MFMA_I8, "TFLOP/s", key)
+    elif ham and os.environ.get("VHIP_HAMMING_KERNEL") != "popcount":
+        # packed codes run on the fp4 matrix cores: 2 K operations per (query, row), K = the
+        # padded code bits (a power of two, at least 64)
+        rl = roofline(dict(prof), "mfma", PEAK_MFMA_FP4, "TFLOP/s", key)
         if rl:
-            rl["unit"] = "TOP/s (int8 MFMA)"
+            rl["unit"] = "TOP/s (fp4 MFMA)"
     else:
         # VALU-bound: work counts element (or word) operations, each costing two VALU ops
         p2 = dict(prof)
@@ -501,7 +500,8 @@ def bench_knn_workload(vh, key, steps, warmup, with_cpu):
     out = {"metric": METRIC, "value": round(w["nq"] * 1e3 / ms, 2), "unit": "queries/s", "n_gpus": 1,
            "steps": steps, "warmup": warmup, "ms_per_step": round(ms, 3), "higher_is_better": True,
            "scaling": "strong", "vs_baseline": None,
-           "dtype": ("i8" if w["d"] <= 16 else "u32") if ham else "f32", "data": "synthetic",
+           "dtype": ("u32" if os.environ.get("VHIP_HAMMING_KERNEL") == "popcount" else "fp4") if ham else "f32",
+           "data": "synthetic",
            "config": {"workload": w["name"], "base_rows": w["n"], "dim": w["d"] * (32 if ham else 1),
                       "queries": w["nq"], "k": w["k"], "metric": w["metric"], "parallelism": "single GPU"},
            "roofline": rl,

@@ -14,8 +14,7 @@ def vh():
     return vector_hip
 
 
-# Codes of up to 512 bits run on the int8 matrix cores (32..512 bits: every expanded width),
-# wider ones on the popcount kernel (1024 bits).
+# Every width runs on the fp4 matrix cores by default (32..1024 bits: every expanded width).
 @pytest.mark.parametrize("n,bits,nq,k", [(100_000, 256, 50, 10), (5000, 64, 17, 33), (777, 96, 3, 777),
                                          (300_000, 256, 8, 100), (20_000, 32, 40, 10), (3000, 160, 11, 64),
                                          (50_000, 512, 20, 50), (10_000, 1024, 9, 20), (300, 256, 130, 7)])
@@ -29,6 +28,34 @@ def test_hamming_bit_exact(vh, oracle, n, bits, nq, k):
     assert np.all(lens == min(k, n))
     assert np.array_equal(dist, rdist), "distances must be bit-exact"
     assert np.array_equal(ids, rids), "(distance, id) order makes ids identical"
+
+
+@pytest.mark.parametrize("kernel", ["popcount", "fp4"])
+@pytest.mark.parametrize("n,bits,nq,k", [(20_000, 32, 33, 10), (4000, 96, 130, 40), (60_000, 256, 17, 100),
+                                         (9000, 512, 5, 9), (3000, 1024, 64, 300)])
+def test_hamming_kernels_bit_exact(vh, oracle, monkeypatch, kernel, n, bits, nq, k):
+    """Both scan kernels, chosen with VHIP_HAMMING_KERNEL at engine creation: the popcount kernel
+    over the packed words (the engine's path when the fp4 copy does not fit) and the fp4
+    matrix-core kernel.  The profiler's work count shows which one ran: words per (query, row)
+    for popcount, 2 K for fp4 (K = the padded bits, at least 64)."""
+    from vector_hip import datasets as ds
+
+    print(f"hamming kernel={kernel} n={n} bits={bits} nq={nq} k={k}", flush=True)
+    monkeypatch.setenv("VHIP_HAMMING_KERNEL", kernel)
+    codes = ds.packed_bits(n, bits, 31)
+    q = ds.packed_bits(nq, bits, 32)
+    eng = vh.HammingKnnEngine(codes)
+    monkeypatch.delenv("VHIP_HAMMING_KERNEL")
+    eng.profile(True)
+    ids, dist, lens = eng.search_batch_arrays(q, k)
+    per = eng.profile_read()["work"] / (nq * n)
+    words = bits // 32
+    padded = 1 << (words - 1).bit_length()
+    assert per == (words if kernel == "popcount" else 2 * 32 * max(2, padded))
+    rids, rdist, _ = oracle.hamming_packed_knn(codes, q, k)
+    kk = min(k, n)
+    assert np.all(lens == kk)
+    assert np.array_equal(dist[:, :kk], rdist[:, :kk]) and np.array_equal(ids[:, :kk], rids[:, :kk])
 
 
 def test_hamming_equals_reference_float_hamming(vh, oracle):

@@ -5,7 +5,7 @@ Each case draws its shape at random from a fixed seed: base rows (1 to 20,000), 
 128-query tile), k (1 to 300, above n as well) and metric.  The case list is fixed, so a failure
 names a reproducible case.  It covers the paths the workload tests reach only at one shape:
 round sizing and balanced items at small n, the norm-seeded L2 accumulators at every
-K-chunk count, and the int8 Hamming kernel at every expanded width.
+K-chunk count, and the fp4 Hamming kernel at every expanded width.
 """
 import numpy as np
 import pytest
@@ -60,7 +60,7 @@ def test_float_engine_sweep(vh, oracle, case):
 
 @pytest.mark.parametrize("case", _cases(12, 77), ids=lambda c: f"{c[0]}-n{c[1]}-q{c[3]}-k{c[4]}")
 def test_packed_hamming_sweep(vh, oracle, case):
-    """Bit widths 32 to 1024 (int8 matrix-core and popcount kernels), bit-exact."""
+    """Bit widths 32 to 1024 (the fp4 matrix-core kernel at every chunk count), bit-exact."""
     from vector_hip import datasets as ds
 
     i, n, _, nq, k, _ = case

@@ -1,19 +1,22 @@
-// hamming_mfma.hip -- packed-bit Hamming kNN on the int8 matrix cores.
+// hamming_mfma.hip -- packed-bit Hamming kNN on the fp4 matrix cores.
 //
 // The popcount kernel (hamming.hip) runs at the VALU issue limit: two VALU operations (XOR,
-// bit count) per 32-bit word per query.  Here each bit of a code is expanded once to one int8,
-// x = 1 - 2 b (+1 for 0, -1 for 1).  For K-bit codes a and b the expanded vectors give
-// x . y = K - 2 popcount(a ^ b), so the Hamming distance is (K - x . y) / 2, exact in int32,
-// and the scan becomes an int8 GEMM on v_mfma_i32_32x32x32_i8 fused with the same threshold
-// filter as the FP32 kernels.  The reference's thresholded float Hamming (scalar.rs:143-153)
-// equals this distance on 0/1 codes.
+// bit count) per 32-bit word per query.  Here each bit of a code is expanded once to one fp4
+// (e2m1) value, x = 1 - 2 b (+1.0 for 0, -1.0 for 1), two to a byte.  For K-bit codes a and b
+// the expanded vectors give x . y = K - 2 popcount(a ^ b), so the Hamming distance is
+// (K - x . y) / 2.  Every product is +-1 and every partial sum an integer of magnitude <= K <=
+// 1024, so the f32 accumulation is exact, and the scan becomes an fp4 GEMM on
+// v_mfma_scale_f32_32x32x64_f8f6f4 (block scales fixed at 2^0) fused with the same threshold
+// filter as the FP32 kernels.  That instruction takes 64 K per 32 x 32 tile in the issue time
+// of the int8 one's 32 K, and its operands are half the bytes.  The reference's thresholded
+// float Hamming (scalar.rs:143-153) equals this distance on 0/1 codes.
 //
-// Tiling: a workgroup of 8 waves owns a work item of 128 query columns (their K-byte rows
+// Tiling: a workgroup of 8 waves owns a work item of 128 query columns (their expanded rows
 // resident in LDS, 16-byte slots XOR-swizzled by column so a 16-lane pass of ds_read_b128 is
 // conflict-free) x item_rows base rows, in stages of 512 rows; every wave streams its own 64
 // rows from L2 straight into registers, three K-chunks ahead (the base is stored in the A
 // operand's lane order, so each load is 1 KB contiguous), and computes a 64 x 128 block as 2 x 4
-// 32 x 32 tiles, so each base byte feeds 128 queries from registers.  The grid is persistent
+// 32 x 32 tiles, so each base code feeds 128 queries from registers.  The grid is persistent
 // and XCD-aware like the FP32 kernels.  FILTER keeps (distance, row) pairs with distance <= tau
 // in per-query LDS slots flushed once per item; DENSE (the first round) writes every pair.
 #include <algorithm>
@@ -23,7 +26,8 @@
 namespace vh {
 
 typedef int intx4 __attribute__((ext_vector_type(4)));
-typedef int intx16 __attribute__((ext_vector_type(16)));
+typedef int intx8 __attribute__((ext_vector_type(8)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 namespace {
 
@@ -33,8 +37,8 @@ constexpr int kHmSlots = kGemmSlotsReg;  // LDS candidate slots per query per wo
 constexpr int kHmFilter = 0, kHmDense = 1;
 
 struct HamArgs {
-    const int8_t *A;  // expanded base codes, K bytes per row, rows readable up to row_end + kHmStage
-    const int8_t *B;  // expanded query codes, K bytes per row, rows padded to a multiple of 128
+    const int8_t *A;  // expanded base codes, 32 KC bytes per row, rows readable up to row_end + kHmStage
+    const int8_t *B;  // expanded query codes, 32 KC bytes per row, rows padded to a multiple of 128
     const float *tau;
     int nq, n_ctiles, n_items;
     long row_begin, row_end, item_rows;
@@ -43,40 +47,48 @@ struct HamArgs {
     int cap;
 };
 
-// Expands rows of `words` packed uint32 (row stride wstride) to K = 32 * words int8 values
-// (bit i of word w -> byte 32 w + i: +1 for a clear bit, -1 for a set one).  Rows at or past
-// `rows` become all +1.  One thread writes the 4 bytes of one nibble.
-//  * tiled = false: row-major, K bytes per row (the query tiles, staged through LDS).
+// Expands rows of `words` packed uint32 (row stride wstride) to one fp4 value per bit, two to a
+// byte (bit i of word w -> nibble 32 w + i, the low nibble of a byte first): 0x2 (+1.0) for a
+// clear bit, 0xA (-1.0) for a set one.  Words from `words` up to `wout` (even) and rows at or past
+// `rows` read as clear bits.  A row is wout / 2 K-chunks of 32 bytes (64 bits).  One thread
+// writes the 4 bytes that hold one byte of a code.
+//  * tiled = false: row-major (the query tiles, staged through LDS).
 //  * tiled = true: the layout of the MFMA A operand, so that one 16-byte load per lane of a wave
 //    reads 1 KB contiguous (8 whole cache lines, not 32 partial ones): byte b of row r sits at
 //    ((r / 32) * KC + b / 32) * 1024 + ((b / 16) & 1) * 512 + (r % 32) * 16 + b % 16.
 __global__ __launch_bounds__(256) void k_ham_expand(const uint32_t *__restrict__ src, size_t rows, int words,
-                                                    int wstride, size_t rows_out, bool tiled,
+                                                    int wout, int wstride, size_t rows_out, bool tiled,
                                                     uint32_t *__restrict__ dst) {
-    const size_t per_row = (size_t)words * 8, total = rows_out * per_row;
+    const size_t per_row = (size_t)wout * 4, total = rows_out * per_row;  // 4-byte units
+    const int kc = wout >> 1;
     for (size_t t = blockIdx.x * (size_t)blockDim.x + threadIdx.x; t < total; t += (size_t)gridDim.x * blockDim.x) {
         const size_t r = t / per_row;
-        const int rem = (int)(t - r * per_row), w = rem >> 3, nib = rem & 7;
-        const uint32_t word = r < rows ? src[r * (size_t)wstride + w] : 0u;
-        const uint32_t b = (word >> (4 * nib)) & 15u;
-        uint32_t out = 0;
+        const int rem = (int)(t - r * per_row), w = rem >> 2, sel = rem & 3;
+        const uint32_t word = r < rows && w < words ? src[r * (size_t)wstride + w] : 0u;
+        const uint32_t b = (word >> (8 * sel)) & 255u;
+        uint32_t out = 0x22222222u;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) out |= ((b >> i) & 1u ? 0xffu : 0x01u) << (8 * i);
-        size_t o = t;  // in 4-byte units
+        for (int i = 0; i < 8; ++i) out |= ((b >> i) & 1u) << (4 * i + 3);
+        size_t o = t;
         if (tiled) {
             const int byte = 4 * rem;  // first of the 4 bytes within the row
-            const size_t blk = (r >> 5) * (size_t)words + (size_t)(byte >> 5);
+            const size_t blk = (r >> 5) * (size_t)kc + (size_t)(byte >> 5);
             o = (blk * 1024 + (size_t)((byte >> 4) & 1) * 512 + (r & 31) * 16 + (byte & 15)) >> 2;
         }
         dst[o] = out;
     }
 }
 
+// the fp4 operand: 32 nibbles in the low four registers (the upper four are not read)
+__device__ __forceinline__ intx8 fp4_operand(const intx4 &v) {
+    return __builtin_shufflevector(v, v, 0, 1, 2, 3, -1, -1, -1, -1);
+}
+
 __device__ __forceinline__ int ham_first_item() { return (blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3); }
 
 template <int MODE, int KC>
 __global__ __launch_bounds__(512, 1) void k_mfma_ham(HamArgs a) {
-    constexpr int K = 32 * KC, NS = K / 16;  // bytes per row, 16-byte slots per row
+    constexpr int K = 64 * KC, RB = 32 * KC, NS = RB / 16;  // bits (K), bytes and 16-byte slots per row
     constexpr int SW = NS < 16 ? NS - 1 : 15;
     __shared__ intx4 sB[kHmCols * NS];
     __shared__ uint32_t s_qcnt[MODE == kHmFilter ? kHmCols : 1];
@@ -98,7 +110,7 @@ __global__ __launch_bounds__(512, 1) void k_mfma_ham(HamArgs a) {
     auto fill_b = [&](int c0) {
         for (int f = tid; f < kHmCols * NS; f += 512) {
             const int c = f / NS, sidx = f - c * NS;
-            sB[bslot(c, sidx)] = *(const intx4 *)(a.B + (size_t)(c0 + c) * K + 16 * sidx);
+            sB[bslot(c, sidx)] = *(const intx4 *)(a.B + (size_t)(c0 + c) * RB + 16 * sidx);
         }
     };
     // the two 16-byte operands of K-chunk kc for this wave's rows rs + 64 wave + 32 rb + l32
@@ -116,14 +128,14 @@ __global__ __launch_bounds__(512, 1) void k_mfma_ham(HamArgs a) {
     if constexpr (MODE == kHmFilter) {
         if (tid < kHmCols) s_qcnt[tid] = 0;
     }
-    // per column: distance <= tq  <=>  dot >= T = K - 2 tq (distances are integers)
-    int T[4];
+    // per column: distance <= tq  <=>  dot >= T = K - 2 floor(tq) (distances are integers)
+    float T[4];
     auto item_begin = [&]() {
 #pragma unroll
         for (int cb = 0; cb < 4; ++cb) {
             const int q = col0 + 32 * cb + l32;
             const float t = q < a.nq ? a.tau[q] : -1.0f;
-            T[cb] = t < 0.0f ? K + 1 : (t >= (float)K ? -K : K - 2 * (int)t);
+            T[cb] = (float)(t < 0.0f ? K + 1 : (t >= (float)K ? -K : K - 2 * (int)t));
         }
     };
     item_begin();
@@ -151,11 +163,11 @@ __global__ __launch_bounds__(512, 1) void k_mfma_ham(HamArgs a) {
                 nrs = nlo;
             }
         }
-        intx16 acc[2][4];
+        floatx16 acc[2][4];
 #pragma unroll
         for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-            for (int cb = 0; cb < 4; ++cb) acc[rb][cb] = intx16{0};
+            for (int cb = 0; cb < 4; ++cb) acc[rb][cb] = floatx16{0.0f};
         // B operands one K-chunk ahead (the LDS read of chunk kc + 1 overlaps the MFMAs of kc)
         intx4 bq[2][4];
 #pragma unroll
@@ -163,8 +175,10 @@ __global__ __launch_bounds__(512, 1) void k_mfma_ham(HamArgs a) {
 #pragma unroll
         for (int kc = 0; kc < KC; ++kc) {
             if constexpr (PD > 0) {
+                // past the last item this re-reads the current stage (in bounds, never used):
+                // no branch inside the unrolled K loop
                 if (kc + PD < KC) load_a(ring[(kc + PD) % RING], rs, kc + PD);
-                else if (more) load_a(ring[(kc + PD) % RING], nrs, kc + PD - KC);
+                else load_a(ring[(kc + PD) % RING], more ? nrs : rs, kc + PD - KC);
             }
             if (kc + 1 < KC) {
 #pragma unroll
@@ -176,9 +190,16 @@ __global__ __launch_bounds__(512, 1) void k_mfma_ham(HamArgs a) {
             for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
                 for (int cb = 0; cb < 4; ++cb)
-                    acc[rb][cb] =
-                        __builtin_amdgcn_mfma_i32_32x32x32_i8(ring[kc % RING][rb], b[cb], acc[rb][cb], 0, 0, 0);
+                    acc[rb][cb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                        fp4_operand(ring[kc % RING][rb]), fp4_operand(b[cb]), acc[rb][cb], 4, 4, 0, 127, 0, 127);
         }
+        // all eight tiles complete here: without this the compiler sinks the second row block's
+        // products below the first block's filter branch, keeping every K-chunk's query operands
+        // live across it (spills at 512 bits and up)
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+            for (int cb = 0; cb < 4; ++cb) asm volatile("" : "+v"(acc[rb][cb]));
         // ---- epilogue: register 4g+j of tile (rb, cb) holds row rs + 64 wave + 32 rb + 8 g + 4 h + j
         // and column 32 cb + l32 ----
 #pragma unroll
@@ -189,10 +210,10 @@ __global__ __launch_bounds__(512, 1) void k_mfma_ham(HamArgs a) {
                 uint64_t m = 0;
 #pragma unroll
                 for (int cb = 0; cb < 4; ++cb) {
-                    const intx16 &v = acc[rb][cb];
-                    int mx = v[0];
+                    const floatx16 &v = acc[rb][cb];
+                    float mx = v[0];
 #pragma unroll
-                    for (int i = 1; i < 16; ++i) mx = max(mx, v[i]);
+                    for (int i = 1; i < 16; ++i) mx = fmaxf(mx, v[i]);
                     m |= __builtin_amdgcn_ballot_w64(mx >= T[cb]);
                 }
                 if (m == 0) continue;
@@ -210,8 +231,8 @@ __global__ __launch_bounds__(512, 1) void k_mfma_ham(HamArgs a) {
                         for (int j = 0; j < 4; ++j) {
                             const long row = row0 + j;
                             if (row < r_hi) {
-                                const int dist = (K - acc[rb][cb][4 * g + j]) >> 1;
-                                dst[row - a.row_begin] = make_uint2(score_key((float)dist), (uint32_t)row);
+                                const float dist = ((float)K - acc[rb][cb][4 * g + j]) * 0.5f;
+                                dst[row - a.row_begin] = make_uint2(score_key(dist), (uint32_t)row);
                             }
                         }
                     }
@@ -219,8 +240,8 @@ __global__ __launch_bounds__(512, 1) void k_mfma_ham(HamArgs a) {
                     uint64_t m = 0;
 #pragma unroll
                     for (int cb = 0; cb < 4; ++cb) {
-                        const intx16 &v = acc[rb][cb];
-                        const int mx = max(max(v[4 * g], v[4 * g + 1]), max(v[4 * g + 2], v[4 * g + 3]));
+                        const floatx16 &v = acc[rb][cb];
+                        const float mx = fmaxf(fmaxf(v[4 * g], v[4 * g + 1]), fmaxf(v[4 * g + 2], v[4 * g + 3]));
                         m |= __builtin_amdgcn_ballot_w64(mx >= T[cb]);
                     }
                     if (m == 0) continue;
@@ -228,11 +249,11 @@ __global__ __launch_bounds__(512, 1) void k_mfma_ham(HamArgs a) {
                     for (int cb = 0; cb < 4; ++cb)
 #pragma unroll
                         for (int j = 0; j < 4; ++j) {
-                            const int dot = acc[rb][cb][4 * g + j];
+                            const float dot = acc[rb][cb][4 * g + j];
                             const long row = row0 + j;
                             if (dot < T[cb] || row >= r_hi) continue;
                             const int ql = 32 * cb + l32;
-                            const uint32_t key = score_key((float)((K - dot) >> 1));
+                            const uint32_t key = score_key(((float)K - dot) * 0.5f);
                             const uint32_t rii = (uint32_t)(row - r_lo);
                             const uint32_t r = atomicAdd(&s_qcnt[ql], 1u);
                             if (r < (uint32_t)kHmSlots) {
@@ -286,14 +307,20 @@ __global__ __launch_bounds__(512, 1) void k_mfma_ham(HamArgs a) {
 
 size_t ham_mfma_rows(size_t n) { return round_up(n, kHmStage) + kHmStage; }
 
-bool ham_mfma_supported(int wpad) { return wpad >= 1 && wpad <= 16; }
+bool ham_mfma_supported(int wpad) { return wpad >= 1 && wpad <= 32; }
 
-void launch_ham_expand(const uint32_t *src, size_t rows, int words, int wstride, size_t rows_out, bool tiled,
+// 64-bit K-chunks per expanded row (a 32-bit code is padded with one clear word)
+static int ham_chunks(int wpad) { return wpad < 2 ? 1 : wpad / 2; }
+
+size_t ham_mfma_row_bytes(int wpad) { return 32 * (size_t)ham_chunks(wpad); }
+
+void launch_ham_expand(const uint32_t *src, size_t rows, int wpad, int wstride, size_t rows_out, bool tiled,
                        int8_t *dst, hipStream_t s) {
-    const size_t total = rows_out * (size_t)words * 8;
+    const int wout = 2 * ham_chunks(wpad);
+    const size_t total = rows_out * (size_t)wout * 4;
     if (total == 0) return;
     const unsigned blocks = (unsigned)std::min<size_t>(65536, (total + 255) / 256);
-    hipLaunchKernelGGL(k_ham_expand, dim3(blocks), dim3(256), 0, s, src, rows, words, wstride, rows_out, tiled,
+    hipLaunchKernelGGL(k_ham_expand, dim3(blocks), dim3(256), 0, s, src, rows, wpad, wout, wstride, rows_out, tiled,
                        (uint32_t *)dst);
 }
 
@@ -320,7 +347,7 @@ void launch_ham_mfma(bool dense, long item_rows, const int8_t *base8, const int8
     const dim3 grid((unsigned)((g + 7) / 8 * 8)), block(512);
 #define VH_HM(MODE, KC) hipLaunchKernelGGL((k_mfma_ham<MODE, KC>), grid, block, 0, s, a)
 #define VH_HM_K(MODE)                 \
-    switch (wpad) {                    \
+    switch (ham_chunks(wpad)) {        \
         case 1: VH_HM(MODE, 1); break; \
         case 2: VH_HM(MODE, 2); break; \
         case 4: VH_HM(MODE, 4); break; \

@@ -14,6 +14,8 @@
 // is re-run with a capacity equal to the largest round, which cannot overflow.
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
+#include <cstring>
 #include <memory>
 
 #include "vh_runtime.h"
@@ -39,7 +41,7 @@ struct vhip_knn {
     int grid_cap = 512;
     hipStream_t stream = nullptr;
     vh::DevBuf base, norm, perm, inv_perm;
-    vh::DevBuf base8;  // packed Hamming on the int8 matrix cores: one +1/-1 byte per code bit
+    vh::DevBuf base8;  // packed Hamming on the fp4 matrix cores: one +1/-1 nibble per code bit
     bool ham8 = false;
     std::mutex mu;
     vh::Workspace ws;
@@ -117,6 +119,24 @@ static int round_cap(size_t n, size_t k, bool gemm, int dpad) {
 }
 
 // Runs all rounds for nq prepared queries; results stay in topk / have.
+// Packed Hamming keeps a second copy of the codes expanded to one fp4 value per bit (4x the packed
+// bytes) for the matrix-core kernel.  The copy is made when it takes at most half of the device
+// memory free at creation (the rest stays for search workspaces); otherwise the engine scans the
+// packed codes with the popcount kernel.  VHIP_HAMMING_KERNEL = "popcount" or "fp4" overrides
+// the choice for engines created afterwards (both kernels give identical results).
+static bool want_fp4_copy(size_t bytes) {
+    if (const char *env = std::getenv("VHIP_HAMMING_KERNEL")) {
+        if (std::strcmp(env, "popcount") == 0) return false;
+        if (std::strcmp(env, "fp4") == 0) return true;
+    }
+    size_t free_b = 0, total_b = 0;
+    if (hipMemGetInfo(&free_b, &total_b) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    return bytes <= free_b / 2;
+}
+
 static int run_rounds(vhip_knn *E, const float *qpad, const float *qnorm, int nq, int k, int cap, DevBuf &cand,
                       DevBuf &topk, DevBuf &tau, DevBuf &have, DevBuf &cnt, DevBuf &flags, DevBuf &nflag) {
     hipStream_t s = E->stream;
@@ -132,9 +152,9 @@ static int run_rounds(vhip_knn *E, const float *qpad, const float *qnorm, int nq
     const bool gemm = is_gemm_metric(E->metric);
     const int8_t *q8 = nullptr;
     if (E->ham8) {
-        // the queries' +1/-1 bytes, rows padded to the 128-query tiles
+        // the queries' +1/-1 nibbles, rows padded to the 128-query tiles
         const size_t rows = round_up((size_t)nq, kTileCols);
-        VH_CHECK(E->ws.q8.ensure(E->dev, rows * 32 * E->dpad));
+        VH_CHECK(E->ws.q8.ensure(E->dev, rows * ham_mfma_row_bytes((int)E->dpad)));
         launch_ham_expand((const uint32_t *)qpad, (size_t)nq, (int)E->dpad, (int)E->dpad, rows, false,
                           E->ws.q8.as<int8_t>(), s);
         q8 = E->ws.q8.as<int8_t>();
@@ -147,9 +167,9 @@ static int run_rounds(vhip_knn *E, const float *qpad, const float *qnorm, int nq
         // are the base rows and queries each launch must read once.
         const double rows = (double)(re - rb);
         const double work = gemm ? 2.0 * nq * rows * (double)E->dim
-                                 : (E->ham8 ? 2.0 * nq * rows * 32.0 * (double)E->dpad
+                                 : (E->ham8 ? 2.0 * nq * rows * 2.0 * (double)ham_mfma_row_bytes((int)E->dpad)
                                             : (double)nq * rows * (double)E->dim);
-        const double bytes = E->ham8 ? (rows + nq) * 32.0 * (double)E->dpad  // the expanded int8 codes
+        const double bytes = E->ham8 ? (rows + nq) * (double)ham_mfma_row_bytes((int)E->dpad)  // expanded codes
                                      : rows * E->dim * 4.0 + (double)nq * E->dim * 4.0;
         if (dense) launch_fill_u32(cnt.as<uint32_t>(), (size_t)nq, (uint32_t)(re - rb), s);
         const int t = E->timer.begin(s);
@@ -157,7 +177,7 @@ static int run_rounds(vhip_knn *E, const float *qpad, const float *qnorm, int nq
             gemm && !rd.dense ? balanced_item(rd.item_rows, re - rb, ceil_div(nq, kTileCols), E->grid_cap / 2)
                               : rd.item_rows;
         if (E->ham8) {
-            // int8 matrix-core Hamming: 2 K operations per (query, row), K = 32 * dpad bits
+            // fp4 matrix-core Hamming: 2 K operations per (query, row), K = the padded code bits
             const long hitem =
                 dense ? re - rb
                       : balanced_item(rd.item_rows, re - rb, ceil_div(nq, kTileCols), E->grid_cap / 2, 512);
@@ -295,9 +315,10 @@ static int engine_create(const void *base, size_t n, size_t dim, int metric, int
                          E->base.as<float>(), E->norm.as<float>(), norm_kind_of(metric), transform_of(metric),
                          normalize_of(metric), __builtin_nanf(""), E->stream);
         VH_HIP(hipGetLastError());
-        if (metric == HAMMING_PACKED && ham_mfma_supported((int)E->dpad)) {
-            const size_t rows8 = ham_mfma_rows(n);
-            VH_CHECK(E->base8.ensure(ordinal, rows8 * 32 * E->dpad));
+        const size_t rows8 = ham_mfma_rows(n);
+        if (metric == HAMMING_PACKED && ham_mfma_supported((int)E->dpad) &&
+            want_fp4_copy(rows8 * ham_mfma_row_bytes((int)E->dpad))) {
+            VH_CHECK(E->base8.ensure(ordinal, rows8 * ham_mfma_row_bytes((int)E->dpad)));
             launch_ham_expand(E->base.as<uint32_t>(), n, (int)E->dpad, (int)E->dpad, rows8, true,
                               E->base8.as<int8_t>(), E->stream);
             VH_HIP(hipGetLastError());

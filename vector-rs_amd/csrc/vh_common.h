@@ -105,10 +105,12 @@ void launch_topk_refine(int nq, int k, int kout, int metric, const float *qpad, 
                         int ostride, hipStream_t s);
 // hamming.hip
 int hamming_word_pad(int words);
-// int8 matrix-core path of packed Hamming (hamming_mfma.hip): expanded code rows of 32 * wpad bytes
+// fp4 matrix-core path of packed Hamming (hamming_mfma.hip): codes of wpad words expanded to one
+// fp4 value per bit, ham_mfma_row_bytes(wpad) bytes per row (32-bit codes padded to 64 bits)
 size_t ham_mfma_rows(size_t n);
 bool ham_mfma_supported(int wpad);
-void launch_ham_expand(const uint32_t *src, size_t rows, int words, int wstride, size_t rows_out, bool tiled,
+size_t ham_mfma_row_bytes(int wpad);
+void launch_ham_expand(const uint32_t *src, size_t rows, int wpad, int wstride, size_t rows_out, bool tiled,
                        int8_t *dst, hipStream_t s);
 void launch_ham_mfma(bool dense, long item_rows, const int8_t *base8, const int8_t *qry8, int wpad,
                      const float *tau, int nq, long row_begin, long row_end, uint2 *cand, uint32_t *cnt, int cap,
