@@ -134,9 +134,11 @@ size_t vhip_top_k_reduce(const uint32_t *ids, const float *dist, size_t total, s
 /* ---- packed-bit Hamming kNN (extension: the reference has only the thresholded float
  * Hamming of scalar.rs:143-153, which equals popcount(a ^ b) on 0/1 codes) ------- */
 typedef struct vhip_hamming vhip_hamming;
-/* n codes of `words` uint32 each (1..32).  Codes of up to 16 words (512 bits) are also held on
- * the device expanded to one int8 per bit (8x the packed size) and searched on the int8 matrix
- * cores; wider codes use the popcount kernel.  Distances are exact either way. */
+/* n codes of `words` uint32 each (1..32).  The codes are also held on the device expanded to one
+ * fp4 value per bit (4x the packed size) and searched on the fp4 matrix cores, when that copy
+ * takes at most half of the free device memory; otherwise the popcount kernel scans the packed
+ * codes.  The environment variable VHIP_HAMMING_KERNEL ("popcount" or "fp4") overrides the
+ * choice at creation.  Distances are exact either way. */
 int vhip_hamming_create(const uint32_t *codes, size_t n, size_t words, int ordinal, vhip_hamming **out);
 int vhip_hamming_search_batch(vhip_hamming *eng, const uint32_t *queries, size_t nq, size_t k,
                               uint32_t *out_ids, uint32_t *out_dist, size_t *out_len);
