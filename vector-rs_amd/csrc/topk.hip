@@ -283,8 +283,10 @@ void launch_topk_finalize(int nq, int k, int kout, int metric, const unsigned lo
 // cancellation error grows with the norms.  For each kept neighbour the distance is
 // recomputed in the direct form of the reference CPU engine (sum (q-x)^2, sum q*x, or
 // dot / (sqrt(|q|^2) sqrt(|x|^2)) with the 1e-9 guard, scalar.rs:14-75), the k entries are
-// re-sorted by (distance, id), and written out.  One workgroup per query; each wave
-// evaluates one neighbour at a time with a lane-strided sum and a fixed xor butterfly.
+// re-sorted by (distance, id), and written out.  One workgroup per query: its threads first
+// fetch every kept neighbour's id and stored row at once (the id -> row lookup is a dependent
+// load), then groups of 16 lanes evaluate one neighbour each, 16 at a time, with float4 reads of
+// the row and the query (lane s sums pieces s, s + 16, ... in order) and a fixed xor butterfly.
 __global__ __launch_bounds__(256) void k_topk_refine(int k, int kout, int metric, const float *__restrict__ qpad,
                                                      const float *__restrict__ base,
                                                      const uint32_t *__restrict__ inv_perm, int dpad,
@@ -293,31 +295,42 @@ __global__ __launch_bounds__(256) void k_topk_refine(int k, int kout, int metric
                                                      uint32_t *__restrict__ out_ids, float *__restrict__ out_dist,
                                                      int ostride) {
     __shared__ u64 buf[kMaxK];
-    const int q = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    __shared__ uint32_t s_row[kMaxK];
+    const int q = blockIdx.x, tid = threadIdx.x;
     const int h = (int)have[q];
-    const float *qv = qpad + (size_t)q * dpad;
-    for (int j = wave; j < h; j += 4) {
-        const u64 e = topk[(size_t)q * k + j];
-        const uint32_t id = (uint32_t)e;
-        const uint32_t row = inv_perm[id];
-        const float *xv = base + (size_t)row * dpad;
+    for (int j = tid; j < h; j += 256) {
+        const uint32_t id = (uint32_t)topk[(size_t)q * k + j];
+        s_row[j] = inv_perm[id];
+        buf[j] = id;
+    }
+    __syncthreads();
+    const int grp = tid >> 4, s = tid & 15, n4 = dpad >> 2;  // dpad is a multiple of 32
+    const float4 *qv = (const float4 *)(qpad + (size_t)q * dpad);
+    for (int j = grp; j < h; j += 16) {
+        const uint32_t row = s_row[j];
+        const float4 *xv = (const float4 *)(base + (size_t)row * dpad);
         float a = 0.0f, nq = 0.0f, nx = 0.0f;
-        for (int d = lane; d < dpad; d += 64) {
-            const float x = xv[d], y = qv[d];
+        for (int d = s; d < n4; d += 16) {
+            const float4 x = xv[d], y = qv[d];
             if (metric == L2) {
-                const float t = y - x;
-                a = fmaf(t, t, a);
+                const float t0 = y.x - x.x, t1 = y.y - x.y, t2 = y.z - x.z, t3 = y.w - x.w;
+                a = fmaf(t0, t0, a);
+                a = fmaf(t1, t1, a);
+                a = fmaf(t2, t2, a);
+                a = fmaf(t3, t3, a);
             } else {
-                a = fmaf(y, x, a);
-                nq = fmaf(y, y, nq);
-                nx = fmaf(x, x, nx);
+                a = fmaf(y.x, x.x, fmaf(y.y, x.y, fmaf(y.z, x.z, fmaf(y.w, x.w, a))));
+                nq = fmaf(y.x, y.x, fmaf(y.y, y.y, fmaf(y.z, y.z, fmaf(y.w, y.w, nq))));
+                nx = fmaf(x.x, x.x, fmaf(x.y, x.y, fmaf(x.z, x.z, fmaf(x.w, x.w, nx))));
             }
         }
 #pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-            a += __shfl_xor(a, o, 64);
-            nq += __shfl_xor(nq, o, 64);
-            nx += __shfl_xor(nx, o, 64);
+        for (int o = 8; o > 0; o >>= 1) {
+            a += __shfl_xor(a, o, 16);
+            if (metric != L2) {
+                nq += __shfl_xor(nq, o, 16);
+                nx += __shfl_xor(nx, o, 16);
+            }
         }
         float sc;
         if (metric == L2) {
@@ -329,7 +342,7 @@ __global__ __launch_bounds__(256) void k_topk_refine(int k, int kout, int metric
             const float den = sqrtf(nq) * sqrtf(nx);
             sc = (den <= 1e-9f || qnorm[q] * bnorm[row] <= 1e-9f) ? 0.0f : -(a / den) + 0.0f;
         }
-        if (lane == 0) buf[j] = ((u64)score_key(sc) << 32) | id;
+        if (s == 0) buf[j] = ((u64)score_key(sc) << 32) | (uint32_t)buf[j];
     }
     int P = 2;
     while (P < h) P <<= 1;
