@@ -200,9 +200,10 @@ def _check_search(vh, oracle, ix, parts, queries, k, nprobe, metric, m_sub, ks, 
 
 SHAPES = [  # dim, M, Ks: register-held codebooks (ds 4 / 8 / 32 with Ks 256), cached codebooks
     # (ds 2 / 6 / 32, Ks <= 128), code rows through the DMA rings (M 16 / 32) and through
-    # registers (16-, 4- and 1-byte pieces)
+    # registers (16-, 4- and 1-byte pieces); (128, 16, 256) is the benchmark's shape
     (16, 4, 16), (64, 8, 256), (128, 4, 64), (96, 3, 100), (32, 16, 256), (30, 5, 7), (24, 4, 256),
-    (128, 32, 256), (64, 32, 256), (256, 16, 128), (64, 16, 256)]
+    (128, 32, 256), (64, 32, 256), (256, 16, 128), (64, 16, 256), (128, 16, 256), (64, 4, 256),
+    (128, 4, 256)]
 
 
 @pytest.mark.parametrize("dim,m_sub,ks", SHAPES)
@@ -229,6 +230,18 @@ def test_search_float_all_metrics(vh, oracle, metric):
     if metric in ("hellinger", "jaccard"):
         qs = np.abs(qs)
     _check_search(vh, oracle, ix, parts, qs, 20, 3, metric, m_sub, ks, exact=False)
+
+
+@pytest.mark.parametrize("dim,m_sub", [(128, 16), (64, 8), (64, 4), (128, 4)])
+def test_search_float_l2_register_codebooks(vh, oracle, dim, m_sub):
+    """Squared L2 on float parts with register-held codebooks of 8-, 16- and 32-float sub-spaces
+    (the first is the benchmark's shape, code rows through the DMA ring)."""
+    rng = np.random.default_rng(900 + dim + m_sub)
+    ks = 256
+    parts = _parts(rng, dim, m_sub, ks, 12, 4000, integer=False)
+    ix = _index(vh, parts, dim, m_sub, ks, vh.DistanceMetric.L2Squared)
+    qs = rng.standard_normal((30, dim)).astype(np.float32)
+    _check_search(vh, oracle, ix, parts, qs, 25, 4, "l2", m_sub, ks, exact=False)
 
 
 def test_search_large_k_and_short_lists(vh, oracle):
