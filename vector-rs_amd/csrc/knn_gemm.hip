@@ -1017,6 +1017,8 @@ __global__ __launch_bounds__(512, 1) void k_mfma_hs(ScanArgs a) {
         }
     };
     // Interleave the step's MFMAs with the epilogue's VALU work: 1 MFMA, then up to 2 VALU.
+    // ASSIGN raises the wave's priority over each step's MFMAs (1% faster k-means assign); the
+    // filter measured 1% slower with it and keeps equal priorities
     auto interleave = [&]() {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
@@ -1052,7 +1054,9 @@ __global__ __launch_bounds__(512, 1) void k_mfma_hs(ScanArgs a) {
             if (kc + 1 < NK) load_a(nxt, rs, 0, kc + 1);
             else load_a(nxt, rs, 1, 0);
             __builtin_amdgcn_sched_barrier(0);
+            if constexpr (MODE == kAssign) __builtin_amdgcn_s_setprio(1);
             mfma_step(acc[0], cur, kc, init0, FUSE && kc == 0);
+            if constexpr (MODE == kAssign) __builtin_amdgcn_s_setprio(0);
             epi(acc[1], nrm[1], rs - TR, 1, (4 * kc) / NK, (4 * (kc + 1)) / NK, prev);
             interleave();
 #pragma unroll
@@ -1072,7 +1076,9 @@ __global__ __launch_bounds__(512, 1) void k_mfma_hs(ScanArgs a) {
             if (!last) load_a(nxt, rs, 1, kc + 1);
             else if (more) load_a(nxt, nrs, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
+            if constexpr (MODE == kAssign) __builtin_amdgcn_s_setprio(1);
             mfma_step(acc[1], cur, kc, init1, FUSE && kc == 0);
+            if constexpr (MODE == kAssign) __builtin_amdgcn_s_setprio(0);
             epi(acc[0], nrm[0], rs, 0, (4 * kc) / NK, (4 * (kc + 1)) / NK, true);
             interleave();
             if (!last || more) {
