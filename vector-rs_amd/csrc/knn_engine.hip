@@ -119,6 +119,92 @@ static int round_cap(size_t n, size_t k, bool gemm, int dpad) {
 }
 
 // Runs all rounds for nq prepared queries; results stay in topk / have.
+// The engine's pseudo-random row order (positions p -> base rows perm[p], so that every round
+// scores a uniform sample of the base): a 4-round Feistel network over the 2^m >= n codes (m
+// even), cycle-walked back into [0, n).  The walk from x follows x's own cycle, which returns to
+// x < n, so it ends; with 2^m < 4n it takes fewer than 4 steps on average.  The round function
+// is the "lowbias32" integer hash (Chris Wellons).  Built on the device, with the inverse for the
+// GEMM metrics' refine, so engine creation does no host shuffle and no extra upload.
+struct RowShuffle {
+    uint32_t half_bits, mask;
+    uint32_t key[4];
+};
+
+__device__ __forceinline__ uint32_t shuffle_code(uint32_t x, const RowShuffle &f) {
+    uint32_t l = x >> f.half_bits, r = x & f.mask;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        uint32_t h = r ^ f.key[i];
+        h ^= h >> 16;
+        h *= 0x7feb352du;
+        h ^= h >> 15;
+        h *= 0x846ca68bu;
+        h ^= h >> 16;
+        const uint32_t nr = (l ^ h) & f.mask;
+        l = r;
+        r = nr;
+    }
+    return (l << f.half_bits) | r;
+}
+
+__global__ __launch_bounds__(256) void k_row_shuffle(uint32_t n, RowShuffle f, uint32_t *__restrict__ perm,
+                                                     uint32_t *__restrict__ inv) {
+    for (uint32_t p = blockIdx.x * blockDim.x + threadIdx.x; p < n; p += gridDim.x * blockDim.x) {
+        uint32_t x = p;
+        do {
+            x = shuffle_code(x, f);
+        } while (x >= n);
+        perm[p] = x;
+        if (inv) inv[x] = p;
+    }
+}
+
+// Per-block maximum and minimum of x[0, count): the host folds the gridDim.x pairs (NaN values
+// are skipped, as std::max / std::min over the same values would).
+__global__ __launch_bounds__(256) void k_minmax_partial(const float *__restrict__ x, size_t count,
+                                                        float *__restrict__ pmax, float *__restrict__ pmin) {
+    __shared__ float rmax[256], rmin[256];
+    float mx = 0.0f, mn = INFINITY;
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < count; i += (size_t)gridDim.x * blockDim.x) {
+        mx = fmaxf(mx, x[i]);
+        mn = fminf(mn, x[i]);
+    }
+    rmax[threadIdx.x] = mx;
+    rmin[threadIdx.x] = mn;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+        if ((int)threadIdx.x < o) {
+            rmax[threadIdx.x] = fmaxf(rmax[threadIdx.x], rmax[threadIdx.x + o]);
+            rmin[threadIdx.x] = fminf(rmin[threadIdx.x], rmin[threadIdx.x + o]);
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        pmax[blockIdx.x] = rmax[0];
+        pmin[blockIdx.x] = rmin[0];
+    }
+}
+
+constexpr int kMinMaxParts = 1024;
+
+static int build_row_order(vhip_knn *E, size_t n, bool with_inverse) {
+    int m = 2;
+    while (m < 32 && (1ull << m) < n) ++m;
+    m += m & 1;
+    RowShuffle f;
+    f.half_bits = (uint32_t)(m / 2);
+    f.mask = (1u << f.half_bits) - 1u;
+    uint64_t st = kPermSeed;
+    for (int i = 0; i < 4; ++i) f.key[i] = (uint32_t)splitmix64(st);
+    VH_CHECK(E->perm.ensure(E->dev, n * sizeof(uint32_t)));
+    if (with_inverse) VH_CHECK(E->inv_perm.ensure(E->dev, n * sizeof(uint32_t)));
+    const unsigned blocks = (unsigned)std::min<size_t>(4096, (n + 255) / 256);
+    hipLaunchKernelGGL(k_row_shuffle, dim3(blocks), dim3(256), 0, E->stream, (uint32_t)n, f, E->perm.as<uint32_t>(),
+                       with_inverse ? E->inv_perm.as<uint32_t>() : nullptr);
+    VH_HIP(hipGetLastError());
+    return VHIP_OK;
+}
+
 // Packed Hamming keeps a second copy of the codes expanded to one fp4 value per bit (4x the packed
 // bytes) for the matrix-core kernel.  The copy is made when it takes at most half of the device
 // memory free at creation (the rest stays for search workspaces); otherwise the engine scans the
@@ -297,17 +383,10 @@ static int engine_create(const void *base, size_t n, size_t dim, int metric, int
     VH_HIP(hipStreamCreateWithFlags(&E->stream, hipStreamNonBlocking));
     VH_CHECK(E->stager.init(ordinal));
     if (n > 0) {
-        std::vector<uint32_t> perm = row_permutation(n, kPermSeed);
-        VH_CHECK(E->perm.ensure(ordinal, n * sizeof(uint32_t)));
-        VH_CHECK(E->stager.h2d(E->perm.p, perm.data(), n * sizeof(uint32_t), E->stream));
-        if (is_gemm_metric(metric)) {
-            std::vector<uint32_t> inv(n);
-            for (size_t p = 0; p < n; ++p) inv[perm[p]] = (uint32_t)p;
-            VH_CHECK(E->inv_perm.ensure(ordinal, n * sizeof(uint32_t)));
-            VH_CHECK(E->stager.h2d(E->inv_perm.p, inv.data(), n * sizeof(uint32_t), E->stream));
-        }
+        VH_CHECK(build_row_order(E.get(), n, is_gemm_metric(metric)));
         DevBuf raw;
-        VH_CHECK(raw.ensure(ordinal, n * dim * sizeof(float)));
+        // the raw rows; afterwards, scratch for the norm extremes' partials
+        VH_CHECK(raw.ensure(ordinal, std::max(n * dim * sizeof(float), 2 * kMinMaxParts * sizeof(float))));
         VH_CHECK(E->stager.h2d(raw.p, base, n * dim * sizeof(float), E->stream));
         VH_CHECK(E->base.ensure(ordinal, E->n_pad * E->dpad * sizeof(float)));
         VH_CHECK(E->norm.ensure(ordinal, E->n_pad * sizeof(float)));
@@ -325,14 +404,20 @@ static int engine_create(const void *base, size_t n, size_t dim, int metric, int
             E->ham8 = true;
         }
         if (norm_kind_of(metric)) {
-            // extremes of the row norms: the L2 filter's rounding slack and the cosine zero-norm guard
-            std::vector<float> nh(n);
-            VH_HIP(hipMemcpyAsync(nh.data(), E->norm.p, n * sizeof(float), hipMemcpyDeviceToHost, E->stream));
+            // extremes of the row norms (the L2 filter's rounding slack and the cosine zero-norm
+            // guard), reduced on the device into the raw buffer, which row preparation (earlier
+            // on this stream) no longer needs
+            float *part = raw.as<float>();
+            hipLaunchKernelGGL(k_minmax_partial, dim3(kMinMaxParts), dim3(256), 0, E->stream, E->norm.as<float>(), n,
+                               part, part + kMinMaxParts);
+            VH_HIP(hipGetLastError());
+            std::vector<float> ph(2 * kMinMaxParts);
+            VH_HIP(hipMemcpyAsync(ph.data(), part, ph.size() * sizeof(float), hipMemcpyDeviceToHost, E->stream));
             VH_HIP(hipStreamSynchronize(E->stream));
             float mx = 0.0f, mn = INFINITY;
-            for (float v : nh) {
-                mx = std::max(mx, v);
-                mn = std::min(mn, v);
+            for (int b = 0; b < kMinMaxParts; ++b) {
+                mx = std::max(mx, ph[b]);
+                mn = std::min(mn, ph[kMinMaxParts + b]);
             }
             E->norm_max = mx;
             E->norm_min = mn;

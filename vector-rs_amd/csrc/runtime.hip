@@ -2,6 +2,8 @@
 // host-side top_k_reduce of the C ABI.
 #include <algorithm>
 #include <cmath>
+#include <condition_variable>
+#include <mutex>
 #include <thread>
 
 #include "vh_runtime.h"
@@ -70,26 +72,76 @@ int device_grid_cap(int ordinal) {
 namespace {
 // Host copy into a pinned block, split over a few threads for large blocks: a single thread
 // copying from pageable (or freshly mapped, page-cache backed) memory reaches only a fraction of
-// what the PCIe DMA drains.
-void staged_copy(void *dst, const void *src, size_t bytes) {
-    constexpr size_t kPart = 4u << 20;
-    const unsigned hw = std::max(1u, std::thread::hardware_concurrency());
-    const unsigned nt = (unsigned)std::min<size_t>(std::min(8u, hw), (bytes + kPart - 1) / kPart);
-    if (nt <= 1) {
-        std::memcpy(dst, src, bytes);
-        return;
+// what the PCIe DMA drains.  The helper threads are started once per process and kept (spawning
+// them per 32 MiB block cost more than the copy gained); one copy runs at a time, the caller
+// taking the first part itself.
+class CopyPool {
+public:
+    static CopyPool &get() {
+        static CopyPool *p = new CopyPool();  // never destroyed: its threads block until exit
+        return *p;
     }
-    const size_t per = (bytes + nt - 1) / nt;
-    std::vector<std::thread> th;
-    th.reserve(nt - 1);
-    for (unsigned t = 1; t < nt; ++t) {
-        const size_t o = t * per;
-        if (o >= bytes) break;
-        th.emplace_back([=] { std::memcpy((char *)dst + o, (const char *)src + o, std::min(per, bytes - o)); });
+    void copy(void *dst, const void *src, size_t bytes) {
+        constexpr size_t kPart = 4u << 20;
+        const unsigned nt = (unsigned)std::min<size_t>(helpers_ + 1, (bytes + kPart - 1) / kPart);
+        if (nt <= 1) {
+            std::memcpy(dst, src, bytes);
+            return;
+        }
+        std::lock_guard<std::mutex> one(job_mu_);
+        const size_t per = (bytes + nt - 1) / nt;
+        {
+            std::lock_guard<std::mutex> g(mu_);
+            dst_ = (char *)dst;
+            src_ = (const char *)src;
+            bytes_ = bytes;
+            per_ = per;
+            next_ = 1;
+            parts_ = nt;
+            left_ = nt - 1;
+            ++gen_;
+        }
+        cv_.notify_all();
+        std::memcpy(dst, src, std::min(per, bytes));
+        std::unique_lock<std::mutex> g(mu_);
+        done_cv_.wait(g, [&] { return left_ == 0; });
     }
-    std::memcpy(dst, src, std::min(per, bytes));
-    for (auto &x : th) x.join();
-}
+
+private:
+    CopyPool() {
+        const unsigned hw = std::max(1u, std::thread::hardware_concurrency());
+        helpers_ = std::min(7u, hw - 1);
+        for (unsigned t = 0; t < helpers_; ++t) std::thread([this] { run(); }).detach();
+    }
+    void run() {
+        uint64_t seen = 0;
+        std::unique_lock<std::mutex> g(mu_);
+        for (;;) {
+            cv_.wait(g, [&] { return gen_ != seen && next_ < parts_; });
+            seen = gen_;
+            while (next_ < parts_) {
+                const size_t o = (size_t)next_++ * per_;
+                char *d = dst_;
+                const char *s = src_;
+                const size_t n = o < bytes_ ? std::min(per_, bytes_ - o) : 0;
+                g.unlock();
+                if (n) std::memcpy(d + o, s + o, n);
+                g.lock();
+                if (--left_ == 0) done_cv_.notify_all();
+            }
+        }
+    }
+    unsigned helpers_ = 0;
+    std::mutex job_mu_, mu_;
+    std::condition_variable cv_, done_cv_;
+    char *dst_ = nullptr;
+    const char *src_ = nullptr;
+    size_t bytes_ = 0, per_ = 0;
+    unsigned next_ = 0, parts_ = 0, left_ = 0;
+    uint64_t gen_ = 0;
+};
+
+void staged_copy(void *dst, const void *src, size_t bytes) { CopyPool::get().copy(dst, src, bytes); }
 }  // namespace
 
 PinnedStager::~PinnedStager() {
