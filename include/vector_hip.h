@@ -69,6 +69,9 @@ extern "C" {
 const char *vhip_last_error(void);
 /* requested / available of the last InsufficientDevices error of this thread. */
 void vhip_last_error_devices(size_t *requested, size_t *available);
+/* The ordinal of the last DeviceNotFound error of this thread (CudaError::DeviceNotFound{ordinal},
+ * error.rs:13-14); -1 before any. */
+int vhip_last_error_ordinal(void);
 
 /* ---- device context: CudaDeviceContext (device.rs:110-256) ------------------- */
 /* CudaDeviceContext::device_count (device.rs:112-117): number of usable gfx950 GPUs. */

@@ -10,6 +10,8 @@ update wherever the membership agrees.  Each iteration is checked from the same 
 import numpy as np
 import pytest
 
+from kmeans_check import check_step as _check_step
+
 pytestmark = pytest.mark.gpu
 
 
@@ -88,39 +90,6 @@ def test_integration_clustering_then_sharded_search(vh):
 
 
 # ---- per-iteration parity against the oracle -------------------------------------------
-def _check_step(oracle, data, cent, got, metric, max_flip_frac=1e-4):
-    """got: GPU state after one iteration from `cent`."""
-    ref = oracle.kmeans_step(data, cent, metric, threads=0)
-    ga, ra = got["assign"], ref["assign"]
-    flips = np.nonzero(ga != ra)[0]
-    assert len(flips) <= max(1, int(max_flip_frac * len(data))), f"{len(flips)} assignment flips"
-    for p in flips:  # only near-ties may flip
-        dg = oracle.distance(metric, data[p], cent[ga[p]])
-        dr = oracle.distance(metric, data[p], cent[ra[p]])
-        assert abs(dg - dr) <= 1e-4 * max(1.0, abs(dr)), f"point {p}: {dg} vs {dr} is not a near-tie"
-    k, d = cent.shape
-    # update = mean of the assigned points (float64), empty clusters keep their centroid
-    counts = np.bincount(ga, minlength=k)
-    assert np.array_equal(counts, got["counts"])
-    sums = np.zeros((k, d))
-    np.add.at(sums, ga, data.astype(np.float64))
-    for c in range(k):
-        if counts[c] == 0:
-            assert np.array_equal(got["centroids"][c], cent[c]) and got["shifts"][c] == 0
-            continue
-        want = sums[c] / counts[c]
-        err = np.linalg.norm(got["centroids"][c] - want)
-        assert err <= 1e-4 * max(np.linalg.norm(want), 1e-6), f"centroid {c} off by {err}"
-    # and the oracle's own f32 update wherever membership agrees
-    same = np.ones(k, bool)
-    same[np.unique(np.concatenate([ga[flips], ra[flips]]))] = False
-    for c in np.nonzero(same)[0]:
-        want = ref["centroids"][c]
-        assert np.linalg.norm(got["centroids"][c] - want) <= 1e-4 * max(np.linalg.norm(want), 1e-6)
-    assert abs(got["inertia"] - ref["inertia"]) <= 1e-4 * abs(ref["inertia"]) + 1e-3
-    return len(flips)
-
-
 def test_mixture_10_iterations_parity(vh, oracle):
     from vector_hip import datasets as ds
 

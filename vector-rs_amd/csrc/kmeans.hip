@@ -4,22 +4,33 @@
 // kmeans.cu.  One iteration is:
 //   1. assign   -- fused distance + argmin (MFMA tiles for L2 / dot / cosine in knn_gemm.hip,
 //                  VALU tiles for the other metrics in knn_valu.hip); each point also takes an
-//                  atomic ticket pos[p] in its cluster's count (integer atomics: exact);
-//   2. scan     -- exclusive scan of the k counts into segment offsets;
-//   3. scatter  -- point indices into their cluster segment at offsets[c] + pos[p];
-//   4. sums     -- every wave walks a fixed 256-slot window of the cluster-sorted order, adds its
-//                  rows in 64-bit fixed point and, at each cluster boundary, adds the partial sum
-//                  into the cluster's 64-bit accumulators with integer atomics.  Integer addition
-//                  is associative, so the sums -- and every centroid -- are bit-identical whatever
-//                  order the atomics handed out the slots or the windows were scheduled (the
-//                  reference's float atomics, kmeans.cu:298-320, and rayon fold,
-//                  ivf/kmeans.rs:75-118, are order-dependent).  Windows of equal size keep large
-//                  and small clusters balanced across the GPU.  The fixed-point scale 2^E is chosen
-//                  from max|x| and n so no sum can overflow and the resolution (2^-E) is far below
-//                  f32 rounding of the mean;
-//   5. finalize -- one wave per cluster: new = sum / count; shift = sum_d (new - old)^2; an empty
-//                  cluster keeps its centroid with shift 0 (kmeans.cu:350-356); the accumulators
-//                  are cleared for the next iteration.
+//                  atomic ticket pos[p] in its cluster's count (integer atomics: exact).  For
+//                  squared L2 the points and centroids are held minus a per-dimension shift (the
+//                  column means of the points, integers for integer data), which keeps the
+//                  GEMM form well conditioned on data away from the origin.  The MFMA assignment
+//                  is certified: a point whose best and second-best scores are not separated by
+//                  twice its selection error bound goes to a fix-up list instead, and
+//   2. fix-up   -- assigns the listed points by the direct-form metric of the unshifted data over
+//                  all centroids (knn_valu.hip), so every assignment is the argmin of the direct
+//                  form the reference computes (lowest index among equal values);
+//   3. scan     -- exclusive scan of the k counts into segment offsets;
+//   4. scatter  -- point indices into their cluster segment at offsets[c] + pos[p];
+//   5. sums     -- every wave walks a fixed 256-slot window of the cluster-sorted order and adds
+//                  the deviations x - c_old of its rows in 64-bit fixed point; at each cluster
+//                  boundary it adds the partial sum into the cluster's 64-bit accumulators with
+//                  integer atomics.  Integer addition is associative, so the sums -- and every
+//                  centroid -- are bit-identical whatever order the atomics handed out the slots
+//                  or the windows were scheduled (the reference's float atomics,
+//                  kmeans.cu:298-320, and rayon fold, ivf/kmeans.rs:75-118, are
+//                  order-dependent).  Each cluster has its own scale 2^E, from its point count and
+//                  a bound of its points' deviations, so no sum can overflow and the resolution is
+//                  relative to the cluster's own spread (a tight cluster near the origin keeps full
+//                  precision next to wide clusters far away).  The same pass writes each point's
+//                  squared-L2 inertia in direct form;
+//   6. finalize -- one wave per cluster: new = old + deviation sum / count; shift =
+//                  sum_d (new - old)^2; an empty cluster keeps its centroid with shift 0
+//                  (kmeans.cu:350-356); the accumulators are cleared for the next iteration;
+//   7. prepare  -- the centroids' assign rows (shifted), norms and bounds for the next assign.
 // With tol < 0 no per-iteration host synchronisation happens.
 #include <algorithm>
 #include <cmath>
@@ -91,17 +102,45 @@ __device__ __forceinline__ int segment_of(const int32_t *__restrict__ offsets, i
     return lo;
 }
 
+// Fixed-point exponent of each cluster: with every |x_d - c_d| < 2^e1 and count + 1 < 2^e2,
+// a deviation sum times 2^E stays below 2^61 for E = 61 - e1 - e2 (at most 60).
+__global__ void k_update_scales(int k, const float *__restrict__ devmax, const int32_t *__restrict__ counts,
+                                int32_t *__restrict__ exps) {
+    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= k) return;
+    int E = 60;
+    const float dm = devmax[c];
+    if (dm > 0.0f && counts[c] > 0) {
+        int e1, e2;
+        (void)frexpf(dm, &e1);
+        (void)frexp((double)counts[c] + 1.0, &e2);
+        E = min(60, 61 - e1 - e2);
+    }
+    exps[c] = E;
+}
+
+// Deviation bound of the metrics whose assignment keeps no distance: max|x| + max_d |c_d|.
+__global__ void k_dev_bound(int k, float absmax, const float *__restrict__ cabs, float *__restrict__ devmax) {
+    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c < k) devmax[c] = (absmax + cabs[c]) * 1.0001f;
+}
+
 // S = number of 64-dimension slots per lane (dpad <= 64 * S).  Lane l of a wave owns dimensions
-// l, l + 64, ...; the wave adds the rows of its window slot by slot in fixed point and flushes the
-// running sum into sums[c] whenever the window crosses into the next cluster's segment.
+// l, l + 64, ...; the wave adds the deviations x - c of the rows of its window slot by slot in
+// fixed point (the cluster's scale) and flushes the running sum into sums[c] whenever the window
+// crosses into the next cluster's segment.  With `l2_inertia` it also writes each point's
+// squared distance sum_d (x_d - c_d)^2 (lane-strided sum, fixed xor butterfly).
 template <int S>
 constexpr int upd_unroll() { return S >= 8 ? 4 : (S >= 4 ? 8 : 16); }  // rows in flight per wave
 
 template <int S>
-__global__ __launch_bounds__(256) void k_update_sums(const float *__restrict__ pts, int dpad, int dim, int n, int k,
+__global__ __launch_bounds__(256) void k_update_sums(const float *__restrict__ pts, const float *__restrict__ cent,
+                                                     int dpad, int dim, int n, int k,
                                                      const int32_t *__restrict__ sorted,
                                                      const int32_t *__restrict__ offsets,
-                                                     unsigned long long *__restrict__ sums, double scale) {
+                                                     const int32_t *__restrict__ exps,
+                                                     unsigned long long *__restrict__ sums, float *__restrict__ inertia,
+                                                     int l2_inertia) {
     constexpr int kUpdUnroll = upd_unroll<S>();
     const int lane = threadIdx.x & 63;
     const int wave = (int)((blockIdx.x * (size_t)blockDim.x + threadIdx.x) >> 6);
@@ -111,8 +150,19 @@ __global__ __launch_bounds__(256) void k_update_sums(const float *__restrict__ p
     int c = segment_of(offsets, k, s0);
     int next = offsets[c + 1];
     long long acc[S];
+    float cv[S];
+    double scale = 1.0;
+    auto load_c = [&](int cc) {
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            const int d = lane + 64 * s;
+            cv[s] = d < dpad ? cent[(size_t)cc * dpad + d] : 0.0f;
+        }
+        scale = ldexp(1.0, exps[cc]);
+    };
 #pragma unroll
     for (int s = 0; s < S; ++s) acc[s] = 0;
+    load_c(c);
     auto flush = [&](int cc) {
 #pragma unroll
         for (int s = 0; s < S; ++s) {
@@ -141,13 +191,26 @@ __global__ __launch_bounds__(256) void k_update_sums(const float *__restrict__ p
             for (int u = 0; u < kUpdUnroll; ++u) {
                 const int i = b + j + u;
                 if (i < s1) {
-                    while (i >= next) {  // offsets[k] = n > i, so c stays below k
-                        flush(c);
-                        ++c;
-                        next = offsets[c + 1];
+                    if (i >= next) {
+                        while (i >= next) {  // offsets[k] = n > i, so c stays below k
+                            flush(c);
+                            ++c;
+                            next = offsets[c + 1];
+                        }
+                        load_c(c);
                     }
+                    float d2 = 0.0f;
 #pragma unroll
-                    for (int s = 0; s < S; ++s) acc[s] += llrint((double)v[u][s] * scale);
+                    for (int s = 0; s < S; ++s) {
+                        acc[s] += llrint(((double)v[u][s] - (double)cv[s]) * scale);
+                        const float t = v[u][s] - cv[s];
+                        d2 = fmaf(t, t, d2);
+                    }
+                    if (l2_inertia) {
+#pragma unroll
+                        for (int o = 32; o > 0; o >>= 1) d2 += __shfl_xor(d2, o, 64);
+                        if (lane == 0) inertia[__builtin_amdgcn_readlane(mine, j + u)] = d2;
+                    }
                 }
             }
         }
@@ -155,19 +218,19 @@ __global__ __launch_bounds__(256) void k_update_sums(const float *__restrict__ p
     flush(c);
 }
 
-// One wave per cluster: new = sum / count, shift, norm (lane-strided sum + fixed xor butterfly,
-// the order of k_rows_prep), and the accumulators are cleared for the next iteration.
+// One wave per cluster: new = old + deviation sum / (2^E count), shift, and the accumulators are
+// cleared for the next iteration.  `cent` holds the unshifted centroids.
 template <int S>
 __global__ __launch_bounds__(256) void k_update_finalize(int k, int dpad, int dim, unsigned long long *__restrict__ sums,
-                                                         const int32_t *__restrict__ counts, float *__restrict__ cent,
-                                                         float *__restrict__ cnorm, int norm_kind,
-                                                         float *__restrict__ shifts, double inv_scale) {
+                                                         const int32_t *__restrict__ counts,
+                                                         const int32_t *__restrict__ exps, float *__restrict__ cent,
+                                                         float *__restrict__ shifts) {
     const int lane = threadIdx.x & 63;
     const int c = (int)((blockIdx.x * (size_t)blockDim.x + threadIdx.x) >> 6);
     if (c >= k) return;
     const int cnt = counts[c];
-    const double inv_cnt = cnt > 0 ? 1.0 / (double)cnt : 0.0;
-    float sh = 0.0f, nn = 0.0f;
+    const double inv = cnt > 0 ? ldexp(1.0, -exps[c]) / (double)cnt : 0.0;
+    float sh = 0.0f;
 #pragma unroll
     for (int s = 0; s < S; ++s) {
         const int d = lane + 64 * s;
@@ -177,25 +240,54 @@ __global__ __launch_bounds__(256) void k_update_finalize(int k, int dpad, int di
             *sp = 0ull;
             if (cnt > 0) {
                 float *cp = cent + (size_t)c * dpad + d;
-                const float nv = (float)((double)sum * inv_scale * inv_cnt);
-                const float diff = nv - *cp;
+                const float old = *cp;
+                const float nv = (float)((double)old + (double)sum * inv);
+                const float diff = nv - old;
                 sh = fmaf(diff, diff, sh);
-                nn = fmaf(nv, nv, nn);
                 *cp = nv;
             }
         }
     }
 #pragma unroll
+    for (int o = 32; o > 0; o >>= 1) sh += __shfl_xor(sh, o, 64);
+    if (lane == 0) shifts[c] = cnt > 0 ? sh : 0.0f;
+}
+
+// Assign rows of the centroids, one wave per row of kpad: cent = craw - shift (shift may be
+// null), the norm of that row (norm_kind 1 squared, 2 plain; deterministic lane-strided sum and
+// xor butterfly), max_d |craw_d| (cabs), and the largest norm value (cmax, u32 bits of a
+// non-negative float, atomic max; cleared by the caller).  Rows past k are NaN.
+__global__ __launch_bounds__(256) void k_cent_prep(int k, int kpad, int dpad, const float *__restrict__ craw,
+                                                   const float *__restrict__ shift, float *__restrict__ cent,
+                                                   float *__restrict__ cnorm, int norm_kind, float *__restrict__ cabs,
+                                                   uint32_t *__restrict__ cmax) {
+    const int lane = threadIdx.x & 63;
+    const int c = (int)((blockIdx.x * (size_t)blockDim.x + threadIdx.x) >> 6);
+    if (c >= kpad) return;
+    float *orow = cent + (size_t)c * dpad;
+    if (c >= k) {
+        for (int d = lane; d < dpad; d += 64) orow[d] = __builtin_nanf("");
+        if (lane == 0) cnorm[c] = __builtin_nanf("");
+        return;
+    }
+    float ss = 0.0f, am = 0.0f;
+    for (int d = lane; d < dpad; d += 64) {
+        const float x = craw[(size_t)c * dpad + d];
+        const float v = shift ? x - shift[d] : x;
+        orow[d] = v;
+        ss = fmaf(v, v, ss);
+        am = fmaxf(am, fabsf(x));
+    }
+#pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
-        sh += __shfl_xor(sh, o, 64);
-        nn += __shfl_xor(nn, o, 64);
+        ss += __shfl_xor(ss, o, 64);
+        am = fmaxf(am, __shfl_xor(am, o, 64));
     }
     if (lane == 0) {
-        shifts[c] = cnt > 0 ? sh : 0.0f;
-        if (cnt > 0) {
-            if (norm_kind == 1) cnorm[c] = nn;
-            else if (norm_kind == 2) cnorm[c] = sqrtf(nn);
-        }
+        const float nv = norm_kind == 2 ? sqrtf(ss) : ss;
+        cnorm[c] = nv;
+        cabs[c] = am;
+        if (norm_kind) atomicMax(cmax, __float_as_uint(nv));
     }
 }
 
@@ -330,16 +422,6 @@ __global__ void k_fill(float *p, size_t count, float v) {
     if (i < count) p[i] = v;
 }
 
-// dst row r (dpad floats) = src row idx[r], for r < k.
-__global__ __launch_bounds__(256) void k_gather_rows(const float *__restrict__ src, const uint32_t *__restrict__ idx,
-                                                     int k, int dpad, float *__restrict__ dst) {
-    const size_t total = (size_t)k * dpad;
-    for (size_t t = blockIdx.x * 256 + threadIdx.x; t < total; t += (size_t)gridDim.x * 256) {
-        const size_t r = t / dpad, c = t - r * dpad;
-        dst[t] = src[(size_t)idx[r] * dpad + c];
-    }
-}
-
 }  // namespace vh
 
 struct vhip_kmeans {
@@ -347,10 +429,17 @@ struct vhip_kmeans {
     size_t n = 0, n_pad = 0, dim = 0, dpad = 0, k = 0, kpad = 0;
     int metric = 0;
     int grid_cap = 512;
-    double scale = 1.0, inv_scale = 1.0;
+    float absmax = 0.0f;     // max |x| over the points
+    float err_coeff = 0.0f;  // selection error coefficient of the MFMA assignment
     bool assigned = false;
+    bool shifted = false;    // squared L2: pts / cent hold the data minus `shift`
     hipStream_t stream = nullptr;
-    vh::DevBuf pts, pnorm, cent, cnorm, assign, pos, inertia, counts, offsets, sorted, shifts, partial, sums;
+    // pts: the assign rows of the points (shifted for squared L2), praw the unshifted points when
+    // they differ (the update, inertia and fix-up read them); craw: the centroids (the state),
+    // cent: their assign rows (shifted, kpad rows with NaN padding)
+    vh::DevBuf pts, praw, shift, pnorm, craw, cent, cnorm, cabs, cmax, assign, pos, inertia, counts, offsets, sorted,
+        shifts, partial, sums, exps, devmax, fix, nfix, best;
+    const float *points() const { return shifted ? praw.as<float>() : pts.as<float>(); }
     vh::PinnedStager stager;
     vh::KernelTimer timer;
     std::mutex mu;
@@ -365,7 +454,8 @@ struct vhip_kmeans {
 
 namespace vh {
 
-static int km_norm_kind(int metric) { return metric == COS ? 2 : (metric == L2 ? 1 : 0); }
+// squared norms for L2 (epilogue and error bound) and dot product (error bound), norms for cosine
+static int km_norm_kind(int metric) { return metric == COS ? 2 : ((metric == L2 || metric == DOT) ? 1 : 0); }
 
 // Points given as nseg host segments (segment i: counts[i] rows of dim floats), uploaded one after
 // another into one device buffer, so callers with several shards need no concatenated copy.
@@ -403,12 +493,7 @@ static int km_create(int ordinal, const float *const *segs, const size_t *counts
             VH_CHECK(K->stager.h2d(raw.as<float>() + row * dim, segs[i], counts[i] * dim * sizeof(float), s));
         row += counts[i];
     }
-    // points padded to a multiple of 128 rows with zero rows (their results are never written)
-    VH_CHECK(K->pts.ensure(ordinal, K->n_pad * K->dpad * sizeof(float)));
-    VH_CHECK(K->pnorm.ensure(ordinal, K->n_pad * sizeof(float)));
-    launch_rows_prep(raw.as<float>(), n, K->n_pad, (int)dim, (int)K->dpad, nullptr, K->pts.as<float>(),
-                     K->pnorm.as<float>(), km_norm_kind(metric), 0, 0, 0.0f, s);
-    // fixed-point scale from max |x|
+    // max |x|: the finiteness check and the deviation bound of the non-L2 metrics' update
     const int nb = 1024;
     VH_CHECK(K->partial.ensure(ordinal, 8192 * sizeof(double)));
     hipLaunchKernelGGL(k_absmax_partial, dim3(nb), dim3(256), 0, s, raw.as<float>(), n * dim, K->partial.as<float>());
@@ -419,85 +504,156 @@ static int km_create(int ordinal, const float *const *segs, const size_t *counts
     float mx = 0.0f;
     for (float v : pm) mx = std::max(mx, v);
     if (!std::isfinite(mx)) return set_error(VHIP_ERR_INVALID_CONFIG, "data contains non-finite values");
-    // sum over <= n points of |x| * 2^E must stay below 2^62
-    int E = 60;
-    if (mx > 0.0f) {
-        const int ex = (int)std::ceil(std::log2((double)mx)) + (int)std::ceil(std::log2((double)n + 1.0));
-        E = std::min(60, 61 - ex);
+    K->absmax = mx;
+    if (metric == L2) {
+        // per-dimension shift: the column means (integers for integer data)
+        DevBuf part, flag;
+        VH_CHECK(part.ensure(ordinal, (size_t)col_shift_parts() * dim * sizeof(double)));
+        VH_CHECK(flag.ensure(ordinal, sizeof(uint32_t)));
+        VH_CHECK(K->shift.ensure(ordinal, K->dpad * sizeof(float)));
+        launch_fill_u32(flag.as<uint32_t>(), 1, 0u, s);
+        launch_col_shift(raw.as<float>(), n, (int)dim, (int)K->dpad, part.as<double>(), flag.as<uint32_t>(),
+                         K->shift.as<float>(), s);
+        VH_HIP(hipGetLastError());
+        std::vector<float> mu(K->dpad);
+        VH_HIP(hipMemcpyAsync(mu.data(), K->shift.p, K->dpad * sizeof(float), hipMemcpyDeviceToHost, s));
+        VH_HIP(hipStreamSynchronize(s));
+        for (float v : mu) K->shifted = K->shifted || v != 0.0f;
     }
-    K->scale = std::ldexp(1.0, E);
-    K->inv_scale = std::ldexp(1.0, -E);
+    // points padded to a multiple of 128 rows with zero rows (their results are never written)
+    VH_CHECK(K->pts.ensure(ordinal, K->n_pad * K->dpad * sizeof(float)));
+    VH_CHECK(K->pnorm.ensure(ordinal, K->n_pad * sizeof(float)));
+    if (K->shifted) VH_CHECK(K->praw.ensure(ordinal, K->n_pad * K->dpad * sizeof(float)));
+    RowPrep rp;
+    rp.in = raw.as<float>();
+    rp.n = n;
+    rp.n_out = K->n_pad;
+    rp.dim = (int)dim;
+    rp.dpad = (int)K->dpad;
+    rp.shift = K->shifted ? K->shift.as<float>() : nullptr;
+    rp.out = K->pts.as<float>();
+    rp.raw_out = K->shifted ? K->praw.as<float>() : nullptr;
+    rp.norm = K->pnorm.as<float>();
+    rp.norm_kind = km_norm_kind(metric);
+    launch_rows_prep(rp, s);
+    VH_HIP(hipGetLastError());
+    K->err_coeff = sel_err_coeff(metric, (int)K->dpad);
     VH_CHECK(K->assign.ensure(ordinal, n * sizeof(int32_t)));
     VH_CHECK(K->pos.ensure(ordinal, n * sizeof(int32_t)));
     VH_CHECK(K->inertia.ensure(ordinal, n * sizeof(float)));
     VH_CHECK(K->sorted.ensure(ordinal, n * sizeof(int32_t)));
+    if (is_gemm_metric(metric)) {
+        VH_CHECK(K->fix.ensure(ordinal, n * sizeof(int32_t)));
+        VH_CHECK(K->best.ensure(ordinal, n * sizeof(unsigned long long)));
+    }
+    VH_CHECK(K->nfix.ensure(ordinal, sizeof(uint32_t)));
+    VH_CHECK(K->cmax.ensure(ordinal, sizeof(uint32_t)));
+    VH_HIP(hipStreamSynchronize(s));  // `raw` is released at return
     *out = K.release();
     return VHIP_OK;
 }
 
-// Centroid rows are padded to a multiple of 128 with NaN rows: their scores are NaN and
-// never win the argmin.
+// Assign rows, norms and bounds of the current centroids (craw).
+static void km_prep_centroids(vhip_kmeans *K) {
+    launch_fill_u32(K->cmax.as<uint32_t>(), 1, 0u, K->stream);
+    hipLaunchKernelGGL(k_cent_prep, dim3(ceil_div((long)K->kpad, 4)), dim3(256), 0, K->stream, (int)K->k, (int)K->kpad,
+                       (int)K->dpad, K->craw.as<float>(), K->shifted ? K->shift.as<float>() : nullptr,
+                       K->cent.as<float>(), K->cnorm.as<float>(), km_norm_kind(K->metric), K->cabs.as<float>(),
+                       K->cmax.as<uint32_t>());
+}
+
+// Sets k centroids from device rows d_c (row stride `row_stride` floats: dim, or dpad for rows
+// already padded; d_c may be craw itself).  Assign rows are padded to a multiple of 256 with NaN
+// rows: their scores are NaN and never win the argmin.
 static int km_set_centroids_dev(vhip_kmeans *K, const float *d_c, size_t k, size_t row_stride) {
     const size_t kpad = round_up(k, kRowAlign);
+    if (d_c != K->craw.as<float>()) VH_CHECK(K->craw.ensure(K->dev, k * K->dpad * sizeof(float)));
     VH_CHECK(K->cent.ensure(K->dev, kpad * K->dpad * sizeof(float)));
     VH_CHECK(K->cnorm.ensure(K->dev, kpad * sizeof(float)));
+    VH_CHECK(K->cabs.ensure(K->dev, k * sizeof(float)));
     VH_CHECK(K->counts.ensure(K->dev, k * sizeof(int32_t)));
     VH_CHECK(K->offsets.ensure(K->dev, (k + 1) * sizeof(int32_t)));
     VH_CHECK(K->shifts.ensure(K->dev, k * sizeof(float)));
+    VH_CHECK(K->exps.ensure(K->dev, k * sizeof(int32_t)));
+    VH_CHECK(K->devmax.ensure(K->dev, k * sizeof(float)));
     VH_CHECK(K->sums.ensure(K->dev, k * K->dpad * sizeof(unsigned long long)));
     launch_fill_u32(K->sums.as<uint32_t>(), 2 * k * K->dpad, 0u, K->stream);
-    if (row_stride == K->dim) {
-        launch_rows_prep(d_c, k, kpad, (int)K->dim, (int)K->dpad, nullptr, K->cent.as<float>(),
-                         K->cnorm.as<float>(), km_norm_kind(K->metric), 0, 0, __builtin_nanf(""), K->stream);
-    } else {
-        // d_c already holds padded rows (the k-means++ path builds them in place): copy out
-        // and re-prepare so the norms are computed the same way.
-        DevBuf tmp;
-        VH_CHECK(tmp.ensure(K->dev, k * K->dpad * sizeof(float)));
-        VH_HIP(hipMemcpyAsync(tmp.p, d_c, k * K->dpad * sizeof(float), hipMemcpyDeviceToDevice, K->stream));
-        launch_rows_prep(tmp.as<float>(), k, kpad, (int)K->dpad, (int)K->dpad, nullptr, K->cent.as<float>(),
-                         K->cnorm.as<float>(), km_norm_kind(K->metric), 0, 0, __builtin_nanf(""), K->stream);
-        VH_HIP(hipStreamSynchronize(K->stream));
-    }
+    if (row_stride == K->dim)
+        launch_rows_prep(d_c, k, k, (int)K->dim, (int)K->dpad, nullptr, K->craw.as<float>(), nullptr, 0, 0, 0, 0.0f,
+                         K->stream);
+    else if (d_c != K->craw.as<float>())
+        VH_HIP(hipMemcpyAsync(K->craw.p, d_c, k * K->dpad * sizeof(float), hipMemcpyDeviceToDevice, K->stream));
     VH_HIP(hipGetLastError());
     K->k = k;
     K->kpad = kpad;
+    km_prep_centroids(K);
+    VH_HIP(hipGetLastError());
     K->assigned = false;
+    return VHIP_OK;
+}
+
+// Assignment of every point to its nearest centroid, with tickets pos / counts; inertia for all
+// metrics but squared L2 (the update writes that one).
+static int km_assign(vhip_kmeans *K) {
+    hipStream_t s = K->stream;
+    const int n = (int)K->n, k = (int)K->k;
+    launch_fill_u32(K->counts.as<uint32_t>(), k, 0u, s);
+    const int t = K->timer.begin(s);
+    if (is_gemm_metric(K->metric)) {
+        launch_fill_u32(K->devmax.as<uint32_t>(), k, 0u, s);
+        launch_fill_u32(K->nfix.as<uint32_t>(), 1, 0u, s);
+        AssignCert cert;
+        cert.err_coeff = K->err_coeff;
+        cert.cmax = K->cmax.as<float>();
+        cert.fix = K->fix.as<int32_t>();
+        cert.nfix = K->nfix.as<uint32_t>();
+        cert.devmax = K->devmax.as<float>();
+        launch_kmeans_assign(K->metric, K->cent.as<float>(), K->cnorm.as<float>(), (int)K->kpad, K->pts.as<float>(),
+                             K->pnorm.as<float>(), n, (int)K->dpad, K->assign.as<int32_t>(), K->inertia.as<float>(),
+                             K->pos.as<int32_t>(), K->counts.as<int32_t>(), cert, K->grid_cap, s);
+    } else {
+        launch_kmeans_assign_valu(K->metric, K->cent.as<float>(), k, K->pts.as<float>(), n, (int)K->dpad,
+                                  K->assign.as<int32_t>(), K->inertia.as<float>(), K->pos.as<int32_t>(),
+                                  K->counts.as<int32_t>(), K->grid_cap, s);
+    }
+    // algorithmic work: 2*n*k*dim flops (MFMA) or n*k*dim element operations; bytes: points + centroids
+    const double work = (is_gemm_metric(K->metric) ? 2.0 : 1.0) * (double)n * k * (double)K->dim;
+    K->timer.end(t, s, work, ((double)n + k) * K->dim * 4.0);
+    VH_HIP(hipGetLastError());
+    if (is_gemm_metric(K->metric)) {
+        launch_kmeans_fix(K->metric, K->points(), (int)K->dpad, K->fix.as<int32_t>(), K->nfix.as<uint32_t>(),
+                          K->craw.as<float>(), k, K->best.as<unsigned long long>(), K->assign.as<int32_t>(),
+                          K->inertia.as<float>(), K->pos.as<int32_t>(), K->counts.as<int32_t>(),
+                          K->devmax.as<float>(), K->grid_cap, s);
+        VH_HIP(hipGetLastError());
+    }
     return VHIP_OK;
 }
 
 static int km_iterate(vhip_kmeans *K) {
     hipStream_t s = K->stream;
     const int n = (int)K->n, k = (int)K->k;
-    launch_fill_u32(K->counts.as<uint32_t>(), k, 0u, s);
-    const int t = K->timer.begin(s);
-    if (is_gemm_metric(K->metric))
-        launch_kmeans_assign(K->metric, K->cent.as<float>(), K->cnorm.as<float>(), (int)K->kpad, K->pts.as<float>(),
-                             K->pnorm.as<float>(), n, (int)K->dpad, K->assign.as<int32_t>(), K->inertia.as<float>(),
-                             K->pos.as<int32_t>(), K->counts.as<int32_t>(), K->grid_cap, s);
-    else
-        launch_kmeans_assign_valu(K->metric, K->cent.as<float>(), k, K->pts.as<float>(), n, (int)K->dpad,
-                                  K->assign.as<int32_t>(), K->inertia.as<float>(), K->pos.as<int32_t>(),
-                                  K->counts.as<int32_t>(), K->grid_cap, s);
-    // algorithmic work: 2*n*k*dim flops (MFMA) or n*k*dim element operations; bytes: points + centroids
-    const double work = (is_gemm_metric(K->metric) ? 2.0 : 1.0) * (double)n * k * (double)K->dim;
-    K->timer.end(t, s, work, ((double)n + k) * K->dim * 4.0);
-    VH_HIP(hipGetLastError());
+    VH_CHECK(km_assign(K));
+    if (K->metric != L2)
+        hipLaunchKernelGGL(k_dev_bound, dim3(ceil_div(k, 256)), dim3(256), 0, s, k, K->absmax, K->cabs.as<float>(),
+                           K->devmax.as<float>());
+    hipLaunchKernelGGL(k_update_scales, dim3(ceil_div(k, 256)), dim3(256), 0, s, k, K->devmax.as<float>(),
+                       K->counts.as<int32_t>(), K->exps.as<int32_t>());
     hipLaunchKernelGGL(k_scan_counts, dim3(1), dim3(1024), 0, s, K->counts.as<int32_t>(), k, K->offsets.as<int32_t>());
     hipLaunchKernelGGL(k_scatter, dim3(ceil_div(n, 256)), dim3(256), 0, s, K->assign.as<int32_t>(),
                        K->pos.as<int32_t>(), K->offsets.as<int32_t>(), n, K->sorted.as<int32_t>());
     const int slots = ceil_div((long)K->dpad, 64);
-    const int nk = km_norm_kind(K->metric);
     const int waves = ceil_div(n, kUpdSlotsPerWave);
+    const int l2 = K->metric == L2 ? 1 : 0;
     unsigned long long *sums = K->sums.as<unsigned long long>();
 #define VH_UPD(S)                                                                                                  \
     do {                                                                                                           \
-        hipLaunchKernelGGL(k_update_sums<S>, dim3(ceil_div(waves, 4)), dim3(256), 0, s, K->pts.as<float>(),       \
-                           (int)K->dpad, (int)K->dim, n, k, K->sorted.as<int32_t>(), K->offsets.as<int32_t>(),      \
-                           sums, K->scale);                                                                         \
+        hipLaunchKernelGGL(k_update_sums<S>, dim3(ceil_div(waves, 4)), dim3(256), 0, s, K->points(),               \
+                           K->craw.as<float>(), (int)K->dpad, (int)K->dim, n, k, K->sorted.as<int32_t>(),          \
+                           K->offsets.as<int32_t>(), K->exps.as<int32_t>(), sums, K->inertia.as<float>(), l2);     \
         hipLaunchKernelGGL(k_update_finalize<S>, dim3(ceil_div(k, 4)), dim3(256), 0, s, k, (int)K->dpad,          \
-                           (int)K->dim, sums, K->counts.as<int32_t>(), K->cent.as<float>(), K->cnorm.as<float>(), nk, \
-                           K->shifts.as<float>(), K->inv_scale);                                                    \
+                           (int)K->dim, sums, K->counts.as<int32_t>(), K->exps.as<int32_t>(), K->craw.as<float>(), \
+                           K->shifts.as<float>());                                                                  \
     } while (0)
     if (slots <= 1) VH_UPD(1);
     else if (slots <= 2) VH_UPD(2);
@@ -505,6 +661,7 @@ static int km_iterate(vhip_kmeans *K) {
     else if (slots <= 8) VH_UPD(8);
     else VH_UPD(16);
 #undef VH_UPD
+    km_prep_centroids(K);
     VH_HIP(hipGetLastError());
     K->assigned = true;
     return VHIP_OK;
@@ -530,7 +687,9 @@ static int km_total_inertia(vhip_kmeans *K, float *out) {
 static int km_init_kmeanspp(vhip_kmeans *K, size_t k, uint64_t seed) {
     hipStream_t s = K->stream;
     const int n = (int)K->n;
-    VH_CHECK(K->cent.ensure(K->dev, round_up(k, kRowAlign) * K->dpad * sizeof(float)));
+    VH_CHECK(K->craw.ensure(K->dev, k * K->dpad * sizeof(float)));
+    const float *pts = K->points();
+    float *cr = K->craw.as<float>();
     DevBuf mind, part;
     const int nb = ceil_div(n, kKppBlock);
     VH_CHECK(mind.ensure(K->dev, (size_t)n * sizeof(float)));
@@ -538,13 +697,12 @@ static int km_init_kmeanspp(vhip_kmeans *K, size_t k, uint64_t seed) {
     hipLaunchKernelGGL(k_fill, dim3(ceil_div(n, 256)), dim3(256), 0, s, mind.as<float>(), (size_t)n, 3.4028235e38f);
     uint64_t st = seed;
     size_t idx = splitmix64(st) % (size_t)n;
-    VH_HIP(hipMemcpyAsync(K->cent.as<float>(), K->pts.as<float>() + idx * K->dpad, K->dpad * sizeof(float),
-                          hipMemcpyDeviceToDevice, s));
+    VH_HIP(hipMemcpyAsync(cr, pts + idx * K->dpad, K->dpad * sizeof(float), hipMemcpyDeviceToDevice, s));
     std::vector<double> ph(nb);
     std::vector<float> blk(kKppBlock);
     for (size_t j = 1; j < k; ++j) {
-        hipLaunchKernelGGL(k_kpp_update, dim3(nb), dim3(256), 0, s, K->pts.as<float>(), (int)K->dpad, n,
-                           K->cent.as<float>() + (j - 1) * K->dpad, mind.as<float>(), part.as<double>());
+        hipLaunchKernelGGL(k_kpp_update, dim3(nb), dim3(256), 0, s, pts, (int)K->dpad, n, cr + (j - 1) * K->dpad,
+                           mind.as<float>(), part.as<double>());
         VH_HIP(hipGetLastError());
         VH_HIP(hipMemcpyAsync(ph.data(), part.p, nb * sizeof(double), hipMemcpyDeviceToHost, s));
         VH_HIP(hipStreamSynchronize(s));
@@ -570,11 +728,11 @@ static int km_init_kmeanspp(vhip_kmeans *K, size_t k, uint64_t seed) {
                 }
             }
         }
-        VH_HIP(hipMemcpyAsync(K->cent.as<float>() + j * K->dpad, K->pts.as<float>() + idx * K->dpad,
-                              K->dpad * sizeof(float), hipMemcpyDeviceToDevice, s));
+        VH_HIP(hipMemcpyAsync(cr + j * K->dpad, pts + idx * K->dpad, K->dpad * sizeof(float), hipMemcpyDeviceToDevice,
+                              s));
     }
     VH_HIP(hipStreamSynchronize(s));
-    return km_set_centroids_dev(K, K->cent.as<float>(), k, K->dpad);
+    return km_set_centroids_dev(K, cr, k, K->dpad);
 }
 
 }  // namespace vh
@@ -626,27 +784,15 @@ int vhip_kmeans_assign_only(vhip_kmeans *K, int32_t *out_assign, float *out_scor
     std::lock_guard<std::mutex> lock(K->mu);
     VH_CHECK(open_device(K->dev));
     hipStream_t s = K->stream;
-    const int n = (int)K->n, k = (int)K->k;
-    launch_fill_u32(K->counts.as<uint32_t>(), k, 0u, s);
-    const int t = K->timer.begin(s);
-    if (is_gemm_metric(K->metric))
-        launch_kmeans_assign(K->metric, K->cent.as<float>(), K->cnorm.as<float>(), (int)K->kpad, K->pts.as<float>(),
-                             K->pnorm.as<float>(), n, (int)K->dpad, K->assign.as<int32_t>(), K->inertia.as<float>(),
-                             K->pos.as<int32_t>(), K->counts.as<int32_t>(), K->grid_cap, s);
-    else
-        launch_kmeans_assign_valu(K->metric, K->cent.as<float>(), k, K->pts.as<float>(), n, (int)K->dpad,
-                                  K->assign.as<int32_t>(), K->inertia.as<float>(), K->pos.as<int32_t>(),
-                                  K->counts.as<int32_t>(), K->grid_cap, s);
-    K->timer.end(t, s, (is_gemm_metric(K->metric) ? 2.0 : 1.0) * (double)n * k * (double)K->dim,
-                 ((double)n + k) * K->dim * 4.0);
-    VH_HIP(hipGetLastError());
+    const int n = (int)K->n;
+    VH_CHECK(km_assign(K));
     DevBuf score, resid;
     if (out_score || out_residual) {
         VH_CHECK(score.ensure(K->dev, K->n * sizeof(float)));
         if (out_residual) VH_CHECK(resid.ensure(K->dev, K->n * K->dim * sizeof(float)));
         const size_t blocks = std::min<size_t>(65536, (K->n + 3) / 4);
-        hipLaunchKernelGGL(k_coarse_score, dim3((unsigned)blocks), dim3(256), 0, s, K->pts.as<float>(), (int)K->dpad,
-                           (int)K->dim, n, K->cent.as<float>(), K->assign.as<int32_t>(), K->metric,
+        hipLaunchKernelGGL(k_coarse_score, dim3((unsigned)blocks), dim3(256), 0, s, K->points(), (int)K->dpad,
+                           (int)K->dim, n, K->craw.as<float>(), K->assign.as<int32_t>(), K->metric,
                            score.as<float>(), out_residual ? resid.as<float>() : nullptr);
         VH_HIP(hipGetLastError());
     }
@@ -667,7 +813,7 @@ int vhip_kmeans_read(vhip_kmeans *K, float *centroids, int32_t *assign, int64_t 
     VH_CHECK(open_device(K->dev));
     hipStream_t s = K->stream;
     if (centroids && K->k)
-        VH_HIP(hipMemcpy2DAsync(centroids, K->dim * sizeof(float), K->cent.p, K->dpad * sizeof(float),
+        VH_HIP(hipMemcpy2DAsync(centroids, K->dim * sizeof(float), K->craw.p, K->dpad * sizeof(float),
                                 K->dim * sizeof(float), K->k, hipMemcpyDeviceToHost, s));
     if (assign && K->assigned)
         VH_HIP(hipMemcpyAsync(assign, K->assign.p, K->n * sizeof(int32_t), hipMemcpyDeviceToHost, s));
@@ -749,9 +895,7 @@ int vhip_kmeans_fit_state(vhip_kmeans *K, size_t k, size_t max_iters, float tol,
         VH_CHECK(didx.ensure(K->dev, ek * sizeof(uint32_t)));
         VH_CHECK(rows.ensure(K->dev, ek * K->dpad * sizeof(float)));
         VH_HIP(hipMemcpyAsync(didx.p, idx.data(), ek * sizeof(uint32_t), hipMemcpyHostToDevice, K->stream));
-        const unsigned blocks = (unsigned)std::min<size_t>(4096, (ek * K->dpad + 255) / 256);
-        hipLaunchKernelGGL(k_gather_rows, dim3(blocks), dim3(256), 0, K->stream, K->pts.as<float>(),
-                           didx.as<uint32_t>(), (int)ek, (int)K->dpad, rows.as<float>());
+        launch_gather_rows(K->points(), didx.as<uint32_t>(), ek, (int)K->dpad, rows.as<float>(), K->stream);
         VH_HIP(hipGetLastError());
         VH_CHECK(km_set_centroids_dev(K, rows.as<float>(), ek, K->dpad));
         VH_HIP(hipStreamSynchronize(K->stream));  // didx/rows/idx are released at scope end

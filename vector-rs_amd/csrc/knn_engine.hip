@@ -28,7 +28,7 @@ constexpr size_t kQueryBatch = 16384;
 bool is_gemm_metric(int m) { return m == L2 || m == DOT || m == COS; }
 
 struct Workspace {
-    DevBuf qraw, qpad, qnorm, tau, have, cnt, flags, nflag, topk, cand, oids, odist, q8;
+    DevBuf qraw, qpad, qnorm, qerr, tau, have, cnt, flags, mflag, nflag, topk, cand, q8;
 };
 
 }  // namespace vh
@@ -41,6 +41,13 @@ struct vhip_knn {
     int grid_cap = 512;
     hipStream_t stream = nullptr;
     vh::DevBuf base, norm, perm, inv_perm;
+    // Squared L2: the rows are stored minus a per-dimension shift (the column means, integers for
+    // integer data), which keeps the norm form well conditioned on data away from the origin;
+    // `raw` holds the unshifted rows (same order and padding) for the direct-form passes.
+    vh::DevBuf shift, raw;
+    bool shifted = false;
+    bool integral = false;    // every base value is an integer
+    float err_coeff = 0.0f;   // selection error coefficient of the GEMM-form score
     vh::DevBuf base8;  // packed Hamming on the fp4 matrix cores: one +1/-1 nibble per code bit
     bool ham8 = false;
     std::mutex mu;
@@ -148,15 +155,17 @@ __device__ __forceinline__ uint32_t shuffle_code(uint32_t x, const RowShuffle &f
     return (l << f.half_bits) | r;
 }
 
+// The position index is 64-bit: with n close to 2^32 a 32-bit index stepping by the grid size
+// would wrap below n and never end.
 __global__ __launch_bounds__(256) void k_row_shuffle(uint32_t n, RowShuffle f, uint32_t *__restrict__ perm,
                                                      uint32_t *__restrict__ inv) {
-    for (uint32_t p = blockIdx.x * blockDim.x + threadIdx.x; p < n; p += gridDim.x * blockDim.x) {
-        uint32_t x = p;
+    for (uint64_t p = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; p < n; p += (uint64_t)gridDim.x * blockDim.x) {
+        uint32_t x = (uint32_t)p;
         do {
             x = shuffle_code(x, f);
         } while (x >= n);
         perm[p] = x;
-        if (inv) inv[x] = p;
+        if (inv) inv[x] = (uint32_t)p;
     }
 }
 
@@ -224,25 +233,41 @@ static bool want_fp4_copy(size_t bytes) {
     return bytes <= free_b / 2;
 }
 
-static int run_rounds(vhip_knn *E, const float *qpad, const float *qnorm, int nq, int k, int cap, DevBuf &cand,
-                      DevBuf &topk, DevBuf &tau, DevBuf &have, DevBuf &cnt, DevBuf &flags, DevBuf &nflag) {
+// One batch of prepared queries: the rows the scan kernels read (shifted for squared L2), their
+// norms and selection error bounds (null for the non-GEMM metrics), and the unshifted rows of
+// the direct-form passes (qpad itself when the engine keeps no shift).
+struct QueryRows {
+    const float *qpad, *qnorm, *qerr, *qraw;
+};
+
+// Base rows of the direct-form passes: the unshifted copy when the scan rows are shifted.
+static const float *direct_rows(const vhip_knn *E) { return E->shifted ? E->raw.as<float>() : E->base.as<float>(); }
+
+// Runs all rounds for nq prepared queries; results stay in topk (row stride kc) / have.
+// `direct`: score squared L2 in direct form on the unshifted rows (VALU kernel) instead of the
+// engine's own scan; it serves the queries whose GEMM-form margin could not be certified.
+static int run_rounds(vhip_knn *E, const QueryRows &Q, int nq, int k, int kc, int cap, bool direct, DevBuf &cand,
+                      DevBuf &topk, DevBuf &tau, DevBuf &have, DevBuf &cnt, DevBuf &flags, DevBuf &mflag,
+                      DevBuf &nflag) {
     hipStream_t s = E->stream;
     VH_CHECK(cand.ensure(E->dev, (size_t)nq * cap * sizeof(uint2)));
-    VH_CHECK(topk.ensure(E->dev, (size_t)nq * k * sizeof(unsigned long long)));
+    VH_CHECK(topk.ensure(E->dev, (size_t)nq * kc * sizeof(unsigned long long)));
     VH_CHECK(tau.ensure(E->dev, (size_t)nq * sizeof(float)));
     VH_CHECK(have.ensure(E->dev, (size_t)nq * sizeof(uint32_t)));
     VH_CHECK(cnt.ensure(E->dev, (size_t)nq * sizeof(uint32_t)));
     VH_CHECK(flags.ensure(E->dev, (size_t)nq * sizeof(uint32_t)));
-    VH_CHECK(nflag.ensure(E->dev, sizeof(uint32_t)));
+    VH_CHECK(mflag.ensure(E->dev, (size_t)nq * sizeof(uint32_t)));
+    VH_CHECK(nflag.ensure(E->dev, 2 * sizeof(uint32_t)));
     launch_topk_init(nq, tau.as<float>(), have.as<uint32_t>(), cnt.as<uint32_t>(), flags.as<uint32_t>(), s);
-    launch_fill_u32(nflag.as<uint32_t>(), 1, 0u, s);
-    const bool gemm = is_gemm_metric(E->metric);
+    launch_fill_u32(mflag.as<uint32_t>(), (size_t)nq, 0u, s);
+    launch_fill_u32(nflag.as<uint32_t>(), 2, 0u, s);
+    const bool gemm = is_gemm_metric(E->metric) && !direct;
     const int8_t *q8 = nullptr;
     if (E->ham8) {
         // the queries' +1/-1 nibbles, rows padded to the 128-query tiles
         const size_t rows = round_up((size_t)nq, kTileCols);
         VH_CHECK(E->ws.q8.ensure(E->dev, rows * ham_mfma_row_bytes((int)E->dpad)));
-        launch_ham_expand((const uint32_t *)qpad, (size_t)nq, (int)E->dpad, (int)E->dpad, rows, false,
+        launch_ham_expand((const uint32_t *)Q.qpad, (size_t)nq, (int)E->dpad, (int)E->dpad, rows, false,
                           E->ws.q8.as<int8_t>(), s);
         q8 = E->ws.q8.as<int8_t>();
     }
@@ -251,7 +276,8 @@ static int run_rounds(vhip_knn *E, const float *qpad, const float *qnorm, int nq
         const bool dense = rd.dense || (E->ham8 && rb == 0);
         // Algorithmic work per launch: 2*Q*rows*D flops (GEMM metrics), Q*rows*D element
         // operations (VALU metrics) or Q*rows*words word operations (packed Hamming); bytes
-        // are the base rows and queries each launch must read once.
+        // are the base rows and queries each launch must read once.  The direct-form passes
+        // are not timed (they are not the engine's scan).
         const double rows = (double)(re - rb);
         const double work = gemm ? 2.0 * nq * rows * (double)E->dim
                                  : (E->ham8 ? 2.0 * nq * rows * 2.0 * (double)ham_mfma_row_bytes((int)E->dpad)
@@ -259,7 +285,7 @@ static int run_rounds(vhip_knn *E, const float *qpad, const float *qnorm, int nq
         const double bytes = E->ham8 ? (rows + nq) * (double)ham_mfma_row_bytes((int)E->dpad)  // expanded codes
                                      : rows * E->dim * 4.0 + (double)nq * E->dim * 4.0;
         if (dense) launch_fill_u32(cnt.as<uint32_t>(), (size_t)nq, (uint32_t)(re - rb), s);
-        const int t = E->timer.begin(s);
+        const int t = direct ? -1 : E->timer.begin(s);
         const long item =
             gemm && !rd.dense ? balanced_item(rd.item_rows, re - rb, ceil_div(nq, kTileCols), E->grid_cap / 2)
                               : rd.item_rows;
@@ -274,81 +300,135 @@ static int run_rounds(vhip_knn *E, const float *qpad, const float *qnorm, int nq
             launch_ham_mfma(dense, hitem, E->base8.as<int8_t>(), q8, (int)E->dpad, tau.as<float>(), nq, rb, re,
                             cand.as<uint2>(), cnt.as<uint32_t>(), cap, E->grid_cap, s);
         } else if (gemm)
-            launch_gemm_filter(E->metric, rd.dense, item, E->base.as<float>(), E->norm.as<float>(), qpad,
-                               qnorm, tau.as<float>(), nq, (int)E->dpad, rb, re, cand.as<uint2>(),
-                               cnt.as<uint32_t>(), cap, E->norm_max, E->norm_min, E->grid_cap, s);
+            launch_gemm_filter(E->metric, rd.dense, item, E->base.as<float>(), E->norm.as<float>(), Q.qpad, Q.qnorm,
+                               tau.as<float>(), nq, (int)E->dpad, rb, re, cand.as<uint2>(), cnt.as<uint32_t>(), cap,
+                               E->norm_max, E->norm_min, E->grid_cap, s);
         else if (E->metric == HAMMING_PACKED)
-            launch_hamming_filter(E->base.as<uint32_t>(), (const uint32_t *)qpad, tau.as<float>(), nq, (int)E->dpad,
+            launch_hamming_filter(E->base.as<uint32_t>(), (const uint32_t *)Q.qpad, tau.as<float>(), nq, (int)E->dpad,
                                   rb, re, cand.as<uint2>(), cnt.as<uint32_t>(), cap, E->grid_cap, s);
+        else if (direct)
+            launch_valu_filter(L2, direct_rows(E), Q.qraw, tau.as<float>(), nq, (int)E->dim, (int)E->dpad, rb, re,
+                               cand.as<uint2>(), cnt.as<uint32_t>(), cap, E->grid_cap, s);
         else
-            launch_valu_filter(E->metric, E->base.as<float>(), qpad, tau.as<float>(), nq, (int)E->dim,
+            launch_valu_filter(E->metric, E->base.as<float>(), Q.qpad, tau.as<float>(), nq, (int)E->dim,
                                (int)E->dpad, rb, re, cand.as<uint2>(), cnt.as<uint32_t>(), cap, E->grid_cap, s);
-        E->timer.end(t, s, work, bytes);
+        if (t >= 0) E->timer.end(t, s, work, bytes);
         VH_HIP(hipGetLastError());
-        launch_topk_merge(nq, k, cand.as<uint2>(), cnt.as<uint32_t>(), cap, E->perm.as<uint32_t>(),
+        launch_topk_merge(nq, k, kc, cand.as<uint2>(), cnt.as<uint32_t>(), cap, E->perm.as<uint32_t>(),
                           topk.as<unsigned long long>(), have.as<uint32_t>(), tau.as<float>(), flags.as<uint32_t>(),
-                          nflag.as<uint32_t>(), s);
+                          nflag.as<uint32_t>(), gemm ? Q.qerr : nullptr, mflag.as<uint32_t>(), s);
         VH_HIP(hipGetLastError());
     }
     return VHIP_OK;
 }
 
-// Searches nq prepared queries (qpad / qnorm on device) for k = effective_k neighbours;
-// writes kout >= k entries per query (the rest marked empty) into device arrays d_ids and
-// d_dist or d_dist_u32 (row stride ostride).
-static int search_prepared(vhip_knn *E, const float *qpad, const float *qnorm, int nq, int k, int kout,
-                           uint32_t *d_ids, float *d_dist, uint32_t *d_dist_u32, int ostride) {
+// Capacity of a candidate list that no round can overflow: the largest round's rows.
+static int full_cap(const vhip_knn *E, size_t k, bool gemm) {
+    long big = k;
+    for (const Round &rd : plan_rounds(E->n, k, gemm, (int)E->dpad)) big = std::max(big, rd.re - rd.rb);
+    return (int)round_up((size_t)big, kRowAlign);
+}
+
+// Re-runs the queries idx (host list) of the batch Q: `direct` as in run_rounds, with a candidate
+// capacity no round can overflow, and writes their kept entries, counts and margin flags back
+// into the batch's arrays (row stride kc).
+static int rerun_queries(vhip_knn *E, const QueryRows &Q, const std::vector<uint32_t> &idx, int k, int kc,
+                         bool direct) {
+    Workspace &W = E->ws;
+    hipStream_t s = E->stream;
+    const bool gemm = is_gemm_metric(E->metric) && !direct;
+    const int kc_run = direct ? k : kc;
+    const int cap_big = full_cap(E, (size_t)k, gemm);
+    const size_t per_batch = std::max<size_t>(1, ((size_t)1 << 30) / ((size_t)cap_big * sizeof(uint2)));
+    DevBuf didx, fq, fn, fe, fr, fcand, ftopk, ftau, fhave, fcnt, fflags, fmflag, fnflag;
+    VH_CHECK(didx.ensure(E->dev, idx.size() * sizeof(uint32_t)));
+    VH_HIP(hipMemcpyAsync(didx.p, idx.data(), idx.size() * sizeof(uint32_t), hipMemcpyHostToDevice, s));
+    const int dp = (int)E->dpad;
+    for (size_t b0 = 0; b0 < idx.size(); b0 += per_batch) {
+        const int m = (int)std::min(per_batch, idx.size() - b0);
+        const size_t m_pad = round_up((size_t)m, kTileCols);
+        const uint32_t *di = didx.as<uint32_t>() + b0;
+        QueryRows F{nullptr, nullptr, nullptr, nullptr};
+        VH_CHECK(fr.ensure(E->dev, m_pad * E->dpad * sizeof(float)));
+        launch_fill(fr.as<float>() + (size_t)m * dp, (m_pad - m) * E->dpad, 0.0f, s);
+        launch_gather_rows(Q.qraw, di, (size_t)m, dp, fr.as<float>(), s);
+        F.qraw = fr.as<float>();
+        if (!direct) {
+            VH_CHECK(fq.ensure(E->dev, m_pad * E->dpad * sizeof(float)));
+            VH_CHECK(fn.ensure(E->dev, m_pad * sizeof(float)));
+            VH_CHECK(fe.ensure(E->dev, m_pad * sizeof(float)));
+            launch_fill(fq.as<float>() + (size_t)m * dp, (m_pad - m) * E->dpad, 0.0f, s);
+            launch_fill(fn.as<float>() + m, m_pad - m, 0.0f, s);
+            launch_fill(fe.as<float>() + m, m_pad - m, 0.0f, s);
+            launch_gather_rows(Q.qpad, di, (size_t)m, dp, fq.as<float>(), s);
+            launch_gather_rows(Q.qnorm, di, (size_t)m, 1, fn.as<float>(), s);
+            if (Q.qerr) launch_gather_rows(Q.qerr, di, (size_t)m, 1, fe.as<float>(), s);
+            F.qpad = fq.as<float>();
+            F.qnorm = fn.as<float>();
+            F.qerr = Q.qerr ? fe.as<float>() : nullptr;
+        }
+        VH_CHECK(run_rounds(E, F, m, k, kc_run, cap_big, direct, fcand, ftopk, ftau, fhave, fcnt, fflags, fmflag,
+                            fnflag));
+        launch_scatter_topk(ftopk.as<unsigned long long>(), kc_run, fhave.as<uint32_t>(),
+                            direct ? nullptr : fmflag.as<uint32_t>(), di, m, W.topk.as<unsigned long long>(), kc,
+                            W.have.as<uint32_t>(), W.mflag.as<uint32_t>(), s);
+        VH_HIP(hipGetLastError());
+    }
+    VH_HIP(hipStreamSynchronize(s));  // the staging buffers above are released at return
+    return VHIP_OK;
+}
+
+static std::vector<uint32_t> flagged(const std::vector<uint32_t> &f) {
+    std::vector<uint32_t> idx;
+    for (size_t q = 0; q < f.size(); ++q)
+        if (f[q]) idx.push_back((uint32_t)q);
+    return idx;
+}
+
+// Searches nq prepared queries for k = effective_k neighbours; writes kout >= k entries per query
+// (the rest marked empty) into device arrays d_ids and d_dist or d_dist_u32 (row stride ostride).
+//  * A query whose candidate list overflowed (massive ties) is re-run with a capacity that no
+//    round can overflow.
+//  * GEMM metrics keep, besides the k best by GEMM-form score, every entry within twice the
+//    query's selection error bound of the k-th (up to margin_cap(k) more); the direct-form refine
+//    then ranks them.  A squared-L2 query whose margin did not fit is re-run in direct form on the
+//    unshifted rows, so every L2 result is the exact top-k of the direct-form distances.  (For dot
+//    product and cosine a direct-form pass rounds no better than the GEMM form, so a cut margin
+//    keeps the kc best by GEMM score: only near-ties within the error bound are affected.)
+static int search_prepared(vhip_knn *E, const QueryRows &Q, int nq, int k, int kout, uint32_t *d_ids, float *d_dist,
+                           uint32_t *d_dist_u32, int ostride) {
     Workspace &W = E->ws;
     hipStream_t s = E->stream;
     const bool gemm = is_gemm_metric(E->metric);
+    const int kc = gemm ? k + margin_cap(k) : k;
     const int cap = round_cap(E->n, (size_t)k, gemm, (int)E->dpad);
-    VH_CHECK(run_rounds(E, qpad, qnorm, nq, k, cap, W.cand, W.topk, W.tau, W.have, W.cnt, W.flags, W.nflag));
-    uint32_t nflag = 0;
-    VH_HIP(hipMemcpyAsync(&nflag, W.nflag.p, sizeof(uint32_t), hipMemcpyDeviceToHost, s));
+    VH_CHECK(run_rounds(E, Q, nq, k, kc, cap, false, W.cand, W.topk, W.tau, W.have, W.cnt, W.flags, W.mflag,
+                        W.nflag));
+    if (gemm) launch_count_flags(W.mflag.as<uint32_t>(), nq, W.nflag.as<uint32_t>() + 1, s);
+    uint32_t nf[2] = {0, 0};
+    VH_HIP(hipMemcpyAsync(nf, W.nflag.p, sizeof(nf), hipMemcpyDeviceToHost, s));
     VH_HIP(hipStreamSynchronize(s));
-    if (nflag) {
-        // Overflowed queries: re-run with a capacity of the largest round (cannot overflow).
-        std::vector<uint32_t> flags(nq);
-        VH_HIP(hipMemcpy(flags.data(), W.flags.p, nq * sizeof(uint32_t), hipMemcpyDeviceToHost));
-        std::vector<int> idx;
-        for (int q = 0; q < nq; ++q)
-            if (flags[q]) idx.push_back(q);
-        long big = cap;
-        for (const Round &rd : plan_rounds(E->n, (size_t)k, gemm, (int)E->dpad)) big = std::max(big, rd.re - rd.rb);
-        const int cap_big = (int)round_up((size_t)std::max<long>(big, k), kRowAlign);
-        const size_t per_batch = std::max<size_t>(1, ((size_t)1 << 30) / ((size_t)cap_big * sizeof(uint2)));
-        DevBuf fq, fn, fcand, ftopk, ftau, fhave, fcnt, fflags, fnflag;
-        for (size_t b0 = 0; b0 < idx.size(); b0 += per_batch) {
-            const int m = (int)std::min(per_batch, idx.size() - b0);
-            const size_t m_pad = round_up((size_t)m, kTileCols);
-            VH_CHECK(fq.ensure(E->dev, m_pad * E->dpad * sizeof(float)));
-            VH_CHECK(fn.ensure(E->dev, m_pad * sizeof(float)));
-            launch_fill(fq.as<float>() + (size_t)m * E->dpad, (m_pad - m) * E->dpad, 0.0f, s);
-            launch_fill(fn.as<float>() + m, m_pad - m, 0.0f, s);
-            for (int j = 0; j < m; ++j) {
-                const int q = idx[b0 + j];
-                VH_HIP(hipMemcpyAsync(fq.as<float>() + (size_t)j * E->dpad, qpad + (size_t)q * E->dpad,
-                                      E->dpad * sizeof(float), hipMemcpyDeviceToDevice, s));
-                VH_HIP(hipMemcpyAsync(fn.as<float>() + j, qnorm + q, sizeof(float), hipMemcpyDeviceToDevice, s));
-            }
-            VH_CHECK(run_rounds(E, fq.as<float>(), fn.as<float>(), m, k, cap_big, fcand, ftopk, ftau, fhave, fcnt,
-                                fflags, fnflag));
-            for (int j = 0; j < m; ++j) {
-                const int q = idx[b0 + j];
-                VH_HIP(hipMemcpyAsync(W.topk.as<unsigned long long>() + (size_t)q * k,
-                                      ftopk.as<unsigned long long>() + (size_t)j * k, k * sizeof(unsigned long long),
-                                      hipMemcpyDeviceToDevice, s));
-                VH_HIP(hipMemcpyAsync(W.have.as<uint32_t>() + q, fhave.as<uint32_t>() + j, sizeof(uint32_t),
-                                      hipMemcpyDeviceToDevice, s));
-            }
+    if (nf[0]) {
+        std::vector<uint32_t> f(nq);
+        VH_HIP(hipMemcpy(f.data(), W.flags.p, nq * sizeof(uint32_t), hipMemcpyDeviceToHost));
+        VH_CHECK(rerun_queries(E, Q, flagged(f), k, kc, false));
+        if (gemm) {
+            launch_count_flags(W.mflag.as<uint32_t>(), nq, W.nflag.as<uint32_t>() + 1, s);
+            VH_HIP(hipMemcpyAsync(nf + 1, W.nflag.as<uint32_t>() + 1, sizeof(uint32_t), hipMemcpyDeviceToHost, s));
+            VH_HIP(hipStreamSynchronize(s));
         }
     }
-    if (is_gemm_metric(E->metric) && d_dist)
-        launch_topk_refine(nq, k, kout, E->metric, qpad, E->base.as<float>(), E->inv_perm.as<uint32_t>(),
-                           (int)E->dpad, qnorm, E->norm.as<float>(), W.topk.as<unsigned long long>(),
-                           W.have.as<uint32_t>(), d_ids, d_dist, ostride, s);
+    if (nf[1] && E->metric == L2) {
+        std::vector<uint32_t> f(nq);
+        VH_HIP(hipMemcpy(f.data(), W.mflag.p, nq * sizeof(uint32_t), hipMemcpyDeviceToHost));
+        VH_CHECK(rerun_queries(E, Q, flagged(f), k, kc, true));
+    }
+    if (gemm && d_dist)
+        launch_topk_refine(nq, k, kc, kout, E->metric, Q.qraw, direct_rows(E), E->inv_perm.as<uint32_t>(),
+                           (int)E->dpad, Q.qnorm, E->norm.as<float>(), W.topk.as<unsigned long long>(),
+                           W.have.as<uint32_t>(), Q.qerr, d_ids, d_dist, ostride, s);
     else
-        launch_topk_finalize(nq, k, kout, E->metric, W.topk.as<unsigned long long>(), W.have.as<uint32_t>(), d_ids,
+        launch_topk_finalize(nq, kc, kout, E->metric, W.topk.as<unsigned long long>(), W.have.as<uint32_t>(), d_ids,
                              d_dist, d_dist_u32, ostride, s);
     VH_HIP(hipGetLastError());
     return VHIP_OK;
@@ -361,7 +441,10 @@ static int check_search_args(vhip_knn *E, size_t k) {
     return VHIP_OK;
 }
 
-static int norm_kind_of(int metric) { return metric == COS ? 2 : (metric == L2 ? 1 : 0); }
+// L2 and dot keep squared norms (the L2 epilogue, and both metrics' selection error bounds),
+// cosine the norms before normalisation (zero-norm guard)
+static int norm_kind_of(int metric) { return metric == COS ? 2 : ((metric == L2 || metric == DOT) ? 1 : 0); }
+static int err_mode_of(int metric) { return metric == L2 ? 1 : (metric == DOT ? 2 : (metric == COS ? 3 : 0)); }
 static int transform_of(int metric) { return metric == HELL ? 1 : 0; }
 static int normalize_of(int metric) { return metric == COS ? 1 : 0; }
 
@@ -388,15 +471,45 @@ static int engine_create(const void *base, size_t n, size_t dim, int metric, int
     VH_CHECK(E->stager.init(ordinal));
     if (n > 0) {
         VH_CHECK(build_row_order(E.get(), n, is_gemm_metric(metric)));
-        DevBuf raw;
+        DevBuf raw, flag;
         // the raw rows; afterwards, scratch for the norm extremes' partials
         VH_CHECK(raw.ensure(ordinal, std::max(n * dim * sizeof(float), 2 * kMinMaxParts * sizeof(float))));
+        VH_CHECK(flag.ensure(ordinal, sizeof(uint32_t)));
+        launch_fill_u32(flag.as<uint32_t>(), 1, 0u, E->stream);
         VH_CHECK(E->stager.h2d(raw.p, base, n * dim * sizeof(float), E->stream));
+        if (metric == L2) {
+            // per-dimension shift: the column means (integers for integer data)
+            DevBuf part;
+            VH_CHECK(part.ensure(ordinal, (size_t)col_shift_parts() * dim * sizeof(double)));
+            VH_CHECK(E->shift.ensure(ordinal, E->dpad * sizeof(float)));
+            launch_col_shift(raw.as<float>(), n, (int)dim, (int)E->dpad, part.as<double>(), flag.as<uint32_t>(),
+                             E->shift.as<float>(), E->stream);
+            VH_HIP(hipGetLastError());
+            std::vector<float> mu(E->dpad);
+            VH_HIP(hipMemcpyAsync(mu.data(), E->shift.p, E->dpad * sizeof(float), hipMemcpyDeviceToHost, E->stream));
+            VH_HIP(hipStreamSynchronize(E->stream));
+            for (float v : mu) E->shifted = E->shifted || v != 0.0f;
+        }
         VH_CHECK(E->base.ensure(ordinal, E->n_pad * E->dpad * sizeof(float)));
         VH_CHECK(E->norm.ensure(ordinal, E->n_pad * sizeof(float)));
-        launch_rows_prep(raw.as<float>(), n, E->n_pad, (int)dim, (int)E->dpad, E->perm.as<uint32_t>(),
-                         E->base.as<float>(), E->norm.as<float>(), norm_kind_of(metric), transform_of(metric),
-                         normalize_of(metric), __builtin_nanf(""), E->stream);
+        if (E->shifted) VH_CHECK(E->raw.ensure(ordinal, E->n_pad * E->dpad * sizeof(float)));
+        RowPrep rp;
+        rp.in = raw.as<float>();
+        rp.n = n;
+        rp.n_out = E->n_pad;
+        rp.dim = (int)dim;
+        rp.dpad = (int)E->dpad;
+        rp.perm = E->perm.as<uint32_t>();
+        rp.shift = E->shifted ? E->shift.as<float>() : nullptr;
+        rp.out = E->base.as<float>();
+        rp.raw_out = E->shifted ? E->raw.as<float>() : nullptr;
+        rp.norm = E->norm.as<float>();
+        rp.norm_kind = norm_kind_of(metric);
+        rp.transform = transform_of(metric);
+        rp.normalize = normalize_of(metric);
+        rp.pad_fill = __builtin_nanf("");
+        rp.nonint = metric == HAMMING_PACKED ? nullptr : flag.as<uint32_t>();
+        launch_rows_prep(rp, E->stream);
         VH_HIP(hipGetLastError());
         const size_t rows8 = ham_mfma_rows(n);
         if (metric == HAMMING_PACKED && ham_mfma_supported((int)E->dpad) &&
@@ -407,10 +520,12 @@ static int engine_create(const void *base, size_t n, size_t dim, int metric, int
             VH_HIP(hipGetLastError());
             E->ham8 = true;
         }
+        uint32_t nonint = 1;
+        VH_HIP(hipMemcpyAsync(&nonint, flag.p, sizeof(uint32_t), hipMemcpyDeviceToHost, E->stream));
         if (norm_kind_of(metric)) {
-            // extremes of the row norms (the L2 filter's rounding slack and the cosine zero-norm
-            // guard), reduced on the device into the raw buffer, which row preparation (earlier
-            // on this stream) no longer needs
+            // extremes of the row norms (the L2 filter's rounding slack, the selection error bounds
+            // and the cosine zero-norm guard), reduced on the device into the raw buffer, which row
+            // preparation (earlier on this stream) no longer needs
             float *part = raw.as<float>();
             hipLaunchKernelGGL(k_minmax_partial, dim3(kMinMaxParts), dim3(256), 0, E->stream, E->norm.as<float>(), n,
                                part, part + kMinMaxParts);
@@ -427,6 +542,8 @@ static int engine_create(const void *base, size_t n, size_t dim, int metric, int
             E->norm_min = mn;
         }
         VH_HIP(hipStreamSynchronize(E->stream));
+        E->integral = nonint == 0;
+        E->err_coeff = sel_err_coeff(metric, (int)E->dpad);
     }
     *out = E.release();
     return VHIP_OK;
@@ -448,18 +565,41 @@ static int engine_search_device(vhip_knn *E, const void *d_queries, size_t nq, s
         return VHIP_OK;
     }
     Workspace &W = E->ws;
+    const bool gemm = is_gemm_metric(E->metric);
     for (size_t q0 = 0; q0 < nq; q0 += kQueryBatch) {
         const int m = (int)std::min(kQueryBatch, nq - q0);
         const size_t m_pad = round_up((size_t)m, kTileCols);
         VH_CHECK(W.qpad.ensure(E->dev, m_pad * E->dpad * sizeof(float)));
         VH_CHECK(W.qnorm.ensure(E->dev, m_pad * sizeof(float)));
-        launch_rows_prep((const float *)d_queries + q0 * E->dim, m, m_pad, (int)E->dim, (int)E->dpad, nullptr,
-                         W.qpad.as<float>(), W.qnorm.as<float>(), norm_kind_of(E->metric), transform_of(E->metric),
-                         normalize_of(E->metric), 0.0f, E->stream);
+        if (gemm) VH_CHECK(W.qerr.ensure(E->dev, m_pad * sizeof(float)));
+        if (E->shifted) VH_CHECK(W.qraw.ensure(E->dev, m_pad * E->dpad * sizeof(float)));
+        RowPrep rp;
+        rp.in = (const float *)d_queries + q0 * E->dim;
+        rp.n = (size_t)m;
+        rp.n_out = m_pad;
+        rp.dim = (int)E->dim;
+        rp.dpad = (int)E->dpad;
+        rp.shift = E->shifted ? E->shift.as<float>() : nullptr;
+        rp.out = W.qpad.as<float>();
+        rp.raw_out = E->shifted ? W.qraw.as<float>() : nullptr;
+        rp.norm = W.qnorm.as<float>();
+        rp.norm_kind = norm_kind_of(E->metric);
+        rp.transform = transform_of(E->metric);
+        rp.normalize = normalize_of(E->metric);
+        rp.pad_fill = 0.0f;
+        if (gemm) {
+            rp.err = W.qerr.as<float>();
+            rp.err_mode = err_mode_of(E->metric);
+            rp.err_coeff = E->err_coeff;
+            rp.err_nmax = E->norm_max;
+            rp.base_integral = E->integral ? 1 : 0;
+        }
+        launch_rows_prep(rp, E->stream);
         VH_HIP(hipGetLastError());
-        VH_CHECK(search_prepared(E, W.qpad.as<float>(), W.qnorm.as<float>(), m, (int)ek, (int)k, d_ids + q0 * k,
-                                 d_dist ? d_dist + q0 * k : nullptr, d_dist_u32 ? d_dist_u32 + q0 * k : nullptr,
-                                 (int)k));
+        const QueryRows Q{W.qpad.as<float>(), W.qnorm.as<float>(), gemm ? W.qerr.as<float>() : nullptr,
+                          E->shifted ? W.qraw.as<float>() : W.qpad.as<float>()};
+        VH_CHECK(search_prepared(E, Q, m, (int)ek, (int)k, d_ids + q0 * k, d_dist ? d_dist + q0 * k : nullptr,
+                                 d_dist_u32 ? d_dist_u32 + q0 * k : nullptr, (int)k));
     }
     VH_HIP(hipStreamSynchronize(E->stream));
     E->timer.collect();

@@ -59,59 +59,155 @@ constexpr int kStrSlots = kGemmSlotsStream;  // same for the streaming kernel (t
 __device__ __forceinline__ int swz(int row, int c4) { return row * 8 + (c4 ^ ((row >> 1) & 7)); }
 
 // ---------------------------------------------------------------------------------
-// Row preparation: rows [0, n) are copied (optionally gathered through `perm`, optionally
-// sqrt(|x|)-transformed, optionally L2-normalised) into rows of `dpad` floats with zero fill;
-// rows [n, n_out) are filled with `pad_fill`.  norm_kind 1 writes the squared L2 norm,
-// 2 the L2 norm (of the row before normalisation); padding rows get `pad_fill`.
-// One wave per row; the norm is a lane-strided sum followed by a fixed xor butterfly, so
-// it is deterministic.  With norm_kind 0, transform 0 and normalize 0 the copy is bit-exact,
-// so it also moves packed uint32 codes.
+// Row preparation (see RowPrep): one wave per row; the norm is a lane-strided sum followed by
+// a fixed xor butterfly, so it is deterministic.
 // ---------------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_rows_prep(const float *__restrict__ in, size_t n, size_t n_out, int dim,
-                                                   int dpad, const uint32_t *__restrict__ perm,
-                                                   float *__restrict__ out, float *__restrict__ norm, int norm_kind,
-                                                   int transform, int normalize, float pad_fill) {
+__global__ __launch_bounds__(256) void k_rows_prep(RowPrep a) {
     const int lane = threadIdx.x & 63;
     const size_t wave = (blockIdx.x * (size_t)blockDim.x + threadIdx.x) >> 6;
     const size_t nwaves = (gridDim.x * (size_t)blockDim.x) >> 6;
-    for (size_t p = wave; p < n_out; p += nwaves) {
-        float *orow = out + p * (size_t)dpad;
-        if (p >= n) {
-            for (int d = lane; d < dpad; d += 64) orow[d] = pad_fill;
-            if (norm && lane == 0) norm[p] = pad_fill;
+    const int dim = a.dim, dpad = a.dpad;
+    for (size_t p = wave; p < a.n_out; p += nwaves) {
+        float *orow = a.out + p * (size_t)dpad;
+        float *rrow = a.raw_out ? a.raw_out + p * (size_t)dpad : nullptr;
+        if (p >= a.n) {
+            for (int d = lane; d < dpad; d += 64) {
+                orow[d] = a.pad_fill;
+                if (rrow) rrow[d] = a.pad_fill;
+            }
+            if (lane == 0) {
+                if (a.norm) a.norm[p] = a.pad_fill;
+                if (a.err) a.err[p] = 0.0f;
+            }
             continue;
         }
-        const size_t src = perm ? perm[p] : p;
-        const float *row = in + src * (size_t)dim;
+        const size_t src = a.perm ? a.perm[p] : p;
+        const float *row = a.in + src * (size_t)dim;
         float ss = 0.0f;
+        bool whole = true;
         for (int d = lane; d < dpad; d += 64) {
-            float v = d < dim ? row[d] : 0.0f;
-            if (transform) v = sqrtf(fabsf(v));
-            if (!normalize) orow[d] = v;
+            const float x = d < dim ? row[d] : 0.0f;
+            whole = whole && x == rintf(x);
+            if (rrow) rrow[d] = x;
+            float v = a.shift ? x - a.shift[d] : x;
+            if (a.transform) v = sqrtf(fabsf(v));
+            if (!a.normalize) orow[d] = v;
             ss = fmaf(v, v, ss);
         }
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
-        if (normalize) {
+        const bool row_int = __builtin_amdgcn_ballot_w64(!whole) == 0;
+        if (a.normalize) {
             const float nr = sqrtf(ss);
             const float inv = nr > 0.0f ? 1.0f / nr : 0.0f;
             for (int d = lane; d < dpad; d += 64) {
                 float v = d < dim ? row[d] : 0.0f;
-                if (transform) v = sqrtf(fabsf(v));
+                if (a.transform) v = sqrtf(fabsf(v));
                 orow[d] = v * inv;
             }
         }
-        if (norm_kind && lane == 0) norm[p] = norm_kind == 2 ? sqrtf(ss) : ss;
+        if (lane == 0) {
+            if (a.norm_kind && a.norm) a.norm[p] = a.norm_kind == 2 ? sqrtf(ss) : ss;
+            if (a.nonint && !row_int) atomicOr(a.nonint, 1u);
+            if (a.err) {
+                const bool ints = row_int && a.base_integral;
+                float e = 0.0f;
+                if (a.err_mode == 1) {
+                    const float r = sqrtf(ss) + sqrtf(a.err_nmax);
+                    e = (ints && r * r < 0x1.fep23f) ? 0.0f : a.err_coeff * r * r;
+                } else if (a.err_mode == 2) {
+                    const float r = sqrtf(ss) * sqrtf(a.err_nmax);
+                    e = (ints && r < 0x1.fep23f) ? 0.0f : a.err_coeff * r;
+                } else if (a.err_mode == 3) {
+                    e = a.err_coeff;
+                }
+                a.err[p] = e;
+            }
+        }
     }
+}
+
+void launch_rows_prep(const RowPrep &a, hipStream_t s) {
+    if (a.n_out == 0) return;
+    size_t blocks = (a.n_out + 3) / 4;
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL(k_rows_prep, dim3((unsigned)blocks), dim3(256), 0, s, a);
 }
 
 void launch_rows_prep(const float *in, size_t n, size_t n_out, int dim, int dpad, const uint32_t *perm, float *out,
                       float *norm, int norm_kind, int transform, int normalize, float pad_fill, hipStream_t s) {
-    if (n_out == 0) return;
-    size_t blocks = (n_out + 3) / 4;
-    if (blocks > 65536) blocks = 65536;
-    hipLaunchKernelGGL(k_rows_prep, dim3((unsigned)blocks), dim3(256), 0, s, in, n, n_out, dim, dpad, perm, out, norm,
-                       norm_kind, transform, normalize, pad_fill);
+    RowPrep a;
+    a.in = in;
+    a.n = n;
+    a.n_out = n_out;
+    a.dim = dim;
+    a.dpad = dpad;
+    a.perm = perm;
+    a.out = out;
+    a.norm = norm;
+    a.norm_kind = norm_kind;
+    a.transform = transform;
+    a.normalize = normalize;
+    a.pad_fill = pad_fill;
+    launch_rows_prep(a, s);
+}
+
+// ---------------------------------------------------------------------------------
+// Per-dimension shift (the column means): block b sums rows [b*chunk, ...) of every column in
+// double (thread t owns columns t, t + 256, ...), and flags non-integer values; one more kernel
+// adds the nparts partials per column in a fixed order.
+// ---------------------------------------------------------------------------------
+constexpr int kColParts = 512;
+int col_shift_parts() { return kColParts; }
+
+__global__ __launch_bounds__(256) void k_col_partial(const float *__restrict__ x, size_t n, int dim, size_t chunk,
+                                                     double *__restrict__ partial, uint32_t *__restrict__ nonint) {
+    const size_t r0 = blockIdx.x * chunk, r1 = min(n, r0 + chunk);
+    bool whole = true;
+    for (int d = threadIdx.x; d < dim; d += 256) {
+        // 8 rows in flight per step, each into its own accumulator
+        double s[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        size_t r = r0;
+        for (; r + 8 <= r1; r += 8) {
+            float v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = x[(r + j) * (size_t)dim + d];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                whole = whole && v[j] == rintf(v[j]);
+                s[j] += (double)v[j];
+            }
+        }
+        for (; r < r1; ++r) {
+            const float v = x[r * (size_t)dim + d];
+            whole = whole && v == rintf(v);
+            s[0] += (double)v;
+        }
+        partial[(size_t)blockIdx.x * dim + d] = ((s[0] + s[1]) + (s[2] + s[3])) + ((s[4] + s[5]) + (s[6] + s[7]));
+    }
+    if (!whole) atomicOr(nonint, 1u);
+}
+
+__global__ __launch_bounds__(256) void k_col_finish(const double *__restrict__ partial, size_t n, int dim, int dpad,
+                                                    const uint32_t *__restrict__ nonint, float *__restrict__ shift) {
+    const int d = blockIdx.x * blockDim.x + threadIdx.x;
+    if (d >= dpad) return;
+    if (d >= dim) {
+        shift[d] = 0.0f;
+        return;
+    }
+    double s = 0.0;
+    for (int b = 0; b < kColParts; ++b) s += partial[(size_t)b * dim + d];
+    const double m = s / (double)n;
+    shift[d] = *nonint ? (float)m : (float)rint(m);
+}
+
+void launch_col_shift(const float *x, size_t n, int dim, int dpad, double *partial, uint32_t *nonint, float *shift,
+                      hipStream_t s) {
+    const size_t chunk = (n + kColParts - 1) / kColParts;
+    hipLaunchKernelGGL(k_col_partial, dim3(kColParts), dim3(256), 0, s, x, n, dim, chunk, partial, nonint);
+    hipLaunchKernelGGL(k_col_finish, dim3((unsigned)((dpad + 255) / 256)), dim3(256), 0, s, partial, n, dim, dpad,
+                       nonint, shift);
 }
 
 // ---------------------------------------------------------------------------------
@@ -142,6 +238,13 @@ struct ScanArgs {
     float *inertia;
     int32_t *pos;
     int32_t *counts;
+    // ASSIGN certification: a point whose best and second-best scores lie within twice its
+    // selection error bound goes to the fix-up list (fix, nfix) instead of taking its ticket
+    float err_coeff;      // selection error coefficient (sel_err_coeff)
+    const float *cmax;    // device scalar: largest centroid norm value (cnorm units)
+    int32_t *fix;
+    uint32_t *nfix;
+    float *devmax;        // squared L2: per-cluster bound of |x_d - c_d| over its points
 };
 
 // -0.0 and +0.0 are the same distance; give them one key.
@@ -176,7 +279,7 @@ __device__ __forceinline__ void mfma_chunk(floatx16 (&acc)[2][2], const floatx4 
 struct EpiState {
     float tau_e[2], T[2], cn[2];  // FILTER: exact threshold, loose "may pass" threshold, column norm
     bool guard;                   // FILTER cosine: some column may meet a near-zero-norm row
-    float bs[2];                  // ASSIGN: running best (score, row)
+    float bs[2], bs2[2];          // ASSIGN: running best (score, row) and second-best score
     int bi[2];
 };
 
@@ -202,6 +305,7 @@ __device__ __forceinline__ void item_begin(EpiState &st, const ScanArgs &a, int 
             }
         } else if constexpr (MODE == kAssign) {
             st.bs[cb] = INFINITY;
+            st.bs2[cb] = INFINITY;
             st.bi[cb] = 0;
         }
     }
@@ -363,6 +467,37 @@ __device__ __forceinline__ void dense_stage(const floatx16 (&acc)[2][2], NF nf, 
     }
 }
 
+// Running best and second-best of a sequence: the quiet NaN of padding rows is ignored.
+__device__ __forceinline__ void second_min(float &m, float &m2, float u) {
+    m2 = fminf(m2, u < m ? m : u);
+    m = fminf(m, u);
+}
+// Folds a block's (best m, second m2) into the column's running state; `index` gives the block row
+// holding m.  Blocks come in ascending row order and the strict '<' keeps the earlier row on ties
+// (the tie then shows as a zero gap).
+template <class IDX>
+__device__ __forceinline__ void take_min(EpiState &st, int cb, float m, float m2, IDX index) {
+    if (m < st.bs[cb]) {
+        int idx;
+        const int row = index(idx);
+        st.bs2[cb] = fminf(st.bs[cb], m2);
+        st.bs[cb] = m;
+        st.bi[cb] = row;
+    } else {
+        st.bs2[cb] = fminf(st.bs2[cb], m);
+    }
+}
+// Combines another (best, second, row) triple into the column's state: lower score, then lower row.
+__device__ __forceinline__ void combine_best(EpiState &st, int cb, float os, float os2, int oi) {
+    if (os < st.bs[cb] || (os == st.bs[cb] && oi < st.bi[cb])) {
+        st.bs2[cb] = fminf(os2, st.bs[cb]);
+        st.bs[cb] = os;
+        st.bi[cb] = oi;
+    } else {
+        st.bs2[cb] = fminf(st.bs2[cb], os);
+    }
+}
+
 // ASSIGN: per column, the minimum score over this stage's 32 rows held by the lane, then the
 // first (lowest) row reaching it.  Rows are visited in ascending order with a strict '<' across
 // stages, so the lowest index wins ties (kmeans.cu:110-114).
@@ -370,7 +505,7 @@ template <int M, class NF>
 __device__ __forceinline__ void assign_stage(floatx16 (&acc)[2][2], NF nf, EpiState &st, int wr, int h, long rs) {
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb) {
-        float m = INFINITY;
+        float m = INFINITY, m2 = INFINITY;
 #pragma unroll
         for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
@@ -389,38 +524,38 @@ __device__ __forceinline__ void assign_stage(floatx16 (&acc)[2][2], NF nf, EpiSt
                         u = den > 1e-9f ? -(dot / den) : canon(0.0f * dot);
                     }
                     acc[rb][cb][4 * g + j] = u;
-                    m = fminf(m, u);
+                    second_min(m, m2, u);
                 }
             }
-        if (m < st.bs[cb]) {
-            int idx = 31;
+        take_min(st, cb, m, m2, [&](int &idx) {
+            idx = 31;
 #pragma unroll
             for (int r = 31; r >= 0; --r) idx = acc[r >> 4][cb][r & 15] == m ? r : idx;
-            st.bs[cb] = m;
-            st.bi[cb] = (int)rs + 64 * wr + 4 * h + 32 * (idx >> 4) + 8 * ((idx >> 2) & 3) + (idx & 3);
-        }
+            return (int)rs + 64 * wr + 4 * h + 32 * (idx >> 4) + 8 * ((idx >> 2) & 3) + (idx & 3);
+        });
     }
 }
 
 // ASSIGN item end: combine lanes l and l^32 (row halves) and the RW row waves, write the
-// outputs.  Must be called by all threads; contains a barrier.
+// outputs.  Must be called by all threads; contains a barrier.  A point is certified when its
+// second-best score exceeds the best by more than twice its selection error bound: then the
+// GEMM-form argmin is the argmin of the exact distances, and the point takes its ticket in its
+// cluster.  Otherwise (near-ties, or scores too coarse on badly conditioned data) it goes to the
+// fix-up list, whose direct-form pass assigns it.
 template <int M, int RW>
 __device__ __forceinline__ void assign_finish(EpiState &st, const ScanArgs &a, int col0, int wr, int wc, int l32,
-                                              int h, float *s_xs, int *s_xi) {
+                                              int h, float *s_xs, float *s_xs2, int *s_xi) {
 #pragma unroll
-    for (int cb = 0; cb < 2; ++cb) {
-        const float os = __shfl_xor(st.bs[cb], 32, 64);
-        const int oi = __shfl_xor(st.bi[cb], 32, 64);
-        if (os < st.bs[cb] || (os == st.bs[cb] && oi < st.bi[cb])) {
-            st.bs[cb] = os;
-            st.bi[cb] = oi;
-        }
-    }
+    for (int cb = 0; cb < 2; ++cb)
+        combine_best(st, cb, __shfl_xor(st.bs[cb], 32, 64), __shfl_xor(st.bs2[cb], 32, 64),
+                     __shfl_xor(st.bi[cb], 32, 64));
     if (wr > 0 && h == 0) {
 #pragma unroll
         for (int cb = 0; cb < 2; ++cb) {
-            s_xs[(wr - 1) * kTileCols + 64 * wc + 32 * cb + l32] = st.bs[cb];
-            s_xi[(wr - 1) * kTileCols + 64 * wc + 32 * cb + l32] = st.bi[cb];
+            const int o = (wr - 1) * kTileCols + 64 * wc + 32 * cb + l32;
+            s_xs[o] = st.bs[cb];
+            s_xs2[o] = st.bs2[cb];
+            s_xi[o] = st.bi[cb];
         }
     }
     __syncthreads();
@@ -429,23 +564,35 @@ __device__ __forceinline__ void assign_finish(EpiState &st, const ScanArgs &a, i
         for (int cb = 0; cb < 2; ++cb) {
 #pragma unroll
             for (int w = 0; w < RW - 1; ++w) {
-                const float os = s_xs[w * kTileCols + 64 * wc + 32 * cb + l32];
-                const int oi = s_xi[w * kTileCols + 64 * wc + 32 * cb + l32];
-                if (os < st.bs[cb] || (os == st.bs[cb] && oi < st.bi[cb])) {
-                    st.bs[cb] = os;
-                    st.bi[cb] = oi;
-                }
+                const int o = w * kTileCols + 64 * wc + 32 * cb + l32;
+                combine_best(st, cb, s_xs[o], s_xs2[o], s_xi[o]);
             }
             const int p = col0 + 64 * wc + 32 * cb + l32;
             if (p < a.ncols) {
                 const int c = st.bi[cb];
                 a.assign[p] = c;
-                float in;
-                if constexpr (M == L2) in = fmaxf(st.cn[cb] + st.bs[cb], 0.0f);  // + ||x||^2
-                else if constexpr (M == DOT) in = st.bs[cb];                     // -dot
-                else in = 1.0f + st.bs[cb];                                      // 1 - cos
-                a.inertia[p] = in;
-                a.pos[p] = atomicAdd(&a.counts[c], 1);
+                // selection error bound of this point's scores
+                float e;
+                if constexpr (M == L2) {
+                    const float r = sqrtf(st.cn[cb]) + sqrtf(*a.cmax);
+                    e = a.err_coeff * r * r;
+                } else if constexpr (M == DOT) {
+                    e = a.err_coeff * sqrtf(st.cn[cb]) * sqrtf(*a.cmax);
+                } else {
+                    e = a.err_coeff;
+                }
+                if (!(st.bs2[cb] - st.bs[cb] > 2.0f * e)) {
+                    a.fix[atomicAdd(a.nfix, 1u)] = p;
+                } else {
+                    if constexpr (M == L2) {
+                        // |x_d - c_d| <= ||x - c|| <= sqrt(score + error)
+                        const float d = fmaxf(st.cn[cb] + st.bs[cb], 0.0f) + e;
+                        atomicMax((uint32_t *)a.devmax + c, __float_as_uint(sqrtf(d) * 1.0001f));
+                    } else {
+                        a.inertia[p] = M == DOT ? st.bs[cb] : 1.0f + st.bs[cb];  // -dot, 1 - cos
+                    }
+                    a.pos[p] = atomicAdd(&a.counts[c], 1);
+                }
             }
         }
     }
@@ -477,6 +624,7 @@ __global__ __launch_bounds__(256, 2) void k_mfma_stream(ScanArgs a) {
     __shared__ uint32_t s_qcnt[MODE == kFilter ? kTileCols : 1];
     __shared__ uint2 s_slot[MODE == kFilter ? kTileCols * kStrSlots : 1];
     __shared__ float s_xs[MODE == kAssign ? (RW - 1) * kTileCols : 1];
+    __shared__ float s_xs2[MODE == kAssign ? (RW - 1) * kTileCols : 1];
     __shared__ int s_xi[MODE == kAssign ? (RW - 1) * kTileCols : 1];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -571,7 +719,7 @@ __global__ __launch_bounds__(256, 2) void k_mfma_stream(ScanArgs a) {
             dense_stage<M>(acc, nf, st, a, wr, wc, l32, h, rs, col0);
         } else {
             assign_stage<M>(acc, nf, st, wr, h, rs);
-            if (item_end) assign_finish<M, RW>(st, a, col0, wr, wc, l32, h, s_xs, s_xi);
+            if (item_end) assign_finish<M, RW>(st, a, col0, wr, wc, l32, h, s_xs, s_xs2, s_xi);
         }
 
         if (!more) break;
@@ -603,6 +751,7 @@ __global__ __launch_bounds__(512, 1) void k_mfma_pnl(ScanArgs a) {
     __shared__ uint32_t s_qcnt[MODE == kFilter ? kTileCols : 1];
     __shared__ uint2 s_slot[MODE == kFilter ? kTileCols * kPnlSlots : 1];
     __shared__ float s_xs[MODE == kAssign ? (RW - 1) * kTileCols : 1];
+    __shared__ float s_xs2[MODE == kAssign ? (RW - 1) * kTileCols : 1];
     __shared__ int s_xi[MODE == kAssign ? (RW - 1) * kTileCols : 1];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -736,7 +885,7 @@ __global__ __launch_bounds__(512, 1) void k_mfma_pnl(ScanArgs a) {
             dense_stage<M>(acc, nf, st, a, wr, wc, l32, h, rs, col0);
         } else {
             assign_stage<M>(acc, nf, st, wr, h, rs);
-            if (item_end) assign_finish<M, RW>(st, a, col0, wr, wc, l32, h, s_xs, s_xi);
+            if (item_end) assign_finish<M, RW>(st, a, col0, wr, wc, l32, h, s_xs, s_xs2, s_xi);
         }
 
         if (!more) break;
@@ -872,7 +1021,7 @@ template <int M>
 __device__ __forceinline__ void assign_half(floatx16 (&acc2)[2], const floatx4 (&n)[4], EpiState &st, long rb0) {
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb) {
-        float m = INFINITY;
+        float m = INFINITY, m2 = INFINITY;
 #pragma unroll
         for (int g = 0; g < 4; ++g)
 #pragma unroll
@@ -888,15 +1037,14 @@ __device__ __forceinline__ void assign_half(floatx16 (&acc2)[2], const floatx4 (
                     u = den > 1e-9f ? -(dot / den) : canon(0.0f * dot);
                 }
                 acc2[cb][4 * g + j] = u;
-                m = fminf(m, u);
+                second_min(m, m2, u);
             }
-        if (m < st.bs[cb]) {
-            int idx = 15;
+        take_min(st, cb, m, m2, [&](int &idx) {
+            idx = 15;
 #pragma unroll
             for (int r = 15; r >= 0; --r) idx = acc2[cb][r] == m ? r : idx;
-            st.bs[cb] = m;
-            st.bi[cb] = (int)rb0 + 8 * (idx >> 2) + (idx & 3);
-        }
+            return (int)rb0 + 8 * (idx >> 2) + (idx & 3);
+        });
     }
 }
 
@@ -910,6 +1058,7 @@ __global__ __launch_bounds__(512, 1) void k_mfma_hs(ScanArgs a) {
     __shared__ uint32_t s_qcnt[MODE == kFilter ? kTileCols : 1];
     __shared__ uint2 s_slot[MODE == kFilter ? kTileCols * kRegSlots : 1];
     __shared__ float s_xs[MODE == kAssign ? (RW - 1) * kTileCols : 1];
+    __shared__ float s_xs2[MODE == kAssign ? (RW - 1) * kTileCols : 1];
     __shared__ int s_xi[MODE == kAssign ? (RW - 1) * kTileCols : 1];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1091,7 +1240,7 @@ __global__ __launch_bounds__(512, 1) void k_mfma_hs(ScanArgs a) {
             // drain: this stage's half 1, then the item's cross-wave work
             epi(acc[1], nrm[1], rs, 1, 0, 4, true);
             if constexpr (MODE == kFilter) filter_flush<kRegSlots>(a, col0, r_lo, s_qcnt, s_slot);
-            else if constexpr (MODE == kAssign) assign_finish<M, RW>(st, a, col0, wr, wc, l32, h, s_xs, s_xi);
+            else if constexpr (MODE == kAssign) assign_finish<M, RW>(st, a, col0, wr, wc, l32, h, s_xs, s_xs2, s_xi);
             if (!more) break;
             // every wave is past this item's MFMAs (barrier in the flush / combine above; DENSE
             // has none, so take one here)
@@ -1177,7 +1326,7 @@ void launch_gemm_filter(int metric, bool dense, long item_rows, const float *bas
 
 void launch_kmeans_assign(int metric, const float *cent, const float *cnorm, int kpad, const float *pts,
                           const float *pnorm, int n, int dpad, int32_t *assign, float *inertia, int32_t *pos,
-                          int32_t *counts, int grid_cap, hipStream_t s) {
+                          int32_t *counts, const AssignCert &cert, int grid_cap, hipStream_t s) {
     if (n <= 0 || kpad <= 0) return;
     ScanArgs a{};
     a.A = cent;
@@ -1195,6 +1344,11 @@ void launch_kmeans_assign(int metric, const float *cent, const float *cnorm, int
     a.inertia = inertia;
     a.pos = pos;
     a.counts = counts;
+    a.err_coeff = cert.err_coeff;
+    a.cmax = cert.cmax;
+    a.fix = cert.fix;
+    a.nfix = cert.nfix;
+    a.devmax = cert.devmax;
     launch_metric<kAssign>(metric, a, grid_cap, s);
 }
 

@@ -2,8 +2,9 @@
 // filter of the round/merge top-k (topk.hip).
 //
 // Replaces the metric switch of knn_compute_distance_matrix (vector-cuda/src/kernels/knn.cu:84-141,
-// 175-195) for L1, Minkowski p=3, L-inf, thresholded Hamming, Mahalanobis (sqrt of direct
-// L2), weighted Jaccard and Hellinger (direct L2 of sqrt|x|, then sqrt(0.5 * sum)).  Each lane owns
+// 175-195) for squared L2 in direct form (the fallback of the GEMM-form L2 search), L1,
+// Minkowski p=3, L-inf, thresholded Hamming, Mahalanobis (sqrt of direct L2), weighted Jaccard
+// and Hellinger (direct L2 of sqrt|x|, then sqrt(0.5 * sum)).  Each lane owns
 // one query held in registers; a workgroup of 256 lanes streams tiles of base rows through LDS and
 // every wave reads each base element as a broadcast ds_read_b128 (all lanes the same address), so a
 // base element costs two VALU operations per query (sub + add/max with the |x| modifier).  Values
@@ -41,6 +42,11 @@ __device__ __forceinline__ void accum(float &a, float &b, float q, float x) {
         a = fmaf(d * d, d, a);
     } else if constexpr (M == HAMF) {
         a += fabsf(q - x) > 1e-6f ? 1.0f : 0.0f;
+    } else if constexpr (M == DOT) {
+        a = fmaf(q, x, a);
+    } else if constexpr (M == COS) {  // dot product and the row's squared norm
+        a = fmaf(q, x, a);
+        b = fmaf(x, x, b);
     } else {  // JACC: q holds |q|
         const float ax = fabsf(x);
         a += fminf(q, ax);
@@ -160,6 +166,8 @@ void launch_valu_filter(int metric, const float *base, const float *qry, const f
     const dim3 g((unsigned)grid);
     const int it = (int)items;
     switch (metric) {
+        // squared L2 in direct form: the certified fallback of the GEMM-form L2 search
+        case L2: launch_m<L2>(dpad, g, s, base, qry, tau, nq, row_begin, row_end, nqt, it, item_rows, cand, cnt, cap); break;
         case L1: launch_m<L1>(dpad, g, s, base, qry, tau, nq, row_begin, row_end, nqt, it, item_rows, cand, cnt, cap); break;
         case MINK: launch_m<MINK>(dpad, g, s, base, qry, tau, nq, row_begin, row_end, nqt, it, item_rows, cand,
                                           cnt, cap); break;
@@ -250,6 +258,151 @@ __global__ __launch_bounds__(256) void k_kmeans_assign_valu(const float *__restr
             pos[p] = atomicAdd(&counts[bi], 1);
         }
     }
+}
+
+// ---------------------------------------------------------------------------------
+// Fix-up of the MFMA k-means assignment: the points whose GEMM-form argmin could not be
+// certified get the argmin of the direct-form metric over all centroids (squared L2 sum (x-c)^2,
+// dot product, cosine dot / (sqrt(|x|^2) sqrt(|c|^2)) with the 1e-9 guard: the formulas of
+// scalar.rs:14-75 and kmeans.cu:87-170) on the unshifted points and centroids.  A work item is a
+// tile of 256 listed points (one per lane, in registers) times a chunk of kFixChunk centroids
+// (tiles broadcast from LDS); the chunk's best (score key, centroid) is folded into best[i] with
+// a 64-bit atomic min, so the result is the lowest score and then the lowest index, whatever the
+// order of the items.
+// ---------------------------------------------------------------------------------
+constexpr int kFixChunk = 256;
+
+__global__ void k_fix_init(const uint32_t *__restrict__ nfix, unsigned long long *__restrict__ best) {
+    const uint32_t nf = *nfix;
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < nf; i += gridDim.x * blockDim.x) best[i] = ~0ull;
+}
+
+template <int M, int DC>
+__global__ __launch_bounds__(256) void k_fix_argmin(const float *__restrict__ pts, int dpad,
+                                                    const int32_t *__restrict__ fix, const uint32_t *__restrict__ nfix,
+                                                    const float *__restrict__ cent, int k,
+                                                    unsigned long long *__restrict__ best) {
+    constexpr int V4 = DC / 4;
+    __shared__ floatx4 tile[kValuRows * V4];
+    const int tid = threadIdx.x;
+    const int nchunks = (dpad + DC - 1) / DC;
+    const int nf = (int)*nfix;
+    const int n_tiles = (nf + 255) / 256, n_cchunks = (k + kFixChunk - 1) / kFixChunk;
+    const int items = n_tiles * n_cchunks;
+    for (int item = blockIdx.x; item < items; item += gridDim.x) {
+        const int t = item % n_tiles, cc = item / n_tiles;
+        const int i = t * 256 + tid;
+        const bool pv = i < nf;
+        const float *prow = pts + (size_t)(pv ? fix[i] : 0) * dpad;
+        float pr[DC];
+        auto load_p = [&](int c) {
+#pragma unroll
+            for (int u = 0; u < V4; ++u) {
+                const int d = c * DC + 4 * u;
+                const floatx4 v = d < dpad ? *(const floatx4 *)(prow + d) : floatx4{0, 0, 0, 0};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) pr[4 * u + j] = v[j];
+            }
+        };
+        float pn = 0.0f;  // the point's squared norm (cosine)
+        if constexpr (M == COS) {
+            for (int c = 0; c < nchunks; ++c) {
+                load_p(c);
+#pragma unroll
+                for (int j = 0; j < DC; ++j) pn = fmaf(pr[j], pr[j], pn);
+            }
+        }
+        if (nchunks == 1) load_p(0);
+        const int c0 = cc * kFixChunk, c1 = min(k, c0 + kFixChunk);
+        float bv = INFINITY;
+        int bc = c0;
+        for (int cs = c0; cs < c1; cs += kValuRows) {
+            float a[kValuRows], b[kValuRows];
+#pragma unroll
+            for (int r = 0; r < kValuRows; ++r) a[r] = b[r] = 0.0f;
+            for (int c = 0; c < nchunks; ++c) {
+                if (nchunks > 1) load_p(c);
+                __syncthreads();
+                for (int e = tid; e < kValuRows * V4; e += 256) {
+                    const int row = e / V4, c4 = e % V4;
+                    const int r = cs + row;
+                    const int d = c * DC + 4 * c4;
+                    tile[e] = (r < c1 && d < dpad) ? *(const floatx4 *)(cent + (long)r * dpad + d)
+                                                   : floatx4{0, 0, 0, 0};
+                }
+                __syncthreads();
+#pragma unroll
+                for (int r = 0; r < kValuRows; ++r) {
+#pragma unroll
+                    for (int u = 0; u < V4; ++u) {
+                        const floatx4 x = tile[r * V4 + u];
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) accum<M>(a[r], b[r], pr[4 * u + j], x[j]);
+                    }
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < kValuRows; ++r) {
+                float v;
+                if constexpr (M == L2) {
+                    v = a[r];
+                } else if constexpr (M == DOT) {
+                    v = -a[r] + 0.0f;
+                } else {
+                    const float den = sqrtf(pn) * sqrtf(b[r]);
+                    v = den <= 1e-9f ? 0.0f : -(a[r] / den) + 0.0f;
+                }
+                if (v < bv && cs + r < c1) {
+                    bv = v;
+                    bc = cs + r;
+                }
+            }
+        }
+        if (pv && c0 < c1) atomicMin(best + i, ((unsigned long long)score_key(bv) << 32) | (uint32_t)bc);
+    }
+}
+
+// Assignment, ticket and inertia (-dot, 1 - cos; squared L2 leaves it to the update) of the fixed
+// points; squared L2 also raises its cluster's deviation bound.
+__global__ void k_fix_finish(int metric, const uint32_t *__restrict__ nfix, const int32_t *__restrict__ fix,
+                             const unsigned long long *__restrict__ best, int32_t *__restrict__ assign,
+                             float *__restrict__ inertia, int32_t *__restrict__ pos, int32_t *__restrict__ counts,
+                             float *__restrict__ devmax) {
+    const uint32_t nf = *nfix;
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < nf; i += gridDim.x * blockDim.x) {
+        const unsigned long long e = best[i];
+        const int p = fix[i], c = (int)(uint32_t)e;
+        const float v = key_score((uint32_t)(e >> 32));
+        assign[p] = c;
+        pos[p] = atomicAdd(&counts[c], 1);
+        if (metric == L2) atomicMax((uint32_t *)devmax + c, __float_as_uint(sqrtf(fmaxf(v, 0.0f)) * 1.0001f));
+        else inertia[p] = metric == DOT ? v : 1.0f + v;
+    }
+}
+
+void launch_kmeans_fix(int metric, const float *pts, int dpad, const int32_t *fix, const uint32_t *nfix,
+                       const float *cent, int k, unsigned long long *best, int32_t *assign, float *inertia,
+                       int32_t *pos, int32_t *counts, float *devmax, int grid_cap, hipStream_t s) {
+    if (k <= 0) return;
+    hipLaunchKernelGGL(k_fix_init, dim3(64), dim3(256), 0, s, nfix, best);
+    const dim3 g(grid_cap), b(256);
+    const bool wide = dpad <= 128 && dpad > 64;
+    switch (metric) {
+        case L2:
+            if (wide) hipLaunchKernelGGL((k_fix_argmin<L2, 128>), g, b, 0, s, pts, dpad, fix, nfix, cent, k, best);
+            else hipLaunchKernelGGL((k_fix_argmin<L2, 64>), g, b, 0, s, pts, dpad, fix, nfix, cent, k, best);
+            break;
+        case DOT:
+            if (wide) hipLaunchKernelGGL((k_fix_argmin<DOT, 128>), g, b, 0, s, pts, dpad, fix, nfix, cent, k, best);
+            else hipLaunchKernelGGL((k_fix_argmin<DOT, 64>), g, b, 0, s, pts, dpad, fix, nfix, cent, k, best);
+            break;
+        default:
+            if (wide) hipLaunchKernelGGL((k_fix_argmin<COS, 128>), g, b, 0, s, pts, dpad, fix, nfix, cent, k, best);
+            else hipLaunchKernelGGL((k_fix_argmin<COS, 64>), g, b, 0, s, pts, dpad, fix, nfix, cent, k, best);
+            break;
+    }
+    hipLaunchKernelGGL(k_fix_finish, dim3(64), dim3(256), 0, s, metric, nfix, fix, best, assign, inertia, pos, counts,
+                       devmax);
 }
 
 template <int M>

@@ -13,6 +13,7 @@ namespace vh {
 namespace {
 thread_local std::string t_err;
 thread_local size_t t_req = 0, t_avail = 0;
+thread_local int t_ordinal = -1;
 }  // namespace
 
 int set_error(int code, const std::string &msg) {
@@ -47,14 +48,18 @@ int open_device(int ordinal) {
         (void)hipGetLastError();
         return set_error(VHIP_ERR_HARDWARE_NOT_AVAILABLE, "No HIP-capable GPU hardware devices found on this system");
     }
-    if (ordinal < 0 || ordinal >= n)
+    if (ordinal < 0 || ordinal >= n) {
+        t_ordinal = ordinal;
         return set_error(VHIP_ERR_DEVICE_NOT_FOUND,
                          "HIP device with ordinal " + std::to_string(ordinal) + " was not found");
+    }
     hipDeviceProp_t p;
     VH_HIP(hipGetDeviceProperties(&p, ordinal));
-    if (std::strncmp(p.gcnArchName, "gfx950", 6) != 0)
+    if (std::strncmp(p.gcnArchName, "gfx950", 6) != 0) {
+        t_ordinal = ordinal;
         return set_error(VHIP_ERR_DEVICE_NOT_FOUND, "HIP device " + std::to_string(ordinal) + " is " +
                                                        p.gcnArchName + ", this library is built for gfx950");
+    }
     VH_HIP(hipSetDevice(ordinal));
     return VHIP_OK;
 }
@@ -336,6 +341,8 @@ using namespace vh;
 extern "C" {
 
 const char *vhip_last_error(void) { return t_err.c_str(); }
+
+int vhip_last_error_ordinal(void) { return t_ordinal; }
 
 void vhip_last_error_devices(size_t *requested, size_t *available) {
     if (requested) *requested = t_req;

@@ -101,12 +101,13 @@ __device__ __forceinline__ uint32_t block_reduce_u32(uint32_t v, bool is_max, ui
     return v;
 }
 
-// buf holds `bufn` u64 entries (dynamic LDS, bufn >= 2 * pow2(k), >= kMergeDirect).
-__global__ __launch_bounds__(256) void k_topk_merge(int k, int bufn, const uint2 *__restrict__ cand,
+// buf holds `bufn` u64 entries (dynamic LDS, bufn >= 2 * pow2(kc), >= kMergeDirect).
+__global__ __launch_bounds__(256) void k_topk_merge(int k, int kc, int bufn, const uint2 *__restrict__ cand,
                                                     uint32_t *__restrict__ cnt, int cap,
                                                     const uint32_t *__restrict__ perm, u64 *__restrict__ topk,
                                                     uint32_t *__restrict__ have, float *__restrict__ tau,
-                                                    uint32_t *__restrict__ flags, uint32_t *__restrict__ nflagged) {
+                                                    uint32_t *__restrict__ flags, uint32_t *__restrict__ nflagged,
+                                                    const float *__restrict__ qerr, uint32_t *__restrict__ mflag) {
     extern __shared__ u64 buf[];
     __shared__ uint32_t hist[kMergeBins];
     __shared__ uint32_t red[8];
@@ -119,9 +120,12 @@ __global__ __launch_bounds__(256) void k_topk_merge(int k, int bufn, const uint2
         if (tid == 0) cnt[q] = 0;
         return;
     }
+    // entries to keep: k, or kc when the scores carry a selection error
+    const float e2 = qerr ? 2.0f * qerr[q] : 0.0f;
+    const uint32_t kk = e2 > 0.0f ? (uint32_t)kc : (uint32_t)k;
     const bool overflow = c_all > (uint32_t)cap;
     const uint32_t c = overflow ? (uint32_t)cap : c_all;
-    u64 *tk = topk + (size_t)q * k;
+    u64 *tk = topk + (size_t)q * kc;
     const uint2 *cq = cand + (size_t)q * cap;
     const uint32_t h = have[q];
     const uint32_t T = h + c;
@@ -132,9 +136,9 @@ __global__ __launch_bounds__(256) void k_topk_merge(int k, int bufn, const uint2
         return ((u64)e.x << 32) | (u64)perm[e.y];  // base position -> vector id
     };
 
-    uint32_t hn = 0;  // entries of the new top-k, sorted in buf[0 .. hn)
+    uint32_t hn = 0;  // entries of the new kept list, sorted in buf[0 .. hn)
     bool done = false;
-    if (T > (uint32_t)kMergeDirect && T > (uint32_t)k) {
+    if (T > (uint32_t)kMergeDirect && T > kk) {
         // ---- bucket select ----
         uint32_t lo = 0xffffffffu, hi = 0u;
         for (uint32_t i = tid; i < T; i += 256) {
@@ -151,7 +155,7 @@ __global__ __launch_bounds__(256) void k_topk_merge(int k, int bufn, const uint2
             __syncthreads();
             for (uint32_t i = tid; i < T; i += 256) atomicAdd(&hist[bucket(key32(i))], 1u);
             __syncthreads();
-            // bucket b* holding the k-th smallest: cum(b*) < k <= cum(b*) + hist[b*]
+            // bucket b* holding the kk-th smallest: cum(b*) < kk <= cum(b*) + hist[b*]
             constexpr int per = kMergeBins / 256;
             uint32_t loc = 0;
 #pragma unroll
@@ -168,7 +172,7 @@ __global__ __launch_bounds__(256) void k_topk_merge(int k, int bufn, const uint2
 #pragma unroll
             for (int j = 0; j < per; ++j) {
                 const uint32_t hb = hist[tid * per + j];
-                if (cum < (uint32_t)k && (uint32_t)k <= cum + hb) {
+                if (cum < kk && kk <= cum + hb) {
                     s_sel[0] = (uint32_t)(tid * per + j);
                     s_sel[1] = cum;
                 }
@@ -194,13 +198,13 @@ __global__ __launch_bounds__(256) void k_topk_merge(int k, int bufn, const uint2
                 for (uint32_t i = total + tid; i < (uint32_t)P; i += 256) buf[i] = ~0ull;
                 __syncthreads();
                 bitonic_sort_lds(buf, P);
-                hn = (uint32_t)k;
+                hn = kk;
                 done = true;
             }
         }
     }
     if (!done) {
-        // ---- sort everything, in chunks against the running best k ----
+        // ---- sort everything, in chunks against the running best kk ----
         uint32_t hh = 0, next = 0;
         while (next < T || hh == 0) {
             const uint32_t take = min(T - next, (uint32_t)bufn - hh);
@@ -211,7 +215,7 @@ __global__ __launch_bounds__(256) void k_topk_merge(int k, int bufn, const uint2
             for (uint32_t i = total + tid; i < (uint32_t)P; i += 256) buf[i] = ~0ull;
             __syncthreads();
             bitonic_sort_lds(buf, P);
-            hh = min(total, (uint32_t)k);
+            hh = min(total, kk);
             next += take;
             if (next >= T) break;
         }
@@ -228,28 +232,107 @@ __global__ __launch_bounds__(256) void k_topk_merge(int k, int bufn, const uint2
             flags[q] = 1;
             tau[q] = -INFINITY;
             atomicAdd(nflagged, 1u);
+        } else if (hn < (uint32_t)k) {
+            tau[q] = INFINITY;
+            if (mflag) mflag[q] = 0;
         } else {
-            tau[q] = hn >= (uint32_t)k ? key_score((uint32_t)(buf[k - 1] >> 32)) : INFINITY;
+            // Later rows can only matter when they score within the margin of the k-th; once
+            // kk entries are kept, also only when they beat the kk-th.
+            const float sk = key_score((uint32_t)(buf[k - 1] >> 32));
+            float t = sk + e2;
+            bool cut = false;
+            if (kk > (uint32_t)k && hn >= kk) {
+                const float skk = key_score((uint32_t)(buf[kk - 1] >> 32));
+                cut = skk <= t;
+                t = fminf(t, skk);
+            }
+            tau[q] = t;
+            if (mflag) mflag[q] = cut ? 1u : 0u;
         }
     }
 }
 
-int merge_buffer_entries(int k) {
+int merge_buffer_entries(int kc) {
     int p = 1;
-    while (p < k) p <<= 1;
+    while (p < kc) p <<= 1;
     return std::max(2 * p, 1024);
 }
 
-void launch_topk_merge(int nq, int k, const uint2 *cand, uint32_t *cnt, int cap, const uint32_t *perm,
+void launch_topk_merge(int nq, int k, int kc, const uint2 *cand, uint32_t *cnt, int cap, const uint32_t *perm,
                        unsigned long long *topk, uint32_t *have, float *tau, uint32_t *flags, uint32_t *nflagged,
-                       hipStream_t s) {
+                       const float *qerr, uint32_t *mflag, hipStream_t s) {
     if (nq <= 0) return;
-    const int bufn = merge_buffer_entries(k);
-    hipLaunchKernelGGL(k_topk_merge, dim3(nq), dim3(256), (size_t)bufn * sizeof(u64), s, k, bufn, cand, cnt, cap,
-                       perm, topk, have, tau, flags, nflagged);
+    const int bufn = merge_buffer_entries(kc);
+    const size_t lds = (size_t)bufn * sizeof(u64);
+    static bool attr_set = false;
+    if (!attr_set && lds > 65536) {
+        // more than 64 KB of dynamic LDS (gfx950 offers 160 KB per workgroup)
+        (void)hipFuncSetAttribute((const void *)k_topk_merge, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  (int)(merge_buffer_entries(kMaxKeep) * sizeof(u64)));
+        (void)hipGetLastError();
+        attr_set = true;
+    }
+    hipLaunchKernelGGL(k_topk_merge, dim3(nq), dim3(256), lds, s, k, kc, bufn, cand, cnt, cap, perm, topk, have, tau,
+                       flags, nflagged, qerr, mflag);
 }
 
-__global__ void k_topk_finalize(int nq, int k, int kout, int metric, const u64 *__restrict__ topk,
+__global__ void k_count_flags(const uint32_t *__restrict__ flags, int n, uint32_t *__restrict__ count) {
+    __shared__ uint32_t red[4];
+    uint32_t c = 0;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) c += flags[i] != 0;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) c += __shfl_xor(c, o, 64);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = c;
+    __syncthreads();
+    if (threadIdx.x == 0) *count = red[0] + red[1] + red[2] + red[3];
+}
+
+void launch_count_flags(const uint32_t *flags, int n, uint32_t *count, hipStream_t s) {
+    hipLaunchKernelGGL(k_count_flags, dim3(1), dim3(256), 0, s, flags, n, count);
+}
+
+// Row r of a re-run batch (kept entries at stride ks, count, margin flag) back into query idx[r]
+// of the main batch (stride kd >= the entries copied).  A null src_mflag clears the flag.
+__global__ __launch_bounds__(256) void k_scatter_topk(const u64 *__restrict__ src, int ks,
+                                                      const uint32_t *__restrict__ src_have,
+                                                      const uint32_t *__restrict__ src_mflag,
+                                                      const uint32_t *__restrict__ idx, u64 *__restrict__ dst, int kd,
+                                                      uint32_t *__restrict__ dst_have,
+                                                      uint32_t *__restrict__ dst_mflag) {
+    const int r = blockIdx.x;
+    const uint32_t q = idx[r];
+    const uint32_t h = min(src_have[r], (uint32_t)min(ks, kd));
+    for (uint32_t j = threadIdx.x; j < h; j += blockDim.x) dst[(size_t)q * kd + j] = src[(size_t)r * ks + j];
+    if (threadIdx.x == 0) {
+        dst_have[q] = h;
+        dst_mflag[q] = src_mflag ? src_mflag[r] : 0u;
+    }
+}
+
+void launch_scatter_topk(const unsigned long long *src, int ks, const uint32_t *src_have, const uint32_t *src_mflag,
+                         const uint32_t *idx, int m, unsigned long long *dst, int kd, uint32_t *dst_have,
+                         uint32_t *dst_mflag, hipStream_t s) {
+    if (m <= 0) return;
+    hipLaunchKernelGGL(k_scatter_topk, dim3(m), dim3(256), 0, s, src, ks, src_have, src_mflag, idx, dst, kd, dst_have,
+                       dst_mflag);
+}
+
+__global__ __launch_bounds__(256) void k_gather_rows(const float *__restrict__ src, const uint32_t *__restrict__ idx,
+                                                     size_t rows, int width, float *__restrict__ dst) {
+    const size_t total = rows * (size_t)width;
+    for (size_t t = blockIdx.x * 256 + threadIdx.x; t < total; t += (size_t)gridDim.x * 256) {
+        const size_t r = t / width, c = t - r * width;
+        dst[t] = src[(size_t)idx[r] * width + c];
+    }
+}
+
+void launch_gather_rows(const float *src, const uint32_t *idx, size_t rows, int width, float *dst, hipStream_t s) {
+    if (rows == 0) return;
+    const unsigned blocks = (unsigned)std::min<size_t>(4096, (rows * width + 255) / 256);
+    hipLaunchKernelGGL(k_gather_rows, dim3(blocks), dim3(256), 0, s, src, idx, rows, width, dst);
+}
+
+__global__ void k_topk_finalize(int nq, int kc, int kout, int metric, const u64 *__restrict__ topk,
                                 const uint32_t *__restrict__ have, uint32_t *__restrict__ out_ids,
                                 float *__restrict__ out_dist, uint32_t *__restrict__ out_dist_u32, int ostride) {
     const long i = blockIdx.x * (long)blockDim.x + threadIdx.x;
@@ -257,7 +340,7 @@ __global__ void k_topk_finalize(int nq, int k, int kout, int metric, const u64 *
     const int q = (int)(i / kout), j = (int)(i % kout);
     const size_t o = (size_t)q * ostride + j;
     if ((uint32_t)j < have[q]) {
-        const u64 e = topk[(size_t)q * k + j];
+        const u64 e = topk[(size_t)q * kc + j];
         const float sc = key_score((uint32_t)(e >> 32));
         const float d = (metric == DOT || metric == COS) ? -sc + 0.0f : sc;
         out_ids[o] = (uint32_t)e;
@@ -270,42 +353,58 @@ __global__ void k_topk_finalize(int nq, int k, int kout, int metric, const u64 *
     }
 }
 
-void launch_topk_finalize(int nq, int k, int kout, int metric, const unsigned long long *topk,
+void launch_topk_finalize(int nq, int kc, int kout, int metric, const unsigned long long *topk,
                           const uint32_t *have, uint32_t *out_ids, float *out_dist, uint32_t *out_dist_u32,
                           int ostride, hipStream_t s) {
     const long total = (long)nq * kout;
     if (total <= 0) return;
-    hipLaunchKernelGGL(k_topk_finalize, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, nq, k, kout, metric,
+    hipLaunchKernelGGL(k_topk_finalize, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, nq, kc, kout, metric,
                        topk, have, out_ids, out_dist, out_dist_u32, ostride);
 }
 
-// Final pass for the GEMM-form metrics: the selection used ||q||^2 + ||x||^2 - 2 q.x, whose
-// cancellation error grows with the norms.  For each kept neighbour the distance is
-// recomputed in the direct form of the reference CPU engine (sum (q-x)^2, sum q*x, or
-// dot / (sqrt(|q|^2) sqrt(|x|^2)) with the 1e-9 guard, scalar.rs:14-75), the k entries are
-// re-sorted by (distance, id), and written out.  One workgroup per query: its threads first
-// fetch every kept neighbour's id and stored row at once (the id -> row lookup is a dependent
-// load), then groups of 16 lanes evaluate one neighbour each, 16 at a time, with float4 reads of
-// the row and the query (lane s sums pieces s, s + 16, ... in order) and a fixed xor butterfly.
-__global__ __launch_bounds__(256) void k_topk_refine(int k, int kout, int metric, const float *__restrict__ qpad,
-                                                     const float *__restrict__ base,
+// Final pass for the GEMM-form metrics.  The selection used the GEMM-form score (the norm form
+// ||q'||^2 + ||x'||^2 - 2 q'.x' of shifted operands for squared L2, the dot product of normalised
+// rows for cosine), which differs from the reference CPU engine's direct form by at most the
+// query's selection error bound; the kept entries hold every row within twice that bound of the
+// k-th.  For each of them the distance is recomputed in the direct form (sum (q-x)^2 of the
+// unshifted operands, sum q*x, or dot / (sqrt(|q|^2) sqrt(|x|^2)) with the 1e-9 guard,
+// scalar.rs:14-75), the entries are re-sorted by (distance, id), and the best k written out.
+// One workgroup per query: its threads first fetch every kept neighbour's id and stored row at
+// once (the id -> row lookup is a dependent load), then groups of 16 lanes evaluate one neighbour
+// each, 16 at a time, with float4 reads of the row and the query (lane s sums pieces s, s + 16,
+// ... in order) and a fixed xor butterfly.
+__global__ __launch_bounds__(256) void k_topk_refine(int k, int kc, int kout, int metric,
+                                                     const float *__restrict__ qrows, const float *__restrict__ base,
                                                      const uint32_t *__restrict__ inv_perm, int dpad,
                                                      const float *__restrict__ qnorm, const float *__restrict__ bnorm,
                                                      const u64 *__restrict__ topk, const uint32_t *__restrict__ have,
-                                                     uint32_t *__restrict__ out_ids, float *__restrict__ out_dist,
-                                                     int ostride) {
-    __shared__ u64 buf[kMaxK];
-    __shared__ uint32_t s_row[kMaxK];
+                                                     const float *__restrict__ qerr, uint32_t *__restrict__ out_ids,
+                                                     float *__restrict__ out_dist, int ostride) {
+    __shared__ u64 buf[2 * kMaxK];  // a power of two >= kMaxKeep
+    __shared__ uint32_t s_row[kMaxKeep];
+    __shared__ int s_h;
     const int q = blockIdx.x, tid = threadIdx.x;
-    const int h = (int)have[q];
+    const u64 *tq = topk + (size_t)q * kc;
+    const int h_all = (int)have[q];
+    if (tid == 0) s_h = h_all;
+    __syncthreads();
+    if (h_all > k && qerr) {
+        // entries past the k-th count while their score is within the margin of the k-th (the
+        // list is sorted by score)
+        const float lim = key_score((uint32_t)(tq[k - 1] >> 32)) + 2.0f * qerr[q];
+        for (int j = k + tid; j < h_all; j += 256)
+            if (key_score((uint32_t)(tq[j] >> 32)) > lim) atomicMin(&s_h, j);
+        __syncthreads();
+    }
+    const int h = s_h;
     for (int j = tid; j < h; j += 256) {
-        const uint32_t id = (uint32_t)topk[(size_t)q * k + j];
+        const uint32_t id = (uint32_t)tq[j];
         s_row[j] = inv_perm[id];
         buf[j] = id;
     }
     __syncthreads();
     const int grp = tid >> 4, s = tid & 15, n4 = dpad >> 2;  // dpad is a multiple of 32
-    const float4 *qv = (const float4 *)(qpad + (size_t)q * dpad);
+    const float4 *qv = (const float4 *)(qrows + (size_t)q * dpad);
     for (int j = grp; j < h; j += 16) {
         const uint32_t row = s_row[j];
         const float4 *xv = (const float4 *)(base + (size_t)row * dpad);
@@ -349,9 +448,10 @@ __global__ __launch_bounds__(256) void k_topk_refine(int k, int kout, int metric
     for (int i = h + tid; i < P; i += 256) buf[i] = ~0ull;
     __syncthreads();
     bitonic_sort_lds(buf, P);
+    const int hk = h < k ? h : k;
     for (int j = tid; j < kout; j += 256) {
         const size_t o = (size_t)q * ostride + j;
-        if (j < h) {
+        if (j < hk) {
             const float sc = key_score((uint32_t)(buf[j] >> 32));
             out_ids[o] = (uint32_t)buf[j];
             out_dist[o] = metric == L2 ? sc : -sc + 0.0f;
@@ -362,13 +462,13 @@ __global__ __launch_bounds__(256) void k_topk_refine(int k, int kout, int metric
     }
 }
 
-void launch_topk_refine(int nq, int k, int kout, int metric, const float *qpad, const float *base,
+void launch_topk_refine(int nq, int k, int kc, int kout, int metric, const float *qrows, const float *base,
                         const uint32_t *inv_perm, int dpad, const float *qnorm, const float *bnorm,
-                        const unsigned long long *topk, const uint32_t *have, uint32_t *out_ids, float *out_dist,
-                        int ostride, hipStream_t s) {
+                        const unsigned long long *topk, const uint32_t *have, const float *qerr, uint32_t *out_ids,
+                        float *out_dist, int ostride, hipStream_t s) {
     if (nq <= 0) return;
-    hipLaunchKernelGGL(k_topk_refine, dim3(nq), dim3(256), 0, s, k, kout, metric, qpad, base, inv_perm, dpad, qnorm,
-                       bnorm, topk, have, out_ids, out_dist, ostride);
+    hipLaunchKernelGGL(k_topk_refine, dim3(nq), dim3(256), 0, s, k, kc, kout, metric, qrows, base, inv_perm, dpad,
+                       qnorm, bnorm, topk, have, qerr, out_ids, out_dist, ostride);
 }
 
 }  // namespace vh

@@ -48,6 +48,26 @@ __host__ __device__ inline float key_score(uint32_t k) {
     return __builtin_bit_cast(float, u);
 }
 
+// Rounding bound of a sum of n fp32 terms in any order: gamma_n = n u / (1 - n u), u = 2^-24.
+inline double gamma_n(double n) { return n * 0x1p-24 / (1.0 - n * 0x1p-24); }
+// Coefficients of the GEMM-form selection error bound (2 % slack on top):
+//  * squared L2 on shifted operands q' = fl(q - mu), x' = fl(x - mu): the shifts (2u), the norms
+//    and the MFMA sum (2 gamma_{D+2}) and the epilogue add (u) give
+//    |s~ - ||q - x||^2| <= c (||q'|| + ||x'||)^2;
+//  * dot product: |s~ - q.x| <= gamma_D sum |q_i x_i| <= c ||q|| ||x||;
+//  * cosine of rows normalised in fp32: the two normalisations (gamma_D + 6u) and the sum
+//    (gamma_D) give an absolute bound c.
+inline float sel_err_coeff(int metric, int dpad) {
+    const double u = 0x1p-24, g = gamma_n(dpad + 2.0);
+    const double c = metric == 0 ? 2.0 * g + 4.0 * u : (metric == 1 ? g : 2.0 * g + 8.0 * u);
+    return (float)(c * 1.02);
+}
+// Entries kept per query by a GEMM-metric search: the k best by the GEMM-form score plus up to
+// this many within the selection error bound of the k-th, which the final direct-form pass
+// re-ranks.
+inline int margin_cap(int k) { return k < 16 ? 16 : (k > 256 ? 256 : k); }
+constexpr int kMaxKeep = kMaxK + 256;
+
 inline int ceil_div(long a, long b) { return (int)((a + b - 1) / b); }
 inline size_t round_up(size_t a, size_t b) { return (a + b - 1) / b * b; }
 
@@ -56,14 +76,48 @@ inline size_t round_up(size_t a, size_t b) { return (a + b - 1) / b * b; }
 // position in the resident (permuted) base; k_topk_merge maps positions to vector ids.
 
 // knn_gemm.hip
-// Copies rows [0, n) of `dim` floats into rows of `dpad` floats (zero fill), in the order
-// given by `perm` (out row p = in row perm[p]) or identity if perm == nullptr, optionally
-// sqrt(|x|)-transformed (transform 1, Hellinger) and L2-normalised (normalize 1), and fills
-// rows [n, n_out) with `pad_fill`.  norm_kind 1 writes per-row squared L2 norms, 2 L2 norms
-// (before normalisation).  With norm_kind 0, transform 0 and normalize 0 the copy is
-// bit-exact, so it also moves packed uint32 codes.
+// Row preparation.  Rows [0, n) of `dim` floats are copied into rows of `dpad` floats (zero
+// fill), in the order given by `perm` (out row p = in row perm[p]) or identity if perm is null;
+// `shift` (dpad floats, may be null) is subtracted from every element first; then the row is
+// optionally sqrt(|x|)-transformed (transform 1, Hellinger) and L2-normalised (normalize 1).
+// Rows [n, n_out) are filled with `pad_fill`.  norm_kind 1 writes per-row squared L2 norms, 2 L2
+// norms (before normalisation).  With no shift, norm_kind 0, transform 0 and normalize 0 the
+// copy is bit-exact, so it also moves packed uint32 codes.
+//  * raw_out (may be null): the rows before the shift, padded the same way;
+//  * nonint (may be null): set to 1 when some value of a real row is not an integer;
+//  * err (may be null): per-row bound of the selection error of the GEMM-form score of that row
+//    (as a query) against any base row, err_mode 1 squared L2 (err_coeff (||q'|| + sqrt(err_nmax))^2),
+//    2 dot product (err_coeff ||q|| sqrt(err_nmax)), 3 cosine (err_coeff); 0 when every operand
+//    is an integer (the row's and, by base_integral, the base's) and every partial sum stays
+//    below 2^24, where the fp32 GEMM is exact.
+struct RowPrep {
+    const float *in = nullptr;
+    size_t n = 0, n_out = 0;
+    int dim = 0, dpad = 0;
+    const uint32_t *perm = nullptr;
+    const float *shift = nullptr;
+    float *out = nullptr;
+    float *raw_out = nullptr;
+    float *norm = nullptr;
+    int norm_kind = 0, transform = 0, normalize = 0;
+    float pad_fill = 0.0f;
+    uint32_t *nonint = nullptr;
+    float *err = nullptr;
+    int err_mode = 0;
+    float err_coeff = 0.0f, err_nmax = 0.0f;
+    int base_integral = 0;
+};
+void launch_rows_prep(const RowPrep &a, hipStream_t s);
+// Short form: no shift, raw copy, integer check or error bound.
 void launch_rows_prep(const float *in, size_t n, size_t n_out, int dim, int dpad, const uint32_t *perm, float *out,
                       float *norm, int norm_kind, int transform, int normalize, float pad_fill, hipStream_t s);
+// Per-dimension shift of n rows of `dim` floats (row-major, contiguous): the column means, rounded
+// to integers when every value is an integer (so that shifted integer data stays integer), into
+// shift[0, dpad) (zeros past dim); nonint (device u32) is set to 1 when some value is not an
+// integer.  partial: scratch of nparts * dim doubles (nparts = col_shift_parts()).
+int col_shift_parts();
+void launch_col_shift(const float *x, size_t n, int dim, int dpad, double *partial, uint32_t *nonint, float *shift,
+                      hipStream_t s);
 // One round of the fused MFMA distance + threshold filter over base rows [row_begin, row_end)
 // (row_begin a multiple of 256; rows past the real base are NaN padding up to a multiple of 256).
 // `base` has its rows padded to a multiple of 256 with NaN rows; `qry` has nq rows padded to a
@@ -76,33 +130,62 @@ void launch_gemm_filter(int metric, bool dense, long item_rows, const float *bas
                         long row_end, uint2 *cand, uint32_t *cnt, int cap, float anorm_max, float anorm_min,
                         int grid_cap, hipStream_t s);
 
+// Certification of the MFMA k-means assignment: each point's best score must beat its second
+// best by more than twice the point's selection error bound (err_coeff times the norms, with
+// *cmax the largest centroid norm value), else the point goes to fix[atomicAdd(nfix)] and takes
+// no ticket.  Squared L2 records in devmax[c] (u32 bits of a non-negative float, atomic max) a
+// bound of |x_d - c_d| over the certified points of cluster c.
+struct AssignCert {
+    float err_coeff = 0.0f;
+    const float *cmax = nullptr;
+    int32_t *fix = nullptr;
+    uint32_t *nfix = nullptr;
+    float *devmax = nullptr;
+};
 // MFMA k-means assignment (knn_gemm.hip); metric L2 / DOT / COS.  `cent` has kpad rows
 // (a multiple of 128, NaN padding rows), `pts` n rows padded to a multiple of 128 (zeros).
-// cnorm / pnorm hold squared norms for L2 and L2 norms for COS.
+// cnorm / pnorm hold squared norms for L2 and dot product and L2 norms for COS.  Certified
+// points get assign, pos (ticket in counts) and, for dot / cosine, inertia (-dot, 1 - cos).
 void launch_kmeans_assign(int metric, const float *cent, const float *cnorm, int kpad, const float *pts,
                           const float *pnorm, int n, int dpad, int32_t *assign, float *inertia, int32_t *pos,
-                          int32_t *counts, int grid_cap, hipStream_t s);
+                          int32_t *counts, const AssignCert &cert, int grid_cap, hipStream_t s);
 
 // topk.hip
 void launch_topk_init(int nq, float *tau, uint32_t *have, uint32_t *cnt, uint32_t *flags, hipStream_t s);
-void launch_topk_merge(int nq, int k, const uint2 *cand, uint32_t *cnt, int cap, const uint32_t *perm,
+// Merges each query's candidates into its running best entries (row stride kc of topk).  A query
+// with qerr[q] > 0 (qerr may be null: all 0) keeps its kc best entries and filters later rounds at
+// tau = min(kc-th score, k-th score + 2 qerr[q]), so the final entries hold every row whose score
+// lies within 2 qerr of the k-th; mflag[q] (may be null) is set when that margin may have been cut
+// by the capacity kc.  Others keep k entries and filter at the k-th score.
+void launch_topk_merge(int nq, int k, int kc, const uint2 *cand, uint32_t *cnt, int cap, const uint32_t *perm,
                        unsigned long long *topk, uint32_t *have, float *tau, uint32_t *flags, uint32_t *nflagged,
-                       hipStream_t s);
+                       const float *qerr, uint32_t *mflag, hipStream_t s);
 // Writes results: out_ids[q*ostride + j], out_dist[...] for j < have[q]; distance is the
 // metric value recovered from the score (negated for similarities, transformed for
 // Minkowski / Mahalanobis / Hellinger).  Entries past have[q] are set to UINT32_MAX / NaN.
-// k is the stride of topk (kept entries per query); kout <= ostride entries are written per
+// kc is the stride of topk (kept entries per query); kout <= ostride entries are written per
 // query (kout may exceed k when k was clamped to the number of base rows).
-void launch_topk_finalize(int nq, int k, int kout, int metric, const unsigned long long *topk,
+void launch_topk_finalize(int nq, int kc, int kout, int metric, const unsigned long long *topk,
                           const uint32_t *have, uint32_t *out_ids, float *out_dist, uint32_t *out_dist_u32,
                           int ostride, hipStream_t s);
 // GEMM metrics: recompute the kept distances in direct form, re-sort by (distance, id) and
-// write them (same output contract as launch_topk_finalize; out_dist required).  qnorm / bnorm
-// are the original L2 norms (cosine zero-norm guard; unused for the other metrics).
-void launch_topk_refine(int nq, int k, int kout, int metric, const float *qpad, const float *base,
+// write the best k (same output contract as launch_topk_finalize; out_dist required).  Entries
+// past the k-th count only when their GEMM-form score is within 2 qerr[q] of the k-th.  `qrows` /
+// `base` are the unshifted queries and resident rows; qnorm / bnorm are the original L2 norms
+// (cosine zero-norm guard; unused for the other metrics).
+void launch_topk_refine(int nq, int k, int kc, int kout, int metric, const float *qrows, const float *base,
                         const uint32_t *inv_perm, int dpad, const float *qnorm, const float *bnorm,
-                        const unsigned long long *topk, const uint32_t *have, uint32_t *out_ids, float *out_dist,
-                        int ostride, hipStream_t s);
+                        const unsigned long long *topk, const uint32_t *have, const float *qerr, uint32_t *out_ids,
+                        float *out_dist, int ostride, hipStream_t s);
+// Number of nonzero flags among flags[0, n) into *count (device).
+void launch_count_flags(const uint32_t *flags, int n, uint32_t *count, hipStream_t s);
+// Copies the kept entries of re-run queries (row r, stride ks) back to rows idx[r] (stride kd)
+// with their counts and margin flags (src_mflag null: flags cleared).
+void launch_scatter_topk(const unsigned long long *src, int ks, const uint32_t *src_have, const uint32_t *src_mflag,
+                         const uint32_t *idx, int m, unsigned long long *dst, int kd, uint32_t *dst_have,
+                         uint32_t *dst_mflag, hipStream_t s);
+// dst row r (width floats) = src row idx[r] (row stride width), for r < rows.
+void launch_gather_rows(const float *src, const uint32_t *idx, size_t rows, int width, float *dst, hipStream_t s);
 // hamming.hip
 int hamming_word_pad(int words);
 // fp4 matrix-core path of packed Hamming (hamming_mfma.hip): codes of wpad words expanded to one
@@ -122,6 +205,13 @@ void launch_hamming_filter(const uint32_t *codes, const uint32_t *qry, const flo
 void launch_kmeans_assign_valu(int metric, const float *cent, int k, const float *pts, int n, int dpad,
                                int32_t *assign, float *inertia, int32_t *pos, int32_t *counts, int grid_cap,
                                hipStream_t s);
+// Fix-up of the MFMA assignment (metric L2 / DOT / COS): the listed points (fix[0, *nfix)) get the
+// direct-form argmin over the k unshifted centroids (rows of dpad floats) on the unshifted points,
+// their tickets, and inertia (dot / cosine) or the deviation bound (squared L2).  best: scratch of
+// one u64 per listed point.
+void launch_kmeans_fix(int metric, const float *pts, int dpad, const int32_t *fix, const uint32_t *nfix,
+                       const float *cent, int k, unsigned long long *best, int32_t *assign, float *inertia,
+                       int32_t *pos, int32_t *counts, float *devmax, int grid_cap, hipStream_t s);
 void launch_valu_filter(int metric, const float *base, const float *qry, const float *tau, int nq, int dim, int dpad,
                         long row_begin, long row_end, uint2 *cand, uint32_t *cnt, int cap, int grid_cap,
                         hipStream_t s);

@@ -59,6 +59,7 @@ def _sig(name, restype, *argtypes):
 
 _sig("vhip_last_error", ctypes.c_char_p)
 _sig("vhip_last_error_devices", None, _szp, _szp)
+_sig("vhip_last_error_ordinal", _int)
 _sig("vhip_device_count", _int)
 _sig("vhip_device_info", _int, _int, ctypes.c_char_p, _sz, _szp)
 _sig("vhip_knn_create", _int, _f32p, _sz, _sz, _int, _int, ctypes.POINTER(_vp))
@@ -189,6 +190,10 @@ class InsufficientDevices(CudaError):
 class DeviceNotFound(CudaError):
     code = -2
 
+    def __init__(self, ordinal: int = -1, msg: str = ""):
+        super().__init__(msg or f"HIP device with ordinal {ordinal} was not found")
+        self.ordinal = ordinal
+
 
 class DriverError(CudaError):
     code = -3
@@ -231,7 +236,12 @@ def _check(status: int):
         a = _sz()
         _lib.vhip_last_error_devices(ctypes.byref(r), ctypes.byref(a))
         raise InsufficientDevices(r.value, a.value, msg)
+    if status == DeviceNotFound.code:
+        raise DeviceNotFound(int(_lib.vhip_last_error_ordinal()), msg)
     raise _ERRORS.get(status, CudaError)(msg)
+
+
+VHIP_MAX_K = 2048  # largest k one search call serves (VHIP_MAX_K of vector_hip.h)
 
 
 # ---- types ------------------------------------------------------------------------------------
