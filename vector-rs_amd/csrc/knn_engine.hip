@@ -27,8 +27,36 @@ constexpr size_t kQueryBatch = 16384;
 
 bool is_gemm_metric(int m) { return m == L2 || m == DOT || m == COS; }
 
+// Bump allocator over one device region: every buffer of a search batch is carved from it, so
+// a batch costs one growable workspace buffer (or none, in the allocation-free entry point).
+// With a null base it only measures: `used` is then the bytes the same carve sequence needs.
+struct Arena {
+    uintptr_t base = 0;
+    size_t size = SIZE_MAX, used = 0;
+    Arena() = default;
+    Arena(void *p, size_t bytes) : base((uintptr_t)p), size(bytes) {}
+    template <class T>
+    T *take(size_t count) {
+        const size_t b = round_up(std::max<size_t>(count * sizeof(T), 1), 256);
+        T *r = (used + b <= size) ? (T *)(base + used) : nullptr;
+        used += b;
+        return r;
+    }
+    bool fits() const { return used <= size; }
+};
+
+// Buffers of one run of the search rounds over nq prepared queries.
+struct RunBufs {
+    uint2 *cand = nullptr;                 // nq x cap candidates
+    unsigned long long *topk = nullptr;    // nq x kc kept entries
+    float *tau = nullptr;                  // nq thresholds
+    uint32_t *have = nullptr, *cnt = nullptr, *flags = nullptr, *mflag = nullptr;  // nq each
+    uint32_t *nflag = nullptr;             // 2 counters
+    int8_t *q8 = nullptr;                  // expanded query codes (packed Hamming on fp4 MFMA)
+};
+
 struct Workspace {
-    DevBuf qraw, qpad, qnorm, qerr, tau, have, cnt, flags, mflag, nflag, topk, cand, q8;
+    DevBuf arena;
 };
 
 }  // namespace vh
@@ -126,7 +154,6 @@ static int round_cap(size_t n, size_t k, bool gemm, int dpad) {
     return (int)round_up(cap, kRowAlign);
 }
 
-// Runs all rounds for nq prepared queries; results stay in topk / have.
 // The engine's pseudo-random row order (positions p -> base rows perm[p], so that every round
 // scores a uniform sample of the base): a 4-round Feistel network over the 2^m >= n codes (m
 // even), cycle-walked back into [0, n).  The walk from x follows x's own cycle, which returns to
@@ -243,35 +270,55 @@ struct QueryRows {
 // Base rows of the direct-form passes: the unshifted copy when the scan rows are shifted.
 static const float *direct_rows(const vhip_knn *E) { return E->shifted ? E->raw.as<float>() : E->base.as<float>(); }
 
-// Runs all rounds for nq prepared queries; results stay in topk (row stride kc) / have.
+// Carves the buffers of one run over nq queries: kc kept entries and (with_cand) cap candidates
+// per query.
+static RunBufs carve_run(Arena &A, const vhip_knn *E, size_t nq, int kc, int cap, bool with_cand) {
+    RunBufs B;
+    if (with_cand) B.cand = A.take<uint2>(nq * (size_t)cap);
+    B.topk = A.take<unsigned long long>(nq * (size_t)kc);
+    B.tau = A.take<float>(nq);
+    B.have = A.take<uint32_t>(nq);
+    B.cnt = A.take<uint32_t>(nq);
+    B.flags = A.take<uint32_t>(nq);
+    B.mflag = A.take<uint32_t>(nq);
+    B.nflag = A.take<uint32_t>(2);
+    if (E->ham8) B.q8 = A.take<int8_t>(round_up(nq, kTileCols) * ham_mfma_row_bytes((int)E->dpad));
+    return B;
+}
+
+// Splits every round into pieces of at most max_rows rows (a multiple of kRowAlign, at least the
+// first round's rows; 0 = no split).  A query's candidates from one piece cannot outnumber the
+// piece's rows, so pieces no longer than the candidate capacity cannot overflow it.
+static std::vector<Round> split_rounds(const std::vector<Round> &r, long max_rows) {
+    if (max_rows <= 0) return r;
+    std::vector<Round> out;
+    for (const Round &x : r)
+        for (long b = x.rb; b < x.re; b += max_rows) {
+            Round p = x;
+            p.rb = b;
+            p.re = std::min(x.re, b + max_rows);
+            out.push_back(p);
+        }
+    return out;
+}
+
+// Runs all rounds for nq prepared queries; results stay in B.topk (row stride kc) / B.have.
 // `direct`: score squared L2 in direct form on the unshifted rows (VALU kernel) instead of the
 // engine's own scan; it serves the queries whose GEMM-form margin could not be certified.
-static int run_rounds(vhip_knn *E, const QueryRows &Q, int nq, int k, int kc, int cap, bool direct, DevBuf &cand,
-                      DevBuf &topk, DevBuf &tau, DevBuf &have, DevBuf &cnt, DevBuf &flags, DevBuf &mflag,
-                      DevBuf &nflag) {
+// max_round_rows: see split_rounds.  `timed`: the scan launches feed the engine's kernel timer.
+static int run_rounds(vhip_knn *E, const QueryRows &Q, int nq, int k, int kc, int cap, bool direct, const RunBufs &B,
+                      long max_round_rows, bool timed) {
     hipStream_t s = E->stream;
-    VH_CHECK(cand.ensure(E->dev, (size_t)nq * cap * sizeof(uint2)));
-    VH_CHECK(topk.ensure(E->dev, (size_t)nq * kc * sizeof(unsigned long long)));
-    VH_CHECK(tau.ensure(E->dev, (size_t)nq * sizeof(float)));
-    VH_CHECK(have.ensure(E->dev, (size_t)nq * sizeof(uint32_t)));
-    VH_CHECK(cnt.ensure(E->dev, (size_t)nq * sizeof(uint32_t)));
-    VH_CHECK(flags.ensure(E->dev, (size_t)nq * sizeof(uint32_t)));
-    VH_CHECK(mflag.ensure(E->dev, (size_t)nq * sizeof(uint32_t)));
-    VH_CHECK(nflag.ensure(E->dev, 2 * sizeof(uint32_t)));
-    launch_topk_init(nq, tau.as<float>(), have.as<uint32_t>(), cnt.as<uint32_t>(), flags.as<uint32_t>(), s);
-    launch_fill_u32(mflag.as<uint32_t>(), (size_t)nq, 0u, s);
-    launch_fill_u32(nflag.as<uint32_t>(), 2, 0u, s);
+    launch_topk_init(nq, B.tau, B.have, B.cnt, B.flags, s);
+    launch_fill_u32(B.mflag, (size_t)nq, 0u, s);
+    launch_fill_u32(B.nflag, 2, 0u, s);
     const bool gemm = is_gemm_metric(E->metric) && !direct;
-    const int8_t *q8 = nullptr;
     if (E->ham8) {
         // the queries' +1/-1 nibbles, rows padded to the 128-query tiles
         const size_t rows = round_up((size_t)nq, kTileCols);
-        VH_CHECK(E->ws.q8.ensure(E->dev, rows * ham_mfma_row_bytes((int)E->dpad)));
-        launch_ham_expand((const uint32_t *)Q.qpad, (size_t)nq, (int)E->dpad, (int)E->dpad, rows, false,
-                          E->ws.q8.as<int8_t>(), s);
-        q8 = E->ws.q8.as<int8_t>();
+        launch_ham_expand((const uint32_t *)Q.qpad, (size_t)nq, (int)E->dpad, (int)E->dpad, rows, false, B.q8, s);
     }
-    for (const Round &rd : plan_rounds(E->n, (size_t)k, gemm, (int)E->dpad)) {
+    for (const Round &rd : split_rounds(plan_rounds(E->n, (size_t)k, gemm, (int)E->dpad), max_round_rows)) {
         const long rb = rd.rb, re = rd.re;
         const bool dense = rd.dense || (E->ham8 && rb == 0);
         // Algorithmic work per launch: 2*Q*rows*D flops (GEMM metrics), Q*rows*D element
@@ -284,8 +331,8 @@ static int run_rounds(vhip_knn *E, const QueryRows &Q, int nq, int k, int kc, in
                                             : (double)nq * rows * (double)E->dim);
         const double bytes = E->ham8 ? (rows + nq) * (double)ham_mfma_row_bytes((int)E->dpad)  // expanded codes
                                      : rows * E->dim * 4.0 + (double)nq * E->dim * 4.0;
-        if (dense) launch_fill_u32(cnt.as<uint32_t>(), (size_t)nq, (uint32_t)(re - rb), s);
-        const int t = direct ? -1 : E->timer.begin(s);
+        if (dense) launch_fill_u32(B.cnt, (size_t)nq, (uint32_t)(re - rb), s);
+        const int t = (direct || !timed) ? -1 : E->timer.begin(s);
         const long item =
             gemm && !rd.dense ? balanced_item(rd.item_rows, re - rb, ceil_div(nq, kTileCols), E->grid_cap / 2)
                               : rd.item_rows;
@@ -297,26 +344,25 @@ static int run_rounds(vhip_knn *E, const QueryRows &Q, int nq, int k, int kc, in
                 dense ? re - rb
                       : balanced_item(std::min<long>(32768, rd.slot_rows), re - rb, ceil_div(nq, kTileCols),
                                       E->grid_cap / 2, 512);
-            launch_ham_mfma(dense, hitem, E->base8.as<int8_t>(), q8, (int)E->dpad, tau.as<float>(), nq, rb, re,
-                            cand.as<uint2>(), cnt.as<uint32_t>(), cap, E->grid_cap, s);
+            launch_ham_mfma(dense, hitem, E->base8.as<int8_t>(), B.q8, (int)E->dpad, B.tau, nq, rb, re, B.cand, B.cnt,
+                            cap, E->grid_cap, s);
         } else if (gemm)
             launch_gemm_filter(E->metric, rd.dense, item, E->base.as<float>(), E->norm.as<float>(), Q.qpad, Q.qnorm,
-                               tau.as<float>(), nq, (int)E->dpad, rb, re, cand.as<uint2>(), cnt.as<uint32_t>(), cap,
-                               E->norm_max, E->norm_min, E->grid_cap, s);
+                               B.tau, nq, (int)E->dpad, rb, re, B.cand, B.cnt, cap, E->norm_max, E->norm_min,
+                               E->grid_cap, s);
         else if (E->metric == HAMMING_PACKED)
-            launch_hamming_filter(E->base.as<uint32_t>(), (const uint32_t *)Q.qpad, tau.as<float>(), nq, (int)E->dpad,
-                                  rb, re, cand.as<uint2>(), cnt.as<uint32_t>(), cap, E->grid_cap, s);
+            launch_hamming_filter(E->base.as<uint32_t>(), (const uint32_t *)Q.qpad, B.tau, nq, (int)E->dpad, rb, re,
+                                  B.cand, B.cnt, cap, E->grid_cap, s);
         else if (direct)
-            launch_valu_filter(L2, direct_rows(E), Q.qraw, tau.as<float>(), nq, (int)E->dim, (int)E->dpad, rb, re,
-                               cand.as<uint2>(), cnt.as<uint32_t>(), cap, E->grid_cap, s);
+            launch_valu_filter(L2, direct_rows(E), Q.qraw, B.tau, nq, (int)E->dim, (int)E->dpad, rb, re, B.cand,
+                               B.cnt, cap, E->grid_cap, s);
         else
-            launch_valu_filter(E->metric, E->base.as<float>(), Q.qpad, tau.as<float>(), nq, (int)E->dim,
-                               (int)E->dpad, rb, re, cand.as<uint2>(), cnt.as<uint32_t>(), cap, E->grid_cap, s);
+            launch_valu_filter(E->metric, E->base.as<float>(), Q.qpad, B.tau, nq, (int)E->dim, (int)E->dpad, rb, re,
+                               B.cand, B.cnt, cap, E->grid_cap, s);
         if (t >= 0) E->timer.end(t, s, work, bytes);
         VH_HIP(hipGetLastError());
-        launch_topk_merge(nq, k, kc, cand.as<uint2>(), cnt.as<uint32_t>(), cap, E->perm.as<uint32_t>(),
-                          topk.as<unsigned long long>(), have.as<uint32_t>(), tau.as<float>(), flags.as<uint32_t>(),
-                          nflag.as<uint32_t>(), gemm ? Q.qerr : nullptr, mflag.as<uint32_t>(), s);
+        launch_topk_merge(nq, k, kc, B.cand, B.cnt, cap, E->perm.as<uint32_t>(), B.topk, B.have, B.tau, B.flags,
+                          B.nflag, gemm ? Q.qerr : nullptr, B.mflag, s);
         VH_HIP(hipGetLastError());
     }
     return VHIP_OK;
@@ -329,52 +375,86 @@ static int full_cap(const vhip_knn *E, size_t k, bool gemm) {
     return (int)round_up((size_t)big, kRowAlign);
 }
 
-// Re-runs the queries idx (host list) of the batch Q: `direct` as in run_rounds, with a candidate
-// capacity no round can overflow, and writes their kept entries, counts and margin flags back
-// into the batch's arrays (row stride kc).
+// Buffers of a re-run of nidx queries in sub-batches of per_batch.
+struct RerunMem {
+    uint32_t *didx;
+    float *fr, *fq, *fn, *fe;
+    RunBufs F;
+};
+static RerunMem carve_rerun(Arena &A, const vhip_knn *E, size_t nidx, size_t per_batch, int kc_run, int cap,
+                            bool direct, bool with_cand) {
+    const size_t m_pad = round_up(per_batch, kTileCols);
+    RerunMem r{};
+    r.didx = A.take<uint32_t>(nidx);
+    r.fr = A.take<float>(m_pad * E->dpad);
+    if (!direct) {
+        r.fq = A.take<float>(m_pad * E->dpad);
+        r.fn = A.take<float>(m_pad);
+        r.fe = A.take<float>(m_pad);
+    }
+    r.F = carve_run(A, E, per_batch, kc_run, cap, with_cand);
+    return r;
+}
+
+// Re-runs the queries idx (host list) of the batch Q: `direct` as in run_rounds, and writes their
+// kept entries, counts and margin flags back into the batch's buffers M (row stride kc).
+//  * fixed == null: the re-run allocates candidate lists that no round can overflow.
+//  * Otherwise every buffer is carved from *fixed (sized by the caller for a re-run of up to the
+//    batch's query count) and the batch's own candidate buffer (cand_slots entries, no longer
+//    needed) holds the candidate lists; rounds longer than each query's share of it are split
+//    into pieces of that length, which cannot overflow.
 static int rerun_queries(vhip_knn *E, const QueryRows &Q, const std::vector<uint32_t> &idx, int k, int kc,
-                         bool direct) {
-    Workspace &W = E->ws;
+                         bool direct, const RunBufs &M, const Arena *fixed, uint2 *cand, size_t cand_slots) {
     hipStream_t s = E->stream;
     const bool gemm = is_gemm_metric(E->metric) && !direct;
     const int kc_run = direct ? k : kc;
     const int cap_big = full_cap(E, (size_t)k, gemm);
-    const size_t per_batch = std::max<size_t>(1, ((size_t)1 << 30) / ((size_t)cap_big * sizeof(uint2)));
-    DevBuf didx, fq, fn, fe, fr, fcand, ftopk, ftau, fhave, fcnt, fflags, fmflag, fnflag;
-    VH_CHECK(didx.ensure(E->dev, idx.size() * sizeof(uint32_t)));
-    VH_HIP(hipMemcpyAsync(didx.p, idx.data(), idx.size() * sizeof(uint32_t), hipMemcpyHostToDevice, s));
     const int dp = (int)E->dpad;
+    size_t per_batch = idx.size();
+    int cap = cap_big;
+    long max_rows = 0;
+    DevBuf own;
+    Arena A;
+    if (fixed) {
+        A = *fixed;
+        cap = (int)std::min<size_t>((size_t)cap_big, cand_slots / idx.size() / kRowAlign * kRowAlign);
+        if (cap < cap_big) max_rows = cap;
+    } else {
+        per_batch = std::min(idx.size(), std::max<size_t>(1, ((size_t)1 << 30) / ((size_t)cap_big * sizeof(uint2))));
+        Arena meas;
+        carve_rerun(meas, E, idx.size(), per_batch, kc_run, cap, direct, true);
+        VH_CHECK(own.ensure(E->dev, meas.used));
+        A = Arena(own.p, own.bytes);
+    }
+    RerunMem R = carve_rerun(A, E, idx.size(), per_batch, kc_run, cap, direct, fixed == nullptr);
+    if (!A.fits()) return set_error(VHIP_ERR_DRIVER, "re-run workspace larger than its reserve");
+    if (fixed) R.F.cand = cand;
+    VH_HIP(hipMemcpyAsync(R.didx, idx.data(), idx.size() * sizeof(uint32_t), hipMemcpyHostToDevice, s));
     for (size_t b0 = 0; b0 < idx.size(); b0 += per_batch) {
         const int m = (int)std::min(per_batch, idx.size() - b0);
         const size_t m_pad = round_up((size_t)m, kTileCols);
-        const uint32_t *di = didx.as<uint32_t>() + b0;
+        const uint32_t *di = R.didx + b0;
         QueryRows F{nullptr, nullptr, nullptr, nullptr};
-        VH_CHECK(fr.ensure(E->dev, m_pad * E->dpad * sizeof(float)));
-        launch_fill(fr.as<float>() + (size_t)m * dp, (m_pad - m) * E->dpad, 0.0f, s);
-        launch_gather_rows(Q.qraw, di, (size_t)m, dp, fr.as<float>(), s);
-        F.qraw = fr.as<float>();
+        launch_fill(R.fr + (size_t)m * dp, (m_pad - m) * E->dpad, 0.0f, s);
+        launch_gather_rows(Q.qraw, di, (size_t)m, dp, R.fr, s);
+        F.qraw = R.fr;
         if (!direct) {
-            VH_CHECK(fq.ensure(E->dev, m_pad * E->dpad * sizeof(float)));
-            VH_CHECK(fn.ensure(E->dev, m_pad * sizeof(float)));
-            VH_CHECK(fe.ensure(E->dev, m_pad * sizeof(float)));
-            launch_fill(fq.as<float>() + (size_t)m * dp, (m_pad - m) * E->dpad, 0.0f, s);
-            launch_fill(fn.as<float>() + m, m_pad - m, 0.0f, s);
-            launch_fill(fe.as<float>() + m, m_pad - m, 0.0f, s);
-            launch_gather_rows(Q.qpad, di, (size_t)m, dp, fq.as<float>(), s);
-            launch_gather_rows(Q.qnorm, di, (size_t)m, 1, fn.as<float>(), s);
-            if (Q.qerr) launch_gather_rows(Q.qerr, di, (size_t)m, 1, fe.as<float>(), s);
-            F.qpad = fq.as<float>();
-            F.qnorm = fn.as<float>();
-            F.qerr = Q.qerr ? fe.as<float>() : nullptr;
+            launch_fill(R.fq + (size_t)m * dp, (m_pad - m) * E->dpad, 0.0f, s);
+            launch_fill(R.fn + m, m_pad - m, 0.0f, s);
+            launch_fill(R.fe + m, m_pad - m, 0.0f, s);
+            launch_gather_rows(Q.qpad, di, (size_t)m, dp, R.fq, s);
+            launch_gather_rows(Q.qnorm, di, (size_t)m, 1, R.fn, s);
+            if (Q.qerr) launch_gather_rows(Q.qerr, di, (size_t)m, 1, R.fe, s);
+            F.qpad = R.fq;
+            F.qnorm = R.fn;
+            F.qerr = Q.qerr ? R.fe : nullptr;
         }
-        VH_CHECK(run_rounds(E, F, m, k, kc_run, cap_big, direct, fcand, ftopk, ftau, fhave, fcnt, fflags, fmflag,
-                            fnflag));
-        launch_scatter_topk(ftopk.as<unsigned long long>(), kc_run, fhave.as<uint32_t>(),
-                            direct ? nullptr : fmflag.as<uint32_t>(), di, m, W.topk.as<unsigned long long>(), kc,
-                            W.have.as<uint32_t>(), W.mflag.as<uint32_t>(), s);
+        VH_CHECK(run_rounds(E, F, m, k, kc_run, cap, direct, R.F, max_rows, fixed == nullptr));
+        launch_scatter_topk(R.F.topk, kc_run, R.F.have, direct ? nullptr : R.F.mflag, di, m, M.topk, kc, M.have,
+                            M.mflag, s);
         VH_HIP(hipGetLastError());
     }
-    VH_HIP(hipStreamSynchronize(s));  // the staging buffers above are released at return
+    VH_HIP(hipStreamSynchronize(s));  // idx and the re-run's own buffers are released at return
     return VHIP_OK;
 }
 
@@ -387,6 +467,8 @@ static std::vector<uint32_t> flagged(const std::vector<uint32_t> &f) {
 
 // Searches nq prepared queries for k = effective_k neighbours; writes kout >= k entries per query
 // (the rest marked empty) into device arrays d_ids and d_dist or d_dist_u32 (row stride ostride).
+// B: the batch's run buffers (kc entries and cap candidates per query); fixed: the re-runs' reserve
+// when the search must not allocate (see rerun_queries), else null.
 //  * A query whose candidate list overflowed (massive ties) is re-run with a capacity that no
 //    round can overflow.
 //  * GEMM metrics keep, besides the k best by GEMM-form score, every entry within twice the
@@ -395,41 +477,38 @@ static std::vector<uint32_t> flagged(const std::vector<uint32_t> &f) {
 //    unshifted rows, so every L2 result is the exact top-k of the direct-form distances.  (For dot
 //    product and cosine a direct-form pass rounds no better than the GEMM form, so a cut margin
 //    keeps the kc best by GEMM score: only near-ties within the error bound are affected.)
-static int search_prepared(vhip_knn *E, const QueryRows &Q, int nq, int k, int kout, uint32_t *d_ids, float *d_dist,
-                           uint32_t *d_dist_u32, int ostride) {
-    Workspace &W = E->ws;
+static int search_prepared(vhip_knn *E, const QueryRows &Q, int nq, int k, int kc, int cap, const RunBufs &B,
+                           const Arena *fixed, int kout, uint32_t *d_ids, float *d_dist, uint32_t *d_dist_u32,
+                           int ostride) {
     hipStream_t s = E->stream;
     const bool gemm = is_gemm_metric(E->metric);
-    const int kc = gemm ? k + margin_cap(k) : k;
-    const int cap = round_cap(E->n, (size_t)k, gemm, (int)E->dpad);
-    VH_CHECK(run_rounds(E, Q, nq, k, kc, cap, false, W.cand, W.topk, W.tau, W.have, W.cnt, W.flags, W.mflag,
-                        W.nflag));
-    if (gemm) launch_count_flags(W.mflag.as<uint32_t>(), nq, W.nflag.as<uint32_t>() + 1, s);
+    VH_CHECK(run_rounds(E, Q, nq, k, kc, cap, false, B, 0, fixed == nullptr));
+    if (gemm) launch_count_flags(B.mflag, nq, B.nflag + 1, s);
     uint32_t nf[2] = {0, 0};
-    VH_HIP(hipMemcpyAsync(nf, W.nflag.p, sizeof(nf), hipMemcpyDeviceToHost, s));
+    VH_HIP(hipMemcpyAsync(nf, B.nflag, sizeof(nf), hipMemcpyDeviceToHost, s));
     VH_HIP(hipStreamSynchronize(s));
+    const size_t slots = (size_t)nq * cap;
     if (nf[0]) {
         std::vector<uint32_t> f(nq);
-        VH_HIP(hipMemcpy(f.data(), W.flags.p, nq * sizeof(uint32_t), hipMemcpyDeviceToHost));
-        VH_CHECK(rerun_queries(E, Q, flagged(f), k, kc, false));
+        VH_HIP(hipMemcpy(f.data(), B.flags, nq * sizeof(uint32_t), hipMemcpyDeviceToHost));
+        VH_CHECK(rerun_queries(E, Q, flagged(f), k, kc, false, B, fixed, B.cand, slots));
         if (gemm) {
-            launch_count_flags(W.mflag.as<uint32_t>(), nq, W.nflag.as<uint32_t>() + 1, s);
-            VH_HIP(hipMemcpyAsync(nf + 1, W.nflag.as<uint32_t>() + 1, sizeof(uint32_t), hipMemcpyDeviceToHost, s));
+            launch_count_flags(B.mflag, nq, B.nflag + 1, s);
+            VH_HIP(hipMemcpyAsync(nf + 1, B.nflag + 1, sizeof(uint32_t), hipMemcpyDeviceToHost, s));
             VH_HIP(hipStreamSynchronize(s));
         }
     }
     if (nf[1] && E->metric == L2) {
         std::vector<uint32_t> f(nq);
-        VH_HIP(hipMemcpy(f.data(), W.mflag.p, nq * sizeof(uint32_t), hipMemcpyDeviceToHost));
-        VH_CHECK(rerun_queries(E, Q, flagged(f), k, kc, true));
+        VH_HIP(hipMemcpy(f.data(), B.mflag, nq * sizeof(uint32_t), hipMemcpyDeviceToHost));
+        VH_CHECK(rerun_queries(E, Q, flagged(f), k, kc, true, B, fixed, B.cand, slots));
     }
     if (gemm && d_dist)
         launch_topk_refine(nq, k, kc, kout, E->metric, Q.qraw, direct_rows(E), E->inv_perm.as<uint32_t>(),
-                           (int)E->dpad, Q.qnorm, E->norm.as<float>(), W.topk.as<unsigned long long>(),
-                           W.have.as<uint32_t>(), Q.qerr, d_ids, d_dist, ostride, s);
+                           (int)E->dpad, Q.qnorm, E->norm.as<float>(), B.topk, B.have, Q.qerr, d_ids, d_dist, ostride,
+                           s);
     else
-        launch_topk_finalize(nq, kc, kout, E->metric, W.topk.as<unsigned long long>(), W.have.as<uint32_t>(), d_ids,
-                             d_dist, d_dist_u32, ostride, s);
+        launch_topk_finalize(nq, kc, kout, E->metric, B.topk, B.have, d_ids, d_dist, d_dist_u32, ostride, s);
     VH_HIP(hipGetLastError());
     return VHIP_OK;
 }
@@ -549,9 +628,37 @@ static int engine_create(const void *base, size_t n, size_t dim, int metric, int
     return VHIP_OK;
 }
 
-// Device-side search: d_queries (nq x dim elements), outputs nq x k with row stride k.
+// Buffers of one query batch of m queries: the prepared rows and the run buffers.
+struct BatchMem {
+    float *qpad, *qnorm, *qerr, *qraw;
+    RunBufs B;
+};
+static BatchMem carve_batch(Arena &A, const vhip_knn *E, size_t m, int kc, int cap) {
+    const size_t m_pad = round_up(m, kTileCols);
+    BatchMem b{};
+    b.qpad = A.take<float>(m_pad * E->dpad);
+    b.qnorm = A.take<float>(m_pad);
+    b.qerr = is_gemm_metric(E->metric) ? A.take<float>(m_pad) : nullptr;
+    b.qraw = E->shifted ? A.take<float>(m_pad * E->dpad) : nullptr;
+    b.B = carve_run(A, E, m, kc, cap, true);
+    return b;
+}
+
+// Device memory a batch of m queries needs; with_rerun adds the reserve of an allocation-free
+// re-run of up to m queries (everything but the candidate lists, which reuse the batch's).
+static size_t batch_bytes(const vhip_knn *E, size_t m, int kc, int cap, bool with_rerun) {
+    Arena A;
+    carve_batch(A, E, m, kc, cap);
+    if (with_rerun) carve_rerun(A, E, m, m, kc, cap, false, false);
+    return A.used;
+}
+
+// Device-side search: d_queries (nq x dim elements), outputs nq x k with row stride k.  Working
+// memory comes from the engine's workspace buffer (grown as needed) or, when `scratch` is given,
+// from that fixed region only, in query batches sized to fit it (no allocation, no kernel timing).
 static int engine_search_device(vhip_knn *E, const void *d_queries, size_t nq, size_t k, uint32_t *d_ids,
-                                float *d_dist, uint32_t *d_dist_u32) {
+                                float *d_dist, uint32_t *d_dist_u32, void *scratch = nullptr,
+                                size_t scratch_bytes = 0) {
     clear_error();
     VH_CHECK(check_search_args(E, k));
     std::lock_guard<std::mutex> lock(E->mu);
@@ -564,15 +671,43 @@ static int engine_search_device(vhip_knn *E, const void *d_queries, size_t nq, s
         VH_HIP(hipStreamSynchronize(E->stream));
         return VHIP_OK;
     }
-    Workspace &W = E->ws;
     const bool gemm = is_gemm_metric(E->metric);
-    for (size_t q0 = 0; q0 < nq; q0 += kQueryBatch) {
-        const int m = (int)std::min(kQueryBatch, nq - q0);
+    const int kk = (int)ek;
+    const int kc = gemm ? kk + margin_cap(kk) : kk;
+    const int cap = round_cap(E->n, ek, gemm, (int)E->dpad);
+    size_t batch = std::min(nq, kQueryBatch);
+    if (scratch) {
+        // the largest batch whose buffers and re-run reserve fit the scratch region
+        if (batch_bytes(E, 1, kc, cap, true) > scratch_bytes)
+            return set_error(VHIP_ERR_INVALID_CONFIG,
+                             "k = " + std::to_string(k) + " over " + std::to_string(E->n) + " rows of dimension " +
+                                 std::to_string(E->dim) + " needs " + std::to_string(batch_bytes(E, 1, kc, cap, true)) +
+                                 " bytes of working memory per query; the allocation-free search has " +
+                                 std::to_string(scratch_bytes));
+        size_t lo = 1, hi = batch;
+        while (lo < hi) {
+            const size_t mid = (lo + hi + 1) / 2;
+            if (batch_bytes(E, mid, kc, cap, true) <= scratch_bytes)
+                lo = mid;
+            else
+                hi = mid - 1;
+        }
+        batch = lo;
+    }
+    for (size_t q0 = 0; q0 < nq; q0 += batch) {
+        const int m = (int)std::min(batch, nq - q0);
         const size_t m_pad = round_up((size_t)m, kTileCols);
-        VH_CHECK(W.qpad.ensure(E->dev, m_pad * E->dpad * sizeof(float)));
-        VH_CHECK(W.qnorm.ensure(E->dev, m_pad * sizeof(float)));
-        if (gemm) VH_CHECK(W.qerr.ensure(E->dev, m_pad * sizeof(float)));
-        if (E->shifted) VH_CHECK(W.qraw.ensure(E->dev, m_pad * E->dpad * sizeof(float)));
+        Arena A;
+        if (scratch) {
+            A = Arena(scratch, scratch_bytes);
+        } else {
+            VH_CHECK(E->ws.arena.ensure(E->dev, batch_bytes(E, (size_t)m, kc, cap, false)));
+            A = Arena(E->ws.arena.p, E->ws.arena.bytes);
+        }
+        const BatchMem bm = carve_batch(A, E, (size_t)m, kc, cap);
+        const Arena reserve = A;  // the re-runs' buffers follow the batch's (allocation-free search)
+        if (scratch) carve_rerun(A, E, (size_t)m, (size_t)m, kc, cap, false, false);
+        if (!A.fits()) return set_error(VHIP_ERR_DRIVER, "search workspace larger than its region");
         RowPrep rp;
         rp.in = (const float *)d_queries + q0 * E->dim;
         rp.n = (size_t)m;
@@ -580,15 +715,15 @@ static int engine_search_device(vhip_knn *E, const void *d_queries, size_t nq, s
         rp.dim = (int)E->dim;
         rp.dpad = (int)E->dpad;
         rp.shift = E->shifted ? E->shift.as<float>() : nullptr;
-        rp.out = W.qpad.as<float>();
-        rp.raw_out = E->shifted ? W.qraw.as<float>() : nullptr;
-        rp.norm = W.qnorm.as<float>();
+        rp.out = bm.qpad;
+        rp.raw_out = bm.qraw;
+        rp.norm = bm.qnorm;
         rp.norm_kind = norm_kind_of(E->metric);
         rp.transform = transform_of(E->metric);
         rp.normalize = normalize_of(E->metric);
         rp.pad_fill = 0.0f;
         if (gemm) {
-            rp.err = W.qerr.as<float>();
+            rp.err = bm.qerr;
             rp.err_mode = err_mode_of(E->metric);
             rp.err_coeff = E->err_coeff;
             rp.err_nmax = E->norm_max;
@@ -596,10 +731,10 @@ static int engine_search_device(vhip_knn *E, const void *d_queries, size_t nq, s
         }
         launch_rows_prep(rp, E->stream);
         VH_HIP(hipGetLastError());
-        const QueryRows Q{W.qpad.as<float>(), W.qnorm.as<float>(), gemm ? W.qerr.as<float>() : nullptr,
-                          E->shifted ? W.qraw.as<float>() : W.qpad.as<float>()};
-        VH_CHECK(search_prepared(E, Q, m, (int)ek, (int)k, d_ids + q0 * k, d_dist ? d_dist + q0 * k : nullptr,
-                                 d_dist_u32 ? d_dist_u32 + q0 * k : nullptr, (int)k));
+        const QueryRows Q{bm.qpad, bm.qnorm, bm.qerr, E->shifted ? bm.qraw : bm.qpad};
+        VH_CHECK(search_prepared(E, Q, m, kk, kc, cap, bm.B, scratch ? &reserve : nullptr, (int)k, d_ids + q0 * k,
+                                 d_dist ? d_dist + q0 * k : nullptr, d_dist_u32 ? d_dist_u32 + q0 * k : nullptr,
+                                 (int)k));
     }
     VH_HIP(hipStreamSynchronize(E->stream));
     E->timer.collect();
@@ -640,6 +775,42 @@ static int engine_search_host(vhip_knn *E, const void *queries, size_t nq, size_
     return VHIP_OK;
 }
 
+// ---- allocation-free search -----------------------------------------------------------------
+// The working memory of vhip_knn_search_batch_device_noalloc: one fixed array in the library's
+// code object, of which every device that runs the library holds its own copy until the process
+// ends.  On the host the array's name is only a stand-in, never a device address: each device's
+// address comes from hipGetSymbolAddress, taken once per device with that device current, and
+// only that address reaches kernels.
+static __device__ __align__(256) unsigned char scratch[VHIP_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxScratchDevices = 64;
+struct ScratchSlot {
+    std::mutex mu;         // held for a whole call: calls on one device run one after another
+    void *ptr = nullptr;   // this device's copy of `scratch`
+};
+ScratchSlot g_scratch[kMaxScratchDevices];
+}  // namespace
+
+static int search_device_noalloc(vhip_knn *E, const float *d_queries, size_t nq, size_t k, uint32_t *d_ids,
+                                 float *d_dist) {
+    clear_error();
+    if (!E) return set_error(VHIP_ERR_INVALID_CONFIG, "null engine");
+    if (E->dev < 0 || E->dev >= kMaxScratchDevices)
+        return set_error(VHIP_ERR_INVALID_CONFIG, "device ordinal " + std::to_string(E->dev) +
+                                                      " is beyond the allocation-free search's device table");
+    ScratchSlot &S = g_scratch[E->dev];
+    std::lock_guard<std::mutex> lock(S.mu);
+    if (!S.ptr) {
+        VH_CHECK(open_device(E->dev));
+        void *p = nullptr;
+        VH_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        if (!p) return set_error(VHIP_ERR_DRIVER, "hipGetSymbolAddress(scratch) returned a null address");
+        S.ptr = p;
+    }
+    return engine_search_device(E, d_queries, nq, k, d_ids, d_dist, nullptr, S.ptr, VHIP_NOALLOC_SCRATCH_BYTES);
+}
+
 }  // namespace vh
 
 using namespace vh;
@@ -657,6 +828,11 @@ int vhip_knn_create(const float *base, size_t n, size_t dim, int metric, int ord
 int vhip_knn_search_batch_device(vhip_knn *E, const float *d_queries, size_t nq, size_t k, uint32_t *d_ids,
                                  float *d_dist) {
     return engine_search_device(E, d_queries, nq, k, d_ids, d_dist, nullptr);
+}
+
+int vhip_knn_search_batch_device_noalloc(vhip_knn *E, const float *d_queries, size_t nq, size_t k, uint32_t *d_ids,
+                                         float *d_dist) {
+    return search_device_noalloc(E, d_queries, nq, k, d_ids, d_dist);
 }
 
 int vhip_knn_search_batch(vhip_knn *E, const float *queries, size_t nq, size_t k, uint32_t *out_ids, float *out_dist,

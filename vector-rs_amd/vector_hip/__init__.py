@@ -65,6 +65,7 @@ _sig("vhip_device_info", _int, _int, ctypes.c_char_p, _sz, _szp)
 _sig("vhip_knn_create", _int, _f32p, _sz, _sz, _int, _int, ctypes.POINTER(_vp))
 _sig("vhip_knn_search_batch", _int, _vp, _f32p, _sz, _sz, _u32p, _f32p, _szp)
 _sig("vhip_knn_search_batch_device", _int, _vp, _vp, _sz, _sz, _vp, _vp)
+_sig("vhip_knn_search_batch_device_noalloc", _int, _vp, _vp, _sz, _sz, _vp, _vp)
 _sig("vhip_knn_dimension", _sz, _vp)
 _sig("vhip_knn_num_vectors", _sz, _vp)
 _sig("vhip_knn_metric", _int, _vp)
@@ -242,6 +243,7 @@ def _check(status: int):
 
 
 VHIP_MAX_K = 2048  # largest k one search call serves (VHIP_MAX_K of vector_hip.h)
+NOALLOC_SCRATCH_BYTES = 64 << 20  # per-GPU working array of the allocation-free search (VHIP_NOALLOC_SCRATCH_BYTES)
 
 
 # ---- types ------------------------------------------------------------------------------------
@@ -408,6 +410,11 @@ class CudaKnnEngine(_Profiled):
     def search_batch_device(self, d_queries: int, nq: int, k: int, d_ids: int, d_dist: int):
         """Queries / outputs are device pointers (ints) on the engine's GPU."""
         _check(_lib.vhip_knn_search_batch_device(self._h, d_queries, nq, k, d_ids, d_dist))
+
+    def search_batch_device_noalloc(self, d_queries: int, nq: int, k: int, d_ids: int, d_dist: int):
+        """As search_batch_device, with working memory from the library's fixed per-GPU array of
+        NOALLOC_SCRATCH_BYTES (no device allocation); same results."""
+        _check(_lib.vhip_knn_search_batch_device_noalloc(self._h, d_queries, nq, k, d_ids, d_dist))
 
     def dimension(self) -> int:
         return _lib.vhip_knn_dimension(self._h)
