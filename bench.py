@@ -8,9 +8,15 @@ iterations from the first 4,096 points) under "kmeans".
 
 Printed JSON (one line): metric/value/unit, ms_per_step, "roofline" of the dominant kernel
 (FP32-MFMA distance + filter kernel, its algorithmic flops per launch divided by its average
-launch time, measured with HIP events on the engine's stream over the timed region) and
+launch time, measured with HIP events on the engine's stream over the timed region),
 "cpu_baseline": the oracle's restatement of the reference CPU path (CudaKnnEngine::search_batch_cpu,
-knn.rs:312-377, AVX-512 dispatch as vector-simd) timed on this host on a bounded query sample.
+knn.rs:312-377, AVX-512 dispatch as vector-simd) timed on this host on a bounded query sample, and
+"parity": the timed run's results against the oracle's on that sample (tie-aware recall >= 0.999,
+distances within 1e-4 relative, exact on integer data).  The default line also carries the other
+workloads under "kmeans" (first iteration checked against the oracle's: <= 0.01% flips, all
+near-ties, centroids within 1e-4), "cos768", "hamming" (bit-exact against the oracle's popcount
+search over all 10M codes), "l1" and "linf", each with its own roofline, CPU baseline and parity.
+The process exits with status 3, after printing the line, when any parity check fails.
 
 Other workloads: --workload cos768 | kmeans | hamming | l1 | linf | gauss (see WORKLOADS), ivf_coarse
 (the IVF coarse quantizer), ivfpq (IVF-PQ search), upload (engine builds from VECRSTOR files),
@@ -42,10 +48,12 @@ def log(*a):
 
 
 def cpu_threads() -> int:
-    env = os.environ.get("OMP_NUM_THREADS")
-    if env and env.isdigit():
-        return int(env)
-    return min(16, os.cpu_count() or 1)
+    """Threads of the CPU baseline: every core this process may run on (its affinity mask), as
+    rayon's default pool in the reference uses every logical core it is given."""
+    try:
+        return max(1, len(os.sched_getaffinity(0)))
+    except (AttributeError, OSError):
+        return os.cpu_count() or 1
 
 
 def cpu_model() -> str:
@@ -154,12 +162,92 @@ def cpu_knn_baseline(base, queries, k, metric, max_sample=None):
     probe = time.perf_counter() - t0
     sample = int(max(16, min(cap, 16 * CPU_TARGET_S / max(probe, 1e-6))))
     t0 = time.perf_counter()
-    oracle.knn_search_batch(base, queries[:sample], k, metric, threads=th)
+    ref = oracle.knn_search_batch(base, queries[:sample], k, metric, threads=th)
     dt = time.perf_counter() - t0
     be = {0: "scalar", 1: "AVX2+FMA", 2: "AVX-512F"}[oracle.detect_backend()]
     return {"value": round(sample / dt, 3), "unit": "queries/s", "cores": th, "kind": "port",
             "sample": f"{sample} of the {queries.shape[0]} queries against the full base, k={k}, "
-                      f"{be} backend, {dt:.2f} s wall on {th} threads ({cpu_model()})"}
+                      f"{be} backend, {dt:.2f} s wall on {th} threads (affinity mask) ({cpu_model()})"}, ref
+
+
+def knn_parity(base, queries, ids, dist, ref, k, metric, rtol, atol, min_recall=0.999):
+    """Parity of the timed GPU search with the oracle on the queries the oracle searched (ref =
+    its ids, distances and lengths for queries[:len]): tie-aware recall (a returned id counts
+    when its oracle value is at least as good as the oracle's k-th), every reported distance
+    against the oracle's value of the same (query, id) pair within rtol / atol, the k best values
+    as a multiset, and unique in-range ids.  Packed Hamming compares popcount distances."""
+    import oracle
+
+    rids, rdist, _ = ref
+    m = rids.shape[0]
+    hib = metric in ("dot", "cosine")
+    ok_ids = total = 0
+    max_abs = max_rel = 0.0
+    dist_ok = multiset_ok = ids_ok = True
+    for q0 in range(0, m, 512):
+        q1 = min(m, q0 + 512)
+        got = ids[q0:q1, :k].astype(np.int64)
+        ids_ok = ids_ok and bool(np.all(got < base.shape[0]))
+        ids_ok = ids_ok and all(len(set(r.tolist())) == k for r in got)
+        got = np.minimum(got, base.shape[0] - 1)
+        if metric == "hamming":
+            refv = np.bitwise_count(base[got] ^ queries[q0:q1, None, :]).sum(-1).astype(np.float64)
+        else:
+            qq = np.repeat(queries[q0:q1], k, 0)
+            refv = oracle.distance_rows(metric, qq, base[got.reshape(-1)]).reshape(q1 - q0, k).astype(np.float64)
+        kth = rdist[q0:q1, k - 1:k].astype(np.float64)
+        tol = rtol * np.abs(kth) + atol
+        good = refv >= kth - tol if hib else refv <= kth + tol
+        ok_ids += int(good.sum())
+        total += good.size
+        diff = np.abs(dist[q0:q1, :k].astype(np.float64) - refv)
+        dist_ok = dist_ok and bool(np.all(diff <= rtol * np.abs(refv) + atol))
+        max_abs = max(max_abs, float(diff.max()))
+        nz = np.abs(refv) > 0
+        if nz.any():
+            max_rel = max(max_rel, float((diff[nz] / np.abs(refv[nz])).max()))
+        rs = np.sort(rdist[q0:q1, :k].astype(np.float64), 1)
+        multiset_ok = multiset_ok and bool(np.all(np.abs(rs - np.sort(refv, 1)) <= rtol * np.abs(rs) + atol))
+    recall = ok_ids / max(total, 1)
+    ok = bool(ids_ok and dist_ok and multiset_ok and recall >= min_recall)
+    return {"queries_checked": int(m), "k": k, "recall_tie_aware": round(recall, 6), "min_recall": min_recall,
+            "max_abs_dist_err": max_abs, "max_rel_dist_err": max_rel,
+            "distance_tolerance": {"rtol": rtol, "atol": atol}, "distances_ok": dist_ok,
+            "kbest_values_match": multiset_ok, "ids_unique_in_range": ids_ok, "ok": ok}
+
+
+def kmeans_parity(data, cent, got, ref):
+    """One Lloyd iteration of the GPU from centroids `cent` against the oracle's iteration from
+    the same centroids (ref): assignments differ on at most 0.01% of the points and only at
+    near-ties (the two centroids' oracle distances within 1e-4 relative); member counts equal the
+    GPU assignment's; each centroid within 1e-4 of its norm of the oracle's update where the
+    membership agrees, and of the float64 mean of the GPU's members where a flip touched it;
+    inertia within 1e-4 relative."""
+    import oracle
+
+    ga, ra = got["assign"].astype(np.int64), ref["assign"].astype(np.int64)
+    n, kc = len(data), len(cent)
+    flips = np.nonzero(ga != ra)[0]
+    near = True
+    if len(flips):
+        dg = oracle.distance_rows("l2", data[flips], cent[ga[flips]]).astype(np.float64)
+        dr = oracle.distance_rows("l2", data[flips], cent[ra[flips]]).astype(np.float64)
+        near = bool(np.all(np.abs(dg - dr) <= 1e-4 * np.maximum(1.0, np.abs(dr))))
+    counts_ok = bool(np.array_equal(np.bincount(ga, minlength=kc), got["counts"]))
+    touched = np.zeros(kc, bool)
+    touched[np.unique(np.concatenate([ga[flips], ra[flips]]))] = True
+    gc_, rc_ = got["centroids"].astype(np.float64), ref["centroids"].astype(np.float64)
+    err = np.linalg.norm(gc_ - rc_, axis=1) / np.maximum(np.linalg.norm(rc_, axis=1), 1e-6)
+    worst = float(err[~touched].max()) if (~touched).any() else 0.0
+    for c in np.nonzero(touched)[0]:
+        mem = np.nonzero(ga == c)[0]
+        want = data[mem].astype(np.float64).mean(0) if len(mem) else cent[c].astype(np.float64)
+        worst = max(worst, float(np.linalg.norm(gc_[c] - want) / max(np.linalg.norm(want), 1e-6)))
+    inertia_rel = abs(float(got["inertia"]) - float(ref["inertia"])) / max(abs(float(ref["inertia"])), 1e-30)
+    ok = bool(len(flips) <= max(1, int(1e-4 * n)) and near and counts_ok and worst <= 1e-4 and inertia_rel <= 1e-4)
+    return {"iteration": "first, from the initial centroids", "points": int(n), "assignment_flips": int(len(flips)),
+            "max_flip_frac": 1e-4, "flips_all_near_ties": near, "counts_match": counts_ok,
+            "max_centroid_rel_err": worst, "inertia_rel_err": inertia_rel, "ok": ok}
 
 
 def bench_kmeans(vh, steps_iters, with_cpu):
@@ -171,7 +259,8 @@ def bench_kmeans(vh, steps_iters, with_cpu):
     init = data[:kc].copy()
     st = vh.KMeansState(data)
     st.set_centroids(init)
-    st.run(1)  # warm-up iteration
+    st.run(1)  # warm-up: the first iteration from the initial centroids, kept for the parity check
+    first = st.read()
     st.set_centroids(init)
     st.profile(True)
     vh.synchronize()
@@ -186,23 +275,28 @@ def bench_kmeans(vh, steps_iters, with_cpu):
            "value": round(1e3 / ms_iter, 3), "unit": "iterations/s", "ms_per_iteration": round(ms_iter, 3),
            "inertia": out["inertia"],
            "roofline": roofline(prof, "mfma", PEAK_MFMA_F32, "TFLOP/s", "kmeans")}
-    if with_cpu:
-        import oracle
+    import oracle
 
-        # whole Lloyd iterations (KMeans::fit body) over all points from the same initial
-        # centroids, repeated until about CPU_TARGET_S seconds have passed
-        th = cpu_threads()
-        its = 0
-        t0 = time.perf_counter()
-        while True:
-            oracle.kmeans_step(data, init, "l2", threads=th)
-            its += 1
-            if time.perf_counter() - t0 >= CPU_TARGET_S or its >= 10:
-                break
-        dt = (time.perf_counter() - t0) / its
+    # whole Lloyd iterations (KMeans::fit body) over all points from the same initial centroids,
+    # repeated until about CPU_TARGET_S seconds have passed (one without the CPU leg: the parity
+    # reference)
+    th = cpu_threads()
+    its = 0
+    ref = None
+    t0 = time.perf_counter()
+    while True:
+        r = oracle.kmeans_step(data, init, "l2", threads=th)
+        ref = r if ref is None else ref
+        its += 1
+        if not with_cpu or time.perf_counter() - t0 >= CPU_TARGET_S or its >= 10:
+            break
+    dt = (time.perf_counter() - t0) / its
+    res["parity"] = kmeans_parity(data, init, first, ref)
+    if with_cpu:
         res["cpu_baseline"] = {"value": round(1.0 / dt, 5), "unit": "iterations/s", "cores": th, "kind": "port",
                                "sample": f"{its} full Lloyd iteration(s) (KMeans::fit body) over all {n} points "
-                                         f"and {kc} centroids, {dt:.2f} s each on {th} threads ({cpu_model()})"}
+                                         f"and {kc} centroids, {dt:.2f} s each on {th} threads (affinity mask) "
+                                         f"({cpu_model()})"}
         res["speedup_vs_cpu"] = round(res["value"] / res["cpu_baseline"]["value"], 1)
     return res
 
@@ -513,20 +607,32 @@ def bench_knn_workload(vh, key, steps, warmup, with_cpu):
            "host_buffers": {"value": round(w["nq"] * 1e3 / host_ms, 2), "unit": "queries/s", "ms": round(host_ms, 3),
                             "note": "one batch through the host-buffer entry point (PCIe copies included), "
                                     "median of 3 after a warm-up call; not the headline value"}}
-    if with_cpu:
-        if ham:
-            import oracle
+    import oracle
 
+    k = w["k"]
+    if ham:
+        if with_cpu:
             sub = 500_000
             un_b = oracle.unpack_bits(base[:sub])
             un_q = oracle.unpack_bits(q)
-            cb = cpu_knn_baseline(un_b, un_q, w["k"], "hamming")
+            cb, _ = cpu_knn_baseline(un_b, un_q, k, "hamming")
+            del un_b, un_q
             cb["value"] = round(cb["value"] * sub / w["n"], 4)
             cb["sample"] = (f"reference semantics (thresholded float Hamming over codes unpacked to 0/1 floats) "
                             f"against {sub} of the {w['n']} codes, rate scaled by {sub}/{w['n']}; " + cb["sample"])
             out["cpu_baseline"] = cb
+        # parity over the full base: the oracle's popcount search on a query sample, bit-exact
+        ref = oracle.hamming_packed_knn(base, q[:512], k, threads=cpu_threads())
+        out["parity"] = knn_parity(base, q, ids, dist, ref, k, "hamming", 0.0, 0.0, min_recall=1.0)
+    else:
+        if with_cpu:
+            out["cpu_baseline"], ref = cpu_knn_baseline(base, q, k, w["metric"])
         else:
-            out["cpu_baseline"] = cpu_knn_baseline(base, q, w["k"], w["metric"])
+            ref = oracle.knn_search_batch(base, q[:64], k, w["metric"], threads=cpu_threads())
+        # distances within 1e-4 relative; integer data is exact in every summation order
+        exact = w["gen"] == "uniform_int"
+        out["parity"] = knn_parity(base, q, ids, dist, ref, k, w["metric"], 0.0 if exact else 1e-4,
+                                   0.0 if exact else 1e-6)
     return out
 
 
@@ -563,14 +669,24 @@ def main():
                "ms_per_step": r["ms_per_iteration"], "higher_is_better": True, "scaling": "strong",
                "vs_baseline": None, "dtype": "f32", "data": "synthetic",
                "config": {"workload": r["workload"], "parallelism": "single GPU"}, "roofline": r["roofline"],
-               "cpu_baseline": r.get("cpu_baseline")}
+               "cpu_baseline": r.get("cpu_baseline"), "parity": r["parity"]}
     else:
         key = "l2int" if args.workload == "default" else args.workload
         out = bench_knn_workload(vh, key, args.steps, args.warmup, not args.no_cpu)
         if args.workload == "default":
             out["kmeans"] = bench_kmeans(vh, 10, not args.no_cpu)
+            # the other benchmark workloads, each with its roofline, CPU baseline and parity
+            for extra in ("cos768", "hamming", "l1", "linf"):
+                r = bench_knn_workload(vh, extra, args.steps, args.warmup, not args.no_cpu)
+                out[extra] = {kk: r[kk] for kk in ("value", "unit", "ms_per_step", "dtype", "config", "roofline",
+                                                   "host_buffers", "cpu_baseline", "parity") if kk in r}
     out["config"]["device"] = ctx.device_name()
     print(json.dumps(out))
+    bad = [name for name, part in [("top", out)] + [(kk, v) for kk, v in out.items() if isinstance(v, dict)]
+           if isinstance(part.get("parity"), dict) and not part["parity"]["ok"]]
+    if bad:
+        log(f"parity check failed: {bad}")
+        sys.exit(3)
 
 
 if __name__ == "__main__":
