@@ -2,7 +2,7 @@
  * vector_hip.hpp -- C++ host API over the C ABI of vector_hip.h, mirroring the Rust API of the
  * reference's GPU hot path (crate vector-cuda) so that code written against it reads the same:
  *
- *   CudaDeviceContext     vector-cuda/src/device.rs:81-256      (hardware only, no emulator)
+ *   CudaDeviceContext     vector-cuda/src/device.rs:81-256      (an emulator context is a descriptor only)
  *   CudaKnnEngine         vector-cuda/src/knn.rs:45-401
  *   DistributedKnnEngine  vector-cuda/src/ddp/distributed_knn.rs:24-262, GpuShardMode :14-19
  *   CollectiveOps         vector-cuda/src/ddp/collective.rs:115-159 (top_k_reduce only)
@@ -74,15 +74,16 @@ struct SearchResult {
 class CudaError : public std::runtime_error {
 public:
     enum class Kind { InsufficientDevices, DeviceNotFound, DriverError, HardwareNotAvailable, InvalidConfig, EmptyIndex };
-    CudaError(Kind kind, const std::string &msg, size_t requested = 0, size_t available = 0)
-        : std::runtime_error(msg), kind_(kind), requested_(requested), available_(available) {}
+    CudaError(Kind kind, const std::string &msg, size_t requested = 0, size_t available = 0, size_t ordinal = 0)
+        : std::runtime_error(msg), kind_(kind), requested_(requested), available_(available), ordinal_(ordinal) {}
     Kind kind() const { return kind_; }
     size_t requested() const { return requested_; } /* InsufficientDevices */
     size_t available() const { return available_; } /* InsufficientDevices */
+    size_t ordinal() const { return ordinal_; }     /* DeviceNotFound */
 
 private:
     Kind kind_;
-    size_t requested_, available_;
+    size_t requested_, available_, ordinal_;
 };
 
 namespace detail {
@@ -95,7 +96,10 @@ inline void check(int status) {
             vhip_last_error_devices(&r, &a);
             throw CudaError(CudaError::Kind::InsufficientDevices, msg, r, a);
         }
-        case VHIP_ERR_DEVICE_NOT_FOUND: throw CudaError(CudaError::Kind::DeviceNotFound, msg);
+        case VHIP_ERR_DEVICE_NOT_FOUND: {
+            const int o = vhip_last_error_ordinal();
+            throw CudaError(CudaError::Kind::DeviceNotFound, msg, 0, 0, o < 0 ? 0 : (size_t)o);
+        }
         case VHIP_ERR_HARDWARE_NOT_AVAILABLE: throw CudaError(CudaError::Kind::HardwareNotAvailable, msg);
         case VHIP_ERR_INVALID_CONFIG: throw CudaError(CudaError::Kind::InvalidConfig, msg);
         case VHIP_ERR_EMPTY_INDEX: throw CudaError(CudaError::Kind::EmptyIndex, msg);
@@ -121,13 +125,28 @@ inline std::vector<std::vector<SearchResult>> to_lists(size_t nq, size_t k, cons
 class CudaDeviceContext {
 public:
     static size_t device_count() { return (size_t)vhip_device_count(); }
-    /* CudaDeviceContext::new(): ordinal 0 */
-    CudaDeviceContext() : CudaDeviceContext(0) {}
+    /* CudaDeviceContext::new() (device.rs:120-122): with_ordinal(0) */
+    CudaDeviceContext() : CudaDeviceContext(with_ordinal(0)) {}
+    /* device.rs:127-170: the GPU's context, or DeviceNotFound / DriverError */
     static CudaDeviceContext with_ordinal_strict(size_t ordinal) { return CudaDeviceContext(ordinal); }
+    /* device.rs:188-221: the GPU's context, or a software-emulator descriptor
+     * (is_hardware_available() false) when that ordinal has no usable gfx950 device.  Engines
+     * built on such an ordinal throw DeviceNotFound; nothing runs on the CPU in its place. */
+    static CudaDeviceContext with_ordinal(size_t ordinal) {
+        char buf[256];
+        size_t mem = 0;
+        if (vhip_device_info((int)ordinal, buf, sizeof buf, &mem) != VHIP_OK) return software_emulator(ordinal);
+        return CudaDeviceContext(ordinal, buf, mem, true);
+    }
+    /* device.rs:173-185: a descriptor only (no device, total memory 0) */
+    static CudaDeviceContext software_emulator(size_t ordinal) {
+        return CudaDeviceContext(ordinal, "HIP Software Emulator (GPU " + std::to_string(ordinal) + ", no device)", 0,
+                                 false);
+    }
     size_t device_id() const { return id_; }
     const std::string &device_name() const { return name_; }
     size_t total_memory_bytes() const { return mem_; }
-    bool is_hardware_available() const { return true; }
+    bool is_hardware_available() const { return hw_; }
 
 private:
     explicit CudaDeviceContext(size_t ordinal) : id_(ordinal) {
@@ -135,8 +154,11 @@ private:
         detail::check(vhip_device_info((int)ordinal, buf, sizeof buf, &mem_));
         name_ = buf;
     }
+    CudaDeviceContext(size_t ordinal, std::string name, size_t mem, bool hw)
+        : id_(ordinal), mem_(mem), name_(std::move(name)), hw_(hw) {}
     size_t id_ = 0, mem_ = 0;
     std::string name_;
+    bool hw_ = true;
 };
 
 /* ---- CudaKnnEngine (knn.rs:45-401) ------------------------------------------------------- */
@@ -327,6 +349,8 @@ inline CudaKMeansResult kmeans_fit(size_t ordinal, const float *data, size_t len
 }
 }  // namespace detail
 
+/* CudaKMeansEngine (kmeans.rs:36-466).  fit() runs on the GPU.  fit_cpu() (kmeans.rs:240-357)
+ * is the reference's host Rust code and stays there: this header mirrors the GPU path only. */
 class CudaKMeansEngine {
 public:
     CudaKMeansEngine() : ctx_(CudaDeviceContext()) {}

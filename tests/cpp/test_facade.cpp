@@ -158,6 +158,17 @@ static void host_tests() {
         auto e = expect_error([&] { DistributedKMeansEngine::try_new(req); });
         CHECK(e.kind() == CudaError::Kind::InsufficientDevices && e.requested() == req && e.available() == avail);
     });
+    run("device context with_ordinal / software_emulator (device.rs:173-221)", [] {
+        const size_t missing = CudaDeviceContext::device_count() + 100;
+        auto emu = CudaDeviceContext::with_ordinal(missing);
+        CHECK(!emu.is_hardware_available() && emu.device_id() == missing && emu.total_memory_bytes() == 0);
+        CHECK(!emu.device_name().empty());
+        auto sw = CudaDeviceContext::software_emulator(3);
+        CHECK(!sw.is_hardware_available() && sw.device_id() == 3 && sw.total_memory_bytes() == 0);
+        auto e = expect_error([&] { CudaDeviceContext::with_ordinal_strict(missing); });
+        CHECK(e.kind() == CudaError::Kind::DeviceNotFound || e.kind() == CudaError::Kind::HardwareNotAvailable);
+        if (e.kind() == CudaError::Kind::DeviceNotFound) CHECK(e.ordinal() == missing);
+    });
     run("ddp_kmeans_getters (distributed_kmeans.rs:619)", [] {
         CHECK(DistributedKMeansEngine::emulator(6).num_gpus() == 6);
     });
@@ -344,6 +355,17 @@ static void gpu_tests() {
         for (size_t i = 0; i < data.size(); ++i) data[i] = (float)i * 0.01f;
         auto r = CudaKMeansEngine().fit(data, 128, 4, 5, 1e-3f, DistanceMetric::L2Squared);
         CHECK(r.k == 4 && r.dimension == 128);
+    });
+    run("test_device_context (device.rs:329)", [] {
+        CudaDeviceContext ctx;
+        CHECK(ctx.device_id() == 0 && ctx.total_memory_bytes() > 0 && !ctx.device_name().empty());
+        CHECK(ctx.is_hardware_available());
+        auto w = CudaDeviceContext::with_ordinal(0);
+        CHECK(w.device_name() == ctx.device_name() && w.total_memory_bytes() == ctx.total_memory_bytes());
+        auto copy = ctx;
+        CHECK(copy.total_memory_bytes() == ctx.total_memory_bytes());
+        CudaKnnEngine e({1, 2, 3, 4}, 2, DistanceMetric::L2Squared);
+        CHECK(e.context().device_id() == 0 && e.context().is_hardware_available());
     });
     run("cuda_kmeans_engine_context (kmeans.rs:573)", [] {
         CudaKMeansEngine eng;

@@ -108,3 +108,22 @@ def test_top_k_reduce_matches_reference_kats_and_oracle(oracle):
                                             vh.DistanceMetric.CosineSimilarity if trial % 2 else
                                             vh.DistanceMetric.L2Squared)
         assert [r.id for r in got] == list(oi) and np.allclose([r.distance for r in got], od)
+
+
+def test_device_context_emulator_descriptor():
+    """CudaDeviceContext.with_ordinal / new (device.rs:120-221) return a software-emulator
+    descriptor for an ordinal with no usable device; with_ordinal_strict raises.  A descriptor
+    runs nothing: an engine on that ordinal raises instead of falling back to the CPU."""
+    import vector_hip as vh
+
+    missing = vh.CudaDeviceContext.device_count() + 100
+    c = vh.CudaDeviceContext.with_ordinal(missing)
+    assert not c.is_hardware_available() and c.device_id() == missing and c.total_memory_bytes() == 0
+    s = vh.CudaDeviceContext.software_emulator(3)
+    assert not s.is_hardware_available() and s.device_id() == 3
+    with pytest.raises((vh.DeviceNotFound, vh.HardwareNotAvailable)) as ei:
+        vh.CudaDeviceContext.with_ordinal_strict(missing)
+    if isinstance(ei.value, vh.DeviceNotFound):
+        assert ei.value.ordinal == missing
+    with pytest.raises((vh.DeviceNotFound, vh.HardwareNotAvailable)):
+        vh.CudaKnnEngine.with_ordinal(np.zeros((4, 2), np.float32), 2, vh.DistanceMetric.L2Squared, missing)

@@ -26,6 +26,11 @@ void set_insufficient(size_t requested, size_t available) {
     t_err = "Insufficient hardware GPUs: requested " + std::to_string(requested) + " device(s), but only " +
             std::to_string(available) + " physical GPU(s) found";
 }
+int set_device_not_found(int ordinal, const std::string &msg) {
+    t_ordinal = ordinal;
+    t_err = msg;
+    return VHIP_ERR_DEVICE_NOT_FOUND;
+}
 void clear_error() { t_err.clear(); }
 
 int device_count() {
@@ -49,15 +54,12 @@ int open_device(int ordinal) {
         return set_error(VHIP_ERR_HARDWARE_NOT_AVAILABLE, "No HIP-capable GPU hardware devices found on this system");
     }
     if (ordinal < 0 || ordinal >= n) {
-        t_ordinal = ordinal;
-        return set_error(VHIP_ERR_DEVICE_NOT_FOUND,
-                         "HIP device with ordinal " + std::to_string(ordinal) + " was not found");
+        return set_device_not_found(ordinal, "HIP device with ordinal " + std::to_string(ordinal) + " was not found");
     }
     hipDeviceProp_t p;
     VH_HIP(hipGetDeviceProperties(&p, ordinal));
     if (std::strncmp(p.gcnArchName, "gfx950", 6) != 0) {
-        t_ordinal = ordinal;
-        return set_error(VHIP_ERR_DEVICE_NOT_FOUND, "HIP device " + std::to_string(ordinal) + " is " +
+        return set_device_not_found(ordinal, "HIP device " + std::to_string(ordinal) + " is " +
                                                        p.gcnArchName + ", this library is built for gfx950");
     }
     VH_HIP(hipSetDevice(ordinal));
@@ -354,8 +356,8 @@ int vhip_device_count(void) { return device_count(); }
 int vhip_device_info(int ordinal, char *name, size_t name_len, size_t *total_memory_bytes) {
     const int avail = device_count();
     if (ordinal < 0 || ordinal >= avail)
-        return set_error(VHIP_ERR_DEVICE_NOT_FOUND,
-                         "HIP device with ordinal " + std::to_string(ordinal) + " was not found or could not be initialized");
+        return set_device_not_found(
+            ordinal, "HIP device with ordinal " + std::to_string(ordinal) + " was not found or could not be initialized");
     hipDeviceProp_t p;
     VH_HIP(hipGetDeviceProperties(&p, ordinal));
     if (name && name_len) {

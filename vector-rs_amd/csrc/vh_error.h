@@ -11,6 +11,8 @@ namespace vh {
 int set_error(int code, const std::string &msg);
 // Records an InsufficientDevices{requested, available} error.
 void set_insufficient(size_t requested, size_t available);
+// Records a DeviceNotFound{ordinal} error and returns its status.
+int set_device_not_found(int ordinal, const std::string &msg);
 void clear_error();
 
 }  // namespace vh

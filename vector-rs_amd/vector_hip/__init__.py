@@ -302,7 +302,10 @@ def _to_lists(ids, dist, lens) -> List[List[SearchResult]]:
 
 
 class CudaDeviceContext:
-    """device.rs:81-256 (hardware only: there is no software emulator context)."""
+    """device.rs:81-256.  The constructor is with_ordinal_strict (DeviceNotFound when the ordinal
+    has no usable gfx950 device); with_ordinal / new return a software-emulator descriptor
+    instead, as the reference does.  A descriptor runs nothing: engines on its ordinal raise
+    DeviceNotFound rather than falling back to the CPU."""
 
     def __init__(self, ordinal: int = 0):
         name = ctypes.create_string_buffer(256)
@@ -311,6 +314,7 @@ class CudaDeviceContext:
         self._id = ordinal
         self._name = name.value.decode()
         self._mem = mem.value
+        self._hw = True
 
     @staticmethod
     def device_count() -> int:
@@ -319,6 +323,29 @@ class CudaDeviceContext:
     @classmethod
     def with_ordinal_strict(cls, ordinal: int) -> "CudaDeviceContext":
         return cls(ordinal)
+
+    @classmethod
+    def with_ordinal(cls, ordinal: int) -> "CudaDeviceContext":
+        """device.rs:188-221"""
+        try:
+            return cls(ordinal)
+        except CudaError:
+            return cls.software_emulator(ordinal)
+
+    @classmethod
+    def new(cls) -> "CudaDeviceContext":
+        """device.rs:120-122"""
+        return cls.with_ordinal(0)
+
+    @classmethod
+    def software_emulator(cls, ordinal: int) -> "CudaDeviceContext":
+        """device.rs:173-185: a descriptor with no device and total memory 0."""
+        c = cls.__new__(cls)
+        c._id = ordinal
+        c._name = f"HIP Software Emulator (GPU {ordinal}, no device)"
+        c._mem = 0
+        c._hw = False
+        return c
 
     def device_id(self) -> int:
         return self._id
@@ -330,7 +357,7 @@ class CudaDeviceContext:
         return self._mem
 
     def is_hardware_available(self) -> bool:
-        return True
+        return self._hw
 
 
 class _Profiled:
@@ -415,6 +442,10 @@ class CudaKnnEngine(_Profiled):
         """As search_batch_device, with working memory from the library's fixed per-GPU array of
         NOALLOC_SCRATCH_BYTES (no device allocation); same results."""
         _check(_lib.vhip_knn_search_batch_device_noalloc(self._h, d_queries, nq, k, d_ids, d_dist))
+
+    def context(self) -> CudaDeviceContext:
+        """knn.rs:381-383: the context of the engine's GPU."""
+        return CudaDeviceContext(_lib.vhip_knn_device_id(self._h))
 
     def dimension(self) -> int:
         return _lib.vhip_knn_dimension(self._h)
@@ -590,7 +621,8 @@ def _kmeans_fit(data, dimension, k, max_iters, tolerance, metric, init, init_mod
 
 class CudaKMeansEngine:
     """kmeans.rs:37-467 -- fit() runs on the GPU; init is k-means++ seeded by `seed`
-    unless explicit init centroids are given."""
+    unless explicit init centroids are given.  fit_cpu (kmeans.rs:240-357) is the reference's
+    host code and is not mirrored: this binding covers the GPU path only."""
 
     def __init__(self, ordinal: int = 0):
         self._ord = ordinal
