@@ -256,18 +256,20 @@ __global__ __launch_bounds__(256) void k_update_finalize(int k, int dpad, int di
 // Assign rows of the centroids, one wave per row of kpad: cent = craw - shift (shift may be
 // null), the norm of that row (norm_kind 1 squared, 2 plain; deterministic lane-strided sum and
 // xor butterfly), max_d |craw_d| (cabs), and the largest norm value (cmax, u32 bits of a
-// non-negative float, atomic max; cleared by the caller).  Rows past k are NaN.
+// non-negative float, atomic max; cleared by the caller).  Rows past k are NaN, or with pad_big
+// (squared L2) zero rows of norm FLT_MAX, whose assign scores are FLT_MAX (finite, so they never
+// disturb the best / second-best tracking).
 __global__ __launch_bounds__(256) void k_cent_prep(int k, int kpad, int dpad, const float *__restrict__ craw,
                                                    const float *__restrict__ shift, float *__restrict__ cent,
-                                                   float *__restrict__ cnorm, int norm_kind, float *__restrict__ cabs,
-                                                   uint32_t *__restrict__ cmax) {
+                                                   float *__restrict__ cnorm, int norm_kind, int pad_big,
+                                                   float *__restrict__ cabs, uint32_t *__restrict__ cmax) {
     const int lane = threadIdx.x & 63;
     const int c = (int)((blockIdx.x * (size_t)blockDim.x + threadIdx.x) >> 6);
     if (c >= kpad) return;
     float *orow = cent + (size_t)c * dpad;
     if (c >= k) {
-        for (int d = lane; d < dpad; d += 64) orow[d] = __builtin_nanf("");
-        if (lane == 0) cnorm[c] = __builtin_nanf("");
+        for (int d = lane; d < dpad; d += 64) orow[d] = pad_big ? 0.0f : __builtin_nanf("");
+        if (lane == 0) cnorm[c] = pad_big ? 0x1.fffffep127f : __builtin_nanf("");
         return;
     }
     float ss = 0.0f, am = 0.0f;
@@ -558,13 +560,14 @@ static void km_prep_centroids(vhip_kmeans *K) {
     launch_fill_u32(K->cmax.as<uint32_t>(), 1, 0u, K->stream);
     hipLaunchKernelGGL(k_cent_prep, dim3(ceil_div((long)K->kpad, 4)), dim3(256), 0, K->stream, (int)K->k, (int)K->kpad,
                        (int)K->dpad, K->craw.as<float>(), K->shifted ? K->shift.as<float>() : nullptr,
-                       K->cent.as<float>(), K->cnorm.as<float>(), km_norm_kind(K->metric), K->cabs.as<float>(),
-                       K->cmax.as<uint32_t>());
+                       K->cent.as<float>(), K->cnorm.as<float>(), km_norm_kind(K->metric), K->metric == L2 ? 1 : 0,
+                       K->cabs.as<float>(), K->cmax.as<uint32_t>());
 }
 
 // Sets k centroids from device rows d_c (row stride `row_stride` floats: dim, or dpad for rows
-// already padded; d_c may be craw itself).  Assign rows are padded to a multiple of 256 with NaN
-// rows: their scores are NaN and never win the argmin.
+// already padded; d_c may be craw itself).  Assign rows are padded to a multiple of 256 with rows
+// that never win the argmin: NaN rows (NaN scores), or for squared L2 zero rows of norm FLT_MAX
+// (scores FLT_MAX; the assignment also rejects any row past k).
 static int km_set_centroids_dev(vhip_kmeans *K, const float *d_c, size_t k, size_t row_stride) {
     const size_t kpad = round_up(k, kRowAlign);
     if (d_c != K->craw.as<float>()) VH_CHECK(K->craw.ensure(K->dev, k * K->dpad * sizeof(float)));
@@ -608,6 +611,7 @@ static int km_assign(vhip_kmeans *K) {
         cert.fix = K->fix.as<int32_t>();
         cert.nfix = K->nfix.as<uint32_t>();
         cert.devmax = K->devmax.as<float>();
+        cert.k = (int)K->k;
         launch_kmeans_assign(K->metric, K->cent.as<float>(), K->cnorm.as<float>(), (int)K->kpad, K->pts.as<float>(),
                              K->pnorm.as<float>(), n, (int)K->dpad, K->assign.as<int32_t>(), K->inertia.as<float>(),
                              K->pos.as<int32_t>(), K->counts.as<int32_t>(), cert, K->grid_cap, s);

@@ -245,6 +245,7 @@ struct ScanArgs {
     int32_t *fix;
     uint32_t *nfix;
     float *devmax;        // squared L2: per-cluster bound of |x_d - c_d| over its points
+    int nrows_valid;      // rows past this (padding) never take a point
 };
 
 // -0.0 and +0.0 are the same distance; give them one key.
@@ -467,9 +468,16 @@ __device__ __forceinline__ void dense_stage(const floatx16 (&acc)[2][2], NF nf, 
     }
 }
 
-// Running best and second-best of a sequence: the quiet NaN of padding rows is ignored.
+// Running best and second-best of a sequence.  Dot product and cosine: the quiet NaN of padding
+// rows is ignored (a compare and select per score).  Squared L2: padding centroids score FLT_MAX
+// (zero rows of norm FLT_MAX), so plain max / min keep the pair.  Non-finite input makes the
+// point's error bound NaN or infinite, which leaves it uncertified for the direct-form fix-up.
+template <int M>
 __device__ __forceinline__ void second_min(float &m, float &m2, float u) {
-    m2 = fminf(m2, u < m ? m : u);
+    if constexpr (M == L2)
+        m2 = fminf(m2, fmaxf(m, u));
+    else
+        m2 = fminf(m2, u < m ? m : u);
     m = fminf(m, u);
 }
 // Folds a block's (best m, second m2) into the column's running state; `index` gives the block row
@@ -524,7 +532,7 @@ __device__ __forceinline__ void assign_stage(floatx16 (&acc)[2][2], NF nf, EpiSt
                         u = den > 1e-9f ? -(dot / den) : canon(0.0f * dot);
                     }
                     acc[rb][cb][4 * g + j] = u;
-                    second_min(m, m2, u);
+                    second_min<M>(m, m2, u);
                 }
             }
         take_min(st, cb, m, m2, [&](int &idx) {
@@ -542,7 +550,7 @@ __device__ __forceinline__ void assign_stage(floatx16 (&acc)[2][2], NF nf, EpiSt
 // GEMM-form argmin is the argmin of the exact distances, and the point takes its ticket in its
 // cluster.  Otherwise (near-ties, or scores too coarse on badly conditioned data) it goes to the
 // fix-up list, whose direct-form pass assigns it.
-template <int M, int RW>
+template <int M, int RW, bool PACKED = false>
 __device__ __forceinline__ void assign_finish(EpiState &st, const ScanArgs &a, int col0, int wr, int wc, int l32,
                                               int h, float *s_xs, float *s_xs2, int *s_xi) {
 #pragma unroll
@@ -581,7 +589,12 @@ __device__ __forceinline__ void assign_finish(EpiState &st, const ScanArgs &a, i
                 } else {
                     e = a.err_coeff;
                 }
-                if (!(st.bs2[cb] - st.bs[cb] > 2.0f * e)) {
+                // the register-fed kernel's squared-L2 scores are packed keys (assign_half): the
+                // margin also covers their 15-ulp perturbation; a padding row never certifies
+                float margin = 2.0f * e;
+                if constexpr (M == L2 && PACKED)
+                    margin += 0x1p-18f * (fabsf(st.bs[cb]) + fabsf(st.bs2[cb])) + 0x1p-140f;
+                if (!(st.bs2[cb] - st.bs[cb] > margin) || c >= a.nrows_valid) {
                     a.fix[atomicAdd(a.nfix, 1u)] = p;
                 } else {
                     if constexpr (M == L2) {
@@ -1017,8 +1030,46 @@ __device__ __forceinline__ void dense_group(const floatx16 (&acc2)[2], floatx4 n
 // ASSIGN for one half: per column, the minimum over the half's 16 rows held by the lane, then
 // the first (lowest) row reaching it; halves and stages are visited in ascending row order with
 // a strict '<', so the lowest index wins ties (kmeans.cu:110-114).
-template <int M>
+template <int M, bool FUSED = false>
 __device__ __forceinline__ void assign_half(floatx16 (&acc2)[2], const floatx4 (&n)[4], EpiState &st, long rb0) {
+    if constexpr (M == L2) {
+        // Squared L2: each score carries its row within the half (0..15) in its 4 low mantissa
+        // bits, so one min yields the best score and its row, and one med3 the second best (4
+        // VALU operations per score, no search for the row).  A key differs from its score by
+        // at most 15 ulp; the certification at item end widens its margin by 2^-18 of the scores
+        // to cover that, so a certified argmin is the argmin of the unpacked scores.  Exact ties
+        // are near-ties and go to the direct-form fix-up, which applies the lowest-index rule.
+        // Padding centroids score FLT_MAX (finite keys).  Denormals are preserved (the packed
+        // bits of scores near zero survive the min).  Both the min and the second come from
+        // v_med3 (no canonicalisation of the keys); a non-finite score only arises from
+        // non-finite or overflowing input, whose margin at item end is infinite or NaN, so such a
+        // point is never certified.
+        // -inf the compiler cannot see, so that med3(m, key, -inf) stays a med3 (folded to a
+        // min it would canonicalise every key first)
+        float neg_inf;
+        asm("v_mov_b32 %0, 0xff800000" : "=v"(neg_inf));
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) {
+            float m = INFINITY, m2 = INFINITY;
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    // FUSED: the accumulators already hold ||c||^2 - 2 c.x
+                    const float u = FUSED ? acc2[cb][4 * g + j] : fmaf(-2.0f, acc2[cb][4 * g + j], n[g][j]);
+                    const float key = __uint_as_float((__float_as_uint(u) & ~15u) | (uint32_t)(4 * g + j));
+                    m2 = __builtin_amdgcn_fmed3f(m, m2, key);
+                    m = __builtin_amdgcn_fmed3f(m, key, neg_inf);
+                }
+            const uint32_t r = __float_as_uint(m) & 15u;
+            const int row = (int)rb0 + 8 * (int)(r >> 2) + (int)(r & 3u);
+            st.bs2[cb] = fminf(fminf(st.bs2[cb], m2), fmaxf(st.bs[cb], m));
+            const bool better = m < st.bs[cb];
+            st.bi[cb] = better ? row : st.bi[cb];
+            st.bs[cb] = better ? m : st.bs[cb];
+        }
+        return;
+    }
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb) {
         float m = INFINITY, m2 = INFINITY;
@@ -1037,7 +1088,7 @@ __device__ __forceinline__ void assign_half(floatx16 (&acc2)[2], const floatx4 (
                     u = den > 1e-9f ? -(dot / den) : canon(0.0f * dot);
                 }
                 acc2[cb][4 * g + j] = u;
-                second_min(m, m2, u);
+                second_min<M>(m, m2, u);
             }
         take_min(st, cb, m, m2, [&](int &idx) {
             idx = 15;
@@ -1052,8 +1103,9 @@ template <int MODE, int M, int NK>
 __global__ __launch_bounds__(512, 1) void k_mfma_hs(ScanArgs a) {
     constexpr int RW = 4, TR = 256, D = 32 * NK;
     // squared-L2 scan: accumulators start from the row norms and the column tile holds -2 q, so
-    // they end as ||x||^2 - 2 q.x (the filter's test value) with no epilogue arithmetic
-    constexpr bool FUSE = M == L2 && MODE != kAssign;
+    // they end as ||x||^2 - 2 q.x (the filter's test value, and the assign score) with no
+    // epilogue arithmetic
+    constexpr bool FUSE = M == L2;
     __shared__ floatx4 sB[kTileCols * 8 * NK];
     __shared__ uint32_t s_qcnt[MODE == kFilter ? kTileCols : 1];
     __shared__ uint2 s_slot[MODE == kFilter ? kTileCols * kRegSlots : 1];
@@ -1150,7 +1202,7 @@ __global__ __launch_bounds__(512, 1) void k_mfma_hs(ScanArgs a) {
     // one basic block and the scheduler can interleave them).
     auto epi = [&](floatx16 (&ac)[2], const floatx4 (&n)[4], long srs, int hf, int g0, int g1, bool enable) {
         if constexpr (MODE == kAssign) {
-            if (g0 == 0 && enable) assign_half<M>(ac, n, st, srs + 64 * wr + 32 * hf + 4 * h);
+            if (g0 == 0 && enable) assign_half<M, FUSE>(ac, n, st, srs + 64 * wr + 32 * hf + 4 * h);
         } else {
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
@@ -1240,7 +1292,8 @@ __global__ __launch_bounds__(512, 1) void k_mfma_hs(ScanArgs a) {
             // drain: this stage's half 1, then the item's cross-wave work
             epi(acc[1], nrm[1], rs, 1, 0, 4, true);
             if constexpr (MODE == kFilter) filter_flush<kRegSlots>(a, col0, r_lo, s_qcnt, s_slot);
-            else if constexpr (MODE == kAssign) assign_finish<M, RW>(st, a, col0, wr, wc, l32, h, s_xs, s_xs2, s_xi);
+            else if constexpr (MODE == kAssign)
+                assign_finish<M, RW, true>(st, a, col0, wr, wc, l32, h, s_xs, s_xs2, s_xi);
             if (!more) break;
             // every wave is past this item's MFMAs (barrier in the flush / combine above; DENSE
             // has none, so take one here)
@@ -1349,6 +1402,7 @@ void launch_kmeans_assign(int metric, const float *cent, const float *cnorm, int
     a.fix = cert.fix;
     a.nfix = cert.nfix;
     a.devmax = cert.devmax;
+    a.nrows_valid = cert.k > 0 ? cert.k : kpad;
     launch_metric<kAssign>(metric, a, grid_cap, s);
 }
 

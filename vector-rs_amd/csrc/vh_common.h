@@ -141,9 +141,11 @@ struct AssignCert {
     int32_t *fix = nullptr;
     uint32_t *nfix = nullptr;
     float *devmax = nullptr;
+    int k = 0;  // real centroid rows (the rest of kpad is padding); 0: all kpad rows
 };
 // MFMA k-means assignment (knn_gemm.hip); metric L2 / DOT / COS.  `cent` has kpad rows
-// (a multiple of 128, NaN padding rows), `pts` n rows padded to a multiple of 128 (zeros).
+// (a multiple of 128; padding rows are NaN, or for squared L2 zero rows of norm FLT_MAX), `pts` n
+// rows padded to a multiple of 128 (zeros).
 // cnorm / pnorm hold squared norms for L2 and dot product and L2 norms for COS.  Certified
 // points get assign, pos (ticket in counts) and, for dot / cosine, inertia (-dot, 1 - cos).
 void launch_kmeans_assign(int metric, const float *cent, const float *cnorm, int kpad, const float *pts,
