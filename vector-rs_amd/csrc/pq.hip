@@ -9,6 +9,8 @@
 //    (k = nprobe, best first), then the fused ADC scan k_ivfpq_scan (pq_scan.h).
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
+#include <cstring>
 #include <memory>
 #include <vector>
 
@@ -156,6 +158,8 @@ struct vhip_ivfpq {
     hipStream_t stream = nullptr;
     DevBuf d_coarse, d_cb, d_cbt, d_off, d_ids, d_codes;
     DevBuf d_q, d_pid, d_pdist, d_oid, d_odist, d_olen;
+    // list-major search: lists by decreasing size, and the per-search plan and pair results
+    DevBuf d_order, d_lcnt, d_loff, d_pairs, d_items, d_lctr, d_pout, d_tau;
     PinnedStager stager;
     KernelTimer timer;
     std::mutex mu;
@@ -274,6 +278,16 @@ static int ivfpq_init(vhip_ivfpq *X, int ordinal, size_t dim, int metric, const 
     VH_CHECK(upload(X->d_coarse, ordinal, X->coarse.data(), X->coarse.size() * 4, s));
     VH_CHECK(upload(X->d_cb, ordinal, X->codebooks.data(), X->codebooks.size() * 4, s));
     VH_CHECK(upload(X->d_off, ordinal, X->list_off.data(), X->list_off.size() * 4, s));
+    {
+        // lists by decreasing size (ties by id): the list-major search takes their work first
+        std::vector<uint32_t> order(nlist);
+        for (size_t c = 0; c < nlist; ++c) order[c] = (uint32_t)c;
+        std::stable_sort(order.begin(), order.end(), [&](uint32_t a, uint32_t b) {
+            return X->list_off[a + 1] - X->list_off[a] > X->list_off[b + 1] - X->list_off[b];
+        });
+        VH_CHECK(upload(X->d_order, ordinal, order.data(), nlist * 4, s));
+        VH_HIP(hipStreamSynchronize(s));  // `order` is released at the end of this block
+    }
     VH_CHECK(X->d_ids.ensure(ordinal, std::max<size_t>(4, total * 4)));
     VH_CHECK(X->d_codes.ensure(ordinal, std::max<size_t>(16, round_up(total * m_sub, 16))));
     if (total) {
@@ -288,6 +302,103 @@ static int ivfpq_init(vhip_ivfpq *X, int ordinal, size_t dim, int metric, const 
     VH_HIP(hipStreamSynchronize(s));
     VH_CHECK(vhip_knn_create(X->coarse.data(), nlist, dim, metric, ordinal, &X->probe));
     return VHIP_OK;
+}
+
+// ---- plan of the list-major search -----------------------------------------------------------
+__global__ void k_pair_count(const uint32_t *__restrict__ probes, int total, int nlist, uint32_t *__restrict__ cnt) {
+    for (int t = blockIdx.x * blockDim.x + threadIdx.x; t < total; t += gridDim.x * blockDim.x) {
+        const uint32_t c = probes[t];
+        if (c < (uint32_t)nlist) atomicAdd(&cnt[c], 1u);
+    }
+}
+
+// One workgroup of 1024 threads: in the order `order`, exclusive prefix sums of the lists' pair
+// counts (pair_off, indexed by list) and item counts (item_off, indexed by position), and the
+// number of items.
+__global__ __launch_bounds__(1024) void k_list_plan(const uint32_t *__restrict__ cnt, const uint32_t *__restrict__ order,
+                                                    int nlist, int qb, uint32_t *__restrict__ pair_off,
+                                                    uint32_t *__restrict__ item_off, uint32_t *__restrict__ n_items) {
+    __shared__ uint32_t sp[1024], si[1024];
+    __shared__ uint32_t carry_p, carry_i;
+    const int t = threadIdx.x;
+    if (t == 0) {
+        carry_p = 0;
+        carry_i = 0;
+    }
+    __syncthreads();
+    for (int base = 0; base < nlist; base += 1024) {
+        const int i = base + t;
+        uint32_t c = 0, l = 0;
+        if (i < nlist) {
+            l = order[i];
+            c = cnt[l];
+        }
+        const uint32_t items = (c + (uint32_t)qb - 1) / (uint32_t)qb;
+        sp[t] = c;
+        si[t] = items;
+        __syncthreads();
+        for (int o = 1; o < 1024; o <<= 1) {  // inclusive scans
+            const uint32_t vp = t >= o ? sp[t - o] : 0u, vi = t >= o ? si[t - o] : 0u;
+            __syncthreads();
+            sp[t] += vp;
+            si[t] += vi;
+            __syncthreads();
+        }
+        if (i < nlist) {
+            pair_off[l] = carry_p + sp[t] - c;
+            item_off[i] = carry_i + si[t] - items;
+        }
+        __syncthreads();
+        if (t == 1023) {
+            carry_p += sp[1023];
+            carry_i += si[1023];
+        }
+        __syncthreads();
+    }
+    if (t == 0) *n_items = carry_i;
+}
+
+// Pair ids q * nprobe + p into their list's range (the order within a list is arbitrary: every
+// pair's result is the same whichever item scans it).
+__global__ void k_pair_scatter(const uint32_t *__restrict__ probes, int total, int nlist,
+                               const uint32_t *__restrict__ pair_off, uint32_t *__restrict__ cursor,
+                               uint32_t *__restrict__ pairs) {
+    for (int t = blockIdx.x * blockDim.x + threadIdx.x; t < total; t += gridDim.x * blockDim.x) {
+        const uint32_t c = probes[t];
+        if (c < (uint32_t)nlist) pairs[pair_off[c] + atomicAdd(&cursor[c], 1u)] = (uint32_t)t;
+    }
+}
+
+// Work items of each list, in the order `order`: (list, first pair, pair count) in runs of qb.
+__global__ void k_item_fill(const uint32_t *__restrict__ cnt, const uint32_t *__restrict__ order,
+                            const uint32_t *__restrict__ item_off, const uint32_t *__restrict__ pair_off, int nlist,
+                            int qb, uint4 *__restrict__ items) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < nlist; i += gridDim.x * blockDim.x) {
+        const uint32_t l = order[i], c = cnt[l], po = pair_off[l], io = item_off[i];
+        for (uint32_t t = 0; t * (uint32_t)qb < c; ++t)
+            items[io + t] = make_uint4(l, po + t * (uint32_t)qb, min((uint32_t)qb, c - t * (uint32_t)qb), 0u);
+    }
+}
+
+void ivfpq_list_plan(const uint32_t *probes, int nq, int nprobe, int nlist, const uint32_t *order, uint32_t *cnt,
+                     uint32_t *cursor, uint32_t *pair_off, uint32_t *item_off, uint32_t *pairs, uint4 *items,
+                     uint32_t *n_items, hipStream_t s) {
+    const int total = nq * nprobe;
+    const unsigned gp = (unsigned)std::min(4096, (total + 255) / 256), gl = (unsigned)std::min(1024, (nlist + 255) / 256);
+    hipLaunchKernelGGL(k_pair_count, dim3(gp), dim3(256), 0, s, probes, total, nlist, cnt);
+    hipLaunchKernelGGL(k_list_plan, dim3(1), dim3(1024), 0, s, cnt, order, nlist, kListQb, pair_off, item_off, n_items);
+    hipLaunchKernelGGL(k_pair_scatter, dim3(gp), dim3(256), 0, s, probes, total, nlist, pair_off, cursor, pairs);
+    hipLaunchKernelGGL(k_item_fill, dim3(gl), dim3(256), 0, s, cnt, order, item_off, pair_off, nlist, kListQb, items);
+}
+
+// The list-major search applies to 16-byte code rows of 256 sub-centroids with the register-held
+// codebook (ds 4 or 8) and k <= kListMaxK; VHIP_IVFPQ_SCAN=query forces the query-major kernel.
+static bool list_path(const vhip_ivfpq *X, size_t k, size_t np) {
+    if (const char *e = std::getenv("VHIP_IVFPQ_SCAN"))
+        if (std::strcmp(e, "query") == 0) return false;
+    return X->reg && X->ks == 256 && X->m_sub == 16 && (X->ds == 4 || X->ds == 8) && k >= 1 &&
+           k <= (size_t)kListMaxK && np * k <= (size_t)kListMaxMerge && scan_capw(k) == 256 &&
+           sizeof(ListLds<kListThreads>) <= X->lds_limit;
 }
 
 // Coarse probe + scan for device-resident queries; results stay on the device.
@@ -330,6 +441,36 @@ static int ivfpq_search_dev(vhip_ivfpq *X, const float *d_q, size_t nq, size_t k
         return set_error(VHIP_ERR_INVALID_CONFIG, "k = " + std::to_string(k) + " needs " + std::to_string(lds) +
                                                       " bytes of LDS with this index, the device allows " +
                                                       std::to_string(X->lds_limit));
+    if (list_path(X, k, np)) {
+        const size_t total = nq * np;
+        VH_CHECK(X->d_lcnt.ensure(X->dev, 2 * X->nlist * 4));
+        VH_CHECK(X->d_loff.ensure(X->dev, 2 * X->nlist * 4));
+        VH_CHECK(X->d_pairs.ensure(X->dev, total * 4));
+        VH_CHECK(X->d_items.ensure(X->dev, total * sizeof(uint4)));
+        VH_CHECK(X->d_lctr.ensure(X->dev, 2 * 4));
+        VH_CHECK(X->d_pout.ensure(X->dev, total * k * 8));
+        VH_CHECK(X->d_tau.ensure(X->dev, nq * 8));
+        launch_fill_u32(X->d_tau.as<uint32_t>(), 2 * nq, 0xffffffffu, s);
+        uint32_t *cnt = X->d_lcnt.as<uint32_t>(), *ctr = X->d_lctr.as<uint32_t>();
+        launch_fill_u32(cnt, 2 * X->nlist, 0u, s);
+        launch_fill_u32(ctr, 2, 0u, s);
+        ivfpq_list_plan(A.probes, (int)nq, (int)np, (int)X->nlist, X->d_order.as<uint32_t>(), cnt, cnt + X->nlist,
+                        X->d_loff.as<uint32_t>(), X->d_loff.as<uint32_t>() + X->nlist, X->d_pairs.as<uint32_t>(),
+                        X->d_items.as<uint4>(), ctr, s);
+        VH_HIP(hipGetLastError());
+        ListArgs L{A, X->d_pairs.as<uint32_t>(), X->d_items.as<uint4>(), ctr, ctr + 1,
+                   X->d_pout.as<unsigned long long>(), X->d_tau.as<unsigned long long>()};
+        const int t = X->timer.begin(s);
+        if (X->metric == L2)
+            launch_ivfpq_lists_l2(L, (int)X->ds, X->cus, s);
+        else
+            launch_ivfpq_lists_ip(L, (int)X->ds, X->cus, s);
+        VH_HIP(hipGetLastError());
+        X->timer.end(t, s, 0.0, 0.0);  // the scan kernel alone
+        launch_ivfpq_list_merge(L, X->cus, s);
+        VH_HIP(hipGetLastError());
+        return VHIP_OK;
+    }
     const int t = X->timer.begin(s);
     if (!X->reg)
         launch_ivfpq_scan_mem(A, nv, X->cus, lds, s);

@@ -67,6 +67,54 @@ constexpr int kMetaWin = 128;  // probes whose list bounds are staged in LDS at 
 constexpr int ring_chunk_bytes(int nv) { return nv * 1024 + 256; }
 constexpr int ring_bytes(int nv) { return kScanWaves * ring_chunks(nv) * ring_chunk_bytes(nv); }
 
+// ---- list-major scan --------------------------------------------------------------------------
+// For 16-byte code rows (16 sub-spaces of 256 sub-centroids) and k <= kListMaxK the search runs
+// list-major: the (query, probe) pairs are grouped by list, and a work item is one list with up to
+// kListQb of the queries probing it.  Its kListQb ADC tables are built in LDS at once (thread j of
+// each half of the workgroup computes sub-centroid j's entries from its register-held codebook),
+// then the list's codes and ids stream once through a shared LDS ring of kListRing chunks of
+// kListChunk rows (global->LDS DMA, one barrier per chunk), and wave w scores every row against
+// its own pair's table with the summation order of compute_distance_with_lut (pq.rs:270-293),
+// keeping its k best.  A list's codes are therefore read once per kListQb probing queries instead
+// of once per probing query.  Each pair's k best go to pair_out; k_ivfpq_merge then sorts each
+// query's nprobe x k keys.  Keys are unique (score, id), so the result equals the query-major scan's.
+// The query's threshold carries across its pairs through tau_q: a finished pair lowers it to its
+// k-th key (atomic min), and a pair starts from it and re-reads it every chunk, so only the
+// first pairs of a query offer many candidates.  tau_q is always the k-th key of some of the
+// query's candidates, never below the final k-th, so no key of the final k best is filtered.
+
+// A workgroup of NT threads (NT / 64 waves) takes items of NT / 64 pairs and streams the list in
+// chunks of NT / 2 rows (the first half of the threads copies the code rows, the second the ids).
+constexpr int kListThreads = 256;    // 4 pairs per item; two workgroups per CU overlap their phases
+constexpr int kListQb = kListThreads / 64;
+constexpr int kListRing = 3;
+constexpr int kListRowBytes = 20;    // a 16-byte code row and its 4-byte id
+constexpr int kListMaxK = 128;
+constexpr int kListCapw = 256;       // candidate keys per wave
+constexpr int kListMaxMerge = 8192;  // nprobe x k keys sorted per query in the merge
+
+struct ListArgs {
+    ScanArgs s;                    // queries, lists, codebooks, outputs, k, nprobe, capw
+    const uint32_t *pairs;         // pair ids q * nprobe + p, grouped by list
+    const uint4 *items;            // (list, first pair, pair count, 0)
+    const uint32_t *n_items;       // device scalar: items of this search
+    uint32_t *work;                // device scalar: next item to take (zero before the launch)
+    unsigned long long *pair_out;  // nq * nprobe * k keys: each pair's k best, ~0 past its count
+    unsigned long long *tau_q;     // nq keys (~0 before the launch): the k-th best key found so far
+};
+
+// LDS of k_ivfpq_lists with NT threads, one object with the tables first: a wave's table then
+// lies at a constant address below 64 KB, and a lookup takes it as the instruction's offset.
+template <int NT>
+struct ListLds {
+    float lut[NT / 64][16 * 256];                              // the ADC tables of the item's pairs
+    unsigned long long cand[(NT / 64) * kListCapw];            // candidates (residuals before the scan)
+    unsigned char ring[kListRing * (NT / 2) * kListRowBytes];  // chunks: NT / 2 code rows, then ids
+    uint32_t tau[2 * (NT / 64)];                               // per wave, two slots: a DMA'd score word
+    uint32_t item;
+};
+
+
 namespace {
 
 // ---- direct-form metric of two short vectors: the formulas of scalar.rs:14-263 -------------
@@ -140,6 +188,31 @@ __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Workgroup barrier that publishes LDS data only: the wave's LDS operations complete, its
+// global->LDS DMAs in flight do not (a wave waits for the chunks it publishes with vmcnt first).
+// __syncthreads() would wait for every DMA in flight, since they write LDS.  The memory clobber
+// keeps the compiler from moving memory accesses across the barrier.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// Global->LDS DMA of 16 (4) bytes per lane from `src` to LDS byte address m0_base + 16 (4) x lane.
+// Written as asm so that the compiler neither counts the DMA among the loads it waits for nor
+// makes later LDS accesses wait for it: the caller waits with vmcnt before reading the data (M0
+// is restored; the DMA takes its value when issued).
+__device__ __forceinline__ void dma_lds16(const void *src, uint32_t m0_base) {
+    uint32_t sv;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+                 : "=&s"(sv)
+                 : "v"(src), "s"(m0_base)
+                 : "memory");
+}
+__device__ __forceinline__ void dma_lds4(const void *src, uint32_t m0_base) {
+    uint32_t sv;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %1, off\n\ts_mov_b32 m0, %0"
+                 : "=&s"(sv)
+                 : "v"(src), "s"(m0_base)
+                 : "memory");
 }
 
 // Ascending bitonic sort of s[0, P) (P a power of two) by `nthr` threads with index `tid`;
@@ -318,8 +391,8 @@ __device__ __forceinline__ void coarse_dma(const ScanArgs &A, const uint32_t *pc
         const int f = min(i0 + lane, pieces - 1);
         const int w = 4 * f / A.dim, d = 4 * f - w * A.dim;
         const uint32_t c = pc[w] != 0xffffffffu ? pc[w] : 0u;
-        __builtin_amdgcn_global_load_lds((const void *)(A.coarse + (size_t)c * A.dim + d),
-                                         (__attribute__((address_space(3))) void *)(s_cr + 4 * i0), 16, 0, 0);
+        const uint32_t dst = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)(s_cr + 4 * i0);
+        dma_lds16(A.coarse + (size_t)c * A.dim + d, __builtin_amdgcn_readfirstlane(dst));
     }
 }
 
@@ -340,13 +413,10 @@ template <int NV>
 __device__ __forceinline__ void ring_dma(const RingScan &R, int t) {
     const uint32_t i = min((uint32_t)((R.part + t * R.wpl) * 64 + R.lane), R.len - 1);
     const unsigned char *src = R.codes + (size_t)(R.beg + i) * (16 * NV);
-    unsigned char *dst = R.ring + (t % ring_chunks(NV)) * ring_chunk_bytes(NV);
+    const uint32_t dst = __builtin_amdgcn_readfirstlane(R.ring_lds + (t % ring_chunks(NV)) * ring_chunk_bytes(NV));
 #pragma unroll
-    for (int v = 0; v < NV; ++v)
-        __builtin_amdgcn_global_load_lds((const void *)(src + 16 * v),
-                                         (__attribute__((address_space(3))) void *)(dst + v * 1024), 16, 0, 0);
-    __builtin_amdgcn_global_load_lds((const void *)(R.ids + R.beg + i),
-                                     (__attribute__((address_space(3))) void *)(dst + NV * 1024), 4, 0, 0);
+    for (int v = 0; v < NV; ++v) dma_lds16(src + 16 * v, dst + v * 1024);
+    dma_lds4(R.ids + R.beg + i, dst + NV * 1024);
 }
 
 // Reads the code pieces and ids of two ring chunks at LDS byte addresses a0 and a1 (lane
@@ -380,6 +450,40 @@ __device__ __forceinline__ void lds_read_pair(uint32_t a0, uint32_t a1, uint32_t
     }
 }
 
+// Reads the 16-byte code rows at LDS byte addresses a + 1024 st and the ids at i + 256 st (rows
+// lane + 64 st of a chunk), st < R, with one wait.
+template <int R>
+__device__ __forceinline__ void lds_read_rows(uint32_t a, uint32_t i, uint4 (&w)[R], uint32_t (&id)[R]);
+template <>
+__device__ __forceinline__ void lds_read_rows<2>(uint32_t a, uint32_t i, uint4 (&w)[2], uint32_t (&id)[2]) {
+    asm volatile(
+        "ds_read_b128 %0, %4\n\t"
+        "ds_read_b128 %1, %4 offset:1024\n\t"
+        "ds_read_b32 %2, %5\n\t"
+        "ds_read_b32 %3, %5 offset:256\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(w[0]), "=&v"(w[1]), "=&v"(id[0]), "=&v"(id[1])
+        : "v"(a), "v"(i)
+        : "memory");
+}
+template <>
+__device__ __forceinline__ void lds_read_rows<4>(uint32_t a, uint32_t i, uint4 (&w)[4], uint32_t (&id)[4]) {
+    asm volatile(
+        "ds_read_b128 %0, %8\n\t"
+        "ds_read_b128 %1, %8 offset:1024\n\t"
+        "ds_read_b128 %2, %8 offset:2048\n\t"
+        "ds_read_b128 %3, %8 offset:3072\n\t"
+        "ds_read_b32 %4, %9\n\t"
+        "ds_read_b32 %5, %9 offset:256\n\t"
+        "ds_read_b32 %6, %9 offset:512\n\t"
+        "ds_read_b32 %7, %9 offset:768\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]), "=&v"(w[3]), "=&v"(id[0]), "=&v"(id[1]), "=&v"(id[2]),
+          "=&v"(id[3])
+        : "v"(a), "v"(i)
+        : "memory");
+}
+
 template <int NV>
 __device__ __forceinline__ float ring_score(const float *lut, const uint4 (&w)[NV]) {
     constexpr int KS = 256;
@@ -396,6 +500,38 @@ __device__ __forceinline__ float ring_score(const float *lut, const uint4 (&w)[N
         }
     }
     return total;
+}
+
+// ring_score<1> of one row against table `lut` at a constant LDS address: one SDWA shift gives
+// each byte times 4, and the table's address becomes the lookup's offset.  Same summation order.
+template <int B>
+__device__ __forceinline__ uint32_t byte_x4(uint32_t w) {
+    uint32_t a;
+    if constexpr (B == 0)
+        asm("v_lshlrev_b32_sdwa %0, 2, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_0" : "=v"(a) : "v"(w));
+    else if constexpr (B == 1)
+        asm("v_lshlrev_b32_sdwa %0, 2, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_1" : "=v"(a) : "v"(w));
+    else if constexpr (B == 2)
+        asm("v_lshlrev_b32_sdwa %0, 2, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_2" : "=v"(a) : "v"(w));
+    else
+        asm("v_lshlrev_b32_sdwa %0, 2, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_3" : "=v"(a) : "v"(w));
+    return a;
+}
+// Adds the quads h in [H0, H1) of ring_score<1>'s sum to `total` (H0 = 0, H1 = 4 from
+// total = 0 is the whole sum, in the same order).
+template <int H0, int H1>
+__device__ __forceinline__ void row_score_part(const float *lut, uint4 w, float &total) {
+    const char *base = reinterpret_cast<const char *>(lut);
+    const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int h = H0; h < H1; ++h) {
+        const char *L = base + 4 * h * 1024;
+        const float d0 = *reinterpret_cast<const float *>(L + byte_x4<0>(ww[h]));
+        const float d1 = *reinterpret_cast<const float *>(L + 1024 + byte_x4<1>(ww[h]));
+        const float d2 = *reinterpret_cast<const float *>(L + 2048 + byte_x4<2>(ww[h]));
+        const float d3 = *reinterpret_cast<const float *>(L + 3072 + byte_x4<3>(ww[h]));
+        total += (d0 + d1) + (d2 + d3);
+    }
 }
 
 // Chunks are taken two at a time.  Invariant: before the pair (t, t + 1) is read, the chunks
@@ -424,8 +560,14 @@ __device__ __forceinline__ void ring_scan(const ScanArgs &A, const RingScan &R, 
         const float tot1 = ring_score<NV>(lut, w1);
         const uint32_t i0 = (uint32_t)((R.part + t * R.wpl) * 64 + R.lane);
         const uint32_t i1 = (uint32_t)((R.part + (t + 1) * R.wpl) * 64 + R.lane);
-        offer<HIB>(tot0, i0 < R.len, id0, s_w, cnt, tau, lanes_below);
-        offer<HIB>(tot1, t + 1 < mine && i1 < R.len, id1, s_w, cnt, tau, lanes_below);
+        const bool v0 = i0 < R.len, v1 = t + 1 < mine && i1 < R.len;
+        // pre-filter (exact): a key below tau scores at most key_score(tau's score word)
+        const float thr = key_score((uint32_t)(tau >> 32));
+        const float h0 = (HIB ? -tot0 : tot0) + 0.0f, h1 = (HIB ? -tot1 : tot1) + 0.0f;
+        if (__ballot((v0 && !(h0 > thr)) || (v1 && !(h1 > thr))) != 0ull) {
+            offer<HIB>(tot0, v0, id0, s_w, cnt, tau, lanes_below);
+            offer<HIB>(tot1, v1, id1, s_w, cnt, tau, lanes_below);
+        }
     }
 }
 
@@ -461,6 +603,9 @@ __global__ __launch_bounds__(kScanThreads) void k_ivfpq_scan(ScanArgs A) {
             cbr[4 * v + 2] = f.z;
             cbr[4 * v + 3] = f.w;
         }
+        // landed before any DMA is issued: the compiler would otherwise wait for them at their
+        // first use with counts that also cover the DMAs, which it does not see
+        __builtin_amdgcn_s_waitcnt(VH_VMCNT(0));
     }
     constexpr bool hib = hib_metric(MT);
 
@@ -471,7 +616,7 @@ __global__ __launch_bounds__(kScanThreads) void k_ivfpq_scan(ScanArgs A) {
         for (int g0 = 0; g0 < A.nprobe; g0 += pg) {
             const int wbase = g0 - g0 % kMetaWin;  // pg divides kMetaWin
             const int w0 = g0 - wbase;               // this group's first probe in the window
-            __syncthreads();  // the previous group's tables, residuals and metadata are no longer read
+            lds_barrier();  // the previous group's tables, residuals and metadata are no longer read
             if (w0 == 0) {
                 // probe lists and their bounds for the next kMetaWin probes (ivf/mod.rs:286-298:
                 // empty lists, and slots past the last probe, get length 0)
@@ -485,13 +630,13 @@ __global__ __launch_bounds__(kScanThreads) void k_ivfpq_scan(ScanArgs A) {
                     s_pl[t] = ok ? A.list_off[c + 1] - beg : 0u;
                 }
                 if constexpr (NV > 0) {
-                    __syncthreads();
+                    lds_barrier();
                     if (wave == 0) {
                         coarse_dma(A, s_pc, s_cr, pg, lane);
                         __builtin_amdgcn_s_waitcnt(VH_VMCNT(0));
                     }
                 }
-                __syncthreads();
+                lds_barrier();
             }
             for (int t = threadIdx.x; t < pg * A.dim; t += kScanThreads) {
                 const int w = t / A.dim, d = t - w * A.dim;
@@ -505,7 +650,7 @@ __global__ __launch_bounds__(kScanThreads) void k_ivfpq_scan(ScanArgs A) {
                 }
                 s_r[t] = r;
             }
-            __syncthreads();
+            lds_barrier();
             // this wave's list; the DMA path scans chunks part + t * wpl (64 rows each), t < mine
             const uint32_t beg = s_pb[w0 + slot], len = s_pl[w0 + slot];
             const float *lut = s_lut + slot * tstride;
@@ -523,7 +668,7 @@ __global__ __launch_bounds__(kScanThreads) void k_ivfpq_scan(ScanArgs A) {
                 lut_build_reg<MT, DS>(A, pg, s_r, s_lut, cbr);
             else
                 lut_build_mem<MT>(A, pg, s_r, s_lut);
-            __syncthreads();
+            lds_barrier();
             if constexpr (NV > 0) {
                 const float *lut0 = reinterpret_cast<const float *>(s_dyn);
                 switch (slot) {
@@ -580,6 +725,253 @@ __global__ __launch_bounds__(kScanThreads) void k_ivfpq_scan(ScanArgs A) {
     }
 }
 
+template <int MT, int DS, int NT>
+__global__ __launch_bounds__(NT) void k_ivfpq_lists(ListArgs L) {
+    constexpr int M = 16, KS = 256, TS = M * KS;
+    constexpr int kListQb = NT / 64, kListChunk = NT / 2, kListThreads = NT;
+    const ScanArgs &A = L.s;
+    // The ring and score words are written by DMAs issued in asm, so the compiler makes no LDS
+    // access wait for them; every read of DMA'd data follows a vmcnt wait and a barrier.
+    __shared__ __attribute__((aligned(16))) ListLds<NT> S;
+    static_assert(kListQb * 128 * sizeof(float) <= sizeof(S.cand), "residuals of dim <= 128 fit");
+    float *s_r = reinterpret_cast<float *>(S.cand);  // residuals, before the scan
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    constexpr int capw = kListCapw;
+    unsigned long long *s_w = S.cand + wave * capw;
+    const unsigned long long lanes_below = (1ull << lane) - 1ull;
+    constexpr bool hib = hib_metric(MT);
+    const uint32_t ring_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)S.ring;
+    const uint32_t tau_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)S.tau;
+    const int wave_u = __builtin_amdgcn_readfirstlane(wave);  // in a scalar register: uniform branches
+
+    // sub-centroid j = tid % 256 of every sub-space, DS floats each (thread-major layout)
+    float cbr[kLutRegs];
+    {
+        const float4 *src = reinterpret_cast<const float4 *>(A.cbt + (size_t)(tid & (KS - 1)) * kLutRegs);
+#pragma unroll
+        for (int v = 0; v < kLutRegs / 4; ++v) {
+            const float4 f = src[v];
+            cbr[4 * v] = f.x;
+            cbr[4 * v + 1] = f.y;
+            cbr[4 * v + 2] = f.z;
+            cbr[4 * v + 3] = f.w;
+        }
+        // landed before any DMA is issued: the compiler would otherwise wait for them at their
+        // first use with counts that also cover the DMAs, which it does not see
+        __builtin_amdgcn_s_waitcnt(VH_VMCNT(0));
+    }
+
+    for (;;) {
+        if (tid == 0) S.item = atomicAdd(L.work, 1u);
+        lds_barrier();  // also: every wave is past the previous item (its candidates and ring)
+        const uint32_t it = S.item;
+        if (it >= *L.n_items) break;
+        const uint4 item = L.items[it];
+        const uint32_t list = item.x, first = item.y, npairs = item.z;
+        const uint32_t beg = A.list_off[list], len = A.list_off[list + 1] - beg;
+        const int nch = (int)((len + kListChunk - 1) / kListChunk);
+        // chunk c of the list into ring slot c % kListRing: threads below kListChunk copy a code
+        // row each, the others its id (rows past the list's end repeat its last row, never
+        // scored; chunks c >= nch re-read it into a slot no wave reads any more).  len > 0.
+        auto chunk_dma = [&](int c) {
+            const uint32_t slot = ring_lds + (uint32_t)((c % kListRing) * (kListChunk * kListRowBytes));
+            if (wave_u < kListChunk / 64) {
+                const uint32_t i = min((uint32_t)(c * kListChunk + tid), len - 1);
+                dma_lds16(A.codes + (size_t)(beg + i) * 16, slot + 16 * 64 * wave_u);
+            } else {
+                const int r = tid - kListChunk;
+                const uint32_t i = min((uint32_t)(c * kListChunk + r), len - 1);
+                dma_lds4(A.ids + beg + i, slot + 16 * kListChunk + 4 * 64 * (wave_u - kListChunk / 64));
+            }
+        };
+        // residuals q - c of the item's pairs (zero rows for unused slots)
+        for (int t = tid; t < kListQb * A.dim; t += kListThreads) {
+            const int sl = t / A.dim, d = t - sl * A.dim;
+            float r = 0.0f;
+            if (sl < (int)npairs) {
+                const uint32_t q = L.pairs[first + sl] / (uint32_t)A.nprobe;
+                r = A.qry[(size_t)q * A.dim + d] - A.coarse[(size_t)list * A.dim + d];
+            }
+            s_r[t] = r;
+        }
+        // the wave's pair and its query's k-th best key so far (read before the ring's DMAs)
+        const bool active = wave < (int)npairs;
+        const uint32_t pid = L.pairs[first + (active ? wave : 0)];
+        const uint32_t qid = pid / (uint32_t)A.nprobe;
+        unsigned long long tau = __hip_atomic_load(L.tau_q + qid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (!active) tau = ~0ull;
+        lds_barrier();  // residuals visible
+        // the first chunks land while the tables are built; no other load is in flight after them
+        __builtin_amdgcn_s_waitcnt(VH_VMCNT(0));
+        if (nch > 0)
+            for (int c = 0; c < kListRing - 1; ++c) chunk_dma(c);
+        // ADC tables (ProductQuantizer::compute_adc_lut, pq.rs:233-266): thread j of half h
+        // computes entry j of every sub-space for the slots h, h + 2, ...
+        {
+            const int j = tid & (KS - 1), h = tid >> 8;
+            for (int sl = h; sl < (int)npairs; sl += (kListThreads + KS - 1) / KS) {
+                const float *r = s_r + sl * A.dim;
+                float *lut = &S.lut[sl][j];
+#pragma unroll
+                for (int m = 0; m < M; ++m) {
+                    Acc<MT> acc;
+#pragma unroll
+                    for (int d4 = 0; d4 < DS; d4 += 4) {
+                        const float4 rv = *reinterpret_cast<const float4 *>(r + m * DS + d4);
+                        acc.step(rv.x, cbr[m * DS + d4]);
+                        acc.step(rv.y, cbr[m * DS + d4 + 1]);
+                        acc.step(rv.z, cbr[m * DS + d4 + 2]);
+                        acc.step(rv.w, cbr[m * DS + d4 + 3]);
+                    }
+                    lut[m * KS] = acc.finish();
+                }
+            }
+        }
+        uint32_t cnt = 0;
+        // score word of the query's k-th best key (the high half: a 4-byte read cannot tear)
+        const uint32_t *tau_hi = reinterpret_cast<const uint32_t *>(L.tau_q + qid) + 1;
+        static_assert(kListRing == 3, "the waits below count the DMAs of a 3-chunk ring");
+        for (int c = 0; c < nch; ++c) {
+            // Every iteration issues two DMAs per wave: the score word, then chunk c + 2 (the
+            // item's start issues chunks 0 and 1).  They complete in issue order, so with at most
+            // one in flight, chunk c and the score word of iteration c - 1 have landed.
+            __builtin_amdgcn_s_waitcnt(VH_VMCNT(1));
+            // every share of chunk c has landed and every wave is done with chunk c - 1 (and, at
+            // c = 0, with the tables' build and the residuals, whose region the candidates reuse)
+            lds_barrier();
+            if (c >= 1) {
+                // the query's k-th best score as other pairs have left it; keys of that score
+                // pass (a tie's id is not read), so the filter stays conservative
+                const unsigned long long ext =
+                    ((unsigned long long)S.tau[2 * wave + ((c - 1) & 1)] << 32) | 0xffffffffull;
+                tau = ext < tau ? ext : tau;
+            }
+            if (lane == 0) dma_lds4(tau_hi, tau_lds + 4 * (2 * wave_u + (c & 1)));
+            chunk_dma(c + kListRing - 1);
+            if (active) {
+                // the lane's 4 rows of the chunk (rows lane + 64 st) and their ids, one wait: the 64
+                // table lookups of the 4 scores are then independent and overlap
+                constexpr int RPL = kListChunk / 64;  // rows per lane
+                const uint32_t cb = ring_lds + (uint32_t)((c % kListRing) * (kListChunk * kListRowBytes));
+                uint4 w[RPL];
+                uint32_t id[RPL];
+                lds_read_rows<RPL>(cb + 16 * lane, cb + 16 * kListChunk + 4 * lane, w, id);
+                float tot[RPL];
+#pragma unroll
+                for (int st = 0; st < RPL; ++st) tot[st] = 0.0f;
+                // the wave's table at a constant address: one copy of the scoring per wave
+                switch (wave_u) {
+                    case 0:
+#pragma unroll
+                        for (int st = 0; st < RPL; ++st) row_score_part<0, 4>(S.lut[0], w[st], tot[st]);
+                        break;
+                    case 1:
+#pragma unroll
+                        for (int st = 0; st < RPL; ++st) row_score_part<0, 4>(S.lut[1], w[st], tot[st]);
+                        break;
+                    case 2:
+#pragma unroll
+                        for (int st = 0; st < RPL; ++st) row_score_part<0, 4>(S.lut[2], w[st], tot[st]);
+                        break;
+                    default:
+#pragma unroll
+                        for (int st = 0; st < RPL; ++st) row_score_part<0, 4>(S.lut[3], w[st], tot[st]);
+                        break;
+                }
+                // Pre-filter: a key below tau has a score at most key_score(tau's score word) (NaN
+                // scores, and tau = ~0, pass), so a chunk none of whose rows passes offers nothing.
+                const float thr = key_score((uint32_t)(tau >> 32));
+                bool maybe = false;
+#pragma unroll
+                for (int st = 0; st < RPL; ++st) {
+                    const float hs = (hib ? -tot[st] : tot[st]) + 0.0f;
+                    maybe |= !(hs > thr) && (uint32_t)(c * kListChunk + st * 64 + lane) < len;
+                }
+                if (__ballot(maybe) != 0ull) {
+#pragma unroll
+                    for (int st = 0; st < RPL; ++st) {
+                        if (cnt > (uint32_t)(capw - 64)) wave_compact(s_w, cnt, tau, A.k);
+                        const uint32_t row = (uint32_t)(st * 64 + lane);
+                        offer<hib>(tot[st], (uint32_t)(c * kListChunk) + row < len, id[st], s_w, cnt, tau,
+                                   lanes_below);
+                    }
+                }
+            }
+        }
+        // the last re-read chunks have landed before any wave's next item writes the ring
+        __builtin_amdgcn_s_waitcnt(VH_VMCNT(0));
+        if (active) {
+            wave_compact(s_w, cnt, tau, A.k);  // sorted, at most k kept
+            for (int j = lane; j < A.k; j += 64)
+                L.pair_out[(size_t)pid * A.k + j] = j < (int)cnt ? s_w[j] : ~0ull;
+            if (lane == 0 && cnt >= (uint32_t)A.k) atomicMin(L.tau_q + qid, s_w[A.k - 1]);
+        }
+    }
+}
+
+// Per query: the k best of its nprobe pairs' k best (pairs of unused probe slots count as empty);
+// writes ids, distances and the count as k_ivfpq_scan does.  Dynamic LDS: P keys, P the power of
+// two >= nprobe * k.
+template <bool HIB>
+__global__ __launch_bounds__(256) void k_ivfpq_merge(ListArgs L, int P) {
+    const ScanArgs &A = L.s;
+    extern __shared__ unsigned long long s_keys[];
+    const int n = A.nprobe * A.k;
+    for (int q = blockIdx.x; q < A.nq; q += gridDim.x) {
+        for (int t = threadIdx.x; t < P; t += 256) {
+            unsigned long long key = ~0ull;
+            if (t < n) {
+                const int p = t / A.k;
+                if (A.probes[(size_t)q * A.nprobe + p] < (uint32_t)A.nlist)
+                    key = L.pair_out[(size_t)q * n + t];
+            }
+            s_keys[t] = key;
+        }
+        __syncthreads();
+        bitonic_sort_u64(s_keys, P, threadIdx.x, 256, [] { __syncthreads(); });
+        for (int j = threadIdx.x; j < A.k; j += 256) {
+            const size_t o = (size_t)q * A.k + j;
+            const unsigned long long cnd = s_keys[j];
+            if (cnd != ~0ull) {
+                const float hs = key_score((uint32_t)(cnd >> 32));
+                A.out_ids[o] = (uint32_t)cnd;
+                A.out_dist[o] = HIB ? -hs : hs;
+            } else {
+                A.out_ids[o] = 0xffffffffu;
+                A.out_dist[o] = __builtin_nanf("");
+            }
+        }
+        if (threadIdx.x == 0) {
+            int lo = 0, hi = A.k;
+            while (lo < hi) {
+                const int mid = (lo + hi) >> 1;
+                if (s_keys[mid] != ~0ull) lo = mid + 1; else hi = mid;
+            }
+            A.out_len[q] = (uint32_t)lo;
+        }
+        __syncthreads();
+    }
+}
+
+template <int MT>
+void launch_lists_mt(const ListArgs &L, int ds, int cus, hipStream_t s) {
+    // persistent: as many workgroups as fit (each CU holds 163840 bytes of LDS)
+    const size_t per_cu = std::max<size_t>(1, 163840 / (sizeof(ListLds<kListThreads>) + 256));
+    const unsigned grid = (unsigned)((size_t)cus * per_cu);
+    if (ds == 4)
+        hipLaunchKernelGGL((k_ivfpq_lists<MT, 4, kListThreads>), dim3(grid), dim3(kListThreads), 0, s, L);
+    else
+        hipLaunchKernelGGL((k_ivfpq_lists<MT, 8, kListThreads>), dim3(grid), dim3(kListThreads), 0, s, L);
+}
+
+template <bool HIB>
+void launch_lists_merge(const ListArgs &L, int cus, hipStream_t s) {
+    int P = 2;
+    while (P < L.s.nprobe * L.s.k) P <<= 1;
+    const unsigned mg = (unsigned)std::min<long>((long)L.s.nq, 4L * cus);
+    hipLaunchKernelGGL((k_ivfpq_merge<HIB>), dim3(mg), dim3(256), (size_t)P * 8, s, L, P);
+}
+
 // Launches one persistent workgroup per resident slot (the occupancy of this instantiation at
 // `lds` bytes of dynamic LDS on `cus` compute units), at most one per query.
 template <class K>
@@ -629,5 +1021,16 @@ inline size_t scan_lds_bytes(size_t dim, size_t m_sub, size_t ks, int capw, int 
 void launch_ivfpq_scan_l2(const ScanArgs &A, int ds, int nv, int cus, size_t lds, hipStream_t s);
 void launch_ivfpq_scan_ip(const ScanArgs &A, int ds, int nv, int cus, size_t lds, hipStream_t s);
 void launch_ivfpq_scan_mem(const ScanArgs &A, int nv, int cus, size_t lds, hipStream_t s);
+// List-major scan and merge (16-byte code rows, 256 sub-centroids, ds 4 or 8, k <= kListMaxK,
+// nprobe * k <= kListMaxMerge); the plan (pairs, items, counters) is built by ivfpq_list_plan.
+void launch_ivfpq_lists_l2(const ListArgs &L, int ds, int cus, hipStream_t s);
+void launch_ivfpq_lists_ip(const ListArgs &L, int ds, int cus, hipStream_t s);
+// The merge of the pairs' k best into each query's (after either list launch).
+void launch_ivfpq_list_merge(const ListArgs &L, int cus, hipStream_t s);
+// Groups the nq x nprobe probes by list: cnt / cursor (nlist each) must be zero; order lists the
+// lists by decreasing size; writes pairs, items, *n_items (and pair_off, item_off: nlist each).
+void ivfpq_list_plan(const uint32_t *probes, int nq, int nprobe, int nlist, const uint32_t *order, uint32_t *cnt,
+                     uint32_t *cursor, uint32_t *pair_off, uint32_t *item_off, uint32_t *pairs, uint4 *items,
+                     uint32_t *n_items, hipStream_t s);
 
 }  // namespace vh

@@ -11,4 +11,11 @@ void launch_ivfpq_scan_ip(const ScanArgs &A, int ds, int nv, int cus, size_t lds
         launch_scan_reg<COS>(A, ds, nv, cus, lds, s);
 }
 
+void launch_ivfpq_lists_ip(const ListArgs &L, int ds, int cus, hipStream_t s) {
+    if (L.s.metric == DOT)
+        launch_lists_mt<DOT>(L, ds, cus, s);
+    else
+        launch_lists_mt<COS>(L, ds, cus, s);
+}
+
 }  // namespace vh

@@ -8,4 +8,13 @@ void launch_ivfpq_scan_l2(const ScanArgs &A, int ds, int nv, int cus, size_t lds
     launch_scan_reg<L2>(A, ds, nv, cus, lds, s);
 }
 
+void launch_ivfpq_lists_l2(const ListArgs &L, int ds, int cus, hipStream_t s) { launch_lists_mt<L2>(L, ds, cus, s); }
+
+void launch_ivfpq_list_merge(const ListArgs &L, int cus, hipStream_t s) {
+    if (hib_metric(L.s.metric))
+        launch_lists_merge<true>(L, cus, s);
+    else
+        launch_lists_merge<false>(L, cus, s);
+}
+
 }  // namespace vh
