@@ -625,6 +625,7 @@ __device__ __forceinline__ int first_item() {
     return (blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3);
 }
 
+
 // =========================================================================================
 // Streaming kernel: 4 waves, 128-row stages, both operands streamed per K-chunk (any dpad).
 // =========================================================================================
@@ -770,8 +771,8 @@ __global__ __launch_bounds__(512, 1) void k_mfma_pnl(ScanArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wr = wave & 3, wc = wave >> 2;
     const int l32 = lane & 31, h = lane >> 5;
-    const int G = gridDim.x;
     const int D = a.dpad, NK = D / kKChunk, NP = NK / 4;
+    const int G = gridDim.x;
     int item = first_item();
     if (item >= a.n_items) return;
 
@@ -785,19 +786,21 @@ __global__ __launch_bounds__(512, 1) void k_mfma_pnl(ScanArgs a) {
     const int dr = tid >> 5, drem = tid & 31;
     const int dkc = (drem >> 3) ^ (dr & 1), dc4 = (drem & 7) ^ ((tid >> 6) & 7);
     const long dstride = 16L * D;
+    // The DMAs are asm (dma_lds16): the compiler then makes no read of the other buffer wait for
+    // them (it cannot tell the two buffers apart), nor counts them in the waits for the A loads.
+    // Each panel ends with a full vmcnt wait and a barrier before its buffer is read.
+    const uint32_t sB_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)&sB[0][0];
+    const uint32_t sN_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)&sN[0][0];
+    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
     auto dma_panel = [&](int b, int c0, int p) {
         const float *src = a.B + (long)(c0 + dr) * D + 128 * p + 32 * dkc + 4 * dc4;
+        const uint32_t dst = sB_lds + (uint32_t)(b * kTileCols * 32 + 64 * wave_u) * 16u;
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
-            __builtin_amdgcn_global_load_lds((const void *)(src + i * dstride),
-                                             (__attribute__((address_space(3))) void *)&sB[b][512 * i + 64 * wave],
-                                             16, 0, 0);
+        for (int i = 0; i < 8; ++i) dma_lds16(src + i * dstride, dst + 512u * 16u * i);
     };
     // row epilogue values of the stage at row rs into norm buffer b (wave 0: 64 lanes x 16 bytes)
     auto dma_norms = [&](int b, long rs) {
-        if (wave == 0)
-            __builtin_amdgcn_global_load_lds((const void *)(a.anorm + rs + 4 * lane),
-                                             (__attribute__((address_space(3))) void *)&sN[b][0], 16, 0, 0);
+        if (wave_u == 0) dma_lds16(a.anorm + rs + 4 * lane, sN_lds + (uint32_t)(b * (TR / 4)) * 16u);
     };
     auto load_a = [&](floatx4 (&r)[8], long rs, int kc) {
         const float *p0 = a.A + (rs + 64 * wr + l32) * (long)D + 32 * kc + 4 * h;
@@ -855,6 +858,10 @@ __global__ __launch_bounds__(512, 1) void k_mfma_pnl(ScanArgs a) {
                 dma_norms(sb ^ 1, nrs);
             }
             const bool last_p = p + 1 == NP;
+            const int rb0 = 64 * wc + l32, rb1 = rb0 + 32;
+            // B pieces one group ahead (across K-chunks too): the LDS reads of the next group are
+            // in flight while the 16 MFMAs of this one issue
+            floatx4 nb0 = sB[pb][bidx(rb0, 0, h)], nb1 = sB[pb][bidx(rb1, 0, h)];
 #pragma unroll
             for (int kc = 0; kc < 4; ++kc) {
                 floatx4 nxt[8];
@@ -862,13 +869,18 @@ __global__ __launch_bounds__(512, 1) void k_mfma_pnl(ScanArgs a) {
                 if (!last) load_a(nxt, rs, 4 * p + kc + 1);
                 else if (more) load_a(nxt, nrs, 0);
                 __builtin_amdgcn_sched_barrier(0);
-                const int rb0 = 64 * wc + l32, rb1 = rb0 + 32;
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
-                    const int c4 = 2 * g + h;
                     const floatx4 a0 = cur[g], a1 = cur[4 + g];
-                    const floatx4 b0 = sB[pb][bidx(rb0, kc, c4)];
-                    const floatx4 b1 = sB[pb][bidx(rb1, kc, c4)];
+                    const floatx4 b0 = nb0, b1 = nb1;
+                    if (g < 3) {
+                        nb0 = sB[pb][bidx(rb0, kc, 2 * g + 2 + h)];
+                        nb1 = sB[pb][bidx(rb1, kc, 2 * g + 2 + h)];
+                    } else if (kc < 3) {
+                        nb0 = sB[pb][bidx(rb0, kc + 1, h)];
+                        nb1 = sB[pb][bidx(rb1, kc + 1, h)];
+                    }
+                    __builtin_amdgcn_sched_barrier(0);  // the reads stay ahead of the MFMAs
 #pragma unroll
                     for (int t = 0; t < 4; ++t) {
                         acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[t], b0[t], acc[0][0], 0, 0, 0);

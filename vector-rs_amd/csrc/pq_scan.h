@@ -190,31 +190,6 @@ __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// Workgroup barrier that publishes LDS data only: the wave's LDS operations complete, its
-// global->LDS DMAs in flight do not (a wave waits for the chunks it publishes with vmcnt first).
-// __syncthreads() would wait for every DMA in flight, since they write LDS.  The memory clobber
-// keeps the compiler from moving memory accesses across the barrier.
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-
-// Global->LDS DMA of 16 (4) bytes per lane from `src` to LDS byte address m0_base + 16 (4) x lane.
-// Written as asm so that the compiler neither counts the DMA among the loads it waits for nor
-// makes later LDS accesses wait for it: the caller waits with vmcnt before reading the data (M0
-// is restored; the DMA takes its value when issued).
-__device__ __forceinline__ void dma_lds16(const void *src, uint32_t m0_base) {
-    uint32_t sv;
-    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
-                 : "=&s"(sv)
-                 : "v"(src), "s"(m0_base)
-                 : "memory");
-}
-__device__ __forceinline__ void dma_lds4(const void *src, uint32_t m0_base) {
-    uint32_t sv;
-    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %1, off\n\ts_mov_b32 m0, %0"
-                 : "=&s"(sv)
-                 : "v"(src), "s"(m0_base)
-                 : "memory");
-}
-
 // Ascending bitonic sort of s[0, P) (P a power of two) by `nthr` threads with index `tid`;
 // `sync` orders the stages.
 template <class Sync>

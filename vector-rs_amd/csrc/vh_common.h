@@ -38,6 +38,31 @@ typedef __attribute__((address_space(1))) uint64_t gu64;
 // the 8 bytes of a uint2 {x, y} as one little-endian 64-bit word
 __device__ __forceinline__ uint64_t pack_u2(uint32_t x, uint32_t y) { return (uint64_t)y << 32 | x; }
 
+// Workgroup barrier that publishes LDS data only: the wave's LDS operations complete, its
+// global->LDS DMAs in flight do not (a wave waits for the chunks it publishes with vmcnt first).
+// __syncthreads() would wait for every DMA in flight, since they write LDS.  The memory clobber
+// keeps the compiler from moving memory accesses across the barrier.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// Global->LDS DMA of 16 (4) bytes per lane from `src` to LDS byte address m0_base + 16 (4) x lane.
+// Written as asm so that the compiler neither counts the DMA among the loads it waits for nor
+// makes later LDS accesses wait for it: the caller waits with vmcnt before reading the data (M0
+// is restored; the DMA takes its value when issued).
+__device__ __forceinline__ void dma_lds16(const void *src, uint32_t m0_base) {
+    uint32_t sv;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+                 : "=&s"(sv)
+                 : "v"(src), "s"(m0_base)
+                 : "memory");
+}
+__device__ __forceinline__ void dma_lds4(const void *src, uint32_t m0_base) {
+    uint32_t sv;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %1, off\n\ts_mov_b32 m0, %0"
+                 : "=&s"(sv)
+                 : "v"(src), "s"(m0_base)
+                 : "memory");
+}
+
 // Maps a float score (smaller is better) to an unsigned key with the same order.
 __host__ __device__ inline uint32_t score_key(float s) {
     uint32_t u = __builtin_bit_cast(uint32_t, s);
