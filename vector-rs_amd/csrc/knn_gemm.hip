@@ -355,6 +355,28 @@ __device__ __forceinline__ void filter_stage(const floatx16 (&acc)[2][2], NF nf,
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             const floatx4 n4 = nf(rb, g);
+            if (!(M == COS && st.guard)) {
+                // Wave test on each column's extremum over the group's 4 rows (fminf / fmaxf skip
+                // the NaN of padding rows, which fail every test): a group none of whose lanes
+                // can pass skips the per-score tests.
+                float e[2];
+#pragma unroll
+                for (int cb = 0; cb < 2; ++cb) {
+                    float v[4];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const float dot = acc[rb][cb][4 * g + j];
+                        v[j] = M == L2 ? fmaf(-2.0f, dot, n4[j]) : dot;
+                    }
+                    e[cb] = M == L2 ? fminf(fminf(v[0], v[1]), fminf(v[2], v[3]))
+                                    : fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
+                }
+                const uint64_t m = M == L2 ? __builtin_amdgcn_ballot_w64(e[0] <= st.T[0]) |
+                                                 __builtin_amdgcn_ballot_w64(e[1] <= st.T[1])
+                                           : __builtin_amdgcn_ballot_w64(e[0] >= st.T[0]) |
+                                                 __builtin_amdgcn_ballot_w64(e[1] >= st.T[1]);
+                if (m == 0) continue;
+            }
             bool p[4][2];
             bool any = false;
 #pragma unroll
