@@ -15,7 +15,9 @@ knn.rs:312-377, AVX-512 dispatch as vector-simd) timed on this host on a bounded
 distances within 1e-4 relative, exact on integer data).  The default line also carries the other
 workloads under "kmeans" (first iteration checked against the oracle's: <= 0.01% flips, all
 near-ties, centroids within 1e-4), "cos768", "hamming" (bit-exact against the oracle's popcount
-search over all 10M codes), "l1" and "linf", each with its own roofline, CPU baseline and parity.
+search over all 10M codes), "l1", "linf" and "ivfpq" (the IVF-PQ search on clustered data,
+checked against the oracle's search_with_nprobe), each with its own roofline, CPU baseline and
+parity.
 The process exits with status 3, after printing the line, when any parity check fails.
 
 Other workloads: --workload cos768 | kmeans | hamming | l1 | linf | gauss (see WORKLOADS), ivf_coarse
@@ -403,6 +405,7 @@ def bench_ivfpq(vh, steps, warmup, with_cpu):
     ms = (time.perf_counter() - t0) * 1e3 / steps
     prof = ix.profile_read()
     ids = di.to_host(np.empty((nq, k), np.uint32))
+    dist = dd.to_host(np.empty((nq, k), np.float32))
     # algorithmic work of one scan launch: every (query, probed list) builds an M x Ks table over
     # D dimensions (a subtract and a multiply-add per element), every scanned code does M table
     # lookups and M adds
@@ -464,23 +467,62 @@ def bench_ivfpq(vh, steps, warmup, with_cpu):
         cc = ix.coarse_centroids().reshape(-1, d)
         cb = ix.pq().codebooks
 
+        ref = []
+
         def run(nsamp):
+            ref.clear()
             t = time.perf_counter()
             for i in range(nsamp):
                 pr, _ = oracle.find_top_centroids(q[i], cc, nprobe, "l2")
-                oracle.ivfpq_search(q[i], cc, cb, m_sub, ks, off, lids, lcodes, pr, k, "l2")
+                ri, rd = oracle.ivfpq_search(q[i], cc, cb, m_sub, ks, off, lids, lcodes, pr, k, "l2")
+                ref.append((pr, ri, rd))
             return time.perf_counter() - t
 
         sp = 16
         dt = run(sp)
         sp = int(min(nq, max(sp, sp * CPU_TARGET_S / max(dt, 1e-6))))
         dt = run(sp)
+        out["parity"] = ivfpq_parity(ids, dist, probes, ref, k)
         be = {0: "scalar", 1: "AVX2+FMA", 2: "AVX-512F"}[oracle.detect_backend()]
         out["cpu_baseline"] = {"value": round(sp / dt, 2), "unit": "queries/s", "cores": 1, "kind": "port",
                                "sample": f"{sp} of the {nq} queries through the oracle's find_top_centroids + "
                                          f"search_with_nprobe on the built index, {be} backend, {dt:.2f} s on "
                                          f"1 thread ({cpu_model()})"}
     return out
+
+
+def ivfpq_parity(ids, dist, probes, ref, k):
+    """Parity of the timed IVF-PQ search with the oracle's search_with_nprobe on the oracle's own
+    probes (ref: (probes, ids, distances) per sampled query).  A query whose GPU probe set differs
+    from the oracle's (a near-tie at the nprobe-th centroid) is counted and skipped.  Otherwise
+    the result counts must match, the distances as sorted lists within 1e-4 relative to the
+    largest, and an id outside the oracle's k best may only tie with its k-th distance."""
+    checked = probe_ties = 0
+    dist_ok = ids_ok = True
+    max_err = 0.0
+    for i, (pr, ri, rd) in enumerate(ref):
+        if set(np.asarray(pr).tolist()) != set(probes[i].tolist()):
+            probe_ties += 1
+            continue
+        checked += 1
+        n = len(ri)
+        gi, gd = ids[i, :n].astype(np.int64), dist[i, :n].astype(np.float64)
+        if n < k and not (np.all(ids[i, n:] == 0xFFFFFFFF) and np.all(np.isnan(dist[i, n:]))):
+            ids_ok = False
+        if n == 0:
+            continue
+        rd = np.asarray(rd, np.float64)
+        tol = 1e-4 * max(1.0, float(np.max(np.abs(rd))))
+        err = float(np.max(np.abs(np.sort(gd) - np.sort(rd))))
+        max_err = max(max_err, err)
+        dist_ok = dist_ok and err <= tol and len(set(gi.tolist())) == n
+        extra = set(gi.tolist()) - set(np.asarray(ri).tolist())
+        if extra:
+            ids_ok = ids_ok and all(abs(gd[list(gi).index(v)] - rd[n - 1]) <= tol for v in extra)
+    ok = bool(dist_ok and ids_ok and checked >= 0.99 * len(ref))
+    return {"queries_checked": checked, "probe_ties_skipped": probe_ties, "k": k, "max_abs_dist_err": max_err,
+            "distance_tolerance": "1e-4 x max(1, |largest distance|)", "distances_ok": dist_ok,
+            "ids_ok_up_to_ties": ids_ok, "ok": ok}
 
 
 def bench_copy(vh, nbytes=1 << 30, reps=5):
@@ -709,6 +751,9 @@ def main():
                 r = bench_knn_workload(vh, extra, args.steps, args.warmup, not args.no_cpu)
                 out[extra] = {kk: r[kk] for kk in ("value", "unit", "ms_per_step", "dtype", "config", "roofline",
                                                    "host_buffers", "cpu_baseline", "parity") if kk in r}
+            r = bench_ivfpq(vh, args.steps, args.warmup, not args.no_cpu)
+            out["ivfpq"] = {kk: r[kk] for kk in ("metric", "value", "unit", "ms_per_step", "dtype", "config",
+                                                 "roofline", "cpu_baseline", "parity") if kk in r}
     out["config"]["device"] = ctx.device_name()
     print(json.dumps(out))
     bad = [name for name, part in [("top", out)] + [(kk, v) for kk, v in out.items() if isinstance(v, dict)]

@@ -1,7 +1,9 @@
-"""CPU checks of the benchmark's parity checks (bench.knn_parity, bench.kmeans_parity).
+"""CPU checks of the benchmark's parity checks (bench.knn_parity, bench.kmeans_parity,
+bench.ivfpq_parity).
 
 The oracle's own results pass; results with a planted mistake (a wrong neighbour, a perturbed
-distance, a flipped assignment that is not a near-tie, a shifted centroid) fail.
+distance, a flipped assignment that is not a near-tie, a shifted centroid, an IVF-PQ id that does
+not tie with the k-th) fail.
 """
 import numpy as np
 
@@ -76,3 +78,46 @@ def test_kmeans_parity(oracle):
     bad["centroids"][4] *= 1.001
     r = bench.kmeans_parity(data, cent, bad, ref)
     assert not r["ok"]
+
+
+def _ivfpq_case(oracle, seed=3, nlist=6, m_sub=4, ks=16, dim=16, n=600, nq=12, k=5, nprobe=3):
+    """A small IVF-PQ index from random parts, and the oracle's search of each query."""
+    rng = np.random.default_rng(seed)
+    coarse = rng.standard_normal((nlist, dim)).astype(np.float32)
+    cb = rng.standard_normal(m_sub * ks * (dim // m_sub)).astype(np.float32)
+    sizes = np.bincount(rng.integers(0, nlist, n), minlength=nlist)
+    off = np.concatenate([[0], np.cumsum(sizes)]).astype(np.uint64)
+    lids = rng.permutation(n).astype(np.uint32)
+    codes = rng.integers(0, ks, (n, m_sub)).astype(np.uint8)
+    q = rng.standard_normal((nq, dim)).astype(np.float32)
+    probes, ref = [], []
+    for i in range(nq):
+        pr, _ = oracle.find_top_centroids(q[i], coarse, nprobe, "l2")
+        ri, rd = oracle.ivfpq_search(q[i], coarse, cb, m_sub, ks, off, lids, codes, pr, k, "l2")
+        probes.append(np.asarray(pr, np.uint32))
+        ref.append((pr, ri, rd))
+    ids = np.full((nq, k), 0xFFFFFFFF, np.uint32)
+    dist = np.full((nq, k), np.nan, np.float32)
+    for i, (_, ri, rd) in enumerate(ref):
+        ids[i, :len(ri)], dist[i, :len(rd)] = ri, rd
+    return ids, dist, np.stack(probes), ref, k
+
+
+def test_ivfpq_parity_accepts_oracle_results_and_rejects_mistakes(oracle):
+    ids, dist, probes, ref, k = _ivfpq_case(oracle)
+    r = bench.ivfpq_parity(ids, dist, probes, ref, k)
+    assert r["ok"] and r["queries_checked"] == len(ref) and r["probe_ties_skipped"] == 0, r
+    # a perturbed distance fails
+    bad = dist.copy()
+    bad[2, 1] += 0.5
+    assert not bench.ivfpq_parity(ids, bad, probes, ref, k)["distances_ok"]
+    # an id outside the oracle's k best that does not tie with the k-th fails
+    bad_ids = ids.copy()
+    others = set(range(600)) - set(ids[4].tolist())
+    bad_ids[4, 0] = min(others)
+    assert not bench.ivfpq_parity(bad_ids, dist, probes, ref, k)["ids_ok_up_to_ties"]
+    # a query whose probes differ is skipped, not failed; too many skipped fails
+    alt = probes.copy()
+    alt[0] = (alt[0] + 1) % 6
+    r = bench.ivfpq_parity(ids, dist, alt, ref, k)
+    assert r["probe_ties_skipped"] == 1 and not r["ok"]
