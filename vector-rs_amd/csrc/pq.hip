@@ -397,7 +397,7 @@ static bool list_path(const vhip_ivfpq *X, size_t k, size_t np) {
     if (const char *e = std::getenv("VHIP_IVFPQ_SCAN"))
         if (std::strcmp(e, "query") == 0) return false;
     return X->reg && X->ks == 256 && X->m_sub == 16 && (X->ds == 4 || X->ds == 8) && k >= 1 &&
-           k <= (size_t)kListMaxK && np * k <= (size_t)kListMaxMerge && scan_capw(k) == 256 &&
+           k <= (size_t)kListMaxK && np * k <= (size_t)kListMaxMerge &&
            sizeof(ListLds<kListThreads>) <= X->lds_limit;
 }
 

@@ -73,7 +73,7 @@ constexpr int ring_bytes(int nv) { return kScanWaves * ring_chunks(nv) * ring_ch
 // kListQb of the queries probing it.  Its kListQb ADC tables are built in LDS at once (thread j of
 // each half of the workgroup computes sub-centroid j's entries from its register-held codebook),
 // then the list's codes and ids stream once through a shared LDS ring of kListRing chunks of
-// kListChunk rows (global->LDS DMA, one barrier per chunk), and wave w scores every row against
+// kListChunkRows rows (global->LDS DMA, one barrier per chunk), and wave w scores every row against
 // its own pair's table with the summation order of compute_distance_with_lut (pq.rs:270-293),
 // keeping its k best.  A list's codes are therefore read once per kListQb probing queries instead
 // of once per probing query.  Each pair's k best go to pair_out; k_ivfpq_merge then sorts each
@@ -84,13 +84,16 @@ constexpr int ring_bytes(int nv) { return kScanWaves * ring_chunks(nv) * ring_ch
 // query's candidates, never below the final k-th, so no key of the final k best is filtered.
 
 // A workgroup of NT threads (NT / 64 waves) takes items of NT / 64 pairs and streams the list in
-// chunks of NT / 2 rows (the first half of the threads copies the code rows, the second the ids).
+// chunks of NT rows (each thread copies a code row and its id; each lane scores 4 rows a chunk).
+// Candidate buffers of 128 keys (hence k <= 64) leave room for the 2 x 256-row ring beside the
+// 64 KB of tables at two workgroups per CU.
 constexpr int kListThreads = 256;    // 4 pairs per item; two workgroups per CU overlap their phases
 constexpr int kListQb = kListThreads / 64;
-constexpr int kListRing = 3;
+constexpr int kListRing = 2;
+constexpr int kListChunkRows = 256;  // rows per ring chunk: 4 per lane of each wave
 constexpr int kListRowBytes = 20;    // a 16-byte code row and its 4-byte id
-constexpr int kListMaxK = 128;
-constexpr int kListCapw = 256;       // candidate keys per wave
+constexpr int kListMaxK = 64;
+constexpr int kListCapw = 128;       // candidate keys per wave: k kept + one offer of 64
 constexpr int kListMaxMerge = 8192;  // nprobe x k keys sorted per query in the merge
 
 struct ListArgs {
@@ -109,7 +112,7 @@ template <int NT>
 struct ListLds {
     float lut[NT / 64][16 * 256];                              // the ADC tables of the item's pairs
     unsigned long long cand[(NT / 64) * kListCapw];            // candidates (residuals before the scan)
-    unsigned char ring[kListRing * (NT / 2) * kListRowBytes];  // chunks: NT / 2 code rows, then ids
+    unsigned char ring[kListRing * kListChunkRows * kListRowBytes];  // chunks: code rows, then ids
     uint32_t tau[2 * (NT / 64)];                               // per wave, two slots: a DMA'd score word
     uint32_t item;
 };
@@ -703,7 +706,8 @@ __global__ __launch_bounds__(kScanThreads) void k_ivfpq_scan(ScanArgs A) {
 template <int MT, int DS, int NT>
 __global__ __launch_bounds__(NT) void k_ivfpq_lists(ListArgs L) {
     constexpr int M = 16, KS = 256, TS = M * KS;
-    constexpr int kListQb = NT / 64, kListChunk = NT / 2, kListThreads = NT;
+    constexpr int kListQb = NT / 64, kListChunk = kListChunkRows, kListThreads = NT;
+    static_assert(kListChunk == NT, "a chunk is one code row and one id per thread");
     const ScanArgs &A = L.s;
     // The ring and score words are written by DMAs issued in asm, so the compiler makes no LDS
     // access wait for them; every read of DMA'd data follows a vmcnt wait and a barrier.
@@ -745,19 +749,14 @@ __global__ __launch_bounds__(NT) void k_ivfpq_lists(ListArgs L) {
         const uint32_t list = item.x, first = item.y, npairs = item.z;
         const uint32_t beg = A.list_off[list], len = A.list_off[list + 1] - beg;
         const int nch = (int)((len + kListChunk - 1) / kListChunk);
-        // chunk c of the list into ring slot c % kListRing: threads below kListChunk copy a code
+        // chunk c of the list into ring slot c % kListRing: every thread copies a code row and its id
         // row each, the others its id (rows past the list's end repeat its last row, never
         // scored; chunks c >= nch re-read it into a slot no wave reads any more).  len > 0.
         auto chunk_dma = [&](int c) {
             const uint32_t slot = ring_lds + (uint32_t)((c % kListRing) * (kListChunk * kListRowBytes));
-            if (wave_u < kListChunk / 64) {
-                const uint32_t i = min((uint32_t)(c * kListChunk + tid), len - 1);
-                dma_lds16(A.codes + (size_t)(beg + i) * 16, slot + 16 * 64 * wave_u);
-            } else {
-                const int r = tid - kListChunk;
-                const uint32_t i = min((uint32_t)(c * kListChunk + r), len - 1);
-                dma_lds4(A.ids + beg + i, slot + 16 * kListChunk + 4 * 64 * (wave_u - kListChunk / 64));
-            }
+            const uint32_t i = min((uint32_t)(c * kListChunk + tid), len - 1);
+            dma_lds16(A.codes + (size_t)(beg + i) * 16, slot + 16 * 64 * wave_u);
+            dma_lds4(A.ids + beg + i, slot + 16 * kListChunk + 4 * 64 * wave_u);
         };
         // residuals q - c of the item's pairs (zero rows for unused slots)
         for (int t = tid; t < kListQb * A.dim; t += kListThreads) {
@@ -805,12 +804,11 @@ __global__ __launch_bounds__(NT) void k_ivfpq_lists(ListArgs L) {
         uint32_t cnt = 0;
         // score word of the query's k-th best key (the high half: a 4-byte read cannot tear)
         const uint32_t *tau_hi = reinterpret_cast<const uint32_t *>(L.tau_q + qid) + 1;
-        static_assert(kListRing == 3, "the waits below count the DMAs of a 3-chunk ring");
+        static_assert(kListRing == 2, "the wait below covers the DMAs of a 2-chunk ring");
         for (int c = 0; c < nch; ++c) {
-            // Every iteration issues two DMAs per wave: the score word, then chunk c + 2 (the
-            // item's start issues chunks 0 and 1).  They complete in issue order, so with at most
-            // one in flight, chunk c and the score word of iteration c - 1 have landed.
-            __builtin_amdgcn_s_waitcnt(VH_VMCNT(1));
+            // Iteration c - 1 issued the score word and chunk c (the item's start, chunk 0): all
+            // have landed for this wave.
+            __builtin_amdgcn_s_waitcnt(VH_VMCNT(0));
             // every share of chunk c has landed and every wave is done with chunk c - 1 (and, at
             // c = 0, with the tables' build and the residuals, whose region the candidates reuse)
             lds_barrier();
