@@ -740,8 +740,12 @@ __global__ __launch_bounds__(NT) void k_ivfpq_lists(ListArgs L) {
         __builtin_amdgcn_s_waitcnt(VH_VMCNT(0));
     }
 
+    // Items are claimed one ahead: the claim of the next item is in flight during this one's
+    // table build.
+    uint32_t next = 0;
+    if (tid == 0) next = atomicAdd(L.work, 1u);
     for (;;) {
-        if (tid == 0) S.item = atomicAdd(L.work, 1u);
+        if (tid == 0) S.item = next;
         lds_barrier();  // also: every wave is past the previous item (its candidates and ring)
         const uint32_t it = S.item;
         if (it >= *L.n_items) break;
@@ -779,6 +783,9 @@ __global__ __launch_bounds__(NT) void k_ivfpq_lists(ListArgs L) {
         __builtin_amdgcn_s_waitcnt(VH_VMCNT(0));
         if (nch > 0)
             for (int c = 0; c < kListRing - 1; ++c) chunk_dma(c);
+        // the next item's claim, in flight while the tables are built (the claim's wave waits
+        // for it with the first chunk; the atomic is not wave-aggregated, see the Makefile)
+        if (tid == 0) next = atomicAdd(L.work, 1u);
         // ADC tables (ProductQuantizer::compute_adc_lut, pq.rs:233-266): thread j of half h
         // computes entry j of every sub-space for the slots h, h + 2, ...
         {
