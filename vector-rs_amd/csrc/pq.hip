@@ -369,26 +369,45 @@ __global__ void k_pair_scatter(const uint32_t *__restrict__ probes, int total, i
     }
 }
 
-// Work items of each list, in the order `order`: (list, first pair, pair count) in runs of qb.
+// Work items of each list, in the order `order`, in runs of qb pairs: (list, first pair, the
+// list's first row, its length << 3 | pair count), and the item's pair ids (unused slots repeat
+// the first), so that a scan reads everything an item needs in one round trip.  One thread per
+// item: its list is the last position i of `order` with item_off[i] <= item (lists without items
+// share their successor's offset, so the last such position is the one holding the item).
 __global__ void k_item_fill(const uint32_t *__restrict__ cnt, const uint32_t *__restrict__ order,
-                            const uint32_t *__restrict__ item_off, const uint32_t *__restrict__ pair_off, int nlist,
-                            int qb, uint4 *__restrict__ items) {
-    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < nlist; i += gridDim.x * blockDim.x) {
-        const uint32_t l = order[i], c = cnt[l], po = pair_off[l], io = item_off[i];
-        for (uint32_t t = 0; t * (uint32_t)qb < c; ++t)
-            items[io + t] = make_uint4(l, po + t * (uint32_t)qb, min((uint32_t)qb, c - t * (uint32_t)qb), 0u);
+                            const uint32_t *__restrict__ item_off, const uint32_t *__restrict__ pair_off,
+                            const uint32_t *__restrict__ list_off, const uint32_t *__restrict__ pairs, int nlist,
+                            int qb, const uint32_t *__restrict__ n_items, uint4 *__restrict__ items,
+                            uint4 *__restrict__ item_pairs) {
+    const uint32_t ni = *n_items;
+    for (uint32_t it = blockIdx.x * blockDim.x + threadIdx.x; it < ni; it += gridDim.x * blockDim.x) {
+        int lo = 0, hi = nlist - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (item_off[mid] <= it) lo = mid; else hi = mid - 1;
+        }
+        const uint32_t l = order[lo], c = cnt[l], t = it - item_off[lo];
+        const uint32_t first = pair_off[l] + t * (uint32_t)qb, np = min((uint32_t)qb, c - t * (uint32_t)qb);
+        const uint32_t beg = list_off[l], len = list_off[l + 1] - beg;
+        items[it] = make_uint4(l, first, beg, len << 3 | np);
+        uint32_t p[4];
+        for (uint32_t sl = 0; sl < 4; ++sl) p[sl] = pairs[first + (sl < np ? sl : 0u)];
+        item_pairs[it] = make_uint4(p[0], p[1], p[2], p[3]);
     }
 }
 
-void ivfpq_list_plan(const uint32_t *probes, int nq, int nprobe, int nlist, const uint32_t *order, uint32_t *cnt,
-                     uint32_t *cursor, uint32_t *pair_off, uint32_t *item_off, uint32_t *pairs, uint4 *items,
-                     uint32_t *n_items, hipStream_t s) {
+void ivfpq_list_plan(const uint32_t *probes, int nq, int nprobe, int nlist, const uint32_t *order,
+                     const uint32_t *list_off, uint32_t *cnt, uint32_t *cursor, uint32_t *pair_off,
+                     uint32_t *item_off, uint32_t *pairs, uint4 *items, uint4 *item_pairs, uint32_t *n_items,
+                     hipStream_t s) {
     const int total = nq * nprobe;
-    const unsigned gp = (unsigned)std::min(4096, (total + 255) / 256), gl = (unsigned)std::min(1024, (nlist + 255) / 256);
+    const unsigned gp = (unsigned)std::min(4096, (total + 255) / 256);
     hipLaunchKernelGGL(k_pair_count, dim3(gp), dim3(256), 0, s, probes, total, nlist, cnt);
     hipLaunchKernelGGL(k_list_plan, dim3(1), dim3(1024), 0, s, cnt, order, nlist, kListQb, pair_off, item_off, n_items);
     hipLaunchKernelGGL(k_pair_scatter, dim3(gp), dim3(256), 0, s, probes, total, nlist, pair_off, cursor, pairs);
-    hipLaunchKernelGGL(k_item_fill, dim3(gl), dim3(256), 0, s, cnt, order, item_off, pair_off, nlist, kListQb, items);
+    // items <= pairs: one thread per item, grid-stride over the device-side count
+    hipLaunchKernelGGL(k_item_fill, dim3(gp), dim3(256), 0, s, cnt, order, item_off, pair_off, list_off, pairs, nlist,
+                       kListQb, n_items, items, item_pairs);
 }
 
 // The list-major search applies to 16-byte code rows of 256 sub-centroids with the register-held
@@ -446,7 +465,7 @@ static int ivfpq_search_dev(vhip_ivfpq *X, const float *d_q, size_t nq, size_t k
         VH_CHECK(X->d_lcnt.ensure(X->dev, 2 * X->nlist * 4));
         VH_CHECK(X->d_loff.ensure(X->dev, 2 * X->nlist * 4));
         VH_CHECK(X->d_pairs.ensure(X->dev, total * 4));
-        VH_CHECK(X->d_items.ensure(X->dev, total * sizeof(uint4)));
+        VH_CHECK(X->d_items.ensure(X->dev, 2 * total * sizeof(uint4)));  // records, then pair ids
         VH_CHECK(X->d_lctr.ensure(X->dev, 2 * 4));
         VH_CHECK(X->d_pout.ensure(X->dev, total * k * 8));
         VH_CHECK(X->d_tau.ensure(X->dev, nq * 8));
@@ -454,12 +473,13 @@ static int ivfpq_search_dev(vhip_ivfpq *X, const float *d_q, size_t nq, size_t k
         uint32_t *cnt = X->d_lcnt.as<uint32_t>(), *ctr = X->d_lctr.as<uint32_t>();
         launch_fill_u32(cnt, 2 * X->nlist, 0u, s);
         launch_fill_u32(ctr, 2, 0u, s);
-        ivfpq_list_plan(A.probes, (int)nq, (int)np, (int)X->nlist, X->d_order.as<uint32_t>(), cnt, cnt + X->nlist,
-                        X->d_loff.as<uint32_t>(), X->d_loff.as<uint32_t>() + X->nlist, X->d_pairs.as<uint32_t>(),
-                        X->d_items.as<uint4>(), ctr, s);
+        uint4 *items = X->d_items.as<uint4>(), *item_pairs = items + total;
+        ivfpq_list_plan(A.probes, (int)nq, (int)np, (int)X->nlist, X->d_order.as<uint32_t>(), A.list_off, cnt,
+                        cnt + X->nlist, X->d_loff.as<uint32_t>(), X->d_loff.as<uint32_t>() + X->nlist,
+                        X->d_pairs.as<uint32_t>(), items, item_pairs, ctr, s);
         VH_HIP(hipGetLastError());
-        ListArgs L{A, X->d_pairs.as<uint32_t>(), X->d_items.as<uint4>(), ctr, ctr + 1,
-                   X->d_pout.as<unsigned long long>(), X->d_tau.as<unsigned long long>()};
+        ListArgs L{A, items, item_pairs, ctr, ctr + 1, X->d_pout.as<unsigned long long>(),
+                   X->d_tau.as<unsigned long long>()};
         const int t = X->timer.begin(s);
         if (X->metric == L2)
             launch_ivfpq_lists_l2(L, (int)X->ds, X->cus, s);

@@ -98,8 +98,8 @@ constexpr int kListMaxMerge = 8192;  // nprobe x k keys sorted per query in the 
 
 struct ListArgs {
     ScanArgs s;                    // queries, lists, codebooks, outputs, k, nprobe, capw
-    const uint32_t *pairs;         // pair ids q * nprobe + p, grouped by list
-    const uint4 *items;            // (list, first pair, pair count, 0)
+    const uint4 *items;            // (list, first pair, list's first row, its length << 3 | pair count)
+    const uint4 *item_pairs;       // each item's pair ids q * nprobe + p (unused slots repeat the first)
     const uint32_t *n_items;       // device scalar: items of this search
     uint32_t *work;                // device scalar: next item to take (zero before the launch)
     unsigned long long *pair_out;  // nq * nprobe * k keys: each pair's k best, ~0 past its count
@@ -705,7 +705,7 @@ __global__ __launch_bounds__(kScanThreads) void k_ivfpq_scan(ScanArgs A) {
 
 template <int MT, int DS, int NT>
 __global__ __launch_bounds__(NT) void k_ivfpq_lists(ListArgs L) {
-    constexpr int M = 16, KS = 256, TS = M * KS;
+    constexpr int M = 16, KS = 256;
     constexpr int kListQb = NT / 64, kListChunk = kListChunkRows, kListThreads = NT;
     static_assert(kListChunk == NT, "a chunk is one code row and one id per thread");
     const ScanArgs &A = L.s;
@@ -744,14 +744,16 @@ __global__ __launch_bounds__(NT) void k_ivfpq_lists(ListArgs L) {
     // table build.
     uint32_t next = 0;
     if (tid == 0) next = atomicAdd(L.work, 1u);
+    const uint32_t n_items = *L.n_items;
     for (;;) {
         if (tid == 0) S.item = next;
         lds_barrier();  // also: every wave is past the previous item (its candidates and ring)
         const uint32_t it = S.item;
-        if (it >= *L.n_items) break;
-        const uint4 item = L.items[it];
-        const uint32_t list = item.x, first = item.y, npairs = item.z;
-        const uint32_t beg = A.list_off[list], len = A.list_off[list + 1] - beg;
+        if (it >= n_items) break;
+        // the item's record and pair ids in one round trip
+        const uint4 item = L.items[it], ip = L.item_pairs[it];
+        const uint32_t list = item.x, beg = item.z, len = item.w >> 3, npairs = item.w & 7u;
+        auto pair_of = [&](int sl) { return sl == 0 ? ip.x : sl == 1 ? ip.y : sl == 2 ? ip.z : ip.w; };
         const int nch = (int)((len + kListChunk - 1) / kListChunk);
         // chunk c of the list into ring slot c % kListRing: every thread copies a code row and its id
         // row each, the others its id (rows past the list's end repeat its last row, never
@@ -767,14 +769,14 @@ __global__ __launch_bounds__(NT) void k_ivfpq_lists(ListArgs L) {
             const int sl = t / A.dim, d = t - sl * A.dim;
             float r = 0.0f;
             if (sl < (int)npairs) {
-                const uint32_t q = L.pairs[first + sl] / (uint32_t)A.nprobe;
+                const uint32_t q = pair_of(sl) / (uint32_t)A.nprobe;
                 r = A.qry[(size_t)q * A.dim + d] - A.coarse[(size_t)list * A.dim + d];
             }
             s_r[t] = r;
         }
         // the wave's pair and its query's k-th best key so far (read before the ring's DMAs)
         const bool active = wave < (int)npairs;
-        const uint32_t pid = L.pairs[first + (active ? wave : 0)];
+        const uint32_t pid = pair_of(wave_u);  // an unused slot repeats the first pair
         const uint32_t qid = pid / (uint32_t)A.nprobe;
         unsigned long long tau = __hip_atomic_load(L.tau_q + qid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (!active) tau = ~0ull;
@@ -1009,8 +1011,9 @@ void launch_ivfpq_lists_ip(const ListArgs &L, int ds, int cus, hipStream_t s);
 void launch_ivfpq_list_merge(const ListArgs &L, int cus, hipStream_t s);
 // Groups the nq x nprobe probes by list: cnt / cursor (nlist each) must be zero; order lists the
 // lists by decreasing size; writes pairs, items, *n_items (and pair_off, item_off: nlist each).
-void ivfpq_list_plan(const uint32_t *probes, int nq, int nprobe, int nlist, const uint32_t *order, uint32_t *cnt,
-                     uint32_t *cursor, uint32_t *pair_off, uint32_t *item_off, uint32_t *pairs, uint4 *items,
-                     uint32_t *n_items, hipStream_t s);
+void ivfpq_list_plan(const uint32_t *probes, int nq, int nprobe, int nlist, const uint32_t *order,
+                     const uint32_t *list_off, uint32_t *cnt, uint32_t *cursor, uint32_t *pair_off,
+                     uint32_t *item_off, uint32_t *pairs, uint4 *items, uint4 *item_pairs, uint32_t *n_items,
+                     hipStream_t s);
 
 }  // namespace vh
