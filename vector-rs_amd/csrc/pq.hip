@@ -305,10 +305,33 @@ static int ivfpq_init(vhip_ivfpq *X, int ordinal, size_t dim, int metric, const 
 }
 
 // ---- plan of the list-major search -----------------------------------------------------------
-__global__ void k_pair_count(const uint32_t *__restrict__ probes, int total, int nlist, uint32_t *__restrict__ cnt) {
-    for (int t = blockIdx.x * blockDim.x + threadIdx.x; t < total; t += gridDim.x * blockDim.x) {
-        const uint32_t c = probes[t];
-        if (c < (uint32_t)nlist) atomicAdd(&cnt[c], 1u);
+// Pair counting and scattering per workgroup over runs of kPlanPairs pairs, aggregated in an LDS
+// histogram when the lists fit it: a popular list then takes one global atomic per workgroup and
+// run instead of one per pair (the per-pair atomics serialised on its counter).
+constexpr int kPlanBins = 8192, kPlanPer = 16, kPlanPairs = 256 * kPlanPer;
+
+__global__ __launch_bounds__(256) void k_pair_count(const uint32_t *__restrict__ probes, int total, int nlist,
+                                                    uint32_t *__restrict__ cnt) {
+    __shared__ uint32_t h[kPlanBins];
+    const bool lds = nlist <= kPlanBins;
+    const int tid = threadIdx.x;
+    for (long b0 = (long)blockIdx.x * kPlanPairs; b0 < total; b0 += (long)gridDim.x * kPlanPairs) {
+        if (lds) {
+            for (int i = tid; i < nlist; i += 256) h[i] = 0;
+            __syncthreads();
+        }
+        for (int j = 0; j < kPlanPer; ++j) {
+            const long t = b0 + j * 256 + tid;
+            if (t >= total) break;
+            const uint32_t c = probes[t];
+            if (c < (uint32_t)nlist) atomicAdd(lds ? &h[c] : &cnt[c], 1u);
+        }
+        if (lds) {
+            __syncthreads();
+            for (int i = tid; i < nlist; i += 256)
+                if (h[i]) atomicAdd(&cnt[i], h[i]);
+            __syncthreads();
+        }
     }
 }
 
@@ -360,12 +383,35 @@ __global__ __launch_bounds__(1024) void k_list_plan(const uint32_t *__restrict__
 
 // Pair ids q * nprobe + p into their list's range (the order within a list is arbitrary: every
 // pair's result is the same whichever item scans it).
-__global__ void k_pair_scatter(const uint32_t *__restrict__ probes, int total, int nlist,
-                               const uint32_t *__restrict__ pair_off, uint32_t *__restrict__ cursor,
-                               uint32_t *__restrict__ pairs) {
-    for (int t = blockIdx.x * blockDim.x + threadIdx.x; t < total; t += gridDim.x * blockDim.x) {
-        const uint32_t c = probes[t];
-        if (c < (uint32_t)nlist) pairs[pair_off[c] + atomicAdd(&cursor[c], 1u)] = (uint32_t)t;
+__global__ __launch_bounds__(256) void k_pair_scatter(const uint32_t *__restrict__ probes, int total, int nlist,
+                                                      const uint32_t *__restrict__ pair_off,
+                                                      uint32_t *__restrict__ cursor, uint32_t *__restrict__ pairs) {
+    __shared__ uint32_t h[kPlanBins];
+    const bool lds = nlist <= kPlanBins;
+    const int tid = threadIdx.x;
+    for (long b0 = (long)blockIdx.x * kPlanPairs; b0 < total; b0 += (long)gridDim.x * kPlanPairs) {
+        if (lds) {
+            for (int i = tid; i < nlist; i += 256) h[i] = 0;
+            __syncthreads();
+        }
+        uint32_t cc[kPlanPer], loc[kPlanPer];
+        for (int j = 0; j < kPlanPer; ++j) {
+            const long t = b0 + j * 256 + tid;
+            cc[j] = t < total ? probes[t] : 0xffffffffu;
+            loc[j] = 0;
+            if (cc[j] < (uint32_t)nlist)
+                loc[j] = lds ? atomicAdd(&h[cc[j]], 1u) : pair_off[cc[j]] + atomicAdd(&cursor[cc[j]], 1u);
+        }
+        if (lds) {
+            __syncthreads();
+            // each list's slots for this run: one global reservation, kept in place of its count
+            for (int i = tid; i < nlist; i += 256)
+                if (h[i]) h[i] = pair_off[i] + atomicAdd(&cursor[i], h[i]);
+            __syncthreads();
+        }
+        for (int j = 0; j < kPlanPer; ++j)
+            if (cc[j] < (uint32_t)nlist) pairs[(lds ? h[cc[j]] : 0u) + loc[j]] = (uint32_t)(b0 + j * 256 + tid);
+        if (lds) __syncthreads();  // the next run clears h
     }
 }
 
@@ -402,9 +448,10 @@ void ivfpq_list_plan(const uint32_t *probes, int nq, int nprobe, int nlist, cons
                      hipStream_t s) {
     const int total = nq * nprobe;
     const unsigned gp = (unsigned)std::min(4096, (total + 255) / 256);
-    hipLaunchKernelGGL(k_pair_count, dim3(gp), dim3(256), 0, s, probes, total, nlist, cnt);
+    const unsigned gr = (unsigned)std::min(1024, (total + kPlanPairs - 1) / kPlanPairs);  // runs of kPlanPairs
+    hipLaunchKernelGGL(k_pair_count, dim3(gr), dim3(256), 0, s, probes, total, nlist, cnt);
     hipLaunchKernelGGL(k_list_plan, dim3(1), dim3(1024), 0, s, cnt, order, nlist, kListQb, pair_off, item_off, n_items);
-    hipLaunchKernelGGL(k_pair_scatter, dim3(gp), dim3(256), 0, s, probes, total, nlist, pair_off, cursor, pairs);
+    hipLaunchKernelGGL(k_pair_scatter, dim3(gr), dim3(256), 0, s, probes, total, nlist, pair_off, cursor, pairs);
     // items <= pairs: one thread per item, grid-stride over the device-side count
     hipLaunchKernelGGL(k_item_fill, dim3(gp), dim3(256), 0, s, cnt, order, item_off, pair_off, list_off, pairs, nlist,
                        kListQb, n_items, items, item_pairs);

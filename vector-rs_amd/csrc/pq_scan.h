@@ -892,25 +892,34 @@ __global__ __launch_bounds__(NT) void k_ivfpq_lists(ListArgs L) {
 }
 
 // Per query: the k best of its nprobe pairs' k best (pairs of unused probe slots count as empty);
-// writes ids, distances and the count as k_ivfpq_scan does.  Dynamic LDS: P keys, P the power of
-// two >= nprobe * k.
+// writes ids, distances and the count as k_ivfpq_scan does.  The query's final k best are all at
+// or below tau_q (the smallest k-th key of its pairs, or ~0 while no pair held k), so only those
+// keys are kept, in arbitrary order through an LDS counter, and sorted.  Dynamic LDS: P keys, P
+// the power of two >= nprobe * k.
 template <bool HIB>
 __global__ __launch_bounds__(256) void k_ivfpq_merge(ListArgs L, int P) {
     const ScanArgs &A = L.s;
     extern __shared__ unsigned long long s_keys[];
+    __shared__ uint32_t s_n;
     const int n = A.nprobe * A.k;
     for (int q = blockIdx.x; q < A.nq; q += gridDim.x) {
-        for (int t = threadIdx.x; t < P; t += 256) {
-            unsigned long long key = ~0ull;
-            if (t < n) {
-                const int p = t / A.k;
-                if (A.probes[(size_t)q * A.nprobe + p] < (uint32_t)A.nlist)
-                    key = L.pair_out[(size_t)q * n + t];
+        const unsigned long long tq = L.tau_q[q];
+        if (threadIdx.x == 0) s_n = 0;
+        __syncthreads();
+        for (int t = threadIdx.x; t < n; t += 256) {
+            const int p = t / A.k;
+            if (A.probes[(size_t)q * A.nprobe + p] < (uint32_t)A.nlist) {
+                const unsigned long long key = L.pair_out[(size_t)q * n + t];
+                if (key != ~0ull && key <= tq) s_keys[atomicAdd(&s_n, 1u)] = key;
             }
-            s_keys[t] = key;
         }
         __syncthreads();
-        bitonic_sort_u64(s_keys, P, threadIdx.x, 256, [] { __syncthreads(); });
+        const int m = (int)s_n;
+        int P2 = 1;
+        while (P2 < m) P2 <<= 1;
+        for (int t = m + (int)threadIdx.x; t < max(P2, A.k); t += 256) s_keys[t] = ~0ull;
+        __syncthreads();
+        bitonic_sort_u64(s_keys, P2, threadIdx.x, 256, [] { __syncthreads(); });
         for (int j = threadIdx.x; j < A.k; j += 256) {
             const size_t o = (size_t)q * A.k + j;
             const unsigned long long cnd = s_keys[j];
@@ -923,14 +932,7 @@ __global__ __launch_bounds__(256) void k_ivfpq_merge(ListArgs L, int P) {
                 A.out_dist[o] = __builtin_nanf("");
             }
         }
-        if (threadIdx.x == 0) {
-            int lo = 0, hi = A.k;
-            while (lo < hi) {
-                const int mid = (lo + hi) >> 1;
-                if (s_keys[mid] != ~0ull) lo = mid + 1; else hi = mid;
-            }
-            A.out_len[q] = (uint32_t)lo;
-        }
+        if (threadIdx.x == 0) A.out_len[q] = (uint32_t)min(m, A.k);
         __syncthreads();
     }
 }
