@@ -111,3 +111,16 @@ def test_lists_repeatable_and_batch_independent(vh):
     sel = rng.choice(3000, 100, replace=False)
     r3 = ix.search_batch_arrays(qs[sel], 10, 12)
     _assert_same((r1[0][sel], r1[1][sel], r1[2][sel]), r3)
+
+
+def test_lists_many_lists_plan_without_lds_histogram(vh, oracle):
+    """More lists (8,200) than the plan's LDS histogram holds (8,192 bins): the pair counting and
+    scattering take their global-atomic path.  Checked against the query-major kernel and, exactly
+    on integer parts, against the oracle."""
+    rng = np.random.default_rng(93)
+    parts = _skewed_parts(rng, 64, 8200, 30_000, integer=True)
+    ix = _index(vh, parts, 64, 16, 256, vh.DistanceMetric.L2Squared)
+    qs = rng.integers(-4, 5, (200, 64)).astype(np.float32)
+    a, b = _both_paths(ix, qs, 10, 24)
+    _assert_same(a, b)
+    _check_search(vh, oracle, ix, parts, qs[:20], 10, 24, "l2", 16, 256, exact=True)
