@@ -433,18 +433,6 @@ __device__ __forceinline__ void lds_read_pair(uint32_t a0, uint32_t a1, uint32_t
 template <int R>
 __device__ __forceinline__ void lds_read_rows(uint32_t a, uint32_t i, uint4 (&w)[R], uint32_t (&id)[R]);
 template <>
-__device__ __forceinline__ void lds_read_rows<2>(uint32_t a, uint32_t i, uint4 (&w)[2], uint32_t (&id)[2]) {
-    asm volatile(
-        "ds_read_b128 %0, %4\n\t"
-        "ds_read_b128 %1, %4 offset:1024\n\t"
-        "ds_read_b32 %2, %5\n\t"
-        "ds_read_b32 %3, %5 offset:256\n\t"
-        "s_waitcnt lgkmcnt(0)"
-        : "=&v"(w[0]), "=&v"(w[1]), "=&v"(id[0]), "=&v"(id[1])
-        : "v"(a), "v"(i)
-        : "memory");
-}
-template <>
 __device__ __forceinline__ void lds_read_rows<4>(uint32_t a, uint32_t i, uint4 (&w)[4], uint32_t (&id)[4]) {
     asm volatile(
         "ds_read_b128 %0, %8\n\t"
@@ -480,8 +468,7 @@ __device__ __forceinline__ float ring_score(const float *lut, const uint4 (&w)[N
     return total;
 }
 
-// ring_score<1> of one row against table `lut` at a constant LDS address: one SDWA shift gives
-// each byte times 4, and the table's address becomes the lookup's offset.  Same summation order.
+// Byte B of w times 4 (a table offset in bytes) in one SDWA shift.
 template <int B>
 __device__ __forceinline__ uint32_t byte_x4(uint32_t w) {
     uint32_t a;
@@ -495,14 +482,15 @@ __device__ __forceinline__ uint32_t byte_x4(uint32_t w) {
         asm("v_lshlrev_b32_sdwa %0, 2, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_3" : "=v"(a) : "v"(w));
     return a;
 }
-// Adds the quads h in [H0, H1) of ring_score<1>'s sum to `total` (H0 = 0, H1 = 4 from
-// total = 0 is the whole sum, in the same order).
-template <int H0, int H1>
-__device__ __forceinline__ void row_score_part(const float *lut, uint4 w, float &total) {
+// ring_score<1> of one row against table `lut` at a constant LDS address: each lookup is one
+// SDWA shift of the code byte plus an LDS read with the table's address as its offset.  Same
+// summation order.
+__device__ __forceinline__ float row_score_at(const float *lut, uint4 w) {
     const char *base = reinterpret_cast<const char *>(lut);
     const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+    float total = 0.0f;
 #pragma unroll
-    for (int h = H0; h < H1; ++h) {
+    for (int h = 0; h < 4; ++h) {
         const char *L = base + 4 * h * 1024;
         const float d0 = *reinterpret_cast<const float *>(L + byte_x4<0>(ww[h]));
         const float d1 = *reinterpret_cast<const float *>(L + 1024 + byte_x4<1>(ww[h]));
@@ -510,6 +498,7 @@ __device__ __forceinline__ void row_score_part(const float *lut, uint4 w, float 
         const float d3 = *reinterpret_cast<const float *>(L + 3072 + byte_x4<3>(ww[h]));
         total += (d0 + d1) + (d2 + d3);
     }
+    return total;
 }
 
 // Chunks are taken two at a time.  Invariant: before the pair (t, t + 1) is read, the chunks
@@ -839,25 +828,23 @@ __global__ __launch_bounds__(NT) void k_ivfpq_lists(ListArgs L) {
                 uint32_t id[RPL];
                 lds_read_rows<RPL>(cb + 16 * lane, cb + 16 * kListChunk + 4 * lane, w, id);
                 float tot[RPL];
-#pragma unroll
-                for (int st = 0; st < RPL; ++st) tot[st] = 0.0f;
                 // the wave's table at a constant address: one copy of the scoring per wave
                 switch (wave_u) {
                     case 0:
 #pragma unroll
-                        for (int st = 0; st < RPL; ++st) row_score_part<0, 4>(S.lut[0], w[st], tot[st]);
+                        for (int st = 0; st < RPL; ++st) tot[st] = row_score_at(S.lut[0], w[st]);
                         break;
                     case 1:
 #pragma unroll
-                        for (int st = 0; st < RPL; ++st) row_score_part<0, 4>(S.lut[1], w[st], tot[st]);
+                        for (int st = 0; st < RPL; ++st) tot[st] = row_score_at(S.lut[1], w[st]);
                         break;
                     case 2:
 #pragma unroll
-                        for (int st = 0; st < RPL; ++st) row_score_part<0, 4>(S.lut[2], w[st], tot[st]);
+                        for (int st = 0; st < RPL; ++st) tot[st] = row_score_at(S.lut[2], w[st]);
                         break;
                     default:
 #pragma unroll
-                        for (int st = 0; st < RPL; ++st) row_score_part<0, 4>(S.lut[3], w[st], tot[st]);
+                        for (int st = 0; st < RPL; ++st) tot[st] = row_score_at(S.lut[3], w[st]);
                         break;
                 }
                 // Pre-filter: a key below tau has a score at most key_score(tau's score word) (NaN
