@@ -85,15 +85,20 @@ constexpr int ring_bytes(int nv) { return kScanWaves * ring_chunks(nv) * ring_ch
 
 // A workgroup of NT threads (NT / 64 waves) takes items of NT / 64 pairs and streams the list in
 // chunks of NT rows (each thread copies a code row and its id; each lane scores 4 rows a chunk).
-// Candidate buffers of 128 keys (hence k <= 64) leave room for the 2 x 256-row ring beside the
-// 64 KB of tables at two workgroups per CU.
+// Candidate buffers of 128 keys (k kept plus one offer of 64) leave room for the 2 x 256-row ring
+// beside the 64 KB of tables at two workgroups per CU.
 constexpr int kListThreads = 256;    // 4 pairs per item; two workgroups per CU overlap their phases
 constexpr int kListQb = kListThreads / 64;
 constexpr int kListRing = 2;
 constexpr int kListChunkRows = 256;  // rows per ring chunk: 4 per lane of each wave
 constexpr int kListRowBytes = 20;    // a 16-byte code row and its 4-byte id
-constexpr int kListMaxK = 64;
 constexpr int kListCapw = 128;       // candidate keys per wave: k kept + one offer of 64
+// The list path takes k <= 48: at larger k a wave's buffer, holding k keys after each sort, fills
+// with any later offer, so nearly every offer sorts it again (1M rows, 1024-component mixture,
+// nprobe 32: 13.9 ms at k = 64 against 7.8 ms for the query-major scan, 6.1 against 7.5 ms at
+// k = 48).
+constexpr int kListMaxK = 48;
+static_assert(kListMaxK + 64 <= kListCapw, "k kept plus one offer fit a wave's buffer");
 constexpr int kListMaxMerge = 8192;  // nprobe x k keys sorted per query in the merge
 
 struct ListArgs {
@@ -778,25 +783,41 @@ __global__ __launch_bounds__(NT) void k_ivfpq_lists(ListArgs L) {
         // for it with the first chunk; the atomic is not wave-aggregated, see the Makefile)
         if (tid == 0) next = atomicAdd(L.work, 1u);
         // ADC tables (ProductQuantizer::compute_adc_lut, pq.rs:233-266): thread j of half h
-        // computes entry j of every sub-space for the slots h, h + 2, ...
+        // computes entry j of every sub-space for the slots h, h + 2, ...  A slot's 16 entries
+        // are stored after all are computed: a store between the residual reads would keep the
+        // compiler from issuing the reads ahead (it cannot tell the two regions apart), and each
+        // sub-space would wait for its own LDS round trip.
         {
             const int j = tid & (KS - 1), h = tid >> 8;
             for (int sl = h; sl < (int)npairs; sl += (kListThreads + KS - 1) / KS) {
                 const float *r = s_r + sl * A.dim;
+                float e[M];
+                constexpr int MB = 4, NR = MB * DS / 4;  // sub-spaces per batch, float4 reads per batch
+#pragma unroll
+                for (int m0 = 0; m0 < M; m0 += MB) {
+                    // the batch's residual values in one round of reads
+                    float4 rv[NR];
+#pragma unroll
+                    for (int i = 0; i < NR; ++i) rv[i] = *reinterpret_cast<const float4 *>(r + m0 * DS + 4 * i);
+                    __builtin_amdgcn_sched_barrier(0);  // all of them issued before the first use
+#pragma unroll
+                    for (int mm = 0; mm < MB; ++mm) {
+                        const int m = m0 + mm;
+                        Acc<MT> acc;
+#pragma unroll
+                        for (int d4 = 0; d4 < DS; d4 += 4) {
+                            const float4 v = rv[(mm * DS + d4) / 4];
+                            acc.step(v.x, cbr[m * DS + d4]);
+                            acc.step(v.y, cbr[m * DS + d4 + 1]);
+                            acc.step(v.z, cbr[m * DS + d4 + 2]);
+                            acc.step(v.w, cbr[m * DS + d4 + 3]);
+                        }
+                        e[m] = acc.finish();
+                    }
+                }
                 float *lut = &S.lut[sl][j];
 #pragma unroll
-                for (int m = 0; m < M; ++m) {
-                    Acc<MT> acc;
-#pragma unroll
-                    for (int d4 = 0; d4 < DS; d4 += 4) {
-                        const float4 rv = *reinterpret_cast<const float4 *>(r + m * DS + d4);
-                        acc.step(rv.x, cbr[m * DS + d4]);
-                        acc.step(rv.y, cbr[m * DS + d4 + 1]);
-                        acc.step(rv.z, cbr[m * DS + d4 + 2]);
-                        acc.step(rv.w, cbr[m * DS + d4 + 3]);
-                    }
-                    lut[m * KS] = acc.finish();
-                }
+                for (int m = 0; m < M; ++m) lut[m * KS] = e[m];
             }
         }
         uint32_t cnt = 0;
