@@ -94,8 +94,8 @@ struct vhip_knn {
 namespace vh {
 
 // Search rounds.  Round 0 scores rows [0, b0) with b0 about 20 k, the first 256-row multiple
-// at or above it: for the GEMM metrics densely (every score written, no atomics), for the others
-// through the filter with tau = +inf.  Every later round covers about 8 times the rows seen so
+// at or above it (all rows when the base has at most max(2048, 32 k)): for the GEMM metrics
+// densely (every score written, no atomics), for the others through the filter with tau = +inf.  Every later round covers about 8 times the rows seen so
 // far and keeps only rows scoring <= tau, the k-th best so far.  Because the base rows are in a
 // pseudo-random order, round i passes about k * (rows_i / seen_i) ~ 7 k candidates per query at a
 // rate p_i = k / seen_i per scored pair.  item_rows of the MFMA filter is sized so that a work
@@ -111,7 +111,10 @@ static std::vector<Round> plan_rounds(size_t n, size_t k, bool gemm, int dpad) {
     std::vector<Round> r;
     if (n == 0) return r;
     const size_t kk = std::max<size_t>(k, 1);
-    const size_t b0 = std::min(n, round_up(std::max<size_t>(256, 20 * kk), kRowAlign));
+    size_t b0 = std::min(n, round_up(std::max<size_t>(256, 20 * kk), kRowAlign));
+    // A base within the candidate capacity's floor (round_cap) is scored in one dense round: its
+    // later rounds would cost more launches than rows (the IVF coarse probe: 1,024 centroids).
+    if (n <= std::max<size_t>(2048, 32 * kk)) b0 = n;
     r.push_back({0, (long)b0, gemm, (long)kRowAlign, (long)kRowAlign});
     const int slots = gemm_slots(dpad);
     size_t seen = b0;
