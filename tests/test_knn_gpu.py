@@ -278,12 +278,14 @@ def test_repeat_runs_bit_identical(vh):
     assert np.array_equal(a[0], b[0]) and np.array_equal(a[1], b[1])
 
 
-@pytest.mark.parametrize("dim", [256, 768, 200, 300])
+@pytest.mark.parametrize("dim", [256, 384, 512, 640, 768, 896, 1024, 200, 300])
 @pytest.mark.parametrize("metric", ["l2", "dot", "cosine"])
 def test_high_dimension_parity(vh, oracle, metric, dim):
-    """Dimensions above 128: multiples of 128 run the panel kernel (the 1M x 768 cosine
-    workload's shape), others the streaming kernel.  300 queries span three column tiles
-    and k = 100 makes the dense first round cover 2048 rows."""
+    """Dimensions above 128: multiples of 128 up to 896 run the narrow resident-tile kernel
+    (every one of its K-chunk counts; 768 is the 1M x 768 cosine workload's shape), 1024 the
+    panel kernel, others the streaming kernel.  300 queries span ten 32-column tiles (the last
+    partial) and three 128-column tiles; k = 100 makes the dense first round cover 2048 rows,
+    and the last round's 9,952 rows end inside a 512-row stage."""
     from vector_hip import datasets as ds
 
     base = ds.normalized(12_000, dim, 31) if metric == "cosine" else ds.gaussian(12_000, dim, 31)

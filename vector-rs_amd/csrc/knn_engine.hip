@@ -336,9 +336,12 @@ static int run_rounds(vhip_knn *E, const QueryRows &Q, int nq, int k, int kc, in
                                      : rows * E->dim * 4.0 + (double)nq * E->dim * 4.0;
         if (dense) launch_fill_u32(B.cnt, (size_t)nq, (uint32_t)(re - rb), s);
         const int t = (direct || !timed) ? -1 : E->timer.begin(s);
-        const long item =
-            gemm && !rd.dense ? balanced_item(rd.item_rows, re - rb, ceil_div(nq, kTileCols), E->grid_cap / 2)
-                              : rd.item_rows;
+        // the narrow resident-tile kernel (gemm_narrow) works in 512-row stages on 32-column tiles
+        const bool narrow = gemm && gemm_narrow((int)E->dpad);
+        const long item = gemm && !rd.dense
+                              ? balanced_item(rd.item_rows, re - rb, ceil_div(nq, gemm_filter_cols((int)E->dpad)),
+                                              E->grid_cap / 2, narrow ? 512 : kRowAlign)
+                              : (narrow ? std::max<long>(rd.item_rows, 512) : rd.item_rows);
         if (E->ham8) {
             // fp4 matrix-core Hamming: 2 K operations per (query, row), K = the padded code bits.
             // Items up to 32768 rows where the slot rule allows: each spreads its query-tile fill

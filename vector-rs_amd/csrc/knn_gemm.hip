@@ -54,6 +54,7 @@ constexpr int kFilter = 0, kAssign = 1, kDense = 2;
 constexpr int kRegSlots = kGemmSlotsReg;     // LDS candidate slots per query per work item (register-fed kernel)
 constexpr int kPnlSlots = kGemmSlotsPanel;   // same for the panel kernel
 constexpr int kStrSlots = kGemmSlotsStream;  // same for the streaming kernel (two workgroups share a CU's LDS)
+constexpr int kNtSlots = kGemmSlotsNarrow;   // same for the narrow resident-tile kernel
 
 // float4 index of (row, c4) in a 32-float-wide swizzled tile
 __device__ __forceinline__ int swz(int row, int c4) { return row * 8 + (c4 ^ ((row >> 1) & 7)); }
@@ -284,10 +285,11 @@ struct EpiState {
     int bi[2];
 };
 
-template <int MODE, int M>
+// CB: the wave's 32-column blocks (2, or 1 in the narrow-tile kernel).
+template <int MODE, int M, int CB = 2>
 __device__ __forceinline__ void item_begin(EpiState &st, const ScanArgs &a, int col0, int wc, int l32) {
 #pragma unroll
-    for (int cb = 0; cb < 2; ++cb) {
+    for (int cb = 0; cb < CB; ++cb) {
         const int q = col0 + 64 * wc + 32 * cb + l32;
         const bool v = q < a.ncols;
         st.cn[cb] = v ? a.bnorm[q] : 0.0f;
@@ -313,7 +315,7 @@ __device__ __forceinline__ void item_begin(EpiState &st, const ScanArgs &a, int 
     st.guard = false;
     if constexpr (MODE == kFilter && M == COS) {
         const bool g0 = (col0 + 64 * wc + l32 < a.ncols) && st.cn[0] * a.anorm_min <= 1e-9f;
-        const bool g1 = (col0 + 64 * wc + 32 + l32 < a.ncols) && st.cn[1] * a.anorm_min <= 1e-9f;
+        const bool g1 = CB > 1 && (col0 + 64 * wc + 32 + l32 < a.ncols) && st.cn[1] * a.anorm_min <= 1e-9f;
         st.guard = __builtin_amdgcn_ballot_w64(g0 || g1) != 0;
     }
 }
@@ -427,12 +429,12 @@ __device__ __forceinline__ void filter_stage(const floatx16 (&acc)[2][2], NF nf,
 
 // FILTER item end: one global atomic per query with staged candidates.  Must be called by
 // all threads; contains a barrier.
-template <int SLOTS>
+template <int SLOTS, int TC = kTileCols>
 __device__ __forceinline__ void filter_flush(const ScanArgs &a, int col0, long r_lo, uint32_t *s_qcnt,
                                              uint2 *s_slot) {
     __syncthreads();
     const int tid = threadIdx.x;
-    if (tid < kTileCols) {
+    if (tid < TC) {
         uint32_t c = s_qcnt[tid];
         if (c) {
             s_qcnt[tid] = 0;
@@ -633,10 +635,11 @@ __device__ __forceinline__ void assign_finish(EpiState &st, const ScanArgs &a, i
     }
 }
 
+template <int TC = kTileCols>
 __device__ __forceinline__ void decode_item(const ScanArgs &a, int it, int &c0, long &lo, long &hi) {
     const int ct = it % a.n_ctiles;
     const long chunk = it / a.n_ctiles;
-    c0 = ct * kTileCols;
+    c0 = ct * TC;
     lo = a.row_begin + chunk * a.item_rows;
     hi = min(lo + a.item_rows, a.row_end);
 }
@@ -965,33 +968,30 @@ __global__ __launch_bounds__(512, 1) void k_mfma_pnl(ScanArgs a) {
 // For squared L2 the register kernel's accumulators start from the row norms and its column
 // tile holds the queries times -2, so a register already holds u = ||x||^2 - 2 q.x and the
 // score is max(||q||^2 + u, 0); for the other metrics it holds q.x.
-template <int M, int SLOTS>
-__device__ __forceinline__ void filter_group(const floatx16 (&acc2)[2], floatx4 n4, const EpiState &st,
+template <int M, int SLOTS, int CB = 2>
+__device__ __forceinline__ void filter_group(const floatx16 (&acc2)[CB], floatx4 n4, const EpiState &st,
                                              const ScanArgs &a, int wc, int l32, uint32_t row_g, long r_lo,
                                              int col0, uint32_t *s_qcnt, uint2 *s_slot, int g, bool enable) {
-    bool p[4][2];
+    bool p[4][CB];
     bool any = false;
     if (!(M == COS && st.guard)) {
-        // Wave test on each column's extremum over the group's 4 rows: two compares, whose lane
-        // masks are OR-ed in scalar registers.  Only a group with some candidate lane takes the
-        // per-score tests below.
-        float e[2];
+        // Wave test on each column's extremum over the group's 4 rows: one compare per column
+        // block, whose lane masks are OR-ed in scalar registers.  Only a group with some
+        // candidate lane takes the per-score tests below.
+        uint64_t m = 0;
 #pragma unroll
-        for (int cb = 0; cb < 2; ++cb) {
+        for (int cb = 0; cb < CB; ++cb) {
             const float v0 = acc2[cb][4 * g], v1 = acc2[cb][4 * g + 1];
             const float v2 = acc2[cb][4 * g + 2], v3 = acc2[cb][4 * g + 3];
             // fminf / fmaxf ignore the quiet NaN of padding rows
-            e[cb] = M == L2 ? fminf(fminf(v0, v1), fminf(v2, v3)) : fmaxf(fmaxf(v0, v1), fmaxf(v2, v3));
+            const float e = M == L2 ? fminf(fminf(v0, v1), fminf(v2, v3)) : fmaxf(fmaxf(v0, v1), fmaxf(v2, v3));
+            m |= M == L2 ? __builtin_amdgcn_ballot_w64(e <= st.T[cb]) : __builtin_amdgcn_ballot_w64(e >= st.T[cb]);
         }
-        const uint64_t m = M == L2 ? __builtin_amdgcn_ballot_w64(e[0] <= st.T[0]) |
-                                         __builtin_amdgcn_ballot_w64(e[1] <= st.T[1])
-                                   : __builtin_amdgcn_ballot_w64(e[0] >= st.T[0]) |
-                                         __builtin_amdgcn_ballot_w64(e[1] >= st.T[1]);
         if (!(m != 0 && enable)) return;
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
-            for (int cb = 0; cb < 2; ++cb) {
+            for (int cb = 0; cb < CB; ++cb) {
                 const float v = acc2[cb][4 * g + j];
                 p[j][cb] = M == L2 ? v <= st.T[cb] : v >= st.T[cb];
             }
@@ -1002,7 +1002,7 @@ __device__ __forceinline__ void filter_group(const floatx16 (&acc2)[2], floatx4 
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
-            for (int cb = 0; cb < 2; ++cb) {
+            for (int cb = 0; cb < CB; ++cb) {
                 const float dot = acc2[cb][4 * g + j];
                 const float sc = st.cn[cb] * n4[j] > 1e-9f ? -dot : 0.0f * dot;
                 p[j][cb] = sc <= st.tau_e[cb];
@@ -1013,7 +1013,7 @@ __device__ __forceinline__ void filter_group(const floatx16 (&acc2)[2], floatx4 
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
-            for (int cb = 0; cb < 2; ++cb) {
+            for (int cb = 0; cb < CB; ++cb) {
                 if (!p[j][cb]) continue;
                 const float dot = acc2[cb][4 * g + j];
                 float sc;
@@ -1031,11 +1031,11 @@ __device__ __forceinline__ void filter_group(const floatx16 (&acc2)[2], floatx4 
     }
 }
 
-template <int M>
-__device__ __forceinline__ void dense_group(const floatx16 (&acc2)[2], floatx4 n4, const EpiState &st,
+template <int M, int CB = 2>
+__device__ __forceinline__ void dense_group(const floatx16 (&acc2)[CB], floatx4 n4, const EpiState &st,
                                             const ScanArgs &a, int wc, int l32, long row, int col0, int g) {
 #pragma unroll
-    for (int cb = 0; cb < 2; ++cb) {
+    for (int cb = 0; cb < CB; ++cb) {
         const int q = col0 + 64 * wc + 32 * cb + l32;
         if (q >= a.ncols) continue;
         uint2 *dst = a.cand + (size_t)q * a.cap;
@@ -1345,6 +1345,234 @@ __global__ __launch_bounds__(512, 1) void k_mfma_hs(ScanArgs a) {
     }
 }
 
+// =========================================================================================
+// Narrow resident-tile kernel (kNN search at dpad a multiple of 128 from 256 to 896).  A work item is
+// kNtCols = 32 query columns, whose 32 x dpad tile stays resident in LDS (96 KB at dpad 768), x
+// item_rows base rows in stages of 512: each of the 8 waves streams its own 64 rows of A from L2
+// into registers two K-chunks ahead and computes its 64 x 32 block in two
+// halves of 32 rows, the epilogue of one half running under the MFMAs of the other, as in
+// k_mfma_hs.  The tile operand of each 4-MFMA group is read from LDS one group ahead.  Each half
+// accumulates in two chains (even and odd K pairs) summed at its end, so that a wave's
+// consecutive MFMAs do not wait for each other.  Against the panel kernel, whose 128-column
+// tiles pass through LDS in K-panels, the query tile is read once per work item instead of once
+// per 256-row stage, nothing inside an item takes a barrier, and the 32 workgroups of an XCD
+// (32 consecutive column tiles of one row range) share each base row through its L2.
+// Items are multiples of 256 rows, so a stage can reach past the item's last row: a wave whose 64
+// rows start at or past it reads the item's first 64 rows instead (always inside the padded
+// base) and evaluates nothing.
+// =========================================================================================
+template <int MODE, int M, int NK>
+__global__ __launch_bounds__(512, 1) void k_mfma_nt(ScanArgs a) {
+    static_assert(MODE != kAssign, "search modes only");
+    constexpr int TR = 512, D = 32 * NK, TC = kNtCols;
+    constexpr bool FUSE = M == L2;  // accumulators start from the row norms; the tile holds -2 q
+    // prefetch distance in K-chunks: 2 (4% faster at dpad 768 than 1; 3 gains nothing at dpad 256
+    // to 512), 1 in the dense round at dpad 896, whose registers would spill
+    constexpr int PD = MODE == kDense && NK >= 28 ? 1 : 2;
+    __shared__ floatx4 sB[TC * 8 * NK];
+    __shared__ uint32_t s_qcnt[MODE == kFilter ? TC : 1];
+    __shared__ uint2 s_slot[MODE == kFilter ? TC * kNtSlots : 1];
+
+    const int tid = threadIdx.x, lane = tid & 63, wr = tid >> 6;  // wave wr: rows 64 wr .. of a stage
+    const int l32 = lane & 31, h = lane >> 5;
+    const int G = gridDim.x;
+    int item = first_item();
+    if (item >= a.n_items) return;
+
+    // swizzled tile layout, as in k_mfma_hs (row r = query column, chunk kc, 16-byte slot c4)
+    auto bidx_kc = [](int r, int kc, int c4) {
+        const int pch = (NK % 2 == 0) ? (kc ^ (r & 1)) : kc;
+        return r * (8 * NK) + pch * 8 + (c4 ^ ((r >> 1) & 7));
+    };
+    auto fill_b = [&](int c0) {
+        constexpr int PER = TC * 8 * NK / 512;
+        floatx4 rq[PER];
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int f = tid + 512 * i;
+            const int r = f / (8 * NK), rem = f % (8 * NK);
+            rq[i] = *(const floatx4 *)(a.B + (long)(c0 + r) * D + 4 * rem);
+        }
+        if constexpr (FUSE) {
+#pragma unroll
+            for (int i = 0; i < PER; ++i) rq[i] = rq[i] * -2.0f;  // exact
+        }
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int f = tid + 512 * i;
+            const int r = f / (8 * NK), rem = f % (8 * NK);
+            sB[bidx_kc(r, rem >> 3, rem & 7)] = rq[i];
+        }
+    };
+    // A of half hf, chunk kc of the rows at `base`: row base + 64 wr + 32 hf + l32, floats 32 kc + 8 g + 4 h.
+    auto load_a = [&](floatx4 (&r)[4], long base, int hf, int kc) {
+        const float *p0 = a.A + (base + 64 * wr + 32 * hf + l32) * (long)D + 32 * kc + 4 * h;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) r[g] = *(const floatx4 *)(p0 + 8 * g);
+    };
+    auto load_n = [&](floatx4 (&n)[4], long base, int hf) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) n[g] = *(const floatx4 *)(a.anorm + base + 64 * wr + 32 * hf + 8 * g + 4 * h);
+    };
+    // one K-chunk of a half into its two chains; at kc = 0 chain 0 starts from `init`, chain 1 from 0.
+    // bq holds the tile operand of (kc, group 0) on entry; each group reads the next group's
+    // (wrapping to chunk 0, which the next half and stage start with) before its own MFMAs, so
+    // the LDS latency runs under them.
+    const floatx16 zero16 = floatx16{0};
+    auto mfma_step = [&](floatx16 (&ch)[2], const floatx4 (&ra)[4], floatx4 &bq, int kc, const floatx16 &init) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const floatx4 b = bq;
+            const int nkc = g < 3 ? kc : (kc + 1 < NK ? kc + 1 : 0);
+            bq = sB[bidx_kc(l32, nkc, 2 * ((g + 1) & 3) + h)];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const bool first = kc == 0 && g == 0 && t < 2;
+                ch[t & 1] = __builtin_amdgcn_mfma_f32_32x32x2f32(ra[g][t], b[t],
+                                                                 first ? (t == 0 ? init : zero16) : ch[t & 1], 0, 0, 0);
+            }
+        }
+    };
+    auto n16 = [](const floatx4 (&n)[4]) {
+        floatx16 v;
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[4 * g + j] = n[g][j];
+        return v;
+    };
+
+    int col0;
+    long r_lo, r_hi;
+    decode_item<TC>(a, item, col0, r_lo, r_hi);
+    fill_b(col0);
+    if constexpr (MODE == kFilter) {
+        if (tid < TC) s_qcnt[tid] = 0;
+    }
+    long rs = r_lo;
+    bool act = rs + 64 * wr < r_hi;  // this wave's rows of the stage belong to the item
+    EpiState st;
+    item_begin<MODE, M, 1>(st, a, col0, 0, l32);
+    // A chunks in flight: pf[0] is this step's, pf[j] the one j steps ahead
+    floatx4 pf[PD][4];
+#pragma unroll
+    for (int j = 0; j < PD; ++j) load_a(pf[j], act ? rs : r_lo - 64 * wr, 0, j);
+    __syncthreads();
+    floatx4 bq = sB[bidx_kc(l32, 0, h)];
+
+    floatx16 ch[2];      // the running half's two chains
+    floatx16 res[2][1];  // each half's summed accumulators, for its epilogue
+    floatx4 nrm[2][4];   // epilogue values (row norms) of each half's rows
+    bool prev = false;   // the previous stage's second half is still to be evaluated
+    bool pact = false;   // ... and belonged to the item
+
+    auto epi = [&](const floatx16 (&ac)[1], const floatx4 (&n)[4], long srs, int hf, int g0, int g1, bool enable) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            if (g < g0 || g >= g1) continue;
+            if constexpr (MODE == kFilter) {
+                filter_group<M, kNtSlots, 1>(ac, n[g], st, a, 0, l32,
+                                             (uint32_t)(srs - r_lo) + 64 * wr + 32 * hf + 8 * g + 4 * h, r_lo, col0,
+                                             s_qcnt, s_slot, g, enable);
+            } else if (enable) {
+                dense_group<M, 1>(ac, n[g], st, a, 0, l32, srs + 64 * wr + 32 * hf + 8 * g + 4 * h, col0, g);
+            }
+        }
+    };
+    auto interleave = [&]() {  // per group: the next group's LDS read, then 1 MFMA and up to 2 VALU
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+            }
+        }
+    };
+
+    for (;;) {
+        long nrs = rs + TR;
+        int nitem = item, ncol0 = col0;
+        long nlo = r_lo, nhi = r_hi;
+        const bool item_end = nrs >= r_hi;
+        bool more = true;
+        if (item_end) {
+            nitem = item + G;
+            more = nitem < a.n_items;
+            if (more) {
+                decode_item<TC>(a, nitem, ncol0, nlo, nhi);
+                nrs = nlo;
+            }
+        }
+        // the rows this wave reads: its own, or (an idle wave) the item's first 64
+        const long base = act ? rs : r_lo - 64 * wr;
+        const bool nact = nrs + 64 * wr < nhi;
+        const long nbase = nact ? nrs : nlo - 64 * wr;
+        // ---- half 0: MFMAs into the chains; epilogue of the previous stage's half 1 ----
+        load_n(nrm[0], base, 0);
+        const floatx16 init0 = FUSE ? n16(nrm[0]) : zero16;
+#pragma unroll
+        for (int kc = 0; kc < NK; ++kc) {
+            floatx4 nn[4];
+            if (kc + PD < NK) load_a(nn, base, 0, kc + PD);
+            else load_a(nn, base, 1, kc + PD - NK);
+            __builtin_amdgcn_sched_barrier(0);
+            mfma_step(ch, pf[0], bq, kc, init0);
+            epi(res[1], nrm[1], rs - TR, 1, (4 * kc) / NK, (4 * (kc + 1)) / NK, prev && pact);
+            interleave();
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+#pragma unroll
+                for (int j = 0; j + 1 < PD; ++j) pf[j][i] = pf[j + 1][i];
+                pf[PD - 1][i] = nn[i];
+            }
+        }
+        res[0][0] = ch[0] + ch[1];
+        // ---- half 1: MFMAs into the chains; epilogue of this stage's half 0 ----
+        load_n(nrm[1], base, 1);
+        const floatx16 init1 = FUSE ? n16(nrm[1]) : zero16;
+#pragma unroll
+        for (int kc = 0; kc < NK; ++kc) {
+            floatx4 nn[4];
+            if (kc + PD < NK) load_a(nn, base, 1, kc + PD);
+            else if (more) load_a(nn, nbase, 0, kc + PD - NK);  // the next stage's first chunks
+            __builtin_amdgcn_sched_barrier(0);
+            mfma_step(ch, pf[0], bq, kc, init1);
+            epi(res[0], nrm[0], rs, 0, (4 * kc) / NK, (4 * (kc + 1)) / NK, act);
+            interleave();
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {  // past the last stage nn is unset, and no step uses it
+#pragma unroll
+                for (int j = 0; j + 1 < PD; ++j) pf[j][i] = pf[j + 1][i];
+                pf[PD - 1][i] = nn[i];
+            }
+        }
+        res[1][0] = ch[0] + ch[1];
+        prev = true;
+        pact = act;
+        if (item_end) {
+            // drain: this stage's half 1, then the item's candidates
+            epi(res[1], nrm[1], rs, 1, 0, 4, act);
+            if constexpr (MODE == kFilter) filter_flush<kNtSlots, TC>(a, col0, r_lo, s_qcnt, s_slot);
+            if (!more) break;
+            // every wave is past this item's MFMAs (the flush has a barrier; DENSE takes one here)
+            if constexpr (MODE == kDense) __syncthreads();
+            fill_b(ncol0);
+            __syncthreads();
+            bq = sB[bidx_kc(l32, 0, h)];
+            item = nitem;
+            col0 = ncol0;
+            r_lo = nlo;
+            r_hi = nhi;
+            item_begin<MODE, M, 1>(st, a, col0, 0, l32);
+            prev = false;
+        }
+        rs = nrs;
+        act = nact;
+    }
+}
+
 // ---- launch ----------------------------------------------------------------------------
 static int grid_for(long n_items, int cap) {
     long g = n_items < cap ? n_items : cap;
@@ -1366,8 +1594,19 @@ static void launch_scan(const ScanArgs &a, int grid_cap, hipStream_t s) {
             default: hipLaunchKernelGGL((k_mfma_hs<MODE, M, 4>), g, b, 0, s, a); break;
         }
     } else if (nk % 4 == 0) {
-        const dim3 g(grid_for(a.n_items, cus)), b(512);
-        hipLaunchKernelGGL((k_mfma_pnl<MODE, M>), g, b, 0, s, a);
+        const dim3 g(grid_for(a.n_items, cus));
+        if constexpr (MODE != kAssign) {
+            switch (gemm_filter_cols(a.dpad) == kNtCols ? nk : 0) {  // the narrow-tile instantiations
+                case 8: hipLaunchKernelGGL((k_mfma_nt<MODE, M, 8>), g, dim3(512), 0, s, a); return;
+                case 12: hipLaunchKernelGGL((k_mfma_nt<MODE, M, 12>), g, dim3(512), 0, s, a); return;
+                case 16: hipLaunchKernelGGL((k_mfma_nt<MODE, M, 16>), g, dim3(512), 0, s, a); return;
+                case 20: hipLaunchKernelGGL((k_mfma_nt<MODE, M, 20>), g, dim3(512), 0, s, a); return;
+                case 24: hipLaunchKernelGGL((k_mfma_nt<MODE, M, 24>), g, dim3(512), 0, s, a); return;
+                case 28: hipLaunchKernelGGL((k_mfma_nt<MODE, M, 28>), g, dim3(512), 0, s, a); return;
+                default: break;
+            }
+        }
+        hipLaunchKernelGGL((k_mfma_pnl<MODE, M>), g, dim3(512), 0, s, a);
     } else {
         const dim3 g(grid_for(a.n_items, 2 * cus)), b(256);
         hipLaunchKernelGGL((k_mfma_stream<MODE, M>), g, b, 0, s, a);
@@ -1395,7 +1634,7 @@ void launch_gemm_filter(int metric, bool dense, long item_rows, const float *bas
     a.bnorm = qnorm;
     a.dpad = dpad;
     a.ncols = nq;
-    a.n_ctiles = ceil_div(nq, kTileCols);
+    a.n_ctiles = ceil_div(nq, gemm_filter_cols(dpad));
     a.item_rows = item_rows;
     a.row_begin = row_begin;
     a.row_end = row_end;

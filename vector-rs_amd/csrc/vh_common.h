@@ -16,12 +16,20 @@ constexpr int kMaxK = 2048;          // VHIP_MAX_K
 constexpr int kGemmSlotsReg = 48;    // LDS candidate slots per query and work item, register-fed MFMA kernel
 constexpr int kGemmSlotsPanel = 24;  // same, panel MFMA kernel (dpad a multiple of 128 above 128)
 constexpr int kGemmSlotsStream = 14; // same, streaming MFMA kernel (other dpad > 128)
-// LDS candidate slots of the MFMA filter kernel that serves rows of dpad floats
-inline int gemm_slots(int dpad) {
-    return dpad <= 128 ? kGemmSlotsReg : (dpad % 128 == 0 ? kGemmSlotsPanel : kGemmSlotsStream);
-}
+constexpr int kGemmSlotsNarrow = 48; // same, narrow resident-tile MFMA kernel (see gemm_filter_cols)
 constexpr int kKChunk = 32;          // K (dimension) chunk of the MFMA tiles
 constexpr int kTileCols = 128;       // queries (or k-means points) per MFMA work item
+constexpr int kNtCols = 32;          // queries per work item of the narrow resident-tile kernel
+// Query columns per work item of the MFMA search kernel that serves rows of dpad floats: the
+// narrow resident-tile kernel takes dpad a multiple of 128 from 256 to 896 (its 32 x dpad query
+// tile stays in LDS), the others kTileCols.
+inline bool gemm_narrow(int dpad) { return dpad % 128 == 0 && dpad >= 256 && dpad <= 896; }
+inline int gemm_filter_cols(int dpad) { return gemm_narrow(dpad) ? kNtCols : kTileCols; }
+// LDS candidate slots of the MFMA search kernel that serves rows of dpad floats
+inline int gemm_slots(int dpad) {
+    return dpad <= 128 ? kGemmSlotsReg
+                       : (gemm_narrow(dpad) ? kGemmSlotsNarrow : (dpad % 128 == 0 ? kGemmSlotsPanel : kGemmSlotsStream));
+}
 constexpr int kRowAlign = 256;       // row counts of MFMA row operands and round boundaries
                                      // are multiples of this (the largest MFMA stage)
 
