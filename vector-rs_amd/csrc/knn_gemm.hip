@@ -1479,7 +1479,9 @@ __global__ __launch_bounds__(512, 1) void k_mfma_nt(ScanArgs a) {
             }
         }
     };
-    auto interleave = [&]() {  // per group: the next group's LDS read, then 1 MFMA and up to 2 VALU
+    // per group: the next group's LDS read, then 1 MFMA and up to 2 VALU.  Placed in the MFMA block
+    // (before the epilogue's branches), where the scheduler applies it
+    auto interleave = [&]() {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
@@ -1519,8 +1521,8 @@ __global__ __launch_bounds__(512, 1) void k_mfma_nt(ScanArgs a) {
             else load_a(nn, base, 1, kc + PD - NK);
             __builtin_amdgcn_sched_barrier(0);
             mfma_step(ch, pf[0], bq, kc, init0);
-            epi(res[1], nrm[1], rs - TR, 1, (4 * kc) / NK, (4 * (kc + 1)) / NK, prev && pact);
             interleave();
+            epi(res[1], nrm[1], rs - TR, 1, (4 * kc) / NK, (4 * (kc + 1)) / NK, prev && pact);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
 #pragma unroll
@@ -1539,8 +1541,8 @@ __global__ __launch_bounds__(512, 1) void k_mfma_nt(ScanArgs a) {
             else if (more) load_a(nn, nbase, 0, kc + PD - NK);  // the next stage's first chunks
             __builtin_amdgcn_sched_barrier(0);
             mfma_step(ch, pf[0], bq, kc, init1);
-            epi(res[0], nrm[0], rs, 0, (4 * kc) / NK, (4 * (kc + 1)) / NK, act);
             interleave();
+            epi(res[0], nrm[0], rs, 0, (4 * kc) / NK, (4 * (kc + 1)) / NK, act);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {  // past the last stage nn is unset, and no step uses it
 #pragma unroll
