@@ -86,3 +86,55 @@ def test_hamming_massive_ties(vh, oracle, bits):
     assert np.all(lens == 12)
     assert np.array_equal(dist, rdist) and np.array_equal(ids, rids)
     assert np.array_equal(ids, np.tile(np.arange(12, dtype=ids.dtype), (5, 1)))
+
+
+# The 1024-column kernel serves filter rounds of codes up to 256 bits once a batch has at least
+# 2048 queries and the round starts past 2048 * 3 k / 8 rows seen; the rest of a search runs on
+# the 128-column kernel.  nq = 2500 leaves the last column block with 4 of its 8 waves active.
+@pytest.mark.parametrize("n,bits,nq,k", [(150_000, 256, 2048, 10), (150_000, 256, 2500, 100),
+                                         (120_000, 128, 2100, 10), (120_000, 32, 2048, 25),
+                                         (140_000, 64, 3000, 1)])
+def test_hamming_wide_kernel_bit_exact(vh, oracle, n, bits, nq, k):
+    from vector_hip import datasets as ds
+
+    print(f"hamming wide n={n} bits={bits} nq={nq} k={k}", flush=True)
+    codes = ds.packed_bits(n, bits, 41)
+    q = ds.packed_bits(nq, bits, 42)
+    ids, dist, lens = vh.HammingKnnEngine(codes).search_batch_arrays(q, k)
+    rids, rdist, _ = oracle.hamming_packed_knn(codes, q, k)
+    assert np.all(lens == k)
+    assert np.array_equal(dist, rdist), "distances must be bit-exact"
+    assert np.array_equal(ids, rids), "(distance, id) order makes ids identical"
+
+
+def test_hamming_wide_kernel_ties(vh, oracle):
+    """Few distinct codes: whole items tie, so the 8 LDS slots per query overflow into the
+    global lists and the capacity re-run, and the (distance, id) order must still hold."""
+    from vector_hip import datasets as ds
+
+    print("hamming wide ties", flush=True)
+    distinct = ds.packed_bits(16, 256, 5)
+    rng = np.random.default_rng(6)
+    codes = distinct[rng.integers(0, 16, 90_000)]
+    q = ds.packed_bits(2048, 256, 7)
+    ids, dist, lens = vh.HammingKnnEngine(codes).search_batch_arrays(q, 10)
+    rids, rdist, _ = oracle.hamming_packed_knn(codes, q, 10)
+    assert np.all(lens == 10)
+    assert np.array_equal(dist, rdist) and np.array_equal(ids, rids)
+
+
+def test_hamming_wide_matches_tile_kernel(vh, monkeypatch):
+    """The 1024-column kernel and the 128-column kernel (VHIP_HAMMING_KERNEL=fp4-tile) return
+    identical results on the same engine data."""
+    from vector_hip import datasets as ds
+
+    print("hamming wide vs tile", flush=True)
+    codes = ds.packed_bits(200_000, 256, 8)
+    q = ds.packed_bits(4096, 256, 9)
+    wide = vh.HammingKnnEngine(codes).search_batch_arrays(q, 20)
+    monkeypatch.setenv("VHIP_HAMMING_KERNEL", "fp4-tile")
+    tile_eng = vh.HammingKnnEngine(codes)
+    monkeypatch.delenv("VHIP_HAMMING_KERNEL")
+    tile = tile_eng.search_batch_arrays(q, 20)
+    for a, b in zip(wide, tile):
+        assert np.array_equal(a, b)

@@ -20,6 +20,7 @@
 // and XCD-aware like the FP32 kernels.  FILTER keeps (distance, row) pairs with distance <= tau
 // in per-query LDS slots flushed once per item; DENSE (the first round) writes every pair.
 #include <algorithm>
+#include <climits>
 
 #include "vh_common.h"
 
@@ -307,6 +308,304 @@ __global__ __launch_bounds__(512, 1) void k_mfma_ham(HamArgs a) {
     }
 }
 
+// =========================================================================================
+// Wide filter kernel (codes of at most 256 bits, filter rounds).  The kernel above streams each
+// wave's base rows from L2 into registers and shares a 128-query tile through LDS: every base
+// byte then crosses the L2 -> L1 path once per 128 queries, and that feed (not the matrix pipe)
+// bounds it.  Here the roles swap.  A work item is 1024 query columns; each of the 8 waves keeps
+// its 128 columns' expanded codes in registers for the whole item (4 tiles x KC chunks x 16
+// bytes per lane), and the base passes through a ring of 64-row stages in LDS, copied by
+// global_load_lds (one 1 KB piece per wave and stage), which all 8 waves read.  Each base byte
+// then feeds 1024 queries per fetch.  Every wave scores each stage as two halves of 32 rows, and
+// interleaves the MFMAs of one half with the threshold pre-test of the other (the previous
+// stage's second half, or this stage's first), so the epilogue's VALU work runs in the matrix
+// pipe's shadow.
+// Ring protocol: one LDS barrier every kHwSync stages, in the middle of stage t (t a multiple of
+// kHwSync), after the wave's reads of stage t's first half.  Before it each wave waits for its
+// own DMAs (stages up to t + kHwSync, issued at the previous barrier); after it every wave's
+// pieces of those stages are visible and every wave is done with the stages before t, so the
+// DMAs of stages t + kHwSync + 1 .. t + 2 kHwSync go into those slots (2 kHwSync + 1 slots keep
+// stages t .. t + 2 kHwSync apart).  Sparse barriers let a wave that appends candidates in one
+// stage catch up in the next ones instead of holding all eight waves at every stage.
+// =========================================================================================
+constexpr int kHwCols = ham_wide_cols();    // query columns per work item: 8 waves x 128
+constexpr int kHwStage = 64;                 // base rows per stage (all 8 waves score the same rows)
+constexpr int kHwSync = 4;                   // stages per workgroup barrier
+constexpr int kHwRing = 2 * kHwSync + 1;     // LDS ring stages (see k_mfma_ham_wide)
+constexpr int kHwSlots = ham_wide_slots();   // LDS candidate slots per query per work item
+static_assert(kHwCols == 8 * 128, "one 128-column block per wave");
+
+template <int KC>
+__global__ __launch_bounds__(512, 1) void k_mfma_ham_wide(HamArgs a) {
+    constexpr int K = 64 * KC, RB = 32 * KC, SB = kHwStage * RB;  // bits, bytes per row, bytes per stage
+    constexpr int NPIECE = 2 * KC;                                 // 1 KB pieces per stage
+    static_assert(KC == 1 || KC == 2 || KC == 4, "codes of 64 to 256 expanded bits");
+    __shared__ __attribute__((aligned(16))) int8_t s_ring[kHwRing * SB];
+    __shared__ uint32_t s_qcnt[kHwCols];
+    __shared__ uint2 s_slot[kHwCols * kHwSlots];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int l32 = lane & 31, h = lane >> 5;
+    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+    const int G = gridDim.x;
+    int item = ham_first_item();
+    if (item >= a.n_items) return;  // uniform over the workgroup
+
+    auto decode = [&](int it, int &c0, long &lo, long &hi) {
+        const int ct = it % a.n_ctiles;
+        const long chunk = it / a.n_ctiles;
+        c0 = ct * kHwCols;
+        lo = a.row_begin + chunk * a.item_rows;
+        hi = min(lo + a.item_rows, a.row_end);
+    };
+    const uint32_t ring_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)&s_ring[0];
+    // The DMA cursor runs up to 2 kHwSync stages ahead of the scored stage over the same sequence
+    // of (item, stage).  Past the last stage it keeps re-reading the last one (in bounds, never
+    // scored), so every wave issues exactly one DMA per stage and its vmcnt waits stay constant.
+    int d_item = item;
+    long d_rs, d_hi;
+    {
+        int c0;
+        long lo;
+        decode(d_item, c0, lo, d_hi);
+        d_rs = lo;
+    }
+    auto dma_stage = [&](int t) {
+        if (wave_u < NPIECE)
+            dma_lds16(a.A + ((size_t)(d_rs >> 5) * KC) * 1024 + 1024 * wave_u + 16 * lane,
+                      ring_lds + (uint32_t)((t % kHwRing) * SB + 1024 * wave_u));
+    };
+    auto d_advance = [&]() {
+        const long n = d_rs + kHwStage;
+        if (n < d_hi) {
+            d_rs = n;
+        } else if (d_item + G < a.n_items) {
+            d_item += G;
+            int c0;
+            long lo;
+            decode(d_item, c0, lo, d_hi);
+            d_rs = lo;
+        }
+    };
+    // the A operand of half hf, K-chunk kc of the stage in ring slot t % kHwRing
+    auto read_a = [&](int t, int hf, int kc) {
+        return *(const intx4 *)(s_ring + (t % kHwRing) * SB + (hf * KC + kc) * 1024 + 16 * lane);
+    };
+
+    int col0;
+    long r_lo, r_hi;
+    decode(item, col0, r_lo, r_hi);
+    // this wave's 128 columns: query operands in registers, thresholds per column
+    // (distance <= tq  <=>  dot >= T = K - 2 floor(tq); columns past nq never pass)
+    intx4 bq[4][KC];
+    float T[4];
+    int TI[4];  // the pre-test's integer form of T
+    bool active = false;
+    auto item_begin = [&]() {
+        // A wave whose columns all lie past nq (the last column block) skips its MFMAs and drops
+        // its masks; its operands are zeroed so that no register is read undefined.
+        active = col0 + 128 * wave_u < a.nq;  // rows of B are allocated up to a multiple of 128
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+            for (int kc = 0; kc < KC; ++kc)
+                bq[cb][kc] = active ? *(const intx4 *)(a.B + (size_t)(col0 + 128 * wave + 32 * cb + l32) * RB +
+                                                       32 * kc + 16 * h)
+                                    : intx4{0, 0, 0, 0};
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb) {
+            const int q = col0 + 128 * wave + 32 * cb + l32;
+            const float t = q < a.nq ? a.tau[q] : -1.0f;
+            T[cb] = (float)(t < 0.0f ? K + 1 : (t >= (float)K ? -K : K - 2 * (int)t));
+            TI[cb] = T[cb] > 0.0f ? __builtin_bit_cast(int, T[cb]) : INT_MIN;
+        }
+    };
+    item_begin();
+    for (int i = tid; i < kHwCols; i += 512) s_qcnt[i] = 0;
+    // prologue: stages 0 .. kHwSync (and the query operands) landed and visible
+    int t = 0;  // stages scored so far by this workgroup (ring slot t % kHwRing)
+#pragma unroll
+    for (int i = 0; i <= kHwSync; ++i) {
+        dma_stage(i);
+        d_advance();
+    }
+    __builtin_amdgcn_s_waitcnt(VH_VMCNT(0));
+    lds_barrier();
+
+    floatx16 acc[2][4];
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb) acc[hf][cb] = floatx16{0.0f};
+    // Threshold pre-test of tile cb of a half: some value of the lane's column among the tile's
+    // 16 rows may reach T.  The values are integers in [-K, K] held as floats.  For T > 0 the
+    // test runs on their bit patterns as signed integers: non-negative floats order like their
+    // patterns, and negative ones read as negative integers, below every positive T.  That makes
+    // the maximum one tree of 8 integer max3 operations (no NaN canonicalisation, 3 deep).  For
+    // T <= 0 (a threshold of at least K / 2 bits, early rounds only) TI = INT_MIN sends the half
+    // to the exact per-row tests.
+    auto pretest = [&](const floatx16 &v, int cb) {
+        int x[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            // through a scalar: this compiler's __builtin_bit_cast of a vector-element expression
+            // reads element 0 whatever the index
+            const float f = v[i];
+            x[i] = __builtin_bit_cast(int, f);
+        }
+        auto m3 = [](int a, int b, int c) { return max(max(a, b), c); };
+        const int a0 = m3(x[0], x[1], x[2]), a1 = m3(x[3], x[4], x[5]), a2 = m3(x[6], x[7], x[8]);
+        const int a3 = m3(x[9], x[10], x[11]), a4 = m3(x[12], x[13], x[14]);
+        const int mx = max(m3(a0, a1, a2), m3(a3, a4, x[15]));
+        return __builtin_amdgcn_ballot_w64(mx >= TI[cb]);
+    };
+    // per-row tests and LDS slot appends of a half that passed the pre-test; register 4g+j of
+    // tile cb holds row srs + 32 hf + 8 g + 4 h + j and column 128 wave + 32 cb + l32
+    auto append = [&](const floatx16 (&ac)[4], long srs, int hf) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const long row0 = srs + 32 * hf + 8 * g + 4 * h;
+            uint64_t m = 0;
+#pragma unroll
+            for (int cb = 0; cb < 4; ++cb) {
+                const floatx16 &v = ac[cb];
+                const float mx = fmaxf(fmaxf(v[4 * g], v[4 * g + 1]), fmaxf(v[4 * g + 2], v[4 * g + 3]));
+                m |= __builtin_amdgcn_ballot_w64(mx >= T[cb]);
+            }
+            if (m == 0) continue;
+#pragma unroll
+            for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float dot = ac[cb][4 * g + j];
+                    const long row = row0 + j;
+                    if (dot < T[cb] || row >= r_hi) continue;
+                    const int ql = 128 * wave + 32 * cb + l32;
+                    const uint32_t key = score_key(((float)K - dot) * 0.5f);
+                    const uint32_t r = atomicAdd(&s_qcnt[ql], 1u);
+                    if (r < (uint32_t)kHwSlots) {
+                        s_slot[ql * kHwSlots + r] = make_uint2(key, (uint32_t)(row - r_lo));
+                    } else {
+                        // rare overflow: straight to the global list, drained here so no store
+                        // is pending where this path rejoins the loop
+                        const int q = col0 + ql;
+                        const uint32_t at =
+                            __hip_atomic_fetch_add((gu32 *)a.cnt + q, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        if (at < (uint32_t)a.cap) ((gu64 *)a.cand)[(size_t)q * a.cap + at] = pack_u2(key, (uint32_t)row);
+                        __builtin_amdgcn_s_waitcnt(VH_VMCNT(0));
+                    }
+                }
+        }
+    };
+    // one step: the 4 MFMAs of (half hf, chunk kc) on operand `cur`, interleaved with the
+    // pre-test of the tiles [4 kc / KC, 4 (kc + 1) / KC) of the other half's accumulators `oth`
+    // (unconditional, so it stays in the MFMAs' basic block; the caller ignores the mask of a
+    // half that holds no scores)
+    auto step = [&](floatx16 (&ac)[4], const intx4 &cur, int kc, const floatx16 (&oth)[4], uint64_t &mask) {
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb)
+            ac[cb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fp4_operand(cur), fp4_operand(bq[cb][kc]),
+                                                                     kc == 0 ? floatx16{0.0f} : ac[cb], 4, 4, 0, 127,
+                                                                     0, 127);
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb)
+            if (cb >= 4 * kc / KC && cb < 4 * (kc + 1) / KC) mask |= pretest(oth[cb], cb);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+        }
+    };
+
+    long rs = r_lo, prs = 0;
+    bool prev = false;  // the previous stage's second half still awaits its pre-test
+    intx4 cur = read_a(0, 0, 0);
+    for (;;) {
+        long nrs = rs + kHwStage;
+        int nitem = item, ncol0 = col0;
+        long nlo = r_lo, nhi = r_hi;
+        const bool item_end = nrs >= r_hi;
+        bool more = true;
+        if (item_end) {
+            nitem = item + G;
+            more = nitem < a.n_items;
+            if (more) {
+                decode(nitem, ncol0, nlo, nhi);
+                nrs = nlo;
+            }
+        }
+        // ---- half 0: MFMAs into acc[0]; pre-test of the previous stage's half 1 ----
+        uint64_t m1 = 0;
+#pragma unroll
+        for (int kc = 0; kc < KC; ++kc) {
+            const intx4 nxt = kc + 1 < KC ? read_a(t, 0, kc + 1) : read_a(t, 1, 0);
+            if (active) step(acc[0], cur, kc, acc[1], m1);
+            cur = nxt;
+        }
+        if (!prev || !active) m1 = 0;  // acc[1] holds no scores of this item, or no real columns
+        if (t % kHwSync == 0) {
+            __builtin_amdgcn_s_waitcnt(VH_VMCNT(0));  // this wave's pieces of stages <= t + kHwSync
+            lds_barrier();
+#pragma unroll
+            for (int i = 1; i <= kHwSync; ++i) {
+                dma_stage(t + kHwSync + i);
+                d_advance();
+            }
+        }
+        if (m1) append(acc[1], prs, 1);
+        // ---- half 1: MFMAs into acc[1]; pre-test of this stage's half 0 ----
+        uint64_t m0 = 0;
+#pragma unroll
+        for (int kc = 0; kc < KC; ++kc) {
+            // stage t + 1 is visible since the last barrier; past the last stage this reads a
+            // slot's stale data, never used
+            const intx4 nxt = kc + 1 < KC ? read_a(t, 1, kc + 1) : read_a(t + 1, 0, 0);
+            if (active) step(acc[1], cur, kc, acc[0], m0);
+            cur = nxt;
+        }
+        if (!active) m0 = 0;
+        if (m0) append(acc[0], rs, 0);
+        prev = true;
+        prs = rs;
+        ++t;
+        if (item_end) {
+            // drain: this stage's half 1, then the item's candidate flush
+            if (active) {
+                uint64_t m = 0;
+#pragma unroll
+                for (int cb = 0; cb < 4; ++cb) m |= pretest(acc[1][cb], cb);
+                if (m) append(acc[1], rs, 1);
+            }
+            prev = false;
+            lds_barrier();  // every wave's slot appends of this item are complete
+            for (int ql = tid; ql < kHwCols; ql += 512) {
+                uint32_t c = s_qcnt[ql];
+                if (c) {
+                    s_qcnt[ql] = 0;
+                    c = min(c, (uint32_t)kHwSlots);
+                    const int q = col0 + ql;
+                    const uint32_t base = atomicAdd(&a.cnt[q], c);
+                    for (uint32_t j = 0; j < c; ++j)
+                        if (base + j < (uint32_t)a.cap) {
+                            const uint2 e = s_slot[ql * kHwSlots + j];
+                            a.cand[(size_t)q * a.cap + base + j] = make_uint2(e.x, (uint32_t)(r_lo + e.y));
+                        }
+                }
+            }
+            lds_barrier();  // the counters are clear before the next item's appends
+            if (!more) break;
+            item = nitem;
+            col0 = ncol0;
+            r_lo = nlo;
+            r_hi = nhi;
+            item_begin();
+        }
+        rs = nrs;
+    }
+    // the re-reads past the last stage still write this workgroup's LDS: let them land first
+    __builtin_amdgcn_s_waitcnt(VH_VMCNT(0));
+}
+
 }  // namespace
 
 size_t ham_mfma_rows(size_t n) { return round_up(n, kHmStage) + kHmStage; }
@@ -365,6 +664,36 @@ void launch_ham_mfma(bool dense, long item_rows, const int8_t *base8, const int8
     }
 #undef VH_HM_K
 #undef VH_HM
+}
+
+bool ham_wide_supported(int wpad) { return ham_mfma_supported(wpad) && ham_chunks(wpad) <= 4; }
+
+void launch_ham_mfma_wide(long item_rows, const int8_t *base8, const int8_t *qry8, int wpad, const float *tau, int nq,
+                          long row_begin, long row_end, uint2 *cand, uint32_t *cnt, int cap, int grid_cap,
+                          hipStream_t s) {
+    if (nq <= 0 || row_end <= row_begin) return;
+    HamArgs a{};
+    a.A = base8;
+    a.B = qry8;
+    a.tau = tau;
+    a.nq = nq;
+    a.n_ctiles = ceil_div(nq, kHwCols);
+    a.item_rows = item_rows;
+    a.row_begin = row_begin;
+    a.row_end = row_end;
+    const long n_chunks = (row_end - row_begin + item_rows - 1) / item_rows;
+    a.n_items = (int)((long)a.n_ctiles * n_chunks);
+    a.cand = cand;
+    a.cnt = cnt;
+    a.cap = cap;
+    const int cus = grid_cap / 2;
+    long g = a.n_items < cus ? a.n_items : cus;
+    const dim3 grid((unsigned)((g + 7) / 8 * 8)), block(512);
+    switch (ham_chunks(wpad)) {
+        case 1: hipLaunchKernelGGL((k_mfma_ham_wide<1>), grid, block, 0, s, a); break;
+        case 2: hipLaunchKernelGGL((k_mfma_ham_wide<2>), grid, block, 0, s, a); break;
+        default: hipLaunchKernelGGL((k_mfma_ham_wide<4>), grid, block, 0, s, a); break;
+    }
 }
 
 }  // namespace vh

@@ -78,6 +78,7 @@ struct vhip_knn {
     float err_coeff = 0.0f;   // selection error coefficient of the GEMM-form score
     vh::DevBuf base8;  // packed Hamming on the fp4 matrix cores: one +1/-1 nibble per code bit
     bool ham8 = false;
+    bool ham_wide = false;  // filter rounds may use the 1024-column fp4 kernel (codes <= 256 bits)
     std::mutex mu;
     vh::Workspace ws;
     vh::PinnedStager stager;
@@ -95,10 +96,11 @@ namespace vh {
 
 // Search rounds.  Round 0 scores rows [0, b0) with b0 about 20 k, the first 256-row multiple
 // at or above it (all rows when the base has at most max(2048, 32 k)): for the GEMM metrics
-// densely (every score written, no atomics), for the others through the filter with tau = +inf.  Every later round covers about 8 times the rows seen so
-// far and keeps only rows scoring <= tau, the k-th best so far.  Because the base rows are in a
-// pseudo-random order, round i passes about k * (rows_i / seen_i) ~ 7 k candidates per query at a
-// rate p_i = k / seen_i per scored pair.  item_rows of the MFMA filter is sized so that a work
+// densely (every score written, no atomics), for the others through the filter with tau = +inf.
+// Every later round covers about 8 times the rows seen so far (the growth factor, see
+// round_growth) and keeps only rows scoring <= tau, the k-th best so far.  Because the base rows
+// are in a pseudo-random order, round i passes about k * (rows_i / seen_i) ~ 7 k candidates per
+// query at a rate p_i = k / seen_i per scored pair.  item_rows of the MFMA filter is sized so that a work
 // item's expected passes per query, item_rows * p_i, stay at most a third of the LDS slots.
 struct Round {
     long rb, re;
@@ -107,7 +109,7 @@ struct Round {
     long slot_rows;  // the slot rule's length alone
 };
 
-static std::vector<Round> plan_rounds(size_t n, size_t k, bool gemm, int dpad) {
+static std::vector<Round> plan_rounds(size_t n, size_t k, bool gemm, int dpad, int growth = 8) {
     std::vector<Round> r;
     if (n == 0) return r;
     const size_t kk = std::max<size_t>(k, 1);
@@ -119,7 +121,7 @@ static std::vector<Round> plan_rounds(size_t n, size_t k, bool gemm, int dpad) {
     const int slots = gemm_slots(dpad);
     size_t seen = b0;
     while (seen < n) {
-        const size_t e = std::min(n, round_up(seen * 8, kRowAlign));
+        const size_t e = std::min(n, round_up(seen * growth, kRowAlign));
         const size_t slot_item = std::max<size_t>(kRowAlign, (size_t)slots * seen / (3 * kk) / kRowAlign * kRowAlign);
         const size_t item = std::min<size_t>(8192, slot_item);
         r.push_back({(long)seen, (long)e, false, (long)item, (long)slot_item});
@@ -150,6 +152,12 @@ static long balanced_item(long cap_item, long rows, int n_ctiles, int wgs, long 
 // Candidate capacity per query and round: the dense round's rows, and room for several times
 // the ~7 k expected passes of a filter round.  A query that still overflows is re-run with a
 // capacity equal to the largest round.
+// Round growth: each round covers `growth` times the rows seen so far (8 above).  The fp4 Hamming
+// scan grows by 4: its candidate appends cost more, relative to its fast scan, than the extra
+// round's merge and launch (10M x 256 bits, Q = 10k, k = 10: 9.25 ms against 9.56 at 8; 3 and 4
+// measured alike, 2 slower).
+static int round_growth(const vhip_knn *E) { return E->ham8 ? 4 : 8; }
+
 static int round_cap(size_t n, size_t k, bool gemm, int dpad) {
     size_t cap = std::max<size_t>(2048, 32 * std::max<size_t>(k, 1));
     for (const Round &r : plan_rounds(n, k, gemm, dpad))
@@ -249,11 +257,12 @@ static int build_row_order(vhip_knn *E, size_t n, bool with_inverse) {
 // bytes) for the matrix-core kernel.  The copy is made when it takes at most half of the device
 // memory free at creation (the rest stays for search workspaces); otherwise the engine scans the
 // packed codes with the popcount kernel.  VHIP_HAMMING_KERNEL = "popcount" or "fp4" overrides
-// the choice for engines created afterwards (both kernels give identical results).
+// the choice for engines created afterwards, and "fp4-tile" takes the fp4 copy but keeps every
+// round on the 128-column tile kernel (all kernels give identical results).
 static bool want_fp4_copy(size_t bytes) {
     if (const char *env = std::getenv("VHIP_HAMMING_KERNEL")) {
         if (std::strcmp(env, "popcount") == 0) return false;
-        if (std::strcmp(env, "fp4") == 0) return true;
+        if (std::strcmp(env, "fp4") == 0 || std::strcmp(env, "fp4-tile") == 0) return true;
     }
     size_t free_b = 0, total_b = 0;
     if (hipMemGetInfo(&free_b, &total_b) != hipSuccess) {
@@ -321,7 +330,8 @@ static int run_rounds(vhip_knn *E, const QueryRows &Q, int nq, int k, int kc, in
         const size_t rows = round_up((size_t)nq, kTileCols);
         launch_ham_expand((const uint32_t *)Q.qpad, (size_t)nq, (int)E->dpad, (int)E->dpad, rows, false, B.q8, s);
     }
-    for (const Round &rd : split_rounds(plan_rounds(E->n, (size_t)k, gemm, (int)E->dpad), max_round_rows)) {
+    for (const Round &rd :
+         split_rounds(plan_rounds(E->n, (size_t)k, gemm, (int)E->dpad, round_growth(E)), max_round_rows)) {
         const long rb = rd.rb, re = rd.re;
         const bool dense = rd.dense || (E->ham8 && rb == 0);
         // Algorithmic work per launch: 2*Q*rows*D flops (GEMM metrics), Q*rows*D element
@@ -346,12 +356,23 @@ static int run_rounds(vhip_knn *E, const QueryRows &Q, int nq, int k, int kc, in
             // fp4 matrix-core Hamming: 2 K operations per (query, row), K = the padded code bits.
             // Items up to 32768 rows where the slot rule allows: each spreads its query-tile fill
             // and flush over more 512-row stages (5% faster at 10M x 256 bits than 8192)
-            const long hitem =
-                dense ? re - rb
-                      : balanced_item(std::min<long>(32768, rd.slot_rows), re - rb, ceil_div(nq, kTileCols),
-                                      E->grid_cap / 2, 512);
-            launch_ham_mfma(dense, hitem, E->base8.as<int8_t>(), B.q8, (int)E->dpad, B.tau, nq, rb, re, B.cand, B.cnt,
-                            cap, E->grid_cap, s);
+            // Filter rounds with at least 2048 queries whose slot rule allows items of 2048 rows
+            // take the 1024-column kernel (8 candidate slots per query and item, so its items are
+            // sized by the same rule with 8 slots).
+            const long wide_rows = (long)ham_wide_slots() * rb / (3 * (long)std::max(k, 1)) / 512 * 512;
+            if (!dense && E->ham_wide && nq >= 2048 && wide_rows >= 2048) {
+                const long witem = balanced_item(std::min<long>(65536, wide_rows), re - rb,
+                                                 ceil_div(nq, ham_wide_cols()), E->grid_cap / 2, 512);
+                launch_ham_mfma_wide(witem, E->base8.as<int8_t>(), B.q8, (int)E->dpad, B.tau, nq, rb, re, B.cand,
+                                     B.cnt, cap, E->grid_cap, s);
+            } else {
+                const long hitem =
+                    dense ? re - rb
+                          : balanced_item(std::min<long>(32768, rd.slot_rows), re - rb, ceil_div(nq, kTileCols),
+                                          E->grid_cap / 2, 512);
+                launch_ham_mfma(dense, hitem, E->base8.as<int8_t>(), B.q8, (int)E->dpad, B.tau, nq, rb, re, B.cand,
+                                B.cnt, cap, E->grid_cap, s);
+            }
         } else if (gemm)
             launch_gemm_filter(E->metric, rd.dense, item, E->base.as<float>(), E->norm.as<float>(), Q.qpad, Q.qnorm,
                                B.tau, nq, (int)E->dpad, rb, re, B.cand, B.cnt, cap, E->norm_max, E->norm_min,
@@ -377,7 +398,8 @@ static int run_rounds(vhip_knn *E, const QueryRows &Q, int nq, int k, int kc, in
 // Capacity of a candidate list that no round can overflow: the largest round's rows.
 static int full_cap(const vhip_knn *E, size_t k, bool gemm) {
     long big = k;
-    for (const Round &rd : plan_rounds(E->n, k, gemm, (int)E->dpad)) big = std::max(big, rd.re - rd.rb);
+    for (const Round &rd : plan_rounds(E->n, k, gemm, (int)E->dpad, round_growth(E)))
+        big = std::max(big, rd.re - rd.rb);
     return (int)round_up((size_t)big, kRowAlign);
 }
 
@@ -604,6 +626,8 @@ static int engine_create(const void *base, size_t n, size_t dim, int metric, int
                               E->base8.as<int8_t>(), E->stream);
             VH_HIP(hipGetLastError());
             E->ham8 = true;
+            const char *env = std::getenv("VHIP_HAMMING_KERNEL");
+            E->ham_wide = ham_wide_supported((int)E->dpad) && !(env && std::strcmp(env, "fp4-tile") == 0);
         }
         uint32_t nonint = 1;
         VH_HIP(hipMemcpyAsync(&nonint, flag.p, sizeof(uint32_t), hipMemcpyDeviceToHost, E->stream));

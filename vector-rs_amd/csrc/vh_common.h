@@ -233,6 +233,16 @@ void launch_ham_expand(const uint32_t *src, size_t rows, int wpad, int wstride, 
 void launch_ham_mfma(bool dense, long item_rows, const int8_t *base8, const int8_t *qry8, int wpad,
                      const float *tau, int nq, long row_begin, long row_end, uint2 *cand, uint32_t *cnt, int cap,
                      int grid_cap, hipStream_t s);
+// Filter rounds of codes up to 256 bits (ham_wide_supported) with many queries: work items of
+// ham_wide_cols() query columns held in registers, the base through an LDS ring, and
+// ham_wide_slots() LDS candidate slots per query and item.  Rows of qry8 are allocated up to a
+// multiple of 128; base row starts and item_rows are multiples of 64.
+bool ham_wide_supported(int wpad);
+constexpr int ham_wide_cols() { return 1024; }
+constexpr int ham_wide_slots() { return 8; }
+void launch_ham_mfma_wide(long item_rows, const int8_t *base8, const int8_t *qry8, int wpad, const float *tau, int nq,
+                          long row_begin, long row_end, uint2 *cand, uint32_t *cnt, int cap, int grid_cap,
+                          hipStream_t s);
 void launch_hamming_filter(const uint32_t *codes, const uint32_t *qry, const float *tau, int nq, int wpad,
                            long row_begin, long row_end, uint2 *cand, uint32_t *cnt, int cap, int grid_cap,
                            hipStream_t s);
