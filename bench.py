@@ -74,7 +74,7 @@ PROFILES = {
     "l2int": "k_mfma_hs_filter__knn_l2_int_1000000x128_q10000_k100.txt",
     "kmeans": "k_mfma_hs_assign__kmeans_l2_2000000x96_k4096.txt",
     "cos768": "k_mfma_nt_filter__knn_cosine_1000000x768_q10000_k10.txt",
-    "hamming": "k_mfma_ham__knn_hamming_packed256_10000000_q10000_k10.txt",
+    "hamming": "k_mfma_ham_wide__knn_hamming_packed256_10000000_q10000_k10.txt",
     "l1": "k_valu_filter__knn_l1_uniform_500000x128_q4096_k10.txt",
     "linf": "k_valu_filter__knn_linf_uniform_500000x128_q4096_k10.txt",
     "ivf_coarse": "k_mfma_hs_assign__ivf_coarse_l2_2000000x96_nlist4096.txt",
