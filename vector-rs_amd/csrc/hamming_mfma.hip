@@ -333,6 +333,7 @@ constexpr int kHwStage = 64;                 // base rows per stage (all 8 waves
 constexpr int kHwSync = 4;                   // stages per workgroup barrier
 constexpr int kHwRing = 2 * kHwSync + 1;     // LDS ring stages (see k_mfma_ham_wide)
 constexpr int kHwSlots = ham_wide_slots();   // LDS candidate slots per query per work item
+constexpr int kHwHalf = kHwSlots / 2;        // of them, per query and accumulator row half (h)
 static_assert(kHwCols == 8 * 128, "one 128-column block per wave");
 
 template <int KC>
@@ -341,7 +342,10 @@ __global__ __launch_bounds__(512, 1) void k_mfma_ham_wide(HamArgs a) {
     constexpr int NPIECE = 2 * KC;                                 // 1 KB pieces per stage
     static_assert(KC == 1 || KC == 2 || KC == 4, "codes of 64 to 256 expanded bits");
     __shared__ __attribute__((aligned(16))) int8_t s_ring[kHwRing * SB];
-    __shared__ uint32_t s_qcnt[kHwCols];
+    // Candidate slots: a query column ql belongs to lanes l32 and l32 + 32 of one wave (rows of
+    // the two accumulator halves h), so each (column, h) gets kHwHalf slots of its own, counted
+    // in a register of its lane (no LDS atomics).  The counts reach LDS at the item's end.
+    __shared__ uint32_t s_hcnt[kHwCols * 2];
     __shared__ uint2 s_slot[kHwCols * kHwSlots];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -421,7 +425,7 @@ __global__ __launch_bounds__(512, 1) void k_mfma_ham_wide(HamArgs a) {
         }
     };
     item_begin();
-    for (int i = tid; i < kHwCols; i += 512) s_qcnt[i] = 0;
+    uint32_t cnt4 = 0;  // this lane's slots used per tile cb, 8 bits each (at most kHwHalf)
     // prologue: stages 0 .. kHwSync (and the query operands) landed and visible
     int t = 0;  // stages scored so far by this workgroup (ring slot t % kHwRing)
 #pragma unroll
@@ -482,9 +486,10 @@ __global__ __launch_bounds__(512, 1) void k_mfma_ham_wide(HamArgs a) {
                     if (dot < T[cb] || row >= r_hi) continue;
                     const int ql = 128 * wave + 32 * cb + l32;
                     const uint32_t key = score_key(((float)K - dot) * 0.5f);
-                    const uint32_t r = atomicAdd(&s_qcnt[ql], 1u);
-                    if (r < (uint32_t)kHwSlots) {
-                        s_slot[ql * kHwSlots + r] = make_uint2(key, (uint32_t)(row - r_lo));
+                    const uint32_t r = (cnt4 >> (8 * cb)) & 255u;
+                    if (r < (uint32_t)kHwHalf) {
+                        s_slot[(2 * ql + h) * kHwHalf + r] = make_uint2(key, (uint32_t)(row - r_lo));
+                        cnt4 += 1u << (8 * cb);
                     } else {
                         // rare overflow: straight to the global list, drained here so no store
                         // is pending where this path rejoins the loop
@@ -577,22 +582,23 @@ __global__ __launch_bounds__(512, 1) void k_mfma_ham_wide(HamArgs a) {
                 if (m) append(acc[1], rs, 1);
             }
             prev = false;
-            lds_barrier();  // every wave's slot appends of this item are complete
+#pragma unroll
+            for (int cb = 0; cb < 4; ++cb) s_hcnt[2 * (128 * wave + 32 * cb + l32) + h] = (cnt4 >> (8 * cb)) & 255u;
+            cnt4 = 0;
+            lds_barrier();  // every wave's slot appends and counts of this item are in LDS
             for (int ql = tid; ql < kHwCols; ql += 512) {
-                uint32_t c = s_qcnt[ql];
-                if (c) {
-                    s_qcnt[ql] = 0;
-                    c = min(c, (uint32_t)kHwSlots);
+                const uint32_t c0 = s_hcnt[2 * ql], c1 = s_hcnt[2 * ql + 1];
+                if (c0 + c1) {
                     const int q = col0 + ql;
-                    const uint32_t base = atomicAdd(&a.cnt[q], c);
-                    for (uint32_t j = 0; j < c; ++j)
+                    const uint32_t base = atomicAdd(&a.cnt[q], c0 + c1);
+                    for (uint32_t j = 0; j < c0 + c1; ++j)
                         if (base + j < (uint32_t)a.cap) {
-                            const uint2 e = s_slot[ql * kHwSlots + j];
+                            const uint2 e = s_slot[j < c0 ? 2 * ql * kHwHalf + j : (2 * ql + 1) * kHwHalf + (j - c0)];
                             a.cand[(size_t)q * a.cap + base + j] = make_uint2(e.x, (uint32_t)(r_lo + e.y));
                         }
                 }
             }
-            lds_barrier();  // the counters are clear before the next item's appends
+            lds_barrier();  // the slots are read before the next item's appends
             if (!more) break;
             item = nitem;
             col0 = ncol0;
