@@ -463,50 +463,51 @@ __global__ __launch_bounds__(512, 1) void k_mfma_ham_wide(HamArgs a) {
         const int mx = max(m3(a0, a1, a2), m3(a3, a4, x[15]));
         return __builtin_amdgcn_ballot_w64(mx >= TI[cb]);
     };
-    // per-row tests and LDS slot appends of a half that passed the pre-test; register 4g+j of
-    // tile cb holds row srs + 32 hf + 8 g + 4 h + j and column 128 wave + 32 cb + l32
-    auto append = [&](const floatx16 (&ac)[4], long srs, int hf) {
+    // Per-row tests and LDS slot appends of a half whose pre-test passed; mk[cb] holds the lanes
+    // of tile cb whose column may pass, so only those tiles are examined.  Register 4g+j of tile
+    // cb holds row srs + 32 hf + 8 g + 4 h + j and column 128 wave + 32 cb + l32.
+    auto append = [&](const floatx16 (&ac)[4], long srs, int hf, const uint64_t (&mk)[4]) {
+        // the lane's first row as an offset within the item, and how many rows from it lie inside
+        const uint32_t rel0 = (uint32_t)(srs - r_lo) + 32 * hf + 4 * h;
+        const int room = (int)((uint32_t)(r_hi - r_lo) - rel0);
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            const long row0 = srs + 32 * hf + 8 * g + 4 * h;
-            uint64_t m = 0;
+        for (int cb = 0; cb < 4; ++cb) {
+            if (mk[cb] == 0) continue;
+            const floatx16 &v = ac[cb];
+            const int ql = 128 * wave + 32 * cb + l32;
 #pragma unroll
-            for (int cb = 0; cb < 4; ++cb) {
-                const floatx16 &v = ac[cb];
+            for (int g = 0; g < 4; ++g) {
                 const float mx = fmaxf(fmaxf(v[4 * g], v[4 * g + 1]), fmaxf(v[4 * g + 2], v[4 * g + 3]));
-                m |= __builtin_amdgcn_ballot_w64(mx >= T[cb]);
-            }
-            if (m == 0) continue;
+                if (__builtin_amdgcn_ballot_w64(mx >= T[cb]) == 0) continue;
 #pragma unroll
-            for (int cb = 0; cb < 4; ++cb)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const float dot = ac[cb][4 * g + j];
-                    const long row = row0 + j;
-                    if (dot < T[cb] || row >= r_hi) continue;
-                    const int ql = 128 * wave + 32 * cb + l32;
+                for (int jj = 0; jj < 4; ++jj) {
+                    const float dot = v[4 * g + jj];
+                    const int off = 8 * g + jj;  // row of this register after the lane's first
+                    if (dot < T[cb] || off >= room) continue;
                     const uint32_t key = score_key(((float)K - dot) * 0.5f);
                     const uint32_t r = (cnt4 >> (8 * cb)) & 255u;
                     if (r < (uint32_t)kHwHalf) {
-                        s_slot[(2 * ql + h) * kHwHalf + r] = make_uint2(key, (uint32_t)(row - r_lo));
+                        s_slot[(2 * ql + h) * kHwHalf + r] = make_uint2(key, rel0 + off);
                         cnt4 += 1u << (8 * cb);
                     } else {
                         // rare overflow: straight to the global list, drained here so no store
                         // is pending where this path rejoins the loop
                         const int q = col0 + ql;
-                        const uint32_t at =
-                            __hip_atomic_fetch_add((gu32 *)a.cnt + q, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        if (at < (uint32_t)a.cap) ((gu64 *)a.cand)[(size_t)q * a.cap + at] = pack_u2(key, (uint32_t)row);
+                        const uint32_t at = __hip_atomic_fetch_add((gu32 *)a.cnt + q, 1u, __ATOMIC_RELAXED,
+                                                                   __HIP_MEMORY_SCOPE_AGENT);
+                        if (at < (uint32_t)a.cap)
+                            ((gu64 *)a.cand)[(size_t)q * a.cap + at] = pack_u2(key, (uint32_t)(r_lo + rel0 + off));
                         __builtin_amdgcn_s_waitcnt(VH_VMCNT(0));
                     }
                 }
+            }
         }
     };
     // one step: the 4 MFMAs of (half hf, chunk kc) on operand `cur`, interleaved with the
     // pre-test of the tiles [4 kc / KC, 4 (kc + 1) / KC) of the other half's accumulators `oth`
-    // (unconditional, so it stays in the MFMAs' basic block; the caller ignores the mask of a
-    // half that holds no scores)
-    auto step = [&](floatx16 (&ac)[4], const intx4 &cur, int kc, const floatx16 (&oth)[4], uint64_t &mask) {
+    // into mask[cb] (unconditional, so it stays in the MFMAs' basic block; the caller ignores the
+    // masks of a half that holds no scores)
+    auto step = [&](floatx16 (&ac)[4], const intx4 &cur, int kc, const floatx16 (&oth)[4], uint64_t (&mask)[4]) {
 #pragma unroll
         for (int cb = 0; cb < 4; ++cb)
             ac[cb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fp4_operand(cur), fp4_operand(bq[cb][kc]),
@@ -514,7 +515,7 @@ __global__ __launch_bounds__(512, 1) void k_mfma_ham_wide(HamArgs a) {
                                                                      0, 127);
 #pragma unroll
         for (int cb = 0; cb < 4; ++cb)
-            if (cb >= 4 * kc / KC && cb < 4 * (kc + 1) / KC) mask |= pretest(oth[cb], cb);
+            if (cb >= 4 * kc / KC && cb < 4 * (kc + 1) / KC) mask[cb] = pretest(oth[cb], cb);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
@@ -540,14 +541,15 @@ __global__ __launch_bounds__(512, 1) void k_mfma_ham_wide(HamArgs a) {
             }
         }
         // ---- half 0: MFMAs into acc[0]; pre-test of the previous stage's half 1 ----
-        uint64_t m1 = 0;
+        uint64_t m1[4] = {0, 0, 0, 0};
 #pragma unroll
         for (int kc = 0; kc < KC; ++kc) {
             const intx4 nxt = kc + 1 < KC ? read_a(t, 0, kc + 1) : read_a(t, 1, 0);
             if (active) step(acc[0], cur, kc, acc[1], m1);
             cur = nxt;
         }
-        if (!prev || !active) m1 = 0;  // acc[1] holds no scores of this item, or no real columns
+        // acc[1] holds scores of this item's previous stage (and real columns) only if prev && active
+        const bool any1 = prev && active && (m1[0] | m1[1] | m1[2] | m1[3]) != 0;
         if (t % kHwSync == 0) {
             __builtin_amdgcn_s_waitcnt(VH_VMCNT(0));  // this wave's pieces of stages <= t + kHwSync
             lds_barrier();
@@ -557,9 +559,9 @@ __global__ __launch_bounds__(512, 1) void k_mfma_ham_wide(HamArgs a) {
                 d_advance();
             }
         }
-        if (m1) append(acc[1], prs, 1);
+        if (any1) append(acc[1], prs, 1, m1);
         // ---- half 1: MFMAs into acc[1]; pre-test of this stage's half 0 ----
-        uint64_t m0 = 0;
+        uint64_t m0[4] = {0, 0, 0, 0};
 #pragma unroll
         for (int kc = 0; kc < KC; ++kc) {
             // stage t + 1 is visible since the last barrier; past the last stage this reads a
@@ -568,18 +570,18 @@ __global__ __launch_bounds__(512, 1) void k_mfma_ham_wide(HamArgs a) {
             if (active) step(acc[1], cur, kc, acc[0], m0);
             cur = nxt;
         }
-        if (!active) m0 = 0;
-        if (m0) append(acc[0], rs, 0);
+        const bool any0 = active && (m0[0] | m0[1] | m0[2] | m0[3]) != 0;
+        if (any0) append(acc[0], rs, 0, m0);
         prev = true;
         prs = rs;
         ++t;
         if (item_end) {
             // drain: this stage's half 1, then the item's candidate flush
             if (active) {
-                uint64_t m = 0;
+                uint64_t m[4];
 #pragma unroll
-                for (int cb = 0; cb < 4; ++cb) m |= pretest(acc[1][cb], cb);
-                if (m) append(acc[1], rs, 1);
+                for (int cb = 0; cb < 4; ++cb) m[cb] = pretest(acc[1][cb], cb);
+                if ((m[0] | m[1] | m[2] | m[3]) != 0) append(acc[1], rs, 1, m);
             }
             prev = false;
 #pragma unroll
