@@ -97,9 +97,9 @@ namespace vh {
 // Search rounds.  Round 0 scores rows [0, b0) with b0 about 20 k, the first 256-row multiple
 // at or above it (all rows when the base has at most max(2048, 32 k)): for the GEMM metrics
 // densely (every score written, no atomics), for the others through the filter with tau = +inf.
-// Every later round covers about 8 times the rows seen so far (the growth factor, see
-// round_growth) and keeps only rows scoring <= tau, the k-th best so far.  Because the base rows
-// are in a pseudo-random order, round i passes about k * (rows_i / seen_i) ~ 7 k candidates per
+// Every later round covers about 4 times the rows seen so far (the growth factor, see
+// kRoundGrowth) and keeps only rows scoring <= tau, the k-th best so far.  Because the base rows
+// are in a pseudo-random order, round i passes about k * (rows_i / seen_i) ~ 3 k candidates per
 // query at a rate p_i = k / seen_i per scored pair.  item_rows of the MFMA filter is sized so that a work
 // item's expected passes per query, item_rows * p_i, stay at most a third of the LDS slots.
 struct Round {
@@ -109,7 +109,15 @@ struct Round {
     long slot_rows;  // the slot rule's length alone
 };
 
-static std::vector<Round> plan_rounds(size_t n, size_t k, bool gemm, int dpad, int growth = 8) {
+// Round growth: each round covers `growth` times the rows seen so far.  A round passes about
+// k (growth - 1) candidates per query, so a smaller factor passes fewer in all (the filter's
+// appends and the merges' sorts) at the cost of more launches and merges.  4 measured best:
+// squared L2 1M x 128, Q = 10k, k = 100: 20.0 ms against 20.3 at 8 (3 alike); L1 500k x 128,
+// Q = 4096: 13.3 ms against 13.8 (3 slower); fp4 Hamming 10M x 256 bits: 9.25 against 9.56
+// (2 slower).
+constexpr int kRoundGrowth = 4;
+
+static std::vector<Round> plan_rounds(size_t n, size_t k, bool gemm, int dpad, int growth) {
     std::vector<Round> r;
     if (n == 0) return r;
     const size_t kk = std::max<size_t>(k, 1);
@@ -150,17 +158,12 @@ static long balanced_item(long cap_item, long rows, int n_ctiles, int wgs, long 
 }
 
 // Candidate capacity per query and round: the dense round's rows, and room for several times
-// the ~7 k expected passes of a filter round.  A query that still overflows is re-run with a
+// the ~3 k expected passes of a filter round.  A query that still overflows is re-run with a
 // capacity equal to the largest round.
-// Round growth: each round covers `growth` times the rows seen so far (8 above).  The fp4 Hamming
-// scan grows by 4: its candidate appends cost more, relative to its fast scan, than the extra
-// round's merge and launch (10M x 256 bits, Q = 10k, k = 10: 9.25 ms against 9.56 at 8; 3 and 4
-// measured alike, 2 slower).
-static int round_growth(const vhip_knn *E) { return E->ham8 ? 4 : 8; }
 
 static int round_cap(size_t n, size_t k, bool gemm, int dpad) {
     size_t cap = std::max<size_t>(2048, 32 * std::max<size_t>(k, 1));
-    for (const Round &r : plan_rounds(n, k, gemm, dpad))
+    for (const Round &r : plan_rounds(n, k, gemm, dpad, kRoundGrowth))
         if (r.rb == 0) cap = std::max(cap, (size_t)(r.re - r.rb));
     return (int)round_up(cap, kRowAlign);
 }
@@ -331,7 +334,7 @@ static int run_rounds(vhip_knn *E, const QueryRows &Q, int nq, int k, int kc, in
         launch_ham_expand((const uint32_t *)Q.qpad, (size_t)nq, (int)E->dpad, (int)E->dpad, rows, false, B.q8, s);
     }
     for (const Round &rd :
-         split_rounds(plan_rounds(E->n, (size_t)k, gemm, (int)E->dpad, round_growth(E)), max_round_rows)) {
+         split_rounds(plan_rounds(E->n, (size_t)k, gemm, (int)E->dpad, kRoundGrowth), max_round_rows)) {
         const long rb = rd.rb, re = rd.re;
         const bool dense = rd.dense || (E->ham8 && rb == 0);
         // Algorithmic work per launch: 2*Q*rows*D flops (GEMM metrics), Q*rows*D element
@@ -398,7 +401,7 @@ static int run_rounds(vhip_knn *E, const QueryRows &Q, int nq, int k, int kc, in
 // Capacity of a candidate list that no round can overflow: the largest round's rows.
 static int full_cap(const vhip_knn *E, size_t k, bool gemm) {
     long big = k;
-    for (const Round &rd : plan_rounds(E->n, k, gemm, (int)E->dpad, round_growth(E)))
+    for (const Round &rd : plan_rounds(E->n, k, gemm, (int)E->dpad, kRoundGrowth))
         big = std::max(big, rd.re - rd.rb);
     return (int)round_up((size_t)big, kRowAlign);
 }
