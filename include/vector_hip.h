@@ -99,13 +99,16 @@ int vhip_knn_search_batch_device(vhip_knn *eng, const float *d_queries, size_t n
  * reference.  It is for callers that cannot allocate device memory: code that must not call
  * hipMalloc inside a serving loop, and harnesses that forbid it.  It returns the same results.
  * Its working memory is one fixed array of VHIP_NOALLOC_SCRATCH_BYTES per GPU inside the
- * library (each GPU that runs it holds that array until the process ends); queries are served
- * in batches that fit it.  It calls no hipMalloc or hipFree.  Error VHIP_ERR_INVALID_CONFIG
+ * library, in a code object of its own that a GPU loads at the first allocation-free call on it
+ * and holds until the process ends (GPUs and engines that never call it reserve nothing);
+ * queries are served in batches that fit it.  It calls no hipMalloc or hipFree.  Error VHIP_ERR_INVALID_CONFIG
  * when a single query at this k and engine size needs more than the array holds (about
  * 8 * max(2048, 32 k) bytes per query plus the row buffers).  Every call on one GPU shares that
  * GPU's array and leaves its contents behind: the library takes a per-GPU lock for the whole
  * call, so calls from several threads run one after another; calls that overlapped on one GPU
- * would race on the array.  Returns after the results are written. */
+ * would race on the array.  Every return, errors included, comes after the call's kernels have
+ * finished, so the lock is never released with work on the array still queued.  Returns after
+ * the results are written. */
 #define VHIP_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
 int vhip_knn_search_batch_device_noalloc(vhip_knn *eng, const float *d_queries, size_t nq, size_t k,
                                          uint32_t *d_ids, float *d_dist);

@@ -28,11 +28,48 @@ def test_library_exports_every_declared_symbol():
     assert not missing, f"not exported: {missing}"
 
 
-def test_no_torch_or_oracle_in_product_binding():
+def _dt_needed(path):
+    """DT_NEEDED entries of an ELF64 little-endian shared library, read from its dynamic section."""
+    import struct
+
+    data = open(path, "rb").read()
+    assert data[:4] == b"\x7fELF" and data[4] == 2 and data[5] == 1, "not an ELF64 little-endian file"
+    shoff, = struct.unpack_from("<Q", data, 0x28)
+    shentsize, shnum = struct.unpack_from("<HH", data, 0x3A)
+    secs = [struct.unpack_from("<IIQQQQIIQQ", data, shoff + i * shentsize) for i in range(shnum)]
+    dyn = [s for s in secs if s[1] == 6]  # SHT_DYNAMIC
+    assert len(dyn) == 1, "no dynamic section"
+    _, _, _, _, off, size, link, _, _, _ = dyn[0]
+    stroff = secs[link][4]
+    out = []
+    for i in range(0, size, 16):
+        tag, val = struct.unpack_from("<qQ", data, off + i)
+        if tag == 0:
+            break
+        if tag == 1:  # DT_NEEDED
+            end = data.index(b"\0", stroff + val)
+            out.append(data[stroff + val:end].decode())
+    return out
+
+
+def test_no_torch_or_oracle_in_product():
+    """The product neither imports nor links the oracle (test infrastructure only) or torch: the
+    Python binding, every native source, and the built library's DT_NEEDED list."""
     import vector_hip as vh
 
-    src = open(os.path.join(os.path.dirname(vh.__file__), "__init__.py")).read()
-    assert "import oracle" not in src and "vh_oracle" not in src
+    pkg = os.path.dirname(vh.__file__)
+    srcs = [os.path.join(pkg, f) for f in os.listdir(pkg) if f.endswith(".py")]
+    csrc = os.path.join(os.path.dirname(pkg), "csrc")
+    srcs += [os.path.join(csrc, f) for f in os.listdir(csrc)]
+    srcs += [os.path.join(ROOT, "include", f) for f in os.listdir(os.path.join(ROOT, "include"))]
+    assert len(srcs) > 20
+    for path in srcs:
+        src = open(path).read()
+        for bad in ("import oracle", "from oracle", "vh_oracle", "import torch", "torch/"):
+            assert bad not in src, f"{path} names {bad!r}"
+    needed = _dt_needed(vh.library_path())
+    assert any(n.startswith("libamdhip64") for n in needed), needed
+    assert not [n for n in needed if "oracle" in n or "torch" in n or "c10" in n], needed
 
 
 def test_device_count_is_nonnegative():

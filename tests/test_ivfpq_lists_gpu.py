@@ -124,3 +124,19 @@ def test_lists_many_lists_plan_without_lds_histogram(vh, oracle):
     a, b = _both_paths(ix, qs, 10, 24)
     _assert_same(a, b)
     _check_search(vh, oracle, ix, parts, qs[:20], 10, 24, "l2", 16, 256, exact=True)
+
+
+def test_batch_of_several_chunks(vh):
+    """A batch whose (query, probe) pairs exceed one search chunk (2^22 pairs: 65,536 queries at
+    nprobe 64) runs as several chunks; its results equal those of the same queries searched in
+    batches of one chunk or less, bit for bit."""
+    rng = np.random.default_rng(77)
+    dim, nlist = 64, 64
+    parts = _skewed_parts(rng, dim, nlist, 20_000)
+    ix = _index(vh, parts, dim, 16, 256, vh.DistanceMetric.L2Squared)
+    qs = rng.standard_normal((70_000, dim)).astype(np.float32)
+    print("  70,000 queries at nprobe 64 (two chunks)", flush=True)
+    whole = ix.search_batch_arrays(qs, 10, 64)
+    head = ix.search_batch_arrays(qs[:40_000], 10, 64)
+    tail = ix.search_batch_arrays(qs[40_000:], 10, 64)
+    _assert_same(whole, tuple(np.concatenate([h, t]) for h, t in zip(head, tail)))

@@ -34,6 +34,32 @@ def _free_bytes():
     return free.value
 
 
+def test_first_call_loads_the_array(vh):
+    """The array lives in a code object of its own with no kernels, loaded onto the GPU by the
+    first allocation-free call: creating engines and searching with the allocating entry point
+    reserve nothing for it.  (This is the first test of the file, and no other test file calls
+    the allocation-free entry point, so in one process this call is the first.)"""
+    from vector_hip import datasets as ds
+
+    gc.collect()
+    base = ds.uniform_int(20_000, 128, 31)
+    eng = vh.CudaKnnEngine(base, 128)
+    q = ds.uniform_int(100, 128, 32)
+    dq = vh.DeviceBuffer.from_host(q)
+    di = vh.DeviceBuffer(100 * 10 * 4)
+    dd = vh.DeviceBuffer(100 * 10 * 4)
+    eng.search_batch_device(dq.ptr, 100, 10, di.ptr, dd.ptr)
+    vh.synchronize()
+    f0 = _free_bytes()
+    eng.search_batch_device_noalloc(dq.ptr, 100, 10, di.ptr, dd.ptr)
+    vh.synchronize()
+    f1 = _free_bytes()
+    print(f"  free memory before {f0}, after the first allocation-free call {f1}", flush=True)
+    assert f0 - f1 >= vh.NOALLOC_SCRATCH_BYTES - (4 << 20), (
+        f"the first allocation-free call should load the {vh.NOALLOC_SCRATCH_BYTES}-byte array; free memory "
+        f"fell by {f0 - f1} bytes")
+
+
 def _both(vh, eng, q, k):
     """(ids, dist) of the allocating and the allocation-free entry point for the same queries."""
     nq = q.shape[0]
@@ -67,11 +93,11 @@ def test_integer_l2_several_batches(vh, oracle):
     _check_pair(vh, oracle, eng, base, q[:300], 100, "l2", rtol=0.0, atol=0.0)
 
 
-@pytest.mark.parametrize("metric", ["l2", "cosine", "l1"])
+@pytest.mark.parametrize("metric", ["l2", "cosine", "dot", "l1"])
 def test_float_metrics_two_calls(vh, oracle, metric):
     from vector_hip import datasets as ds
 
-    names = {"l2": "L2Squared", "cosine": "CosineSimilarity", "l1": "Manhattan"}
+    names = {"l2": "L2Squared", "cosine": "CosineSimilarity", "dot": "DotProduct", "l1": "Manhattan"}
     base = ds.gaussian(30_000, 96, 23)
     eng = vh.CudaKnnEngine(base, 96, vh.DistanceMetric[names[metric]])
     q = ds.gaussian(700, 96, 24)

@@ -510,7 +510,7 @@ static int km_create(int ordinal, const float *const *segs, const size_t *counts
     if (metric == L2) {
         // per-dimension shift: the column means (integers for integer data)
         DevBuf part, flag;
-        VH_CHECK(part.ensure(ordinal, (size_t)col_shift_parts() * dim * sizeof(double)));
+        VH_CHECK(part.ensure(ordinal, col_shift_scratch_bytes((int)dim)));
         VH_CHECK(flag.ensure(ordinal, sizeof(uint32_t)));
         VH_CHECK(K->shift.ensure(ordinal, K->dpad * sizeof(float)));
         launch_fill_u32(flag.as<uint32_t>(), 1, 0u, s);

@@ -4,7 +4,7 @@
 // transpose on one host thread and kept a host copy.  Here the base is uploaded once
 // through pinned staging and laid out on the GPU: rows in a fixed pseudo-random order
 // (so every prefix of the resident base is an unbiased sample of it), padded to a
-// multiple of 32 floats, the row count padded to a multiple of 128 with NaN rows, with
+// multiple of 32 floats, the row count padded to a multiple of 256 with NaN rows, with
 // per-row norms computed on the device (cosine rows are stored L2-normalised).
 //
 // search_batch (knn.rs:151-310) materialised the Q x N distance matrix.  Here a search
@@ -210,15 +210,19 @@ __global__ __launch_bounds__(256) void k_row_shuffle(uint32_t n, RowShuffle f, u
     }
 }
 
-// Per-block maximum and minimum of x[0, count): the host folds the gridDim.x pairs (NaN values
-// are skipped, as std::max / std::min over the same values would).
+// Per-block maximum and minimum of the finite values of x[0, count): the host folds the
+// gridDim.x pairs.  A row holding a NaN or an infinity has a non-finite norm; its scores are NaN
+// or infinite and never pass a filter, so it takes no part in the bounds the extremes feed.
 __global__ __launch_bounds__(256) void k_minmax_partial(const float *__restrict__ x, size_t count,
                                                         float *__restrict__ pmax, float *__restrict__ pmin) {
     __shared__ float rmax[256], rmin[256];
     float mx = 0.0f, mn = INFINITY;
     for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < count; i += (size_t)gridDim.x * blockDim.x) {
-        mx = fmaxf(mx, x[i]);
-        mn = fminf(mn, x[i]);
+        const float v = x[i];
+        if (__builtin_isfinite(v)) {
+            mx = fmaxf(mx, v);
+            mn = fminf(mn, v);
+        }
     }
     rmax[threadIdx.x] = mx;
     rmin[threadIdx.x] = mn;
@@ -590,7 +594,7 @@ static int engine_create(const void *base, size_t n, size_t dim, int metric, int
         if (metric == L2) {
             // per-dimension shift: the column means (integers for integer data)
             DevBuf part;
-            VH_CHECK(part.ensure(ordinal, (size_t)col_shift_parts() * dim * sizeof(double)));
+            VH_CHECK(part.ensure(ordinal, col_shift_scratch_bytes((int)dim)));
             VH_CHECK(E->shift.ensure(ordinal, E->dpad * sizeof(float)));
             launch_col_shift(raw.as<float>(), n, (int)dim, (int)E->dpad, part.as<double>(), flag.as<uint32_t>(),
                              E->shift.as<float>(), E->stream);
@@ -809,39 +813,25 @@ static int engine_search_host(vhip_knn *E, const void *queries, size_t nq, size_
 }
 
 // ---- allocation-free search -----------------------------------------------------------------
-// The working memory of vhip_knn_search_batch_device_noalloc: one fixed array in the library's
-// code object, of which every device that runs the library holds its own copy until the process
-// ends.  On the host the array's name is only a stand-in, never a device address: each device's
-// address comes from hipGetSymbolAddress, taken once per device with that device current, and
-// only that address reaches kernels.
-static __device__ __align__(256) unsigned char scratch[VHIP_NOALLOC_SCRATCH_BYTES];
-
-namespace {
-constexpr int kMaxScratchDevices = 64;
-struct ScratchSlot {
-    std::mutex mu;         // held for a whole call: calls on one device run one after another
-    void *ptr = nullptr;   // this device's copy of `scratch`
-};
-ScratchSlot g_scratch[kMaxScratchDevices];
-}  // namespace
-
+// The working memory is the per-device array of noalloc_scratch.hip, whose lock is held for the
+// whole call.  Every exit, error paths included, first waits for the engine's stream: kernels
+// this call queued read and write the array, so they must finish before another call (another
+// engine, on another stream) may reuse it.
 static int search_device_noalloc(vhip_knn *E, const float *d_queries, size_t nq, size_t k, uint32_t *d_ids,
                                  float *d_dist) {
     clear_error();
     if (!E) return set_error(VHIP_ERR_INVALID_CONFIG, "null engine");
-    if (E->dev < 0 || E->dev >= kMaxScratchDevices)
-        return set_error(VHIP_ERR_INVALID_CONFIG, "device ordinal " + std::to_string(E->dev) +
-                                                      " is beyond the allocation-free search's device table");
-    ScratchSlot &S = g_scratch[E->dev];
-    std::lock_guard<std::mutex> lock(S.mu);
-    if (!S.ptr) {
-        VH_CHECK(open_device(E->dev));
-        void *p = nullptr;
-        VH_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
-        if (!p) return set_error(VHIP_ERR_DRIVER, "hipGetSymbolAddress(scratch) returned a null address");
-        S.ptr = p;
+    std::unique_lock<std::mutex> lock;
+    void *ptr = nullptr;
+    VH_CHECK(noalloc_scratch_acquire(E->dev, lock, &ptr));
+    const int rc = engine_search_device(E, d_queries, nq, k, d_ids, d_dist, nullptr, ptr, VHIP_NOALLOC_SCRATCH_BYTES);
+    const hipError_t se = hipSetDevice(E->dev) == hipSuccess ? hipStreamSynchronize(E->stream) : hipErrorInvalidDevice;
+    if (rc != VHIP_OK) return rc;  // the first error's message stands
+    if (se != hipSuccess) {
+        (void)hipGetLastError();
+        return set_error(VHIP_ERR_DRIVER, std::string("hipStreamSynchronize: ") + hipGetErrorString(se));
     }
-    return engine_search_device(E, d_queries, nq, k, d_ids, d_dist, nullptr, S.ptr, VHIP_NOALLOC_SCRATCH_BYTES);
+    return VHIP_OK;
 }
 
 }  // namespace vh

@@ -155,19 +155,23 @@ void launch_rows_prep(const float *in, size_t n, size_t n_out, int dim, int dpad
 
 // ---------------------------------------------------------------------------------
 // Per-dimension shift (the column means): block b sums rows [b*chunk, ...) of every column in
-// double (thread t owns columns t, t + 256, ...), and flags non-integer values; one more kernel
-// adds the nparts partials per column in a fixed order.
+// double (thread t owns columns t, t + 256, ...) and counts them, skipping non-finite values, and
+// flags non-integer finite values; one more kernel adds the nparts partials per column in a fixed
+// order.  A NaN or infinity then affects only the distances of its own row, as in the reference,
+// instead of turning its whole column's shift (and so every shifted row) non-finite.
 // ---------------------------------------------------------------------------------
 constexpr int kColParts = 512;
-int col_shift_parts() { return kColParts; }
+size_t col_shift_scratch_bytes(int dim) { return 2 * (size_t)kColParts * (size_t)dim * sizeof(double); }
 
 __global__ __launch_bounds__(256) void k_col_partial(const float *__restrict__ x, size_t n, int dim, size_t chunk,
                                                      double *__restrict__ partial, uint32_t *__restrict__ nonint) {
     const size_t r0 = blockIdx.x * chunk, r1 = min(n, r0 + chunk);
+    double *__restrict__ count = partial + (size_t)kColParts * dim;
     bool whole = true;
     for (int d = threadIdx.x; d < dim; d += 256) {
         // 8 rows in flight per step, each into its own accumulator
         double s[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        uint32_t c = 0;
         size_t r = r0;
         for (; r + 8 <= r1; r += 8) {
             float v[8];
@@ -175,21 +179,26 @@ __global__ __launch_bounds__(256) void k_col_partial(const float *__restrict__ x
             for (int j = 0; j < 8; ++j) v[j] = x[(r + j) * (size_t)dim + d];
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                whole = whole && v[j] == rintf(v[j]);
-                s[j] += (double)v[j];
+                const bool fin = __builtin_isfinite(v[j]);
+                whole = whole && (!fin || v[j] == rintf(v[j]));
+                s[j] += fin ? (double)v[j] : 0.0;
+                c += fin ? 1u : 0u;
             }
         }
         for (; r < r1; ++r) {
             const float v = x[r * (size_t)dim + d];
-            whole = whole && v == rintf(v);
-            s[0] += (double)v;
+            const bool fin = __builtin_isfinite(v);
+            whole = whole && (!fin || v == rintf(v));
+            s[0] += fin ? (double)v : 0.0;
+            c += fin ? 1u : 0u;
         }
         partial[(size_t)blockIdx.x * dim + d] = ((s[0] + s[1]) + (s[2] + s[3])) + ((s[4] + s[5]) + (s[6] + s[7]));
+        count[(size_t)blockIdx.x * dim + d] = (double)c;
     }
     if (!whole) atomicOr(nonint, 1u);
 }
 
-__global__ __launch_bounds__(256) void k_col_finish(const double *__restrict__ partial, size_t n, int dim, int dpad,
+__global__ __launch_bounds__(256) void k_col_finish(const double *__restrict__ partial, int dim, int dpad,
                                                     const uint32_t *__restrict__ nonint, float *__restrict__ shift) {
     const int d = blockIdx.x * blockDim.x + threadIdx.x;
     if (d >= dpad) return;
@@ -197,9 +206,14 @@ __global__ __launch_bounds__(256) void k_col_finish(const double *__restrict__ p
         shift[d] = 0.0f;
         return;
     }
-    double s = 0.0;
-    for (int b = 0; b < kColParts; ++b) s += partial[(size_t)b * dim + d];
-    const double m = s / (double)n;
+    const double *count = partial + (size_t)kColParts * dim;
+    double s = 0.0, c = 0.0;
+    for (int b = 0; b < kColParts; ++b) {
+        s += partial[(size_t)b * dim + d];
+        c += count[(size_t)b * dim + d];
+    }
+    // a column with no finite value keeps no shift
+    const double m = c > 0.0 ? s / c : 0.0;
     shift[d] = *nonint ? (float)m : (float)rint(m);
 }
 
@@ -207,7 +221,7 @@ void launch_col_shift(const float *x, size_t n, int dim, int dpad, double *parti
                       hipStream_t s) {
     const size_t chunk = (n + kColParts - 1) / kColParts;
     hipLaunchKernelGGL(k_col_partial, dim3(kColParts), dim3(256), 0, s, x, n, dim, chunk, partial, nonint);
-    hipLaunchKernelGGL(k_col_finish, dim3((unsigned)((dpad + 255) / 256)), dim3(256), 0, s, partial, n, dim, dpad,
+    hipLaunchKernelGGL(k_col_finish, dim3((unsigned)((dpad + 255) / 256)), dim3(256), 0, s, partial, dim, dpad,
                        nonint, shift);
 }
 
@@ -474,10 +488,15 @@ __device__ __forceinline__ void dense_stage(const floatx16 (&acc)[2][2], NF nf, 
                 for (int j = 0; j < 4; ++j) {
                     const float dot = acc[rb][cb][4 * g + j];
                     float sc;
-                    if constexpr (M == L2) sc = fmaxf(fmaf(-2.0f, dot, st.cn[cb] + n4[j]), 0.0f);
-                    else if constexpr (M == DOT) sc = canon(-dot);
-                    else sc = st.cn[cb] * n4[j] > 1e-9f ? canon(-dot) : 0.0f;
-                    key[j] = score_key(sc);
+                    if constexpr (M == L2) {
+                        const float v = fmaf(-2.0f, dot, st.cn[cb] + n4[j]);
+                        sc = v == v ? fmaxf(v, 0.0f) : v;
+                    } else if constexpr (M == DOT) {
+                        sc = canon(-dot);
+                    } else {
+                        sc = st.cn[cb] * n4[j] > 1e-9f ? canon(-dot) : canon(0.0f * dot);
+                    }
+                    key[j] = score_key(nan_last(sc));
                 }
                 const uint32_t p0 = (uint32_t)(row - a.row_begin);
                 if (row + 3 < a.row_end) {
@@ -1044,10 +1063,15 @@ __device__ __forceinline__ void dense_group(const floatx16 (&acc2)[CB], floatx4 
         for (int j = 0; j < 4; ++j) {
             const float dot = acc2[cb][4 * g + j];
             float sc;
-            if constexpr (M == L2) sc = fmaxf(st.cn[cb] + dot, 0.0f);  // dot holds u (see filter_group)
-            else if constexpr (M == DOT) sc = canon(-dot);
-            else sc = st.cn[cb] * n4[j] > 1e-9f ? canon(-dot) : 0.0f;
-            key[j] = score_key(sc);
+            if constexpr (M == L2) {
+                const float v = st.cn[cb] + dot;  // dot holds u (see filter_group)
+                sc = v == v ? fmaxf(v, 0.0f) : v;
+            } else if constexpr (M == DOT) {
+                sc = canon(-dot);
+            } else {
+                sc = st.cn[cb] * n4[j] > 1e-9f ? canon(-dot) : canon(0.0f * dot);
+            }
+            key[j] = score_key(nan_last(sc));
         }
         const uint32_t p0 = (uint32_t)(row - a.row_begin);
         if (row + 3 < a.row_end) {

@@ -446,7 +446,7 @@ void ivfpq_list_plan(const uint32_t *probes, int nq, int nprobe, int nlist, cons
                      const uint32_t *list_off, uint32_t *cnt, uint32_t *cursor, uint32_t *pair_off,
                      uint32_t *item_off, uint32_t *pairs, uint4 *items, uint4 *item_pairs, uint32_t *n_items,
                      hipStream_t s) {
-    const int total = nq * nprobe;
+    const int total = nq * nprobe;  // at most kIvfpqChunkPairs (the caller's chunks)
     const unsigned gp = (unsigned)std::min(4096, (total + 255) / 256);
     const unsigned gr = (unsigned)std::min(1024, (total + kPlanPairs - 1) / kPlanPairs);  // runs of kPlanPairs
     hipLaunchKernelGGL(k_pair_count, dim3(gr), dim3(256), 0, s, probes, total, nlist, cnt);
@@ -467,10 +467,13 @@ static bool list_path(const vhip_ivfpq *X, size_t k, size_t np) {
            sizeof(ListLds<kListThreads>) <= X->lds_limit;
 }
 
-// Coarse probe + scan for device-resident queries; results stay on the device.
-static int ivfpq_search_dev(vhip_ivfpq *X, const float *d_q, size_t nq, size_t k, size_t nprobe, uint32_t *d_ids,
-                            float *d_dist, uint32_t *d_len) {
-    const size_t np = std::max<size_t>(1, std::min(nprobe, X->nlist));  // ivf/mod.rs:276
+// (query, probe) pairs of one search chunk: pair ids are 32-bit (q * nprobe + p) and the plan's
+// grids and buffers scale with them, so larger batches run as several chunks.
+constexpr size_t kIvfpqChunkPairs = (size_t)1 << 22;
+
+// Coarse probe + scan for device-resident queries of one chunk; results stay on the device.
+static int ivfpq_search_chunk(vhip_ivfpq *X, const float *d_q, size_t nq, size_t k, size_t np, uint32_t *d_ids,
+                              float *d_dist, uint32_t *d_len) {
     hipStream_t s = X->stream;
     VH_CHECK(X->d_pid.ensure(X->dev, nq * np * 4));
     VH_CHECK(X->d_pdist.ensure(X->dev, nq * np * 4));
@@ -548,6 +551,21 @@ static int ivfpq_search_dev(vhip_ivfpq *X, const float *d_q, size_t nq, size_t k
     VH_HIP(hipGetLastError());
     // work and bytes are filled in by the caller's accounting (scanned entries are data dependent)
     X->timer.end(t, s, 0.0, 0.0);
+    return VHIP_OK;
+}
+
+// Coarse probe + scan for device-resident queries, in chunks of at most kIvfpqChunkPairs pairs.
+static int ivfpq_search_dev(vhip_ivfpq *X, const float *d_q, size_t nq, size_t k, size_t nprobe, uint32_t *d_ids,
+                            float *d_dist, uint32_t *d_len) {
+    const size_t np = std::max<size_t>(1, std::min(nprobe, X->nlist));  // ivf/mod.rs:276
+    const size_t qb = std::max<size_t>(1, kIvfpqChunkPairs / np);
+    for (size_t q0 = 0; q0 < nq; q0 += qb) {
+        const size_t m = std::min(qb, nq - q0);
+        // the next chunk's probe (on the probe engine's own stream) rewrites the probe lists and
+        // plan buffers that this stream's scan of the previous chunk reads
+        if (q0 > 0) VH_HIP(hipStreamSynchronize(X->stream));
+        VH_CHECK(ivfpq_search_chunk(X, d_q + q0 * X->dim, m, k, np, d_ids + q0 * k, d_dist + q0 * k, d_len + q0));
+    }
     return VHIP_OK;
 }
 

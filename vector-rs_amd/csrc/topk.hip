@@ -246,7 +246,8 @@ __global__ __launch_bounds__(256) void k_topk_merge(int k, int kc, int bufn, con
                 cut = skk <= t;
                 t = fminf(t, skk);
             }
-            tau[q] = t;
+            // a NaN k-th score (fewer than k rows with a finite score so far) filters nothing yet
+            tau[q] = t == t ? t : INFINITY;
             if (mflag) mflag[q] = cut ? 1u : 0u;
         }
     }
@@ -441,7 +442,7 @@ __global__ __launch_bounds__(256) void k_topk_refine(int k, int kc, int kout, in
             const float den = sqrtf(nq) * sqrtf(nx);
             sc = (den <= 1e-9f || qnorm[q] * bnorm[row] <= 1e-9f) ? 0.0f : -(a / den) + 0.0f;
         }
-        if (s == 0) buf[j] = ((u64)score_key(sc) << 32) | (uint32_t)buf[j];
+        if (s == 0) buf[j] = ((u64)score_key(nan_last(sc)) << 32) | (uint32_t)buf[j];
     }
     int P = 2;
     while (P < h) P <<= 1;

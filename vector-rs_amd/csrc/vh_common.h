@@ -76,6 +76,10 @@ __host__ __device__ inline uint32_t score_key(float s) {
     uint32_t u = __builtin_bit_cast(uint32_t, s);
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
+// Every NaN score (a row holding a NaN or an infinity) as the positive quiet NaN, whose key
+// follows that of +inf: such a row ranks after every other whatever the sign bit of the NaN that
+// reached it.
+__host__ __device__ inline float nan_last(float s) { return s == s ? s : __builtin_nanf(""); }
 __host__ __device__ inline float key_score(uint32_t k) {
     uint32_t u = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
     return __builtin_bit_cast(float, u);
@@ -144,11 +148,12 @@ void launch_rows_prep(const RowPrep &a, hipStream_t s);
 // Short form: no shift, raw copy, integer check or error bound.
 void launch_rows_prep(const float *in, size_t n, size_t n_out, int dim, int dpad, const uint32_t *perm, float *out,
                       float *norm, int norm_kind, int transform, int normalize, float pad_fill, hipStream_t s);
-// Per-dimension shift of n rows of `dim` floats (row-major, contiguous): the column means, rounded
-// to integers when every value is an integer (so that shifted integer data stays integer), into
-// shift[0, dpad) (zeros past dim); nonint (device u32) is set to 1 when some value is not an
-// integer.  partial: scratch of nparts * dim doubles (nparts = col_shift_parts()).
-int col_shift_parts();
+// Per-dimension shift of n rows of `dim` floats (row-major, contiguous): the column means over
+// the finite values, rounded to integers when every finite value is an integer (so that shifted
+// integer data stays integer), into shift[0, dpad) (zeros past dim); nonint (device u32) is set
+// to 1 when some finite value is not an integer.  partial: col_shift_scratch_bytes(dim) bytes of
+// device scratch.
+size_t col_shift_scratch_bytes(int dim);
 void launch_col_shift(const float *x, size_t n, int dim, int dpad, double *partial, uint32_t *nonint, float *shift,
                       hipStream_t s);
 // One round of the fused MFMA distance + threshold filter over base rows [row_begin, row_end)

@@ -105,8 +105,13 @@ struct KernelTimer {
     void reset() { ms = work = bytes = 0.0; launches = 0; used = 0; }
 };
 
+// The allocation-free search's working memory on device dev (VHIP_NOALLOC_SCRATCH_BYTES): takes
+// that device's lock into `lock`, held until the caller releases it, and returns the array's
+// device address (looked up once per device).
+int noalloc_scratch_acquire(int dev, std::unique_lock<std::mutex> &lock, void **ptr);
+
 uint64_t splitmix64(uint64_t &state);
-// Fisher-Yates permutation of [0, n) from a fixed seed (row order of the resident base).
+// Fisher-Yates permutation of [0, n) from a seed (the seeded shuffle init of k-means).
 std::vector<uint32_t> row_permutation(size_t n, uint64_t seed);
 
 // Rust BinaryHeap-based bounded top-k merge: CollectiveOps::top_k_reduce
