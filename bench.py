@@ -10,14 +10,16 @@ Printed JSON (one line): metric/value/unit, ms_per_step, "roofline" of the domin
 (FP32-MFMA distance + filter kernel, its algorithmic flops per launch divided by its average
 launch time, measured with HIP events on the engine's stream over the timed region),
 "cpu_baseline": the oracle's restatement of the reference CPU path (CudaKnnEngine::search_batch_cpu,
-knn.rs:312-377, AVX-512 dispatch as vector-simd) timed on this host on a bounded query sample, and
-"parity": the timed run's results against the oracle's on that sample (tie-aware recall >= 0.999,
-distances within 1e-4 relative, exact on integer data).  The default line also carries the other
-workloads under "kmeans" (first iteration checked against the oracle's: <= 0.01% flips, all
-near-ties, centroids within 1e-4), "cos768", "hamming" (bit-exact against the oracle's popcount
-search over all 10M codes), "l1", "linf" and "ivfpq" (the IVF-PQ search on clustered data,
-checked against the oracle's search_with_nprobe), each with its own roofline, CPU baseline and
-parity.
+knn.rs:312-377, AVX-512 dispatch as vector-simd) timed on this host, and "parity": the timed run's
+results against the oracle's (tie-aware recall >= 0.999, distances within 1e-4 relative, exact on
+integer data).  The oracle searches every query when that takes at most FULL_PARITY_S seconds
+(the headline workload, L1, Linf), else a strided sample that always holds the last 128 queries,
+i.e. the last, partial query tile of every scan kernel; each parity object names its queries.  The
+default line also carries the other workloads under "kmeans" (each of the 10 iterations checked
+against the oracle's iteration from the GPU's previous centroids: <= 0.01% flips, all near-ties,
+centroids within 1e-4), "cos768", "hamming" (bit-exact against the oracle's popcount search over
+all 10M codes), "l1", "linf" and "ivfpq" (the IVF-PQ search on clustered data, checked against
+the oracle's search_with_nprobe), each with its own roofline, CPU baseline and parity.
 The process exits with status 3, after printing the line, when any parity check fails.
 
 Other workloads: --workload cos768 | kmeans | hamming | l1 | linf | gauss (see WORKLOADS), ivf_coarse
@@ -154,37 +156,62 @@ def run_knn(vh, base, queries, k, metric, steps, warmup, hamming=False):
 
 
 CPU_TARGET_S = 10.0  # wall time the CPU baseline leg aims for (bounded sample of the workload)
+FULL_PARITY_S = 20.0  # the oracle searches every query when that takes at most this long
+TAIL_QUERIES = 128    # the last queries: the last (partial) query tile of every scan kernel
 
 
-def cpu_knn_baseline(base, queries, k, metric, max_sample=None):
-    """Times the oracle's restatement of search_batch_cpu on a query sample sized (from a 16-query
-    probe) to take about CPU_TARGET_S seconds on this host's threads."""
+def parity_sample(nq, size, tail=TAIL_QUERIES):
+    """Query indices of the parity leg: all nq when size >= nq, else an even stride over the
+    first nq - tail queries plus the last `tail` (the last, partial query tile of every scan
+    kernel, which a prefix sample never reaches), about `size` in all."""
+    if size >= nq:
+        return np.arange(nq)
+    head = nq - tail
+    stride = max(1, -(-head // max(1, size - tail)))
+    return np.concatenate([np.arange(0, head, stride), np.arange(head, nq)])
+
+
+def describe_sample(idx, nq):
+    if len(idx) == nq:
+        return f"all {nq} queries"
+    stride = int(idx[1] - idx[0]) if len(idx) > 1 else 1
+    head = nq - TAIL_QUERIES
+    return (f"{len(idx)} of the {nq} queries: every {stride}th of queries 0..{head - 1} and all of "
+            f"{head}..{nq - 1} (the last query tiles)")
+
+
+def cpu_knn_baseline(base, queries, k, metric, full_under_s=FULL_PARITY_S):
+    """Times the oracle's restatement of search_batch_cpu on every query when a 16-query probe
+    says that takes at most full_under_s seconds on this host's threads, else on a sample sized to
+    take about CPU_TARGET_S seconds (parity_sample: strided, with the last queries).  Returns the
+    baseline and (oracle result, query indices), the parity leg's reference."""
     import oracle
 
     th = cpu_threads()
-    cap = min(queries.shape[0], max_sample or queries.shape[0])
+    nq = queries.shape[0]
     t0 = time.perf_counter()
     oracle.knn_search_batch(base, queries[:16], k, metric, threads=th)
-    probe = time.perf_counter() - t0
-    sample = int(max(16, min(cap, 16 * CPU_TARGET_S / max(probe, 1e-6))))
+    per_q = max(time.perf_counter() - t0, 1e-6) / 16
+    size = nq if per_q * nq <= full_under_s else int(max(TAIL_QUERIES + 16, CPU_TARGET_S / per_q))
+    idx = parity_sample(nq, size)
     t0 = time.perf_counter()
-    ref = oracle.knn_search_batch(base, queries[:sample], k, metric, threads=th)
+    ref = oracle.knn_search_batch(base, np.ascontiguousarray(queries[idx]), k, metric, threads=th)
     dt = time.perf_counter() - t0
     be = {0: "scalar", 1: "AVX2+FMA", 2: "AVX-512F"}[oracle.detect_backend()]
-    return {"value": round(sample / dt, 3), "unit": "queries/s", "cores": th, "kind": "port",
-            "sample": f"{sample} of the {queries.shape[0]} queries against the full base, k={k}, "
-                      f"{be} backend, {dt:.2f} s wall on {th} threads (affinity mask) ({cpu_model()})"}, ref
+    return {"value": round(len(idx) / dt, 3), "unit": "queries/s", "cores": th, "kind": "port",
+            "sample": f"{describe_sample(idx, nq)} against the full base, k={k}, {be} backend, {dt:.2f} s wall "
+                      f"on {th} threads (affinity mask) ({cpu_model()})"}, (ref, idx)
 
 
 def knn_parity(base, queries, ids, dist, ref, k, metric, rtol, atol, min_recall=0.999):
     """Parity of the timed GPU search with the oracle on the queries the oracle searched (ref =
-    its ids, distances and lengths for queries[:len]): tie-aware recall (a returned id counts
+    (its ids, distances and lengths, the query indices)): tie-aware recall (a returned id counts
     when its oracle value is at least as good as the oracle's k-th), every reported distance
     against the oracle's value of the same (query, id) pair within rtol / atol, the k best values
     as a multiset, and unique in-range ids.  Packed Hamming compares popcount distances."""
     import oracle
 
-    rids, rdist, _ = ref
+    (rids, rdist, _), idx = ref
     m = rids.shape[0]
     hib = metric in ("dot", "cosine")
     ok_ids = total = 0
@@ -192,21 +219,22 @@ def knn_parity(base, queries, ids, dist, ref, k, metric, rtol, atol, min_recall=
     dist_ok = multiset_ok = ids_ok = True
     for q0 in range(0, m, 512):
         q1 = min(m, q0 + 512)
-        got = ids[q0:q1, :k].astype(np.int64)
+        qi = idx[q0:q1]
+        got = ids[qi, :k].astype(np.int64)
         ids_ok = ids_ok and bool(np.all(got < base.shape[0]))
         ids_ok = ids_ok and all(len(set(r.tolist())) == k for r in got)
         got = np.minimum(got, base.shape[0] - 1)
         if metric == "hamming":
-            refv = np.bitwise_count(base[got] ^ queries[q0:q1, None, :]).sum(-1).astype(np.float64)
+            refv = np.bitwise_count(base[got] ^ queries[qi, None, :]).sum(-1).astype(np.float64)
         else:
-            qq = np.repeat(queries[q0:q1], k, 0)
+            qq = np.repeat(queries[qi], k, 0)
             refv = oracle.distance_rows(metric, qq, base[got.reshape(-1)]).reshape(q1 - q0, k).astype(np.float64)
         kth = rdist[q0:q1, k - 1:k].astype(np.float64)
         tol = rtol * np.abs(kth) + atol
         good = refv >= kth - tol if hib else refv <= kth + tol
         ok_ids += int(good.sum())
         total += good.size
-        diff = np.abs(dist[q0:q1, :k].astype(np.float64) - refv)
+        diff = np.abs(dist[qi, :k].astype(np.float64) - refv)
         dist_ok = dist_ok and bool(np.all(diff <= rtol * np.abs(refv) + atol))
         max_abs = max(max_abs, float(diff.max()))
         nz = np.abs(refv) > 0
@@ -216,7 +244,10 @@ def knn_parity(base, queries, ids, dist, ref, k, metric, rtol, atol, min_recall=
         multiset_ok = multiset_ok and bool(np.all(np.abs(rs - np.sort(refv, 1)) <= rtol * np.abs(rs) + atol))
     recall = ok_ids / max(total, 1)
     ok = bool(ids_ok and dist_ok and multiset_ok and recall >= min_recall)
-    return {"queries_checked": int(m), "k": k, "recall_tie_aware": round(recall, 6), "min_recall": min_recall,
+    nq = queries.shape[0]
+    return {"queries_checked": int(m), "query_sample": describe_sample(idx, nq), "first_query": int(idx[0]),
+            "last_query": int(idx[-1]), "last_tile_checked": bool(np.all(np.isin(np.arange(nq - TAIL_QUERIES, nq), idx))),
+            "k": k, "recall_tie_aware": round(recall, 6), "min_recall": min_recall,
             "max_abs_dist_err": max_abs, "max_rel_dist_err": max_rel,
             "distance_tolerance": {"rtol": rtol, "atol": atol}, "distances_ok": dist_ok,
             "kbest_values_match": multiset_ok, "ids_unique_in_range": ids_ok, "ok": ok}
@@ -245,28 +276,50 @@ def kmeans_parity(data, cent, got, ref):
     gc_, rc_ = got["centroids"].astype(np.float64), ref["centroids"].astype(np.float64)
     err = np.linalg.norm(gc_ - rc_, axis=1) / np.maximum(np.linalg.norm(rc_, axis=1), 1e-6)
     worst = float(err[~touched].max()) if (~touched).any() else 0.0
-    for c in np.nonzero(touched)[0]:
-        mem = np.nonzero(ga == c)[0]
-        want = data[mem].astype(np.float64).mean(0) if len(mem) else cent[c].astype(np.float64)
-        worst = max(worst, float(np.linalg.norm(gc_[c] - want) / max(np.linalg.norm(want), 1e-6)))
+    if touched.any():
+        # float64 means of the GPU's members of every touched cluster, in one pass over the points
+        sel = touched[ga]
+        sums = np.zeros((kc, data.shape[1]), np.float64)
+        np.add.at(sums, ga[sel], data[sel].astype(np.float64))
+        cnt = np.bincount(ga[sel], minlength=kc)
+        for c in np.nonzero(touched)[0]:
+            want = sums[c] / cnt[c] if cnt[c] else cent[c].astype(np.float64)
+            worst = max(worst, float(np.linalg.norm(gc_[c] - want) / max(np.linalg.norm(want), 1e-6)))
     inertia_rel = abs(float(got["inertia"]) - float(ref["inertia"])) / max(abs(float(ref["inertia"])), 1e-30)
     ok = bool(len(flips) <= max(1, int(1e-4 * n)) and near and counts_ok and worst <= 1e-4 and inertia_rel <= 1e-4)
-    return {"iteration": "first, from the initial centroids", "points": int(n), "assignment_flips": int(len(flips)),
-            "max_flip_frac": 1e-4, "flips_all_near_ties": near, "counts_match": counts_ok,
+    return {"assignment_flips": int(len(flips)), "flips_all_near_ties": near, "counts_match": counts_ok,
             "max_centroid_rel_err": worst, "inertia_rel_err": inertia_rel, "ok": ok}
 
 
 def bench_kmeans(vh, steps_iters, with_cpu):
+    """2,000,000 x 96 mixture of 4,096 components, 4,096 centroids from the first 4,096 points,
+    `steps_iters` Lloyd iterations timed back to back.  Parity (untimed, before the timed run):
+    the same iterations run one at a time, each checked against the oracle's Lloyd iteration
+    (KMeans::fit body) from the GPU's own previous centroids; with_cpu false checks the first
+    only.  Those oracle iterations are also the CPU baseline."""
     from vector_hip import datasets as ds
+    import oracle
 
     n, d, kc = 2_000_000, 96, 4096
     log(f"kmeans: generating {n} x {d} mixture of {kc}")
     data, _, _ = ds.gaussian_mixture(n, d, kc, ds.SEED_MIXTURE)
     init = data[:kc].copy()
     st = vh.KMeansState(data)
+    th = cpu_threads()
     st.set_centroids(init)
-    st.run(1)  # warm-up: the first iteration from the initial centroids, kept for the parity check
-    first = st.read()
+    cent = init
+    checks, cpu_s = [], []
+    for it in range(steps_iters if with_cpu else 1):
+        st.run(1)
+        got = st.read()
+        t0 = time.perf_counter()
+        ref = oracle.kmeans_step(data, cent, "l2", threads=th)
+        cpu_s.append(time.perf_counter() - t0)
+        r = kmeans_parity(data, cent, got, ref)
+        log(f"  iteration {it + 1} against the oracle: flips {r['assignment_flips']}, "
+            f"centroid err {r['max_centroid_rel_err']:.2e}, ok {r['ok']}")
+        checks.append(r)
+        cent = got["centroids"]
     st.set_centroids(init)
     st.profile(True)
     vh.synchronize()
@@ -281,28 +334,25 @@ def bench_kmeans(vh, steps_iters, with_cpu):
            "value": round(1e3 / ms_iter, 3), "unit": "iterations/s", "ms_per_iteration": round(ms_iter, 3),
            "inertia": out["inertia"],
            "roofline": roofline(prof, "mfma", PEAK_MFMA_F32, "TFLOP/s", "kmeans")}
-    import oracle
-
-    # whole Lloyd iterations (KMeans::fit body) over all points from the same initial centroids,
-    # repeated until about CPU_TARGET_S seconds have passed (one without the CPU leg: the parity
-    # reference)
-    th = cpu_threads()
-    its = 0
-    ref = None
-    t0 = time.perf_counter()
-    while True:
-        r = oracle.kmeans_step(data, init, "l2", threads=th)
-        ref = r if ref is None else ref
-        its += 1
-        if not with_cpu or time.perf_counter() - t0 >= CPU_TARGET_S or its >= 10:
-            break
-    dt = (time.perf_counter() - t0) / its
-    res["parity"] = kmeans_parity(data, init, first, ref)
+    # the update's fixed-point sums are order-independent: the timed run's centroids equal those
+    # of the checked one-at-a-time iterations bit for bit
+    same = len(checks) == steps_iters and bool(np.array_equal(out["centroids"].view(np.uint32), cent.view(np.uint32)))
+    res["parity"] = {"iterations_checked": len(checks), "points": int(n),
+                     "rule": "each iteration from the GPU's previous centroids against the oracle's: <= 0.01% "
+                             "assignment flips, all near-ties; counts equal; centroids within 1e-4 of their "
+                             "norm; inertia within 1e-4",
+                     "max_flips": max(c["assignment_flips"] for c in checks), "max_flip_frac": 1e-4,
+                     "max_centroid_rel_err": max(c["max_centroid_rel_err"] for c in checks),
+                     "max_inertia_rel_err": max(c["inertia_rel_err"] for c in checks),
+                     "timed_run_equals_checked_iterations": same if len(checks) == steps_iters else None,
+                     "per_iteration": checks,
+                     "ok": all(c["ok"] for c in checks) and (same or len(checks) < steps_iters)}
     if with_cpu:
+        dt = float(np.mean(cpu_s))
         res["cpu_baseline"] = {"value": round(1.0 / dt, 5), "unit": "iterations/s", "cores": th, "kind": "port",
-                               "sample": f"{its} full Lloyd iteration(s) (KMeans::fit body) over all {n} points "
-                                         f"and {kc} centroids, {dt:.2f} s each on {th} threads (affinity mask) "
-                                         f"({cpu_model()})"}
+                               "sample": f"{len(cpu_s)} full Lloyd iterations (KMeans::fit body) over all {n} points "
+                                         f"and {kc} centroids (the parity leg's), {dt:.2f} s each on average on "
+                                         f"{th} threads (affinity mask) ({cpu_model()})"}
         res["speedup_vs_cpu"] = round(res["value"] / res["cpu_baseline"]["value"], 1)
     return res
 
@@ -474,23 +524,23 @@ def bench_ivfpq(vh, steps, warmup, with_cpu):
 
         ref = []
 
-        def run(nsamp):
+        def run(idx):
             ref.clear()
             t = time.perf_counter()
-            for i in range(nsamp):
+            for i in idx:
                 pr, _ = oracle.find_top_centroids(q[i], cc, nprobe, "l2")
                 ri, rd = oracle.ivfpq_search(q[i], cc, cb, m_sub, ks, off, lids, lcodes, pr, k, "l2")
-                ref.append((pr, ri, rd))
+                ref.append((int(i), pr, ri, rd))
             return time.perf_counter() - t
 
-        sp = 16
-        dt = run(sp)
-        sp = int(min(nq, max(sp, sp * CPU_TARGET_S / max(dt, 1e-6))))
-        dt = run(sp)
+        dt = run(range(16))
+        idx = parity_sample(nq, int(max(TAIL_QUERIES + 16, 16 * CPU_TARGET_S / max(dt, 1e-6))))
+        dt = run(idx)
         out["parity"] = ivfpq_parity(ids, dist, probes, ref, k)
+        out["parity"]["query_sample"] = describe_sample(idx, nq)
         be = {0: "scalar", 1: "AVX2+FMA", 2: "AVX-512F"}[oracle.detect_backend()]
-        out["cpu_baseline"] = {"value": round(sp / dt, 2), "unit": "queries/s", "cores": 1, "kind": "port",
-                               "sample": f"{sp} of the {nq} queries through the oracle's find_top_centroids + "
+        out["cpu_baseline"] = {"value": round(len(idx) / dt, 2), "unit": "queries/s", "cores": 1, "kind": "port",
+                               "sample": f"{describe_sample(idx, nq)} through the oracle's find_top_centroids + "
                                          f"search_with_nprobe on the built index, {be} backend, {dt:.2f} s on "
                                          f"1 thread ({cpu_model()})"}
     return out
@@ -498,14 +548,14 @@ def bench_ivfpq(vh, steps, warmup, with_cpu):
 
 def ivfpq_parity(ids, dist, probes, ref, k):
     """Parity of the timed IVF-PQ search with the oracle's search_with_nprobe on the oracle's own
-    probes (ref: (probes, ids, distances) per sampled query).  A query whose GPU probe set differs
+    probes (ref: (query index, probes, ids, distances) per sampled query).  A query whose GPU probe set differs
     from the oracle's (a near-tie at the nprobe-th centroid) is counted and skipped.  Otherwise
     the result counts must match, the distances as sorted lists within 1e-4 relative to the
     largest, and an id outside the oracle's k best may only tie with its k-th distance."""
     checked = probe_ties = 0
     dist_ok = ids_ok = True
     max_err = 0.0
-    for i, (pr, ri, rd) in enumerate(ref):
+    for i, pr, ri, rd in ref:
         if set(np.asarray(pr).tolist()) != set(probes[i].tolist()):
             probe_ties += 1
             continue
@@ -693,20 +743,24 @@ def bench_knn_workload(vh, key, steps, warmup, with_cpu):
             sub = 500_000
             un_b = oracle.unpack_bits(base[:sub])
             un_q = oracle.unpack_bits(q)
-            cb, _ = cpu_knn_baseline(un_b, un_q, k, "hamming")
+            cb, _ = cpu_knn_baseline(un_b, un_q, k, "hamming", full_under_s=0.0)
             del un_b, un_q
             cb["value"] = round(cb["value"] * sub / w["n"], 4)
             cb["sample"] = (f"reference semantics (thresholded float Hamming over codes unpacked to 0/1 floats) "
                             f"against {sub} of the {w['n']} codes, rate scaled by {sub}/{w['n']}; " + cb["sample"])
             out["cpu_baseline"] = cb
-        # parity over the full base: the oracle's popcount search on a query sample, bit-exact
-        ref = oracle.hamming_packed_knn(base, q[:512], k, threads=cpu_threads())
+        # parity over the full base: the oracle's popcount search on a strided query sample with
+        # the last queries, bit-exact
+        idx = parity_sample(w["nq"], 640 if with_cpu else 192)
+        ref = (oracle.hamming_packed_knn(base, np.ascontiguousarray(q[idx]), k, threads=cpu_threads()), idx)
         out["parity"] = knn_parity(base, q, ids, dist, ref, k, "hamming", 0.0, 0.0, min_recall=1.0)
     else:
         if with_cpu:
             out["cpu_baseline"], ref = cpu_knn_baseline(base, q, k, w["metric"])
         else:
-            ref = oracle.knn_search_batch(base, q[:64], k, w["metric"], threads=cpu_threads())
+            idx = parity_sample(w["nq"], 192)
+            ref = (oracle.knn_search_batch(base, np.ascontiguousarray(q[idx]), k, w["metric"], threads=cpu_threads()),
+                   idx)
         # distances within 1e-4 relative; integer data is exact in every summation order
         exact = w["gen"] == "uniform_int"
         out["parity"] = knn_parity(base, q, ids, dist, ref, k, w["metric"], 0.0 if exact else 1e-4,
