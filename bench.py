@@ -580,6 +580,151 @@ def ivfpq_parity(ids, dist, probes, ref, k):
             "ids_ok_up_to_ties": ids_ok, "ok": ok}
 
 
+def bench_kmeans_fit(vh, with_cpu):
+    """CudaKMeansEngine::fit end to end with its default seeded k-means++ init (kmeans.rs:58-97,
+    409-460), the init timed apart from the Lloyd iterations:
+    (a) the 2,000,000 x 96, 4,096-centroid mixture, 10 iterations (tol < 0), points resident
+        (KMeansState.fit), plus the whole host-buffer fit; the init's HBM bound is one read of the
+        points per drawn centre after the first, (K - 1) n dpad 4 B / 8 TB/s;
+    (b) cuda_bench.rs:156-211's shape: 10,000 x 768 U[-1, 1], cosine, K = 16 .. 256, at most 15
+        iterations, tol 1e-4, through CudaKMeansEngine.fit (host data in, centroids out), beside
+        the oracle's KMeans::fit body from the same initial centroids on the host threads."""
+    from vector_hip import datasets as ds
+    import oracle
+
+    def timed(fn, reps=1):
+        fn()
+        ts = []
+        for _ in range(reps):
+            vh.synchronize()
+            t0 = time.perf_counter()
+            r = fn()
+            vh.synchronize()
+            ts.append(time.perf_counter() - t0)
+        return float(np.median(ts)), r
+
+    n, d, kc = 2_000_000, 96, 4096
+    log(f"kmeans_fit: {n} x {d} mixture, K = {kc}")
+    data, _, _ = ds.gaussian_mixture(n, d, kc, ds.SEED_MIXTURE)
+    st = vh.KMeansState(data)
+    t_init, _ = timed(lambda: st.fit(kc, 0, -1.0, init_mode=vh.INIT_KMEANSPP, seed=42), reps=3)
+    t_fit, (_, _, (_, _, iters, inertia)) = timed(lambda: st.fit(kc, 10, -1.0, init_mode=vh.INIT_KMEANSPP, seed=42),
+                                                  reps=3)
+    eng = vh.CudaKMeansEngine()
+    t_host, _ = timed(lambda: eng.fit(data, d, kc, 10, -1.0))
+    bound = (kc - 1) * n * d * 4 / PEAK_HBM
+    big = {"workload": f"kmeans_l2_{n}x{d}_k{kc}_10iters_kmeanspp", "init_ms": round(t_init * 1e3, 2),
+           "init_hbm_bound_ms": round(bound * 1e3, 2), "init_over_bound": round(t_init / bound, 3),
+           "fit_ms": round(t_fit * 1e3, 2), "lloyd_ms": round((t_fit - t_init) * 1e3, 2), "iterations": iters,
+           "inertia": inertia, "host_fit_ms": round(t_host * 1e3, 2),
+           "note": "fit_ms: KMeansState.fit (points resident), median of 3; host_fit_ms: CudaKMeansEngine.fit with "
+                   "the 768 MB of points uploaded and the centroids returned"}
+    small = []
+    dn, dd = 10_000, 768
+    x = ds.uniform(dn, dd, ds.SEED_BASE)
+    th = cpu_threads()
+    for kk in (16, 32, 64, 128, 256):
+        t_i, r0 = timed(lambda: eng.fit(x, dd, kk, 0, 1e-4, vh.DistanceMetric.CosineSimilarity), reps=5)
+        t_f, r = timed(lambda: eng.fit(x, dd, kk, 15, 1e-4, vh.DistanceMetric.CosineSimilarity), reps=5)
+        row = {"k": kk, "fit_ms": round(t_f * 1e3, 3), "init_ms": round(t_i * 1e3, 3), "iterations": r.iterations}
+        if with_cpu:
+            t0 = time.perf_counter()
+            ref = oracle.kmeans_fit(x, r0.centroids, 15, 1e-4, "cosine", threads=th)
+            row["cpu_lloyd_ms"] = round((time.perf_counter() - t0) * 1e3, 2)
+            row["cpu_iterations"] = ref["iterations"]
+        small.append(row)
+        log(f"  k={kk}: {row}")
+    out = {"metric": "CudaKMeansEngine::fit with k-means++ init (ms)", "value": big["fit_ms"], "unit": "ms",
+           "n_gpus": 1, "steps": 3, "warmup": 1, "ms_per_step": big["fit_ms"], "higher_is_better": False,
+           "scaling": "strong", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+           "config": {"workload": big["workload"], "parallelism": "single GPU"},
+           "kmeans_2m": big, "cuda_bench_shape": {"data": f"{dn} x {dd} U[-1,1], cosine, at most 15 iterations, "
+                                                          f"tol 1e-4, host buffers", "rows": small}}
+    if with_cpu:
+        out["cuda_bench_shape"]["cpu_note"] = (f"cpu_lloyd_ms: the oracle's KMeans::fit body from the GPU's k-means++ "
+                                               f"centroids on {th} threads (affinity mask) ({cpu_model()})")
+    return out
+
+
+SWEEP_BATCHES = (1, 2, 4, 8, 16, 32, 64, 128)
+
+
+def bench_batch_sweep(vh, reps, with_cpu):
+    """cuda_bench.rs:41-55, 98-152: DistributedKnnEngine::search_batch at G = 1 over batch sizes 1 to
+    128 with k = 10, on its default 10,000 x 768 U[-1, 1] base under cosine, and on the headline
+    1,000,000 x 128 integer base under squared L2.  Per batch size: the host-buffer call (the
+    reference's path: queries in, results out over PCIe) and the device-resident call, each the
+    median of `reps` calls after two warm-up calls, against one pass over the base at 8 TB/s; every
+    batch checked against the oracle (tie-aware recall, distances within 1e-4)."""
+    from vector_hip import datasets as ds
+    import oracle
+
+    shapes = [("cos768_10k", ds.uniform(10_000, 768, ds.SEED_BASE), ds.uniform(128, 768, ds.SEED_QUERIES),
+               vh.DistanceMetric.CosineSimilarity, "cosine"),
+              ("l2int_1m", ds.uniform_int(1_000_000, 128, ds.SEED_BASE), ds.uniform_int(128, 128, ds.SEED_QUERIES),
+               vh.DistanceMetric.L2Squared, "l2")]
+    k = 10
+    th = cpu_threads()
+    out_shapes = {}
+    all_ok = True
+    for name, base, qs, metric, mname in shapes:
+        n, d = base.shape
+        log(f"batch_sweep: {name}")
+        eng = vh.DistributedKnnEngine.try_new(base, d, 1, vh.GpuShardMode.Sharded, metric)
+        dev = vh.CudaKnnEngine(base, d, metric)
+        bound_us = n * d * 4 / PEAK_HBM * 1e6
+        rows = []
+        for b in SWEEP_BATCHES:
+            q = np.ascontiguousarray(qs[:b])
+            dq = vh.DeviceBuffer.from_host(q)
+            di = vh.DeviceBuffer(b * k * 4)
+            dd = vh.DeviceBuffer(b * k * 4)
+
+            def med(fn):
+                for _ in range(2):
+                    fn()
+                ts = []
+                for _ in range(reps):
+                    vh.synchronize()
+                    t0 = time.perf_counter()
+                    fn()
+                    ts.append(time.perf_counter() - t0)
+                return float(np.median(ts)) * 1e6
+
+            host_us = med(lambda: eng.search_batch(q, k))
+            dev_us = med(lambda: dev.search_batch_device(dq.ptr, b, k, di.ptr, dd.ptr))
+            ids, dist, _ = dev.search_batch_arrays(q, k)
+            ref = oracle.knn_search_batch(base, q, k, mname, threads=th)
+            par = knn_parity(base, q, ids, dist, (ref, np.arange(b)), k, mname, 0.0 if mname == "l2" else 1e-4,
+                             0.0 if mname == "l2" else 1e-6)
+            host_res = eng.search_batch(q, k)
+            # top_k_reduce may order equal distances differently: compare each query's id set
+            same = all({r.id for r in host_res[i]} == set(ids[i].tolist()) for i in range(b))
+            all_ok = all_ok and par["ok"] and same
+            row = {"batch": b, "host_us": round(host_us, 1), "host_qps": round(b / host_us * 1e6, 1),
+                   "device_us": round(dev_us, 1), "device_qps": round(b / dev_us * 1e6, 1),
+                   "device_over_bound": round(dev_us / bound_us, 2), "parity_ok": par["ok"] and same}
+            if with_cpu:
+                t0 = time.perf_counter()
+                oracle.knn_search_batch(base, q, k, mname, threads=th)
+                row["cpu_us"] = round((time.perf_counter() - t0) * 1e6, 1)
+            rows.append(row)
+            log(f"  {name} batch {b}: {row}")
+        out_shapes[name] = {"base": f"{n} x {d}", "metric": mname, "k": k, "one_pass_bound_us": round(bound_us, 2),
+                            "rows": rows}
+    b1 = out_shapes["cos768_10k"]["rows"][0]
+    return {"metric": "kNN batch latency sweep (cuda_bench shape)", "value": b1["host_qps"], "unit": "queries/s",
+            "n_gpus": 1, "steps": reps, "warmup": 2, "ms_per_step": round(b1["host_us"] / 1e3, 4),
+            "higher_is_better": True, "scaling": "strong", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+            "config": {"workload": "batch_sweep_cos768_10k_and_l2int_1m_k10", "batches": list(SWEEP_BATCHES),
+                       "parallelism": "single GPU"},
+            "shapes": out_shapes,
+            "cpu_note": f"cpu_us: the oracle's search_batch_cpu on {th} threads (affinity mask) ({cpu_model()})",
+            "parity": {"ok": all_ok, "rule": "every batch against the oracle (tie-aware recall >= 0.999, distances "
+                                             "exact for l2 integer data, 1e-4 for cosine); host-buffer ids equal "
+                                             "the device call's"}}
+
+
 def bench_copy(vh, nbytes=1 << 30, reps=5):
     """Plain device-to-device copy of `nbytes` (the runtime's blit kernel).  Its FETCH_SIZE and
     WRITE_SIZE counters calibrate the HBM traffic figures of the other kernels."""
@@ -774,7 +919,8 @@ def main():
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--workload", default="default",
-                    choices=["default", "kmeans", "copy", "ivf_coarse", "ivfpq", "upload"] + sorted(WORKLOADS))
+                    choices=["default", "kmeans", "kmeans_fit", "batch_sweep", "copy", "ivf_coarse", "ivfpq",
+                             "upload"] + sorted(WORKLOADS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -795,6 +941,10 @@ def main():
         out = bench_ivfpq(vh, args.steps, args.warmup, not args.no_cpu)
     elif args.workload == "upload":
         out = bench_upload(vh, args.steps, args.warmup)
+    elif args.workload == "kmeans_fit":
+        out = bench_kmeans_fit(vh, not args.no_cpu)
+    elif args.workload == "batch_sweep":
+        out = bench_batch_sweep(vh, max(args.steps, 20), not args.no_cpu)
     elif args.workload == "kmeans":
         r = bench_kmeans(vh, 10, not args.no_cpu)
         out = {"metric": METRIC, "value": r["value"], "unit": r["unit"], "n_gpus": 1, "steps": 10, "warmup": 1,

@@ -1,0 +1,51 @@
+"""GPU parity of the reference benchmark's batch sweep (cuda_bench.rs:41-55, 98-152).
+
+DistributedKnnEngine::search_batch at one GPU over batch sizes 1 to 128 with k = 10: on the
+benchmark's default 10,000 x 768 U[-1, 1] base under cosine (and dot product, and squared L2),
+and on a 200,000 x 128 integer base under squared L2 (exact distances).  Every batch is checked
+against the oracle's search_batch_cpu.
+"""
+import numpy as np
+import pytest
+
+from knn_check import check_knn
+
+pytestmark = pytest.mark.gpu
+
+BATCHES = (1, 2, 3, 4, 8, 16, 31, 32, 64, 127, 128)
+
+
+@pytest.fixture(scope="module")
+def vh():
+    import vector_hip
+
+    assert vector_hip.CudaDeviceContext.device_count() >= 1, "no gfx950 GPU visible"
+    return vector_hip
+
+
+def _sweep(vh, oracle, base, queries, metric, mname, **tol):
+    eng = vh.DistributedKnnEngine.try_new(base, base.shape[1], 1, vh.GpuShardMode.Sharded, metric)
+    for b in BATCHES:
+        q = np.ascontiguousarray(queries[:b])
+        print(f"  {mname} {base.shape[0]} x {base.shape[1]} batch {b}", flush=True)
+        ids, dist, lens = eng.search_batch_arrays(q, 10)
+        assert np.all(lens == 10)
+        check_knn(oracle, base, q, ids, dist, 10, mname, **tol)
+
+
+@pytest.mark.parametrize("mname", ["cosine", "dot", "l2"])
+def test_cuda_bench_default_shape(vh, oracle, mname):
+    from vector_hip import datasets as ds
+
+    names = {"cosine": "CosineSimilarity", "dot": "DotProduct", "l2": "L2Squared"}
+    base = ds.uniform(10_000, 768, 51)
+    q = ds.uniform(128, 768, 52)
+    _sweep(vh, oracle, base, q, vh.DistanceMetric[names[mname]], mname, rtol=1e-4, atol=1e-5)
+
+
+def test_integer_l2_batches(vh, oracle):
+    from vector_hip import datasets as ds
+
+    base = ds.uniform_int(200_000, 128, 53)
+    q = ds.uniform_int(128, 128, 54)
+    _sweep(vh, oracle, base, q, vh.DistanceMetric.L2Squared, "l2", rtol=0.0, atol=0.0)

@@ -201,3 +201,53 @@ def test_high_dimension_one_step(vh, oracle, dim):
     st.set_centroids(cent)
     st.run(1)
     _check_step(oracle, data, cent, st.read(), "l2")
+
+
+def _splitmix64_draws(seed, count):
+    m = (1 << 64) - 1
+    st, out = seed, []
+    for _ in range(count):
+        st = (st + 0x9E3779B97F4A7C15) & m
+        z = st
+        z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & m
+        z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & m
+        out.append(z ^ (z >> 31))
+    return out
+
+
+def _kmeanspp_restated(x, k, seed):
+    """kmeans.rs:409-460 with the build's seeded draws: the first centre is draw 0 mod n; each next
+    one is the first point of positive weight whose running sum of D(x)^2 reaches u * total (u the
+    draw's top 53 bits in [0, 1)), or draw mod n when the total is at most 1e-6.  In float64, which
+    is exact here: the data are small integers."""
+    draws = _splitmix64_draws(seed, k)
+    xd = x.astype(np.float64)
+    n = len(x)
+    picks = [draws[0] % n]
+    mind = np.full(n, np.finfo(np.float32).max, np.float64)
+    for j in range(1, k):
+        mind = np.minimum(mind, ((xd - xd[picks[-1]]) ** 2).sum(1))
+        total = mind.sum()
+        if total <= 1e-6:
+            picks.append(draws[j] % n)
+            continue
+        thr = (draws[j] >> 11) * (1.0 / 9007199254740992.0) * total
+        cum = np.cumsum(mind)
+        picks.append(int(np.argmax((cum >= thr) & (mind > 0))))
+    return picks
+
+
+@pytest.mark.parametrize("n,dim,k,seed", [(3000, 40, 200, 5), (1_100_000, 8, 12, 9), (700, 128, 700, 3)])
+def test_kmeanspp_matches_its_restatement(vh, n, dim, k, seed):
+    """The device draws (k_kpp_update + k_kpp_select) pick exactly the rows of the float64
+    restatement: every distance and running sum is an exact integer here.  The shapes cover
+    several point blocks per step, more blocks than the select's threads (each thread then owns a
+    run of block sums), and k = n (the last draws find every remaining weight zero but one)."""
+    rng = np.random.default_rng(seed)
+    x = rng.integers(-8, 9, (n, dim)).astype(np.float32)
+    st = vh.KMeansState(x)
+    print(f"  k-means++ n={n} dim={dim} k={k}", flush=True)
+    c, _, (_, kk, iters, _) = st.fit(k, 0, -1.0, init_mode=0, seed=seed)
+    assert (kk, iters) == (k, 0)
+    want = x[_kmeanspp_restated(x, k, seed)]
+    assert np.array_equal(c, want)

@@ -385,30 +385,65 @@ __global__ __launch_bounds__(256) void k_coarse_score(const float *__restrict__ 
     }
 }
 
-// k-means++ step (CudaKMeansEngine::init_random, kmeans.rs:424-436): mind[i] =
-// min(mind[i], ||x_i - c||^2) in direct form, plus per-block sums of mind in double.
-constexpr int kKppBlock = 4096;
+// Seeded k-means++ on the device (CudaKMeansEngine::init_random, kmeans.rs:409-460).  Each step
+// is two launches on the state's stream, with no host round trip:
+//  * k_kpp_update: mind[i] = min(mind[i], ||x_i - c||^2) for the newest centre c, in direct form,
+//    and the sum of mind over each block of kKppBlock points (double, fixed tree order).  Eight
+//    lanes share a row (each a 16-byte column slice), so every load instruction of a wave reads
+//    eight whole 128-byte row pieces: the pass streams the points at HBM rate.
+//  * k_kpp_select: one workgroup draws the next centre with probability mind[i] / sum(mind), as
+//    the reference's linear scan does (the first i whose running sum reaches u * total), through
+//    the block sums and then the chosen block's values, and copies that point into the centres.
+// Both sums are in a fixed order, so a seed gives the same centres on every run.
+constexpr int kKppBlock = 1024;       // points per k_kpp_update block (256 threads)
+constexpr int kKppSelectThreads = 1024;  // equal to kKppBlock: the select reads a block one value per thread
+
 __global__ __launch_bounds__(256) void k_kpp_update(const float *__restrict__ pts, int dpad, int n,
                                                     const float *__restrict__ c, float *__restrict__ mind,
                                                     double *__restrict__ partial) {
+    extern __shared__ float4 s_c[];  // the centre, dpad / 4 float4
     __shared__ double red[256];
-    const int b0 = blockIdx.x * kKppBlock;
+    const int nc4 = dpad >> 2;
+    for (int i = threadIdx.x; i < nc4; i += 256) s_c[i] = ((const float4 *)c)[i];
+    __syncthreads();
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int part = lane & 7;  // this lane's column slices: part, part + 8, ...
+    const int b0 = blockIdx.x * kKppBlock + wave * (kKppBlock / 4);
+    const int b1 = min(n, b0 + kKppBlock / 4);
     double s = 0.0;
-    for (int i = b0 + threadIdx.x; i < min(n, b0 + kKppBlock); i += 256) {
-        const float *x = pts + (size_t)i * dpad;
-        float d2 = 0.0f;
-        for (int d = 0; d < dpad; d += 4) {
-            const float4 xv = *(const float4 *)(x + d);
-            const float4 cv = *(const float4 *)(c + d);
-            const float a0 = xv.x - cv.x, a1 = xv.y - cv.y, a2 = xv.z - cv.z, a3 = xv.w - cv.w;
-            d2 = fmaf(a0, a0, d2);
-            d2 = fmaf(a1, a1, d2);
-            d2 = fmaf(a2, a2, d2);
-            d2 = fmaf(a3, a3, d2);
+    constexpr int G = 4;  // groups of 8 rows in flight per wave
+    for (int r0 = b0 + (lane >> 3); r0 < b1; r0 += 8 * G) {
+        float d2[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g) d2[g] = 0.0f;
+        for (int j = part; j < nc4; j += 8) {
+            const float4 cv = s_c[j];
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const int r = r0 + 8 * g;
+                if (r < b1) {
+                    const float4 xv = ((const float4 *)(pts + (size_t)r * dpad))[j];
+                    const float a0 = xv.x - cv.x, a1 = xv.y - cv.y, a2 = xv.z - cv.z, a3 = xv.w - cv.w;
+                    d2[g] = fmaf(a0, a0, d2[g]);
+                    d2[g] = fmaf(a1, a1, d2[g]);
+                    d2[g] = fmaf(a2, a2, d2[g]);
+                    d2[g] = fmaf(a3, a3, d2[g]);
+                }
+            }
         }
-        const float m = fminf(mind[i], d2);
-        mind[i] = m;
-        s += (double)m;
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            float v = d2[g];
+            v += __shfl_xor(v, 1, 64);
+            v += __shfl_xor(v, 2, 64);
+            v += __shfl_xor(v, 4, 64);
+            const int r = r0 + 8 * g;
+            if (part == 0 && r < b1) {
+                const float m = fminf(mind[r], v);
+                mind[r] = m;
+                s += (double)m;
+            }
+        }
     }
     red[threadIdx.x] = s;
     __syncthreads();
@@ -417,6 +452,101 @@ __global__ __launch_bounds__(256) void k_kpp_update(const float *__restrict__ pt
         __syncthreads();
     }
     if (threadIdx.x == 0) partial[blockIdx.x] = red[0];
+}
+
+// Inclusive prefix sum of one double per thread over the workgroup (kKppSelectThreads), in a
+// fixed order; `tmp` holds kKppSelectThreads doubles.
+__device__ __forceinline__ double block_scan_incl(double v, double *tmp) {
+    const int t = threadIdx.x;
+    tmp[t] = v;
+    __syncthreads();
+    for (int o = 1; o < kKppSelectThreads; o <<= 1) {
+        const double a = t >= o ? tmp[t - o] : 0.0;
+        __syncthreads();
+        v += a;
+        tmp[t] = v;
+        __syncthreads();
+    }
+    return v;
+}
+
+// Step j's draw.  draw: the step's 64-bit random value.  A total weight of at most 1e-6 (every
+// point on a centre) takes draw mod n, as the reference takes a uniform index there.  Otherwise
+// the threshold is u * total with u = the draw's top 53 bits in [0, 1), and the centre is the
+// first point of positive weight whose running sum of mind reaches it: the first run of blocks,
+// then block, then point, at which the running sum reaches the threshold.  Running sums of
+// non-negative values never decrease, and the last run's sum is the total itself, so a run is
+// always found; should the sequential sums inside it round short of the threshold, its last block
+// (point) of positive weight is taken.  Every choice is a minimum or maximum over the threads, so
+// the result does not depend on their timing.
+__global__ __launch_bounds__(kKppSelectThreads) void k_kpp_select(const double *__restrict__ partial, int nb,
+                                                                  const float *__restrict__ mind, int n,
+                                                                  const uint64_t *__restrict__ draws, int j,
+                                                                  const float *__restrict__ pts, int dpad,
+                                                                  float *__restrict__ cent) {
+    __shared__ double tmp[kKppSelectThreads];
+    __shared__ int s_run, s_blk, s_pt, s_last;
+    __shared__ double s_before;
+    const int t = threadIdx.x;
+    const uint64_t draw = draws[j];
+    // block sums: thread t owns a contiguous run of them
+    const int per = (nb + kKppSelectThreads - 1) / kKppSelectThreads;
+    const int c0 = min(nb, t * per), c1 = min(nb, c0 + per);
+    double own = 0.0;
+    for (int b = c0; b < c1; ++b) own += partial[b];
+    const double incl = block_scan_incl(own, tmp);
+    const double excl = t > 0 ? tmp[t - 1] : 0.0;
+    const double total = tmp[kKppSelectThreads - 1];
+    if (t == 0) {
+        s_run = kKppSelectThreads;
+        s_pt = 0x7fffffff;
+        s_last = -1;
+    }
+    __syncthreads();
+    int idx;
+    if (total <= 1e-6) {
+        idx = (int)(draw % (uint64_t)n);
+    } else {
+        const double thr = (double)(draw >> 11) * (1.0 / 9007199254740992.0) * total;
+        if (own > 0.0 && incl >= thr) atomicMin(&s_run, t);
+        __syncthreads();
+        if (t == s_run) {
+            double cum = excl, cum_last = excl;
+            int pb = -1, lastb = -1;
+            for (int b = c0; b < c1; ++b) {
+                const double w = partial[b];
+                if (w > 0.0) {
+                    if (cum + w >= thr) {
+                        pb = b;
+                        break;
+                    }
+                    lastb = b;
+                    cum_last = cum;
+                }
+                cum += w;
+            }
+            if (pb < 0) {
+                pb = lastb;
+                cum = cum_last;
+            }
+            s_blk = pb;
+            s_before = cum;
+        }
+        __syncthreads();
+        const int pb = s_blk;
+        const int i = pb * kKppBlock + t;  // kKppSelectThreads == kKppBlock: one value per thread
+        const double w = i < n ? (double)mind[i] : 0.0;
+        const double ci = s_before + block_scan_incl(w, tmp);
+        if (w > 0.0) {
+            if (ci >= thr) atomicMin(&s_pt, i);
+            atomicMax(&s_last, i);
+        }
+        __syncthreads();
+        idx = s_pt != 0x7fffffff ? s_pt : s_last;
+    }
+    const float *src = pts + (size_t)idx * dpad;
+    float *dst = cent + (size_t)j * dpad;
+    for (int d = t; d < dpad; d += kKppSelectThreads) dst[d] = src[d];
 }
 
 __global__ void k_fill(float *p, size_t count, float v) {
@@ -687,55 +817,36 @@ static int km_total_inertia(vhip_kmeans *K, float *out) {
 }
 
 // Seeded k-means++ (kmeans.rs:409-460): first centre uniform, then each next centre drawn
-// with probability proportional to the squared L2 distance to the nearest chosen centre.
+// with probability proportional to the squared L2 distance to the nearest chosen centre.  The
+// draws (one 64-bit splitmix64 value per centre) are made on the host up front; every step then
+// runs on the device (k_kpp_update + k_kpp_select), with no host round trip.
 static int km_init_kmeanspp(vhip_kmeans *K, size_t k, uint64_t seed) {
     hipStream_t s = K->stream;
     const int n = (int)K->n;
     VH_CHECK(K->craw.ensure(K->dev, k * K->dpad * sizeof(float)));
     const float *pts = K->points();
     float *cr = K->craw.as<float>();
-    DevBuf mind, part;
+    DevBuf mind, part, draws;
     const int nb = ceil_div(n, kKppBlock);
     VH_CHECK(mind.ensure(K->dev, (size_t)n * sizeof(float)));
     VH_CHECK(part.ensure(K->dev, (size_t)nb * sizeof(double)));
-    hipLaunchKernelGGL(k_fill, dim3(ceil_div(n, 256)), dim3(256), 0, s, mind.as<float>(), (size_t)n, 3.4028235e38f);
+    VH_CHECK(draws.ensure(K->dev, k * sizeof(uint64_t)));
+    std::vector<uint64_t> dh(k);
     uint64_t st = seed;
-    size_t idx = splitmix64(st) % (size_t)n;
+    for (size_t j = 0; j < k; ++j) dh[j] = splitmix64(st);
+    VH_HIP(hipMemcpyAsync(draws.p, dh.data(), k * sizeof(uint64_t), hipMemcpyHostToDevice, s));
+    hipLaunchKernelGGL(k_fill, dim3(ceil_div(n, 256)), dim3(256), 0, s, mind.as<float>(), (size_t)n, 3.4028235e38f);
+    const size_t idx = dh[0] % (size_t)n;
     VH_HIP(hipMemcpyAsync(cr, pts + idx * K->dpad, K->dpad * sizeof(float), hipMemcpyDeviceToDevice, s));
-    std::vector<double> ph(nb);
-    std::vector<float> blk(kKppBlock);
+    const size_t lds = K->dpad * sizeof(float);
     for (size_t j = 1; j < k; ++j) {
-        hipLaunchKernelGGL(k_kpp_update, dim3(nb), dim3(256), 0, s, pts, (int)K->dpad, n, cr + (j - 1) * K->dpad,
+        hipLaunchKernelGGL(k_kpp_update, dim3(nb), dim3(256), lds, s, pts, (int)K->dpad, n, cr + (j - 1) * K->dpad,
                            mind.as<float>(), part.as<double>());
-        VH_HIP(hipGetLastError());
-        VH_HIP(hipMemcpyAsync(ph.data(), part.p, nb * sizeof(double), hipMemcpyDeviceToHost, s));
-        VH_HIP(hipStreamSynchronize(s));
-        double total = 0.0;
-        for (double v : ph) total += v;
-        if (total <= 1e-6) {
-            idx = splitmix64(st) % (size_t)n;
-        } else {
-            const double u = (double)(splitmix64(st) >> 11) * (1.0 / 9007199254740992.0);
-            const double thr = u * total;
-            double cum = 0.0;
-            int b = 0;
-            while (b < nb - 1 && cum + ph[b] < thr) cum += ph[b++];
-            const int b0 = b * kKppBlock, cntb = std::min(kKppBlock, n - b0);
-            VH_HIP(hipMemcpyAsync(blk.data(), mind.as<float>() + b0, cntb * sizeof(float), hipMemcpyDeviceToHost, s));
-            VH_HIP(hipStreamSynchronize(s));
-            idx = 0;
-            for (int i = 0; i < cntb; ++i) {
-                cum += blk[i];
-                if (cum >= thr) {
-                    idx = (size_t)(b0 + i);
-                    break;
-                }
-            }
-        }
-        VH_HIP(hipMemcpyAsync(cr + j * K->dpad, pts + idx * K->dpad, K->dpad * sizeof(float), hipMemcpyDeviceToDevice,
-                              s));
+        hipLaunchKernelGGL(k_kpp_select, dim3(1), dim3(kKppSelectThreads), 0, s, part.as<double>(), nb,
+                           mind.as<float>(), n, draws.as<uint64_t>(), (int)j, pts, (int)K->dpad, cr);
     }
-    VH_HIP(hipStreamSynchronize(s));
+    VH_HIP(hipGetLastError());
+    VH_HIP(hipStreamSynchronize(s));  // mind, part, draws and dh are released at return
     return km_set_centroids_dev(K, cr, k, K->dpad);
 }
 
