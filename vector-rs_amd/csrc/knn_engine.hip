@@ -76,6 +76,7 @@ struct vhip_knn {
     bool shifted = false;
     bool integral = false;    // every base value is an integer
     float err_coeff = 0.0f;   // selection error coefficient of the GEMM-form score
+    uint32_t *flags_host = nullptr;  // pinned, coherent: the flagged-query counts of the running search
     vh::DevBuf base8;  // packed Hamming on the fp4 matrix cores: one +1/-1 nibble per code bit
     bool ham8 = false;
     bool ham_wide = false;  // filter rounds may use the 1024-column fp4 kernel (codes <= 256 bits)
@@ -89,6 +90,7 @@ struct vhip_knn {
             (void)hipStreamSynchronize(stream);
             (void)hipStreamDestroy(stream);
         }
+        if (flags_host) (void)hipHostFree(flags_host);
     }
 };
 
@@ -117,7 +119,16 @@ struct Round {
 // (2 slower).
 constexpr int kRoundGrowth = 4;
 
-static std::vector<Round> plan_rounds(size_t n, size_t k, bool gemm, int dpad, int growth) {
+// Small batches (`small`: at most kSmallCols queries on the GEMM metrics) pay mostly for launches
+// and merges, not for scanned pairs: their first, dense round covers kSmallDenseRows rows (all of a
+// base of up to twice that), and the rest follows in one filter round when its expected passes per
+// query, k (n - seen) / seen, stay within a quarter of the candidate capacity, else in rounds growing
+// 16 times.  (1M rows at k = 10: 8,192 rows, then the other 991,808 with about 1,200 passes; at
+// k = 100 three rounds.)  A larger first round costs more in its merge (32,768 rows: 27 us against
+// about 12) than the fewer passes save.
+constexpr size_t kSmallDenseRows = 8192;
+
+static std::vector<Round> plan_rounds(size_t n, size_t k, bool gemm, int dpad, int growth, bool small = false) {
     std::vector<Round> r;
     if (n == 0) return r;
     const size_t kk = std::max<size_t>(k, 1);
@@ -125,11 +136,14 @@ static std::vector<Round> plan_rounds(size_t n, size_t k, bool gemm, int dpad, i
     // A base within the candidate capacity's floor (round_cap) is scored in one dense round: its
     // later rounds would cost more launches than rows (the IVF coarse probe: 1,024 centroids).
     if (n <= std::max<size_t>(2048, 32 * kk)) b0 = n;
+    if (small) b0 = n <= 2 * kSmallDenseRows ? n : std::max(b0, kSmallDenseRows);
     r.push_back({0, (long)b0, gemm, (long)kRowAlign, (long)kRowAlign});
     const int slots = gemm_slots(dpad);
+    const size_t cap_floor = std::max<size_t>({2048, 32 * kk, b0});
     size_t seen = b0;
     while (seen < n) {
-        const size_t e = std::min(n, round_up(seen * growth, kRowAlign));
+        size_t e = std::min(n, round_up(seen * growth, kRowAlign));
+        if (small) e = kk * (n - seen) / seen <= cap_floor / 4 ? n : std::min(n, round_up(seen * 16, kRowAlign));
         const size_t slot_item = std::max<size_t>(kRowAlign, (size_t)slots * seen / (3 * kk) / kRowAlign * kRowAlign);
         const size_t item = std::min<size_t>(8192, slot_item);
         r.push_back({(long)seen, (long)e, false, (long)item, (long)slot_item});
@@ -161,9 +175,9 @@ static long balanced_item(long cap_item, long rows, int n_ctiles, int wgs, long 
 // the ~3 k expected passes of a filter round.  A query that still overflows is re-run with a
 // capacity equal to the largest round.
 
-static int round_cap(size_t n, size_t k, bool gemm, int dpad) {
+static int round_cap(size_t n, size_t k, bool gemm, int dpad, bool small) {
     size_t cap = std::max<size_t>(2048, 32 * std::max<size_t>(k, 1));
-    for (const Round &r : plan_rounds(n, k, gemm, dpad, kRoundGrowth))
+    for (const Round &r : plan_rounds(n, k, gemm, dpad, kRoundGrowth, small))
         if (r.rb == 0) cap = std::max(cap, (size_t)(r.re - r.rb));
     return (int)round_up(cap, kRowAlign);
 }
@@ -321,24 +335,34 @@ static std::vector<Round> split_rounds(const std::vector<Round> &r, long max_row
     return out;
 }
 
+// The round plan of a search over nq queries: the small-batch plan for at most kSmallCols queries
+// on the GEMM metrics (not the direct-form re-runs).
+static bool small_plan(const vhip_knn *E, size_t nq, bool direct) {
+    return is_gemm_metric(E->metric) && !direct && !E->ham8 && small_batch((int)std::min<size_t>(nq, 1 << 20), (int)E->dpad);
+}
+
 // Runs all rounds for nq prepared queries; results stay in B.topk (row stride kc) / B.have.
 // `direct`: score squared L2 in direct form on the unshifted rows (VALU kernel) instead of the
 // engine's own scan; it serves the queries whose GEMM-form margin could not be certified.
+// `small`: the small-batch round plan (see plan_rounds; cap must be that plan's).
 // max_round_rows: see split_rounds.  `timed`: the scan launches feed the engine's kernel timer.
-static int run_rounds(vhip_knn *E, const QueryRows &Q, int nq, int k, int kc, int cap, bool direct, const RunBufs &B,
-                      long max_round_rows, bool timed) {
+static int run_rounds(vhip_knn *E, const QueryRows &Q, int nq, int k, int kc, int cap, bool direct, bool small,
+                      const RunBufs &B, long max_round_rows, bool timed) {
     hipStream_t s = E->stream;
-    launch_topk_init(nq, B.tau, B.have, B.cnt, B.flags, s);
-    launch_fill_u32(B.mflag, (size_t)nq, 0u, s);
-    launch_fill_u32(B.nflag, 2, 0u, s);
     const bool gemm = is_gemm_metric(E->metric) && !direct;
+    const std::vector<Round> rounds =
+        split_rounds(plan_rounds(E->n, (size_t)k, gemm, (int)E->dpad, kRoundGrowth, small), max_round_rows);
+    // the first round's candidate count: its rows when it is dense (every score is written)
+    const bool dense0 = !rounds.empty() && (rounds[0].dense || (E->ham8 && rounds[0].rb == 0));
+    launch_topk_init(nq, B.tau, B.have, B.cnt, B.flags, B.mflag, B.nflag,
+                     dense0 ? (uint32_t)(rounds[0].re - rounds[0].rb) : 0u, s);
     if (E->ham8) {
         // the queries' +1/-1 nibbles, rows padded to the 128-query tiles
         const size_t rows = round_up((size_t)nq, kTileCols);
         launch_ham_expand((const uint32_t *)Q.qpad, (size_t)nq, (int)E->dpad, (int)E->dpad, rows, false, B.q8, s);
     }
-    for (const Round &rd :
-         split_rounds(plan_rounds(E->n, (size_t)k, gemm, (int)E->dpad, kRoundGrowth), max_round_rows)) {
+    for (size_t ri = 0; ri < rounds.size(); ++ri) {
+        const Round &rd = rounds[ri];
         const long rb = rd.rb, re = rd.re;
         const bool dense = rd.dense || (E->ham8 && rb == 0);
         // Algorithmic work per launch: 2*Q*rows*D flops (GEMM metrics), Q*rows*D element
@@ -351,7 +375,7 @@ static int run_rounds(vhip_knn *E, const QueryRows &Q, int nq, int k, int kc, in
                                             : (double)nq * rows * (double)E->dim);
         const double bytes = E->ham8 ? (rows + nq) * (double)ham_mfma_row_bytes((int)E->dpad)  // expanded codes
                                      : rows * E->dim * 4.0 + (double)nq * E->dim * 4.0;
-        if (dense) launch_fill_u32(B.cnt, (size_t)nq, (uint32_t)(re - rb), s);
+        if (dense && ri > 0) launch_fill_u32(B.cnt, (size_t)nq, (uint32_t)(re - rb), s);
         const int t = (direct || !timed) ? -1 : E->timer.begin(s);
         // the narrow resident-tile kernel (gemm_narrow) works in 512-row stages on 32-column tiles
         const bool narrow = gemm && gemm_narrow((int)E->dpad);
@@ -380,7 +404,10 @@ static int run_rounds(vhip_knn *E, const QueryRows &Q, int nq, int k, int kc, in
                 launch_ham_mfma(dense, hitem, E->base8.as<int8_t>(), B.q8, (int)E->dpad, B.tau, nq, rb, re, B.cand,
                                 B.cnt, cap, E->grid_cap, s);
             }
-        } else if (gemm)
+        } else if (gemm && small_batch(nq, (int)E->dpad))
+            launch_small_scan(E->metric, rd.dense, E->base.as<float>(), E->norm.as<float>(), Q.qpad, Q.qnorm, B.tau,
+                              nq, (int)E->dpad, rb, re, B.cand, B.cnt, cap, E->grid_cap, s);
+        else if (gemm)
             launch_gemm_filter(E->metric, rd.dense, item, E->base.as<float>(), E->norm.as<float>(), Q.qpad, Q.qnorm,
                                B.tau, nq, (int)E->dpad, rb, re, B.cand, B.cnt, cap, E->norm_max, E->norm_min,
                                E->grid_cap, s);
@@ -395,18 +422,23 @@ static int run_rounds(vhip_knn *E, const QueryRows &Q, int nq, int k, int kc, in
                                B.cand, B.cnt, cap, E->grid_cap, s);
         if (t >= 0) E->timer.end(t, s, work, bytes);
         VH_HIP(hipGetLastError());
+        // the last round counts the standing margin flags into nflag[1]
+        const bool last = ri + 1 == rounds.size();
         launch_topk_merge(nq, k, kc, B.cand, B.cnt, cap, E->perm.as<uint32_t>(), B.topk, B.have, B.tau, B.flags,
-                          B.nflag, gemm ? Q.qerr : nullptr, B.mflag, s);
+                          B.nflag, gemm ? Q.qerr : nullptr, B.mflag, last && gemm ? B.nflag + 1 : nullptr,
+                          dense && re - rb > 4096, s);
         VH_HIP(hipGetLastError());
     }
     return VHIP_OK;
 }
 
-// Capacity of a candidate list that no round can overflow: the largest round's rows.
+// Capacity of a candidate list that no round can overflow: the largest round's rows, of either
+// round plan.
 static int full_cap(const vhip_knn *E, size_t k, bool gemm) {
     long big = k;
-    for (const Round &rd : plan_rounds(E->n, k, gemm, (int)E->dpad, kRoundGrowth))
-        big = std::max(big, rd.re - rd.rb);
+    for (int sm = 0; sm < 2; ++sm)
+        for (const Round &rd : plan_rounds(E->n, k, gemm, (int)E->dpad, kRoundGrowth, sm == 1))
+            big = std::max(big, rd.re - rd.rb);
     return (int)round_up((size_t)big, kRowAlign);
 }
 
@@ -484,7 +516,8 @@ static int rerun_queries(vhip_knn *E, const QueryRows &Q, const std::vector<uint
             F.qnorm = R.fn;
             F.qerr = Q.qerr ? R.fe : nullptr;
         }
-        VH_CHECK(run_rounds(E, F, m, k, kc_run, cap, direct, R.F, max_rows, fixed == nullptr));
+        VH_CHECK(run_rounds(E, F, m, k, kc_run, cap, direct, small_plan(E, per_batch, direct), R.F, max_rows,
+                            fixed == nullptr));
         launch_scatter_topk(R.F.topk, kc_run, R.F.have, direct ? nullptr : R.F.mflag, di, m, M.topk, kc, M.have,
                             M.mflag, s);
         VH_HIP(hipGetLastError());
@@ -512,25 +545,51 @@ static std::vector<uint32_t> flagged(const std::vector<uint32_t> &f) {
 //    unshifted rows, so every L2 result is the exact top-k of the direct-form distances.  (For dot
 //    product and cosine a direct-form pass rounds no better than the GEMM form, so a cut margin
 //    keeps the kc best by GEMM score: only near-ties within the error bound are affected.)
-static int search_prepared(vhip_knn *E, const QueryRows &Q, int nq, int k, int kc, int cap, const RunBufs &B,
-                           const Arena *fixed, int kout, uint32_t *d_ids, float *d_dist, uint32_t *d_dist_u32,
-                           int ostride) {
+// The counts of both kinds of flagged query come back to pinned host memory behind the final pass
+// (refine or finalize), so a batch with none, the usual case, waits once, at its end; a batch with
+// some waits for them, re-runs those queries and runs the final pass again.
+static int search_prepared(vhip_knn *E, const QueryRows &Q, int nq, int k, int kc, int cap, bool small,
+                           const RunBufs &B, const Arena *fixed, int kout, uint32_t *d_ids, float *d_dist,
+                           uint32_t *d_dist_u32, int ostride) {
     hipStream_t s = E->stream;
     const bool gemm = is_gemm_metric(E->metric);
-    VH_CHECK(run_rounds(E, Q, nq, k, kc, cap, false, B, 0, fixed == nullptr));
-    if (gemm) launch_count_flags(B.mflag, nq, B.nflag + 1, s);
-    uint32_t nf[2] = {0, 0};
-    VH_HIP(hipMemcpyAsync(nf, B.nflag, sizeof(nf), hipMemcpyDeviceToHost, s));
+    uint32_t *nfh = E->flags_host;
+    auto final_pass = [&](bool publish) -> int {
+        FlagPublish pub;
+        if (publish) {
+            pub.src = B.nflag;
+            pub.host = nfh;
+        }
+        if (gemm && d_dist)
+            launch_topk_refine(nq, k, kc, kout, E->metric, Q.qraw, direct_rows(E), E->inv_perm.as<uint32_t>(),
+                               (int)E->dpad, Q.qnorm, E->norm.as<float>(), B.topk, B.have, Q.qerr, d_ids, d_dist,
+                               ostride, pub, s);
+        else
+            launch_topk_finalize(nq, kc, kout, E->metric, B.topk, B.have, d_ids, d_dist, d_dist_u32, ostride, pub, s);
+        VH_HIP(hipGetLastError());
+        return VHIP_OK;
+    };
+    VH_CHECK(run_rounds(E, Q, nq, k, kc, cap, false, small, B, 0, fixed == nullptr));
+    volatile uint32_t *vn = nfh;
+    vn[0] = vn[1] = 0xffffffffu;  // overwritten by the final kernel
+    VH_CHECK(final_pass(true));
     VH_HIP(hipStreamSynchronize(s));
+    uint32_t nf[2] = {vn[0], vn[1]};
+    if (nf[0] == 0xffffffffu || nf[1] == 0xffffffffu)
+        return set_error(VHIP_ERR_DRIVER, "the search's flag counts did not reach the host");
+    if (!gemm) nf[1] = 0;
+    if (!nf[0] && !(nf[1] && E->metric == L2)) return VHIP_OK;
     const size_t slots = (size_t)nq * cap;
     if (nf[0]) {
         std::vector<uint32_t> f(nq);
         VH_HIP(hipMemcpy(f.data(), B.flags, nq * sizeof(uint32_t), hipMemcpyDeviceToHost));
         VH_CHECK(rerun_queries(E, Q, flagged(f), k, kc, false, B, fixed, B.cand, slots));
         if (gemm) {
+            uint32_t c = 0;
             launch_count_flags(B.mflag, nq, B.nflag + 1, s);
-            VH_HIP(hipMemcpyAsync(nf + 1, B.nflag + 1, sizeof(uint32_t), hipMemcpyDeviceToHost, s));
+            VH_HIP(hipMemcpyAsync(&c, B.nflag + 1, sizeof(uint32_t), hipMemcpyDeviceToHost, s));
             VH_HIP(hipStreamSynchronize(s));
+            nf[1] = c;
         }
     }
     if (nf[1] && E->metric == L2) {
@@ -538,14 +597,7 @@ static int search_prepared(vhip_knn *E, const QueryRows &Q, int nq, int k, int k
         VH_HIP(hipMemcpy(f.data(), B.mflag, nq * sizeof(uint32_t), hipMemcpyDeviceToHost));
         VH_CHECK(rerun_queries(E, Q, flagged(f), k, kc, true, B, fixed, B.cand, slots));
     }
-    if (gemm && d_dist)
-        launch_topk_refine(nq, k, kc, kout, E->metric, Q.qraw, direct_rows(E), E->inv_perm.as<uint32_t>(),
-                           (int)E->dpad, Q.qnorm, E->norm.as<float>(), B.topk, B.have, Q.qerr, d_ids, d_dist, ostride,
-                           s);
-    else
-        launch_topk_finalize(nq, kc, kout, E->metric, B.topk, B.have, d_ids, d_dist, d_dist_u32, ostride, s);
-    VH_HIP(hipGetLastError());
-    return VHIP_OK;
+    return final_pass(false);
 }
 
 static int check_search_args(vhip_knn *E, size_t k) {
@@ -583,6 +635,8 @@ static int engine_create(const void *base, size_t n, size_t dim, int metric, int
     E->grid_cap = device_grid_cap(ordinal);
     VH_HIP(hipStreamCreateWithFlags(&E->stream, hipStreamNonBlocking));
     VH_CHECK(E->stager.init(ordinal));
+    // coherent: the search's final kernel stores the flag counts here directly
+    VH_HIP(hipHostMalloc((void **)&E->flags_host, 2 * sizeof(uint32_t), hipHostMallocCoherent));
     if (n > 0) {
         VH_CHECK(build_row_order(E.get(), n, is_gemm_metric(metric)));
         DevBuf raw, flag;
@@ -711,8 +765,14 @@ static int engine_search_device(vhip_knn *E, const void *d_queries, size_t nq, s
     const bool gemm = is_gemm_metric(E->metric);
     const int kk = (int)ek;
     const int kc = gemm ? kk + margin_cap(kk) : kk;
-    const int cap = round_cap(E->n, ek, gemm, (int)E->dpad);
     size_t batch = std::min(nq, kQueryBatch);
+    // every batch of the call takes the plan its first does: the buffers are sized for that plan
+    bool small = small_plan(E, batch, false);
+    int cap = round_cap(E->n, ek, gemm, (int)E->dpad, small);
+    if (scratch && small && batch_bytes(E, batch, kc, cap, true) > scratch_bytes) {
+        small = false;
+        cap = round_cap(E->n, ek, gemm, (int)E->dpad, false);
+    }
     if (scratch) {
         // the largest batch whose buffers and re-run reserve fit the scratch region
         if (batch_bytes(E, 1, kc, cap, true) > scratch_bytes)
@@ -769,7 +829,7 @@ static int engine_search_device(vhip_knn *E, const void *d_queries, size_t nq, s
         launch_rows_prep(rp, E->stream);
         VH_HIP(hipGetLastError());
         const QueryRows Q{bm.qpad, bm.qnorm, bm.qerr, E->shifted ? bm.qraw : bm.qpad};
-        VH_CHECK(search_prepared(E, Q, m, kk, kc, cap, bm.B, scratch ? &reserve : nullptr, (int)k, d_ids + q0 * k,
+        VH_CHECK(search_prepared(E, Q, m, kk, kc, cap, small, bm.B, scratch ? &reserve : nullptr, (int)k, d_ids + q0 * k,
                                  d_dist ? d_dist + q0 * k : nullptr, d_dist_u32 ? d_dist_u32 + q0 * k : nullptr,
                                  (int)k));
     }

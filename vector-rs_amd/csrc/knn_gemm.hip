@@ -86,14 +86,27 @@ __global__ __launch_bounds__(256) void k_rows_prep(RowPrep a) {
         const float *row = a.in + src * (size_t)dim;
         float ss = 0.0f;
         bool whole = true;
-        for (int d = lane; d < dpad; d += 64) {
-            const float x = d < dim ? row[d] : 0.0f;
-            whole = whole && x == rintf(x);
-            if (rrow) rrow[d] = x;
-            float v = a.shift ? x - a.shift[d] : x;
-            if (a.transform) v = sqrtf(fabsf(v));
-            if (!a.normalize) orow[d] = v;
-            ss = fmaf(v, v, ss);
+        // four elements per lane in flight at a time (the loads first), the sum in the order d
+        for (int d0 = lane; d0 < dpad; d0 += 256) {
+            float xs[4], sh[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int d = d0 + 64 * u;
+                xs[u] = d < dim ? row[d] : 0.0f;
+                sh[u] = (a.shift && d < dpad) ? a.shift[d] : 0.0f;
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int d = d0 + 64 * u;
+                if (d >= dpad) break;
+                const float x = xs[u];
+                whole = whole && x == rintf(x);
+                if (rrow) rrow[d] = x;
+                float v = a.shift ? x - sh[u] : x;
+                if (a.transform) v = sqrtf(fabsf(v));
+                if (!a.normalize) orow[d] = v;
+                ss = fmaf(v, v, ss);
+            }
         }
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
@@ -101,10 +114,21 @@ __global__ __launch_bounds__(256) void k_rows_prep(RowPrep a) {
         if (a.normalize) {
             const float nr = sqrtf(ss);
             const float inv = nr > 0.0f ? 1.0f / nr : 0.0f;
-            for (int d = lane; d < dpad; d += 64) {
-                float v = d < dim ? row[d] : 0.0f;
-                if (a.transform) v = sqrtf(fabsf(v));
-                orow[d] = v * inv;
+            for (int d0 = lane; d0 < dpad; d0 += 256) {
+                float xs[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int d = d0 + 64 * u;
+                    xs[u] = d < dim ? row[d] : 0.0f;
+                }
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int d = d0 + 64 * u;
+                    if (d >= dpad) break;
+                    float v = xs[u];
+                    if (a.transform) v = sqrtf(fabsf(v));
+                    orow[d] = v * inv;
+                }
             }
         }
         if (lane == 0) {

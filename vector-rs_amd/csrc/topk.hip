@@ -15,14 +15,17 @@ namespace vh {
 
 typedef unsigned long long u64;
 
-__global__ void k_topk_init(int nq, float *tau, uint32_t *have, uint32_t *cnt, uint32_t *flags) {
+__global__ void k_topk_init(int nq, float *tau, uint32_t *have, uint32_t *cnt, uint32_t *flags, uint32_t *mflag,
+                            uint32_t *nflag, uint32_t cnt0) {
     const int q = blockIdx.x * blockDim.x + threadIdx.x;
     if (q < nq) {
         tau[q] = INFINITY;
         have[q] = 0;
-        cnt[q] = 0;
+        cnt[q] = cnt0;
         flags[q] = 0;
+        mflag[q] = 0;
     }
+    if (q < 2) nflag[q] = 0;
 }
 
 __global__ void k_fill_f32(float *p, size_t count, float v) {
@@ -47,9 +50,11 @@ void launch_fill_u32(uint32_t *p, size_t count, uint32_t v, hipStream_t s) {
     hipLaunchKernelGGL(k_fill_u32, dim3((unsigned)blocks), dim3(256), 0, s, p, count, v);
 }
 
-void launch_topk_init(int nq, float *tau, uint32_t *have, uint32_t *cnt, uint32_t *flags, hipStream_t s) {
+void launch_topk_init(int nq, float *tau, uint32_t *have, uint32_t *cnt, uint32_t *flags, uint32_t *mflag,
+                      uint32_t *nflag, uint32_t cnt0, hipStream_t s) {
     if (nq <= 0) return;
-    hipLaunchKernelGGL(k_topk_init, dim3(ceil_div(nq, 256)), dim3(256), 0, s, nq, tau, have, cnt, flags);
+    hipLaunchKernelGGL(k_topk_init, dim3(ceil_div(nq, 256)), dim3(256), 0, s, nq, tau, have, cnt, flags, mflag, nflag,
+                       cnt0);
 }
 
 // Bitonic sort of P (power of two) keys in LDS, ascending.  Must be called by all threads.
@@ -101,23 +106,32 @@ __device__ __forceinline__ uint32_t block_reduce_u32(uint32_t v, bool is_max, ui
     return v;
 }
 
-// buf holds `bufn` u64 entries (dynamic LDS, bufn >= 2 * pow2(kc), >= kMergeDirect).
-__global__ __launch_bounds__(256) void k_topk_merge(int k, int kc, int bufn, const uint2 *__restrict__ cand,
+// buf holds `bufn` u64 entries (dynamic LDS, bufn >= 2 * pow2(kc), >= kMergeDirect).  NT threads
+// per query: 256, or 1024 for a dense round of many rows, whose selection passes over all its
+// scores are latency-bound (each thread keeps four independent loads in flight).
+template <int NT>
+__global__ __launch_bounds__(NT) void k_topk_merge(int k, int kc, int bufn, const uint2 *__restrict__ cand,
                                                     uint32_t *__restrict__ cnt, int cap,
                                                     const uint32_t *__restrict__ perm, u64 *__restrict__ topk,
                                                     uint32_t *__restrict__ have, float *__restrict__ tau,
                                                     uint32_t *__restrict__ flags, uint32_t *__restrict__ nflagged,
-                                                    const float *__restrict__ qerr, uint32_t *__restrict__ mflag) {
+                                                    const float *__restrict__ qerr, uint32_t *__restrict__ mflag,
+                                                    uint32_t *__restrict__ mcount) {
     extern __shared__ u64 buf[];
     __shared__ uint32_t hist[kMergeBins];
-    __shared__ uint32_t red[8];
-    __shared__ uint32_t s_part[256];
+    __shared__ uint32_t red[2 * (NT / 64)];
+    __shared__ uint32_t s_part[NT];
     __shared__ uint32_t s_sel[4];  // boundary bucket, count below it, gather counters
     const int q = blockIdx.x, tid = threadIdx.x;
     const uint32_t c_all = cnt[q];
     if (flags[q] || c_all == 0) {
         __syncthreads();
-        if (tid == 0) cnt[q] = 0;
+        if (tid == 0) {
+            cnt[q] = 0;
+            // the last round counts the margin flags as they stand (an overflowed query is re-run
+            // and counted again afterwards)
+            if (mcount && !flags[q] && mflag[q]) atomicAdd(mcount, 1u);
+        }
         return;
     }
     // entries to keep: k, or kc when the scores carry a selection error
@@ -141,28 +155,41 @@ __global__ __launch_bounds__(256) void k_topk_merge(int k, int kc, int bufn, con
     if (T > (uint32_t)kMergeDirect && T > kk) {
         // ---- bucket select ----
         uint32_t lo = 0xffffffffu, hi = 0u;
-        for (uint32_t i = tid; i < T; i += 256) {
-            const uint32_t v = key32(i);
-            lo = min(lo, v);
-            hi = max(hi, v);
+        for (uint32_t i0 = tid; i0 < T; i0 += 4 * NT) {
+            uint32_t v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) v[u] = i0 + u * NT < T ? key32(i0 + u * NT) : 0u;
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                if (i0 + u * NT < T) {
+                    lo = min(lo, v[u]);
+                    hi = max(hi, v[u]);
+                }
         }
         lo = block_reduce_u32(lo, false, red);
-        hi = block_reduce_u32(hi, true, red + 4);
+        hi = block_reduce_u32(hi, true, red + NT / 64);
         if (lo < hi) {
             const float scale = (float)kMergeBins / ((float)(hi - lo) + 1.0f);
             auto bucket = [&](uint32_t v) { return min(kMergeBins - 1, (int)((float)(v - lo) * scale)); };
-            for (int i = tid; i < kMergeBins; i += 256) hist[i] = 0;
+            for (int i = tid; i < kMergeBins; i += NT) hist[i] = 0;
             __syncthreads();
-            for (uint32_t i = tid; i < T; i += 256) atomicAdd(&hist[bucket(key32(i))], 1u);
+            for (uint32_t i0 = tid; i0 < T; i0 += 4 * NT) {
+                uint32_t v[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) v[u] = i0 + u * NT < T ? key32(i0 + u * NT) : 0u;
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    if (i0 + u * NT < T) atomicAdd(&hist[bucket(v[u])], 1u);
+            }
             __syncthreads();
             // bucket b* holding the kk-th smallest: cum(b*) < kk <= cum(b*) + hist[b*]
-            constexpr int per = kMergeBins / 256;
+            constexpr int per = kMergeBins / NT;
             uint32_t loc = 0;
 #pragma unroll
             for (int j = 0; j < per; ++j) loc += hist[tid * per + j];
             s_part[tid] = loc;
             __syncthreads();
-            for (int o = 1; o < 256; o <<= 1) {
+            for (int o = 1; o < NT; o <<= 1) {
                 const uint32_t v = tid >= o ? s_part[tid - o] : 0u;
                 __syncthreads();
                 s_part[tid] += v;
@@ -187,15 +214,23 @@ __global__ __launch_bounds__(256) void k_topk_merge(int k, int kc, int bufn, con
             const uint32_t below = s_sel[1];
             const uint32_t inb = hist[bstar];
             if (below + inb <= (uint32_t)bufn) {
-                for (uint32_t i = tid; i < T; i += 256) {
-                    const int b = bucket(key32(i));
-                    if (b < bstar) buf[atomicAdd(&s_sel[2], 1u)] = key64(i);
-                    else if (b == bstar) buf[below + atomicAdd(&s_sel[3], 1u)] = key64(i);
+                for (uint32_t i0 = tid; i0 < T; i0 += 4 * NT) {
+                    uint32_t v[4];
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) v[u] = i0 + u * NT < T ? key32(i0 + u * NT) : 0xffffffffu;
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        const uint32_t i = i0 + u * NT;
+                        if (i >= T) continue;
+                        const int b = bucket(v[u]);
+                        if (b < bstar) buf[atomicAdd(&s_sel[2], 1u)] = key64(i);
+                        else if (b == bstar) buf[below + atomicAdd(&s_sel[3], 1u)] = key64(i);
+                    }
                 }
                 const uint32_t total = below + inb;
                 int P = 2;
                 while ((uint32_t)P < total) P <<= 1;
-                for (uint32_t i = total + tid; i < (uint32_t)P; i += 256) buf[i] = ~0ull;
+                for (uint32_t i = total + tid; i < (uint32_t)P; i += NT) buf[i] = ~0ull;
                 __syncthreads();
                 bitonic_sort_lds(buf, P);
                 hn = kk;
@@ -208,11 +243,11 @@ __global__ __launch_bounds__(256) void k_topk_merge(int k, int kc, int bufn, con
         uint32_t hh = 0, next = 0;
         while (next < T || hh == 0) {
             const uint32_t take = min(T - next, (uint32_t)bufn - hh);
-            for (uint32_t i = tid; i < take; i += 256) buf[hh + i] = key64(next + i);
+            for (uint32_t i = tid; i < take; i += NT) buf[hh + i] = key64(next + i);
             const uint32_t total = hh + take;
             int P = 2;
             while ((uint32_t)P < total) P <<= 1;
-            for (uint32_t i = total + tid; i < (uint32_t)P; i += 256) buf[i] = ~0ull;
+            for (uint32_t i = total + tid; i < (uint32_t)P; i += NT) buf[i] = ~0ull;
             __syncthreads();
             bitonic_sort_lds(buf, P);
             hh = min(total, kk);
@@ -222,7 +257,7 @@ __global__ __launch_bounds__(256) void k_topk_merge(int k, int kc, int bufn, con
         hn = hh;
     }
     __syncthreads();
-    for (uint32_t i = tid; i < hn; i += 256) tk[i] = buf[i];
+    for (uint32_t i = tid; i < hn; i += NT) tk[i] = buf[i];
     if (tid == 0) {
         have[q] = hn;
         cnt[q] = 0;
@@ -249,6 +284,7 @@ __global__ __launch_bounds__(256) void k_topk_merge(int k, int kc, int bufn, con
             // a NaN k-th score (fewer than k rows with a finite score so far) filters nothing yet
             tau[q] = t == t ? t : INFINITY;
             if (mflag) mflag[q] = cut ? 1u : 0u;
+            if (mcount && cut) atomicAdd(mcount, 1u);
         }
     }
 }
@@ -259,22 +295,34 @@ int merge_buffer_entries(int kc) {
     return std::max(2 * p, 1024);
 }
 
-void launch_topk_merge(int nq, int k, int kc, const uint2 *cand, uint32_t *cnt, int cap, const uint32_t *perm,
-                       unsigned long long *topk, uint32_t *have, float *tau, uint32_t *flags, uint32_t *nflagged,
-                       const float *qerr, uint32_t *mflag, hipStream_t s) {
-    if (nq <= 0) return;
+template <int NT>
+static void launch_merge_nt(int nq, int k, int kc, const uint2 *cand, uint32_t *cnt, int cap, const uint32_t *perm,
+                            unsigned long long *topk, uint32_t *have, float *tau, uint32_t *flags, uint32_t *nflagged,
+                            const float *qerr, uint32_t *mflag, uint32_t *mcount, hipStream_t s) {
     const int bufn = merge_buffer_entries(kc);
     const size_t lds = (size_t)bufn * sizeof(u64);
     static bool attr_set = false;
     if (!attr_set && lds > 65536) {
         // more than 64 KB of dynamic LDS (gfx950 offers 160 KB per workgroup)
-        (void)hipFuncSetAttribute((const void *)k_topk_merge, hipFuncAttributeMaxDynamicSharedMemorySize,
+        (void)hipFuncSetAttribute((const void *)k_topk_merge<NT>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                   (int)(merge_buffer_entries(kMaxKeep) * sizeof(u64)));
         (void)hipGetLastError();
         attr_set = true;
     }
-    hipLaunchKernelGGL(k_topk_merge, dim3(nq), dim3(256), lds, s, k, kc, bufn, cand, cnt, cap, perm, topk, have, tau,
-                       flags, nflagged, qerr, mflag);
+    hipLaunchKernelGGL(k_topk_merge<NT>, dim3(nq), dim3(NT), lds, s, k, kc, bufn, cand, cnt, cap, perm, topk, have,
+                       tau, flags, nflagged, qerr, mflag, mcount);
+}
+
+void launch_topk_merge(int nq, int k, int kc, const uint2 *cand, uint32_t *cnt, int cap, const uint32_t *perm,
+                       unsigned long long *topk, uint32_t *have, float *tau, uint32_t *flags, uint32_t *nflagged,
+                       const float *qerr, uint32_t *mflag, uint32_t *mcount, bool wide, hipStream_t s) {
+    if (nq <= 0) return;
+    if (wide)
+        launch_merge_nt<1024>(nq, k, kc, cand, cnt, cap, perm, topk, have, tau, flags, nflagged, qerr, mflag, mcount,
+                              s);
+    else
+        launch_merge_nt<256>(nq, k, kc, cand, cnt, cap, perm, topk, have, tau, flags, nflagged, qerr, mflag, mcount,
+                             s);
 }
 
 __global__ void k_count_flags(const uint32_t *__restrict__ flags, int n, uint32_t *__restrict__ count) {
@@ -333,10 +381,22 @@ void launch_gather_rows(const float *src, const uint32_t *idx, size_t rows, int 
     hipLaunchKernelGGL(k_gather_rows, dim3(blocks), dim3(256), 0, s, src, idx, rows, width, dst);
 }
 
+// The search's two flag counters (device) copied to pinned host memory by one thread of the final
+// kernel, with a system-scope release, so that the host reads them after the stream's sync with no
+// copy of their own.
+__device__ __forceinline__ void publish_flags(const FlagPublish &p) {
+    if (p.host) {
+        __hip_atomic_store(p.host, p.src[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        __hip_atomic_store(p.host + 1, p.src[1], __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+}
+
 __global__ void k_topk_finalize(int nq, int kc, int kout, int metric, const u64 *__restrict__ topk,
                                 const uint32_t *__restrict__ have, uint32_t *__restrict__ out_ids,
-                                float *__restrict__ out_dist, uint32_t *__restrict__ out_dist_u32, int ostride) {
+                                float *__restrict__ out_dist, uint32_t *__restrict__ out_dist_u32, int ostride,
+                                FlagPublish pub) {
     const long i = blockIdx.x * (long)blockDim.x + threadIdx.x;
+    if (i == 0) publish_flags(pub);
     if (i >= (long)nq * kout) return;
     const int q = (int)(i / kout), j = (int)(i % kout);
     const size_t o = (size_t)q * ostride + j;
@@ -356,11 +416,10 @@ __global__ void k_topk_finalize(int nq, int kc, int kout, int metric, const u64 
 
 void launch_topk_finalize(int nq, int kc, int kout, int metric, const unsigned long long *topk,
                           const uint32_t *have, uint32_t *out_ids, float *out_dist, uint32_t *out_dist_u32,
-                          int ostride, hipStream_t s) {
-    const long total = (long)nq * kout;
-    if (total <= 0) return;
+                          int ostride, const FlagPublish &pub, hipStream_t s) {
+    const long total = std::max((long)nq * kout, 1L);
     hipLaunchKernelGGL(k_topk_finalize, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, nq, kc, kout, metric,
-                       topk, have, out_ids, out_dist, out_dist_u32, ostride);
+                       topk, have, out_ids, out_dist, out_dist_u32, ostride, pub);
 }
 
 // Final pass for the GEMM-form metrics.  The selection used the GEMM-form score (the norm form
@@ -380,8 +439,9 @@ __global__ __launch_bounds__(256) void k_topk_refine(int k, int kc, int kout, in
                                                      const float *__restrict__ qnorm, const float *__restrict__ bnorm,
                                                      const u64 *__restrict__ topk, const uint32_t *__restrict__ have,
                                                      const float *__restrict__ qerr, uint32_t *__restrict__ out_ids,
-                                                     float *__restrict__ out_dist, int ostride) {
+                                                     float *__restrict__ out_dist, int ostride, FlagPublish pub) {
     __shared__ u64 buf[2 * kMaxK];  // a power of two >= kMaxKeep
+    if (blockIdx.x == 0 && threadIdx.x == 0) publish_flags(pub);
     __shared__ uint32_t s_row[kMaxKeep];
     __shared__ int s_h;
     const int q = blockIdx.x, tid = threadIdx.x;
@@ -466,10 +526,10 @@ __global__ __launch_bounds__(256) void k_topk_refine(int k, int kc, int kout, in
 void launch_topk_refine(int nq, int k, int kc, int kout, int metric, const float *qrows, const float *base,
                         const uint32_t *inv_perm, int dpad, const float *qnorm, const float *bnorm,
                         const unsigned long long *topk, const uint32_t *have, const float *qerr, uint32_t *out_ids,
-                        float *out_dist, int ostride, hipStream_t s) {
+                        float *out_dist, int ostride, const FlagPublish &pub, hipStream_t s) {
     if (nq <= 0) return;
     hipLaunchKernelGGL(k_topk_refine, dim3(nq), dim3(256), 0, s, k, kc, kout, metric, qrows, base, inv_perm, dpad,
-                       qnorm, bnorm, topk, have, qerr, out_ids, out_dist, ostride);
+                       qnorm, bnorm, topk, have, qerr, out_ids, out_dist, ostride, pub);
 }
 
 }  // namespace vh

@@ -30,6 +30,11 @@ inline int gemm_slots(int dpad) {
     return dpad <= 128 ? kGemmSlotsReg
                        : (gemm_narrow(dpad) ? kGemmSlotsNarrow : (dpad % 128 == 0 ? kGemmSlotsPanel : kGemmSlotsStream));
 }
+// Batches of at most kSmallCols queries (one 32-query tile) with rows of at most kSmallMaxDpad
+// floats take the small-batch MFMA scan (knn_small.hip), which spreads every round over all CUs.
+constexpr int kSmallCols = 32;
+constexpr int kSmallMaxDpad = 1024;
+inline bool small_batch(int nq, int dpad) { return nq <= kSmallCols && dpad <= kSmallMaxDpad; }
 constexpr int kRowAlign = 256;       // row counts of MFMA row operands and round boundaries
                                      // are multiples of this (the largest MFMA stage)
 
@@ -167,6 +172,11 @@ void launch_gemm_filter(int metric, bool dense, long item_rows, const float *bas
                         const float *qry, const float *qnorm, const float *tau, int nq, int dpad, long row_begin,
                         long row_end, uint2 *cand, uint32_t *cnt, int cap, float anorm_max, float anorm_min,
                         int grid_cap, hipStream_t s);
+// The same round for a small batch (small_batch(nq, dpad)): one wave per 32-row block against the
+// batch's 32-query tile, DENSE or FILTER as above, squared L2, dot product or cosine.
+void launch_small_scan(int metric, bool dense, const float *base, const float *bnorm, const float *qry,
+                       const float *qnorm, const float *tau, int nq, int dpad, long row_begin, long row_end,
+                       uint2 *cand, uint32_t *cnt, int cap, int grid_cap, hipStream_t s);
 
 // Certification of the MFMA k-means assignment: each point's best score must beat its second
 // best by more than twice the point's selection error bound (err_coeff times the norms, with
@@ -191,15 +201,27 @@ void launch_kmeans_assign(int metric, const float *cent, const float *cnorm, int
                           int32_t *counts, const AssignCert &cert, int grid_cap, hipStream_t s);
 
 // topk.hip
-void launch_topk_init(int nq, float *tau, uint32_t *have, uint32_t *cnt, uint32_t *flags, hipStream_t s);
+// Resets a run's per-query state: tau = +inf, have = flags = mflag = 0, cnt = cnt0 (the first
+// round's rows when that round is dense), and the two flag counters.
+void launch_topk_init(int nq, float *tau, uint32_t *have, uint32_t *cnt, uint32_t *flags, uint32_t *mflag,
+                      uint32_t *nflag, uint32_t cnt0, hipStream_t s);
 // Merges each query's candidates into its running best entries (row stride kc of topk).  A query
 // with qerr[q] > 0 (qerr may be null: all 0) keeps its kc best entries and filters later rounds at
 // tau = min(kc-th score, k-th score + 2 qerr[q]), so the final entries hold every row whose score
 // lies within 2 qerr of the k-th; mflag[q] (may be null) is set when that margin may have been cut
-// by the capacity kc.  Others keep k entries and filter at the k-th score.
+// by the capacity kc.  Others keep k entries and filter at the k-th score.  mcount (non-null in a
+// run's last round only): incremented once per query whose margin flag stands at the end of the
+// round, overflowed queries excepted.  wide: 1024 threads per query instead of 256 (a dense round
+// of many rows).
 void launch_topk_merge(int nq, int k, int kc, const uint2 *cand, uint32_t *cnt, int cap, const uint32_t *perm,
                        unsigned long long *topk, uint32_t *have, float *tau, uint32_t *flags, uint32_t *nflagged,
-                       const float *qerr, uint32_t *mflag, hipStream_t s);
+                       const float *qerr, uint32_t *mflag, uint32_t *mcount, bool wide, hipStream_t s);
+// Where the final kernel of a search (refine or finalize) copies the two flag counters src[0..1]:
+// host = pinned host memory, or null for no copy.
+struct FlagPublish {
+    const uint32_t *src = nullptr;
+    uint32_t *host = nullptr;
+};
 // Writes results: out_ids[q*ostride + j], out_dist[...] for j < have[q]; distance is the
 // metric value recovered from the score (negated for similarities, transformed for
 // Minkowski / Mahalanobis / Hellinger).  Entries past have[q] are set to UINT32_MAX / NaN.
@@ -207,7 +229,7 @@ void launch_topk_merge(int nq, int k, int kc, const uint2 *cand, uint32_t *cnt, 
 // query (kout may exceed k when k was clamped to the number of base rows).
 void launch_topk_finalize(int nq, int kc, int kout, int metric, const unsigned long long *topk,
                           const uint32_t *have, uint32_t *out_ids, float *out_dist, uint32_t *out_dist_u32,
-                          int ostride, hipStream_t s);
+                          int ostride, const FlagPublish &pub, hipStream_t s);
 // GEMM metrics: recompute the kept distances in direct form, re-sort by (distance, id) and
 // write the best k (same output contract as launch_topk_finalize; out_dist required).  Entries
 // past the k-th count only when their GEMM-form score is within 2 qerr[q] of the k-th.  `qrows` /
@@ -216,7 +238,7 @@ void launch_topk_finalize(int nq, int kc, int kout, int metric, const unsigned l
 void launch_topk_refine(int nq, int k, int kc, int kout, int metric, const float *qrows, const float *base,
                         const uint32_t *inv_perm, int dpad, const float *qnorm, const float *bnorm,
                         const unsigned long long *topk, const uint32_t *have, const float *qerr, uint32_t *out_ids,
-                        float *out_dist, int ostride, hipStream_t s);
+                        float *out_dist, int ostride, const FlagPublish &pub, hipStream_t s);
 // Number of nonzero flags among flags[0, n) into *count (device).
 void launch_count_flags(const uint32_t *flags, int n, uint32_t *count, hipStream_t s);
 // Copies the kept entries of re-run queries (row r, stride ks) back to rows idx[r] (stride kd)
