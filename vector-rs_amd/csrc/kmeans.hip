@@ -386,20 +386,50 @@ __global__ __launch_bounds__(256) void k_coarse_score(const float *__restrict__ 
 }
 
 // Seeded k-means++ on the device (CudaKMeansEngine::init_random, kmeans.rs:409-460).  Each step
-// is two launches on the state's stream, with no host round trip:
+// is three launches on the state's stream, with no host round trip:
+//  * k_kpp_dcc: the squared distance from the newest centre to every earlier one;
 //  * k_kpp_update: mind[i] = min(mind[i], ||x_i - c||^2) for the newest centre c, in direct form,
-//    and the sum of mind over each block of kKppBlock points (double, fixed tree order).  Eight
-//    lanes share a row (each a 16-byte column slice), so every load instruction of a wave reads
-//    eight whole 128-byte row pieces: the pass streams the points at HBM rate.
+//    and the sum of mind over each block of kKppBlock points (double, fixed tree order).  A point
+//    whose nearest centre so far, a = near[i], lies at ||c_a - c||^2 >= 4 mind[i] (1 + margin)
+//    from c cannot come closer to c (triangle inequality: ||x - c|| >= ||c_a - c|| - ||x - c_a||
+//    >= ||x - c_a||), so its row is not read; the margin covers the rounding of all three computed
+//    squared distances, so the values of mind are exactly those of the unpruned pass.  Eight lanes
+//    share a row (each a 16-byte column slice), so each load instruction of a wave reads eight
+//    whole 128-byte row pieces;
 //  * k_kpp_select: one workgroup draws the next centre with probability mind[i] / sum(mind), as
 //    the reference's linear scan does (the first i whose running sum reaches u * total), through
 //    the block sums and then the chosen block's values, and copies that point into the centres.
 // Both sums are in a fixed order, so a seed gives the same centres on every run.
-constexpr int kKppBlock = 1024;       // points per k_kpp_update block (256 threads)
+constexpr int kKppBlock = 1024;          // points per k_kpp_update block (256 threads)
 constexpr int kKppSelectThreads = 1024;  // equal to kKppBlock: the select reads a block one value per thread
 
+__global__ __launch_bounds__(256) void k_kpp_dcc(const float *__restrict__ cent, int dpad, int m,
+                                                 float *__restrict__ dcc) {
+    extern __shared__ float4 s_c[];  // centre m, dpad / 4 float4
+    const int nc4 = dpad >> 2;
+    const float4 *cm = (const float4 *)(cent + (size_t)m * dpad);
+    for (int i = threadIdx.x; i < nc4; i += 256) s_c[i] = cm[i];
+    __syncthreads();
+    const int a = blockIdx.x * 256 + threadIdx.x;
+    if (a >= m) return;
+    const float4 *ca = (const float4 *)(cent + (size_t)a * dpad);
+    float d2 = 0.0f;
+    for (int j = 0; j < nc4; ++j) {
+        const float4 x = ca[j], c = s_c[j];
+        const float a0 = x.x - c.x, a1 = x.y - c.y, a2 = x.z - c.z, a3 = x.w - c.w;
+        d2 = fmaf(a0, a0, d2);
+        d2 = fmaf(a1, a1, d2);
+        d2 = fmaf(a2, a2, d2);
+        d2 = fmaf(a3, a3, d2);
+    }
+    dcc[a] = d2;
+}
+
+// cidx: the newest centre's index (its row is c); prune: 4 (1 + margin), or 0 for no pruning.
 __global__ __launch_bounds__(256) void k_kpp_update(const float *__restrict__ pts, int dpad, int n,
-                                                    const float *__restrict__ c, float *__restrict__ mind,
+                                                    const float *__restrict__ c, int cidx,
+                                                    float *__restrict__ mind, int32_t *__restrict__ near,
+                                                    const float *__restrict__ dcc, float prune,
                                                     double *__restrict__ partial) {
     extern __shared__ float4 s_c[];  // the centre, dpad / 4 float4
     __shared__ double red[256];
@@ -413,16 +443,22 @@ __global__ __launch_bounds__(256) void k_kpp_update(const float *__restrict__ pt
     double s = 0.0;
     constexpr int G = 4;  // groups of 8 rows in flight per wave
     for (int r0 = b0 + (lane >> 3); r0 < b1; r0 += 8 * G) {
-        float d2[G];
+        float m[G], d2[G];
+        bool need[G];
 #pragma unroll
-        for (int g = 0; g < G; ++g) d2[g] = 0.0f;
+        for (int g = 0; g < G; ++g) {
+            const int r = r0 + 8 * g;
+            m[g] = r < b1 ? mind[r] : 0.0f;
+            const int a = r < b1 ? near[r] : -1;
+            need[g] = r < b1 && !(a >= 0 && dcc[a] >= prune * m[g]);
+            d2[g] = 0.0f;
+        }
         for (int j = part; j < nc4; j += 8) {
             const float4 cv = s_c[j];
 #pragma unroll
             for (int g = 0; g < G; ++g) {
-                const int r = r0 + 8 * g;
-                if (r < b1) {
-                    const float4 xv = ((const float4 *)(pts + (size_t)r * dpad))[j];
+                if (need[g]) {
+                    const float4 xv = ((const float4 *)(pts + (size_t)(r0 + 8 * g) * dpad))[j];
                     const float a0 = xv.x - cv.x, a1 = xv.y - cv.y, a2 = xv.z - cv.z, a3 = xv.w - cv.w;
                     d2[g] = fmaf(a0, a0, d2[g]);
                     d2[g] = fmaf(a1, a1, d2[g]);
@@ -439,9 +475,12 @@ __global__ __launch_bounds__(256) void k_kpp_update(const float *__restrict__ pt
             v += __shfl_xor(v, 4, 64);
             const int r = r0 + 8 * g;
             if (part == 0 && r < b1) {
-                const float m = fminf(mind[r], v);
-                mind[r] = m;
-                s += (double)m;
+                if (need[g] && v < m[g]) {
+                    m[g] = v;
+                    mind[r] = v;
+                    near[r] = cidx;
+                }
+                s += (double)m[g];
             }
         }
     }
@@ -454,39 +493,39 @@ __global__ __launch_bounds__(256) void k_kpp_update(const float *__restrict__ pt
     if (threadIdx.x == 0) partial[blockIdx.x] = red[0];
 }
 
-// Inclusive prefix sum of one double per thread over the workgroup (kKppSelectThreads), in a
-// fixed order; `tmp` holds kKppSelectThreads doubles.
+// Inclusive prefix sum of one double per thread over the workgroup (kKppSelectThreads threads), in
+// a fixed order: within each wave by shuffles, then the wave totals; `tmp` holds 16 doubles.
 __device__ __forceinline__ double block_scan_incl(double v, double *tmp) {
-    const int t = threadIdx.x;
-    tmp[t] = v;
-    __syncthreads();
-    for (int o = 1; o < kKppSelectThreads; o <<= 1) {
-        const double a = t >= o ? tmp[t - o] : 0.0;
-        __syncthreads();
-        v += a;
-        tmp[t] = v;
-        __syncthreads();
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const double a = __shfl_up(v, o, 64);
+        if (lane >= o) v += a;
     }
-    return v;
+    __syncthreads();  // tmp is free (an earlier scan's readers are done)
+    if (lane == 63) tmp[w] = v;
+    __syncthreads();
+    double before = 0.0;
+    for (int i = 0; i < w; ++i) before += tmp[i];
+    return before + v;
 }
 
 // Step j's draw.  draw: the step's 64-bit random value.  A total weight of at most 1e-6 (every
 // point on a centre) takes draw mod n, as the reference takes a uniform index there.  Otherwise
 // the threshold is u * total with u = the draw's top 53 bits in [0, 1), and the centre is the
 // first point of positive weight whose running sum of mind reaches it: the first run of blocks,
-// then block, then point, at which the running sum reaches the threshold.  Running sums of
-// non-negative values never decrease, and the last run's sum is the total itself, so a run is
-// always found; should the sequential sums inside it round short of the threshold, its last block
-// (point) of positive weight is taken.  Every choice is a minimum or maximum over the threads, so
-// the result does not depend on their timing.
+// then block, then point, at which the running sum reaches the threshold.  Should rounding leave
+// the running sums short of a threshold near the total, the last run (block, point) of positive
+// weight is taken.  Every choice is a minimum or maximum over the threads, so the result does not
+// depend on their timing.
 __global__ __launch_bounds__(kKppSelectThreads) void k_kpp_select(const double *__restrict__ partial, int nb,
                                                                   const float *__restrict__ mind, int n,
                                                                   const uint64_t *__restrict__ draws, int j,
                                                                   const float *__restrict__ pts, int dpad,
                                                                   float *__restrict__ cent) {
-    __shared__ double tmp[kKppSelectThreads];
-    __shared__ int s_run, s_blk, s_pt, s_last;
-    __shared__ double s_before;
+    __shared__ double tmp[kKppSelectThreads / 64];
+    __shared__ int s_run, s_lastrun, s_blk, s_pt, s_last;
+    __shared__ double s_before, s_total;
     const int t = threadIdx.x;
     const uint64_t draw = draws[j];
     // block sums: thread t owns a contiguous run of them
@@ -495,22 +534,29 @@ __global__ __launch_bounds__(kKppSelectThreads) void k_kpp_select(const double *
     double own = 0.0;
     for (int b = c0; b < c1; ++b) own += partial[b];
     const double incl = block_scan_incl(own, tmp);
-    const double excl = t > 0 ? tmp[t - 1] : 0.0;
-    const double total = tmp[kKppSelectThreads - 1];
+    const double excl = incl - own;  // unused for runs of no weight
+    if (t == kKppSelectThreads - 1) s_total = incl;
     if (t == 0) {
         s_run = kKppSelectThreads;
+        s_lastrun = -1;
         s_pt = 0x7fffffff;
         s_last = -1;
     }
     __syncthreads();
+    const double total = s_total;
     int idx;
     if (total <= 1e-6) {
         idx = (int)(draw % (uint64_t)n);
     } else {
         const double thr = (double)(draw >> 11) * (1.0 / 9007199254740992.0) * total;
-        if (own > 0.0 && incl >= thr) atomicMin(&s_run, t);
+        if (own > 0.0) {
+            if (incl >= thr) atomicMin(&s_run, t);
+            atomicMax(&s_lastrun, t);
+        }
         __syncthreads();
-        if (t == s_run) {
+        // the scan's rounding may leave every run of weight short of a threshold near the total:
+        // then the last run of weight
+        if (t == (s_run < kKppSelectThreads ? s_run : s_lastrun)) {
             double cum = excl, cum_last = excl;
             int pb = -1, lastb = -1;
             for (int b = c0; b < c1; ++b) {
@@ -819,34 +865,45 @@ static int km_total_inertia(vhip_kmeans *K, float *out) {
 // Seeded k-means++ (kmeans.rs:409-460): first centre uniform, then each next centre drawn
 // with probability proportional to the squared L2 distance to the nearest chosen centre.  The
 // draws (one 64-bit splitmix64 value per centre) are made on the host up front; every step then
-// runs on the device (k_kpp_update + k_kpp_select), with no host round trip.
+// runs on the device (k_kpp_dcc, k_kpp_update, k_kpp_select), with no host round trip.
 static int km_init_kmeanspp(vhip_kmeans *K, size_t k, uint64_t seed) {
     hipStream_t s = K->stream;
     const int n = (int)K->n;
     VH_CHECK(K->craw.ensure(K->dev, k * K->dpad * sizeof(float)));
     const float *pts = K->points();
     float *cr = K->craw.as<float>();
-    DevBuf mind, part, draws;
+    DevBuf mind, near, part, draws, dcc;
     const int nb = ceil_div(n, kKppBlock);
     VH_CHECK(mind.ensure(K->dev, (size_t)n * sizeof(float)));
+    VH_CHECK(near.ensure(K->dev, (size_t)n * sizeof(int32_t)));
     VH_CHECK(part.ensure(K->dev, (size_t)nb * sizeof(double)));
     VH_CHECK(draws.ensure(K->dev, k * sizeof(uint64_t)));
+    VH_CHECK(dcc.ensure(K->dev, k * sizeof(float)));
     std::vector<uint64_t> dh(k);
     uint64_t st = seed;
     for (size_t j = 0; j < k; ++j) dh[j] = splitmix64(st);
     VH_HIP(hipMemcpyAsync(draws.p, dh.data(), k * sizeof(uint64_t), hipMemcpyHostToDevice, s));
     hipLaunchKernelGGL(k_fill, dim3(ceil_div(n, 256)), dim3(256), 0, s, mind.as<float>(), (size_t)n, 3.4028235e38f);
+    launch_fill_u32((uint32_t *)near.as<int32_t>(), (size_t)n, 0xffffffffu, s);
     const size_t idx = dh[0] % (size_t)n;
     VH_HIP(hipMemcpyAsync(cr, pts + idx * K->dpad, K->dpad * sizeof(float), hipMemcpyDeviceToDevice, s));
+    // Pruning factor 4 (1 + 64 g), g = gamma_{dpad+2}: each of the three computed squared
+    // distances (the centres', the point's to its nearest, the point's to the new centre) is
+    // within a factor (1 +- g) of its value, and (1 + 64 g) leaves room for all three.
+    const float prune = (float)(4.0 * (1.0 + 64.0 * gamma_n((double)K->dpad + 2.0)));
     const size_t lds = K->dpad * sizeof(float);
     for (size_t j = 1; j < k; ++j) {
-        hipLaunchKernelGGL(k_kpp_update, dim3(nb), dim3(256), lds, s, pts, (int)K->dpad, n, cr + (j - 1) * K->dpad,
-                           mind.as<float>(), part.as<double>());
+        const int m = (int)j - 1;  // the newest centre
+        if (m > 0)
+            hipLaunchKernelGGL(k_kpp_dcc, dim3(ceil_div(m, 256)), dim3(256), lds, s, cr, (int)K->dpad, m,
+                               dcc.as<float>());
+        hipLaunchKernelGGL(k_kpp_update, dim3(nb), dim3(256), lds, s, pts, (int)K->dpad, n, cr + (size_t)m * K->dpad, m,
+                           mind.as<float>(), near.as<int32_t>(), dcc.as<float>(), prune, part.as<double>());
         hipLaunchKernelGGL(k_kpp_select, dim3(1), dim3(kKppSelectThreads), 0, s, part.as<double>(), nb,
                            mind.as<float>(), n, draws.as<uint64_t>(), (int)j, pts, (int)K->dpad, cr);
     }
     VH_HIP(hipGetLastError());
-    VH_HIP(hipStreamSynchronize(s));  // mind, part, draws and dh are released at return
+    VH_HIP(hipStreamSynchronize(s));  // mind, near, part, draws, dcc and dh are released at return
     return km_set_centroids_dev(K, cr, k, K->dpad);
 }
 
