@@ -54,6 +54,17 @@ __device__ __forceinline__ void accum(float &a, float &b, float q, float x) {
     }
 }
 
+// Two consecutive elements; L-inf takes both in one max of three (|.| source modifiers).
+template <int M>
+__device__ __forceinline__ void accum2(float &a, float &b, float q0, float q1, float x0, float x1) {
+    if constexpr (M == LINF) {
+        a = fmaxf(a, fmaxf(fabsf(q0 - x0), fabsf(q1 - x1)));
+    } else {
+        accum<M>(a, b, q0, x0);
+        accum<M>(a, b, q1, x1);
+    }
+}
+
 template <int M>
 __device__ __forceinline__ float finish(float a, float b) {
     if constexpr (M == MINK) return cbrtf(a);
@@ -63,16 +74,24 @@ __device__ __forceinline__ float finish(float a, float b) {
     else return a;
 }
 
-// DC: dimensions per chunk held in registers (64 or 128).
+// DC: dimensions per chunk held in registers (64 or 128).  A wave serves 64 queries: lane (p, h)
+// holds queries 2p and 2p + 1 of its wave's group over half h of each chunk (DC / 2 dimensions of
+// each), so every broadcast tile read feeds two queries and a row costs DC / 8 LDS reads per lane,
+// half of what one query per lane over the whole chunk needs.  After a tile the two halves meet
+// with one cross-half exchange per row, and lane (p, h) finishes and filters query 2p + h.
 template <int M, int DC>
 __global__ __launch_bounds__(256) void k_valu_filter(const float *__restrict__ base,
                                                      const float *__restrict__ qry, const float *__restrict__ tau,
                                                      int nq, int dpad, long row_begin, long row_end, int n_qtiles,
                                                      int n_items, long item_rows, uint2 *__restrict__ cand,
                                                      uint32_t *__restrict__ cnt, int cap) {
-    constexpr int V4 = DC / 4;
+    constexpr int V4 = DC / 4, HD = DC / 2, H4 = HD / 4;
+    // rows interleaved per tile read: 4, or 2 for L-inf, whose max3 chains gain nothing from more
+    // (L1 at 500k x 128, Q = 4096: 10.90 ms at 4 rows, 11.09 at 2; L-inf 10.82 at 2, 10.90 at 4)
+    constexpr int RI = M == LINF ? 2 : 4;
     __shared__ floatx4 tile[kValuRows * V4];
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int h = lane >> 5, pq = lane & 31;
     const int nchunks = (dpad + DC - 1) / DC;
     const int G = gridDim.x, g8 = G >> 3;
     const int slot = (blockIdx.x & 7) * g8 + (blockIdx.x >> 3);
@@ -80,28 +99,34 @@ __global__ __launch_bounds__(256) void k_valu_filter(const float *__restrict__ b
     for (int item = slot; item < n_items; item += G) {
         const int qtile = item % n_qtiles;
         const long chunk = item / n_qtiles;
-        const int q = qtile * 256 + tid;
+        const int q0 = qtile * 256 + wave * 64 + 2 * pq;  // this lane's query pair
+        const int q = q0 + h;                              // the query it finishes
         const bool qv = q < nq;
         const float tq = qv ? tau[q] : -INFINITY;
         const long r_lo = row_begin + chunk * item_rows;
         const long r_hi = min(r_lo + item_rows, row_end);
 
-        float qr[DC];
+        float qr[2][HD];
         auto load_q = [&](int c) {
 #pragma unroll
-            for (int i = 0; i < V4; ++i) {
-                const int d = c * DC + 4 * i;
-                floatx4 v = (qv && d < dpad) ? *(const floatx4 *)(qry + (long)q * dpad + d) : floatx4{0, 0, 0, 0};
+            for (int e = 0; e < 2; ++e) {
+                const bool v = q0 + e < nq;
 #pragma unroll
-                for (int j = 0; j < 4; ++j) qr[4 * i + j] = (M == JACC) ? fabsf(v[j]) : v[j];
+                for (int i = 0; i < H4; ++i) {
+                    const int d = c * DC + h * HD + 4 * i;
+                    floatx4 x = (v && d < dpad) ? *(const floatx4 *)(qry + (long)(q0 + e) * dpad + d)
+                                                : floatx4{0, 0, 0, 0};
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) qr[e][4 * i + j] = (M == JACC) ? fabsf(x[j]) : x[j];
+                }
             }
         };
         if (nchunks == 1) load_q(0);
 
         for (long rs = r_lo; rs < r_hi; rs += kValuRows) {
-            float a[kValuRows], b[kValuRows];
+            float a[2][kValuRows], b[2][kValuRows];
 #pragma unroll
-            for (int r = 0; r < kValuRows; ++r) a[r] = b[r] = 0.0f;
+            for (int r = 0; r < kValuRows; ++r) a[0][r] = a[1][r] = b[0][r] = b[1][r] = 0.0f;
             for (int c = 0; c < nchunks; ++c) {
                 if (nchunks > 1) load_q(c);
                 __syncthreads();
@@ -113,20 +138,39 @@ __global__ __launch_bounds__(256) void k_valu_filter(const float *__restrict__ b
                                                      : floatx4{0, 0, 0, 0};
                 }
                 __syncthreads();
+                // RI rows at a time: 2 RI independent accumulation chains per element
 #pragma unroll
-                for (int r = 0; r < kValuRows; ++r) {
+                for (int r = 0; r < kValuRows; r += RI) {
 #pragma unroll
-                    for (int i = 0; i < V4; ++i) {
-                        const floatx4 x = tile[r * V4 + i];
+                    for (int i = 0; i < H4; ++i) {
+                        floatx4 x[RI];
 #pragma unroll
-                        for (int j = 0; j < 4; ++j) accum<M>(a[r], b[r], qr[4 * i + j], x[j]);
+                        for (int u = 0; u < RI; ++u) x[u] = tile[(r + u) * V4 + h * H4 + i];
+#pragma unroll
+                        for (int j = 0; j < 4; j += 2)
+#pragma unroll
+                            for (int u = 0; u < RI; ++u)
+#pragma unroll
+                                for (int e = 0; e < 2; ++e)
+                                    accum2<M>(a[e][r + u], b[e][r + u], qr[e][4 * i + j], qr[e][4 * i + j + 1],
+                                              x[u][j], x[u][j + 1]);
                     }
                 }
             }
             const int nvalid = (int)min((long)kValuRows, r_hi - rs);
 #pragma unroll
             for (int r = 0; r < kValuRows; ++r) {
-                const float v = finish<M>(a[r], b[r]);
+                // the partner half needs the other query's partial sums; this lane keeps its own
+                const float sa = __shfl_xor(h ? a[0][r] : a[1][r], 32, 64);
+                const float oa = h ? a[1][r] : a[0][r];
+                float sb = 0.0f, ob = 0.0f;
+                if constexpr (M == JACC || M == COS) {
+                    sb = __shfl_xor(h ? b[0][r] : b[1][r], 32, 64);
+                    ob = h ? b[1][r] : b[0][r];
+                }
+                const float ta = M == LINF ? fmaxf(oa, sa) : oa + sa;
+                const float tb = ob + sb;
+                const float v = finish<M>(ta, tb);
                 if (v <= tq && r < nvalid && qv) {
                     const uint32_t at = atomicAdd(&cnt[q], 1u);
                     if (at < (uint32_t)cap) cand[(size_t)q * cap + at] = make_uint2(score_key(v), (uint32_t)(rs + r));
