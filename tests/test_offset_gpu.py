@@ -196,3 +196,55 @@ def test_coarse_assign_offset(vh, oracle, offset):
     refv = oracle.distance_rows("l2", data, cent[cl])
     assert np.all(np.abs(sc - refv) <= 1e-4 * np.abs(refv) + 1e-5)
     assert np.array_equal(res, data - cent[cl])
+
+
+def _free_bytes():
+    import ctypes
+
+    hip = ctypes.CDLL("libamdhip64.so")
+    free, total = ctypes.c_size_t(), ctypes.c_size_t()
+    assert hip.hipMemGetInfo(ctypes.byref(free), ctypes.byref(total)) == 0
+    return free.value
+
+
+def test_integer_base_keeps_one_copy(vh):
+    """Integer rows with an integer column shift give back the unshifted rows exactly as shifted
+    row + shift, so the engine keeps no second, unshifted copy of the base; float rows keep one
+    (their shifted values lose bits)."""
+    import gc
+
+    from vector_hip import datasets as ds
+
+    gc.collect()
+    n, d = 400_000, 128
+    copy = n * d * 4  # 205 MB
+    rng = np.random.default_rng(71)
+    used = {}
+    for name, base in (("int", ds.uniform_int(n, d, 72)), ("float", (0.5 + rng.random((n, d))).astype(np.float32))):
+        f0 = _free_bytes()
+        eng = vh.CudaKnnEngine(base, d)
+        vh.synchronize()
+        used[name] = f0 - _free_bytes()
+        ids, _, _ = eng.search_batch_arrays(base[:3], 1)
+        assert ids[:, 0].tolist() == [0, 1, 2]
+        del eng
+        gc.collect()
+    print(f"  device bytes held: integer base {used['int']}, float base {used['float']} (one copy {copy})",
+          flush=True)
+    assert used["int"] < 1.3 * copy, used
+    assert used["float"] > 1.8 * copy, used
+
+
+def test_integer_far_clusters_direct_form_exact(vh, oracle):
+    """Integer points in tight clusters far from the origin: the GEMM form's error bound admits
+    whole clusters, so most queries take the direct-form re-run, over rows rebuilt as shifted row +
+    shift (the engine keeps no unshifted copy of integer data).  Distances are exact integers."""
+    rng = np.random.default_rng(73)
+    centres = rng.integers(-20_000, 20_000, (40, 64))
+    lab = np.repeat(np.arange(40), 300)
+    base = (centres[lab] + rng.integers(-2, 3, (12_000, 64))).astype(np.float32)
+    q = (centres[rng.integers(0, 40, 30)] + rng.integers(-2, 3, (30, 64))).astype(np.float32)
+    for k in (10, 100):
+        ids, dist, lens = vh.CudaKnnEngine(base, 64).search_batch_arrays(q, k)
+        assert np.all(lens == k)
+        check_knn(oracle, base, q, ids, dist, k, "l2", rtol=0.0, atol=0.0, min_recall=1.0)

@@ -70,8 +70,10 @@ struct vhip_knn {
     hipStream_t stream = nullptr;
     vh::DevBuf base, norm, perm, inv_perm;
     // Squared L2: the rows are stored minus a per-dimension shift (the column means, integers for
-    // integer data), which keeps the norm form well conditioned on data away from the origin;
-    // `raw` holds the unshifted rows (same order and padding) for the direct-form passes.
+    // integer data), which keeps the norm form well conditioned on data away from the origin.  The
+    // direct-form passes need the unshifted rows: when every shifted value v gives back its x
+    // exactly as v + shift (integer data with an integer shift), they add the shift as they read;
+    // otherwise `raw` holds the unshifted rows (same order and padding).
     vh::DevBuf shift, raw;
     bool shifted = false;
     bool integral = false;    // every base value is an integer
@@ -300,8 +302,10 @@ struct QueryRows {
     const float *qpad, *qnorm, *qerr, *qraw;
 };
 
-// Base rows of the direct-form passes: the unshifted copy when the scan rows are shifted.
-static const float *direct_rows(const vhip_knn *E) { return E->shifted ? E->raw.as<float>() : E->base.as<float>(); }
+// Base rows of the direct-form passes: the unshifted copy when there is one, else the scan rows,
+// plus direct_shift(E) when those are shifted (then base + shift is the unshifted row, exactly).
+static const float *direct_rows(const vhip_knn *E) { return E->raw.p ? E->raw.as<float>() : E->base.as<float>(); }
+static const float *direct_shift(const vhip_knn *E) { return E->shifted && !E->raw.p ? E->shift.as<float>() : nullptr; }
 
 // Carves the buffers of one run over nq queries: kc kept entries and (with_cand) cap candidates
 // per query.
@@ -415,11 +419,11 @@ static int run_rounds(vhip_knn *E, const QueryRows &Q, int nq, int k, int kc, in
             launch_hamming_filter(E->base.as<uint32_t>(), (const uint32_t *)Q.qpad, B.tau, nq, (int)E->dpad, rb, re,
                                   B.cand, B.cnt, cap, E->grid_cap, s);
         else if (direct)
-            launch_valu_filter(L2, direct_rows(E), Q.qraw, B.tau, nq, (int)E->dim, (int)E->dpad, rb, re, B.cand,
-                               B.cnt, cap, E->grid_cap, s);
+            launch_valu_filter(L2, direct_rows(E), direct_shift(E), Q.qraw, B.tau, nq, (int)E->dim, (int)E->dpad, rb,
+                               re, B.cand, B.cnt, cap, E->grid_cap, s);
         else
-            launch_valu_filter(E->metric, E->base.as<float>(), Q.qpad, B.tau, nq, (int)E->dim, (int)E->dpad, rb, re,
-                               B.cand, B.cnt, cap, E->grid_cap, s);
+            launch_valu_filter(E->metric, E->base.as<float>(), nullptr, Q.qpad, B.tau, nq, (int)E->dim, (int)E->dpad,
+                               rb, re, B.cand, B.cnt, cap, E->grid_cap, s);
         if (t >= 0) E->timer.end(t, s, work, bytes);
         VH_HIP(hipGetLastError());
         // the last round counts the standing margin flags into nflag[1]
@@ -561,9 +565,9 @@ static int search_prepared(vhip_knn *E, const QueryRows &Q, int nq, int k, int k
             pub.host = nfh;
         }
         if (gemm && d_dist)
-            launch_topk_refine(nq, k, kc, kout, E->metric, Q.qraw, direct_rows(E), E->inv_perm.as<uint32_t>(),
-                               (int)E->dpad, Q.qnorm, E->norm.as<float>(), B.topk, B.have, Q.qerr, d_ids, d_dist,
-                               ostride, pub, s);
+            launch_topk_refine(nq, k, kc, kout, E->metric, Q.qraw, direct_rows(E), direct_shift(E),
+                               E->inv_perm.as<uint32_t>(), (int)E->dpad, Q.qnorm, E->norm.as<float>(), B.topk, B.have,
+                               Q.qerr, d_ids, d_dist, ostride, pub, s);
         else
             launch_topk_finalize(nq, kc, kout, E->metric, B.topk, B.have, d_ids, d_dist, d_dist_u32, ostride, pub, s);
         VH_HIP(hipGetLastError());
@@ -642,9 +646,10 @@ static int engine_create(const void *base, size_t n, size_t dim, int metric, int
         DevBuf raw, flag;
         // the raw rows; afterwards, scratch for the norm extremes' partials
         VH_CHECK(raw.ensure(ordinal, std::max(n * dim * sizeof(float), 2 * kMinMaxParts * sizeof(float))));
-        VH_CHECK(flag.ensure(ordinal, sizeof(uint32_t)));
-        launch_fill_u32(flag.as<uint32_t>(), 1, 0u, E->stream);
+        VH_CHECK(flag.ensure(ordinal, 2 * sizeof(uint32_t)));  // non-integer values, inexact shifted values
+        launch_fill_u32(flag.as<uint32_t>(), 2, 0u, E->stream);
         VH_CHECK(E->stager.h2d(raw.p, base, n * dim * sizeof(float), E->stream));
+        bool try_exact = false;  // the shifted rows may give back the unshifted ones (see `raw`)
         if (metric == L2) {
             // per-dimension shift: the column means (integers for integer data)
             DevBuf part;
@@ -654,13 +659,18 @@ static int engine_create(const void *base, size_t n, size_t dim, int metric, int
                              E->shift.as<float>(), E->stream);
             VH_HIP(hipGetLastError());
             std::vector<float> mu(E->dpad);
+            uint32_t colnonint = 1;
             VH_HIP(hipMemcpyAsync(mu.data(), E->shift.p, E->dpad * sizeof(float), hipMemcpyDeviceToHost, E->stream));
+            VH_HIP(hipMemcpyAsync(&colnonint, flag.p, sizeof(uint32_t), hipMemcpyDeviceToHost, E->stream));
             VH_HIP(hipStreamSynchronize(E->stream));
             for (float v : mu) E->shifted = E->shifted || v != 0.0f;
+            // integer values and an integer shift: x - shift is exact unless the values are huge,
+            // which the row preparation checks
+            try_exact = E->shifted && colnonint == 0;
         }
         VH_CHECK(E->base.ensure(ordinal, E->n_pad * E->dpad * sizeof(float)));
         VH_CHECK(E->norm.ensure(ordinal, E->n_pad * sizeof(float)));
-        if (E->shifted) VH_CHECK(E->raw.ensure(ordinal, E->n_pad * E->dpad * sizeof(float)));
+        if (E->shifted && !try_exact) VH_CHECK(E->raw.ensure(ordinal, E->n_pad * E->dpad * sizeof(float)));
         RowPrep rp;
         rp.in = raw.as<float>();
         rp.n = n;
@@ -670,15 +680,30 @@ static int engine_create(const void *base, size_t n, size_t dim, int metric, int
         rp.perm = E->perm.as<uint32_t>();
         rp.shift = E->shifted ? E->shift.as<float>() : nullptr;
         rp.out = E->base.as<float>();
-        rp.raw_out = E->shifted ? E->raw.as<float>() : nullptr;
+        rp.raw_out = E->raw.p ? E->raw.as<float>() : nullptr;
         rp.norm = E->norm.as<float>();
         rp.norm_kind = norm_kind_of(metric);
         rp.transform = transform_of(metric);
         rp.normalize = normalize_of(metric);
         rp.pad_fill = __builtin_nanf("");
         rp.nonint = metric == HAMMING_PACKED ? nullptr : flag.as<uint32_t>();
+        rp.inexact = try_exact ? flag.as<uint32_t>() + 1 : nullptr;
         launch_rows_prep(rp, E->stream);
         VH_HIP(hipGetLastError());
+        if (try_exact) {
+            uint32_t inexact = 1;
+            VH_HIP(hipMemcpyAsync(&inexact, flag.as<uint32_t>() + 1, sizeof(uint32_t), hipMemcpyDeviceToHost,
+                                  E->stream));
+            VH_HIP(hipStreamSynchronize(E->stream));
+            if (inexact) {
+                // some shifted value lost bits: keep the unshifted rows after all
+                VH_CHECK(E->raw.ensure(ordinal, E->n_pad * E->dpad * sizeof(float)));
+                rp.raw_out = E->raw.as<float>();
+                rp.inexact = nullptr;
+                launch_rows_prep(rp, E->stream);
+                VH_HIP(hipGetLastError());
+            }
+        }
         const size_t rows8 = ham_mfma_rows(n);
         if (metric == HAMMING_PACKED && ham_mfma_supported((int)E->dpad) &&
             want_fp4_copy(rows8 * ham_mfma_row_bytes((int)E->dpad))) {

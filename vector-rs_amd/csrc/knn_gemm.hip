@@ -85,7 +85,7 @@ __global__ __launch_bounds__(256) void k_rows_prep(RowPrep a) {
         const size_t src = a.perm ? a.perm[p] : p;
         const float *row = a.in + src * (size_t)dim;
         float ss = 0.0f;
-        bool whole = true;
+        bool whole = true, exact = true;
         // four elements per lane in flight at a time (the loads first), the sum in the order d
         for (int d0 = lane; d0 < dpad; d0 += 256) {
             float xs[4], sh[4];
@@ -103,6 +103,7 @@ __global__ __launch_bounds__(256) void k_rows_prep(RowPrep a) {
                 whole = whole && x == rintf(x);
                 if (rrow) rrow[d] = x;
                 float v = a.shift ? x - sh[u] : x;
+                exact = exact && (!a.shift || v + sh[u] == x);
                 if (a.transform) v = sqrtf(fabsf(v));
                 if (!a.normalize) orow[d] = v;
                 ss = fmaf(v, v, ss);
@@ -111,6 +112,7 @@ __global__ __launch_bounds__(256) void k_rows_prep(RowPrep a) {
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
         const bool row_int = __builtin_amdgcn_ballot_w64(!whole) == 0;
+        const bool row_exact = __builtin_amdgcn_ballot_w64(!exact) == 0;
         if (a.normalize) {
             const float nr = sqrtf(ss);
             const float inv = nr > 0.0f ? 1.0f / nr : 0.0f;
@@ -134,6 +136,7 @@ __global__ __launch_bounds__(256) void k_rows_prep(RowPrep a) {
         if (lane == 0) {
             if (a.norm_kind && a.norm) a.norm[p] = a.norm_kind == 2 ? sqrtf(ss) : ss;
             if (a.nonint && !row_int) atomicOr(a.nonint, 1u);
+            if (a.inexact && !row_exact) atomicOr(a.inexact, 1u);
             if (a.err) {
                 const bool ints = row_int && a.base_integral;
                 float e = 0.0f;

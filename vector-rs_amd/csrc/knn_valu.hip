@@ -80,7 +80,7 @@ __device__ __forceinline__ float finish(float a, float b) {
 // half of what one query per lane over the whole chunk needs.  After a tile the two halves meet
 // with one cross-half exchange per row, and lane (p, h) finishes and filters query 2p + h.
 template <int M, int DC>
-__global__ __launch_bounds__(256) void k_valu_filter(const float *__restrict__ base,
+__global__ __launch_bounds__(256) void k_valu_filter(const float *__restrict__ base, const float *__restrict__ shift,
                                                      const float *__restrict__ qry, const float *__restrict__ tau,
                                                      int nq, int dpad, long row_begin, long row_end, int n_qtiles,
                                                      int n_items, long item_rows, uint2 *__restrict__ cand,
@@ -134,8 +134,10 @@ __global__ __launch_bounds__(256) void k_valu_filter(const float *__restrict__ b
                     const int row = i / V4, c4 = i % V4;
                     const long r = rs + row;
                     const int d = c * DC + 4 * c4;
-                    tile[i] = (r < r_hi && d < dpad) ? *(const floatx4 *)(base + r * (long)dpad + d)
-                                                     : floatx4{0, 0, 0, 0};
+                    floatx4 v = (r < r_hi && d < dpad) ? *(const floatx4 *)(base + r * (long)dpad + d)
+                                                       : floatx4{0, 0, 0, 0};
+                    if (shift && d < dpad) v += *(const floatx4 *)(shift + d);
+                    tile[i] = v;
                 }
                 __syncthreads();
                 // RI rows at a time: 2 RI independent accumulation chains per element
@@ -181,18 +183,18 @@ __global__ __launch_bounds__(256) void k_valu_filter(const float *__restrict__ b
 }
 
 template <int M>
-static void launch_m(int dpad, dim3 g, hipStream_t s, const float *base, const float *qry,
+static void launch_m(int dpad, dim3 g, hipStream_t s, const float *base, const float *shift, const float *qry,
                      const float *tau, int nq, long rb, long re, int nqt, int items, long item_rows, uint2 *cand,
                      uint32_t *cnt, int cap) {
     if (dpad <= 128 && dpad > 64)
-        hipLaunchKernelGGL((k_valu_filter<M, 128>), g, dim3(256), 0, s, base, qry, tau, nq, dpad, rb, re, nqt,
+        hipLaunchKernelGGL((k_valu_filter<M, 128>), g, dim3(256), 0, s, base, shift, qry, tau, nq, dpad, rb, re, nqt,
                            items, item_rows, cand, cnt, cap);
     else
-        hipLaunchKernelGGL((k_valu_filter<M, 64>), g, dim3(256), 0, s, base, qry, tau, nq, dpad, rb, re, nqt,
+        hipLaunchKernelGGL((k_valu_filter<M, 64>), g, dim3(256), 0, s, base, shift, qry, tau, nq, dpad, rb, re, nqt,
                            items, item_rows, cand, cnt, cap);
 }
 
-void launch_valu_filter(int metric, const float *base, const float *qry, const float *tau,
+void launch_valu_filter(int metric, const float *base, const float *shift, const float *qry, const float *tau,
                         int nq, int dim, int dpad, long row_begin, long row_end, uint2 *cand, uint32_t *cnt, int cap,
                         int grid_cap, hipStream_t s) {
     (void)dim;
@@ -211,19 +213,19 @@ void launch_valu_filter(int metric, const float *base, const float *qry, const f
     const int it = (int)items;
     switch (metric) {
         // squared L2 in direct form: the certified fallback of the GEMM-form L2 search
-        case L2: launch_m<L2>(dpad, g, s, base, qry, tau, nq, row_begin, row_end, nqt, it, item_rows, cand, cnt, cap); break;
-        case L1: launch_m<L1>(dpad, g, s, base, qry, tau, nq, row_begin, row_end, nqt, it, item_rows, cand, cnt, cap); break;
-        case MINK: launch_m<MINK>(dpad, g, s, base, qry, tau, nq, row_begin, row_end, nqt, it, item_rows, cand,
+        case L2: launch_m<L2>(dpad, g, s, base, metric == L2 ? shift : nullptr, qry, tau, nq, row_begin, row_end, nqt, it, item_rows, cand, cnt, cap); break;
+        case L1: launch_m<L1>(dpad, g, s, base, metric == L2 ? shift : nullptr, qry, tau, nq, row_begin, row_end, nqt, it, item_rows, cand, cnt, cap); break;
+        case MINK: launch_m<MINK>(dpad, g, s, base, metric == L2 ? shift : nullptr, qry, tau, nq, row_begin, row_end, nqt, it, item_rows, cand,
                                           cnt, cap); break;
-        case LINF: launch_m<LINF>(dpad, g, s, base, qry, tau, nq, row_begin, row_end, nqt, it, item_rows, cand,
+        case LINF: launch_m<LINF>(dpad, g, s, base, metric == L2 ? shift : nullptr, qry, tau, nq, row_begin, row_end, nqt, it, item_rows, cand,
                                           cnt, cap); break;
-        case HAMF: launch_m<HAMF>(dpad, g, s, base, qry, tau, nq, row_begin, row_end, nqt, it, item_rows, cand,
+        case HAMF: launch_m<HAMF>(dpad, g, s, base, metric == L2 ? shift : nullptr, qry, tau, nq, row_begin, row_end, nqt, it, item_rows, cand,
                                           cnt, cap); break;
-        case MAHA: launch_m<MAHA>(dpad, g, s, base, qry, tau, nq, row_begin, row_end, nqt, it, item_rows, cand,
+        case MAHA: launch_m<MAHA>(dpad, g, s, base, metric == L2 ? shift : nullptr, qry, tau, nq, row_begin, row_end, nqt, it, item_rows, cand,
                                           cnt, cap); break;
-        case JACC: launch_m<JACC>(dpad, g, s, base, qry, tau, nq, row_begin, row_end, nqt, it, item_rows, cand,
+        case JACC: launch_m<JACC>(dpad, g, s, base, metric == L2 ? shift : nullptr, qry, tau, nq, row_begin, row_end, nqt, it, item_rows, cand,
                                           cnt, cap); break;
-        case HELL: launch_m<HELL>(dpad, g, s, base, qry, tau, nq, row_begin, row_end, nqt, it, item_rows, cand,
+        case HELL: launch_m<HELL>(dpad, g, s, base, metric == L2 ? shift : nullptr, qry, tau, nq, row_begin, row_end, nqt, it, item_rows, cand,
                                           cnt, cap); break;
         default: break;
     }

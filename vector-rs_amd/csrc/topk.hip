@@ -435,6 +435,7 @@ void launch_topk_finalize(int nq, int kc, int kout, int metric, const unsigned l
 // ... in order) and a fixed xor butterfly.
 __global__ __launch_bounds__(256) void k_topk_refine(int k, int kc, int kout, int metric,
                                                      const float *__restrict__ qrows, const float *__restrict__ base,
+                                                     const float *__restrict__ shift,
                                                      const uint32_t *__restrict__ inv_perm, int dpad,
                                                      const float *__restrict__ qnorm, const float *__restrict__ bnorm,
                                                      const u64 *__restrict__ topk, const uint32_t *__restrict__ have,
@@ -471,7 +472,15 @@ __global__ __launch_bounds__(256) void k_topk_refine(int k, int kc, int kout, in
         const float4 *xv = (const float4 *)(base + (size_t)row * dpad);
         float a = 0.0f, nq = 0.0f, nx = 0.0f;
         for (int d = s; d < n4; d += 16) {
-            const float4 x = xv[d], y = qv[d];
+            float4 x = xv[d];
+            const float4 y = qv[d];
+            if (shift) {  // squared L2 over shifted rows that give back the unshifted ones exactly
+                const float4 m = ((const float4 *)shift)[d];
+                x.x += m.x;
+                x.y += m.y;
+                x.z += m.z;
+                x.w += m.w;
+            }
             if (metric == L2) {
                 const float t0 = y.x - x.x, t1 = y.y - x.y, t2 = y.z - x.z, t3 = y.w - x.w;
                 a = fmaf(t0, t0, a);
@@ -524,11 +533,11 @@ __global__ __launch_bounds__(256) void k_topk_refine(int k, int kc, int kout, in
 }
 
 void launch_topk_refine(int nq, int k, int kc, int kout, int metric, const float *qrows, const float *base,
-                        const uint32_t *inv_perm, int dpad, const float *qnorm, const float *bnorm,
+                        const float *shift, const uint32_t *inv_perm, int dpad, const float *qnorm, const float *bnorm,
                         const unsigned long long *topk, const uint32_t *have, const float *qerr, uint32_t *out_ids,
                         float *out_dist, int ostride, const FlagPublish &pub, hipStream_t s) {
     if (nq <= 0) return;
-    hipLaunchKernelGGL(k_topk_refine, dim3(nq), dim3(256), 0, s, k, kc, kout, metric, qrows, base, inv_perm, dpad,
+    hipLaunchKernelGGL(k_topk_refine, dim3(nq), dim3(256), 0, s, k, kc, kout, metric, qrows, base, shift, inv_perm, dpad,
                        qnorm, bnorm, topk, have, qerr, out_ids, out_dist, ostride, pub);
 }
 

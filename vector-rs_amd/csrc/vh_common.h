@@ -144,6 +144,8 @@ struct RowPrep {
     int norm_kind = 0, transform = 0, normalize = 0;
     float pad_fill = 0.0f;
     uint32_t *nonint = nullptr;
+    uint32_t *inexact = nullptr;  // (may be null) set to 1 when some shifted value v = fl(x - shift)
+                                  // does not give back x as v + shift
     float *err = nullptr;
     int err_mode = 0;
     float err_coeff = 0.0f, err_nmax = 0.0f;
@@ -233,10 +235,11 @@ void launch_topk_finalize(int nq, int kc, int kout, int metric, const unsigned l
 // GEMM metrics: recompute the kept distances in direct form, re-sort by (distance, id) and
 // write the best k (same output contract as launch_topk_finalize; out_dist required).  Entries
 // past the k-th count only when their GEMM-form score is within 2 qerr[q] of the k-th.  `qrows` /
-// `base` are the unshifted queries and resident rows; qnorm / bnorm are the original L2 norms
-// (cosine zero-norm guard; unused for the other metrics).
+// `base` are the unshifted queries and resident rows, or (shift non-null, squared L2) base +
+// shift gives back the unshifted rows exactly; qnorm / bnorm are the original L2 norms (cosine
+// zero-norm guard; unused for the other metrics).
 void launch_topk_refine(int nq, int k, int kc, int kout, int metric, const float *qrows, const float *base,
-                        const uint32_t *inv_perm, int dpad, const float *qnorm, const float *bnorm,
+                        const float *shift, const uint32_t *inv_perm, int dpad, const float *qnorm, const float *bnorm,
                         const unsigned long long *topk, const uint32_t *have, const float *qerr, uint32_t *out_ids,
                         float *out_dist, int ostride, const FlagPublish &pub, hipStream_t s);
 // Number of nonzero flags among flags[0, n) into *count (device).
@@ -284,9 +287,11 @@ void launch_kmeans_assign_valu(int metric, const float *cent, int k, const float
 void launch_kmeans_fix(int metric, const float *pts, int dpad, const int32_t *fix, const uint32_t *nfix,
                        const float *cent, int k, unsigned long long *best, int32_t *assign, float *inertia,
                        int32_t *pos, int32_t *counts, float *devmax, int grid_cap, hipStream_t s);
-void launch_valu_filter(int metric, const float *base, const float *qry, const float *tau, int nq, int dim, int dpad,
-                        long row_begin, long row_end, uint2 *cand, uint32_t *cnt, int cap, int grid_cap,
-                        hipStream_t s);
+// shift (may be null): added to every base value as the tiles are read (the direct-form pass of
+// squared L2 over shifted rows that give back the unshifted ones exactly).
+void launch_valu_filter(int metric, const float *base, const float *shift, const float *qry, const float *tau, int nq,
+                        int dim, int dpad, long row_begin, long row_end, uint2 *cand, uint32_t *cnt, int cap,
+                        int grid_cap, hipStream_t s);
 // Fills count floats (32-bit words) with v.  Kernels rather than hipMemsetAsync, so a caller may
 // capture the engines' work in a HIP graph.
 void launch_fill(float *p, size_t count, float v, hipStream_t s);
