@@ -22,9 +22,13 @@ all 10M codes), "l1", "linf" and "ivfpq" (the IVF-PQ search on clustered data, c
 the oracle's search_with_nprobe), each with its own roofline, CPU baseline and parity.
 The process exits with status 3, after printing the line, when any parity check fails.
 
+The default line also carries "batch_sweep" (search_batch at batch sizes 1 to 128, as the
+reference's cuda_bench.rs does, each batch checked against the oracle) and "kmeans_fit" (fit() with
+its default k-means++ init, init timed apart from the Lloyd iterations).
+
 Other workloads: --workload cos768 | kmeans | hamming | l1 | linf | gauss (see WORKLOADS), ivf_coarse
-(the IVF coarse quantizer), ivfpq (IVF-PQ search), upload (engine builds from VECRSTOR files),
-copy (counter calibration).
+(the IVF coarse quantizer), ivfpq (IVF-PQ search), kmeans_fit, batch_sweep, upload (engine builds
+from VECRSTOR files), copy (counter calibration).
 """
 import argparse
 import json
@@ -655,7 +659,9 @@ def bench_batch_sweep(vh, reps, with_cpu):
     1,000,000 x 128 integer base under squared L2.  Per batch size: the host-buffer call (the
     reference's path: queries in, results out over PCIe) and the device-resident call, each the
     median of `reps` calls after two warm-up calls, against one pass over the base at 8 TB/s; every
-    batch checked against the oracle (tie-aware recall, distances within 1e-4)."""
+    batch checked against the oracle (tie-aware recall, distances within 1e-4).  The host-buffer leg
+    goes through DistributedKnnEngine.search_batch_arrays (the same C call as search_batch, without
+    building Python result objects)."""
     from vector_hip import datasets as ds
     import oracle
 
@@ -691,7 +697,9 @@ def bench_batch_sweep(vh, reps, with_cpu):
                     ts.append(time.perf_counter() - t0)
                 return float(np.median(ts)) * 1e6
 
-            host_us = med(lambda: eng.search_batch(q, k))
+            # the host-buffer C call through the array binding (search_batch builds Python result
+            # objects on top, which is the binding's cost, not the library's)
+            host_us = med(lambda: eng.search_batch_arrays(q, k))
             dev_us = med(lambda: dev.search_batch_device(dq.ptr, b, k, di.ptr, dd.ptr))
             ids, dist, _ = dev.search_batch_arrays(q, k)
             ref = oracle.knn_search_batch(base, q, k, mname, threads=th)
@@ -965,6 +973,12 @@ def main():
             r = bench_ivfpq(vh, args.steps, args.warmup, not args.no_cpu)
             out["ivfpq"] = {kk: r[kk] for kk in ("metric", "value", "unit", "ms_per_step", "dtype", "config",
                                                  "roofline", "cpu_baseline", "parity") if kk in r}
+            # the reference benchmark's own shapes: search_batch over batch sizes 1..128, and fit()
+            # with its default k-means++ init
+            r = bench_batch_sweep(vh, 20, not args.no_cpu)
+            out["batch_sweep"] = {kk: r[kk] for kk in ("metric", "config", "shapes", "cpu_note", "parity")}
+            r = bench_kmeans_fit(vh, not args.no_cpu)
+            out["kmeans_fit"] = {kk: r[kk] for kk in ("metric", "kmeans_2m", "cuda_bench_shape")}
     out["config"]["device"] = ctx.device_name()
     print(json.dumps(out))
     bad = [name for name, part in [("top", out)] + [(kk, v) for kk, v in out.items() if isinstance(v, dict)]

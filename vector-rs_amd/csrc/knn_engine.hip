@@ -57,6 +57,7 @@ struct RunBufs {
 
 struct Workspace {
     DevBuf arena;
+    DevBuf hq, hi, hd;  // the host-buffer path's device copies of queries and results (grow-only)
 };
 
 }  // namespace vh
@@ -342,7 +343,8 @@ static std::vector<Round> split_rounds(const std::vector<Round> &r, long max_row
 // The round plan of a search over nq queries: the small-batch plan for at most kSmallCols queries
 // on the GEMM metrics (not the direct-form re-runs).
 static bool small_plan(const vhip_knn *E, size_t nq, bool direct) {
-    return is_gemm_metric(E->metric) && !direct && !E->ham8 && small_batch((int)std::min<size_t>(nq, 1 << 20), (int)E->dpad);
+    return is_gemm_metric(E->metric) && !direct && !E->ham8 &&
+           small_batch((int)std::min<size_t>(nq, 1 << 20), (int)E->dpad, E->n);
 }
 
 // Runs all rounds for nq prepared queries; results stay in B.topk (row stride kc) / B.have.
@@ -408,7 +410,7 @@ static int run_rounds(vhip_knn *E, const QueryRows &Q, int nq, int k, int kc, in
                 launch_ham_mfma(dense, hitem, E->base8.as<int8_t>(), B.q8, (int)E->dpad, B.tau, nq, rb, re, B.cand,
                                 B.cnt, cap, E->grid_cap, s);
             }
-        } else if (gemm && small_batch(nq, (int)E->dpad))
+        } else if (gemm && small_batch(nq, (int)E->dpad, E->n))
             launch_small_scan(E->metric, rd.dense, E->base.as<float>(), E->norm.as<float>(), Q.qpad, Q.qnorm, B.tau,
                               nq, (int)E->dpad, rb, re, B.cand, B.cnt, cap, E->grid_cap, s);
         else if (gemm)
@@ -772,12 +774,9 @@ static size_t batch_bytes(const vhip_knn *E, size_t m, int kc, int cap, bool wit
 // Device-side search: d_queries (nq x dim elements), outputs nq x k with row stride k.  Working
 // memory comes from the engine's workspace buffer (grown as needed) or, when `scratch` is given,
 // from that fixed region only, in query batches sized to fit it (no allocation, no kernel timing).
-static int engine_search_device(vhip_knn *E, const void *d_queries, size_t nq, size_t k, uint32_t *d_ids,
-                                float *d_dist, uint32_t *d_dist_u32, void *scratch = nullptr,
-                                size_t scratch_bytes = 0) {
-    clear_error();
-    VH_CHECK(check_search_args(E, k));
-    std::lock_guard<std::mutex> lock(E->mu);
+// The search itself; the caller holds E->mu.
+static int engine_search_locked(vhip_knn *E, const void *d_queries, size_t nq, size_t k, uint32_t *d_ids,
+                                float *d_dist, uint32_t *d_dist_u32, void *scratch, size_t scratch_bytes) {
     VH_CHECK(open_device(E->dev));
     const size_t ek = std::min(k, E->n);
     if (nq == 0 || k == 0) return VHIP_OK;
@@ -863,7 +862,18 @@ static int engine_search_device(vhip_knn *E, const void *d_queries, size_t nq, s
     return VHIP_OK;
 }
 
-// Host-side search through pinned staging.
+static int engine_search_device(vhip_knn *E, const void *d_queries, size_t nq, size_t k, uint32_t *d_ids,
+                                float *d_dist, uint32_t *d_dist_u32, void *scratch = nullptr,
+                                size_t scratch_bytes = 0) {
+    clear_error();
+    VH_CHECK(check_search_args(E, k));
+    std::lock_guard<std::mutex> lock(E->mu);
+    return engine_search_locked(E, d_queries, nq, k, d_ids, d_dist, d_dist_u32, scratch, scratch_bytes);
+}
+
+// Host-side search through pinned staging, into the engine's own device buffers (kept between
+// calls, grown as needed); the engine's lock is held for the whole call, as those buffers are
+// shared by its calls.
 static int engine_search_host(vhip_knn *E, const void *queries, size_t nq, size_t k, uint32_t *out_ids,
                               void *out_dist, bool dist_u32, size_t *out_len) {
     clear_error();
@@ -876,23 +886,17 @@ static int engine_search_host(vhip_knn *E, const void *queries, size_t nq, size_
         return VHIP_OK;
     }
     if (!out_ids || !out_dist) return set_error(VHIP_ERR_INVALID_CONFIG, "null output pointer");
-    DevBuf dq, di, dd;
-    {
-        std::lock_guard<std::mutex> lock(E->mu);
-        VH_CHECK(open_device(E->dev));
-        VH_CHECK(dq.ensure(E->dev, nq * E->dim * sizeof(float)));
-        VH_CHECK(di.ensure(E->dev, nq * k * sizeof(uint32_t)));
-        VH_CHECK(dd.ensure(E->dev, nq * k * sizeof(float)));
-        VH_CHECK(E->stager.h2d(dq.p, queries, nq * E->dim * sizeof(float), E->stream));
-    }
-    VH_CHECK(engine_search_device(E, dq.p, nq, k, di.as<uint32_t>(), dist_u32 ? nullptr : dd.as<float>(),
-                                  dist_u32 ? dd.as<uint32_t>() : nullptr));
-    {
-        std::lock_guard<std::mutex> lock(E->mu);
-        VH_CHECK(open_device(E->dev));
-        VH_CHECK(E->stager.d2h(out_ids, di.p, nq * k * sizeof(uint32_t), E->stream));
-        VH_CHECK(E->stager.d2h(out_dist, dd.p, nq * k * sizeof(float), E->stream));
-    }
+    std::lock_guard<std::mutex> lock(E->mu);
+    VH_CHECK(open_device(E->dev));
+    DevBuf &dq = E->ws.hq, &di = E->ws.hi, &dd = E->ws.hd;
+    VH_CHECK(dq.ensure(E->dev, nq * E->dim * sizeof(float)));
+    VH_CHECK(di.ensure(E->dev, nq * k * sizeof(uint32_t)));
+    VH_CHECK(dd.ensure(E->dev, nq * k * sizeof(float)));
+    VH_CHECK(E->stager.h2d(dq.p, queries, nq * E->dim * sizeof(float), E->stream));
+    VH_CHECK(engine_search_locked(E, dq.p, nq, k, di.as<uint32_t>(), dist_u32 ? nullptr : dd.as<float>(),
+                                  dist_u32 ? dd.as<uint32_t>() : nullptr, nullptr, 0));
+    VH_CHECK(E->stager.d2h_pair(out_ids, di.p, nq * k * sizeof(uint32_t), out_dist, dd.p, nq * k * sizeof(float),
+                                E->stream));
     for (size_t q = 0; q < nq; ++q) out_len[q] = ek;
     return VHIP_OK;
 }

@@ -201,6 +201,21 @@ int PinnedStager::d2h(void *dst, const void *src, size_t bytes, hipStream_t s) {
     return VHIP_OK;
 }
 
+int PinnedStager::d2h_pair(void *dst0, const void *src0, size_t b0, void *dst1, const void *src1, size_t b1,
+                           hipStream_t s) {
+    if (b0 > kBlock || b1 > kBlock) {
+        VH_CHECK(d2h(dst0, src0, b0, s));
+        return d2h(dst1, src1, b1, s);
+    }
+    VH_CHECK(init(dev < 0 ? 0 : dev));
+    VH_HIP(hipMemcpyAsync(buf[0], src0, b0, hipMemcpyDeviceToHost, s));
+    VH_HIP(hipMemcpyAsync(buf[1], src1, b1, hipMemcpyDeviceToHost, s));
+    VH_HIP(hipStreamSynchronize(s));
+    std::memcpy(dst0, buf[0], b0);
+    std::memcpy(dst1, buf[1], b1);
+    return VHIP_OK;
+}
+
 // ---- kernel timer -------------------------------------------------------------------------
 KernelTimer::~KernelTimer() {
     for (auto &p : pool) {

@@ -30,11 +30,16 @@ inline int gemm_slots(int dpad) {
     return dpad <= 128 ? kGemmSlotsReg
                        : (gemm_narrow(dpad) ? kGemmSlotsNarrow : (dpad % 128 == 0 ? kGemmSlotsPanel : kGemmSlotsStream));
 }
-// Batches of at most kSmallCols queries (one 32-query tile) with rows of at most kSmallMaxDpad
-// floats take the small-batch MFMA scan (knn_small.hip), which spreads every round over all CUs.
+// Batches of at most kSmallCols queries (one 32-query tile), or up to four tiles over a base of at
+// most kSmallBaseRows rows (where every search is bound by launches, not by scanned pairs), with
+// rows of at most kSmallMaxDpad floats take the small-batch MFMA scan (knn_small.hip), which spreads
+// every round over all CUs.
 constexpr int kSmallCols = 32;
 constexpr int kSmallMaxDpad = 1024;
-inline bool small_batch(int nq, int dpad) { return nq <= kSmallCols && dpad <= kSmallMaxDpad; }
+constexpr size_t kSmallBaseRows = 262144;
+inline bool small_batch(int nq, int dpad, size_t n) {
+    return dpad <= kSmallMaxDpad && (nq <= kSmallCols || (nq <= 4 * kSmallCols && n <= kSmallBaseRows));
+}
 constexpr int kRowAlign = 256;       // row counts of MFMA row operands and round boundaries
                                      // are multiples of this (the largest MFMA stage)
 

@@ -86,6 +86,8 @@ struct PinnedStager {
     int init(int device);
     int h2d(void *dst, const void *src, size_t bytes, hipStream_t s);
     int d2h(void *dst, const void *src, size_t bytes, hipStream_t s);
+    // Two device ranges to host with one wait when each fits a staging buffer.
+    int d2h_pair(void *dst0, const void *src0, size_t b0, void *dst1, const void *src1, size_t b1, hipStream_t s);
 };
 
 // ---- kernel timing with events on the engine's stream ----------------------------------
