@@ -237,14 +237,26 @@ def _kmeanspp_restated(x, k, seed):
     return picks
 
 
-@pytest.mark.parametrize("n,dim,k,seed", [(3000, 40, 200, 5), (1_100_000, 8, 12, 9), (700, 128, 700, 3)])
-def test_kmeanspp_matches_its_restatement(vh, n, dim, k, seed):
-    """The device draws (k_kpp_update + k_kpp_select) pick exactly the rows of the float64
-    restatement: every distance and running sum is an exact integer here.  The shapes cover
-    several point blocks per step, more blocks than the select's threads (each thread then owns a
-    run of block sums), and k = n (the last draws find every remaining weight zero but one)."""
+@pytest.mark.parametrize(
+    "n,dim,k,seed,spread",
+    [(3000, 40, 200, 5, 0), (1_100_000, 8, 12, 9, 0), (700, 128, 700, 3, 0), (20_000, 768, 64, 2, 0),
+     (300_000, 64, 40, 7, 100), (40_000, 800, 24, 4, 60)],
+)
+def test_kmeanspp_matches_its_restatement(vh, n, dim, k, seed, spread):
+    """The device draws (update + k_kpp_select) pick exactly the rows of the float64 restatement:
+    every distance and running sum is an exact integer here.  The shapes cover both update kernels
+    (point blocks of 1024 above 2^20 points, row groups of 8 to 64 lanes below), several blocks per
+    step, more blocks than the select's threads (each thread then owns a run of block sums), k = n
+    (the last draws find every remaining weight zero but one), a dimension that leaves some lanes
+    of a 64-lane row one slice short (800), and pruning in the row-group kernel (more than 2^24
+    point floats): with spread > 0 the points are 64 clusters with centres in [-spread, spread] and
+    noise in [-8, 8], so that most rows are pruned once every cluster holds a centre (the squared
+    distances stay below 2^24, exact in float32)."""
     rng = np.random.default_rng(seed)
-    x = rng.integers(-8, 9, (n, dim)).astype(np.float32)
+    x = rng.integers(-8, 9, (n, dim))
+    if spread:
+        x += rng.integers(-spread, spread + 1, (64, dim))[rng.integers(0, 64, n)]
+    x = x.astype(np.float32)
     st = vh.KMeansState(x)
     print(f"  k-means++ n={n} dim={dim} k={k}", flush=True)
     c, _, (_, kk, iters, _) = st.fit(k, 0, -1.0, init_mode=0, seed=seed)

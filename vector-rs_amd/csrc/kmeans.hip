@@ -90,6 +90,8 @@ __global__ void k_scatter(const int32_t *__restrict__ assign, const int32_t *__r
 
 // ---- update ----------------------------------------------------------------------------
 constexpr int kUpdSlotsPerWave = 256;  // sorted slots per wave window
+constexpr int kUpdMinSlots = 16;       // the window halves down to this while the waves number
+constexpr int kUpdMinWaves = 2048;     // fewer than this
 
 // Largest c in [0, k) with offsets[c] <= i: the (non-empty) cluster whose segment holds slot i.
 __device__ __forceinline__ int segment_of(const int32_t *__restrict__ offsets, int k, int i) {
@@ -126,7 +128,8 @@ __global__ void k_dev_bound(int k, float absmax, const float *__restrict__ cabs,
 }
 
 // S = number of 64-dimension slots per lane (dpad <= 64 * S).  Lane l of a wave owns dimensions
-// l, l + 64, ...; the wave adds the deviations x - c of the rows of its window slot by slot in
+// l, l + 64, ...; the wave adds the deviations x - c of the rows of its window (spw sorted
+// slots; integer sums, so the window size does not change them) slot by slot in
 // fixed point (the cluster's scale) and flushes the running sum into sums[c] whenever the window
 // crosses into the next cluster's segment.  With `l2_inertia` it also writes each point's
 // squared distance sum_d (x_d - c_d)^2 (lane-strided sum, fixed xor butterfly).
@@ -140,13 +143,13 @@ __global__ __launch_bounds__(256) void k_update_sums(const float *__restrict__ p
                                                      const int32_t *__restrict__ offsets,
                                                      const int32_t *__restrict__ exps,
                                                      unsigned long long *__restrict__ sums, float *__restrict__ inertia,
-                                                     int l2_inertia) {
+                                                     int l2_inertia, int spw) {
     constexpr int kUpdUnroll = upd_unroll<S>();
     const int lane = threadIdx.x & 63;
     const int wave = (int)((blockIdx.x * (size_t)blockDim.x + threadIdx.x) >> 6);
-    const int s0 = wave * kUpdSlotsPerWave;
+    const int s0 = wave * spw;
     if (s0 >= n) return;
-    const int s1 = min(n, s0 + kUpdSlotsPerWave);
+    const int s1 = min(n, s0 + spw);
     int c = segment_of(offsets, k, s0);
     int next = offsets[c + 1];
     long long acc[S];
@@ -386,43 +389,78 @@ __global__ __launch_bounds__(256) void k_coarse_score(const float *__restrict__ 
 }
 
 // Seeded k-means++ on the device (CudaKMeansEngine::init_random, kmeans.rs:409-460).  Each step
-// is three launches on the state's stream, with no host round trip:
-//  * k_kpp_dcc: the squared distance from the newest centre to every earlier one;
-//  * k_kpp_update: mind[i] = min(mind[i], ||x_i - c||^2) for the newest centre c, in direct form,
-//    and the sum of mind over each block of kKppBlock points (double, fixed tree order).  A point
-//    whose nearest centre so far, a = near[i], lies at ||c_a - c||^2 >= 4 mind[i] (1 + margin)
-//    from c cannot come closer to c (triangle inequality: ||x - c|| >= ||c_a - c|| - ||x - c_a||
-//    >= ||x - c_a||), so its row is not read; the margin covers the rounding of all three computed
-//    squared distances, so the values of mind are exactly those of the unpruned pass.  Eight lanes
-//    share a row (each a 16-byte column slice), so each load instruction of a wave reads eight
-//    whole 128-byte row pieces;
+// is two or three launches on the state's stream, with no host round trip:
+//  * k_kpp_dcc: the squared distance from the newest centre to every earlier one (only when the
+//    update prunes);
+//  * an update: mind[i] = min(mind[i], ||x_i - c||^2) for the newest centre c, in direct form,
+//    and the sum of mind over each block of points (double, fixed order).  A point whose nearest
+//    centre so far, a = near[i], lies at ||c_a - c||^2 >= 4 mind[i] (1 + margin) from c cannot
+//    come closer to c (triangle inequality: ||x - c|| >= ||c_a - c|| - ||x - c_a|| >=
+//    ||x - c_a||), so a pruning update does not read its row; the margin covers the rounding of
+//    all three computed squared distances, so the values of mind are exactly those of the
+//    unpruned pass.  k_kpp_update serves large point sets: blocks of kKppBlock points, eight
+//    lanes a row (each a 16-byte column slice), so each load instruction of a wave reads eight
+//    whole 128-byte row pieces.  k_kpp_update_rows serves point sets below kKppRowsMaxN: L lanes
+//    a row (L = 8 .. 64 by dimension, so a lane loads at most four 16-byte slices of a row of up
+//    to 1024 floats), blocks of 4 (64 / L) `passes` points, so that a small set still spreads
+//    over thousands of waves; it prunes only when the points exceed the cache (kKppPruneFloats);
 //  * k_kpp_select: one workgroup draws the next centre with probability mind[i] / sum(mind), as
 //    the reference's linear scan does (the first i whose running sum reaches u * total), through
 //    the block sums and then the chosen block's values, and copies that point into the centres.
-// Both sums are in a fixed order, so a seed gives the same centres on every run.
+// Every sum is in a fixed order, so a seed gives the same centres on every run.
 constexpr int kKppBlock = 1024;          // points per k_kpp_update block (256 threads)
-constexpr int kKppSelectThreads = 1024;  // equal to kKppBlock: the select reads a block one value per thread
+constexpr int kKppSelectThreads = 1024;  // at least the points of a block: the select reads one value per thread
+constexpr int kKppRowsMaxN = 1 << 20;    // k_kpp_update_rows below this many points
+constexpr int kKppRowsMaxBlocks = 4096;  // its blocks per step (the select sums at most 4 per thread)
+constexpr size_t kKppPruneFloats = size_t(1) << 24;  // point floats above which k_kpp_update_rows prunes
 
+__device__ __forceinline__ float acc_d2(float d2, float4 x, float4 c) {
+    const float a0 = x.x - c.x, a1 = x.y - c.y, a2 = x.z - c.z, a3 = x.w - c.w;
+    d2 = fmaf(a0, a0, d2);
+    d2 = fmaf(a1, a1, d2);
+    d2 = fmaf(a2, a2, d2);
+    return fmaf(a3, a3, d2);
+}
+
+// ||x - c||^2 over nc4 float4 columns, split over a group of L lanes (sub: this lane's index in
+// the group; its columns are sub, sub + L, ...).  Every lane of the group returns the sum.  Four
+// column slices are loaded before any is used; a slice past the row end loads the last one (in
+// bounds) and is not added.
+template <int L>
+__device__ __forceinline__ float group_d2(const float4 *__restrict__ x, const float4 *__restrict__ c, int nc4,
+                                          int sub) {
+    float d2 = 0.0f;
+    for (int j = sub; j < nc4; j += 4 * L) {
+        float4 xv[4], cv[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int jj = min(j + u * L, nc4 - 1);
+            xv[u] = x[jj];
+            cv[u] = c[jj];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            if (j + u * L < nc4) d2 = acc_d2(d2, xv[u], cv[u]);
+    }
+#pragma unroll
+    for (int o = L / 2; o > 0; o >>= 1) d2 += __shfl_xor(d2, o, 64);
+    return d2;
+}
+
+// Lanes per row for a row of nc4 float4 columns.
+inline int kpp_lanes(int nc4) { return nc4 <= 32 ? 8 : nc4 <= 64 ? 16 : nc4 <= 128 ? 32 : 64; }
+
+// dcc[a] = ||c_a - c_m||^2 for the m earlier centres, L lanes per centre.
+template <int L>
 __global__ __launch_bounds__(256) void k_kpp_dcc(const float *__restrict__ cent, int dpad, int m,
                                                  float *__restrict__ dcc) {
-    extern __shared__ float4 s_c[];  // centre m, dpad / 4 float4
-    const int nc4 = dpad >> 2;
-    const float4 *cm = (const float4 *)(cent + (size_t)m * dpad);
-    for (int i = threadIdx.x; i < nc4; i += 256) s_c[i] = cm[i];
-    __syncthreads();
-    const int a = blockIdx.x * 256 + threadIdx.x;
-    if (a >= m) return;
-    const float4 *ca = (const float4 *)(cent + (size_t)a * dpad);
-    float d2 = 0.0f;
-    for (int j = 0; j < nc4; ++j) {
-        const float4 x = ca[j], c = s_c[j];
-        const float a0 = x.x - c.x, a1 = x.y - c.y, a2 = x.z - c.z, a3 = x.w - c.w;
-        d2 = fmaf(a0, a0, d2);
-        d2 = fmaf(a1, a1, d2);
-        d2 = fmaf(a2, a2, d2);
-        d2 = fmaf(a3, a3, d2);
-    }
-    dcc[a] = d2;
+    constexpr int R = 64 / L;
+    const int lane = threadIdx.x & 63;
+    const int a = (blockIdx.x * 4 + (threadIdx.x >> 6)) * R + lane / L;
+    const int ac = min(a, m - 1);  // rows past the end repeat the last one, unstored
+    const float v = group_d2<L>((const float4 *)(cent + (size_t)ac * dpad), (const float4 *)(cent + (size_t)m * dpad),
+                                dpad >> 2, lane & (L - 1));
+    if (a < m && (lane & (L - 1)) == 0) dcc[a] = v;
 }
 
 // cidx: the newest centre's index (its row is c); prune: 4 (1 + margin), or 0 for no pruning.
@@ -493,6 +531,52 @@ __global__ __launch_bounds__(256) void k_kpp_update(const float *__restrict__ pt
     if (threadIdx.x == 0) partial[blockIdx.x] = red[0];
 }
 
+// The update for point sets below kKppRowsMaxN: a wave holds 64 / L rows at a time, L lanes a row,
+// and takes `passes` such row groups one after another; a workgroup's 4 waves cover 4 (64 / L)
+// passes consecutive points, whose mind values it sums into partial[blockIdx.x] (each lane's
+// rows in order, then the wave by a fixed shuffle tree, then the 4 waves in order).  prune as in
+// k_kpp_update (0: every row is read and dcc is not).
+template <int L>
+__global__ __launch_bounds__(256) void k_kpp_update_rows(const float *__restrict__ pts, int dpad, int n,
+                                                         const float *__restrict__ c, int cidx,
+                                                         float *__restrict__ mind, int32_t *__restrict__ near,
+                                                         const float *__restrict__ dcc, float prune, int passes,
+                                                         double *__restrict__ partial) {
+    constexpr int R = 64 / L;
+    __shared__ double red[4];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, sub = lane & (L - 1);
+    const int nc4 = dpad >> 2;
+    const int r0 = (blockIdx.x * 4 + wave) * R * passes + lane / L;
+    double s = 0.0;
+    for (int p = 0; p < passes; ++p) {
+        const int r = r0 + p * R;
+        if (r < n) {  // uniform over the row's L lanes
+            float m = mind[r];
+            bool need = true;
+            if (prune > 0.0f) {
+                const int a = near[r];
+                need = !(a >= 0 && dcc[a] >= prune * m);
+            }
+            if (need) {  // uniform over the row's L lanes, so the group's shuffles stay within it
+                const float v = group_d2<L>((const float4 *)(pts + (size_t)r * dpad), (const float4 *)c, nc4, sub);
+                if (v < m) {
+                    m = v;
+                    if (sub == 0) {
+                        mind[r] = v;
+                        near[r] = cidx;
+                    }
+                }
+            }
+            if (sub == 0) s += (double)m;
+        }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+    if (lane == 0) red[wave] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) partial[blockIdx.x] = ((red[0] + red[1]) + red[2]) + red[3];
+}
+
 // Inclusive prefix sum of one double per thread over the workgroup (kKppSelectThreads threads), in
 // a fixed order: within each wave by shuffles, then the wave totals; `tmp` holds 16 doubles.
 __device__ __forceinline__ double block_scan_incl(double v, double *tmp) {
@@ -510,7 +594,8 @@ __device__ __forceinline__ double block_scan_incl(double v, double *tmp) {
     return before + v;
 }
 
-// Step j's draw.  draw: the step's 64-bit random value.  A total weight of at most 1e-6 (every
+// Step j's draw over nb blocks of blk points (partial: their sums).  draw: the step's 64-bit
+// random value.  A total weight of at most 1e-6 (every
 // point on a centre) takes draw mod n, as the reference takes a uniform index there.  Otherwise
 // the threshold is u * total with u = the draw's top 53 bits in [0, 1), and the centre is the
 // first point of positive weight whose running sum of mind reaches it: the first run of blocks,
@@ -519,7 +604,7 @@ __device__ __forceinline__ double block_scan_incl(double v, double *tmp) {
 // weight is taken.  Every choice is a minimum or maximum over the threads, so the result does not
 // depend on their timing.
 __global__ __launch_bounds__(kKppSelectThreads) void k_kpp_select(const double *__restrict__ partial, int nb,
-                                                                  const float *__restrict__ mind, int n,
+                                                                  int blk, const float *__restrict__ mind, int n,
                                                                   const uint64_t *__restrict__ draws, int j,
                                                                   const float *__restrict__ pts, int dpad,
                                                                   float *__restrict__ cent) {
@@ -580,8 +665,8 @@ __global__ __launch_bounds__(kKppSelectThreads) void k_kpp_select(const double *
         }
         __syncthreads();
         const int pb = s_blk;
-        const int i = pb * kKppBlock + t;  // kKppSelectThreads == kKppBlock: one value per thread
-        const double w = i < n ? (double)mind[i] : 0.0;
+        const int i = pb * blk + t;  // blk <= kKppSelectThreads: one value per thread
+        const double w = t < blk && i < n ? (double)mind[i] : 0.0;
         const double ci = s_before + block_scan_incl(w, tmp);
         if (w > 0.0) {
             if (ci >= thr) atomicMin(&s_pt, i);
@@ -823,14 +908,16 @@ static int km_iterate(vhip_kmeans *K) {
     hipLaunchKernelGGL(k_scatter, dim3(ceil_div(n, 256)), dim3(256), 0, s, K->assign.as<int32_t>(),
                        K->pos.as<int32_t>(), K->offsets.as<int32_t>(), n, K->sorted.as<int32_t>());
     const int slots = ceil_div((long)K->dpad, 64);
-    const int waves = ceil_div(n, kUpdSlotsPerWave);
+    int spw = kUpdSlotsPerWave;  // slots per wave: fewer for small point sets, so they fill the GPU
+    while (spw > kUpdMinSlots && ceil_div(n, spw) < kUpdMinWaves) spw >>= 1;
+    const int waves = ceil_div(n, spw);
     const int l2 = K->metric == L2 ? 1 : 0;
     unsigned long long *sums = K->sums.as<unsigned long long>();
 #define VH_UPD(S)                                                                                                  \
     do {                                                                                                           \
         hipLaunchKernelGGL(k_update_sums<S>, dim3(ceil_div(waves, 4)), dim3(256), 0, s, K->points(),               \
                            K->craw.as<float>(), (int)K->dpad, (int)K->dim, n, k, K->sorted.as<int32_t>(),          \
-                           K->offsets.as<int32_t>(), K->exps.as<int32_t>(), sums, K->inertia.as<float>(), l2);     \
+                           K->offsets.as<int32_t>(), K->exps.as<int32_t>(), sums, K->inertia.as<float>(), l2, spw); \
         hipLaunchKernelGGL(k_update_finalize<S>, dim3(ceil_div(k, 4)), dim3(256), 0, s, k, (int)K->dpad,          \
                            (int)K->dim, sums, K->counts.as<int32_t>(), K->exps.as<int32_t>(), K->craw.as<float>(), \
                            K->shifts.as<float>());                                                                  \
@@ -865,15 +952,25 @@ static int km_total_inertia(vhip_kmeans *K, float *out) {
 // Seeded k-means++ (kmeans.rs:409-460): first centre uniform, then each next centre drawn
 // with probability proportional to the squared L2 distance to the nearest chosen centre.  The
 // draws (one 64-bit splitmix64 value per centre) are made on the host up front; every step then
-// runs on the device (k_kpp_dcc, k_kpp_update, k_kpp_select), with no host round trip.
+// runs on the device (k_kpp_dcc, an update kernel, k_kpp_select), with no host round trip.
 static int km_init_kmeanspp(vhip_kmeans *K, size_t k, uint64_t seed) {
     hipStream_t s = K->stream;
     const int n = (int)K->n;
+    const int dpad = (int)K->dpad;
     VH_CHECK(K->craw.ensure(K->dev, k * K->dpad * sizeof(float)));
     const float *pts = K->points();
     float *cr = K->craw.as<float>();
+    // the update's shape: blocks of blk points, nb of them
+    const int lanes = kpp_lanes(dpad / 4);
+    const bool rows = n < kKppRowsMaxN;
+    int passes = 1;
+    if (rows)
+        while (ceil_div(n, 4 * (64 / lanes) * passes) > kKppRowsMaxBlocks && 4 * (64 / lanes) * passes < kKppBlock)
+            passes *= 2;
+    const int blk = rows ? 4 * (64 / lanes) * passes : kKppBlock;
+    const int nb = ceil_div(n, blk);
+    const bool prune_on = !rows || (size_t)n * K->dpad > kKppPruneFloats;
     DevBuf mind, near, part, draws, dcc;
-    const int nb = ceil_div(n, kKppBlock);
     VH_CHECK(mind.ensure(K->dev, (size_t)n * sizeof(float)));
     VH_CHECK(near.ensure(K->dev, (size_t)n * sizeof(int32_t)));
     VH_CHECK(part.ensure(K->dev, (size_t)nb * sizeof(double)));
@@ -890,17 +987,37 @@ static int km_init_kmeanspp(vhip_kmeans *K, size_t k, uint64_t seed) {
     // Pruning factor 4 (1 + 64 g), g = gamma_{dpad+2}: each of the three computed squared
     // distances (the centres', the point's to its nearest, the point's to the new centre) is
     // within a factor (1 +- g) of its value, and (1 + 64 g) leaves room for all three.
-    const float prune = (float)(4.0 * (1.0 + 64.0 * gamma_n((double)K->dpad + 2.0)));
+    const float prune = prune_on ? (float)(4.0 * (1.0 + 64.0 * gamma_n((double)K->dpad + 2.0))) : 0.0f;
     const size_t lds = K->dpad * sizeof(float);
     for (size_t j = 1; j < k; ++j) {
         const int m = (int)j - 1;  // the newest centre
-        if (m > 0)
-            hipLaunchKernelGGL(k_kpp_dcc, dim3(ceil_div(m, 256)), dim3(256), lds, s, cr, (int)K->dpad, m,
-                               dcc.as<float>());
-        hipLaunchKernelGGL(k_kpp_update, dim3(nb), dim3(256), lds, s, pts, (int)K->dpad, n, cr + (size_t)m * K->dpad, m,
-                           mind.as<float>(), near.as<int32_t>(), dcc.as<float>(), prune, part.as<double>());
-        hipLaunchKernelGGL(k_kpp_select, dim3(1), dim3(kKppSelectThreads), 0, s, part.as<double>(), nb,
-                           mind.as<float>(), n, draws.as<uint64_t>(), (int)j, pts, (int)K->dpad, cr);
+        const float *c = cr + (size_t)m * K->dpad;
+        if (prune_on && m > 0) {
+            const dim3 g(ceil_div(m, 4 * (64 / lanes)));
+            switch (lanes) {
+                case 8: hipLaunchKernelGGL(k_kpp_dcc<8>, g, dim3(256), 0, s, cr, dpad, m, dcc.as<float>()); break;
+                case 16: hipLaunchKernelGGL(k_kpp_dcc<16>, g, dim3(256), 0, s, cr, dpad, m, dcc.as<float>()); break;
+                case 32: hipLaunchKernelGGL(k_kpp_dcc<32>, g, dim3(256), 0, s, cr, dpad, m, dcc.as<float>()); break;
+                default: hipLaunchKernelGGL(k_kpp_dcc<64>, g, dim3(256), 0, s, cr, dpad, m, dcc.as<float>()); break;
+            }
+        }
+        if (rows) {
+#define VH_KPP_ROWS(LN)                                                                                          \
+    hipLaunchKernelGGL(k_kpp_update_rows<LN>, dim3(nb), dim3(256), 0, s, pts, dpad, n, c, m, mind.as<float>(), \
+                       near.as<int32_t>(), dcc.as<float>(), prune, passes, part.as<double>())
+            switch (lanes) {
+                case 8: VH_KPP_ROWS(8); break;
+                case 16: VH_KPP_ROWS(16); break;
+                case 32: VH_KPP_ROWS(32); break;
+                default: VH_KPP_ROWS(64); break;
+            }
+#undef VH_KPP_ROWS
+        } else {
+            hipLaunchKernelGGL(k_kpp_update, dim3(nb), dim3(256), lds, s, pts, dpad, n, c, m, mind.as<float>(),
+                               near.as<int32_t>(), dcc.as<float>(), prune, part.as<double>());
+        }
+        hipLaunchKernelGGL(k_kpp_select, dim3(1), dim3(kKppSelectThreads), 0, s, part.as<double>(), nb, blk,
+                           mind.as<float>(), n, draws.as<uint64_t>(), (int)j, pts, dpad, cr);
     }
     VH_HIP(hipGetLastError());
     VH_HIP(hipStreamSynchronize(s));  // mind, near, part, draws, dcc and dh are released at return

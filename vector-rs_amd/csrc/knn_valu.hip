@@ -311,12 +311,15 @@ __global__ __launch_bounds__(256) void k_kmeans_assign_valu(const float *__restr
 // certified get the argmin of the direct-form metric over all centroids (squared L2 sum (x-c)^2,
 // dot product, cosine dot / (sqrt(|x|^2) sqrt(|c|^2)) with the 1e-9 guard: the formulas of
 // scalar.rs:14-75 and kmeans.cu:87-170) on the unshifted points and centroids.  A work item is a
-// tile of 256 listed points (one per lane, in registers) times a chunk of kFixChunk centroids
-// (tiles broadcast from LDS); the chunk's best (score key, centroid) is folded into best[i] with
-// a 64-bit atomic min, so the result is the lowest score and then the lowest index, whatever the
-// order of the items.
+// tile of 256 listed points (one per lane, in registers) times a chunk of centroids (tiles
+// broadcast from LDS); the chunk's best (score key, centroid) is folded into best[i] with a
+// 64-bit atomic min, so the result is the lowest score and then the lowest index, whatever the
+// order of the items.  The chunk is kFixChunk centroids, halved (down to one LDS tile) while the
+// items number fewer than twice the workgroups: a short list still spreads over the GPU, and a
+// centroid's score does not depend on the chunk it falls in.
 // ---------------------------------------------------------------------------------
 constexpr int kFixChunk = 256;
+static_assert(kFixChunk % kValuRows == 0 && (kFixChunk & (kFixChunk - 1)) == 0, "chunks halve to whole LDS tiles");
 
 __global__ void k_fix_init(const uint32_t *__restrict__ nfix, unsigned long long *__restrict__ best) {
     const uint32_t nf = *nfix;
@@ -333,7 +336,10 @@ __global__ __launch_bounds__(256) void k_fix_argmin(const float *__restrict__ pt
     const int tid = threadIdx.x;
     const int nchunks = (dpad + DC - 1) / DC;
     const int nf = (int)*nfix;
-    const int n_tiles = (nf + 255) / 256, n_cchunks = (k + kFixChunk - 1) / kFixChunk;
+    const int n_tiles = (nf + 255) / 256;
+    int chunk = kFixChunk;
+    while (chunk > kValuRows && n_tiles * ((k + chunk - 1) / chunk) < 2 * (int)gridDim.x) chunk >>= 1;
+    const int n_cchunks = (k + chunk - 1) / chunk;
     const int items = n_tiles * n_cchunks;
     for (int item = blockIdx.x; item < items; item += gridDim.x) {
         const int t = item % n_tiles, cc = item / n_tiles;
@@ -359,7 +365,7 @@ __global__ __launch_bounds__(256) void k_fix_argmin(const float *__restrict__ pt
             }
         }
         if (nchunks == 1) load_p(0);
-        const int c0 = cc * kFixChunk, c1 = min(k, c0 + kFixChunk);
+        const int c0 = cc * chunk, c1 = min(k, c0 + chunk);
         float bv = INFINITY;
         int bc = c0;
         for (int cs = c0; cs < c1; cs += kValuRows) {
