@@ -464,6 +464,16 @@ __global__ __launch_bounds__(256) void k_kpp_dcc(const float *__restrict__ cent,
 }
 
 // cidx: the newest centre's index (its row is c); prune: 4 (1 + margin), or 0 for no pruning.
+// Each wave owns 256 consecutive points of the block.  It first tests all of them (lane l: points
+// l, l + 64, l + 128, l + 192; their mind, near and the nearest centre's dcc, three loads in
+// flight per point) and lists the points the new centre may come closer to in LDS (ballot
+// order); it then reads only the listed rows, 8 G at a time (8 lanes a row, JU column slices of
+// each in flight per lane), and leaves each distance in LDS for the lane that owns the point,
+// which keeps the smaller of it and mind.  JU = min(4, dpad / 32): the column slices of a row a
+// lane has in flight (the row loop steps 32 JU floats); G = 4 rows a lane for JU <= 2 and 2 above,
+// which keeps the kernel within 64 VGPRs (8 waves per SIMD, so that the 1,954 blocks of a
+// 2,000,000-point step are resident at once).
+template <int JU, int G>
 __global__ __launch_bounds__(256) void k_kpp_update(const float *__restrict__ pts, int dpad, int n,
                                                     const float *__restrict__ c, int cidx,
                                                     float *__restrict__ mind, int32_t *__restrict__ near,
@@ -471,39 +481,65 @@ __global__ __launch_bounds__(256) void k_kpp_update(const float *__restrict__ pt
                                                     double *__restrict__ partial) {
     extern __shared__ float4 s_c[];  // the centre, dpad / 4 float4
     __shared__ double red[256];
+    __shared__ int s_list[4][kKppBlock / 4];    // listed points of each wave (offsets in its 256)
+    __shared__ float s_dist[4][kKppBlock / 4];  // their distances to the centre
     const int nc4 = dpad >> 2;
     for (int i = threadIdx.x; i < nc4; i += 256) s_c[i] = ((const float4 *)c)[i];
-    __syncthreads();
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int part = lane & 7;  // this lane's column slices: part, part + 8, ...
     const int b0 = blockIdx.x * kKppBlock + wave * (kKppBlock / 4);
     const int b1 = min(n, b0 + kKppBlock / 4);
-    double s = 0.0;
-    constexpr int G = 4;  // groups of 8 rows in flight per wave
-    for (int r0 = b0 + (lane >> 3); r0 < b1; r0 += 8 * G) {
-        float m[G], d2[G];
-        bool need[G];
+    // test the wave's points
+    float m[4];
+    bool need[4];
+    int a[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int r = min(b0 + lane + 64 * q, n - 1);
+        m[q] = mind[r];
+        a[q] = near[r];
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const float dc = dcc[a[q] >= 0 ? a[q] : 0];  // not used when a[q] < 0
+        need[q] = b0 + lane + 64 * q < b1 && !(prune > 0.0f && a[q] >= 0 && dc >= prune * m[q]);
+    }
+    int cnt = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const unsigned long long bal = __ballot(need[q]);
+        const int below = __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0));
+        if (need[q]) s_list[wave][cnt + below] = lane + 64 * q;
+        cnt += __popcll(bal);
+    }
+    __syncthreads();  // s_c and the lists
+    // the listed rows, 4 groups of 8 rows per pass
+    const int part = lane & 7, slot = lane >> 3;
+    for (int it = 0; it < cnt; it += 8 * G) {
+        int rl[G];
+        const float4 *row[G];
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-            const int r = r0 + 8 * g;
-            m[g] = r < b1 ? mind[r] : 0.0f;
-            const int a = r < b1 ? near[r] : -1;
-            need[g] = r < b1 && !(a >= 0 && dcc[a] >= prune * m[g]);
-            d2[g] = 0.0f;
+            rl[g] = s_list[wave][min(it + 8 * g + slot, cnt - 1)];
+            row[g] = (const float4 *)(pts + (size_t)(b0 + rl[g]) * dpad);
         }
-        for (int j = part; j < nc4; j += 8) {
-            const float4 cv = s_c[j];
+        float d2[G];
 #pragma unroll
-            for (int g = 0; g < G; ++g) {
-                if (need[g]) {
-                    const float4 xv = ((const float4 *)(pts + (size_t)(r0 + 8 * g) * dpad))[j];
-                    const float a0 = xv.x - cv.x, a1 = xv.y - cv.y, a2 = xv.z - cv.z, a3 = xv.w - cv.w;
-                    d2[g] = fmaf(a0, a0, d2[g]);
-                    d2[g] = fmaf(a1, a1, d2[g]);
-                    d2[g] = fmaf(a2, a2, d2[g]);
-                    d2[g] = fmaf(a3, a3, d2[g]);
-                }
+        for (int g = 0; g < G; ++g) d2[g] = 0.0f;
+        for (int j0 = part; j0 < nc4; j0 += 8 * JU) {
+            float4 xv[G][JU];
+#pragma unroll
+            for (int u = 0; u < JU; ++u) {
+                const int j = min(j0 + 8 * u, nc4 - 1);
+#pragma unroll
+                for (int g = 0; g < G; ++g) xv[g][u] = row[g][j];
             }
+#pragma unroll
+            for (int u = 0; u < JU; ++u)
+                if (j0 + 8 * u < nc4) {
+                    const float4 cv = s_c[j0 + 8 * u];
+#pragma unroll
+                    for (int g = 0; g < G; ++g) d2[g] = acc_d2(d2[g], xv[g][u], cv);
+                }
         }
 #pragma unroll
         for (int g = 0; g < G; ++g) {
@@ -511,15 +547,24 @@ __global__ __launch_bounds__(256) void k_kpp_update(const float *__restrict__ pt
             v += __shfl_xor(v, 1, 64);
             v += __shfl_xor(v, 2, 64);
             v += __shfl_xor(v, 4, 64);
-            const int r = r0 + 8 * g;
-            if (part == 0 && r < b1) {
-                if (need[g] && v < m[g]) {
-                    m[g] = v;
+            if (part == 0 && it + 8 * g + slot < cnt) s_dist[wave][rl[g]] = v;
+        }
+    }
+    __syncthreads();  // the distances
+    double s = 0.0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int r = b0 + lane + 64 * q;
+        if (r < b1) {
+            if (need[q]) {
+                const float v = s_dist[wave][lane + 64 * q];
+                if (v < m[q]) {
+                    m[q] = v;
                     mind[r] = v;
                     near[r] = cidx;
                 }
-                s += (double)m[g];
             }
+            s += (double)m[q];
         }
     }
     red[threadIdx.x] = s;
@@ -1013,8 +1058,17 @@ static int km_init_kmeanspp(vhip_kmeans *K, size_t k, uint64_t seed) {
             }
 #undef VH_KPP_ROWS
         } else {
-            hipLaunchKernelGGL(k_kpp_update, dim3(nb), dim3(256), lds, s, pts, dpad, n, c, m, mind.as<float>(),
-                               near.as<int32_t>(), dcc.as<float>(), prune, part.as<double>());
+#define VH_KPP_BLOCKS(JU)                                                                                    \
+    hipLaunchKernelGGL((k_kpp_update<JU, (JU <= 2 ? 4 : 2)>), dim3(nb), dim3(256), lds, s, pts, dpad, n, c, m, \
+                       mind.as<float>(),                                                                     \
+                       near.as<int32_t>(), dcc.as<float>(), prune, part.as<double>())
+            switch (std::min(4, dpad / 32)) {  // column slices per lane and row in flight
+                case 1: VH_KPP_BLOCKS(1); break;
+                case 2: VH_KPP_BLOCKS(2); break;
+                case 3: VH_KPP_BLOCKS(3); break;
+                default: VH_KPP_BLOCKS(4); break;
+            }
+#undef VH_KPP_BLOCKS
         }
         hipLaunchKernelGGL(k_kpp_select, dim3(1), dim3(kKppSelectThreads), 0, s, part.as<double>(), nb, blk,
                            mind.as<float>(), n, draws.as<uint64_t>(), (int)j, pts, dpad, cr);
