@@ -53,6 +53,8 @@ PEAK_HBM = 8.0e12          # B/s
 # for v_fma_f32 on this part).
 PEAK_VECTOR_F32 = 157.3e12
 PEAK_MFMA_FP4 = 10.1e15    # OP/s, MI355X dense fp4 matrix
+# LDS read rate of MI355X for 4-byte words, GB/s: 256 CUs x 64 banks x 4 B x 2.4 GHz
+PEAK_LDS_GBS = 256 * 64 * 4 * 2.4
 
 
 def log(*a):
@@ -480,6 +482,16 @@ def bench_ivfpq(vh, steps, warmup, with_cpu):
         rl["work_note"] = ("VALU/LDS ops per launch: 2*Ks*D per (query, probed list) table + 2*M per scanned code; "
                            f"{pairs} tables, {scanned} codes; the M lookups are random LDS reads, which bound "
                            "the scan")
+        # the same launch against the LDS: M random 4-byte table reads per scanned code, at most
+        # one 4-byte word per bank per clock (256 CUs x 64 banks x 2.4 GHz)
+        lookups = scanned * m_sub
+        lds_gbs = lookups * 4.0 / (rl["avg_launch_ms"] * 1e-3) / 1e9
+        rl["lds"] = {"bound": "lds", "achieved": round(lds_gbs, 1), "peak": PEAK_LDS_GBS, "unit": "GB/s",
+                     "frac": round(lds_gbs / PEAK_LDS_GBS, 4), "lookups_per_launch": lookups,
+                     "note": "M 4-byte ADC table entries per scanned code (read 16 bytes at a time: the "
+                             "four pairs of a work item share each read) against the CUs' LDS read rate "
+                             "(256 CUs x 64 banks x 4 B x 2.4 GHz); random entries collide in banks, so a "
+                             "wave's gather takes several passes and the full rate is out of reach"}
     # recall@10 against the exact kNN (the GPU engine, itself checked against the oracle), at the
     # benchmark's nprobe and two others
     eid = vh.CudaKnnEngine(base, d, vh.DistanceMetric.L2Squared).search_batch_arrays(q, k)[0]

@@ -464,7 +464,7 @@ static bool list_path(const vhip_ivfpq *X, size_t k, size_t np) {
         if (std::strcmp(e, "query") == 0) return false;
     return X->reg && X->ks == 256 && X->m_sub == 16 && (X->ds == 4 || X->ds == 8) && k >= 1 &&
            k <= (size_t)kListMaxK && np * k <= (size_t)kListMaxMerge &&
-           sizeof(ListLds<kListThreads>) <= X->lds_limit;
+           sizeof(ListLds) <= X->lds_limit;
 }
 
 // (query, probe) pairs of one search chunk: pair ids are 32-bit (q * nprobe + p) and the plan's

@@ -70,28 +70,28 @@ constexpr int ring_bytes(int nv) { return kScanWaves * ring_chunks(nv) * ring_ch
 // ---- list-major scan --------------------------------------------------------------------------
 // For 16-byte code rows (16 sub-spaces of 256 sub-centroids) and k <= kListMaxK the search runs
 // list-major: the (query, probe) pairs are grouped by list, and a work item is one list with up to
-// kListQb of the queries probing it.  Its kListQb ADC tables are built in LDS at once (thread j of
-// each half of the workgroup computes sub-centroid j's entries from its register-held codebook),
-// then the list's codes and ids stream once through a shared LDS ring of kListRing chunks of
-// kListChunkRows rows (global->LDS DMA, one barrier per chunk), and wave w scores every row against
-// its own pair's table with the summation order of compute_distance_with_lut (pq.rs:270-293),
-// keeping its k best.  A list's codes are therefore read once per kListQb probing queries instead
-// of once per probing query.  Each pair's k best go to pair_out; k_ivfpq_merge then sorts each
-// query's nprobe x k keys.  Keys are unique (score, id), so the result equals the query-major scan's.
+// kListQb of the queries probing it.  The item's kListQb ADC tables are built in LDS side by side:
+// entry (m, e) of the four tables is one float4 (thread j computes sub-centroid j's entries from its
+// register-held codebook), so one 16-byte LDS read per code byte serves the item's four pairs.  The
+// list then streams once: wave w scores rows 64 w .. 64 w + 63 of each 256-row chunk, one row a
+// lane (its 16 code bytes loaded straight into registers, one chunk ahead), against the four
+// tables with the summation order of compute_distance_with_lut (pq.rs:270-293), and leaves the
+// four scores in LDS; after one barrier per chunk, wave q filters and offers the chunk's 256
+// scores of pair q, keeping its k best.  A list's codes are therefore read once per kListQb probing
+// queries instead of once per probing query, and a table entry costs a quarter of a 16-byte read
+// instead of a 4-byte read (a wave's 16-byte read passes 16 lanes at a time; random entries collide
+// in banks either way).  Each pair's k best go to pair_out; k_ivfpq_merge then sorts each query's
+// nprobe x k keys.  Keys are unique (score, id), so the result equals the query-major scan's.
 // The query's threshold carries across its pairs through tau_q: a finished pair lowers it to its
 // k-th key (atomic min), and a pair starts from it and re-reads it every chunk, so only the
 // first pairs of a query offer many candidates.  tau_q is always the k-th key of some of the
 // query's candidates, never below the final k-th, so no key of the final k best is filtered.
 
-// A workgroup of NT threads (NT / 64 waves) takes items of NT / 64 pairs and streams the list in
-// chunks of NT rows (each thread copies a code row and its id; each lane scores 4 rows a chunk).
-// Candidate buffers of 128 keys (k kept plus one offer of 64) leave room for the 2 x 256-row ring
-// beside the 64 KB of tables at two workgroups per CU.
+// 64 KB of tables, 4 KB of candidate buffers (128 keys a wave: k kept plus one offer of 64) and
+// 8 KB of chunk scores fit two workgroups per CU.
 constexpr int kListThreads = 256;    // 4 pairs per item; two workgroups per CU overlap their phases
 constexpr int kListQb = kListThreads / 64;
-constexpr int kListRing = 2;
-constexpr int kListChunkRows = 256;  // rows per ring chunk: 4 per lane of each wave
-constexpr int kListRowBytes = 20;    // a 16-byte code row and its 4-byte id
+constexpr int kListChunkRows = 256;  // rows per chunk: one per lane of each wave
 constexpr int kListCapw = 128;       // candidate keys per wave: k kept + one offer of 64
 // The list path takes k <= 48: at larger k a wave's buffer, holding k keys after each sort, fills
 // with any later offer, so nearly every offer sorts it again (1M rows, 1024-component mixture,
@@ -110,18 +110,6 @@ struct ListArgs {
     unsigned long long *pair_out;  // nq * nprobe * k keys: each pair's k best, ~0 past its count
     unsigned long long *tau_q;     // nq keys (~0 before the launch): the k-th best key found so far
 };
-
-// LDS of k_ivfpq_lists with NT threads, one object with the tables first: a wave's table then
-// lies at a constant address below 64 KB, and a lookup takes it as the instruction's offset.
-template <int NT>
-struct ListLds {
-    float lut[NT / 64][16 * 256];                              // the ADC tables of the item's pairs
-    unsigned long long cand[(NT / 64) * kListCapw];            // candidates (residuals before the scan)
-    unsigned char ring[kListRing * kListChunkRows * kListRowBytes];  // chunks: code rows, then ids
-    uint32_t tau[2 * (NT / 64)];                               // per wave, two slots: a DMA'd score word
-    uint32_t item;
-};
-
 
 namespace {
 
@@ -433,28 +421,6 @@ __device__ __forceinline__ void lds_read_pair(uint32_t a0, uint32_t a1, uint32_t
     }
 }
 
-// Reads the 16-byte code rows at LDS byte addresses a + 1024 st and the ids at i + 256 st (rows
-// lane + 64 st of a chunk), st < R, with one wait.
-template <int R>
-__device__ __forceinline__ void lds_read_rows(uint32_t a, uint32_t i, uint4 (&w)[R], uint32_t (&id)[R]);
-template <>
-__device__ __forceinline__ void lds_read_rows<4>(uint32_t a, uint32_t i, uint4 (&w)[4], uint32_t (&id)[4]) {
-    asm volatile(
-        "ds_read_b128 %0, %8\n\t"
-        "ds_read_b128 %1, %8 offset:1024\n\t"
-        "ds_read_b128 %2, %8 offset:2048\n\t"
-        "ds_read_b128 %3, %8 offset:3072\n\t"
-        "ds_read_b32 %4, %9\n\t"
-        "ds_read_b32 %5, %9 offset:256\n\t"
-        "ds_read_b32 %6, %9 offset:512\n\t"
-        "ds_read_b32 %7, %9 offset:768\n\t"
-        "s_waitcnt lgkmcnt(0)"
-        : "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]), "=&v"(w[3]), "=&v"(id[0]), "=&v"(id[1]), "=&v"(id[2]),
-          "=&v"(id[3])
-        : "v"(a), "v"(i)
-        : "memory");
-}
-
 template <int NV>
 __device__ __forceinline__ float ring_score(const float *lut, const uint4 (&w)[NV]) {
     constexpr int KS = 256;
@@ -469,39 +435,6 @@ __device__ __forceinline__ float ring_score(const float *lut, const uint4 (&w)[N
             const float d2 = L[2 * KS + ((ww[h] >> 16) & 255u)], d3 = L[3 * KS + (ww[h] >> 24)];
             total += (d0 + d1) + (d2 + d3);
         }
-    }
-    return total;
-}
-
-// Byte B of w times 4 (a table offset in bytes) in one SDWA shift.
-template <int B>
-__device__ __forceinline__ uint32_t byte_x4(uint32_t w) {
-    uint32_t a;
-    if constexpr (B == 0)
-        asm("v_lshlrev_b32_sdwa %0, 2, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_0" : "=v"(a) : "v"(w));
-    else if constexpr (B == 1)
-        asm("v_lshlrev_b32_sdwa %0, 2, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_1" : "=v"(a) : "v"(w));
-    else if constexpr (B == 2)
-        asm("v_lshlrev_b32_sdwa %0, 2, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_2" : "=v"(a) : "v"(w));
-    else
-        asm("v_lshlrev_b32_sdwa %0, 2, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_3" : "=v"(a) : "v"(w));
-    return a;
-}
-// ring_score<1> of one row against table `lut` at a constant LDS address: each lookup is one
-// SDWA shift of the code byte plus an LDS read with the table's address as its offset.  Same
-// summation order.
-__device__ __forceinline__ float row_score_at(const float *lut, uint4 w) {
-    const char *base = reinterpret_cast<const char *>(lut);
-    const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
-    float total = 0.0f;
-#pragma unroll
-    for (int h = 0; h < 4; ++h) {
-        const char *L = base + 4 * h * 1024;
-        const float d0 = *reinterpret_cast<const float *>(L + byte_x4<0>(ww[h]));
-        const float d1 = *reinterpret_cast<const float *>(L + 1024 + byte_x4<1>(ww[h]));
-        const float d2 = *reinterpret_cast<const float *>(L + 2048 + byte_x4<2>(ww[h]));
-        const float d3 = *reinterpret_cast<const float *>(L + 3072 + byte_x4<3>(ww[h]));
-        total += (d0 + d1) + (d2 + d3);
     }
     return total;
 }
@@ -697,30 +630,69 @@ __global__ __launch_bounds__(kScanThreads) void k_ivfpq_scan(ScanArgs A) {
     }
 }
 
-template <int MT, int DS, int NT>
-__global__ __launch_bounds__(NT) void k_ivfpq_lists(ListArgs L) {
-    constexpr int M = 16, KS = 256;
-    constexpr int kListQb = NT / 64, kListChunk = kListChunkRows, kListThreads = NT;
-    static_assert(kListChunk == NT, "a chunk is one code row and one id per thread");
+// LDS of k_ivfpq_lists, the tables first: they lie at LDS offset 0, so a lookup takes its
+// sub-space's table address as the instruction's offset.
+struct ListLds {
+    float4 lut[16 * 256];                                  // entry (m, e): the four pairs' values
+    unsigned long long cand[kListQb * kListCapw];          // candidates (residuals before the scan)
+    float score[2][kListQb][kListChunkRows];               // per chunk parity: each pair's row scores
+    uint32_t item;
+};
+
+// Byte B of w times 16 (an offset into the float4 tables) in one SDWA shift.
+template <int B>
+__device__ __forceinline__ uint32_t byte_x16(uint32_t w) {
+    uint32_t a;
+    if constexpr (B == 0)
+        asm("v_lshlrev_b32_sdwa %0, 4, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_0" : "=v"(a) : "v"(w));
+    else if constexpr (B == 1)
+        asm("v_lshlrev_b32_sdwa %0, 4, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_1" : "=v"(a) : "v"(w));
+    else if constexpr (B == 2)
+        asm("v_lshlrev_b32_sdwa %0, 4, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_2" : "=v"(a) : "v"(w));
+    else
+        asm("v_lshlrev_b32_sdwa %0, 4, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_3" : "=v"(a) : "v"(w));
+    return a;
+}
+
+// The four pairs' scores of one code row (16 bytes) against the float4 tables at LDS offset 0:
+// per pair, sum over words h of ((d0 + d1) + (d2 + d3)).
+__device__ __forceinline__ float4 row_score4(const float4 *lut, uint4 w) {
+    const char *base = reinterpret_cast<const char *>(lut);
+    const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+    float4 total = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+        const char *L = base + 4 * h * 4096;
+        const float4 d0 = *reinterpret_cast<const float4 *>(L + byte_x16<0>(ww[h]));
+        const float4 d1 = *reinterpret_cast<const float4 *>(L + 4096 + byte_x16<1>(ww[h]));
+        const float4 d2 = *reinterpret_cast<const float4 *>(L + 8192 + byte_x16<2>(ww[h]));
+        const float4 d3 = *reinterpret_cast<const float4 *>(L + 12288 + byte_x16<3>(ww[h]));
+        total.x += (d0.x + d1.x) + (d2.x + d3.x);
+        total.y += (d0.y + d1.y) + (d2.y + d3.y);
+        total.z += (d0.z + d1.z) + (d2.z + d3.z);
+        total.w += (d0.w + d1.w) + (d2.w + d3.w);
+    }
+    return total;
+}
+
+template <int MT, int DS>
+__global__ __launch_bounds__(kListThreads) __attribute__((amdgpu_waves_per_eu(2))) void k_ivfpq_lists(ListArgs L) {
+    constexpr int M = 16, KS = 256, QB = kListQb, CH = kListChunkRows;
+    static_assert(kListThreads == KS && CH == 4 * 64 && QB == 4, "a thread per table entry; a row per lane");
     const ScanArgs &A = L.s;
-    // The ring and score words are written by DMAs issued in asm, so the compiler makes no LDS
-    // access wait for them; every read of DMA'd data follows a vmcnt wait and a barrier.
-    __shared__ __attribute__((aligned(16))) ListLds<NT> S;
-    static_assert(kListQb * 128 * sizeof(float) <= sizeof(S.cand), "residuals of dim <= 128 fit");
+    __shared__ __attribute__((aligned(16))) ListLds S;
+    static_assert(QB * 128 * sizeof(float) <= sizeof(S.cand), "residuals of dim <= 128 fit");
     float *s_r = reinterpret_cast<float *>(S.cand);  // residuals, before the scan
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     constexpr int capw = kListCapw;
     unsigned long long *s_w = S.cand + wave * capw;
     const unsigned long long lanes_below = (1ull << lane) - 1ull;
     constexpr bool hib = hib_metric(MT);
-    const uint32_t ring_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)S.ring;
-    const uint32_t tau_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)S.tau;
-    const int wave_u = __builtin_amdgcn_readfirstlane(wave);  // in a scalar register: uniform branches
 
-    // sub-centroid j = tid % 256 of every sub-space, DS floats each (thread-major layout)
+    // sub-centroid tid of every sub-space, DS floats each (thread-major layout)
     float cbr[kLutRegs];
     {
-        const float4 *src = reinterpret_cast<const float4 *>(A.cbt + (size_t)(tid & (KS - 1)) * kLutRegs);
+        const float4 *src = reinterpret_cast<const float4 *>(A.cbt + (size_t)tid * kLutRegs);
 #pragma unroll
         for (int v = 0; v < kLutRegs / 4; ++v) {
             const float4 f = src[v];
@@ -729,37 +701,22 @@ __global__ __launch_bounds__(NT) void k_ivfpq_lists(ListArgs L) {
             cbr[4 * v + 2] = f.z;
             cbr[4 * v + 3] = f.w;
         }
-        // landed before any DMA is issued: the compiler would otherwise wait for them at their
-        // first use with counts that also cover the DMAs, which it does not see
-        __builtin_amdgcn_s_waitcnt(VH_VMCNT(0));
     }
 
-    // Items are claimed one ahead: the claim of the next item is in flight during this one's
-    // table build.
     uint32_t next = 0;
     if (tid == 0) next = atomicAdd(L.work, 1u);
     const uint32_t n_items = *L.n_items;
     for (;;) {
         if (tid == 0) S.item = next;
-        lds_barrier();  // also: every wave is past the previous item (its candidates and ring)
+        lds_barrier();  // also: every wave is past the previous item (its tables, scores and candidates)
         const uint32_t it = S.item;
         if (it >= n_items) break;
-        // the item's record and pair ids in one round trip
         const uint4 item = L.items[it], ip = L.item_pairs[it];
         const uint32_t list = item.x, beg = item.z, len = item.w >> 3, npairs = item.w & 7u;
         auto pair_of = [&](int sl) { return sl == 0 ? ip.x : sl == 1 ? ip.y : sl == 2 ? ip.z : ip.w; };
-        const int nch = (int)((len + kListChunk - 1) / kListChunk);
-        // chunk c of the list into ring slot c % kListRing: every thread copies a code row and its id
-        // row each, the others its id (rows past the list's end repeat its last row, never
-        // scored; chunks c >= nch re-read it into a slot no wave reads any more).  len > 0.
-        auto chunk_dma = [&](int c) {
-            const uint32_t slot = ring_lds + (uint32_t)((c % kListRing) * (kListChunk * kListRowBytes));
-            const uint32_t i = min((uint32_t)(c * kListChunk + tid), len - 1);
-            dma_lds16(A.codes + (size_t)(beg + i) * 16, slot + 16 * 64 * wave_u);
-            dma_lds4(A.ids + beg + i, slot + 16 * kListChunk + 4 * 64 * wave_u);
-        };
+        const int nch = (int)((len + CH - 1) / CH);
         // residuals q - c of the item's pairs (zero rows for unused slots)
-        for (int t = tid; t < kListQb * A.dim; t += kListThreads) {
+        for (int t = tid; t < QB * A.dim; t += kListThreads) {
             const int sl = t / A.dim, d = t - sl * A.dim;
             float r = 0.0f;
             if (sl < (int)npairs) {
@@ -768,38 +725,44 @@ __global__ __launch_bounds__(NT) void k_ivfpq_lists(ListArgs L) {
             }
             s_r[t] = r;
         }
-        // the wave's pair and its query's k-th best key so far (read before the ring's DMAs)
+        // the wave's pair (wave q offers pair q's candidates) and its query's k-th best key so far
         const bool active = wave < (int)npairs;
-        const uint32_t pid = pair_of(wave_u);  // an unused slot repeats the first pair
+        const uint32_t pid = pair_of(wave);  // an unused slot repeats the first pair
         const uint32_t qid = pid / (uint32_t)A.nprobe;
         unsigned long long tau = __hip_atomic_load(L.tau_q + qid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (!active) tau = ~0ull;
+        const uint32_t *tau_hi = reinterpret_cast<const uint32_t *>(L.tau_q + qid) + 1;
+        // chunk c's loads: this lane's code row (row 64 wave + lane), the ids of the rows the wave
+        // offers (rows lane + 64 st; rows past the list's end repeat its last row, never used) and
+        // the score word of the query's k-th best key as other pairs have left it so far
+        auto load_chunk = [&](int c, uint4 &w, uint32_t (&id)[4], uint32_t &th) {
+            const uint32_t r = min((uint32_t)(c * CH + 64 * wave + lane), len - 1);
+            w = *reinterpret_cast<const uint4 *>(A.codes + (size_t)(beg + r) * 16);
+#pragma unroll
+            for (int st = 0; st < 4; ++st) id[st] = A.ids[beg + min((uint32_t)(c * CH + 64 * st + lane), len - 1)];
+            th = __hip_atomic_load(tau_hi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        };
+        uint4 wa, wb;
+        uint32_t ida[4], idb[4], tha, thb;
+        // the first chunk's loads are in flight during the table build, except for cosine, whose
+        // build needs their registers (three sums a step) to stay at two waves per SIMD
+        if constexpr (MT != COS) load_chunk(0, wa, ida, tha);
+        if (tid == 0) next = atomicAdd(L.work, 1u);  // the next item's claim, in flight during the build
         lds_barrier();  // residuals visible
-        // the first chunks land while the tables are built; no other load is in flight after them
-        __builtin_amdgcn_s_waitcnt(VH_VMCNT(0));
-        if (nch > 0)
-            for (int c = 0; c < kListRing - 1; ++c) chunk_dma(c);
-        // the next item's claim, in flight while the tables are built (the claim's wave waits
-        // for it with the first chunk; the atomic is not wave-aggregated, see the Makefile)
-        if (tid == 0) next = atomicAdd(L.work, 1u);
-        // ADC tables (ProductQuantizer::compute_adc_lut, pq.rs:233-266): thread j of half h
-        // computes entry j of every sub-space for the slots h, h + 2, ...  A slot's 16 entries
-        // are stored after all are computed: a store between the residual reads would keep the
-        // compiler from issuing the reads ahead (it cannot tell the two regions apart), and each
-        // sub-space would wait for its own LDS round trip.
-        {
-            const int j = tid & (KS - 1), h = tid >> 8;
-            for (int sl = h; sl < (int)npairs; sl += (kListThreads + KS - 1) / KS) {
+        // ADC tables (ProductQuantizer::compute_adc_lut, pq.rs:233-266): thread j computes entry j
+        // of every sub-space for one slot at a time and stores it in component `slot` of the
+        // entry's float4 (one slot at a time keeps the registers beside the codebook's few)
+#pragma unroll
+        for (int sl = 0; sl < QB; ++sl) {
+            float e[M];
+            {
                 const float *r = s_r + sl * A.dim;
-                float e[M];
-                constexpr int MB = 4, NR = MB * DS / 4;  // sub-spaces per batch, float4 reads per batch
+                constexpr int MB = 4, NR = MB * DS / 4;
 #pragma unroll
                 for (int m0 = 0; m0 < M; m0 += MB) {
-                    // the batch's residual values in one round of reads
                     float4 rv[NR];
 #pragma unroll
                     for (int i = 0; i < NR; ++i) rv[i] = *reinterpret_cast<const float4 *>(r + m0 * DS + 4 * i);
-                    __builtin_amdgcn_sched_barrier(0);  // all of them issued before the first use
 #pragma unroll
                     for (int mm = 0; mm < MB; ++mm) {
                         const int m = m0 + mm;
@@ -815,81 +778,58 @@ __global__ __launch_bounds__(NT) void k_ivfpq_lists(ListArgs L) {
                         e[m] = acc.finish();
                     }
                 }
-                float *lut = &S.lut[sl][j];
-#pragma unroll
-                for (int m = 0; m < M; ++m) lut[m * KS] = e[m];
             }
+#pragma unroll
+            for (int m = 0; m < M; ++m) reinterpret_cast<float *>(&S.lut[m * KS + tid])[sl] = e[m];
         }
+        if constexpr (MT == COS) load_chunk(0, wa, ida, tha);
         uint32_t cnt = 0;
-        // score word of the query's k-th best key (the high half: a 4-byte read cannot tear)
-        const uint32_t *tau_hi = reinterpret_cast<const uint32_t *>(L.tau_q + qid) + 1;
-        static_assert(kListRing == 2, "the wait below covers the DMAs of a 2-chunk ring");
-        for (int c = 0; c < nch; ++c) {
-            // Iteration c - 1 issued the score word and chunk c (the item's start, chunk 0): all
-            // have landed for this wave.
-            __builtin_amdgcn_s_waitcnt(VH_VMCNT(0));
-            // every share of chunk c has landed and every wave is done with chunk c - 1 (and, at
-            // c = 0, with the tables' build and the residuals, whose region the candidates reuse)
-            lds_barrier();
-            if (c >= 1) {
-                // the query's k-th best score as other pairs have left it; keys of that score
-                // pass (a tie's id is not read), so the filter stays conservative
-                const unsigned long long ext =
-                    ((unsigned long long)S.tau[2 * wave + ((c - 1) & 1)] << 32) | 0xffffffffull;
-                tau = ext < tau ? ext : tau;
-            }
-            if (lane == 0) dma_lds4(tau_hi, tau_lds + 4 * (2 * wave_u + (c & 1)));
-            chunk_dma(c + kListRing - 1);
+        // tables visible; every residual read (the candidate buffers' LDS) done
+        lds_barrier();
+        // chunk c: score this wave's rows for the four pairs, then (after the barrier) offer pair
+        // `wave`'s 256 scores
+        auto do_chunk = [&](int c, const uint4 &w, const uint32_t (&id)[4], uint32_t ext_hi) {
+            const float4 t4 = row_score4(S.lut, w);
+            float *sc = &S.score[c & 1][0][64 * wave + lane];
+            sc[0 * CH] = t4.x;
+            sc[1 * CH] = t4.y;
+            sc[2 * CH] = t4.z;
+            sc[3 * CH] = t4.w;
+            lds_barrier();  // the chunk's scores visible; every wave past chunk c - 2's reads
             if (active) {
-                // the lane's 4 rows of the chunk (rows lane + 64 st) and their ids, one wait: the 64
-                // table lookups of the 4 scores are then independent and overlap
-                constexpr int RPL = kListChunk / 64;  // rows per lane
-                const uint32_t cb = ring_lds + (uint32_t)((c % kListRing) * (kListChunk * kListRowBytes));
-                uint4 w[RPL];
-                uint32_t id[RPL];
-                lds_read_rows<RPL>(cb + 16 * lane, cb + 16 * kListChunk + 4 * lane, w, id);
-                float tot[RPL];
-                // the wave's table at a constant address: one copy of the scoring per wave
-                switch (wave_u) {
-                    case 0:
+                // the query's k-th best score as other pairs have left it; keys of that score pass
+                // (a tie's id is not read), so the filter stays conservative
+                const unsigned long long ext = ((unsigned long long)ext_hi << 32) | 0xffffffffull;
+                tau = ext < tau ? ext : tau;
+                float tot[4];
 #pragma unroll
-                        for (int st = 0; st < RPL; ++st) tot[st] = row_score_at(S.lut[0], w[st]);
-                        break;
-                    case 1:
-#pragma unroll
-                        for (int st = 0; st < RPL; ++st) tot[st] = row_score_at(S.lut[1], w[st]);
-                        break;
-                    case 2:
-#pragma unroll
-                        for (int st = 0; st < RPL; ++st) tot[st] = row_score_at(S.lut[2], w[st]);
-                        break;
-                    default:
-#pragma unroll
-                        for (int st = 0; st < RPL; ++st) tot[st] = row_score_at(S.lut[3], w[st]);
-                        break;
-                }
+                for (int st = 0; st < 4; ++st) tot[st] = S.score[c & 1][wave][64 * st + lane];
                 // Pre-filter: a key below tau has a score at most key_score(tau's score word) (NaN
                 // scores, and tau = ~0, pass), so a chunk none of whose rows passes offers nothing.
                 const float thr = key_score((uint32_t)(tau >> 32));
                 bool maybe = false;
 #pragma unroll
-                for (int st = 0; st < RPL; ++st) {
+                for (int st = 0; st < 4; ++st) {
                     const float hs = (hib ? -tot[st] : tot[st]) + 0.0f;
-                    maybe |= !(hs > thr) && (uint32_t)(c * kListChunk + st * 64 + lane) < len;
+                    maybe |= !(hs > thr) && (uint32_t)(c * CH + st * 64 + lane) < len;
                 }
                 if (__ballot(maybe) != 0ull) {
 #pragma unroll
-                    for (int st = 0; st < RPL; ++st) {
+                    for (int st = 0; st < 4; ++st) {
                         if (cnt > (uint32_t)(capw - 64)) wave_compact(s_w, cnt, tau, A.k);
                         const uint32_t row = (uint32_t)(st * 64 + lane);
-                        offer<hib>(tot[st], (uint32_t)(c * kListChunk) + row < len, id[st], s_w, cnt, tau,
-                                   lanes_below);
+                        offer<hib>(tot[st], (uint32_t)(c * CH) + row < len, id[st], s_w, cnt, tau, lanes_below);
                     }
                 }
             }
+        };
+        // two register sets, so that no loaded value is copied (a copy would wait for its load)
+        for (int c = 0; c < nch; c += 2) {
+            load_chunk(c + 1, wb, idb, thb);
+            do_chunk(c, wa, ida, tha);
+            load_chunk(c + 2, wa, ida, tha);
+            if (c + 1 < nch) do_chunk(c + 1, wb, idb, thb);
         }
-        // the last re-read chunks have landed before any wave's next item writes the ring
-        __builtin_amdgcn_s_waitcnt(VH_VMCNT(0));
         if (active) {
             wave_compact(s_w, cnt, tau, A.k);  // sorted, at most k kept
             for (int j = lane; j < A.k; j += 64)
@@ -948,12 +888,12 @@ __global__ __launch_bounds__(256) void k_ivfpq_merge(ListArgs L, int P) {
 template <int MT>
 void launch_lists_mt(const ListArgs &L, int ds, int cus, hipStream_t s) {
     // persistent: as many workgroups as fit (each CU holds 163840 bytes of LDS)
-    const size_t per_cu = std::max<size_t>(1, 163840 / (sizeof(ListLds<kListThreads>) + 256));
+    const size_t per_cu = std::max<size_t>(1, 163840 / (sizeof(ListLds) + 256));
     const unsigned grid = (unsigned)((size_t)cus * per_cu);
     if (ds == 4)
-        hipLaunchKernelGGL((k_ivfpq_lists<MT, 4, kListThreads>), dim3(grid), dim3(kListThreads), 0, s, L);
+        hipLaunchKernelGGL((k_ivfpq_lists<MT, 4>), dim3(grid), dim3(kListThreads), 0, s, L);
     else
-        hipLaunchKernelGGL((k_ivfpq_lists<MT, 8, kListThreads>), dim3(grid), dim3(kListThreads), 0, s, L);
+        hipLaunchKernelGGL((k_ivfpq_lists<MT, 8>), dim3(grid), dim3(kListThreads), 0, s, L);
 }
 
 template <bool HIB>
