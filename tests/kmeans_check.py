@@ -38,5 +38,41 @@ def check_step(oracle, data, cent, got, metric, max_flip_frac=1e-4):
     for c in np.nonzero(same)[0]:
         want = ref["centroids"][c]
         assert np.linalg.norm(got["centroids"][c] - want) <= 1e-4 * max(np.linalg.norm(want), 1e-6)
-    assert abs(got["inertia"] - ref["inertia"]) <= 1e-4 * abs(ref["inertia"]) + 1e-3
+    if metric in ("dot", "cosine"):
+        # The GPU reports kmeans.cu:110-170's per-point values, -dot and 1 - cos (the oracle's
+        # KMeans::fit step sums the similarities themselves): the sum over the GPU's own
+        # assignment, in float64.
+        x = data.astype(np.float64)
+        c = cent.astype(np.float64)[ga]
+        dots = np.einsum("ij,ij->i", x, c)
+        if metric == "dot":
+            want = -dots.sum()
+        else:
+            den = np.sqrt(np.einsum("ij,ij->i", x, x)) * np.sqrt(np.einsum("ij,ij->i", c, c))
+            want = np.sum(1.0 - np.where(den > 1e-9, dots / np.where(den > 1e-9, den, 1.0), 0.0))
+        assert abs(got["inertia"] - want) <= 1e-5 * abs(want) + 1e-3 * max(1.0, len(data) * 1e-4), \
+            f"inertia {got['inertia']} against {want}"
+    else:
+        assert abs(got["inertia"] - ref["inertia"]) <= 1e-4 * abs(ref["inertia"]) + 1e-3
     return len(flips)
+
+
+def check_chain(vh, oracle, data, init, iters, metric, fit_centroids, fit_assign, fit_inertia,
+                max_flip_frac=1e-4):
+    """A chained fit, pinned step by step: fit()'s centroids, assignment and inertia after `iters`
+    iterations from `init` equal those of a GPU state stepped `iters` times from `init` (bit for
+    bit: the same kernels in the same order), and every one of those steps passes check_step
+    against the oracle's step from the GPU's previous centroids.  Returns the flips per step."""
+    st = vh.KMeansState(data, metric=vh.DistanceMetric(oracle.METRICS[metric]))
+    cent = np.array(init, np.float32)
+    st.set_centroids(cent)
+    flips = []
+    for _ in range(iters):
+        st.run(1)
+        got = st.read()
+        flips.append(check_step(oracle, data, cent, got, metric, max_flip_frac))
+        cent = got["centroids"]
+    assert np.array_equal(fit_centroids.reshape(cent.shape), cent)
+    assert np.array_equal(fit_assign, got["assign"])
+    assert fit_inertia == got["inertia"]
+    return flips

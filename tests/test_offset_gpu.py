@@ -11,7 +11,7 @@ gets wrong (tests/test_offset_host.py replays it on the CPU and shows the failur
 import numpy as np
 import pytest
 
-from kmeans_check import check_step
+from kmeans_check import check_chain, check_step
 from knn_check import check_knn
 
 pytestmark = pytest.mark.gpu
@@ -149,11 +149,10 @@ def test_kmeans_fit_offset_vs_oracle(vh, oracle, metric):
     init = data[:32].copy()
     m = vh.DistanceMetric(oracle.METRICS[metric])
     r, assign = vh.CudaKMeansEngine().fit(data, 48, 32, 4, -1.0, m, init=init, return_assign=True)
-    ref = oracle.kmeans_fit(data, init, 4, -1.0, metric)
-    assert np.mean(ref["assign"] != assign) <= 1e-3
-    ok = np.linalg.norm(r.centroids.reshape(32, 48) - ref["centroids"], axis=1) <= \
-        1e-4 * np.linalg.norm(ref["centroids"], axis=1)
-    assert np.mean(ok) >= 0.9
+    # each of the 4 iterations against the oracle's step from the GPU's previous centroids (near-tie
+    # flips only, centroids within 1e-4 of the mean of the points assigned), and fit() equal to
+    # those 4 steps bit for bit
+    check_chain(vh, oracle, data, init, 4, metric, r.centroids, assign, r.inertia)
 
 
 def test_kmeans_cosine_offset_assign_near_optimal(vh, oracle):
