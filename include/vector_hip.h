@@ -196,7 +196,12 @@ int vhip_kmeans_fit(int ordinal, const float *data, size_t n, size_t dim, size_t
 int vhip_dkmeans_check(size_t num_gpus);
 
 /* Resident k-means state for per-iteration use (no reference counterpart: it exposes
- * one Lloyd step for parity checks and the per-iteration benchmark). */
+ * one Lloyd step for parity checks and the per-iteration benchmark).  Every state, also the
+ * one vhip_kmeans_fit makes, assigns squared L2, dot product and cosine on the FP32 matrix
+ * cores, except small point sets (fewer than 128 points per compute unit, at most 256
+ * centroids and 1e6 point-centroid pairs), which take the direct form on the vector units;
+ * the environment variable VHIP_KMEANS_ASSIGN=mfma at creation keeps those on the matrix
+ * cores.  Both give the reference's assignment. */
 typedef struct vhip_kmeans vhip_kmeans;
 int vhip_kmeans_create(int ordinal, const float *data, size_t n, size_t dim, int metric, vhip_kmeans **out);
 /* The same state from nseg host segments (segment i: counts[i] rows of dim floats) uploaded one

@@ -109,7 +109,7 @@ def test_mixture_10_iterations_parity(vh, oracle):
 
 
 @pytest.mark.parametrize("metric", ["dot", "cosine", "l1", "linf", "minkowski", "hellinger", "jaccard", "mahalanobis"])
-def test_other_metrics_one_step(vh, oracle, metric):
+def test_other_metrics_one_step(vh, oracle, metric, assign_path):
     from vector_hip import datasets as ds
 
     data, _, _ = ds.gaussian_mixture(8_000, 40, 32, 11)
@@ -125,7 +125,7 @@ def test_other_metrics_one_step(vh, oracle, metric):
     _check_step(oracle, data, cent, got, metric, max_flip_frac=2.5e-4)
 
 
-def test_fit_deterministic_and_explicit_init(vh, oracle):
+def test_fit_deterministic_and_explicit_init(vh, oracle, assign_path):
     from vector_hip import datasets as ds
 
     data, _, _ = ds.gaussian_mixture(30_000, 96, 128, 5)
@@ -188,7 +188,7 @@ def test_tolerance_stops_early(vh):
 
 
 @pytest.mark.parametrize("dim", [256, 200])
-def test_high_dimension_one_step(vh, oracle, dim):
+def test_high_dimension_one_step(vh, oracle, dim, assign_path):
     """k-means assign above 128 dimensions: the panel kernel (256) and the streaming kernel (200)."""
     from vector_hip import datasets as ds
 
@@ -260,3 +260,28 @@ def test_kmeanspp_matches_its_restatement(vh, n, dim, k, seed, spread):
     assert (kk, iters) == (k, 0)
     want = x[_kmeanspp_restated(x, k, seed)]
     assert np.array_equal(c, want)
+
+
+@pytest.mark.parametrize("metric,dim", [("l2", 96), ("dot", 40), ("cosine", 768), ("l2", 200)])
+def test_small_set_direct_assign_matches_mfma(vh, oracle, monkeypatch, metric, dim):
+    """The direct-form assignment of small point sets and the MFMA scan with its certified
+    selection give the same assignments on well-separated clusters (no near-ties), and centroids
+    and inertia that agree to rounding, over 3 iterations."""
+    from vector_hip import datasets as ds
+
+    data, _, _ = ds.gaussian_mixture(6_000, dim, 24, 21)
+    data = (data * 4.0 + (3.0 if metric != "l2" else 0.0)).astype(np.float32)
+    m = vh.DistanceMetric(oracle.METRICS[metric])
+    init = data[:24].copy()
+    out = {}
+    for path in ("direct", "mfma"):
+        if path == "mfma":
+            monkeypatch.setenv("VHIP_KMEANS_ASSIGN", "mfma")
+        else:
+            monkeypatch.delenv("VHIP_KMEANS_ASSIGN", raising=False)
+        out[path] = vh.CudaKMeansEngine().fit(data, dim, 24, 3, -1.0, m, init=init, return_assign=True)
+    (rd, ad), (rm, am) = out["direct"], out["mfma"]
+    assert np.array_equal(ad, am)
+    c_d, c_m = rd.centroids.reshape(24, dim), rm.centroids.reshape(24, dim)
+    assert np.all(np.linalg.norm(c_d - c_m, axis=1) <= 1e-6 * np.maximum(np.linalg.norm(c_m, axis=1), 1e-6))
+    assert abs(rd.inertia - rm.inertia) <= 1e-5 * abs(rm.inertia) + 1e-3

@@ -97,7 +97,7 @@ def test_l2_max_k_float_and_integer(vh, oracle):
 
 
 @pytest.mark.parametrize("offset", [100.0, 1000.0])
-def test_kmeans_step_offset_data(vh, oracle, offset):
+def test_kmeans_step_offset_data(vh, oracle, offset, assign_path):
     from vector_hip import datasets as ds
 
     data, _, _ = ds.gaussian_mixture(20_000, 96, 64, 13)
@@ -112,7 +112,7 @@ def test_kmeans_step_offset_data(vh, oracle, offset):
         cent = got["centroids"]
 
 
-def test_kmeans_wide_range_clusters(vh, oracle):
+def test_kmeans_wide_range_clusters(vh, oracle, assign_path):
     """Clusters at |x| ~ 1e4 (spread 1) and at |x| ~ 1e-2 (spread 1e-3) in one dataset: the small
     ones sit 5e3 from the column means, so the assignment goes through the direct-form fix-up, and
     the update must keep 1e-4 of their norm (per-cluster fixed-point scales)."""
@@ -141,7 +141,7 @@ def test_kmeans_wide_range_clusters(vh, oracle):
 
 
 @pytest.mark.parametrize("metric", ["l2", "dot"])
-def test_kmeans_fit_offset_vs_oracle(vh, oracle, metric):
+def test_kmeans_fit_offset_vs_oracle(vh, oracle, metric, assign_path):
     from vector_hip import datasets as ds
 
     data, _, _ = ds.gaussian_mixture(12_000, 48, 32, 15)
@@ -155,7 +155,7 @@ def test_kmeans_fit_offset_vs_oracle(vh, oracle, metric):
     check_chain(vh, oracle, data, init, 4, metric, r.centroids, assign, r.inertia)
 
 
-def test_kmeans_cosine_offset_assign_near_optimal(vh, oracle):
+def test_kmeans_cosine_offset_assign_near_optimal(vh, oracle, assign_path):
     """Cosine at offset 500: every similarity lies within ~1e-6 of 1, so which of several
     centroids wins is decided by fp32 rounding, in the reference as here.  Every GPU assignment must
     be optimal up to that rounding: its direct-form similarity (the oracle's) within 1e-5 of the

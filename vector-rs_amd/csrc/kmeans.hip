@@ -34,6 +34,8 @@
 // With tol < 0 no per-iteration host synchronisation happens.
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
+#include <cstring>
 #include <memory>
 
 #include "vh_runtime.h"
@@ -737,6 +739,7 @@ struct vhip_kmeans {
     size_t n = 0, n_pad = 0, dim = 0, dpad = 0, k = 0, kpad = 0;
     int metric = 0;
     int grid_cap = 512;
+    bool direct_small = true;  // small point sets take the direct-form assignment
     float absmax = 0.0f;     // max |x| over the points
     float err_coeff = 0.0f;  // selection error coefficient of the MFMA assignment
     bool assigned = false;
@@ -789,6 +792,8 @@ static int km_create(int ordinal, const float *const *segs, const size_t *counts
     K->dpad = round_up(dim, kKChunk);
     K->metric = metric;
     K->grid_cap = device_grid_cap(ordinal);
+    // VHIP_KMEANS_ASSIGN=mfma keeps small point sets on the MFMA assignment (tests of both paths)
+    if (const char *e = std::getenv("VHIP_KMEANS_ASSIGN")) K->direct_small = std::strcmp(e, "mfma") != 0;
     hipStream_t s;
     VH_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
     K->stream = s;
@@ -908,7 +913,15 @@ static int km_assign(vhip_kmeans *K) {
     const int n = (int)K->n, k = (int)K->k;
     launch_fill_u32(K->counts.as<uint32_t>(), k, 0u, s);
     const int t = K->timer.begin(s);
-    if (is_gemm_metric(K->metric)) {
+    // small point sets: the direct form for every point (no MFMA tiles, no fix-up)
+    const bool small = is_gemm_metric(K->metric) && K->direct_small &&
+                       kmeans_assign_small_ok(n, k, (int)K->dpad, K->grid_cap / 2);
+    if (small) {
+        launch_fill_u32(K->devmax.as<uint32_t>(), k, 0u, s);
+        launch_kmeans_assign_small(K->metric, K->points(), (int)K->dpad, n, K->craw.as<float>(), k,
+                                   K->assign.as<int32_t>(), K->inertia.as<float>(), K->pos.as<int32_t>(),
+                                   K->counts.as<int32_t>(), K->devmax.as<float>(), s);
+    } else if (is_gemm_metric(K->metric)) {
         launch_fill_u32(K->devmax.as<uint32_t>(), k, 0u, s);
         launch_fill_u32(K->nfix.as<uint32_t>(), 1, 0u, s);
         AssignCert cert;
@@ -930,7 +943,7 @@ static int km_assign(vhip_kmeans *K) {
     const double work = (is_gemm_metric(K->metric) ? 2.0 : 1.0) * (double)n * k * (double)K->dim;
     K->timer.end(t, s, work, ((double)n + k) * K->dim * 4.0);
     VH_HIP(hipGetLastError());
-    if (is_gemm_metric(K->metric)) {
+    if (is_gemm_metric(K->metric) && !small) {
         launch_kmeans_fix(K->metric, K->points(), (int)K->dpad, K->fix.as<int32_t>(), K->nfix.as<uint32_t>(),
                           K->craw.as<float>(), k, K->best.as<unsigned long long>(), K->assign.as<int32_t>(),
                           K->inertia.as<float>(), K->pos.as<int32_t>(), K->counts.as<int32_t>(),

@@ -457,6 +457,131 @@ void launch_kmeans_fix(int metric, const float *pts, int dpad, const int32_t *fi
                        devmax);
 }
 
+// ---------------------------------------------------------------------------------
+// Small point sets.  The MFMA assignment spreads 128-point column tiles over the CUs and pads the
+// centroid rows to 256, so below 128 points per CU most of the GPU idles, and a small k wastes
+// most of each tile.  There every point takes the fix-up's direct form instead, which needs no
+// selection bound: L lanes per point, each holding a strided slice of its dimensions (NS float4
+// at most) in registers, 64 / L points per wave; the centroids stream through L1 four at a
+// time, each lane adding its slice's terms and the L lanes combining them with a fixed xor tree.
+// ---------------------------------------------------------------------------------
+constexpr int kAssignSmallMaxK = 256;           // centroids per point in the direct form, at most
+constexpr long kAssignSmallMaxPairs = 1000000;  // and (point, centroid) pairs: the direct form costs
+// about 1.4 us per centroid at 10,000 x 768 (its lanes' work grows with k), the MFMA scan about
+// 115 us plus its fix-up whatever k up to 256 (its tiles pad k to 256), so the two meet near
+// n k = 1e6
+
+template <int M, int L, int NS>
+__global__ __launch_bounds__(256) void k_kmeans_assign_small(const float *__restrict__ pts, int dpad, int n,
+                                                             const float *__restrict__ cent, int k,
+                                                             int32_t *__restrict__ assign, float *__restrict__ inertia,
+                                                             int32_t *__restrict__ pos, int32_t *__restrict__ counts,
+                                                             float *__restrict__ devmax) {
+    constexpr int PPW = 64 / L;
+    const int lane = threadIdx.x & 63, sub = lane & (L - 1);
+    const int p = (blockIdx.x * 4 + (threadIdx.x >> 6)) * PPW + lane / L;
+    const int pc = min(p, n - 1);  // lanes past the end repeat the last point, unstored
+    const int nc4 = dpad >> 2;
+    const floatx4 *prow = reinterpret_cast<const floatx4 *>(pts + (size_t)pc * dpad);
+    floatx4 x[NS];
+    float pn = 0.0f;  // the point's squared norm (cosine)
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+        const int j = sub + s * L;
+        x[s] = j < nc4 ? prow[j] : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+        if constexpr (M == COS)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) pn = fmaf(x[s][e], x[s][e], pn);
+    }
+    if constexpr (M == COS)
+#pragma unroll
+        for (int o = L / 2; o > 0; o >>= 1) pn += __shfl_xor(pn, o, 64);
+    float bv = INFINITY;
+    int bc = 0;
+    for (int c0 = 0; c0 < k; c0 += 4) {
+        float a[4] = {0.0f, 0.0f, 0.0f, 0.0f}, b[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            const int j = min(sub + s * L, nc4 - 1);  // past the row's end: a zero slice of x
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const floatx4 cv = reinterpret_cast<const floatx4 *>(cent + (size_t)min(c0 + u, k - 1) * dpad)[j];
+                const bool in = sub + s * L < nc4;
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (in) accum<M>(a[u], b[u], x[s][e], cv[e]);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+#pragma unroll
+            for (int o = L / 2; o > 0; o >>= 1) {
+                a[u] += __shfl_xor(a[u], o, 64);
+                if constexpr (M == COS) b[u] += __shfl_xor(b[u], o, 64);
+            }
+            float v;
+            if constexpr (M == L2) {
+                v = a[u];
+            } else if constexpr (M == DOT) {
+                v = -a[u] + 0.0f;
+            } else {
+                const float den = sqrtf(pn) * sqrtf(b[u]);
+                v = den <= 1e-9f ? 0.0f : -(a[u] / den) + 0.0f;
+            }
+            if (v < bv && c0 + u < k) {
+                bv = v;
+                bc = c0 + u;
+            }
+        }
+    }
+    if (sub == 0 && p < n) {
+        assign[p] = bc;
+        pos[p] = atomicAdd(&counts[bc], 1);
+        if constexpr (M == L2) atomicMax((uint32_t *)devmax + bc, __float_as_uint(sqrtf(fmaxf(bv, 0.0f)) * 1.0001f));
+        else inertia[p] = M == DOT ? bv : 1.0f + bv;  // -dot, 1 - cos
+    }
+}
+
+bool kmeans_assign_small_ok(int n, int k, int dpad, int cus) {
+    return n > 0 && n < 128 * cus && k >= 1 && k <= kAssignSmallMaxK && (long)n * k <= kAssignSmallMaxPairs &&
+           dpad <= 1024;
+}
+
+template <int M, int L>
+static void launch_small_l(int dpad, const float *pts, int n, const float *cent, int k, int32_t *assign,
+                           float *inertia, int32_t *pos, int32_t *counts, float *devmax, hipStream_t s) {
+    const dim3 g(ceil_div(n, 4 * (64 / L)));
+    const int ns = ceil_div(dpad / 4, L);
+#define VH_AS(NS)                                                                                                 \
+    hipLaunchKernelGGL((k_kmeans_assign_small<M, L, NS>), g, dim3(256), 0, s, pts, dpad, n, cent, k, assign,     \
+                       inertia, pos, counts, devmax)
+    if (ns <= 2) VH_AS(2);
+    else if (ns <= 4) VH_AS(4);
+    else if (ns <= 8) VH_AS(8);
+    else if (ns <= 12) VH_AS(12);
+    else VH_AS(16);
+#undef VH_AS
+}
+
+template <int M>
+static void launch_small_m(int dpad, const float *pts, int n, const float *cent, int k, int32_t *assign,
+                           float *inertia, int32_t *pos, int32_t *counts, float *devmax, hipStream_t s) {
+    // 8 lanes per point up to 128 dimensions (at most 4 float4 each), 16 above (dpad <= 1024)
+    if (dpad <= 128) launch_small_l<M, 8>(dpad, pts, n, cent, k, assign, inertia, pos, counts, devmax, s);
+    else launch_small_l<M, 16>(dpad, pts, n, cent, k, assign, inertia, pos, counts, devmax, s);
+}
+
+void launch_kmeans_assign_small(int metric, const float *pts, int dpad, int n, const float *cent, int k,
+                                int32_t *assign, float *inertia, int32_t *pos, int32_t *counts, float *devmax,
+                                hipStream_t s) {
+    if (n <= 0 || k <= 0) return;
+    switch (metric) {
+        case L2: launch_small_m<L2>(dpad, pts, n, cent, k, assign, inertia, pos, counts, devmax, s); break;
+        case DOT: launch_small_m<DOT>(dpad, pts, n, cent, k, assign, inertia, pos, counts, devmax, s); break;
+        default: launch_small_m<COS>(dpad, pts, n, cent, k, assign, inertia, pos, counts, devmax, s); break;
+    }
+}
+
 template <int M>
 static void launch_km(int dpad, dim3 g, hipStream_t s, const float *cent, int k, const float *pts, int n, int tiles,
                       int32_t *assign, float *inertia, int32_t *pos, int32_t *counts) {

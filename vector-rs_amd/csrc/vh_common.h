@@ -292,6 +292,14 @@ void launch_kmeans_assign_valu(int metric, const float *cent, int k, const float
 void launch_kmeans_fix(int metric, const float *pts, int dpad, const int32_t *fix, const uint32_t *nfix,
                        const float *cent, int k, unsigned long long *best, int32_t *assign, float *inertia,
                        int32_t *pos, int32_t *counts, float *devmax, int grid_cap, hipStream_t s);
+// Direct-form assignment of small point sets (metric L2 / DOT / COS): every point gets what the
+// fix-up gives a listed point (argmin over the k unshifted centroids, lowest index on ties, on
+// the unshifted points), its ticket, and inertia (dot / cosine) or the deviation bound (squared
+// L2).  kmeans_assign_small_ok says whether a shape takes this path.
+bool kmeans_assign_small_ok(int n, int k, int dpad, int cus);
+void launch_kmeans_assign_small(int metric, const float *pts, int dpad, int n, const float *cent, int k,
+                                int32_t *assign, float *inertia, int32_t *pos, int32_t *counts, float *devmax,
+                                hipStream_t s);
 // shift (may be null): added to every base value as the tiles are read (the direct-form pass of
 // squared L2 over shifted rows that give back the unshifted ones exactly).
 void launch_valu_filter(int metric, const float *base, const float *shift, const float *qry, const float *tau, int nq,
