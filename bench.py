@@ -23,11 +23,13 @@ the oracle's search_with_nprobe), each with its own roofline, CPU baseline and p
 The process exits with status 3, after printing the line, when any parity check fails.
 
 The default line also carries "batch_sweep" (search_batch at batch sizes 1 to 128, as the
-reference's cuda_bench.rs does, each batch checked against the oracle) and "kmeans_fit" (fit() with
-its default k-means++ init, init timed apart from the Lloyd iterations).
+reference's cuda_bench.rs does, each batch checked against the oracle), "kmeans_fit" (fit() with
+its default k-means++ init, init timed apart from the Lloyd iterations) and "reference_published"
+(the shapes of the reference's only published GPU figures: search_batch and fit() on 100,000 x 768
+cosine data, beside those figures).
 
 Other workloads: --workload cos768 | kmeans | hamming | l1 | linf | gauss (see WORKLOADS), ivf_coarse
-(the IVF coarse quantizer), ivfpq (IVF-PQ search), kmeans_fit, batch_sweep, upload (engine builds
+(the IVF coarse quantizer), ivfpq (IVF-PQ search), kmeans_fit, batch_sweep, published, upload (engine builds
 from VECRSTOR files), copy (counter calibration).
 """
 import argparse
@@ -745,6 +747,77 @@ def bench_batch_sweep(vh, reps, with_cpu):
                                              "the device call's"}}
 
 
+# The reference's only published GPU figures (scripts/benchmarks/cuda_benchmark.svg:143, 262 on
+# one NVIDIA T4; they equal the fallback values cuda_benchmark.py:110, 135 substitutes when criterion
+# output is missing, so they are quoted for comparison, never as vs_baseline)
+PUBLISHED_KNN_QPS = 45152.0      # batch kNN, cosine, N = 100,000, D = 768, k = 10, best batch (32)
+PUBLISHED_KMEANS_FIT_S = 7.480   # CudaKMeansEngine::fit, cosine, N = 100,000, D = 768, K = 1024, 15 iters
+PUBLISHED_BATCHES = (1, 2, 4, 8, 16, 32, 64, 128, 256, 512)
+
+
+def bench_reference_published(vh, reps):
+    """The reference's published GPU rows at their own shapes (cuda_benchmark.py:40-51 run
+    cuda_bench.rs with N = 100,000, D = 768, cosine, U[-1, 1] data from generate_flat_vectors):
+    * DistributedKnnEngine::search_batch at G = 1, k = 10, host slices in and results out, over
+      batch sizes 1 to 512 (each the median of `reps` calls after two warm-ups); the batch of 32
+      is checked against the oracle;
+    * CudaKMeansEngine::fit with its default k-means++ init, K = 1024, 15 iterations at most,
+      tolerance 1e-4, host data in and centroids out (median of 3 after one warm-up)."""
+    from vector_hip import datasets as ds
+    import oracle
+
+    n, d, k = 100_000, 768, 10
+    log(f"reference_published: {n} x {d} U[-1, 1], cosine")
+    base = ds.uniform(n, d, ds.SEED_BASE)
+    qs = ds.uniform(max(PUBLISHED_BATCHES), d, ds.SEED_QUERIES)
+    cos = vh.DistanceMetric.CosineSimilarity
+    eng = vh.DistributedKnnEngine.try_new(base, d, 1, vh.GpuShardMode.Sharded, cos)
+    rows = []
+    par = None
+    for b in PUBLISHED_BATCHES:
+        q = np.ascontiguousarray(qs[:b])
+        for _ in range(2):
+            eng.search_batch_arrays(q, k)
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            eng.search_batch_arrays(q, k)
+            ts.append(time.perf_counter() - t0)
+        us = float(np.median(ts)) * 1e6
+        rows.append({"batch": b, "us": round(us, 1), "qps": round(b / us * 1e6, 1)})
+        log(f"  knn batch {b}: {rows[-1]}")
+        if b == 32:
+            ids, dist, _ = eng.search_batch_arrays(q, k)
+            ref = oracle.knn_search_batch(base, q, k, "cosine", threads=cpu_threads())
+            par = knn_parity(base, q, ids, dist, (ref, np.arange(b)), k, "cosine", 1e-4, 1e-6)
+    b32 = next(r for r in rows if r["batch"] == 32)
+    best = max(rows, key=lambda r: r["qps"])
+    knn = {"workload": f"search_batch_cosine_uniform_{n}x{d}_k{k}", "rows": rows,
+           "batch32_qps": b32["qps"], "best": best, "published_t4_batch32_qps": PUBLISHED_KNN_QPS,
+           "batch32_over_published": round(b32["qps"] / PUBLISHED_KNN_QPS, 2),
+           "parity_batch32": {kk: par[kk] for kk in ("ok", "recall_tie_aware", "max_rel_dist_err")}}
+    kc = 1024
+    log(f"  kmeans fit K = {kc}")
+    x = base
+    fe = vh.CudaKMeansEngine()
+    fe.fit(x, d, kc, 15, 1e-4, cos)
+    ts = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        r = fe.fit(x, d, kc, 15, 1e-4, cos)
+        ts.append(time.perf_counter() - t0)
+    fit_s = float(np.median(ts))
+    km = {"workload": f"kmeans_fit_cosine_uniform_{n}x{d}_k{kc}_15iters_tol1e-4", "fit_s": round(fit_s, 4),
+          "iterations": r.iterations, "inertia": r.inertia, "published_t4_fit_s": PUBLISHED_KMEANS_FIT_S,
+          "published_over_this": round(PUBLISHED_KMEANS_FIT_S / fit_s, 1)}
+    log(f"  kmeans fit: {km}")
+    return {"note": "the reference's only published GPU figures, one NVIDIA T4 (cuda_benchmark.svg:143, 262; "
+                    "they equal cuda_benchmark.py's fallback values, so they are quoted, not a baseline)",
+            "knn": knn, "kmeans_fit": km,
+            "parity": {"ok": bool(par["ok"]), "rule": "batch of 32 against the oracle (tie-aware recall >= 0.999, "
+                                                      "distances within 1e-4)"}}
+
+
 def bench_copy(vh, nbytes=1 << 30, reps=5):
     """Plain device-to-device copy of `nbytes` (the runtime's blit kernel).  Its FETCH_SIZE and
     WRITE_SIZE counters calibrate the HBM traffic figures of the other kernels."""
@@ -939,7 +1012,7 @@ def main():
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--workload", default="default",
-                    choices=["default", "kmeans", "kmeans_fit", "batch_sweep", "copy", "ivf_coarse", "ivfpq",
+                    choices=["default", "kmeans", "kmeans_fit", "batch_sweep", "published", "copy", "ivf_coarse", "ivfpq",
                              "upload"] + sorted(WORKLOADS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     args = ap.parse_args()
@@ -965,6 +1038,13 @@ def main():
         out = bench_kmeans_fit(vh, not args.no_cpu)
     elif args.workload == "batch_sweep":
         out = bench_batch_sweep(vh, max(args.steps, 20), not args.no_cpu)
+    elif args.workload == "published":
+        r = bench_reference_published(vh, max(args.steps, 20))
+        out = {"metric": "the reference's published GPU rows at their shapes", "value": r["knn"]["batch32_qps"],
+               "unit": "queries/s", "n_gpus": 1, "steps": max(args.steps, 20), "warmup": 2,
+               "ms_per_step": round(32 / r["knn"]["batch32_qps"] * 1e3, 4), "higher_is_better": True,
+               "scaling": "strong", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+               "config": {"workload": r["knn"]["workload"], "parallelism": "single GPU"}, **r}
     elif args.workload == "kmeans":
         r = bench_kmeans(vh, 10, not args.no_cpu)
         out = {"metric": METRIC, "value": r["value"], "unit": r["unit"], "n_gpus": 1, "steps": 10, "warmup": 1,
@@ -991,6 +1071,7 @@ def main():
             out["batch_sweep"] = {kk: r[kk] for kk in ("metric", "config", "shapes", "cpu_note", "parity")}
             r = bench_kmeans_fit(vh, not args.no_cpu)
             out["kmeans_fit"] = {kk: r[kk] for kk in ("metric", "kmeans_2m", "cuda_bench_shape")}
+            out["reference_published"] = bench_reference_published(vh, 20)
     out["config"]["device"] = ctx.device_name()
     print(json.dumps(out))
     bad = [name for name, part in [("top", out)] + [(kk, v) for kk, v in out.items() if isinstance(v, dict)]
