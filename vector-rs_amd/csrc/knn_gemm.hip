@@ -63,6 +63,8 @@ __device__ __forceinline__ int swz(int row, int c4) { return row * 8 + (c4 ^ ((r
 // Row preparation (see RowPrep): one wave per row; the norm is a lane-strided sum followed by
 // a fixed xor butterfly, so it is deterministic.
 // ---------------------------------------------------------------------------------
+constexpr int kPrepRegs = 16;  // rows of up to 64 * 16 floats are held in registers
+
 __global__ __launch_bounds__(256) void k_rows_prep(RowPrep a) {
     const int lane = threadIdx.x & 63;
     const size_t wave = (blockIdx.x * (size_t)blockDim.x + threadIdx.x) >> 6;
@@ -86,53 +88,92 @@ __global__ __launch_bounds__(256) void k_rows_prep(RowPrep a) {
         const float *row = a.in + src * (size_t)dim;
         float ss = 0.0f;
         bool whole = true, exact = true;
-        // four elements per lane in flight at a time (the loads first), the sum in the order d
-        for (int d0 = lane; d0 < dpad; d0 += 256) {
-            float xs[4], sh[4];
+        if (dpad <= 64 * kPrepRegs) {
+            // the whole row in registers: every load in flight at once, one pass for the norm and the
+            // (normalized) output; the sum in the order d, as below
+            float xs[kPrepRegs], sh[kPrepRegs];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int d = d0 + 64 * u;
-                xs[u] = d < dim ? row[d] : 0.0f;
-                sh[u] = (a.shift && d < dpad) ? a.shift[d] : 0.0f;
+            for (int r = 0; r < kPrepRegs; ++r) {
+                const int d = lane + 64 * r;
+                xs[r] = d < dim ? row[d] : 0.0f;
+                sh[r] = (a.shift && d < dpad) ? a.shift[d] : 0.0f;
             }
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int d = d0 + 64 * u;
-                if (d >= dpad) break;
-                const float x = xs[u];
+            for (int r = 0; r < kPrepRegs; ++r) {
+                const int d = lane + 64 * r;
+                if (d >= dpad) continue;
+                const float x = xs[r];
                 whole = whole && x == rintf(x);
                 if (rrow) rrow[d] = x;
-                float v = a.shift ? x - sh[u] : x;
-                exact = exact && (!a.shift || v + sh[u] == x);
+                float v = a.shift ? x - sh[r] : x;
+                exact = exact && (!a.shift || v + sh[r] == x);
                 if (a.transform) v = sqrtf(fabsf(v));
                 if (!a.normalize) orow[d] = v;
                 ss = fmaf(v, v, ss);
             }
-        }
 #pragma unroll
-        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
-        const bool row_int = __builtin_amdgcn_ballot_w64(!whole) == 0;
-        const bool row_exact = __builtin_amdgcn_ballot_w64(!exact) == 0;
-        if (a.normalize) {
-            const float nr = sqrtf(ss);
-            const float inv = nr > 0.0f ? 1.0f / nr : 0.0f;
+            for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+            if (a.normalize) {  // as the pass below: the raw value (transformed), times 1 / norm
+                const float nr = sqrtf(ss);
+                const float inv = nr > 0.0f ? 1.0f / nr : 0.0f;
+#pragma unroll
+                for (int r = 0; r < kPrepRegs; ++r) {
+                    const int d = lane + 64 * r;
+                    if (d >= dpad) continue;
+                    float v = xs[r];
+                    if (a.transform) v = sqrtf(fabsf(v));
+                    orow[d] = v * inv;
+                }
+            }
+        } else {
+            // four elements per lane in flight at a time (the loads first), the sum in the order d
             for (int d0 = lane; d0 < dpad; d0 += 256) {
-                float xs[4];
+                float xs[4], sh[4];
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
                     const int d = d0 + 64 * u;
                     xs[u] = d < dim ? row[d] : 0.0f;
+                    sh[u] = (a.shift && d < dpad) ? a.shift[d] : 0.0f;
                 }
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
                     const int d = d0 + 64 * u;
                     if (d >= dpad) break;
-                    float v = xs[u];
+                    const float x = xs[u];
+                    whole = whole && x == rintf(x);
+                    if (rrow) rrow[d] = x;
+                    float v = a.shift ? x - sh[u] : x;
+                    exact = exact && (!a.shift || v + sh[u] == x);
                     if (a.transform) v = sqrtf(fabsf(v));
-                    orow[d] = v * inv;
+                    if (!a.normalize) orow[d] = v;
+                    ss = fmaf(v, v, ss);
+                }
+            }
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+            if (a.normalize) {
+                const float nr = sqrtf(ss);
+                const float inv = nr > 0.0f ? 1.0f / nr : 0.0f;
+                for (int d0 = lane; d0 < dpad; d0 += 256) {
+                    float xs[4];
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        const int d = d0 + 64 * u;
+                        xs[u] = d < dim ? row[d] : 0.0f;
+                    }
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        const int d = d0 + 64 * u;
+                        if (d >= dpad) break;
+                        float v = xs[u];
+                        if (a.transform) v = sqrtf(fabsf(v));
+                        orow[d] = v * inv;
+                    }
                 }
             }
         }
+        const bool row_int = __builtin_amdgcn_ballot_w64(!whole) == 0;
+        const bool row_exact = __builtin_amdgcn_ballot_w64(!exact) == 0;
         if (lane == 0) {
             if (a.norm_kind && a.norm) a.norm[p] = a.norm_kind == 2 ? sqrtf(ss) : ss;
             if (a.nonint && !row_int) atomicOr(a.nonint, 1u);

@@ -90,20 +90,29 @@ __device__ __forceinline__ void bitonic_sort_lds(u64 *buf, int P) {
 // elements against the running best k.
 constexpr int kMergeBins = 1024;
 constexpr int kMergeDirect = 512;
+constexpr int kMergeCached = 16;  // list entries per thread held in registers through the select
 
-__device__ __forceinline__ uint32_t block_reduce_u32(uint32_t v, bool is_max, uint32_t *red) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+// The minimum of lo and the maximum of hi over the workgroup, in one round of LDS (red: 2 words
+// per wave).
+__device__ __forceinline__ void block_minmax_u32(uint32_t &lo, uint32_t &hi, uint32_t *red) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = (int)(blockDim.x >> 6);
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
-        const uint32_t w = __shfl_xor(v, o, 64);
-        v = is_max ? max(v, w) : min(v, w);
+        lo = min(lo, __shfl_xor(lo, o, 64));
+        hi = max(hi, __shfl_xor(hi, o, 64));
     }
     __syncthreads();
-    if (lane == 0) red[wave] = v;
+    if (lane == 0) {
+        red[wave] = lo;
+        red[nw + wave] = hi;
+    }
     __syncthreads();
-    v = red[0];
-    for (int w = 1; w < (int)(blockDim.x >> 6); ++w) v = is_max ? max(v, red[w]) : min(v, red[w]);
-    return v;
+    lo = red[0];
+    hi = red[nw];
+    for (int w = 1; w < nw; ++w) {
+        lo = min(lo, red[w]);
+        hi = max(hi, red[nw + w]);
+    }
 }
 
 // buf holds `bufn` u64 entries (dynamic LDS, bufn >= 2 * pow2(kc), >= kMergeDirect).  NT threads
@@ -120,7 +129,7 @@ __global__ __launch_bounds__(NT) void k_topk_merge(int k, int kc, int bufn, cons
     extern __shared__ u64 buf[];
     __shared__ uint32_t hist[kMergeBins];
     __shared__ uint32_t red[2 * (NT / 64)];
-    __shared__ uint32_t s_part[NT];
+    __shared__ uint32_t s_part[NT / 64];
     __shared__ uint32_t s_sel[4];  // boundary bucket, count below it, gather counters
     const int q = blockIdx.x, tid = threadIdx.x;
     const uint32_t c_all = cnt[q];
@@ -154,48 +163,65 @@ __global__ __launch_bounds__(NT) void k_topk_merge(int k, int kc, int bufn, cons
     bool done = false;
     if (T > (uint32_t)kMergeDirect && T > kk) {
         // ---- bucket select ----
-        uint32_t lo = 0xffffffffu, hi = 0u;
-        for (uint32_t i0 = tid; i0 < T; i0 += 4 * NT) {
-            uint32_t v[4];
+        // Up to kMergeCached keys per thread stay in registers for the three passes (one read of
+        // the list); longer lists are read in each pass, four keys in flight per thread.
+        const bool cached = T <= (uint32_t)(kMergeCached * NT);
+        uint32_t kv[kMergeCached];
+        if (cached) {
 #pragma unroll
-            for (int u = 0; u < 4; ++u) v[u] = i0 + u * NT < T ? key32(i0 + u * NT) : 0u;
-#pragma unroll
-            for (int u = 0; u < 4; ++u)
-                if (i0 + u * NT < T) {
-                    lo = min(lo, v[u]);
-                    hi = max(hi, v[u]);
-                }
+            for (int u = 0; u < kMergeCached; ++u) {
+                const uint32_t i = tid + u * NT;
+                kv[u] = i < T ? key32(i) : 0u;
+            }
         }
-        lo = block_reduce_u32(lo, false, red);
-        hi = block_reduce_u32(hi, true, red + NT / 64);
+        // fn(i, score key) for every entry i of this thread
+        auto visit = [&](auto fn) {
+            if (cached) {
+#pragma unroll
+                for (int u = 0; u < kMergeCached; ++u)
+                    if (tid + u * NT < T) fn(tid + u * NT, kv[u]);
+            } else {
+                for (uint32_t i0 = tid; i0 < T; i0 += 4 * NT) {
+                    uint32_t v[4];
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) v[u] = i0 + u * NT < T ? key32(i0 + u * NT) : 0u;
+#pragma unroll
+                    for (int u = 0; u < 4; ++u)
+                        if (i0 + u * NT < T) fn(i0 + u * NT, v[u]);
+                }
+            }
+        };
+        uint32_t lo = 0xffffffffu, hi = 0u;
+        visit([&](uint32_t, uint32_t v) {
+            lo = min(lo, v);
+            hi = max(hi, v);
+        });
+        block_minmax_u32(lo, hi, red);
         if (lo < hi) {
             const float scale = (float)kMergeBins / ((float)(hi - lo) + 1.0f);
             auto bucket = [&](uint32_t v) { return min(kMergeBins - 1, (int)((float)(v - lo) * scale)); };
             for (int i = tid; i < kMergeBins; i += NT) hist[i] = 0;
             __syncthreads();
-            for (uint32_t i0 = tid; i0 < T; i0 += 4 * NT) {
-                uint32_t v[4];
-#pragma unroll
-                for (int u = 0; u < 4; ++u) v[u] = i0 + u * NT < T ? key32(i0 + u * NT) : 0u;
-#pragma unroll
-                for (int u = 0; u < 4; ++u)
-                    if (i0 + u * NT < T) atomicAdd(&hist[bucket(v[u])], 1u);
-            }
+            visit([&](uint32_t, uint32_t v) { atomicAdd(&hist[bucket(v)], 1u); });
             __syncthreads();
-            // bucket b* holding the kk-th smallest: cum(b*) < kk <= cum(b*) + hist[b*]
+            // bucket b* holding the kk-th smallest: cum(b*) < kk <= cum(b*) + hist[b*].  Each thread
+            // sums its run of bins; the runs' exclusive prefix comes from a wave scan (shuffles) and
+            // the waves' totals.
             constexpr int per = kMergeBins / NT;
             uint32_t loc = 0;
 #pragma unroll
             for (int j = 0; j < per; ++j) loc += hist[tid * per + j];
-            s_part[tid] = loc;
-            __syncthreads();
-            for (int o = 1; o < NT; o <<= 1) {
-                const uint32_t v = tid >= o ? s_part[tid - o] : 0u;
-                __syncthreads();
-                s_part[tid] += v;
-                __syncthreads();
+            const int lane = tid & 63, wave = tid >> 6;
+            uint32_t incl = loc;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const uint32_t t = __shfl_up(incl, o, 64);
+                if (lane >= o) incl += t;
             }
-            uint32_t cum = s_part[tid] - loc;  // elements in buckets before this thread's bins
+            if (lane == 63) s_part[wave] = incl;
+            __syncthreads();
+            for (int w = 0; w < wave; ++w) incl += s_part[w];
+            uint32_t cum = incl - loc;  // elements in buckets before this thread's bins
 #pragma unroll
             for (int j = 0; j < per; ++j) {
                 const uint32_t hb = hist[tid * per + j];
@@ -214,19 +240,11 @@ __global__ __launch_bounds__(NT) void k_topk_merge(int k, int kc, int bufn, cons
             const uint32_t below = s_sel[1];
             const uint32_t inb = hist[bstar];
             if (below + inb <= (uint32_t)bufn) {
-                for (uint32_t i0 = tid; i0 < T; i0 += 4 * NT) {
-                    uint32_t v[4];
-#pragma unroll
-                    for (int u = 0; u < 4; ++u) v[u] = i0 + u * NT < T ? key32(i0 + u * NT) : 0xffffffffu;
-#pragma unroll
-                    for (int u = 0; u < 4; ++u) {
-                        const uint32_t i = i0 + u * NT;
-                        if (i >= T) continue;
-                        const int b = bucket(v[u]);
-                        if (b < bstar) buf[atomicAdd(&s_sel[2], 1u)] = key64(i);
-                        else if (b == bstar) buf[below + atomicAdd(&s_sel[3], 1u)] = key64(i);
-                    }
-                }
+                visit([&](uint32_t i, uint32_t v) {
+                    const int b = bucket(v);
+                    if (b < bstar) buf[atomicAdd(&s_sel[2], 1u)] = key64(i);
+                    else if (b == bstar) buf[below + atomicAdd(&s_sel[3], 1u)] = key64(i);
+                });
                 const uint32_t total = below + inb;
                 int P = 2;
                 while ((uint32_t)P < total) P <<= 1;
