@@ -285,3 +285,21 @@ def test_small_set_direct_assign_matches_mfma(vh, oracle, monkeypatch, metric, d
     c_d, c_m = rd.centroids.reshape(24, dim), rm.centroids.reshape(24, dim)
     assert np.all(np.linalg.norm(c_d - c_m, axis=1) <= 1e-6 * np.maximum(np.linalg.norm(c_m, axis=1), 1e-6))
     assert abs(rd.inertia - rm.inertia) <= 1e-5 * abs(rm.inertia) + 1e-3
+
+
+@pytest.mark.parametrize("n,dim,k,metric", [(3, 40, 1, "l2"), (5, 40, 3, "cosine"), (700, 1000, 7, "dot"),
+                                            (700, 1024, 7, "l2"), (2_000, 128, 256, "l2")])
+def test_small_set_edges(vh, oracle, n, dim, k, metric):
+    """Edges of the direct-form assignment: k = 1, fewer points than a wave holds, 1000 and 1024
+    dimensions (dpad 1024, k-means' largest: 16 slices per lane, the last partly and wholly
+    filled), and 256 centroids (its largest k).  Each step against the oracle's from the same
+    centroids."""
+    rng = np.random.default_rng(n + dim + k)
+    data = rng.standard_normal((n, dim)).astype(np.float32)
+    if metric != "l2":
+        data += 2.0
+    st = vh.KMeansState(data, vh.DistanceMetric(oracle.METRICS[metric]))
+    cent = data[:k].copy()
+    st.set_centroids(cent)
+    st.run(1)
+    _check_step(oracle, data, cent, st.read(), metric, max_flip_frac=1.0 / n)

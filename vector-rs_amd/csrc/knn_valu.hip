@@ -542,6 +542,7 @@ __global__ __launch_bounds__(256) void k_kmeans_assign_small(const float *__rest
     }
 }
 
+// (dpad <= 1024 always holds for k-means, which rejects larger dimensions; it bounds NS at 16)
 bool kmeans_assign_small_ok(int n, int k, int dpad, int cus) {
     return n > 0 && n < 128 * cus && k >= 1 && k <= kAssignSmallMaxK && (long)n * k <= kAssignSmallMaxPairs &&
            dpad <= 1024;
