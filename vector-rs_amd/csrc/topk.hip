@@ -450,7 +450,8 @@ void launch_topk_finalize(int nq, int kc, int kout, int metric, const unsigned l
 // One workgroup per query: its threads first fetch every kept neighbour's id and stored row at
 // once (the id -> row lookup is a dependent load), then groups of 16 lanes evaluate one neighbour
 // each, 16 at a time, with float4 reads of the row and the query (lane s sums pieces s, s + 16,
-// ... in order) and a fixed xor butterfly.
+// ... in order) and a fixed xor butterfly.  A query with a zero bound (squared L2 or dot product
+// on integer rows within 2^24) skips the recomputation: its scores are already the exact values.
 __global__ __launch_bounds__(256) void k_topk_refine(int k, int kc, int kout, int metric,
                                                      const float *__restrict__ qrows, const float *__restrict__ base,
                                                      const float *__restrict__ shift,
@@ -466,6 +467,25 @@ __global__ __launch_bounds__(256) void k_topk_refine(int k, int kc, int kout, in
     const int q = blockIdx.x, tid = threadIdx.x;
     const u64 *tq = topk + (size_t)q * kc;
     const int h_all = (int)have[q];
+    if (qerr && qerr[q] == 0.0f && metric != COS) {
+        // No selection error: squared L2 or dot product on integer rows whose every intermediate
+        // stays below 2^24 (the bound is 0 only then), so the scan's scores are the direct form's
+        // exact values and the merge's list, sorted by (score, id), is already the result.
+        const int hk = h_all < k ? h_all : k;
+        for (int j = tid; j < kout; j += 256) {
+            const size_t o = (size_t)q * ostride + j;
+            if (j < hk) {
+                const u64 e = tq[j];
+                const float sc = key_score((uint32_t)(e >> 32));
+                out_ids[o] = (uint32_t)e;
+                out_dist[o] = metric == L2 ? sc : -sc + 0.0f;
+            } else {
+                out_ids[o] = 0xffffffffu;
+                out_dist[o] = __builtin_nanf("");
+            }
+        }
+        return;
+    }
     if (tid == 0) s_h = h_all;
     __syncthreads();
     if (h_all > k && qerr) {
