@@ -110,7 +110,7 @@ void launch_hamming_filter(const uint32_t *codes, const uint32_t *qry, const flo
     const dim3 g((unsigned)grid), b(256);
     const int it = (int)items;
 #define VH_HAM(W)                                                                                              \
-    hipLaunchKernelGGL(k_hamming_filter<W>, g, b, 0, s, codes, qry, tau, nq, wpad, row_begin, row_end, nqt, \
+    scan_launch(k_hamming_filter<W>, g, b, 0, s, codes, qry, tau, nq, wpad, row_begin, row_end, nqt, \
                        it, item_rows, cand, cnt, cap)
     switch (wpad) {
         case 1: VH_HAM(1); break;

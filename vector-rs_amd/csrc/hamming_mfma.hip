@@ -656,7 +656,7 @@ void launch_ham_mfma(bool dense, long item_rows, const int8_t *base8, const int8
     const int cus = grid_cap / 2;
     long g = a.n_items < cus ? a.n_items : cus;
     const dim3 grid((unsigned)((g + 7) / 8 * 8)), block(512);
-#define VH_HM(MODE, KC) hipLaunchKernelGGL((k_mfma_ham<MODE, KC>), grid, block, 0, s, a)
+#define VH_HM(MODE, KC) scan_launch((k_mfma_ham<MODE, KC>), grid, block, 0, s, a)
 #define VH_HM_K(MODE)                 \
     switch (ham_chunks(wpad)) {        \
         case 1: VH_HM(MODE, 1); break; \
@@ -698,9 +698,9 @@ void launch_ham_mfma_wide(long item_rows, const int8_t *base8, const int8_t *qry
     long g = a.n_items < cus ? a.n_items : cus;
     const dim3 grid((unsigned)((g + 7) / 8 * 8)), block(512);
     switch (ham_chunks(wpad)) {
-        case 1: hipLaunchKernelGGL((k_mfma_ham_wide<1>), grid, block, 0, s, a); break;
-        case 2: hipLaunchKernelGGL((k_mfma_ham_wide<2>), grid, block, 0, s, a); break;
-        default: hipLaunchKernelGGL((k_mfma_ham_wide<4>), grid, block, 0, s, a); break;
+        case 1: scan_launch((k_mfma_ham_wide<1>), grid, block, 0, s, a); break;
+        case 2: scan_launch((k_mfma_ham_wide<2>), grid, block, 0, s, a); break;
+        default: scan_launch((k_mfma_ham_wide<4>), grid, block, 0, s, a); break;
     }
 }
 

@@ -1682,28 +1682,28 @@ static void launch_scan(const ScanArgs &a, int grid_cap, hipStream_t s) {
     if (nk <= 4) {
         const dim3 g(grid_for(a.n_items, cus)), b(512);
         switch (nk) {
-            case 1: hipLaunchKernelGGL((k_mfma_hs<MODE, M, 1>), g, b, 0, s, a); break;
-            case 2: hipLaunchKernelGGL((k_mfma_hs<MODE, M, 2>), g, b, 0, s, a); break;
-            case 3: hipLaunchKernelGGL((k_mfma_hs<MODE, M, 3>), g, b, 0, s, a); break;
-            default: hipLaunchKernelGGL((k_mfma_hs<MODE, M, 4>), g, b, 0, s, a); break;
+            case 1: scan_launch((k_mfma_hs<MODE, M, 1>), g, b, 0, s, a); break;
+            case 2: scan_launch((k_mfma_hs<MODE, M, 2>), g, b, 0, s, a); break;
+            case 3: scan_launch((k_mfma_hs<MODE, M, 3>), g, b, 0, s, a); break;
+            default: scan_launch((k_mfma_hs<MODE, M, 4>), g, b, 0, s, a); break;
         }
     } else if (nk % 4 == 0) {
         const dim3 g(grid_for(a.n_items, cus));
         if constexpr (MODE != kAssign) {
             switch (gemm_filter_cols(a.dpad) == kNtCols ? nk : 0) {  // the narrow-tile instantiations
-                case 8: hipLaunchKernelGGL((k_mfma_nt<MODE, M, 8>), g, dim3(512), 0, s, a); return;
-                case 12: hipLaunchKernelGGL((k_mfma_nt<MODE, M, 12>), g, dim3(512), 0, s, a); return;
-                case 16: hipLaunchKernelGGL((k_mfma_nt<MODE, M, 16>), g, dim3(512), 0, s, a); return;
-                case 20: hipLaunchKernelGGL((k_mfma_nt<MODE, M, 20>), g, dim3(512), 0, s, a); return;
-                case 24: hipLaunchKernelGGL((k_mfma_nt<MODE, M, 24>), g, dim3(512), 0, s, a); return;
-                case 28: hipLaunchKernelGGL((k_mfma_nt<MODE, M, 28>), g, dim3(512), 0, s, a); return;
+                case 8: scan_launch((k_mfma_nt<MODE, M, 8>), g, dim3(512), 0, s, a); return;
+                case 12: scan_launch((k_mfma_nt<MODE, M, 12>), g, dim3(512), 0, s, a); return;
+                case 16: scan_launch((k_mfma_nt<MODE, M, 16>), g, dim3(512), 0, s, a); return;
+                case 20: scan_launch((k_mfma_nt<MODE, M, 20>), g, dim3(512), 0, s, a); return;
+                case 24: scan_launch((k_mfma_nt<MODE, M, 24>), g, dim3(512), 0, s, a); return;
+                case 28: scan_launch((k_mfma_nt<MODE, M, 28>), g, dim3(512), 0, s, a); return;
                 default: break;
             }
         }
-        hipLaunchKernelGGL((k_mfma_pnl<MODE, M>), g, dim3(512), 0, s, a);
+        scan_launch((k_mfma_pnl<MODE, M>), g, dim3(512), 0, s, a);
     } else {
         const dim3 g(grid_for(a.n_items, 2 * cus)), b(256);
-        hipLaunchKernelGGL((k_mfma_stream<MODE, M>), g, b, 0, s, a);
+        scan_launch((k_mfma_stream<MODE, M>), g, b, 0, s, a);
     }
 }
 

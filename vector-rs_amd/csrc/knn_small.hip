@@ -244,7 +244,7 @@ static void launch_small_m(const SmallArgs &a, dim3 grid, size_t lds, hipStream_
         else
             (void)hipGetLastError();
     }
-    hipLaunchKernelGGL((k_mfma_small<MODE, M>), grid, dim3(512), lds, s, a);
+    scan_launch((k_mfma_small<MODE, M>), grid, dim3(512), lds, s, a);
 }
 
 void launch_small_scan(int metric, bool dense, const float *base, const float *bnorm, const float *qry,

@@ -187,10 +187,10 @@ static void launch_m(int dpad, dim3 g, hipStream_t s, const float *base, const f
                      const float *tau, int nq, long rb, long re, int nqt, int items, long item_rows, uint2 *cand,
                      uint32_t *cnt, int cap) {
     if (dpad <= 128 && dpad > 64)
-        hipLaunchKernelGGL((k_valu_filter<M, 128>), g, dim3(256), 0, s, base, shift, qry, tau, nq, dpad, rb, re, nqt,
+        scan_launch((k_valu_filter<M, 128>), g, dim3(256), 0, s, base, shift, qry, tau, nq, dpad, rb, re, nqt,
                            items, item_rows, cand, cnt, cap);
     else
-        hipLaunchKernelGGL((k_valu_filter<M, 64>), g, dim3(256), 0, s, base, shift, qry, tau, nq, dpad, rb, re, nqt,
+        scan_launch((k_valu_filter<M, 64>), g, dim3(256), 0, s, base, shift, qry, tau, nq, dpad, rb, re, nqt,
                            items, item_rows, cand, cnt, cap);
 }
 
@@ -554,7 +554,7 @@ static void launch_small_l(int dpad, const float *pts, int n, const float *cent,
     const dim3 g(ceil_div(n, 4 * (64 / L)));
     const int ns = ceil_div(dpad / 4, L);
 #define VH_AS(NS)                                                                                                 \
-    hipLaunchKernelGGL((k_kmeans_assign_small<M, L, NS>), g, dim3(256), 0, s, pts, dpad, n, cent, k, assign,     \
+    scan_launch((k_kmeans_assign_small<M, L, NS>), g, dim3(256), 0, s, pts, dpad, n, cent, k, assign,     \
                        inertia, pos, counts, devmax)
     if (ns <= 2) VH_AS(2);
     else if (ns <= 4) VH_AS(4);
@@ -587,10 +587,10 @@ template <int M>
 static void launch_km(int dpad, dim3 g, hipStream_t s, const float *cent, int k, const float *pts, int n, int tiles,
                       int32_t *assign, float *inertia, int32_t *pos, int32_t *counts) {
     if (dpad <= 128 && dpad > 64)
-        hipLaunchKernelGGL((k_kmeans_assign_valu<M, 128>), g, dim3(256), 0, s, cent, k, pts, n, dpad, tiles, assign,
+        scan_launch((k_kmeans_assign_valu<M, 128>), g, dim3(256), 0, s, cent, k, pts, n, dpad, tiles, assign,
                            inertia, pos, counts);
     else
-        hipLaunchKernelGGL((k_kmeans_assign_valu<M, 64>), g, dim3(256), 0, s, cent, k, pts, n, dpad, tiles, assign,
+        scan_launch((k_kmeans_assign_valu<M, 64>), g, dim3(256), 0, s, cent, k, pts, n, dpad, tiles, assign,
                            inertia, pos, counts);
 }
 

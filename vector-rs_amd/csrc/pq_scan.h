@@ -891,9 +891,9 @@ void launch_lists_mt(const ListArgs &L, int ds, int cus, hipStream_t s) {
     const size_t per_cu = std::max<size_t>(1, 163840 / (sizeof(ListLds) + 256));
     const unsigned grid = (unsigned)((size_t)cus * per_cu);
     if (ds == 4)
-        hipLaunchKernelGGL((k_ivfpq_lists<MT, 4>), dim3(grid), dim3(kListThreads), 0, s, L);
+        scan_launch((k_ivfpq_lists<MT, 4>), dim3(grid), dim3(kListThreads), 0, s, L);
     else
-        hipLaunchKernelGGL((k_ivfpq_lists<MT, 8>), dim3(grid), dim3(kListThreads), 0, s, L);
+        scan_launch((k_ivfpq_lists<MT, 8>), dim3(grid), dim3(kListThreads), 0, s, L);
 }
 
 template <bool HIB>
@@ -915,7 +915,7 @@ void launch_resident(K kernel, const ScanArgs &A, int cus, size_t lds, hipStream
         per_cu = 1;
     }
     const unsigned grid = (unsigned)std::min<long>((long)A.nq, (long)per_cu * cus);
-    hipLaunchKernelGGL(kernel, dim3(grid), dim3(kScanThreads), lds, s, A);
+    scan_launch(kernel, dim3(grid), dim3(kScanThreads), lds, s, A);
 }
 
 template <int MT, int DS>

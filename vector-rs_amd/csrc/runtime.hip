@@ -224,7 +224,14 @@ KernelTimer::~KernelTimer() {
     }
 }
 
-int KernelTimer::begin(hipStream_t s) {
+TimedLaunch &timed_launch_slot() {
+    thread_local TimedLaunch t;
+    return t;
+}
+
+// The pair goes to the region's scan launches (scan_launch), which record it on their own
+// dispatches; a region that launched none records it here, empty.
+int KernelTimer::begin(hipStream_t) {
     if (!enabled) return -1;
     if (used == pool.size()) {
         hipEvent_t a, b;
@@ -235,13 +242,21 @@ int KernelTimer::begin(hipStream_t s) {
         pool.emplace_back(a, b);
     }
     const int idx = (int)used++;
-    (void)hipEventRecord(pool[idx].first, s);
+    TimedLaunch &t = timed_launch_slot();
+    t.start = pool[idx].first;
+    t.stop = pool[idx].second;
+    t.used = false;
     return idx;
 }
 
 void KernelTimer::end(int idx, hipStream_t s, double w, double b) {
     if (idx < 0) return;
-    (void)hipEventRecord(pool[idx].second, s);
+    TimedLaunch &t = timed_launch_slot();
+    if (!t.used) {
+        (void)hipEventRecord(pool[idx].first, s);
+        (void)hipEventRecord(pool[idx].second, s);
+    }
+    t = TimedLaunch{};
     if ((size_t)idx >= meta.size()) meta.resize(idx + 1);
     meta[idx] = {w, b};
 }

@@ -1,11 +1,31 @@
 // vh_common.h -- shared device helpers and internal launcher declarations.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
 
 namespace vh {
+
+// ---- scan-kernel launches and their timing ------------------------------------------------
+// A timed region (KernelTimer::begin .. end on one host thread) hands its event pair to the scan
+// launches inside it, which attach the events to their own dispatches: the first records `start`
+// as its kernel begins and each records `stop` as its kernel ends.  The pair then spans the scan
+// kernels alone, as a kernel trace measures them, without the launch gaps and the fill kernels
+// around them.  Outside a timed region (no pair pending) this is a plain launch.
+struct TimedLaunch {
+    hipEvent_t start = nullptr, stop = nullptr;
+    bool used = false;  // some launch of the region took the start event
+};
+TimedLaunch &timed_launch_slot();  // this host thread's pending pair
+
+template <typename F, typename... Args>
+inline void scan_launch(F kernel, dim3 grid, dim3 block, uint32_t shm, hipStream_t s, Args... args) {
+    TimedLaunch &t = timed_launch_slot();
+    hipExtLaunchKernelGGL(kernel, grid, block, shm, s, t.used ? nullptr : t.start, t.stop, 0u, args...);
+    if (t.stop) t.used = true;
+}
 
 enum Metric : int {
     L2 = 0, DOT = 1, COS = 2, L1 = 3, MINK = 4, LINF = 5, HAMF = 6, MAHA = 7, JACC = 8, HELL = 9,
