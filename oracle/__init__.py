@@ -16,8 +16,8 @@ ctypes bindings over ``oracle/libvh_oracle.so`` (built from ``vh_oracle.c`` by
 * ``find_top_centroids`` ``KMeans::find_top_centroids`` (ivf/kmeans.rs:311-356).
 * ``ivfpq_search``       ``IvfPqIndex::search_with_nprobe`` (ivf/mod.rs:256-345) with given probes.
 
-Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg
-may import this package, and only as the checker / CPU baseline.
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` and parity
+legs may import this package, and only to check the GPU results or to time the CPU baseline.
 """
 from __future__ import annotations
 

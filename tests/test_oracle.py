@@ -1,4 +1,4 @@
-"""Pins the CPU oracle before it is trusted as the checker.
+"""Pins the CPU oracle before the GPU results are checked against it.
 
 Every oracle function is checked against (a) the reference's own known-answer
 tests, restated with their inputs and expected values, and (b) what the
