@@ -49,3 +49,23 @@ def test_integer_l2_batches(vh, oracle):
     base = ds.uniform_int(200_000, 128, 53)
     q = ds.uniform_int(128, 128, 54)
     _sweep(vh, oracle, base, q, vh.DistanceMetric.L2Squared, "l2", rtol=0.0, atol=0.0)
+
+
+@pytest.mark.parametrize("dim", [960, 992, 1000, 1024])
+@pytest.mark.parametrize("mname", ["cosine", "l2", "dot"])
+def test_small_batches_with_the_widest_rows(vh, oracle, dim, mname):
+    """The small-batch scan keeps its 32-query tile of dim floats in LDS and, on rounds of few row
+    blocks, splits K over the waves with partial sums beside the tile.  From 992 floats a row the
+    two no longer fit one workgroup's LDS beside the candidate slots, so such rounds run unsplit
+    (a 1,000-float cosine search of 18 queries at k = 160 once asked for 168,064 bytes)."""
+    names = {"cosine": "CosineSimilarity", "dot": "DotProduct", "l2": "L2Squared"}
+    rng = np.random.default_rng(dim)
+    base = (rng.standard_normal((28_089, dim)) * 0.5 + 3.0).astype(np.float32)
+    queries = (rng.standard_normal((100, dim)) * 0.5 + 3.0).astype(np.float32)
+    eng = vh.DistributedKnnEngine.try_new(base, dim, 1, vh.GpuShardMode.Sharded, vh.DistanceMetric[names[mname]])
+    for nq, k in ((18, 160), (32, 10), (100, 10)):
+        print(f"  {mname} {base.shape[0]} x {dim} batch {nq} k {k}", flush=True)
+        q = np.ascontiguousarray(queries[:nq])
+        ids, dist, lens = eng.search_batch_arrays(q, k)
+        assert np.all(lens == k)
+        check_knn(oracle, base, q, ids, dist, k, mname, rtol=1e-4, atol=1e-4)

@@ -28,6 +28,14 @@ constexpr int kSmallDense = 2, kSmallFilter = 0;
 // candidate capacity, so it rarely meets more than a couple per query; a full list spills to the
 // global list directly.
 constexpr int kSmallSlots = 16;
+// LDS of one workgroup: the query tile (kSmallCols x dpad floats, dynamic), the K-split's partial
+// sums (dynamic, when ksplit > 1) and the static arrays (at most the FILTER counts and slots) share
+// the 160 KiB of a CU; a dispatch asking for more is not valid.
+constexpr size_t kLdsPerWorkgroup = 160 * 1024;
+constexpr size_t kSmallStaticMax = kSmallCols * sizeof(uint32_t) + kSmallCols * kSmallSlots * 8;
+constexpr size_t kSmallSplitBytes = (size_t)kSmallWaves * 16 * 64 * 4;
+constexpr size_t kSmallDynamicMax = kLdsPerWorkgroup - kSmallStaticMax;
+static_assert((size_t)kSmallCols * kSmallMaxDpad * 4 <= kSmallDynamicMax, "the widest tile fits without a K-split");
 
 struct SmallArgs {
     const float *A;      // base rows (dpad floats each; the row count padded to 256 with NaN rows)
@@ -239,7 +247,7 @@ static void launch_small_m(const SmallArgs &a, dim3 grid, size_t lds, hipStream_
     static bool attr = false;
     if (lds > 65536 && !attr) {
         if (hipFuncSetAttribute((const void *)k_mfma_small<MODE, M>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)(kSmallCols * kSmallMaxDpad * 4 + kSmallWaves * 16 * 64 * 4)) == hipSuccess)
+                                (int)kSmallDynamicMax) == hipSuccess)
             attr = true;
         else
             (void)hipGetLastError();
@@ -270,15 +278,18 @@ void launch_small_scan(int metric, bool dense, const float *base, const float *b
     // K-split: the largest of 8, 4, 2 dividing the chunk count while the round's blocks times the
     // split stay within about two waves per SIMD of the chip (grid_cap workgroups of 8 waves)
     const int nk = dpad / 32;
+    const size_t tile = (size_t)kSmallCols * dpad * sizeof(float);
     int ks = 1;
-    while (ks < kSmallWaves && nk % (2 * ks) == 0 && (long)a.row_blocks * 2 * ks <= (long)grid_cap * kSmallWaves / 2)
+    // (the partial sums must fit beside the tile: not at dpad 992 and 1024)
+    while (ks < kSmallWaves && nk % (2 * ks) == 0 && (long)a.row_blocks * 2 * ks <= (long)grid_cap * kSmallWaves / 2 &&
+           tile + kSmallSplitBytes <= kSmallDynamicMax)
         ks *= 2;
     a.ksplit = ks;
     const int groups = ceil_div(a.row_blocks, kSmallWaves / ks);
     // one workgroup of 8 waves per block group up to four per CU (twice grid_cap): at about 60
     // VGPRs a SIMD then holds 8 waves, whose loads cover each other's memory latency
     const dim3 grid((unsigned)std::min(groups, 2 * per_tile), (unsigned)n_ctiles);
-    const size_t lds = (size_t)kSmallCols * dpad * sizeof(float) + (ks > 1 ? (size_t)kSmallWaves * 16 * 64 * 4 : 0);
+    const size_t lds = tile + (ks > 1 ? kSmallSplitBytes : 0);
     if (dense) {
         if (metric == L2) launch_small_m<kSmallDense, L2>(a, grid, lds, s);
         else if (metric == DOT) launch_small_m<kSmallDense, DOT>(a, grid, lds, s);
