@@ -117,6 +117,21 @@ def test_reruns_split_rounds(vh, oracle):
     _check_pair(vh, oracle, eng, base, q[:9], 100, "l2", rtol=1e-4, atol=1e-9, min_recall=1.0)
 
 
+def test_cut_rounds_score_alike(vh, oracle):
+    """Cosine over rows far from the origin, where the similarities of most rows agree to within a
+    few ulps: the queries overflow their candidate lists on the small-batch plan and are re-run,
+    and the allocation-free search cuts the re-run's rounds to fit the batch's candidate buffer.
+    The small-batch scan splits each score's K range by the length of the whole round, not of the
+    piece, so the scores, and with them the results, come out the same bit for bit (splitting by
+    the piece's length changed the results of 25 of these 100 queries)."""
+    rng = np.random.default_rng(1)
+    base = (rng.standard_normal((60_000, 128)) * 0.5 + 1000.0).astype(np.float32)
+    q = (rng.standard_normal((100, 128)) * 0.5 + 1000.0).astype(np.float32)
+    eng = vh.CudaKnnEngine(base, 128, vh.DistanceMetric.CosineSimilarity)
+    _check_pair(vh, oracle, eng, base, q, 10, "cosine", rtol=1e-4, atol=1e-5)
+    _check_pair(vh, oracle, eng, base, q[:31], 10, "cosine", rtol=1e-4, atol=1e-5)
+
+
 def test_max_k(vh, oracle):
     """k = VHIP_MAX_K: each query's candidate list is half a megabyte, so batches are small."""
     from vector_hip import datasets as ds

@@ -112,6 +112,7 @@ struct Round {
     bool dense;
     long item_rows;  // the slot rule's length, capped at 8192 rows
     long slot_rows;  // the slot rule's length alone
+    long plan_rows = 0;  // a piece of a cut round (split_rounds): the whole round's rows
 };
 
 // Round growth: each round covers `growth` times the rows seen so far.  A round passes about
@@ -335,6 +336,7 @@ static std::vector<Round> split_rounds(const std::vector<Round> &r, long max_row
             Round p = x;
             p.rb = b;
             p.re = std::min(x.re, b + max_rows);
+            p.plan_rows = x.re - x.rb;
             out.push_back(p);
         }
     return out;
@@ -412,7 +414,8 @@ static int run_rounds(vhip_knn *E, const QueryRows &Q, int nq, int k, int kc, in
             }
         } else if (gemm && small_batch(nq, (int)E->dpad, E->n))
             launch_small_scan(E->metric, rd.dense, E->base.as<float>(), E->norm.as<float>(), Q.qpad, Q.qnorm, B.tau,
-                              nq, (int)E->dpad, rb, re, B.cand, B.cnt, cap, E->grid_cap, s);
+                              nq, (int)E->dpad, rb, re, rd.plan_rows ? rd.plan_rows : re - rb, B.cand, B.cnt, cap,
+                              E->grid_cap, s);
         else if (gemm)
             launch_gemm_filter(E->metric, rd.dense, item, E->base.as<float>(), E->norm.as<float>(), Q.qpad, Q.qnorm,
                                B.tau, nq, (int)E->dpad, rb, re, B.cand, B.cnt, cap, E->norm_max, E->norm_min,

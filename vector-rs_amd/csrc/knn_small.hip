@@ -257,7 +257,7 @@ static void launch_small_m(const SmallArgs &a, dim3 grid, size_t lds, hipStream_
 
 void launch_small_scan(int metric, bool dense, const float *base, const float *bnorm, const float *qry,
                        const float *qnorm, const float *tau, int nq, int dpad, long row_begin, long row_end,
-                       uint2 *cand, uint32_t *cnt, int cap, int grid_cap, hipStream_t s) {
+                       long plan_rows, uint2 *cand, uint32_t *cnt, int cap, int grid_cap, hipStream_t s) {
     if (nq <= 0 || row_end <= row_begin) return;
     SmallArgs a{};
     a.A = base;
@@ -276,12 +276,15 @@ void launch_small_scan(int metric, bool dense, const float *base, const float *b
     const int n_ctiles = ceil_div(nq, kSmallCols);
     const int per_tile = std::max(1, grid_cap / n_ctiles);
     // K-split: the largest of 8, 4, 2 dividing the chunk count while the round's blocks times the
-    // split stay within about two waves per SIMD of the chip (grid_cap workgroups of 8 waves)
+    // split stay within about two waves per SIMD of the chip (grid_cap workgroups of 8 waves).  The
+    // blocks are those of the whole round (plan_rows), not of this piece of it, so a score's partial
+    // sums meet in the same order however the round was cut.
     const int nk = dpad / 32;
     const size_t tile = (size_t)kSmallCols * dpad * sizeof(float);
+    const long plan_blocks = (std::max(plan_rows, row_end - row_begin) + 31) / 32;
     int ks = 1;
     // (the partial sums must fit beside the tile: not at dpad 992 and 1024)
-    while (ks < kSmallWaves && nk % (2 * ks) == 0 && (long)a.row_blocks * 2 * ks <= (long)grid_cap * kSmallWaves / 2 &&
+    while (ks < kSmallWaves && nk % (2 * ks) == 0 && plan_blocks * 2 * ks <= (long)grid_cap * kSmallWaves / 2 &&
            tile + kSmallSplitBytes <= kSmallDynamicMax)
         ks *= 2;
     a.ksplit = ks;

@@ -200,10 +200,13 @@ void launch_gemm_filter(int metric, bool dense, long item_rows, const float *bas
                         long row_end, uint2 *cand, uint32_t *cnt, int cap, float anorm_max, float anorm_min,
                         int grid_cap, hipStream_t s);
 // The same round for a small batch (small_batch(nq, dpad)): one wave per 32-row block against the
-// batch's 32-query tile, DENSE or FILTER as above, squared L2, dot product or cosine.
+// batch's 32-query tile, DENSE or FILTER as above, squared L2, dot product or cosine.  plan_rows:
+// the length of the round this launch belongs to (a round cut into pieces passes its whole
+// length), which alone sets how the K range is split over the waves, and so the order in which
+// each score's partial sums meet: a score comes out the same whether its round ran whole or cut.
 void launch_small_scan(int metric, bool dense, const float *base, const float *bnorm, const float *qry,
                        const float *qnorm, const float *tau, int nq, int dpad, long row_begin, long row_end,
-                       uint2 *cand, uint32_t *cnt, int cap, int grid_cap, hipStream_t s);
+                       long plan_rows, uint2 *cand, uint32_t *cnt, int cap, int grid_cap, hipStream_t s);
 
 // Certification of the MFMA k-means assignment: each point's best score must beat its second
 // best by more than twice the point's selection error bound (err_coeff times the norms, with
