@@ -73,3 +73,63 @@ def test_packed_hamming_sweep(vh, oracle, case):
     kk = min(k, n)
     assert np.all(lens == kk)
     assert np.array_equal(dist[:, :kk], rdist[:, :kk]) and np.array_equal(ids[:, :kk], rids[:, :kk])
+
+
+def _wide_cases(count, seed):
+    """Wider shapes than _cases: rows of up to 1,100 floats (the small-batch scan's widest tiles
+    included), batches on both sides of the small-batch limits (32 and 128 queries), k up to 2048,
+    and data kinds that stress the selection: integers, rows far from the origin, duplicates."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(count):
+        n = int(rng.choice([1, 100, 5000, 30_000, 120_000]))
+        dim = int(rng.choice([1, 100, 128, 300, 512, 768, 992, 1000, 1024, 1100]))
+        nq = int(rng.choice([1, 17, 32, 33, 100, 129, 700]))
+        k = int(rng.choice([1, 10, 93, 160, 2048]))
+        metric = METRICS[i % len(METRICS)]
+        kind = ["gauss", "int", "offset", "dup"][(i // len(METRICS)) % 4]
+        while n * nq * dim > 6e8 and nq > 1:
+            nq //= 2
+        out.append((i, n, dim, nq, k, metric, kind))
+    return out
+
+
+def _data(kind, rng, n, dim, pool=None):
+    if kind == "int":
+        return rng.integers(0, 256, (n, dim)).astype(np.float32)
+    if kind == "offset":
+        return (rng.standard_normal((n, dim)) * 0.5 + 1000.0).astype(np.float32)
+    if kind == "dup":
+        return pool[rng.integers(0, len(pool), n)]
+    return rng.standard_normal((n, dim)).astype(np.float32)
+
+
+@pytest.mark.parametrize("case", _wide_cases(48, 2026),
+                         ids=lambda c: f"{c[0]}-n{c[1]}-d{c[2]}-q{c[3]}-k{c[4]}-{c[5]}-{c[6]}")
+def test_wide_engine_sweep(vh, oracle, case):
+    i, n, dim, nq, k, metric, kind = case
+    print(f"wide sweep case {case}", flush=True)
+    rng = np.random.default_rng(3000 + i)
+    if metric == "hamming":  # thresholded float Hamming needs coincident values
+        kind = "binary"
+        base = rng.integers(0, 2, (n, dim)).astype(np.float32)
+        q = rng.integers(0, 2, (nq, dim)).astype(np.float32)
+    else:
+        if metric in ("jaccard", "hellinger"):  # non-negative data for these similarity forms
+            kind = "int"
+        if metric == "cosine" and kind == "offset":  # near-parallel rows: ties below float resolution
+            kind = "gauss"
+        pool = rng.standard_normal((20, dim)).astype(np.float32)
+        base = _data(kind, rng, n, dim, pool)
+        q = _data(kind, rng, nq, dim, pool)
+    eng = vh.CudaKnnEngine(base, dim, vh.DistanceMetric(oracle.METRICS[metric]))
+    ids, dist, lens = eng.search_batch_arrays(q, k)
+    kk = min(k, n)
+    assert np.all(lens == kk)
+    scale = float(np.abs(base).max())
+    atol = 1e-3 if kind == "offset" else 1e-5
+    if metric == "dot":  # a dot product's rounding grows with its terms, not with its value
+        atol = max(atol, 2e-6 * dim * scale * scale)
+    exact = metric == "l2" and kind == "int" and dim <= 256
+    check_knn(oracle, base, q, ids[:, :kk], dist[:, :kk], k, metric, rtol=0.0 if exact else 1e-4,
+              atol=0.0 if exact else atol)
