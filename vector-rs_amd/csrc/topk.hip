@@ -58,8 +58,42 @@ void launch_topk_init(int nq, float *tau, uint32_t *have, uint32_t *cnt, uint32_
 }
 
 // Bitonic sort of P (power of two) keys in LDS, ascending.  Must be called by all threads.
+__device__ __forceinline__ u64 shfl_xor_u64(u64 v, int mask) {
+    const uint32_t lo = __shfl_xor((uint32_t)v, mask, 64), hi = __shfl_xor((uint32_t)(v >> 32), mask, 64);
+    return ((u64)hi << 32) | lo;
+}
+
 __device__ __forceinline__ void bitonic_sort_lds(u64 *buf, int P) {
     const int tid = threadIdx.x, nt = blockDim.x;
+    if (P <= 128) {
+        // Up to 128 keys: one wave sorts them in registers, two a lane (key i in lane i % 64,
+        // register i / 64), exchanging through shuffles, so the network's stages need no
+        // workgroup barrier; the other waves wait at the one barrier after it.
+        if (tid < 64) {
+            u64 a0 = tid < P ? buf[tid] : ~0ull, a1 = tid + 64 < P ? buf[tid + 64] : ~0ull;
+            for (int size = 2; size <= P; size <<= 1) {
+                for (int stride = size >> 1; stride > 0; stride >>= 1) {
+                    if (stride == 64) {  // size 128: keys i and i + 64 meet within the lane, ascending
+                        const u64 mn = a0 < a1 ? a0 : a1, mx = a0 < a1 ? a1 : a0;
+                        a0 = mn;
+                        a1 = mx;
+                        continue;
+                    }
+                    // key i keeps the smaller of it and key i ^ stride when it is the lower of the
+                    // two in an ascending block, or the upper in a descending one
+                    const bool low = (tid & stride) == 0;
+                    const u64 b0 = shfl_xor_u64(a0, stride), b1 = shfl_xor_u64(a1, stride);
+                    const bool min0 = low == ((tid & size) == 0), min1 = low == (((tid + 64) & size) == 0);
+                    a0 = min0 ? (a0 < b0 ? a0 : b0) : (a0 < b0 ? b0 : a0);
+                    a1 = min1 ? (a1 < b1 ? a1 : b1) : (a1 < b1 ? b1 : a1);
+                }
+            }
+            if (tid < P) buf[tid] = a0;
+            if (tid + 64 < P) buf[tid + 64] = a1;
+        }
+        __syncthreads();
+        return;
+    }
     for (int size = 2; size <= P; size <<= 1) {
         for (int stride = size >> 1; stride > 0; stride >>= 1) {
             for (int i = tid; i < (P >> 1); i += nt) {
