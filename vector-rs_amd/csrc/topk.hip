@@ -57,12 +57,13 @@ void launch_topk_init(int nq, float *tau, uint32_t *have, uint32_t *cnt, uint32_
                        cnt0);
 }
 
-// Bitonic sort of P (power of two) keys in LDS, ascending.  Must be called by all threads.
+// A 64-bit key from lane (this lane ^ mask) of the wave.
 __device__ __forceinline__ u64 shfl_xor_u64(u64 v, int mask) {
     const uint32_t lo = __shfl_xor((uint32_t)v, mask, 64), hi = __shfl_xor((uint32_t)(v >> 32), mask, 64);
     return ((u64)hi << 32) | lo;
 }
 
+// Bitonic sort of P (power of two) keys in LDS, ascending.  Must be called by all threads.
 __device__ __forceinline__ void bitonic_sort_lds(u64 *buf, int P) {
     const int tid = threadIdx.x, nt = blockDim.x;
     if (P <= 128) {
@@ -116,14 +117,16 @@ __device__ __forceinline__ void bitonic_sort_lds(u64 *buf, int P) {
 // cand[q][i - have[q]]; its 64-bit key is (score key << 32) | vector id.  Keys are unique (every
 // base row is scanned by exactly one round), so "the k smallest keys" is well defined.
 //
-// Small merges (T = have + c <= kMergeDirect) sort everything in LDS.  Larger ones select
-// first: a histogram of the 32-bit score keys over kMergeBins equal-width buckets of
-// [min, max] finds the bucket holding the k-th smallest; the elements below it (fewer than k)
-// and those in it are gathered into LDS and only they are sorted.  When the boundary bucket is
+// Small merges (T = have + c <= kMergeDirect, sorted by one wave in registers) sort everything.
+// Larger ones select first: a histogram of the 32-bit score keys over kMergeBins equal-width
+// buckets of [min, max] finds the bucket holding the k-th smallest; the elements below it (fewer
+// than k) and those in it are gathered into LDS and only they are sorted.  When the boundary bucket is
 // too large for the buffer (massive score ties) the merge falls back to sorting chunks of the
 // elements against the running best k.
 constexpr int kMergeBins = 1024;
-constexpr int kMergeDirect = 512;
+// Selecting first pays from about a hundred entries on: with 400 entries (a k = 100 round), the
+// select and a 128-key register sort take 58 us a merge of 10,000 queries, a 512-key LDS sort 81.
+constexpr int kMergeDirect = 128;
 constexpr int kMergeCached = 16;  // list entries per thread held in registers through the select
 
 // The minimum of lo and the maximum of hi over the workgroup, in one round of LDS (red: 2 words
