@@ -303,3 +303,30 @@ def test_small_set_edges(vh, oracle, n, dim, k, metric):
     st.set_centroids(cent)
     st.run(1)
     _check_step(oracle, data, cent, st.read(), metric, max_flip_frac=1.0 / n)
+
+
+@pytest.mark.parametrize("metric", ["cosine", "dot"])
+def test_inertia_of_points_that_are_centroids(vh, oracle, metric):
+    """Integer points in [0, 255] at 1024 dimensions, 400 of the 600 of them centroids: a point's
+    value against itself is 1 - cos = 0 (or -||x||^2), which a sequential float sum over the
+    dimensions misses by about 6e-6 each (odd squares added to an even running sum above 2^24 all
+    round down).  The reported inertia is the sum of the per-point values in direct form, within
+    rounding of the float64 sum over the GPU's own assignment."""
+    rng = np.random.default_rng(77)
+    n, dim, k = 600, 1024, 400
+    data = rng.integers(0, 256, (n, dim)).astype(np.float32)
+    cent = data[rng.choice(n, size=k, replace=False)].copy()
+    st = vh.KMeansState(data, vh.DistanceMetric(oracle.METRICS[metric]))
+    st.set_centroids(cent)
+    st.run(1)
+    got = st.read()
+    _check_step(oracle, data, cent, got, metric, max_flip_frac=1.0 / n)
+    x, c = data.astype(np.float64), cent.astype(np.float64)[got["assign"]]
+    dots = np.einsum("ij,ij->i", x, c)
+    if metric == "dot":
+        want = -dots.sum()
+        assert abs(got["inertia"] - want) <= 1e-6 * abs(want)
+    else:
+        den = np.linalg.norm(x, axis=1) * np.linalg.norm(c, axis=1)
+        want = np.sum(1.0 - dots / den)
+        assert abs(got["inertia"] - want) <= 2e-7 * n + 2e-6 * abs(want)

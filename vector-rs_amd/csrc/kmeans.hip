@@ -133,8 +133,14 @@ __global__ void k_dev_bound(int k, float absmax, const float *__restrict__ cabs,
 // l, l + 64, ...; the wave adds the deviations x - c of the rows of its window (spw sorted
 // slots; integer sums, so the window size does not change them) slot by slot in
 // fixed point (the cluster's scale) and flushes the running sum into sums[c] whenever the window
-// crosses into the next cluster's segment.  With `l2_inertia` it also writes each point's
-// squared distance sum_d (x_d - c_d)^2 (lane-strided sum, fixed xor butterfly).
+// crosses into the next cluster's segment.  It also writes each point's value against the centroid
+// its assignment used, in direct form (lane-strided sums, fixed xor butterfly), by `inertia_mode`:
+// 1 the squared distance sum_d (x_d - c_d)^2, 2 -x.c, 3 1 - x.c / (||x|| ||c||) (0 below the
+// 1e-9 guard; pnorm and cnorm hold the L2 norms), 0 none (the assignment wrote it).  Lane-strided
+// partial sums keep these values exact-to-rounding where a sequential sum drifts: adding odd
+// squares to an even running sum above 2^24 rounds each of them down, so a point's product with
+// itself as a centroid came out about 6e-6 short of its norm squared at 1024 dimensions of
+// integers in [0, 255].
 template <int S>
 constexpr int upd_unroll() { return S >= 8 ? 4 : (S >= 4 ? 8 : 16); }  // rows in flight per wave
 
@@ -145,7 +151,8 @@ __global__ __launch_bounds__(256) void k_update_sums(const float *__restrict__ p
                                                      const int32_t *__restrict__ offsets,
                                                      const int32_t *__restrict__ exps,
                                                      unsigned long long *__restrict__ sums, float *__restrict__ inertia,
-                                                     int l2_inertia, int spw) {
+                                                     int inertia_mode, const float *__restrict__ pnorm,
+                                                     const float *__restrict__ cnorm, int spw) {
     constexpr int kUpdUnroll = upd_unroll<S>();
     const int lane = threadIdx.x & 63;
     const int wave = (int)((blockIdx.x * (size_t)blockDim.x + threadIdx.x) >> 6);
@@ -204,17 +211,26 @@ __global__ __launch_bounds__(256) void k_update_sums(const float *__restrict__ p
                         }
                         load_c(c);
                     }
-                    float d2 = 0.0f;
+                    float d2 = 0.0f, xc = 0.0f;
 #pragma unroll
                     for (int s = 0; s < S; ++s) {
                         acc[s] += llrint(((double)v[u][s] - (double)cv[s]) * scale);
                         const float t = v[u][s] - cv[s];
                         d2 = fmaf(t, t, d2);
+                        xc = fmaf(v[u][s], cv[s], xc);
                     }
-                    if (l2_inertia) {
+                    if (inertia_mode) {
+                        float r = inertia_mode == 1 ? d2 : xc;
 #pragma unroll
-                        for (int o = 32; o > 0; o >>= 1) d2 += __shfl_xor(d2, o, 64);
-                        if (lane == 0) inertia[__builtin_amdgcn_readlane(mine, j + u)] = d2;
+                        for (int o = 32; o > 0; o >>= 1) r += __shfl_xor(r, o, 64);
+                        const int p = __builtin_amdgcn_readlane(mine, j + u);
+                        if (inertia_mode == 2) {
+                            r = -r + 0.0f;
+                        } else if (inertia_mode == 3) {
+                            const float den = pnorm[p] * cnorm[c];
+                            r = 1.0f + (den > 1e-9f ? -(r / den) + 0.0f : 0.0f);
+                        }
+                        if (lane == 0) inertia[p] = r;
                     }
                 }
             }
@@ -969,13 +985,16 @@ static int km_iterate(vhip_kmeans *K) {
     int spw = kUpdSlotsPerWave;  // slots per wave: fewer for small point sets, so they fill the GPU
     while (spw > kUpdMinSlots && ceil_div(n, spw) < kUpdMinWaves) spw >>= 1;
     const int waves = ceil_div(n, spw);
-    const int l2 = K->metric == L2 ? 1 : 0;
+    // the per-point values in direct form (kmeans.cu:110-170's squared distance, -dot, 1 - cos);
+    // the other metrics' assignment wrote them
+    const int mode = K->metric == L2 ? 1 : (K->metric == DOT ? 2 : (K->metric == COS ? 3 : 0));
     unsigned long long *sums = K->sums.as<unsigned long long>();
 #define VH_UPD(S)                                                                                                  \
     do {                                                                                                           \
         hipLaunchKernelGGL(k_update_sums<S>, dim3(ceil_div(waves, 4)), dim3(256), 0, s, K->points(),               \
                            K->craw.as<float>(), (int)K->dpad, (int)K->dim, n, k, K->sorted.as<int32_t>(),          \
-                           K->offsets.as<int32_t>(), K->exps.as<int32_t>(), sums, K->inertia.as<float>(), l2, spw); \
+                           K->offsets.as<int32_t>(), K->exps.as<int32_t>(), sums, K->inertia.as<float>(), mode,         \
+                           K->pnorm.as<float>(), K->cnorm.as<float>(), spw);                                        \
         hipLaunchKernelGGL(k_update_finalize<S>, dim3(ceil_div(k, 4)), dim3(256), 0, s, k, (int)K->dpad,          \
                            (int)K->dim, sums, K->counts.as<int32_t>(), K->exps.as<int32_t>(), K->craw.as<float>(), \
                            K->shifts.as<float>());                                                                  \
