@@ -310,6 +310,19 @@ static int ivfpq_init(vhip_ivfpq *X, int ordinal, size_t dim, int metric, const 
 // run instead of one per pair (the per-pair atomics serialised on its counter).
 constexpr int kPlanBins = 8192, kPlanPer = 16, kPlanPairs = 256 * kPlanPer;
 
+// The list-major search's starting state in one launch: the queries' thresholds (2 nq words of
+// ones: no threshold yet), the per-list pair counters and cursors (2 nlist zeros) and the item
+// counters (2 zeros).
+__global__ void k_list_reset(uint32_t *__restrict__ tau, size_t n_tau, uint32_t *__restrict__ cnt, size_t n_cnt,
+                             uint32_t *__restrict__ ctr) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n_tau + n_cnt + 2; i += stride) {
+        if (i < n_tau) tau[i] = 0xffffffffu;
+        else if (i < n_tau + n_cnt) cnt[i - n_tau] = 0u;
+        else ctr[i - n_tau - n_cnt] = 0u;
+    }
+}
+
 __global__ __launch_bounds__(256) void k_pair_count(const uint32_t *__restrict__ probes, int total, int nlist,
                                                     uint32_t *__restrict__ cnt) {
     __shared__ uint32_t h[kPlanBins];
@@ -477,6 +490,24 @@ static int ivfpq_search_chunk(vhip_ivfpq *X, const float *d_q, size_t nq, size_t
     hipStream_t s = X->stream;
     VH_CHECK(X->d_pid.ensure(X->dev, nq * np * 4));
     VH_CHECK(X->d_pdist.ensure(X->dev, nq * np * 4));
+    const bool lists = list_path(X, k, np);
+    if (lists) {
+        // the plan's buffers, cleared on this stream while the probe runs on the probe engine's
+        const size_t total = nq * np;
+        VH_CHECK(X->d_lcnt.ensure(X->dev, 2 * X->nlist * 4));
+        VH_CHECK(X->d_loff.ensure(X->dev, 2 * X->nlist * 4));
+        VH_CHECK(X->d_pairs.ensure(X->dev, total * 4));
+        VH_CHECK(X->d_items.ensure(X->dev, 2 * total * sizeof(uint4)));  // records, then pair ids
+        VH_CHECK(X->d_lctr.ensure(X->dev, 2 * 4));
+        VH_CHECK(X->d_pout.ensure(X->dev, total * k * 8));
+        VH_CHECK(X->d_tau.ensure(X->dev, nq * 8));
+        VH_CHECK(open_device(X->dev));
+        const size_t words = 2 * nq + 2 * X->nlist + 2;
+        hipLaunchKernelGGL(k_list_reset, dim3((unsigned)std::min<size_t>(1024, (words + 255) / 256)), dim3(256), 0, s,
+                           X->d_tau.as<uint32_t>(), 2 * nq, X->d_lcnt.as<uint32_t>(), 2 * X->nlist,
+                           X->d_lctr.as<uint32_t>());
+        VH_HIP(hipGetLastError());
+    }
     VH_CHECK(vhip_knn_search_batch_device(X->probe, d_q, nq, np, X->d_pid.as<uint32_t>(), X->d_pdist.as<float>()));
     VH_CHECK(open_device(X->dev));
     ScanArgs A;
@@ -510,19 +541,9 @@ static int ivfpq_search_chunk(vhip_ivfpq *X, const float *d_q, size_t nq, size_t
         return set_error(VHIP_ERR_INVALID_CONFIG, "k = " + std::to_string(k) + " needs " + std::to_string(lds) +
                                                       " bytes of LDS with this index, the device allows " +
                                                       std::to_string(X->lds_limit));
-    if (list_path(X, k, np)) {
+    if (lists) {
         const size_t total = nq * np;
-        VH_CHECK(X->d_lcnt.ensure(X->dev, 2 * X->nlist * 4));
-        VH_CHECK(X->d_loff.ensure(X->dev, 2 * X->nlist * 4));
-        VH_CHECK(X->d_pairs.ensure(X->dev, total * 4));
-        VH_CHECK(X->d_items.ensure(X->dev, 2 * total * sizeof(uint4)));  // records, then pair ids
-        VH_CHECK(X->d_lctr.ensure(X->dev, 2 * 4));
-        VH_CHECK(X->d_pout.ensure(X->dev, total * k * 8));
-        VH_CHECK(X->d_tau.ensure(X->dev, nq * 8));
-        launch_fill_u32(X->d_tau.as<uint32_t>(), 2 * nq, 0xffffffffu, s);
         uint32_t *cnt = X->d_lcnt.as<uint32_t>(), *ctr = X->d_lctr.as<uint32_t>();
-        launch_fill_u32(cnt, 2 * X->nlist, 0u, s);
-        launch_fill_u32(ctr, 2, 0u, s);
         uint4 *items = X->d_items.as<uint4>(), *item_pairs = items + total;
         ivfpq_list_plan(A.probes, (int)nq, (int)np, (int)X->nlist, X->d_order.as<uint32_t>(), A.list_off, cnt,
                         cnt + X->nlist, X->d_loff.as<uint32_t>(), X->d_loff.as<uint32_t>() + X->nlist,

@@ -489,6 +489,13 @@ void launch_topk_finalize(int nq, int kc, int kout, int metric, const unsigned l
 // each, 16 at a time, with float4 reads of the row and the query (lane s sums pieces s, s + 16,
 // ... in order) and a fixed xor butterfly.  A query with a zero bound (squared L2 or dot product
 // on integer rows within 2^24) skips the recomputation: its scores are already the exact values.
+// Sort-buffer entries of the refine: a power of two holding kc keys (at least 2).
+__host__ __device__ __forceinline__ int refine_sort_entries(int kc) {
+    int p = 2;
+    while (p < kc) p <<= 1;
+    return p;
+}
+
 __global__ __launch_bounds__(256) void k_topk_refine(int k, int kc, int kout, int metric,
                                                      const float *__restrict__ qrows, const float *__restrict__ base,
                                                      const float *__restrict__ shift,
@@ -497,9 +504,11 @@ __global__ __launch_bounds__(256) void k_topk_refine(int k, int kc, int kout, in
                                                      const u64 *__restrict__ topk, const uint32_t *__restrict__ have,
                                                      const float *__restrict__ qerr, uint32_t *__restrict__ out_ids,
                                                      float *__restrict__ out_dist, int ostride, FlagPublish pub) {
-    __shared__ u64 buf[2 * kMaxK];  // a power of two >= kMaxKeep
+    // dynamic LDS sized by the launch for kc: the sort buffer (refine_sort_entries(kc), a power of
+    // two >= kc) and the kept entries' rows (kc), so a small kc keeps many workgroups per CU
+    extern __shared__ u64 buf[];
+    uint32_t *s_row = (uint32_t *)(buf + refine_sort_entries(kc));
     if (blockIdx.x == 0 && threadIdx.x == 0) publish_flags(pub);
-    __shared__ uint32_t s_row[kMaxKeep];
     __shared__ int s_h;
     const int q = blockIdx.x, tid = threadIdx.x;
     const u64 *tq = topk + (size_t)q * kc;
@@ -612,8 +621,10 @@ void launch_topk_refine(int nq, int k, int kc, int kout, int metric, const float
                         const unsigned long long *topk, const uint32_t *have, const float *qerr, uint32_t *out_ids,
                         float *out_dist, int ostride, const FlagPublish &pub, hipStream_t s) {
     if (nq <= 0) return;
-    hipLaunchKernelGGL(k_topk_refine, dim3(nq), dim3(256), 0, s, k, kc, kout, metric, qrows, base, shift, inv_perm, dpad,
-                       qnorm, bnorm, topk, have, qerr, out_ids, out_dist, ostride, pub);
+    // at most kMaxKeep entries: 4096 x 8 + 2304 x 4 bytes, within the default 64 KB
+    const size_t lds = (size_t)refine_sort_entries(kc) * sizeof(u64) + (size_t)kc * sizeof(uint32_t);
+    hipLaunchKernelGGL(k_topk_refine, dim3(nq), dim3(256), lds, s, k, kc, kout, metric, qrows, base, shift, inv_perm,
+                       dpad, qnorm, bnorm, topk, have, qerr, out_ids, out_dist, ostride, pub);
 }
 
 }  // namespace vh
