@@ -53,6 +53,7 @@ struct RunBufs {
     uint32_t *have = nullptr, *cnt = nullptr, *flags = nullptr, *mflag = nullptr;  // nq each
     uint32_t *nflag = nullptr;             // 2 counters
     int8_t *q8 = nullptr;                  // expanded query codes (packed Hamming on fp4 MFMA)
+    uint32_t *spad = nullptr;              // the small-batch scan's spread counters (launch_small_scan)
 };
 
 struct Workspace {
@@ -322,6 +323,10 @@ static RunBufs carve_run(Arena &A, const vhip_knn *E, size_t nq, int kc, int cap
     B.mflag = A.take<uint32_t>(nq);
     B.nflag = A.take<uint32_t>(2);
     if (E->ham8) B.q8 = A.take<int8_t>(round_up(nq, kTileCols) * ham_mfma_row_bytes((int)E->dpad));
+    if (is_gemm_metric(E->metric)) {
+        // any run of at most kSmallPadQueries of these queries may take the small-batch scan
+        B.spad = A.take<uint32_t>(std::min<size_t>(nq, kSmallPadQueries) * kSmallPadStride);
+    }
     return B;
 }
 
@@ -363,7 +368,7 @@ static int run_rounds(vhip_knn *E, const QueryRows &Q, int nq, int k, int kc, in
     // the first round's candidate count: its rows when it is dense (every score is written)
     const bool dense0 = !rounds.empty() && (rounds[0].dense || (E->ham8 && rounds[0].rb == 0));
     launch_topk_init(nq, B.tau, B.have, B.cnt, B.flags, B.mflag, B.nflag,
-                     dense0 ? (uint32_t)(rounds[0].re - rounds[0].rb) : 0u, s);
+                     dense0 ? (uint32_t)(rounds[0].re - rounds[0].rb) : 0u, B.spad, s);
     if (E->ham8) {
         // the queries' +1/-1 nibbles, rows padded to the 128-query tiles
         const size_t rows = round_up((size_t)nq, kTileCols);
@@ -384,6 +389,9 @@ static int run_rounds(vhip_knn *E, const QueryRows &Q, int nq, int k, int kc, in
         const double bytes = E->ham8 ? (rows + nq) * (double)ham_mfma_row_bytes((int)E->dpad)  // expanded codes
                                      : rows * E->dim * 4.0 + (double)nq * E->dim * 4.0;
         if (dense && ri > 0) launch_fill_u32(B.cnt, (size_t)nq, (uint32_t)(re - rb), s);
+        // the small-batch scan's FILTER rounds count candidates on B.spad (kSmallPadStride apart)
+        const bool small_scan = !E->ham8 && gemm && small_batch(nq, (int)E->dpad, E->n);
+        const bool spread = small_scan && !rd.dense;
         const int t = (direct || !timed) ? -1 : E->timer.begin(s);
         // the narrow resident-tile kernel (gemm_narrow) works in 512-row stages on 32-column tiles
         const bool narrow = gemm && gemm_narrow((int)E->dpad);
@@ -412,10 +420,10 @@ static int run_rounds(vhip_knn *E, const QueryRows &Q, int nq, int k, int kc, in
                 launch_ham_mfma(dense, hitem, E->base8.as<int8_t>(), B.q8, (int)E->dpad, B.tau, nq, rb, re, B.cand,
                                 B.cnt, cap, E->grid_cap, s);
             }
-        } else if (gemm && small_batch(nq, (int)E->dpad, E->n))
+        } else if (small_scan)
             launch_small_scan(E->metric, rd.dense, E->base.as<float>(), E->norm.as<float>(), Q.qpad, Q.qnorm, B.tau,
-                              nq, (int)E->dpad, rb, re, rd.plan_rows ? rd.plan_rows : re - rb, B.cand, B.cnt, cap,
-                              E->grid_cap, s);
+                              nq, (int)E->dpad, rb, re, rd.plan_rows ? rd.plan_rows : re - rb, B.cand, B.cnt, B.spad,
+                              cap, E->grid_cap, s);
         else if (gemm)
             launch_gemm_filter(E->metric, rd.dense, item, E->base.as<float>(), E->norm.as<float>(), Q.qpad, Q.qnorm,
                                B.tau, nq, (int)E->dpad, rb, re, B.cand, B.cnt, cap, E->norm_max, E->norm_min,
@@ -433,7 +441,8 @@ static int run_rounds(vhip_knn *E, const QueryRows &Q, int nq, int k, int kc, in
         VH_HIP(hipGetLastError());
         // the last round counts the standing margin flags into nflag[1]
         const bool last = ri + 1 == rounds.size();
-        launch_topk_merge(nq, k, kc, B.cand, B.cnt, cap, E->perm.as<uint32_t>(), B.topk, B.have, B.tau, B.flags,
+        launch_topk_merge(nq, k, kc, B.cand, spread ? B.spad : B.cnt, spread ? kSmallPadStride : 1, cap,
+                          E->perm.as<uint32_t>(), B.topk, B.have, B.tau, B.flags,
                           B.nflag, gemm ? Q.qerr : nullptr, B.mflag, last && gemm ? B.nflag + 1 : nullptr,
                           dense && re - rb > 4096, s);
         VH_HIP(hipGetLastError());

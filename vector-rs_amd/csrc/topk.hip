@@ -16,7 +16,7 @@ namespace vh {
 typedef unsigned long long u64;
 
 __global__ void k_topk_init(int nq, float *tau, uint32_t *have, uint32_t *cnt, uint32_t *flags, uint32_t *mflag,
-                            uint32_t *nflag, uint32_t cnt0) {
+                            uint32_t *nflag, uint32_t cnt0, uint32_t *pad) {
     const int q = blockIdx.x * blockDim.x + threadIdx.x;
     if (q < nq) {
         tau[q] = INFINITY;
@@ -24,6 +24,7 @@ __global__ void k_topk_init(int nq, float *tau, uint32_t *have, uint32_t *cnt, u
         cnt[q] = cnt0;
         flags[q] = 0;
         mflag[q] = 0;
+        if (pad && q < kSmallPadQueries) pad[(size_t)q * kSmallPadStride] = 0;
     }
     if (q < 2) nflag[q] = 0;
 }
@@ -51,10 +52,10 @@ void launch_fill_u32(uint32_t *p, size_t count, uint32_t v, hipStream_t s) {
 }
 
 void launch_topk_init(int nq, float *tau, uint32_t *have, uint32_t *cnt, uint32_t *flags, uint32_t *mflag,
-                      uint32_t *nflag, uint32_t cnt0, hipStream_t s) {
+                      uint32_t *nflag, uint32_t cnt0, uint32_t *pad, hipStream_t s) {
     if (nq <= 0) return;
     hipLaunchKernelGGL(k_topk_init, dim3(ceil_div(nq, 256)), dim3(256), 0, s, nq, tau, have, cnt, flags, mflag, nflag,
-                       cnt0);
+                       cnt0, pad);
 }
 
 // A 64-bit key from lane (this lane ^ mask) of the wave.
@@ -157,7 +158,7 @@ __device__ __forceinline__ void block_minmax_u32(uint32_t &lo, uint32_t &hi, uin
 // scores are latency-bound (each thread keeps four independent loads in flight).
 template <int NT>
 __global__ __launch_bounds__(NT) void k_topk_merge(int k, int kc, int bufn, const uint2 *__restrict__ cand,
-                                                    uint32_t *__restrict__ cnt, int cap,
+                                                    uint32_t *__restrict__ cnt, int cnt_stride, int cap,
                                                     const uint32_t *__restrict__ perm, u64 *__restrict__ topk,
                                                     uint32_t *__restrict__ have, float *__restrict__ tau,
                                                     uint32_t *__restrict__ flags, uint32_t *__restrict__ nflagged,
@@ -169,11 +170,12 @@ __global__ __launch_bounds__(NT) void k_topk_merge(int k, int kc, int bufn, cons
     __shared__ uint32_t s_part[NT / 64];
     __shared__ uint32_t s_sel[4];  // boundary bucket, count below it, gather counters
     const int q = blockIdx.x, tid = threadIdx.x;
-    const uint32_t c_all = cnt[q];
+    uint32_t *const cq_cnt = cnt + (size_t)q * cnt_stride;  // this query's candidate count
+    const uint32_t c_all = *cq_cnt;
     if (flags[q] || c_all == 0) {
         __syncthreads();
         if (tid == 0) {
-            cnt[q] = 0;
+            *cq_cnt = 0;
             // the last round counts the margin flags as they stand (an overflowed query is re-run
             // and counted again afterwards)
             if (mcount && !flags[q] && mflag[q]) atomicAdd(mcount, 1u);
@@ -315,7 +317,7 @@ __global__ __launch_bounds__(NT) void k_topk_merge(int k, int kc, int bufn, cons
     for (uint32_t i = tid; i < hn; i += NT) tk[i] = buf[i];
     if (tid == 0) {
         have[q] = hn;
-        cnt[q] = 0;
+        *cq_cnt = 0;
         if (overflow) {
             // The list is incomplete: stop filtering for this query; the host re-runs it
             // with a capacity that cannot overflow.
@@ -351,7 +353,8 @@ int merge_buffer_entries(int kc) {
 }
 
 template <int NT>
-static void launch_merge_nt(int nq, int k, int kc, const uint2 *cand, uint32_t *cnt, int cap, const uint32_t *perm,
+static void launch_merge_nt(int nq, int k, int kc, const uint2 *cand, uint32_t *cnt, int cnt_stride, int cap,
+                            const uint32_t *perm,
                             unsigned long long *topk, uint32_t *have, float *tau, uint32_t *flags, uint32_t *nflagged,
                             const float *qerr, uint32_t *mflag, uint32_t *mcount, hipStream_t s) {
     const int bufn = merge_buffer_entries(kc);
@@ -364,19 +367,20 @@ static void launch_merge_nt(int nq, int k, int kc, const uint2 *cand, uint32_t *
         (void)hipGetLastError();
         attr_set = true;
     }
-    hipLaunchKernelGGL(k_topk_merge<NT>, dim3(nq), dim3(NT), lds, s, k, kc, bufn, cand, cnt, cap, perm, topk, have,
-                       tau, flags, nflagged, qerr, mflag, mcount);
+    hipLaunchKernelGGL(k_topk_merge<NT>, dim3(nq), dim3(NT), lds, s, k, kc, bufn, cand, cnt, cnt_stride, cap, perm,
+                       topk, have, tau, flags, nflagged, qerr, mflag, mcount);
 }
 
-void launch_topk_merge(int nq, int k, int kc, const uint2 *cand, uint32_t *cnt, int cap, const uint32_t *perm,
-                       unsigned long long *topk, uint32_t *have, float *tau, uint32_t *flags, uint32_t *nflagged,
-                       const float *qerr, uint32_t *mflag, uint32_t *mcount, bool wide, hipStream_t s) {
+void launch_topk_merge(int nq, int k, int kc, const uint2 *cand, uint32_t *cnt, int cnt_stride, int cap,
+                       const uint32_t *perm, unsigned long long *topk, uint32_t *have, float *tau, uint32_t *flags,
+                       uint32_t *nflagged, const float *qerr, uint32_t *mflag, uint32_t *mcount, bool wide,
+                       hipStream_t s) {
     if (nq <= 0) return;
     if (wide)
-        launch_merge_nt<1024>(nq, k, kc, cand, cnt, cap, perm, topk, have, tau, flags, nflagged, qerr, mflag, mcount,
+        launch_merge_nt<1024>(nq, k, kc, cand, cnt, cnt_stride, cap, perm, topk, have, tau, flags, nflagged, qerr, mflag, mcount,
                               s);
     else
-        launch_merge_nt<256>(nq, k, kc, cand, cnt, cap, perm, topk, have, tau, flags, nflagged, qerr, mflag, mcount,
+        launch_merge_nt<256>(nq, k, kc, cand, cnt, cnt_stride, cap, perm, topk, have, tau, flags, nflagged, qerr, mflag, mcount,
                              s);
 }
 

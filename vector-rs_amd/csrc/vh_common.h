@@ -204,9 +204,14 @@ void launch_gemm_filter(int metric, bool dense, long item_rows, const float *bas
 // the length of the round this launch belongs to (a round cut into pieces passes its whole
 // length), which alone sets how the K range is split over the waves, and so the order in which
 // each score's partial sums meet: a score comes out the same whether its round ran whole or cut.
+// FILTER launches count each query's candidates on pad[q * kSmallPadStride] (one 128-byte line
+// per query; pad holds min(nq, kSmallPadQueries) counters, zero before the round) instead of
+// cnt[q], and the round's merge reads them there (launch_topk_merge with that stride).
+constexpr int kSmallPadStride = 32, kSmallPadQueries = 4 * kSmallCols;
 void launch_small_scan(int metric, bool dense, const float *base, const float *bnorm, const float *qry,
                        const float *qnorm, const float *tau, int nq, int dpad, long row_begin, long row_end,
-                       long plan_rows, uint2 *cand, uint32_t *cnt, int cap, int grid_cap, hipStream_t s);
+                       long plan_rows, uint2 *cand, uint32_t *cnt, uint32_t *pad, int cap, int grid_cap,
+                       hipStream_t s);
 
 // Certification of the MFMA k-means assignment: each point's best score must beat its second
 // best by more than twice the point's selection error bound (err_coeff times the norms, with
@@ -232,9 +237,10 @@ void launch_kmeans_assign(int metric, const float *cent, const float *cnorm, int
 
 // topk.hip
 // Resets a run's per-query state: tau = +inf, have = flags = mflag = 0, cnt = cnt0 (the first
-// round's rows when that round is dense), and the two flag counters.
+// round's rows when that round is dense), and the two flag counters; with `pad` (may be null) also
+// the small-batch scan's counters pad[q * kSmallPadStride] for q < min(nq, kSmallPadQueries).
 void launch_topk_init(int nq, float *tau, uint32_t *have, uint32_t *cnt, uint32_t *flags, uint32_t *mflag,
-                      uint32_t *nflag, uint32_t cnt0, hipStream_t s);
+                      uint32_t *nflag, uint32_t cnt0, uint32_t *pad, hipStream_t s);
 // Merges each query's candidates into its running best entries (row stride kc of topk).  A query
 // with qerr[q] > 0 (qerr may be null: all 0) keeps its kc best entries and filters later rounds at
 // tau = min(kc-th score, k-th score + 2 qerr[q]), so the final entries hold every row whose score
@@ -243,9 +249,12 @@ void launch_topk_init(int nq, float *tau, uint32_t *have, uint32_t *cnt, uint32_
 // run's last round only): incremented once per query whose margin flag stands at the end of the
 // round, overflowed queries excepted.  wide: 1024 threads per query instead of 256 (a dense round
 // of many rows).
-void launch_topk_merge(int nq, int k, int kc, const uint2 *cand, uint32_t *cnt, int cap, const uint32_t *perm,
-                       unsigned long long *topk, uint32_t *have, float *tau, uint32_t *flags, uint32_t *nflagged,
-                       const float *qerr, uint32_t *mflag, uint32_t *mcount, bool wide, hipStream_t s);
+// cnt: query q's candidate count is cnt[q * cnt_stride] (1, or kSmallPadStride for a small-batch
+// FILTER round's spread counters), cleared by the merge.
+void launch_topk_merge(int nq, int k, int kc, const uint2 *cand, uint32_t *cnt, int cnt_stride, int cap,
+                       const uint32_t *perm, unsigned long long *topk, uint32_t *have, float *tau, uint32_t *flags,
+                       uint32_t *nflagged, const float *qerr, uint32_t *mflag, uint32_t *mcount, bool wide,
+                       hipStream_t s);
 // Where the final kernel of a search (refine or finalize) copies the two flag counters src[0..1]:
 // host = pinned host memory, or null for no copy.
 struct FlagPublish {
