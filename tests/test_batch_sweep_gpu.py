@@ -69,3 +69,23 @@ def test_small_batches_with_the_widest_rows(vh, oracle, dim, mname):
         ids, dist, lens = eng.search_batch_arrays(q, k)
         assert np.all(lens == k)
         check_knn(oracle, base, q, ids, dist, k, mname, rtol=1e-4, atol=1e-4)
+
+
+@pytest.mark.parametrize("mname,k", [("l2", 10), ("l2", 100), ("cosine", 10), ("dot", 10)])
+def test_mid_batches_on_a_large_base_of_short_rows(vh, oracle, mname, k):
+    """Batches of 33 to 128 queries over a base of more than 262,144 rows of at most 128 floats also
+    take the small-batch scan (four 32-query tiles), whose candidate counters sit one cache line
+    apart; each batch against the oracle."""
+    from vector_hip import datasets as ds
+
+    names = {"cosine": "CosineSimilarity", "dot": "DotProduct", "l2": "L2Squared"}
+    n, d = 300_000, 64
+    base = ds.uniform_int(n, d, 55) if mname == "l2" else ds.uniform(n, d, 55)
+    q = ds.uniform_int(128, d, 56) if mname == "l2" else ds.uniform(128, d, 56)
+    eng = vh.CudaKnnEngine(base, d, vh.DistanceMetric[names[mname]])
+    tol = dict(rtol=0.0, atol=0.0) if mname == "l2" else dict(rtol=1e-4, atol=1e-5)
+    for b in (33, 64, 100, 128):
+        print(f"  {mname} {n} x {d} batch {b} k={k}", flush=True)
+        ids, dist, lens = eng.search_batch_arrays(np.ascontiguousarray(q[:b]), k)
+        assert np.all(lens == k)
+        check_knn(oracle, base, q[:b], ids, dist, k, mname, **tol)

@@ -51,14 +51,17 @@ inline int gemm_slots(int dpad) {
                        : (gemm_narrow(dpad) ? kGemmSlotsNarrow : (dpad % 128 == 0 ? kGemmSlotsPanel : kGemmSlotsStream));
 }
 // Batches of at most kSmallCols queries (one 32-query tile), or up to four tiles over a base of at
-// most kSmallBaseRows rows (where every search is bound by launches, not by scanned pairs), with
-// rows of at most kSmallMaxDpad floats take the small-batch MFMA scan (knn_small.hip), which spreads
-// every round over all CUs.
+// most kSmallBaseRows rows (where every search is bound by launches, not by scanned pairs) or of
+// rows of at most 128 floats, with rows of at most kSmallMaxDpad floats take the small-batch MFMA
+// scan (knn_small.hip), which spreads every round over all CUs.  (1M x 128 integer squared L2,
+// k = 10: 64 queries 245 us against 432 on the batch kernels, whose 128-query tiles run half
+// empty, and 128 queries 411 against 440.)
 constexpr int kSmallCols = 32;
 constexpr int kSmallMaxDpad = 1024;
 constexpr size_t kSmallBaseRows = 262144;
 inline bool small_batch(int nq, int dpad, size_t n) {
-    return dpad <= kSmallMaxDpad && (nq <= kSmallCols || (nq <= 4 * kSmallCols && n <= kSmallBaseRows));
+    return dpad <= kSmallMaxDpad &&
+           (nq <= kSmallCols || (nq <= 4 * kSmallCols && (n <= kSmallBaseRows || dpad <= 128)));
 }
 constexpr int kRowAlign = 256;       // row counts of MFMA row operands and round boundaries
                                      // are multiples of this (the largest MFMA stage)
