@@ -422,8 +422,8 @@ static int run_rounds(vhip_knn *E, const QueryRows &Q, int nq, int k, int kc, in
             }
         } else if (small_scan)
             launch_small_scan(E->metric, rd.dense, E->base.as<float>(), E->norm.as<float>(), Q.qpad, Q.qnorm, B.tau,
-                              nq, (int)E->dpad, rb, re, rd.plan_rows ? rd.plan_rows : re - rb, B.cand, B.cnt, B.spad,
-                              cap, E->grid_cap, s);
+                              nq, (int)E->dpad, rb, re, rd.plan_rows ? rd.plan_rows : re - rb, B.cand, B.spad, cap,
+                              E->grid_cap, s);
         else if (gemm)
             launch_gemm_filter(E->metric, rd.dense, item, E->base.as<float>(), E->norm.as<float>(), Q.qpad, Q.qnorm,
                                B.tau, nq, (int)E->dpad, rb, re, B.cand, B.cnt, cap, E->norm_max, E->norm_min,

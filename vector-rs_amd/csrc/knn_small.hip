@@ -22,8 +22,9 @@ typedef __attribute__((address_space(4))) const float cfloat;  // read through t
 constexpr int kSmallWaves = 8;  // waves per workgroup
 constexpr int kSmallDense = 2, kSmallFilter = 0;
 // FILTER: LDS candidate slots per query and workgroup.  Passing pairs are appended with LDS
-// atomics and flushed once, at the workgroup's end, with one global atomic per query: a returning
-// global atomic in the loop would wait for every A prefetch issued before it.  A workgroup covers
+// atomics and flushed once, at the workgroup's end, with one global atomic per query (on that
+// query's own counter line): a returning global atomic in the loop would wait for every A
+// prefetch issued before it.  A workgroup covers
 // a few hundred rows of a round whose expected passes per query are at most a quarter of the
 // candidate capacity, so it rarely meets more than a couple per query; a full list spills to the
 // global list directly.
@@ -48,7 +49,6 @@ struct SmallArgs {
     int ksplit;          // waves per block (K-slices): 1, 2, 4 or 8, dividing dpad / 32
     const float *tau;    // FILTER: per-query threshold
     uint2 *cand;
-    uint32_t *cnt;
     uint32_t *pad;       // FILTER: per-query reservation counters, kSmallPadStride words apart
     int cap;
 };
@@ -262,8 +262,7 @@ static void launch_small_m(const SmallArgs &a, dim3 grid, size_t lds, hipStream_
 
 void launch_small_scan(int metric, bool dense, const float *base, const float *bnorm, const float *qry,
                        const float *qnorm, const float *tau, int nq, int dpad, long row_begin, long row_end,
-                       long plan_rows, uint2 *cand, uint32_t *cnt, uint32_t *pad, int cap, int grid_cap,
-                       hipStream_t s) {
+                       long plan_rows, uint2 *cand, uint32_t *pad, int cap, int grid_cap, hipStream_t s) {
     if (nq <= 0 || row_end <= row_begin) return;
     SmallArgs a{};
     a.A = base;
@@ -277,7 +276,6 @@ void launch_small_scan(int metric, bool dense, const float *base, const float *b
     a.row_blocks = (int)((row_end - row_begin + 31) / 32);
     a.tau = tau;
     a.cand = cand;
-    a.cnt = cnt;
     a.pad = pad;
     a.cap = cap;
     const int n_ctiles = ceil_div(nq, kSmallCols);

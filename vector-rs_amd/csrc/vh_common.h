@@ -208,13 +208,13 @@ void launch_gemm_filter(int metric, bool dense, long item_rows, const float *bas
 // length), which alone sets how the K range is split over the waves, and so the order in which
 // each score's partial sums meet: a score comes out the same whether its round ran whole or cut.
 // FILTER launches count each query's candidates on pad[q * kSmallPadStride] (one 128-byte line
-// per query; pad holds min(nq, kSmallPadQueries) counters, zero before the round) instead of
-// cnt[q], and the round's merge reads them there (launch_topk_merge with that stride).
+// per query; pad holds min(nq, kSmallPadQueries) counters, zero before the round) instead of the
+// run's cnt[q], and the round's merge reads them there (launch_topk_merge with that stride);
+// DENSE launches write row - row_begin and leave the counts to the caller.
 constexpr int kSmallPadStride = 32, kSmallPadQueries = 4 * kSmallCols;
 void launch_small_scan(int metric, bool dense, const float *base, const float *bnorm, const float *qry,
                        const float *qnorm, const float *tau, int nq, int dpad, long row_begin, long row_end,
-                       long plan_rows, uint2 *cand, uint32_t *cnt, uint32_t *pad, int cap, int grid_cap,
-                       hipStream_t s);
+                       long plan_rows, uint2 *cand, uint32_t *pad, int cap, int grid_cap, hipStream_t s);
 
 // Certification of the MFMA k-means assignment: each point's best score must beat its second
 // best by more than twice the point's selection error bound (err_coeff times the norms, with
