@@ -295,3 +295,22 @@ def test_high_dimension_parity(vh, oracle, metric, dim):
                                            ).search_batch_arrays(q, k)
         assert np.all(lens == k)
         check_knn(oracle, base, q, ids, dist, k, metric, rtol=1e-4, atol=1e-5)
+
+
+@pytest.mark.parametrize("mname", ["l2", "cosine"])
+def test_last_query_batch_takes_the_small_scan(vh, oracle, mname):
+    """16,384 + 37 queries: the search runs in batches of 16,384 queries, and the last 37 take the
+    small-batch scan (its spread candidate counters) under the round plan of the first batch.  The
+    first 200 queries and the last 37 against the oracle."""
+    from vector_hip import datasets as ds
+
+    names = {"cosine": "CosineSimilarity", "l2": "L2Squared"}
+    n, d, nq = 20_000, 64, 16_384 + 37
+    base = ds.uniform_int(n, d, 61) if mname == "l2" else ds.uniform(n, d, 61)
+    q = ds.uniform_int(nq, d, 62) if mname == "l2" else ds.uniform(nq, d, 62)
+    print(f"  {mname} {n} x {d} nq={nq}", flush=True)
+    ids, dist, lens = vh.CudaKnnEngine(base, d, vh.DistanceMetric[names[mname]]).search_batch_arrays(q, 10)
+    assert np.all(lens == 10)
+    sel = np.r_[0:200, nq - 37:nq]
+    tol = dict(rtol=0.0, atol=0.0) if mname == "l2" else dict(rtol=1e-4, atol=1e-5)
+    check_knn(oracle, base, q[sel], ids[sel], dist[sel], 10, mname, **tol)
