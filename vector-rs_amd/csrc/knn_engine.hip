@@ -359,16 +359,24 @@ static bool small_plan(const vhip_knn *E, size_t nq, bool direct) {
 // engine's own scan; it serves the queries whose GEMM-form margin could not be certified.
 // `small`: the small-batch round plan (see plan_rounds; cap must be that plan's).
 // max_round_rows: see split_rounds.  `timed`: the scan launches feed the engine's kernel timer.
+// The candidate count a run starts from: the first round's rows when that round is dense (every
+// score is written), else 0.
+static uint32_t first_count(const std::vector<Round> &rounds, const vhip_knn *E) {
+    const bool dense0 = !rounds.empty() && (rounds[0].dense || (E->ham8 && rounds[0].rb == 0));
+    return dense0 ? (uint32_t)(rounds[0].re - rounds[0].rb) : 0u;
+}
+static std::vector<Round> run_plan(const vhip_knn *E, int k, bool gemm, bool small, long max_round_rows) {
+    return split_rounds(plan_rounds(E->n, (size_t)k, gemm, (int)E->dpad, kRoundGrowth, small), max_round_rows);
+}
+
+// reset_done: the run's per-query state was reset with its queries' preparation (RowPrep::init)
 static int run_rounds(vhip_knn *E, const QueryRows &Q, int nq, int k, int kc, int cap, bool direct, bool small,
-                      const RunBufs &B, long max_round_rows, bool timed) {
+                      const RunBufs &B, long max_round_rows, bool timed, bool reset_done = false) {
     hipStream_t s = E->stream;
     const bool gemm = is_gemm_metric(E->metric) && !direct;
-    const std::vector<Round> rounds =
-        split_rounds(plan_rounds(E->n, (size_t)k, gemm, (int)E->dpad, kRoundGrowth, small), max_round_rows);
-    // the first round's candidate count: its rows when it is dense (every score is written)
-    const bool dense0 = !rounds.empty() && (rounds[0].dense || (E->ham8 && rounds[0].rb == 0));
-    launch_topk_init(nq, B.tau, B.have, B.cnt, B.flags, B.mflag, B.nflag,
-                     dense0 ? (uint32_t)(rounds[0].re - rounds[0].rb) : 0u, B.spad, s);
+    const std::vector<Round> rounds = run_plan(E, k, gemm, small, max_round_rows);
+    if (!reset_done)
+        launch_topk_init(nq, B.tau, B.have, B.cnt, B.flags, B.mflag, B.nflag, first_count(rounds, E), B.spad, s);
     if (E->ham8) {
         // the queries' +1/-1 nibbles, rows padded to the 128-query tiles
         const size_t rows = round_up((size_t)nq, kTileCols);
@@ -587,7 +595,8 @@ static int search_prepared(vhip_knn *E, const QueryRows &Q, int nq, int k, int k
         VH_HIP(hipGetLastError());
         return VHIP_OK;
     };
-    VH_CHECK(run_rounds(E, Q, nq, k, kc, cap, false, small, B, 0, fixed == nullptr));
+    // the run's per-query state was reset with the queries' preparation (the caller's RowPrep::init)
+    VH_CHECK(run_rounds(E, Q, nq, k, kc, cap, false, small, B, 0, fixed == nullptr, true));
     volatile uint32_t *vn = nfh;
     vn[0] = vn[1] = 0xffffffffu;  // overwritten by the final kernel
     VH_CHECK(final_pass(true));
@@ -862,6 +871,9 @@ static int engine_search_locked(vhip_knn *E, const void *d_queries, size_t nq, s
             rp.err_nmax = E->norm_max;
             rp.base_integral = E->integral ? 1 : 0;
         }
+        // the batch's run starts here too (search_prepared's first run_rounds skips its reset)
+        rp.init = {bm.B.tau, bm.B.have, bm.B.cnt, bm.B.flags, bm.B.mflag, bm.B.nflag, bm.B.spad,
+                   first_count(run_plan(E, kk, gemm, small, 0), E)};
         launch_rows_prep(rp, E->stream);
         VH_HIP(hipGetLastError());
         const QueryRows Q{bm.qpad, bm.qnorm, bm.qerr, E->shifted ? bm.qraw : bm.qpad};

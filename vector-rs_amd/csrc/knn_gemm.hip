@@ -84,6 +84,18 @@ __global__ __launch_bounds__(256) void k_rows_prep(RowPrep a) {
             }
             continue;
         }
+        if (a.init.tau && lane < 2) {
+            // the run's reset (see launch_topk_init): query p, and the two flag counters at row 0
+            if (lane == 0) {
+                a.init.tau[p] = INFINITY;
+                a.init.have[p] = 0;
+                a.init.cnt[p] = a.init.cnt0;
+                a.init.flags[p] = 0;
+                a.init.mflag[p] = 0;
+                if (a.init.pad && p < (size_t)kSmallPadQueries) a.init.pad[p * kSmallPadStride] = 0;
+            }
+            if (p == 0) a.init.nflag[lane] = 0;
+        }
         const size_t src = a.perm ? a.perm[p] : p;
         const float *row = a.in + src * (size_t)dim;
         float ss = 0.0f;

@@ -178,6 +178,15 @@ struct RowPrep {
     int err_mode = 0;
     float err_coeff = 0.0f, err_nmax = 0.0f;
     int base_integral = 0;
+    // (tau may be null) a search run's per-query state, reset in the same launch as
+    // launch_topk_init would reset it for the n rows: a query batch's preparation and the reset
+    // of its run, one launch instead of two on a launch-bound small search.
+    struct RunInit {
+        float *tau = nullptr;
+        uint32_t *have = nullptr, *cnt = nullptr, *flags = nullptr, *mflag = nullptr, *nflag = nullptr;
+        uint32_t *pad = nullptr;
+        uint32_t cnt0 = 0;
+    } init;
 };
 void launch_rows_prep(const RowPrep &a, hipStream_t s);
 // Short form: no shift, raw copy, integer check or error bound.
