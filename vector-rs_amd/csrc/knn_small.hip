@@ -294,10 +294,15 @@ void launch_small_scan(int metric, bool dense, const float *base, const float *b
         ks *= 2;
     a.ksplit = ks;
     const int groups = ceil_div(a.row_blocks, kSmallWaves / ks);
-    // one workgroup of 8 waves per block group up to four per CU (twice grid_cap): at about 60
-    // VGPRs a SIMD then holds 8 waves, whose loads cover each other's memory latency
-    const dim3 grid((unsigned)std::min(groups, 2 * per_tile), (unsigned)n_ctiles);
     const size_t lds = tile + (ks > 1 ? kSmallSplitBytes : 0);
+    // one workgroup of 8 waves per block group up to four per CU (twice grid_cap): at about 60
+    // VGPRs a SIMD then holds 8 waves, whose loads cover each other's memory latency.  No more
+    // workgroups than the CUs' LDS holds at once: past that they would run in a second wave, each
+    // filling the query tile again, where the resident ones stride on over more block groups
+    // with their tile in place and their loads running ahead across blocks.
+    const int per_cu = std::max(1, std::min(4, (int)(kLdsPerWorkgroup / (lds + kSmallStaticMax))));
+    const int resident = std::max(1, (grid_cap / 2) * per_cu / n_ctiles);
+    const dim3 grid((unsigned)std::min({groups, 2 * per_tile, resident}), (unsigned)n_ctiles);
     if (dense) {
         if (metric == L2) launch_small_m<kSmallDense, L2>(a, grid, lds, s);
         else if (metric == DOT) launch_small_m<kSmallDense, DOT>(a, grid, lds, s);
