@@ -132,6 +132,17 @@ def test_cut_rounds_score_alike(vh, oracle):
     _check_pair(vh, oracle, eng, base, q[:31], 10, "cosine", rtol=1e-4, atol=1e-5)
 
 
+def test_mid_batch_on_a_large_base(vh, oracle):
+    """100 queries over 300,000 rows of 64 floats take the small-batch scan, whose per-query
+    candidate counters (one cache line apart) are carved from the array like the rest; then 33."""
+    from vector_hip import datasets as ds
+
+    base = ds.uniform_int(300_000, 64, 33)
+    eng = vh.CudaKnnEngine(base, 64)
+    q = ds.uniform_int(100, 64, 34)
+    _check_pair(vh, oracle, eng, base, q, 10, "l2", rtol=0.0, atol=0.0)
+    _check_pair(vh, oracle, eng, base, q[:33], 10, "l2", rtol=0.0, atol=0.0)
+
 def test_max_k(vh, oracle):
     """k = VHIP_MAX_K: each query's candidate list is half a megabyte, so batches are small."""
     from vector_hip import datasets as ds
