@@ -354,11 +354,6 @@ static bool small_plan(const vhip_knn *E, size_t nq, bool direct) {
            small_batch((int)std::min<size_t>(nq, 1 << 20), (int)E->dpad, E->n);
 }
 
-// Runs all rounds for nq prepared queries; results stay in B.topk (row stride kc) / B.have.
-// `direct`: score squared L2 in direct form on the unshifted rows (VALU kernel) instead of the
-// engine's own scan; it serves the queries whose GEMM-form margin could not be certified.
-// `small`: the small-batch round plan (see plan_rounds; cap must be that plan's).
-// max_round_rows: see split_rounds.  `timed`: the scan launches feed the engine's kernel timer.
 // The candidate count a run starts from: the first round's rows when that round is dense (every
 // score is written), else 0.
 static uint32_t first_count(const std::vector<Round> &rounds, const vhip_knn *E) {
@@ -369,7 +364,12 @@ static std::vector<Round> run_plan(const vhip_knn *E, int k, bool gemm, bool sma
     return split_rounds(plan_rounds(E->n, (size_t)k, gemm, (int)E->dpad, kRoundGrowth, small), max_round_rows);
 }
 
-// reset_done: the run's per-query state was reset with its queries' preparation (RowPrep::init)
+// Runs all rounds for nq prepared queries; results stay in B.topk (row stride kc) / B.have.
+// `direct`: score squared L2 in direct form on the unshifted rows (VALU kernel) instead of the
+// engine's own scan; it serves the queries whose GEMM-form margin could not be certified.
+// `small`: the small-batch round plan (see plan_rounds; cap must be that plan's).
+// max_round_rows: see split_rounds.  `timed`: the scan launches feed the engine's kernel timer.
+// reset_done: the run's per-query state was reset with its queries' preparation (RowPrep::init).
 static int run_rounds(vhip_knn *E, const QueryRows &Q, int nq, int k, int kc, int cap, bool direct, bool small,
                       const RunBufs &B, long max_round_rows, bool timed, bool reset_done = false) {
     hipStream_t s = E->stream;
